@@ -1,0 +1,52 @@
+"""foldforge_amd: MI355X-native (gfx950) kernels for the Pairformer pair stack behind the
+FoldForge engine-op contract.
+
+``foldforge_amd.load(...)`` builds a trunk of engine-compatible blocks and applies a backend
+plan (``miniworld`` = the native ``hip`` kernels on a gfx950, ``pytorch`` = the reference
+equations in torch ops), the counterpart of ``foldforge.load(..., backend=...)``
+(``src/foldforge/models/__init__.py:134-148`` of the reference).
+"""
+
+from __future__ import annotations
+
+__version__ = "0.1.0"
+
+
+def load(name: str = "pairformer-trunk", checkpoint=None, *, backend: str = "miniworld",
+         dtype=None, device="cuda", blocks: int = 48, seed: int = 0, d_single: int = 384,
+         engine_ops=None, unsupported: str = "fallback", out_scale: float | None = 0.25):
+    """A configured trunk on ``device`` with ``backend`` applied to every op module.
+
+    ``checkpoint``: a ``.safetensors`` file or a weights-only torch state dict in the
+    engine's keys (``blocks.<i>.tri_multi_outgoing.to_left.weight`` ...); without one the
+    parameters are seeded random init (:func:`foldforge_amd.trunk.randomise`).
+    """
+    import torch
+
+    from foldforge_amd.backends import BackendPlan
+    from foldforge_amd.graph import configure_model
+    from foldforge_amd.policy import apply_plan
+    from foldforge_amd.trunk import PairformerTrunk, randomise
+
+    if name != "pairformer-trunk":
+        raise ValueError(f"unknown model {name!r}; this build serves 'pairformer-trunk'")
+    dtype = torch.bfloat16 if dtype is None else dtype
+    plan = BackendPlan.make(backend, engine_ops, unsupported)
+    model = PairformerTrunk(blocks, d_single=d_single)
+    if checkpoint is None:
+        randomise(model, seed, out_scale=out_scale)
+    else:
+        path = str(checkpoint)
+        if path.endswith(".safetensors"):
+            from safetensors.torch import load_file
+
+            state = load_file(path)
+        else:
+            state = torch.load(path, map_location="cpu", weights_only=True)
+        model.load_state_dict(state, strict=True)
+    device = torch.device(device)
+    configure_model(model, dtype, device)
+    plan.resolve(device)
+    model.foldforge_load_report = {"engine_backends": {"plan": plan.report(),
+                                                       "modules": apply_plan(model, plan, device)}}
+    return model

@@ -1,0 +1,402 @@
+// C-ABI of the pair-stack kernels: argument checks, workspace carving, weight packing and
+// launches. Declarations and contracts: include/foldforge_amd.h.
+//
+// Parameters arrive as the engine module's fp32 tensors; each op converts the ones its
+// MFMA kernels read into bf16 inside the caller's workspace (one small launch per call),
+// folding the softmax scale * log2(e) into the query rows and log2(e) into the pair-bias
+// rows. Nothing is cached between calls, so an updated parameter is always seen.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "foldforge_amd.h"
+#include "ffk_device.h"
+#include "ffk_kernels.h"
+
+namespace ffk {
+
+namespace {
+
+thread_local std::string g_error;
+
+int32_t fail(int32_t code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+  return code;
+}
+
+int32_t ok() {
+  g_error.clear();
+  return FFK_OK;
+}
+
+constexpr int kMaxDevices = 64;
+int g_device_state[kMaxDevices];  // 0 unknown, 1 supported, 2 unsupported
+
+int32_t device_state(int device) {
+  if (device < 0 || device >= kMaxDevices) return 2;
+  if (g_device_state[device] == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return 0;
+    g_device_state[device] = strncmp(prop.gcnArchName, "gfx950", 6) == 0 ? 1 : 2;
+  }
+  return g_device_state[device];
+}
+
+int32_t check_device() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FFK_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  const int32_t s = device_state(dev);
+  if (s == 0) return fail(FFK_ERR_HIP, "hipGetDeviceProperties failed for device %d", dev);
+  if (s != 1) return fail(FFK_ERR_DEVICE, "device %d is not a gfx950 (MI355X)", dev);
+  return FFK_OK;
+}
+
+int32_t check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(FFK_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+size_t up256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int64_t pad128(int64_t n) { return (n + 127) / 128 * 128; }
+
+// Sequential sub-allocation of the caller's workspace (256-byte aligned pieces).
+struct Carver {
+  char* base;
+  size_t used = 0;
+  template <typename T>
+  T* take(size_t count) {
+    T* p = reinterpret_cast<T*>(base ? base + used : nullptr);
+    used += up256(count * sizeof(T));
+    return p;
+  }
+};
+
+__global__ __launch_bounds__(256) void pack_bf16(PackJob job) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int s = 0; s < job.nseg; ++s) {
+    const PackSeg sg = job.seg[s];
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < sg.n; i += stride)
+      sg.dst[i] = (bf16)(sg.src ? sg.src[i] * sg.scale : 0.f);
+  }
+}
+
+}  // namespace
+
+void launch_pack(const PackJob& job, hipStream_t stream) {
+  pack_bf16<<<dim3(64), 256, 0, stream>>>(job);
+}
+
+// ---------------------------------------------------------------------------------------
+// workspace layouts (shared by the size queries and the entry points)
+
+struct TrimulWs {
+  bf16 *wp, *wg, *wo, *A, *B, *P;
+  size_t bytes;
+};
+TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
+  Carver cv{static_cast<char*>(ws)};
+  const int64_t np = pad128(n);
+  const size_t plane = (size_t)batch * h * np * np;
+  TrimulWs w;
+  w.wp = cv.take<bf16>((size_t)4 * h * c);
+  w.wg = cv.take<bf16>((size_t)c * c);
+  w.wo = cv.take<bf16>((size_t)c * h);
+  w.A = cv.take<bf16>(plane);
+  w.B = cv.take<bf16>(plane);
+  w.P = cv.take<bf16>(plane);
+  w.bytes = cv.used;
+  return w;
+}
+
+struct TriattnWs {
+  bf16 *wqkv, *wb, *wg, *wo, *q, *k, *vt, *o;
+  f16* bias;
+  size_t bytes;
+};
+TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d) {
+  Carver cv{static_cast<char*>(ws)};
+  const int64_t np = pad128(n);
+  const int hd = heads * d;
+  TriattnWs w;
+  w.wqkv = cv.take<bf16>((size_t)3 * hd * c);
+  w.wb = cv.take<bf16>((size_t)32 * c);
+  w.wg = cv.take<bf16>((size_t)hd * c);
+  w.wo = cv.take<bf16>((size_t)c * hd);
+  w.q = cv.take<bf16>((size_t)batch * heads * np * np * d);
+  w.k = cv.take<bf16>((size_t)batch * heads * np * np * d);
+  w.vt = cv.take<bf16>((size_t)batch * heads * np * np * d);
+  w.bias = cv.take<f16>((size_t)batch * heads * np * np);
+  w.o = cv.take<bf16>((size_t)batch * n * n * hd);
+  w.bytes = cv.used;
+  return w;
+}
+
+struct TransitionWs {
+  bf16 *wa, *wb, *ws;
+  size_t bytes;
+};
+TransitionWs transition_ws(void* ws, int d, int factor) {
+  Carver cv{static_cast<char*>(ws)};
+  TransitionWs w;
+  w.wa = cv.take<bf16>((size_t)factor * d * d);
+  w.wb = cv.take<bf16>((size_t)factor * d * d);
+  w.ws = cv.take<bf16>((size_t)factor * d * d);
+  w.bytes = cv.used;
+  return w;
+}
+
+}  // namespace ffk
+
+using namespace ffk;
+
+extern "C" {
+
+int32_t ffk_version(void) { return 100; }
+
+const char* ffk_last_error(void) { return g_error.c_str(); }
+
+int32_t ffk_device_supported(int32_t device) { return device_state(device) == 1 ? 1 : 0; }
+
+int32_t ffk_layer_norm(const void* x, const float* weight, const float* bias, void* y,
+                       int64_t rows, int32_t cols, float eps, int32_t dtype, void* stream) {
+  if (int32_t s = check_device()) return s;
+  if (!x || !y) return fail(FFK_ERR_INVALID, "layer_norm: null tensor");
+  if (rows < 0 || cols <= 0) return fail(FFK_ERR_INVALID, "layer_norm: bad shape rows=%lld cols=%d", (long long)rows, cols);
+  if (dtype != FFK_DTYPE_BF16 && dtype != FFK_DTYPE_F32)
+    return fail(FFK_ERR_INVALID, "layer_norm: dtype %d is neither bf16 nor fp32", dtype);
+  if (dtype == FFK_DTYPE_BF16 && cols == 128 && (!aligned16(x) || !aligned16(y)))
+    return fail(FFK_ERR_INVALID, "layer_norm: bf16 rows of 128 need 16-byte aligned tensors");
+  if (rows == 0) return ok();
+  launch_layer_norm(x, weight, bias, y, rows, cols, eps, dtype, static_cast<hipStream_t>(stream));
+  return check_launch("layer_norm");
+}
+
+size_t ffk_triangle_multiplication_workspace(int64_t batch, int64_t n, int32_t d_pair,
+                                             int32_t d_hidden) {
+  if (batch <= 0 || n <= 0 || d_pair <= 0 || d_hidden <= 0) return 0;
+  return trimul_ws(nullptr, batch, n, d_pair, d_hidden).bytes;
+}
+
+int32_t ffk_triangle_multiplication(
+    const void* z, const uint8_t* key_mask, const float* ln_pair_w, const float* ln_pair_b,
+    const float* w_left, const float* w_right, const float* w_left_gate,
+    const float* w_right_gate, const float* ln_out_w, const float* ln_out_b,
+    const float* w_out, const float* w_gate, void* out, void* workspace,
+    size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_pair, int32_t d_hidden,
+    int32_t outgoing, int32_t residual, float eps, void* stream) {
+  if (int32_t s = check_device()) return s;
+  if (d_pair != 128 || d_hidden != 128)
+    return fail(FFK_ERR_INVALID, "triangle_multiplication: d_pair=%d d_hidden=%d (kernels take 128/128)", d_pair, d_hidden);
+  if (batch <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "triangle_multiplication: empty shape");
+  if (batch * 128 > 65535 || pad128(n) > 65535)
+    return fail(FFK_ERR_INVALID, "triangle_multiplication: batch=%lld n=%lld exceed the launch grid", (long long)batch, (long long)n);
+  if (!z || !key_mask || !ln_pair_w || !ln_pair_b || !w_left || !w_right || !w_left_gate ||
+      !w_right_gate || !ln_out_w || !ln_out_b || !w_out || !w_gate || !out)
+    return fail(FFK_ERR_INVALID, "triangle_multiplication: null argument");
+  if (!aligned16(z) || !aligned16(out))
+    return fail(FFK_ERR_INVALID, "triangle_multiplication: z/out must be 16-byte aligned");
+  const TrimulWs need = trimul_ws(nullptr, batch, n, d_pair, d_hidden);
+  if (!workspace || workspace_bytes < need.bytes || !aligned16(workspace))
+    return fail(FFK_ERR_WORKSPACE, "triangle_multiplication: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
+  const TrimulWs w = trimul_ws(workspace, batch, n, d_pair, d_hidden);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t hc = (int64_t)d_hidden * d_pair;
+  PackJob job{};
+  job.seg[0] = {w_left, w.wp, hc, 1.f};
+  job.seg[1] = {w_left_gate, w.wp + hc, hc, 1.f};
+  job.seg[2] = {w_right, w.wp + 2 * hc, hc, 1.f};
+  job.seg[3] = {w_right_gate, w.wp + 3 * hc, hc, 1.f};
+  job.seg[4] = {w_gate, w.wg, (int64_t)d_pair * d_pair, 1.f};
+  job.seg[5] = {w_out, w.wo, (int64_t)d_pair * d_hidden, 1.f};
+  job.nseg = 6;
+  launch_pack(job, st);
+  TrimulArgs a;
+  a.z = static_cast<const bf16*>(z);
+  a.mask = key_mask;
+  a.ln_w = ln_pair_w;
+  a.ln_b = ln_pair_b;
+  a.lno_w = ln_out_w;
+  a.lno_b = ln_out_b;
+  a.wp = w.wp;
+  a.wg = w.wg;
+  a.wo = w.wo;
+  a.A = w.A;
+  a.B = w.B;
+  a.P = w.P;
+  a.out = static_cast<bf16*>(out);
+  a.batch = (int)batch;
+  a.n = (int)n;
+  a.np = (int)pad128(n);
+  a.outgoing = outgoing ? 1 : 0;
+  a.residual = residual ? 1 : 0;
+  a.eps = eps;
+  launch_trimul(a, st);
+  return check_launch("triangle_multiplication");
+}
+
+size_t ffk_triangle_attention_workspace(int64_t batch, int64_t n, int32_t d_pair,
+                                        int32_t n_head, int32_t d_head) {
+  if (batch <= 0 || n <= 0 || d_pair <= 0 || n_head <= 0 || d_head <= 0) return 0;
+  return triattn_ws(nullptr, batch, n, d_pair, n_head, d_head).bytes;
+}
+
+int32_t ffk_triangle_attention(
+    const void* z, const uint8_t* key_mask, const float* ln_pair_w, const float* ln_pair_b,
+    const float* w_bias, const float* w_query, const float* w_key, const float* w_value,
+    const float* w_gate, const float* w_out, void* out, void* workspace,
+    size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_pair, int32_t n_head,
+    int32_t d_head, int32_t starting, int32_t transposed_bias, int32_t residual, float eps,
+    void* stream) {
+  if (int32_t s = check_device()) return s;
+  if (d_pair != 128 || d_head != 32 || n_head != 4)
+    return fail(FFK_ERR_INVALID, "triangle_attention: d_pair=%d heads=%d x %d (kernels take 128, 4 x 32)", d_pair, n_head, d_head);
+  if (batch <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "triangle_attention: empty shape");
+  if (batch * n_head > 65535 || pad128(n) > 65535)
+    return fail(FFK_ERR_INVALID, "triangle_attention: batch=%lld n=%lld exceed the launch grid", (long long)batch, (long long)n);
+  if (!z || !key_mask || !ln_pair_w || !ln_pair_b || !w_bias || !w_query || !w_key ||
+      !w_value || !w_gate || !w_out || !out)
+    return fail(FFK_ERR_INVALID, "triangle_attention: null argument");
+  if (!aligned16(z) || !aligned16(out))
+    return fail(FFK_ERR_INVALID, "triangle_attention: z/out must be 16-byte aligned");
+  const TriattnWs need = triattn_ws(nullptr, batch, n, d_pair, n_head, d_head);
+  if (!workspace || workspace_bytes < need.bytes || !aligned16(workspace))
+    return fail(FFK_ERR_WORKSPACE, "triangle_attention: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
+  const TriattnWs w = triattn_ws(workspace, batch, n, d_pair, n_head, d_head);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int hd = n_head * d_head;
+  const int64_t m = (int64_t)hd * d_pair;
+  const float qscale = kLog2e / sqrtf((float)d_head);
+  PackJob job{};
+  job.seg[0] = {w_query, w.wqkv, m, qscale};
+  job.seg[1] = {w_key, w.wqkv + m, m, 1.f};
+  job.seg[2] = {w_value, w.wqkv + 2 * m, m, 1.f};
+  job.seg[3] = {w_bias, w.wb, (int64_t)n_head * d_pair, kLog2e};
+  job.seg[4] = {nullptr, w.wb + (int64_t)n_head * d_pair, (int64_t)(32 - n_head) * d_pair, 0.f};
+  job.seg[5] = {w_gate, w.wg, m, 1.f};
+  job.seg[6] = {w_out, w.wo, m, 1.f};
+  job.nseg = 7;
+  launch_pack(job, st);
+  TriattnArgs a;
+  a.z = static_cast<const bf16*>(z);
+  a.mask = key_mask;
+  a.ln_w = ln_pair_w;
+  a.ln_b = ln_pair_b;
+  a.wqkv = w.wqkv;
+  a.wb = w.wb;
+  a.wg = w.wg;
+  a.wo = w.wo;
+  a.q = w.q;
+  a.k = w.k;
+  a.vt = w.vt;
+  a.bias = w.bias;
+  a.o = w.o;
+  a.out = static_cast<bf16*>(out);
+  a.batch = (int)batch;
+  a.n = (int)n;
+  a.np = (int)pad128(n);
+  a.heads = n_head;
+  a.starting = starting ? 1 : 0;
+  a.transposed_bias = transposed_bias ? 1 : 0;
+  a.residual = residual ? 1 : 0;
+  a.eps = eps;
+  launch_triattn(a, st);
+  return check_launch("triangle_attention");
+}
+
+int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
+                                 const void* bias, void* o, int64_t batch, int32_t heads,
+                                 int64_t rows, int64_t n_pad, int64_t rows_valid,
+                                 int64_t n_valid, int32_t bias_key_major, int64_t o_sb,
+                                 int64_t o_sr, int64_t o_sj, void* stream) {
+  if (int32_t s = check_device()) return s;
+  if (!q || !k || !v_t || !bias || !o) return fail(FFK_ERR_INVALID, "flash_attention_bias: null tensor");
+  if (batch <= 0 || heads <= 0 || rows <= 0 || n_pad <= 0 || n_pad % 128 != 0)
+    return fail(FFK_ERR_INVALID, "flash_attention_bias: bad shape (n_pad %lld must be a positive multiple of 128)", (long long)n_pad);
+  if (rows_valid < 0 || rows_valid > rows || n_valid < 0 || n_valid > n_pad)
+    return fail(FFK_ERR_INVALID, "flash_attention_bias: valid extents exceed the padded shape");
+  if (batch * heads > 65535 || rows > 65535)
+    return fail(FFK_ERR_INVALID, "flash_attention_bias: grid too large");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v_t) || !aligned16(bias))
+    return fail(FFK_ERR_INVALID, "flash_attention_bias: q/k/v_t/bias must be 16-byte aligned");
+  if (((uintptr_t)o & 7u) != 0 || (o_sb | o_sr | o_sj) % 4 != 0)
+    return fail(FFK_ERR_INVALID, "flash_attention_bias: o and its strides must be 8-byte aligned");
+  FlashArgs f;
+  f.q = static_cast<const bf16*>(q);
+  f.k = static_cast<const bf16*>(k);
+  f.vt = static_cast<const bf16*>(v_t);
+  f.bias = static_cast<const f16*>(bias);
+  f.o = static_cast<bf16*>(o);
+  f.batch = batch;
+  f.rows = rows;
+  f.np = n_pad;
+  f.rows_valid = rows_valid;
+  f.n_valid = n_valid;
+  f.o_sb = o_sb;
+  f.o_sr = o_sr;
+  f.o_sj = o_sj;
+  f.heads = heads;
+  f.key_major = bias_key_major ? 1 : 0;
+  if (rows_valid == 0 || n_valid == 0) return ok();
+  launch_flash(f, static_cast<hipStream_t>(stream));
+  return check_launch("flash_attention_bias");
+}
+
+size_t ffk_transition_workspace(int32_t d, int32_t factor) {
+  if (d <= 0 || factor <= 0) return 0;
+  return transition_ws(nullptr, d, factor).bytes;
+}
+
+int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
+                       const float* w_expand_a, const float* w_expand_b,
+                       const float* w_squeeze, void* out, void* workspace,
+                       size_t workspace_bytes, int64_t rows, int32_t d, int32_t factor,
+                       int32_t residual, float eps, void* stream) {
+  if (int32_t s = check_device()) return s;
+  if (d != 128 || factor != 4)
+    return fail(FFK_ERR_INVALID, "transition: d=%d factor=%d (kernels take 128 x 4)", d, factor);
+  if (rows < 0) return fail(FFK_ERR_INVALID, "transition: negative rows");
+  if (!x || !ln_w || !ln_b || !w_expand_a || !w_expand_b || !w_squeeze || !out)
+    return fail(FFK_ERR_INVALID, "transition: null argument");
+  if (!aligned16(x) || !aligned16(out))
+    return fail(FFK_ERR_INVALID, "transition: x/out must be 16-byte aligned");
+  const TransitionWs need = transition_ws(nullptr, d, factor);
+  if (!workspace || workspace_bytes < need.bytes || !aligned16(workspace))
+    return fail(FFK_ERR_WORKSPACE, "transition: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
+  if (rows == 0) return ok();
+  const TransitionWs w = transition_ws(workspace, d, factor);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t m = (int64_t)factor * d * d;
+  PackJob job{};
+  job.seg[0] = {w_expand_a, w.wa, m, 1.f};
+  job.seg[1] = {w_expand_b, w.wb, m, 1.f};
+  job.seg[2] = {w_squeeze, w.ws, m, 1.f};
+  job.nseg = 3;
+  launch_pack(job, st);
+  TransitionArgs a;
+  a.x = static_cast<const bf16*>(x);
+  a.ln_w = ln_w;
+  a.ln_b = ln_b;
+  a.wa = w.wa;
+  a.wb = w.wb;
+  a.ws = w.ws;
+  a.out = static_cast<bf16*>(out);
+  a.rows = rows;
+  a.residual = residual ? 1 : 0;
+  a.eps = eps;
+  launch_transition(a, st);
+  return check_launch("transition");
+}
+
+}  // extern "C"

@@ -1,0 +1,145 @@
+// Device-side building blocks shared by the pair-stack kernels (gfx950 / CDNA4 only).
+//
+// MFMA: v_mfma_f32_32x32x16_bf16 (one wave64 computes a 32x32 fp32 tile from a
+// 32x16 A slice and a 16x32 B slice). Operand layout used throughout:
+//   lane l = 32*g + i (g = 0, 1): A operand = 8 bf16 of row i at k = 8g..8g+7 of the
+//   16-wide k slice; B operand = 8 bf16 of column i at the same k. Because A and B use
+//   the same k <-> (lane group, element) pairing, any consistent permutation of k
+//   inside a slice gives the same sum.
+//   D (16 fp32 per lane): acc[r] is row 8*(r/4) + 4*g + (r%4), column i.
+// Every matrix operand here is "K-contiguous": A rows and B columns are contiguous
+// along k, so one 16-byte load fetches a lane's operand.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ffk {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+typedef bf16 bf16x8 __attribute__((__vector_size__(8 * sizeof(bf16))));
+typedef bf16 bf16x4 __attribute__((__vector_size__(4 * sizeof(bf16))));
+typedef bf16 bf16x2 __attribute__((__vector_size__(2 * sizeof(bf16))));
+typedef f16 f16x4 __attribute__((__vector_size__(4 * sizeof(f16))));
+typedef float f32x16 __attribute__((__vector_size__(16 * sizeof(float))));
+typedef float f32x4 __attribute__((__vector_size__(4 * sizeof(float))));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) z[r] = 0.f;
+  return z;
+}
+
+// Row (within a 32x32 MFMA tile) held by accumulator register r of lane group g.
+__device__ __forceinline__ int acc_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
+
+__device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float sigmoidf_(float x) {
+  return __builtin_amdgcn_rcpf(1.f + fast_exp2(-x * kLog2e));
+}
+
+__device__ __forceinline__ float siluf_(float x) { return x * sigmoidf_(x); }
+
+// acc += A(32 x K) * B(K x 32); a_row / b_row point at k = 0 of this lane's A row and
+// B column (lane l%32), K a multiple of 16.
+template <int K>
+__device__ __forceinline__ void mma_rows(const bf16* a_row, const bf16* b_row, int g, f32x16& acc) {
+#pragma unroll
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    acc = mfma32(ld8(a_row + k0 + 8 * g), ld8(b_row + k0 + 8 * g), acc);
+  }
+}
+
+// Reduction over groups of 16 consecutive lanes.
+__device__ __forceinline__ float sum16(float v) {
+  v += __shfl_xor(v, 8, 16);
+  v += __shfl_xor(v, 4, 16);
+  v += __shfl_xor(v, 2, 16);
+  v += __shfl_xor(v, 1, 16);
+  return v;
+}
+
+__device__ __forceinline__ float sum4(float v) {
+  v += __shfl_xor(v, 2, 4);
+  v += __shfl_xor(v, 1, 4);
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+// Row stride (elements) of a 128-channel bf16 tile in LDS: 16 bytes of padding per row.
+constexpr int kRow = 136;
+
+// Load TM positions of a 128-channel bf16 pair tile and LayerNorm them (fp32 statistics,
+// fp32 affine) into LDS as bf16 [TM][kRow]. Position t lives at base + t * stride
+// (elements) and is real when t < valid; others are written as zeros. When raw is
+// non-null the un-normalised input is stored there too (same layout).
+// 256 threads: 16 lanes per position, 8 channels per lane, 16 positions per pass.
+template <int TM>
+__device__ __forceinline__ void ln_tile_128(const bf16* __restrict__ base, int64_t stride, int valid,
+                                            const float* __restrict__ w, const float* __restrict__ b,
+                                            float eps, bf16* xh, bf16* raw) {
+  const int tid = threadIdx.x;
+  const int sub = tid & 15;   // channel group: channels 8*sub .. 8*sub+7
+  const int pos0 = tid >> 4;  // 0..15
+  float wv[8], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    wv[e] = w[8 * sub + e];
+    bv[e] = b ? b[8 * sub + e] : 0.f;
+  }
+  constexpr int kPass = TM / 16;
+  bf16x8 v[kPass];
+#pragma unroll
+  for (int it = 0; it < kPass; ++it) {
+    const int t = pos0 + 16 * it;
+    if (t < valid) {
+      v[it] = ld8(base + (int64_t)t * stride + 8 * sub);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[it][e] = (bf16)0.f;
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < kPass; ++it) {
+    const int t = pos0 + 16 * it;
+    float x[8];
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = (float)v[it][e];
+      s += x[e];
+    }
+    const float mean = sum16(s) * (1.f / 128.f);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] -= mean;
+      q += x[e] * x[e];
+    }
+    const float rstd = __builtin_amdgcn_rsqf(sum16(q) * (1.f / 128.f) + eps);
+    bf16x8 o;
+    const bool real = t < valid;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = real ? (bf16)(x[e] * rstd * wv[e] + bv[e]) : (bf16)0.f;
+    *reinterpret_cast<bf16x8*>(xh + t * kRow + 8 * sub) = o;
+    if (raw) *reinterpret_cast<bf16x8*>(raw + t * kRow + 8 * sub) = v[it];
+  }
+}
+
+}  // namespace ffk

@@ -1,0 +1,78 @@
+// Host-side launch interfaces of the pair-stack kernels (one struct per op, filled by
+// the C-ABI layer in api.hip after it has validated shapes and carved the workspace).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "ffk_device.h"
+
+namespace ffk {
+
+struct TrimulArgs {
+  const bf16* z;
+  const uint8_t* mask;
+  const float *ln_w, *ln_b, *lno_w, *lno_b;
+  const bf16* wp;  // [4h][c]: left, left_gate, right, right_gate
+  const bf16* wg;  // [c][c]
+  const bf16* wo;  // [c][h]
+  bf16 *A, *B, *P;  // [batch][h][np][np]
+  bf16* out;
+  int batch, n, np, outgoing, residual;
+  float eps;
+};
+void launch_trimul(const TrimulArgs& a, hipStream_t stream);
+
+struct TriattnArgs {
+  const bf16* z;
+  const uint8_t* mask;
+  const float *ln_w, *ln_b;
+  const bf16* wqkv;  // [3 * 128][128], query rows carry d^-1/2 * log2(e)
+  const bf16* wb;    // [32][128], rows < heads carry log2(e) * to_bias, others zero
+  const bf16* wg;    // [128][128] to_gate
+  const bf16* wo;    // [128][128] to_out
+  bf16 *q, *k, *vt;  // [batch * heads][np][np][32], vt: [batch * heads][np][32][np]
+  f16* bias;         // [batch * heads][np][np]
+  bf16* o;           // [batch][n][n][128] z-frame attention output
+  bf16* out;
+  int batch, n, np, heads, starting, transposed_bias, residual;
+  float eps;
+};
+void launch_triattn(const TriattnArgs& a, hipStream_t stream);
+
+struct FlashArgs {
+  const bf16 *q, *k, *vt;
+  const f16* bias;
+  bf16* o;
+  int64_t batch, rows, np, rows_valid, n_valid, o_sb, o_sr, o_sj;
+  int heads, key_major;
+};
+void launch_flash(const FlashArgs& a, hipStream_t stream);
+
+struct TransitionArgs {
+  const bf16* x;
+  const float *ln_w, *ln_b;
+  const bf16 *wa, *wb, *ws;  // [4c][c], [4c][c], [c][4c]
+  bf16* out;
+  int64_t rows;
+  int residual;
+  float eps;
+};
+void launch_transition(const TransitionArgs& a, hipStream_t stream);
+
+struct PackSeg {
+  const float* src;  // NULL: write zeros
+  bf16* dst;
+  int64_t n;
+  float scale;
+};
+struct PackJob {
+  PackSeg seg[8];
+  int nseg;
+};
+void launch_pack(const PackJob& job, hipStream_t stream);
+
+void launch_layer_norm(const void* x, const float* w, const float* b, void* y, int64_t rows,
+                       int cols, float eps, int dtype, hipStream_t stream);
+
+}  // namespace ffk

@@ -1,0 +1,223 @@
+"""Functional entry points of the HIP kernels, named after the engine's kernel functions.
+
+The engine exposes ``layer_norm``, ``triangle_multiplicative_update``,
+``triangle_attention`` and ``transition`` under ``miniworld_engine.kernels``
+(names: ``docs/guides/ENGINE-2.4.2.md:18-21`` of the reference; their signatures are
+not in the reference, so these are this library's own). Each function validates its
+tensors, allocates the output and the workspace with torch's allocator on the input's
+device, and calls the C-ABI on torch's current stream. There is no fallback: the
+module classes decide what to refuse (``unsupported``) before a call ever gets here.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from foldforge_amd import _native
+
+Tensor = torch.Tensor
+
+PAIR_WIDTH = 128
+TRI_HEADS = 4
+TRI_HEAD_DIM = 32
+
+
+def _ptr(t: Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _need(cond: bool, message: str) -> None:
+    if not cond:
+        raise ValueError(message)
+
+
+def _param(t: Tensor, device: torch.device, name: str) -> Tensor:
+    _need(t.device == device, f"{name} is on {t.device}, expected {device}")
+    _need(t.dtype == torch.float32, f"{name} must be fp32 (got {t.dtype})")
+    return t.contiguous()
+
+
+def _workspace(nbytes: int, device: torch.device) -> Tensor:
+    return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
+
+
+def _pair(z: Tensor, mask: Tensor) -> tuple[int, int]:
+    _need(z.is_cuda, "z must be a device tensor")
+    _need(z.dtype == torch.bfloat16, f"z must be bf16 (got {z.dtype})")
+    _need(z.dim() == 4 and z.shape[1] == z.shape[2], f"z must be [B, N, N, c] (got {tuple(z.shape)})")
+    _need(z.shape[3] == PAIR_WIDTH, f"pair width {z.shape[3]} (the kernels take {PAIR_WIDTH})")
+    _need(z.is_contiguous(), "z must be contiguous")
+    _need(mask.dtype == torch.bool and mask.shape == z.shape[:2], "mask must be bool [B, N]")
+    _need(mask.device == z.device and mask.is_contiguous(), "mask must be a contiguous device tensor")
+    return z.shape[0], z.shape[1]
+
+
+def layer_norm(x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: float = 1e-5) -> Tensor:
+    """LayerNorm over the last axis (fp32 statistics and affine), returned in ``x.dtype``."""
+    _need(x.is_cuda and x.is_contiguous(), "x must be a contiguous device tensor")
+    _need(x.dtype in (torch.bfloat16, torch.float32), f"x must be bf16 or fp32 (got {x.dtype})")
+    cols = x.shape[-1]
+    for t, name in ((weight, "weight"), (bias, "bias")):
+        if t is not None:
+            _need(t.numel() == cols, f"{name} has {t.numel()} entries for {cols} channels")
+    weight = None if weight is None else _param(weight, x.device, "weight")
+    bias = None if bias is None else _param(bias, x.device, "bias")
+    y = torch.empty_like(x)
+    dtype = 0 if x.dtype == torch.bfloat16 else 1
+    status = _native.lib().ffk_layer_norm(
+        x.data_ptr(), _ptr(weight), _ptr(bias), y.data_ptr(), x.numel() // cols, cols,
+        float(eps), dtype, _stream(x.device),
+    )
+    _native.check(status, "layer_norm")
+    return y
+
+
+def triangle_multiplicative_update(
+    z: Tensor,
+    mask: Tensor,
+    *,
+    ln_pair_weight: Tensor,
+    ln_pair_bias: Tensor,
+    to_left: Tensor,
+    to_right: Tensor,
+    to_left_gate: Tensor,
+    to_right_gate: Tensor,
+    ln_out_weight: Tensor,
+    ln_out_bias: Tensor,
+    to_out: Tensor,
+    to_gate: Tensor,
+    outgoing: bool,
+    residual: bool = True,
+    eps: float = 1e-5,
+    out: Tensor | None = None,
+) -> Tensor:
+    """Triangle multiplication (outgoing / incoming) of ``z [B, N, N, 128]`` bf16 under the key mask."""
+    batch, n = _pair(z, mask)
+    dev = z.device
+    names = ("ln_pair_weight", "ln_pair_bias", "to_left", "to_right", "to_left_gate",
+             "to_right_gate", "ln_out_weight", "ln_out_bias", "to_out", "to_gate")
+    ps = [_param(t, dev, nm) for t, nm in zip(
+        (ln_pair_weight, ln_pair_bias, to_left, to_right, to_left_gate, to_right_gate,
+         ln_out_weight, ln_out_bias, to_out, to_gate), names)]
+    hidden = to_left.shape[0]
+    _need(to_left.shape == (hidden, PAIR_WIDTH), f"to_left {tuple(to_left.shape)}")
+    lib = _native.lib()
+    ws = _workspace(lib.ffk_triangle_multiplication_workspace(batch, n, PAIR_WIDTH, hidden), dev)
+    out = torch.empty_like(z) if out is None else out
+    status = lib.ffk_triangle_multiplication(
+        z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
+        ws.data_ptr(), ws.numel(), batch, n, PAIR_WIDTH, hidden, int(outgoing), int(residual),
+        float(eps), _stream(dev),
+    )
+    _native.check(status, "triangle_multiplicative_update")
+    return out
+
+
+def triangle_attention(
+    z: Tensor,
+    mask: Tensor,
+    *,
+    ln_pair_weight: Tensor,
+    ln_pair_bias: Tensor,
+    to_bias: Tensor,
+    to_query: Tensor,
+    to_key: Tensor,
+    to_value: Tensor,
+    to_gate: Tensor,
+    to_out: Tensor,
+    n_head: int,
+    starting: bool,
+    transposed_bias: bool = False,
+    residual: bool = True,
+    eps: float = 1e-5,
+    out: Tensor | None = None,
+) -> Tensor:
+    """Triangle attention around the starting / ending node of ``z [B, N, N, 128]`` bf16."""
+    batch, n = _pair(z, mask)
+    dev = z.device
+    ps = [_param(t, dev, nm) for t, nm in zip(
+        (ln_pair_weight, ln_pair_bias, to_bias, to_query, to_key, to_value, to_gate, to_out),
+        ("ln_pair_weight", "ln_pair_bias", "to_bias", "to_query", "to_key", "to_value",
+         "to_gate", "to_out"))]
+    hd = to_query.shape[0]
+    _need(hd % n_head == 0, f"hidden {hd} is not a multiple of {n_head} heads")
+    d = hd // n_head
+    lib = _native.lib()
+    ws = _workspace(lib.ffk_triangle_attention_workspace(batch, n, PAIR_WIDTH, n_head, d), dev)
+    out = torch.empty_like(z) if out is None else out
+    status = lib.ffk_triangle_attention(
+        z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
+        ws.data_ptr(), ws.numel(), batch, n, PAIR_WIDTH, n_head, d, int(starting),
+        int(transposed_bias), int(residual), float(eps), _stream(dev),
+    )
+    _native.check(status, "triangle_attention")
+    return out
+
+
+def transition(
+    x: Tensor,
+    *,
+    ln_weight: Tensor,
+    ln_bias: Tensor,
+    expand_a: Tensor,
+    expand_b: Tensor,
+    squeeze: Tensor,
+    residual: bool = True,
+    eps: float = 1e-5,
+    out: Tensor | None = None,
+) -> Tensor:
+    """Fused SwiGLU transition of ``x [..., 128]`` bf16 (factor 4)."""
+    _need(x.is_cuda and x.is_contiguous(), "x must be a contiguous device tensor")
+    _need(x.dtype == torch.bfloat16, f"x must be bf16 (got {x.dtype})")
+    d = x.shape[-1]
+    _need(d == PAIR_WIDTH, f"width {d} (the kernel takes {PAIR_WIDTH})")
+    factor = expand_a.shape[0] // d
+    dev = x.device
+    ps = [_param(t, dev, nm) for t, nm in zip(
+        (ln_weight, ln_bias, expand_a, expand_b, squeeze),
+        ("ln_weight", "ln_bias", "expand_a", "expand_b", "squeeze"))]
+    lib = _native.lib()
+    ws = _workspace(lib.ffk_transition_workspace(d, factor), dev)
+    out = torch.empty_like(x) if out is None else out
+    status = lib.ffk_transition(
+        x.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(), ws.data_ptr(), ws.numel(),
+        x.numel() // d, d, factor, int(residual), float(eps), _stream(dev),
+    )
+    _native.check(status, "transition")
+    return out
+
+
+def flash_attention_bias(
+    q: Tensor,
+    k: Tensor,
+    v_t: Tensor,
+    bias: Tensor,
+    out: Tensor,
+    *,
+    rows_valid: int,
+    n_valid: int,
+    bias_key_major: bool = False,
+) -> Tensor:
+    """The flash core on prepared operands (see ``ffk_flash_attention_bias``).
+
+    ``q, k [B, H, R, Np, 32]`` bf16 (q pre-scaled by ``d^-1/2 log2 e``),
+    ``v_t [B, H, R, 32, Np]`` bf16, ``bias [B, H, Np, Np]`` fp16 in log2 units;
+    ``out [B, R, n_valid, H * 32]`` bf16 receives ``o`` for rows < rows_valid.
+    """
+    batch, heads, rows, n_pad, d = q.shape
+    _need(d == TRI_HEAD_DIM, f"head dim {d} (the kernel takes {TRI_HEAD_DIM})")
+    _need(k.shape == q.shape and v_t.shape == (batch, heads, rows, d, n_pad), "q/k/v_t shapes")
+    _need(bias.shape == (batch, heads, n_pad, n_pad) and bias.dtype == torch.float16, "bias [B, H, Np, Np] fp16")
+    _need(all(t.is_contiguous() for t in (q, k, v_t, bias)), "operands must be contiguous")
+    _need(out.dtype == torch.bfloat16 and out.shape[-1] == heads * d, "out [..., H * 32] bf16")
+    status = _native.lib().ffk_flash_attention_bias(
+        q.data_ptr(), k.data_ptr(), v_t.data_ptr(), bias.data_ptr(), out.data_ptr(),
+        batch, heads, rows, n_pad, rows_valid, n_valid, int(bias_key_major),
+        out.stride(0), out.stride(1), out.stride(2), _stream(q.device),
+    )
+    _native.check(status, "flash_attention_bias")
+    return out

@@ -1,0 +1,502 @@
+"""Engine-compatible op classes of the pair stack with a native ``hip`` backend.
+
+These mirror the classes FoldForge's graph holds from ``miniworld_engine.modules``
+(imported at ``src/foldforge/modules/engine/modules.py:23-31`` of the reference) and
+keep their contract (``src/foldforge/modules/engine/policy.py:85-101``,
+``tests/kernels/test_backends.py``, ``tests/models/test_dead_modules.py:97-136``):
+
+* ``backends`` (class attribute), ``backend``, ``set_backend(name)``;
+* ``unsupported(*args) -> str | None``: whether the CURRENT backend takes the call,
+  asked before the call; ``forward`` raises :class:`BackendUnsupported` for a call
+  outside the backend's range (the engine never falls back; FoldForge's guard does);
+* ``_forward_<backend>(*args)`` for every listed backend;
+* residual-owning forwards (``x + f(x)``) and ``delta(*args)`` for the bare update;
+* ``dead = False`` class attribute; a dead module returns its input unchanged;
+* fp32 master parameters (:class:`MasterWeights`) that stay fp32 under a bulk
+  ``.to(torch.bfloat16)``; LayerNorm affines are fp32 under any cast;
+* the engine's ``state_dict`` keys (``legacy/released.py:135-368``).
+
+The ``hip`` backend calls :mod:`foldforge_amd.kernels` (one C-ABI call per op) and has
+no fallback of its own: if the native library is missing the call raises.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, fields
+from typing import Any
+
+import torch
+from torch import nn
+
+from foldforge_amd import torch_ops
+
+Tensor = torch.Tensor
+
+HIP_ARCH = "gfx950"
+
+
+class BackendUnsupported(RuntimeError):
+    """A call outside the selected backend's range (the engine's own refusal error)."""
+
+
+def device_arch(device: torch.device) -> str | None:
+    """gfx architecture of a ROCm device (``"gfx950"`` on an MI355X), None elsewhere."""
+    if device.type != "cuda" or not torch.cuda.is_available():
+        return None
+    name = torch.cuda.get_device_properties(device).gcnArchName
+    return name.split(":")[0]
+
+
+def hip_reason(*tensors: Tensor) -> str | None:
+    """Why the hip backend cannot take tensors on these devices (None: it can)."""
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            return f"a {t.device.type} tensor (the hip backend needs a gfx950 device)"
+        arch = device_arch(t.device)
+        if arch != HIP_ARCH:
+            return f"device arch {arch} (the hip kernels are built for {HIP_ARCH})"
+    return None
+
+
+# ------------------------------------------------------------------------------------ mixins
+class MasterWeights:
+    """fp32 master parameters: under ``master_weights`` a bulk cast moves them but keeps fp32.
+
+    Activations are bf16 (autocast) while the parameters stay fp32 masters
+    (``src/foldforge/modules/engine/configure.py:1-6`` of the reference).
+    """
+
+    master_weights: bool = False
+
+    def set_master_weights(self) -> None:
+        for m in self.modules():  # type: ignore[attr-defined]
+            if isinstance(m, MasterWeights):
+                m.master_weights = True
+        self.float()  # type: ignore[attr-defined]
+
+    def _apply(self, fn, recurse=True):  # type: ignore[override]
+        if not self.master_weights:
+            return super()._apply(fn, recurse)  # type: ignore[misc]
+
+        def keep_fp32(t: Tensor) -> Tensor:
+            out = fn(t)
+            if t.dtype == torch.float32 and out.dtype != torch.float32:
+                return t.to(device=out.device)
+            return out
+
+        return super()._apply(keep_fp32, recurse)  # type: ignore[misc]
+
+
+class EngineOp:
+    """Backend dispatch of one op class (mixed into an ``nn.Module``)."""
+
+    backends: tuple[str, ...] = ("pytorch", "hip")
+    dead: bool = False
+
+    def _init_backend(self, backend: str) -> None:
+        self.backend = "pytorch"
+        self.set_backend(backend)
+
+    def set_backend(self, name: str) -> None:
+        if name not in self.backends:
+            raise ValueError(
+                f"{type(self).__name__} has no {name!r} backend (available: {', '.join(self.backends)})"
+            )
+        self.backend = name
+
+    def unsupported(self, *args: Any, **kwargs: Any) -> str | None:
+        """Why the current backend cannot take this call (None: it can)."""
+        if self.backend == "pytorch":
+            return None
+        return getattr(self, f"_unsupported_{self.backend}")(*args, **kwargs)
+
+    def forward(self, *args: Any, **kwargs: Any) -> Any:
+        reason = self.unsupported(*args, **kwargs)
+        if reason is not None:
+            raise BackendUnsupported(f"{type(self).__name__} backend {self.backend!r}: {reason}")
+        return getattr(self, f"_forward_{self.backend}")(*args, **kwargs)
+
+    def delta(self, *args: Any, **kwargs: Any) -> Tensor:
+        """The bare update ``f(x)`` (the forward returns ``x + f(x)``)."""
+        reason = self.unsupported(*args, **kwargs)
+        backend = "pytorch" if reason is not None else self.backend
+        return getattr(self, f"_forward_{backend}")(*args, residual=False, **kwargs)
+
+
+def _linear(d_in: int, d_out: int, bias: bool = False) -> nn.Linear:
+    return nn.Linear(d_in, d_out, bias=bias)
+
+
+# ------------------------------------------------------------------------------------ LayerNorm
+class LayerNorm(EngineOp, nn.LayerNorm):
+    """The engine LayerNorm: fp32 affine under any cast, output in the input dtype
+    (``src/foldforge/modules/engine/modules.py:230-238``)."""
+
+    def __init__(self, normalized_shape, eps: float = 1e-5, bias: bool = True,
+                 elementwise_affine: bool = True, backend: str = "pytorch") -> None:
+        nn.LayerNorm.__init__(self, normalized_shape, eps=eps,
+                              elementwise_affine=elementwise_affine, bias=bias)
+        self._init_backend(backend)
+
+    def _apply(self, fn, recurse=True):  # type: ignore[override]
+        def keep_fp32(t: Tensor) -> Tensor:
+            out = fn(t)
+            if t.dtype == torch.float32 and out.dtype != torch.float32:
+                return t.to(device=out.device)
+            return out
+
+        return super()._apply(keep_fp32, recurse)
+
+    def _unsupported_hip(self, x: Tensor) -> str | None:
+        reason = hip_reason(x)
+        if reason is not None:
+            return reason
+        if x.dtype not in (torch.bfloat16, torch.float32):
+            return f"dtype {x.dtype} (the kernel takes bf16 or fp32)"
+        if len(self.normalized_shape) != 1:
+            return "normalisation over more than one axis"
+        return None
+
+    def _forward_pytorch(self, x: Tensor) -> Tensor:
+        return torch_ops.layer_norm(self, x)
+
+    def _forward_hip(self, x: Tensor) -> Tensor:
+        from foldforge_amd import kernels
+
+        return kernels.layer_norm(x.contiguous(), self.weight, self.bias, self.eps)
+
+
+# ------------------------------------------------------------------------------------ pair ops
+def _pair_reason(z: Tensor, mask: Tensor) -> str | None:
+    reason = hip_reason(z, mask)
+    if reason is not None:
+        return reason
+    if z.dtype != torch.bfloat16:
+        return f"{z.dtype} activations (the kernels take bf16)"
+    if z.dim() != 4 or z.shape[1] != z.shape[2]:
+        return f"pair shape {tuple(z.shape)} (the kernels take [B, N, N, c])"
+    if mask is None or mask.shape != z.shape[:2]:
+        return "the kernels need a [B, N] key mask"
+    if z.shape[0] * 128 > 65535 or z.shape[1] > 65535 - 127:
+        return f"pair shape {tuple(z.shape)} exceeds the launch grid"
+    return None
+
+
+class TriangleMultiplication(EngineOp, MasterWeights, nn.Module):
+    """Triangle multiplicative update (outgoing / incoming), residual included
+    (equations ``legacy/reference/triangle.py:19-49``; parameters ``legacy/released.py:166-173``)."""
+
+    divide_by_length = False
+
+    def __init__(self, d_pair: int, d_hidden: int | None = None, outgoing: bool = True,
+                 p_drop: float = 0.0, model: str | None = None, backend: str = "pytorch") -> None:
+        nn.Module.__init__(self)
+        hidden = d_pair if d_hidden is None else d_hidden
+        self.d_pair, self.d_hidden, self.outgoing, self.p_drop = d_pair, hidden, outgoing, p_drop
+        self.ln_pair = LayerNorm(d_pair)
+        self.to_left = _linear(d_pair, hidden)
+        self.to_right = _linear(d_pair, hidden)
+        self.to_left_gate = _linear(d_pair, hidden)
+        self.to_right_gate = _linear(d_pair, hidden)
+        self.ln_out = LayerNorm(hidden)
+        self.to_out = _linear(hidden, d_pair)
+        self.to_gate = _linear(d_pair, d_pair)
+        self._init_backend(backend)
+
+    def __new__(cls, *args: Any, **kwargs: Any):
+        if cls is TriangleMultiplication and kwargs.get("model") == "rf3":
+            cls = TriangleMultiplicationRF3
+        return super().__new__(cls)
+
+    def _unsupported_hip(self, x: Tensor, mask: Tensor) -> str | None:
+        reason = _pair_reason(x, mask)
+        if reason is not None:
+            return reason
+        if x.shape[-1] != 128 or self.d_hidden != 128:
+            return f"d_pair={x.shape[-1]} d_hidden={self.d_hidden} (the kernels take 128/128)"
+        if self.divide_by_length:
+            return "the length-divided (RF3) contraction is not in the hip kernels"
+        return None
+
+    def _forward_pytorch(self, x: Tensor, mask: Tensor, *, residual: bool = True) -> Tensor:
+        if self.dead:
+            return x if residual else torch.zeros_like(x)
+        return torch_ops.triangle_multiplication(self, x, mask, residual=residual)
+
+    def _forward_hip(self, x: Tensor, mask: Tensor, *, residual: bool = True) -> Tensor:
+        if self.dead:
+            return x if residual else torch.zeros_like(x)
+        from foldforge_amd import kernels
+
+        return kernels.triangle_multiplicative_update(
+            x.contiguous(), mask.contiguous(),
+            ln_pair_weight=self.ln_pair.weight, ln_pair_bias=self.ln_pair.bias,
+            to_left=self.to_left.weight, to_right=self.to_right.weight,
+            to_left_gate=self.to_left_gate.weight, to_right_gate=self.to_right_gate.weight,
+            ln_out_weight=self.ln_out.weight, ln_out_bias=self.ln_out.bias,
+            to_out=self.to_out.weight, to_gate=self.to_gate.weight,
+            outgoing=self.outgoing, residual=residual, eps=self.ln_pair.eps,
+        )
+
+
+class TriangleMultiplicationRF3(TriangleMultiplication):
+    """RoseTTAFold3's exact form: the contraction divided by the real length
+    (``legacy/routing.py:33-41``). Served by the pytorch backend only."""
+
+    divide_by_length = True
+
+
+#: ``TriangleAttention(model=...)`` key -> whether the ending node takes its bias from the
+#: transposed pair (the OpenFold lineage; ``src/foldforge/modules/dense/spec.py:116-125``).
+TRIANGLE_ATTENTION_MODELS: dict[str, bool] = {
+    "af3": False,
+    "openfold3": False,
+    "intellifold2": False,
+    "openfold3_preview2": True,
+    "protenix": True,
+    "boltz2": True,
+    "opendde": True,
+}
+
+
+class TriangleAttention(EngineOp, MasterWeights, nn.Module):
+    """Triangle attention around the starting / ending node, residual included
+    (``legacy/attention.py:60-171``; parameters ``legacy/released.py:176-208``).
+
+    ``TriangleAttention(..., model=key)`` builds the key's class (``TriangleAttentionAF3`` or
+    ``TriangleAttentionOpenFold``). ``d_hidden`` is the total hidden width (default ``d_pair``).
+    """
+
+    transposed_bias = False
+
+    def __new__(cls, *args: Any, **kwargs: Any):
+        if cls is TriangleAttention:
+            model = kwargs.get("model", "af3")
+            if model not in TRIANGLE_ATTENTION_MODELS:
+                raise ValueError(
+                    f"no triangle attention class for model {model!r} in this build "
+                    f"(known: {', '.join(TRIANGLE_ATTENTION_MODELS)})"
+                )
+            cls = TriangleAttentionOpenFold if TRIANGLE_ATTENTION_MODELS[model] else TriangleAttentionAF3
+        return super().__new__(cls)
+
+    def __init__(self, d_pair: int, n_head: int, d_hidden: int | None = None,
+                 starting: bool = True, p_drop: float = 0.0, model: str = "af3",
+                 backend: str = "pytorch") -> None:
+        nn.Module.__init__(self)
+        hidden = d_pair if d_hidden is None else d_hidden
+        self.d_pair, self.n_head, self.d_hidden = d_pair, n_head, hidden
+        self.starting, self.p_drop, self.model = starting, p_drop, model
+        self.ln_pair = LayerNorm(d_pair)
+        self.to_bias = _linear(d_pair, n_head)
+        self.to_query = _linear(d_pair, hidden)
+        self.to_key = _linear(d_pair, hidden)
+        self.to_value = _linear(d_pair, hidden)
+        self.to_gate = _linear(d_pair, hidden)
+        self.to_out = _linear(hidden, d_pair)
+        self._init_backend(backend)
+
+    def _unsupported_hip(self, x: Tensor, mask: Tensor) -> str | None:
+        reason = _pair_reason(x, mask)
+        if reason is not None:
+            return reason
+        if x.shape[-1] != 128 or self.n_head != 4 or self.d_hidden != 128:
+            return (f"d_pair={x.shape[-1]} heads={self.n_head} hidden={self.d_hidden} "
+                    "(the kernels take 128, 4 x 32)")
+        return None
+
+    def _forward_pytorch(self, x: Tensor, mask: Tensor, *, residual: bool = True) -> Tensor:
+        if self.dead:
+            return x if residual else torch.zeros_like(x)
+        return torch_ops.triangle_attention(self, x, mask, residual=residual)
+
+    def _forward_hip(self, x: Tensor, mask: Tensor, *, residual: bool = True) -> Tensor:
+        if self.dead:
+            return x if residual else torch.zeros_like(x)
+        from foldforge_amd import kernels
+
+        return kernels.triangle_attention(
+            x.contiguous(), mask.contiguous(),
+            ln_pair_weight=self.ln_pair.weight, ln_pair_bias=self.ln_pair.bias,
+            to_bias=self.to_bias.weight, to_query=self.to_query.weight,
+            to_key=self.to_key.weight, to_value=self.to_value.weight,
+            to_gate=self.to_gate.weight, to_out=self.to_out.weight, n_head=self.n_head,
+            starting=self.starting, transposed_bias=self.transposed_bias,
+            residual=residual, eps=self.ln_pair.eps,
+        )
+
+
+class TriangleAttentionAF3(TriangleAttention):
+    """AF3: the ending node's bias comes from the un-transposed pair (``legacy/attention.py:144-147``)."""
+
+    transposed_bias = False
+
+
+class TriangleAttentionOpenFold(TriangleAttention):
+    """OpenFold lineage: the ending node's bias comes from the transposed pair."""
+
+    transposed_bias = True
+
+
+class Transition(EngineOp, MasterWeights, nn.Module):
+    """SwiGLU transition, residual included (``legacy/reference/transition.py:28-59``;
+    parameters ``legacy/released.py:211-224``)."""
+
+    def __init__(self, d_hidden: int, n: int = 4, backend: str = "pytorch") -> None:
+        nn.Module.__init__(self)
+        self.d, self.n = d_hidden, n
+        self.ln_in = LayerNorm(d_hidden)
+        self.expand_a = _linear(d_hidden, n * d_hidden)
+        self.expand_b = _linear(d_hidden, n * d_hidden)
+        self.squeeze = _linear(n * d_hidden, d_hidden)
+        self._init_backend(backend)
+
+    def _unsupported_hip(self, x: Tensor) -> str | None:
+        reason = hip_reason(x)
+        if reason is not None:
+            return reason
+        if x.dtype != torch.bfloat16:
+            return f"{x.dtype} activations (the kernel takes bf16)"
+        if self.d != 128 or self.n != 4:
+            return f"width {self.d} x {self.n} (the kernel takes 128 x 4)"
+        return None
+
+    def _forward_pytorch(self, x: Tensor, *, residual: bool = True) -> Tensor:
+        if self.dead:
+            return x if residual else torch.zeros_like(x)
+        return torch_ops.transition(self, x, residual=residual)
+
+    def _forward_hip(self, x: Tensor, *, residual: bool = True) -> Tensor:
+        if self.dead:
+            return x if residual else torch.zeros_like(x)
+        from foldforge_amd import kernels
+
+        return kernels.transition(
+            x.contiguous(), ln_weight=self.ln_in.weight, ln_bias=self.ln_in.bias,
+            expand_a=self.expand_a.weight, expand_b=self.expand_b.weight,
+            squeeze=self.squeeze.weight, residual=residual, eps=self.ln_in.eps,
+        )
+
+
+class AttentionPairBias(EngineOp, MasterWeights, nn.Module):
+    """Single-track attention with pair bias, residual included
+    (``legacy/transformer.py:28-137``; parameters ``legacy/released.py:268-315``).
+    The pair norm has no offset (a per-head constant is softmax-invariant)."""
+
+    backends = ("pytorch",)
+
+    def __init__(self, d_single: int, d_pair: int, n_head: int = 16, gate_bias: float = 0.0,
+                 backend: str = "pytorch") -> None:
+        nn.Module.__init__(self)
+        self.d_single, self.d_pair, self.n_head, self.gate_bias = d_single, d_pair, n_head, gate_bias
+        self.ln_single = LayerNorm(d_single)
+        self.to_query = _linear(d_single, d_single, bias=True)
+        self.to_key = _linear(d_single, d_single)
+        self.to_value = _linear(d_single, d_single)
+        self.ln_pair = LayerNorm(d_pair, bias=False)
+        self.to_bias = _linear(d_pair, n_head)
+        self.to_gate = _linear(d_single, d_single)
+        self.to_out = _linear(d_single, d_single)
+        self._init_backend(backend)
+
+    def _forward_pytorch(self, s: Tensor, z: Tensor, mask: Tensor, extra_bias: Tensor | None = None,
+                         *, residual: bool = True) -> Tensor:
+        if self.dead:
+            return s if residual else torch.zeros_like(s)
+        return torch_ops.attention_pair_bias(self, s, z, mask, extra_bias, residual=residual)
+
+
+# ------------------------------------------------------------------------------------ block
+@dataclass(frozen=True)
+class PairformerConfig:
+    """The engine's block configuration (``src/foldforge/modules/engine/pairformer.py:38-52``).
+    ``d_hidden_tri_attention`` is the per-head width."""
+
+    d_pair: int = 128
+    d_hidden_tri_multi: int = 128
+    d_hidden_tri_attention: int = 32
+    n_head_tri_attention: int = 4
+    p_drop: float = 0.0
+    use_triangle_attention: bool = True
+    model: str = "af3"
+    d_single: int = 0
+    n_head_single: int = 16
+    single_gate_bias: float = 0.0
+    pair_transition_n: int = 4
+    single_transition_n: int = 4
+    parallel: bool = False
+
+    def as_dict(self) -> dict[str, Any]:
+        return {f.name: getattr(self, f.name) for f in fields(self)}
+
+
+class PairformerBlock(MasterWeights, nn.Module):
+    """One Pairformer block: a composite that stays on ``pytorch`` itself while every child
+    op carries its own backend (``src/foldforge/modules/engine/policy.py:118-121``).
+
+    ``block(pair, key_mask)`` -> pair; ``block(pair, key_mask, single[, bias])`` ->
+    ``(pair, single)`` (``src/foldforge/modules/engine/graph.py:226-233``). Order: the
+    sequential AF3 schedule of ``legacy/pairformer.py:191-230`` (``parallel``: every update
+    reads the block's input, ``legacy/pairformer.py:176-190``).
+    """
+
+    backends = ("pytorch",)
+
+    def __init__(self, config: PairformerConfig) -> None:
+        super().__init__()
+        self.config = config
+        c = config
+        self.tri_multi_outgoing = TriangleMultiplication(c.d_pair, c.d_hidden_tri_multi, outgoing=True)
+        self.tri_multi_incoming = TriangleMultiplication(c.d_pair, c.d_hidden_tri_multi, outgoing=False)
+        if c.use_triangle_attention:
+            hidden = c.n_head_tri_attention * c.d_hidden_tri_attention
+            self.tri_atten_starting = TriangleAttention(
+                c.d_pair, c.n_head_tri_attention, d_hidden=hidden, starting=True, model=c.model)
+            self.tri_atten_ending = TriangleAttention(
+                c.d_pair, c.n_head_tri_attention, d_hidden=hidden, starting=False, model=c.model)
+        self.transition_pair = Transition(c.d_pair, c.pair_transition_n)
+        if c.d_single > 0:
+            self.single_attention = AttentionPairBias(
+                c.d_single, c.d_pair, c.n_head_single, c.single_gate_bias)
+            self.single_transition = Transition(c.d_single, c.single_transition_n)
+        self.backend = "pytorch"
+
+    def children_ops(self) -> list[nn.Module]:
+        return [m for m in self.children() if isinstance(m, EngineOp)]
+
+    def set_backend(self, name: str) -> None:
+        """The block itself stays ``pytorch``; each child takes ``name`` where it has it."""
+        self.backend = "pytorch"
+        for m in self.children_ops():
+            m.set_backend(name if name in m.backends else "pytorch")
+
+    def forward(self, pair: Tensor, key_mask: Tensor, single: Tensor | None = None,
+                bias: Tensor | None = None):
+        c = self.config
+        if c.parallel:
+            z0 = pair
+            upd = self.tri_multi_outgoing.delta(z0, key_mask) + self.tri_multi_incoming.delta(z0, key_mask)
+            upd = upd + self.transition_pair.delta(z0)
+            z1 = z0 + upd
+            if c.use_triangle_attention:
+                z1 = z1 + self.tri_atten_starting.delta(z1, key_mask) + self.tri_atten_ending.delta(z1, key_mask)
+            pair_out = z1
+        else:
+            z = self.tri_multi_outgoing(pair, key_mask)
+            z = self.tri_multi_incoming(z, key_mask)
+            if c.use_triangle_attention:
+                z = self.tri_atten_starting(z, key_mask)
+                z = self.tri_atten_ending(z, key_mask)
+            pair_out = self.transition_pair(z)
+        if single is None or c.d_single == 0:
+            return pair_out
+        source = pair if c.parallel else pair_out
+        if c.parallel:
+            s = single + self.single_attention.delta(single, source, key_mask, bias) \
+                + self.single_transition.delta(single)
+        else:
+            s = self.single_attention(single, source, key_mask, bias)
+            s = self.single_transition(s)
+        return pair_out, s

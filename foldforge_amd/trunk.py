@@ -1,0 +1,65 @@
+"""The Pairformer trunk: 48 blocks run in order for every pass, plus seeded random init.
+
+Call site mirrored: ``Evoformer.trunk_pairformer`` and its loop
+(``src/foldforge/models/architectures/af3.py:245-247,813-821`` of the reference); the
+recycle embedding between passes is not part of the pair stack, so each pass feeds its
+output pair / single straight into the next.
+"""
+
+from __future__ import annotations
+
+import torch
+from torch import nn
+
+from foldforge_amd.factories import pairformer_block
+
+Tensor = torch.Tensor
+
+
+def randomise(model: nn.Module, seed: int, *, out_scale: float | None = None) -> nn.Module:
+    """Seeded init in the convention of the reference's block tests
+    (``tests/models/test_engine_graph.py:40-51``): matrices ``0.08 N(0,1)``, norm weights
+    ``1 + 0.1 N(0,1)``, other vectors ``0.05 N(0,1)``. ``out_scale`` additionally
+    multiplies every residual-feeding output matrix (``to_out``, ``squeeze``) so that a
+    deep stack keeps a bounded residual stream."""
+    generator = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            noise = torch.randn(p.shape, generator=generator)
+            if p.ndim > 1:
+                value = 0.08 * noise
+                if out_scale is not None and (name.endswith("to_out.weight") or name.endswith("squeeze.weight")):
+                    value = value * out_scale
+            elif name.endswith("weight") or "scale" in name:
+                value = 1.0 + 0.1 * noise
+            else:
+                value = 0.05 * noise
+            p.copy_(value.to(p.dtype))
+    return model
+
+
+class PairformerTrunk(nn.Module):
+    """``n_blocks`` Pairformer blocks with a single track (AF3 trunk widths by default)."""
+
+    def __init__(self, n_blocks: int = 48, *, d_pair: int = 128, d_single: int = 384,
+                 n_head_single: int = 16, triangle_model: str = "af3",
+                 precision: str = "master") -> None:
+        super().__init__()
+        self.blocks = nn.ModuleList(
+            pairformer_block(d_pair=d_pair, triangle_model=triangle_model, d_single=d_single,
+                             n_head_single=n_head_single, precision=precision)  # type: ignore[arg-type]
+            for _ in range(n_blocks)
+        )
+
+    def forward(self, pair: Tensor, key_mask: Tensor, single: Tensor | None = None,
+                passes: int = 1, on_block=None):
+        """``passes`` times over the blocks; ``on_block(pass, index, pair, single)`` observes each output."""
+        for p in range(passes):
+            for i, block in enumerate(self.blocks):
+                if single is None:
+                    pair = block(pair, key_mask)
+                else:
+                    pair, single = block(pair, key_mask, single)
+                if on_block is not None:
+                    on_block(p, i, pair, single)
+        return pair if single is None else (pair, single)

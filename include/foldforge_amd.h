@@ -1,0 +1,134 @@
+/*
+ * foldforge_amd: C-ABI of the MI355X (gfx950) Pairformer pair-stack kernels.
+ *
+ * Plain pointers and sizes only. Every tensor argument is a device pointer on the
+ * current HIP device; `stream` is a hipStream_t (NULL = the default stream). All
+ * entry points are asynchronous on `stream`, allocate nothing, keep no state between
+ * calls (no weight caches), never throw, and return an FFK_* status; the text of the
+ * last failure on the calling thread is ffk_last_error().
+ *
+ * Layouts (engine layout of the reference, src/foldforge/modules/engine/graph.py:191-235):
+ *   pair z      [batch, n, n, d_pair] bf16, channel-last, contiguous
+ *   key mask    [batch, n] uint8 (torch.bool), 1 = real token
+ *   parameters  fp32, the engine module's own tensors (state_dict layout), contiguous
+ * Outputs are caller-allocated; `out` may alias the pair input (each output tile reads
+ * its own input before writing it). Entry points with a workspace take a caller-
+ * allocated device buffer of at least the matching *_workspace() bytes, 256-byte
+ * aligned. "residual" = 1 returns x + f(x) (the engine's residual-owning forward),
+ * 0 returns the bare update f(x) (the engine's `.delta`).
+ */
+#ifndef FOLDFORGE_AMD_H
+#define FOLDFORGE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FFK_OK 0
+#define FFK_ERR_INVALID 1   /* an argument is outside the kernels' range */
+#define FFK_ERR_WORKSPACE 2 /* workspace missing or too small */
+#define FFK_ERR_HIP 3       /* HIP runtime error (device query, launch) */
+#define FFK_ERR_DEVICE 4    /* the current device is not a gfx950 (MI355X) */
+
+#define FFK_DTYPE_BF16 0
+#define FFK_DTYPE_F32 1
+
+/* Library version (major * 10000 + minor * 100 + patch). */
+int32_t ffk_version(void);
+
+/* Text of the last non-zero status returned on this thread ("" if none). */
+const char* ffk_last_error(void);
+
+/* 1 when HIP device `device` is a gfx950 the kernels were built for, else 0. */
+int32_t ffk_device_supported(int32_t device);
+
+/*
+ * LayerNorm over the last axis: y = (x - mean) / sqrt(var + eps) * weight + bias,
+ * fp32 statistics and fp32 affine, input dtype kept (bf16 or fp32).
+ * Replaces: the engine LayerNorm module and `miniworld_engine.kernels.layer_norm`
+ * (src/foldforge/modules/engine/modules.py:230-238; kernel name in
+ * docs/guides/ENGINE-2.4.2.md:18-21). weight/bias may be NULL (no affine / no offset).
+ */
+int32_t ffk_layer_norm(const void* x, const float* weight, const float* bias, void* y,
+                       int64_t rows, int32_t cols, float eps, int32_t dtype, void* stream);
+
+/*
+ * Triangle multiplicative update, outgoing (outgoing = 1) or incoming (0), including
+ * the LayerNorm + gated projections prologue and the centre norm + output projection +
+ * output gate epilogue. d_pair = d_hidden = 128.
+ * Replaces: engine TriangleMultiplication.forward / `triangle_multiplicative_update`
+ * (equations src/foldforge/models/checkpoints/legacy/reference/triangle.py:19-49,
+ * engine parameters legacy/released.py:135-173; op name "trimul",
+ * src/foldforge/modules/engine/backends.py:36-40).
+ */
+size_t ffk_triangle_multiplication_workspace(int64_t batch, int64_t n, int32_t d_pair,
+                                             int32_t d_hidden);
+int32_t ffk_triangle_multiplication(
+    const void* z, const uint8_t* key_mask, const float* ln_pair_w, const float* ln_pair_b,
+    const float* w_left, const float* w_right, const float* w_left_gate,
+    const float* w_right_gate, const float* ln_out_w, const float* ln_out_b,
+    const float* w_out, const float* w_gate, void* out, void* workspace,
+    size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_pair, int32_t d_hidden,
+    int32_t outgoing, int32_t residual, float eps, void* stream);
+
+/*
+ * Triangle attention around the starting (starting = 1) or ending (0) node: LayerNorm,
+ * pair bias, q/k/v/gate projections, flash attention with key mask, gate, output
+ * projection. d_pair = 128, n_head * d_head = 128, d_head = 32. transposed_bias = 1
+ * takes the ending node's bias from the transposed pair (OpenFold lineage).
+ * Replaces: engine TriangleAttention(AF3).forward / `triangle_attention`
+ * (src/foldforge/models/checkpoints/legacy/attention.py:108-163,
+ * legacy/reference/attention.py:77-100; engine parameters legacy/released.py:176-208;
+ * op name "triangle_attention", src/foldforge/modules/engine/backends.py:41-47).
+ */
+size_t ffk_triangle_attention_workspace(int64_t batch, int64_t n, int32_t d_pair,
+                                        int32_t n_head, int32_t d_head);
+int32_t ffk_triangle_attention(
+    const void* z, const uint8_t* key_mask, const float* ln_pair_w, const float* ln_pair_b,
+    const float* w_bias, const float* w_query, const float* w_key, const float* w_value,
+    const float* w_gate, const float* w_out, void* out, void* workspace,
+    size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_pair, int32_t n_head,
+    int32_t d_head, int32_t starting, int32_t transposed_bias, int32_t residual, float eps,
+    void* stream);
+
+/*
+ * Flash attention core with an additive pair bias, the building block of triangle
+ * attention (and of the single track's attention with pair bias):
+ *   o[b, h, r, j, :] = sum_k softmax_k(q[b,h,r,j,:] . k[b,h,r,k,:] + bias) v[b,h,r,k,:]
+ * in the base-2 domain: q must already carry the softmax scale times log2(e), bias is
+ * fp16 in log2 units with -inf at masked keys. Shapes: q, k [bh, rows, n_pad, 32] bf16;
+ * v_t [bh, rows, 32, n_pad] bf16 (v transposed); bias [bh, n_pad, n_pad] f16 read as
+ * bias[h][query][key] (bias_key_major = 0) or bias[h][key][query] (1); output bf16
+ * written at o + b*o_sb + r*o_sr + j*o_sj + h*32 + d for r < rows_valid, j < n_valid.
+ * n_pad must be a multiple of 128. Replaces the engine's triangle-attention kernel
+ * (docs/engine-kernel-gaps.md:10-23 names its sm90 source); no reference C signature.
+ */
+int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
+                                 const void* bias, void* o, int64_t batch, int32_t heads,
+                                 int64_t rows, int64_t n_pad, int64_t rows_valid,
+                                 int64_t n_valid, int32_t bias_key_major, int64_t o_sb,
+                                 int64_t o_sr, int64_t o_sj, void* stream);
+
+/*
+ * Pair (or single) transition: x + squeeze(silu(expand_a(LN(x))) * expand_b(LN(x))),
+ * fully fused (the 4x hidden never reaches HBM). d = 128, factor = 4.
+ * Replaces: engine Transition.forward / `transition`
+ * (src/foldforge/models/checkpoints/legacy/reference/transition.py:28-59,
+ * engine parameters legacy/released.py:211-224; op name "transition",
+ * src/foldforge/modules/engine/backends.py:51).
+ */
+size_t ffk_transition_workspace(int32_t d, int32_t factor);
+int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
+                       const float* w_expand_a, const float* w_expand_b,
+                       const float* w_squeeze, void* out, void* workspace,
+                       size_t workspace_bytes, int64_t rows, int32_t d, int32_t factor,
+                       int32_t residual, float eps, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FOLDFORGE_AMD_H */

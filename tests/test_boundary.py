@@ -1,0 +1,299 @@
+"""The drop-in boundary on the CPU: backend names and policy, the guard with its fallback and
+error policy, factories and precision, dead modules, the residual contract, and the
+``pytorch`` backend against the oracle.
+
+Mirrors the reference's ``tests/kernels/test_backends.py``, ``test_engine_factories.py``,
+``tests/models/test_dead_modules.py:97-136`` and ``test_released_conversions.py`` (the
+parity is checked only where the pair is real, ``:61-64``). The ``hip`` backend's
+refusals are forced from the host with CPU tensors and a faked device capability.
+"""
+
+from __future__ import annotations
+
+import logging
+
+import pytest
+import torch
+from torch import nn
+
+from foldforge_amd import backends, factories, graph, policy, serving
+from foldforge_amd.modules import (
+    AttentionPairBias,
+    BackendUnsupported,
+    MasterWeights,
+    PairformerBlock,
+    Transition,
+    TriangleAttention,
+    TriangleAttentionAF3,
+    TriangleAttentionOpenFold,
+    TriangleMultiplication,
+    TriangleMultiplicationRF3,
+)
+from foldforge_amd.trunk import PairformerTrunk, randomise
+from oracle import pairstack as ps
+
+
+def fake_gfx950(monkeypatch):
+    monkeypatch.setattr(backends, "capability", lambda _d: "gfx950")
+
+
+def test_names_and_aliases():
+    assert set(backends.ENGINE_BACKENDS) >= {"pytorch", "hip", "cuda", "triton", "anthropic", "cueq"}
+    assert "miniworld" in backends.BACKENDS
+    with pytest.raises(ValueError, match="Unknown backend"):
+        backends.BackendPlan.make("magma")
+    with pytest.raises(ValueError, match="unknown op"):
+        backends.validate_ops({"nope": "pytorch"})
+    with pytest.raises(ValueError, match="unknown backend"):
+        backends.validate_ops({"trimul": "nope"})
+    with pytest.raises(ValueError, match="engine.unsupported"):
+        backends.BackendPlan.make("pytorch", unsupported="ignore")
+
+
+def test_serves_is_derived_from_the_classes():
+    table = backends.SERVES
+    assert set(table) == set(backends.OPS)
+    for op in ("trimul", "triangle_attention", "transition", "layernorm"):
+        assert table[op] == ("miniworld", "pytorch", "hip"), op
+    assert table["single_attention"] == ("pytorch",)
+    assert table["opm"] == ()  # named, no class in this build
+
+
+def test_choose_backend(monkeypatch):
+    monkeypatch.setattr(backends, "capability", lambda _d: None)
+    assert backends.choose_backend("miniworld", Transition) == ("pytorch", None)
+    name, why = backends.choose_backend("hip", Transition)
+    assert name == "pytorch" and "gfx950" in why
+    fake_gfx950(monkeypatch)
+    assert backends.choose_backend("miniworld", Transition) == ("hip", None)
+    assert backends.choose_backend("hip", TriangleMultiplication) == ("hip", None)
+    assert backends.choose_backend("miniworld", AttentionPairBias) == ("pytorch", None)
+    name, why = backends.choose_backend("cuda", Transition)
+    assert name == "pytorch" and "no 'cuda' backend" in why
+    # another ROCm card: the hip kernels are gfx950 code objects
+    monkeypatch.setattr(backends, "capability", lambda _d: "gfx942")
+    assert backends.choose_backend("miniworld", Transition) == ("pytorch", None)
+    assert backends.choose_backend("hip", Transition)[0] == "pytorch"
+
+
+def test_plan_resolve_reports_refused_ops(monkeypatch, caplog):
+    fake_gfx950(monkeypatch)
+    plan = backends.BackendPlan.make("pytorch", {"transition": "hip", "single_attention": "hip"})
+    with caplog.at_level(logging.WARNING, logger="foldforge.backend"):
+        plan.resolve()
+    assert plan.of("transition") == "hip"
+    assert plan.resolved["single_attention"].reason is not None
+    assert plan.report()["fallbacks"].keys() == {"single_attention"}
+    assert sum("single_attention" in r.message for r in caplog.records) == 1
+    strict = backends.BackendPlan.make("pytorch", {"single_attention": "hip"}, "error")
+    with pytest.raises(backends.BackendUnsupportedError):
+        strict.resolve()
+
+
+class _Model(nn.Module):
+    def __init__(self) -> None:
+        super().__init__()
+        self.transition = factories.transition(16, 2, precision="fp32")
+        self.trimul = factories.triangle_multiplication(16, outgoing=True, precision="fp32")
+        self.norm = factories.layer_norm(16)
+
+
+def _x(batch: int = 1) -> torch.Tensor:
+    torch.manual_seed(0)
+    return torch.randn(batch, 4, 16)
+
+
+def test_apply_plan_sets_the_backend_per_module_and_guards(monkeypatch):
+    fake_gfx950(monkeypatch)
+    model = _Model()
+    choices = policy.apply_plan(model, backends.BackendPlan.make("miniworld", {"trimul": "pytorch"}))
+    assert model.transition.backend == "hip"
+    assert model.norm.backend == "hip"
+    assert model.trimul.backend == "pytorch"
+    assert choices["transition"]["backend"] == "hip"
+    assert choices["trimul"]["op"] == "trimul"
+
+
+def test_unsupported_call_falls_back_once_and_logs_once(monkeypatch, caplog):
+    fake_gfx950(monkeypatch)
+    model = _Model()
+    expected = Transition.forward(model.transition, _x())  # pytorch backend
+    policy.apply_plan(model, backends.BackendPlan.make("hip"))
+    assert model.transition.backend == "hip"
+    # a CPU tensor is outside the hip backend's range: the op raises, the guard falls back
+    assert model.transition.unsupported(_x()) is not None
+    with pytest.raises(BackendUnsupported):
+        Transition.forward(model.transition, _x())
+    with caplog.at_level(logging.WARNING, logger="foldforge.backend"):
+        first = model.transition(_x())
+        second = model.transition(_x())
+    torch.testing.assert_close(first, expected)
+    torch.testing.assert_close(second, expected)
+    assert model.transition.backend == "hip"  # restored after the call
+    assert sum("refuses a call" in r.message for r in caplog.records) == 1
+    stats = serving.report_observations(model)["modules"]["transition"]
+    assert stats["served_host_calls"] == {"pytorch": 2}
+    assert len(stats["refused_host_calls"]) == 1
+
+
+def test_unsupported_error_policy_raises(monkeypatch):
+    fake_gfx950(monkeypatch)
+    model = _Model()
+    policy.apply_plan(model, backends.BackendPlan.make("hip", unsupported="error"))
+    with pytest.raises(backends.BackendUnsupportedError, match=r"engine.unsupported: error"):
+        model.transition(_x())
+
+
+def test_composite_children_are_set_one_by_one(monkeypatch):
+    fake_gfx950(monkeypatch)
+    block = factories.pairformer_block(d_pair=32, triangle_model="af3", d_single=64,
+                                       n_head_single=4, precision="fp32")
+    holder = nn.ModuleList([block])
+    policy.apply_plan(holder, backends.BackendPlan.make("miniworld"))
+    assert block.backend == "pytorch"
+    assert block.tri_multi_outgoing.backend == "hip"
+    assert block.tri_atten_ending.backend == "hip"
+    assert block.transition_pair.backend == "hip"
+    assert block.single_attention.backend == "pytorch"  # no hip kernel: not a refusal
+    # widths outside the kernels (32 != 128) are refused per call even on a gfx950
+    from foldforge_amd import modules
+
+    monkeypatch.setattr(modules, "hip_reason", lambda *_t: None)
+    reason = block.tri_multi_outgoing.unsupported(
+        torch.zeros(1, 4, 4, 32, dtype=torch.bfloat16), torch.ones(1, 4, dtype=torch.bool))
+    assert reason is not None and "128" in reason
+    reason = block.tri_atten_starting.unsupported(
+        torch.zeros(1, 4, 4, 32, dtype=torch.float32), torch.ones(1, 4, dtype=torch.bool))
+    assert reason is not None and "bf16" in reason
+
+
+def test_factories_precision_and_model_keys():
+    for precision in ("master", "fp32"):
+        m = factories.transition(32, 4, precision=precision)
+        assert {p.dtype for p in m.parameters()} == {torch.float32}
+        assert m.master_weights is (precision == "master")
+        m.to(torch.bfloat16)
+        assert m.expand_a.weight.dtype == (torch.float32 if precision == "master" else torch.bfloat16)
+        assert m.ln_in.weight.dtype == torch.float32
+    with pytest.raises(ValueError, match="precision"):
+        factories.finish(Transition(8, 2), "bf16")
+    assert type(factories.triangle_attention(32, 4, starting=True, model="af3")) is TriangleAttentionAF3
+    assert type(factories.triangle_attention(32, 4, starting=False, model="protenix")) is TriangleAttentionOpenFold
+    assert type(factories.triangle_multiplication(32, outgoing=True)) is TriangleMultiplication
+    assert type(factories.triangle_multiplication(32, outgoing=True, divide_by_length=True)) is TriangleMultiplicationRF3
+    assert factories.triangle_multiplication(64, outgoing=False, d_hidden=128).to_left.weight.shape == (128, 64)
+    with pytest.raises(ValueError, match="no triangle attention class"):
+        TriangleAttention(32, 4, model="chai1")
+    assert factories.model_keys("alphafold3").triangle == "af3"
+    with pytest.raises(ValueError, match="no engine selector keys"):
+        factories.model_keys("nope")
+
+
+def test_master_flag_reaches_every_mixin_below():
+    block = factories.pairformer_block(d_pair=32, triangle_model="af3", d_single=64, n_head_single=4)
+    mixins = [m for m in block.modules() if isinstance(m, MasterWeights)]
+    assert mixins and all(m.master_weights for m in mixins)
+    assert {p.dtype for p in block.parameters()} == {torch.float32}
+
+
+def test_engine_state_dict_keys():
+    block = factories.pairformer_block(d_pair=128, triangle_model="af3", d_single=384)
+    keys = set(block.state_dict())
+    for key in (
+        "tri_multi_outgoing.to_left.weight", "tri_multi_incoming.ln_out.bias",
+        "tri_multi_outgoing.to_gate.weight", "tri_atten_starting.to_bias.weight",
+        "tri_atten_ending.to_query.weight", "transition_pair.expand_a.weight",
+        "transition_pair.squeeze.weight", "single_attention.to_query.bias",
+        "single_attention.ln_pair.weight", "single_transition.ln_in.weight",
+    ):
+        assert key in keys, key
+    assert "single_attention.ln_pair.bias" not in keys
+    assert block.tri_multi_outgoing.to_out.weight.shape == (128, 128)
+    assert block.tri_atten_starting.to_bias.weight.shape == (4, 128)
+
+
+def test_dead_flag_and_identity():
+    for cls in (Transition, TriangleAttention, TriangleMultiplication, AttentionPairBias):
+        assert cls.dead is False
+    module = factories.transition(16, 2, precision="fp32").eval()
+    module.dead = True
+    x = torch.randn(3, 16, dtype=torch.bfloat16)
+    assert torch.equal(module(x), x)
+    module.dead = False
+    assert not torch.equal(module(x), x)
+
+
+def test_residual_contract_and_delta():
+    torch.manual_seed(0)
+    m = randomise(factories.triangle_multiplication(16, outgoing=False, precision="fp32"), 3)
+    x = torch.randn(1, 5, 5, 16)
+    mask = torch.ones(1, 5, dtype=torch.bool)
+    torch.testing.assert_close(m(x, mask), x + m.delta(x, mask))
+
+
+def _valid(x, mask):
+    pm = mask[:, :, None] & mask[:, None, :]
+    return x[pm]
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_pytorch_backend_trimul_matches_oracle(outgoing):
+    m = randomise(factories.triangle_multiplication(32, outgoing=outgoing, precision="fp32"), 1)
+    torch.manual_seed(2)
+    x = torch.randn(2, 9, 9, 32)
+    mask = torch.ones(2, 9, dtype=torch.bool)
+    mask[1, -3:] = False
+    got = m(x, mask)
+    want = ps.triangle_multiplication(x, mask, m.state_dict(), outgoing=outgoing, dtype=torch.float64)
+    torch.testing.assert_close(_valid(got.double(), mask), _valid(want, mask), atol=2e-5, rtol=2e-5)
+
+
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("model", ["af3", "boltz2"])
+def test_pytorch_backend_triattn_matches_oracle(starting, model):
+    m = randomise(factories.triangle_attention(32, 4, starting=starting, model=model, precision="fp32"), 1)
+    torch.manual_seed(3)
+    x = torch.randn(1, 10, 10, 32)
+    mask = torch.ones(1, 10, dtype=torch.bool)
+    mask[0, -2:] = False
+    got = m(x, mask)
+    want = ps.triangle_attention(x, mask, m.state_dict(), starting=starting, n_head=4,
+                                 transposed_bias=m.transposed_bias, dtype=torch.float64)
+    torch.testing.assert_close(_valid(got.double(), mask), _valid(want, mask), atol=2e-5, rtol=2e-5)
+
+
+def test_pytorch_backend_block_and_run_block_match_oracle():
+    block = randomise(factories.pairformer_block(d_pair=32, triangle_model="af3", d_single=48,
+                                                 n_head_single=4, precision="fp32"), 4)
+    torch.manual_seed(5)
+    n = 8
+    pair = torch.randn(n, n, 32)
+    single = torch.randn(n, 48)
+    tokens = torch.ones(n)
+    tokens[-2:] = 0
+    pair_mask = tokens[:, None] * tokens[None, :]
+    got_pair, got_single = graph.run_block(block, pair, pair_mask, single.clone(), tokens)
+    mask = (tokens > 0)[None]
+    want_pair, want_single = ps.pairformer_block(pair[None], mask, block.state_dict(), n_head_pair=4,
+                                                 s=single[None], n_head_single=4, dtype=torch.float64)
+    torch.testing.assert_close(_valid(got_pair[None].double(), mask), _valid(want_pair, mask), atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(got_single[tokens > 0].double(), want_single[0][tokens > 0], atol=1e-4, rtol=1e-4)
+
+
+def test_token_mask_is_the_pair_mask_diagonal():
+    tokens = torch.tensor([1.0, 1.0, 0.0, 1.0])
+    pm = tokens[:, None] * tokens[None, :]
+    assert factories.token_mask(pm).tolist() == [True, True, False, True]
+    assert factories.residue_mask(pm).shape == (1, 4)
+
+
+def test_trunk_runs_passes_on_cpu():
+    trunk = randomise(PairformerTrunk(2, d_pair=32, d_single=48, n_head_single=4, precision="fp32"), 7)
+    assert isinstance(trunk.blocks[0], PairformerBlock)
+    z = torch.randn(1, 6, 6, 32)
+    s = torch.randn(1, 6, 48)
+    mask = torch.ones(1, 6, dtype=torch.bool)
+    seen = []
+    pair, single = trunk(z, mask, s, passes=2, on_block=lambda p, i, *_: seen.append((p, i)))
+    assert seen == [(0, 0), (0, 1), (1, 0), (1, 1)]
+    assert torch.isfinite(pair).all() and torch.isfinite(single).all()

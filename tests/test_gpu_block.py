@@ -1,0 +1,102 @@
+"""GPU: a whole Pairformer block and a short trunk through the drop-in boundary.
+
+``foldforge_amd.load(..., backend="miniworld")`` on a gfx950 must serve every pair op with
+the native ``hip`` backend (checked through the guard's host-call counters), and the
+result must match the fp64 oracle: the block's update within rel-RMS 3e-2 on the valid
+pairs, the trunk's final pair and single within 5e-2. At the full N = 512 the
+size-independent properties are checked: finiteness, run-to-run bitwise determinism,
+and bitwise invariance of the valid region to padded content.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import foldforge_amd
+from foldforge_amd import factories, serving
+from foldforge_amd.trunk import randomise
+from oracle import pairstack as ps
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU in this environment")
+    from foldforge_amd import _native
+
+    _native.lib()
+
+
+def _valid_pairs(mask: torch.Tensor) -> torch.Tensor:
+    return mask[:, :, None] & mask[:, None, :]
+
+
+def test_block_update_matches_oracle():
+    n, length = 128, 101
+    g = torch.Generator().manual_seed(3)
+    z = torch.randn(1, n, n, 128, generator=g).bfloat16()
+    mask = torch.ones(1, n, dtype=torch.bool)
+    mask[0, length:] = False
+    block = randomise(factories.pairformer_block(d_pair=128, triangle_model="af3"), seed=4).cuda()
+    block.set_backend("hip")
+    got = block(z.cuda(), mask.cuda()).cpu()
+    want = ps.pairformer_block(z, mask, block.state_dict(), n_head_pair=4, dtype=torch.float64)
+    where = _valid_pairs(mask)
+    rr = ps.rel_rms(got.double() - z.double(), want - z.double(), where)
+    print(f"block update rel_rms={rr:.3e}", flush=True)
+    assert rr <= 3e-2
+
+
+def test_load_serves_every_pair_op_with_hip_and_matches_oracle():
+    n = 96
+    model = foldforge_amd.load(backend="miniworld", device="cuda", blocks=2, seed=1, d_single=384)
+    report = model.foldforge_load_report["engine_backends"]
+    backends_of = {name: r["backend"] for name, r in report["modules"].items()}
+    for name, backend in backends_of.items():
+        if ".single_" not in name:
+            assert backend == "hip", (name, backend)
+    g = torch.Generator().manual_seed(2)
+    z = torch.randn(1, n, n, 128, generator=g).bfloat16()
+    s = torch.randn(1, n, 384, generator=g).bfloat16()
+    mask = torch.ones(1, n, dtype=torch.bool)
+    mask[0, 90:] = False
+    with torch.no_grad():
+        pair, single = model(z.cuda(), mask.cuda(), s.cuda(), passes=1)
+    served = serving.report_observations(model)["modules"]
+    pair_ops = {k: v for k, v in served.items() if ".single_" not in k}
+    hip_calls = sum(v["served_host_calls"].get("hip", 0) for v in pair_ops.values())
+    assert hip_calls == 2 * 5, served  # 5 pair ops per block served natively
+    assert all(not v["refused_host_calls"] for v in pair_ops.values())
+    state = model.state_dict()
+    wz, ws = z, s
+    for i in range(2):
+        sub = {k[len(f"blocks.{i}."):]: v for k, v in state.items() if k.startswith(f"blocks.{i}.")}
+        wz, ws = ps.pairformer_block(wz, mask, sub, n_head_pair=4, s=ws, n_head_single=16, dtype=torch.float64)
+    where = _valid_pairs(mask)
+    rp = ps.rel_rms(pair.cpu().double(), wz, where)
+    rs = ps.rel_rms(single.cpu().double(), ws, mask)
+    print(f"2-block trunk: pair rel_rms={rp:.3e} single rel_rms={rs:.3e}", flush=True)
+    assert rp <= 5e-2 and rs <= 5e-2
+
+
+def test_full_size_block_properties():
+    n, length = 512, 413
+    g = torch.Generator().manual_seed(5)
+    z = torch.randn(1, n, n, 128, generator=g).bfloat16().cuda()
+    mask = torch.ones(1, n, dtype=torch.bool)
+    mask[0, length:] = False
+    mask = mask.cuda()
+    block = randomise(factories.pairformer_block(d_pair=128, triangle_model="af3"), seed=6).cuda()
+    block.set_backend("hip")
+    a = block(z, mask)
+    b = block(z, mask)
+    assert torch.isfinite(a.float()).all()
+    assert torch.equal(a, b)
+    z2 = z.clone()
+    z2[0, length:] = 7.0
+    z2[0, :, length:] = -3.0
+    c = block(z2, mask)
+    assert torch.equal(a[0, :length, :length], c[0, :length, :length])

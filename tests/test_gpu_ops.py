@@ -1,0 +1,157 @@
+"""GPU parity of the HIP kernels against the CPU oracle (gfx950 only).
+
+Inputs are seeded fp32 draws rounded to bf16; the oracle gets the same rounded values and
+the module's fp32 parameters and runs in fp64. Op-level parity compares the bare update
+``f(x)`` (``residual=False``: the bf16 residual stream would otherwise hide errors in f)
+on the valid pairs, to the tolerance stated for bf16 kernels against an fp32 reference:
+rel-RMS <= 1e-2 and max-abs <= 4e-2 * max|ref|. Masking is exact: a masked key gets zero
+weight, so the valid region is bitwise independent of whatever the padded positions hold.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from foldforge_amd import factories, kernels
+from foldforge_amd.trunk import randomise
+from oracle import pairstack as ps
+
+pytestmark = pytest.mark.gpu
+
+REL_RMS = 1e-2
+MAX_ABS = 4e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU in this environment")
+    from foldforge_amd import _native
+
+    _native.lib()  # a missing library is an error on a GPU box, not a skip
+    torch.manual_seed(0)
+
+
+def _pair(n: int, batch: int = 1, seed: int = 0, lengths=None):
+    g = torch.Generator().manual_seed(seed)
+    z = torch.randn(batch, n, n, 128, generator=g).bfloat16()
+    mask = torch.ones(batch, n, dtype=torch.bool)
+    for b, length in enumerate(lengths or []):
+        mask[b, length:] = False
+    return z, mask
+
+
+def _check(got: torch.Tensor, want: torch.Tensor, where: torch.Tensor | None, what: str) -> None:
+    rr = ps.rel_rms(got, want, where)
+    ma = ps.max_abs(got, want, where)
+    ref = want.double()[where].abs().max().item() if where is not None else want.abs().max().item()
+    print(f"{what}: rel_rms={rr:.2e} max_abs={ma:.2e} max_ref={ref:.2e}", flush=True)
+    assert rr <= REL_RMS, f"{what}: rel-RMS {rr:.3e}"
+    assert ma <= MAX_ABS * ref, f"{what}: max-abs {ma:.3e} vs {MAX_ABS} * {ref:.3e}"
+
+
+def _pairs(mask: torch.Tensor) -> torch.Tensor:
+    return mask[:, :, None] & mask[:, None, :]
+
+
+def test_layer_norm_matches_oracle():
+    g = torch.Generator().manual_seed(1)
+    for rows, cols, dtype in ((4097, 128, torch.bfloat16), (300, 384, torch.bfloat16), (77, 100, torch.float32)):
+        x = (torch.randn(rows, cols, generator=g) * 2 + 0.5).to(dtype)
+        w = 1 + 0.1 * torch.randn(cols, generator=g)
+        b = 0.05 * torch.randn(cols, generator=g)
+        got = kernels.layer_norm(x.cuda(), w.cuda(), b.cuda(), 1e-5).cpu()
+        want = ps.layer_norm(x.double(), w.double(), b.double(), 1e-5)
+        assert got.dtype == dtype
+        _check(got, want, None, f"layer_norm {rows}x{cols} {dtype}")
+
+
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("n,lengths", [(64, None), (100, [77]), (130, [130, 41])])
+def test_trimul_matches_oracle(outgoing, n, lengths):
+    batch = len(lengths) if lengths else 1
+    z, mask = _pair(n, batch, seed=n, lengths=lengths)
+    m = randomise(factories.triangle_multiplication(128, outgoing=outgoing), seed=n).cuda()
+    m.set_backend("hip")
+    got = m.delta(z.cuda(), mask.cuda()).cpu()
+    want = ps.triangle_multiplication(z, mask, m.state_dict(), outgoing=outgoing, dtype=torch.float64) - z.double()
+    _check(got, want, _pairs(mask), f"trimul outgoing={outgoing} n={n}")
+    full = m(z.cuda(), mask.cuda()).cpu()
+    torch.testing.assert_close(full.float(), (z.float() + got.float()), atol=3e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("model", ["af3", "protenix"])
+@pytest.mark.parametrize("n,lengths", [(64, None), (100, [61]), (160, [160, 129])])
+def test_triattn_matches_oracle(starting, model, n, lengths):
+    batch = len(lengths) if lengths else 1
+    z, mask = _pair(n, batch, seed=7 * n, lengths=lengths)
+    m = randomise(factories.triangle_attention(128, 4, starting=starting, model=model), seed=n).cuda()
+    m.set_backend("hip")
+    got = m.delta(z.cuda(), mask.cuda()).cpu()
+    want = ps.triangle_attention(z, mask, m.state_dict(), starting=starting, n_head=4,
+                                 transposed_bias=m.transposed_bias, dtype=torch.float64) - z.double()
+    _check(got, want, _pairs(mask), f"triattn starting={starting} {model} n={n}")
+
+
+def test_transition_matches_oracle():
+    z, _ = _pair(72, 2, seed=3)
+    m = randomise(factories.transition(128, 4), seed=5).cuda()
+    m.set_backend("hip")
+    got = m.delta(z.cuda()).cpu()
+    want = ps.transition(z, m.state_dict(), dtype=torch.float64) - z.double()
+    _check(got, want, None, "transition")
+
+
+def test_padding_is_bitwise_invisible_to_the_valid_region():
+    n, length = 96, 70
+    z, mask = _pair(n, 1, seed=11, lengths=[length])
+    z2 = z.clone()
+    g = torch.Generator().manual_seed(12)
+    z2[0, length:] = (100 * torch.randn(n - length, n, 128, generator=g)).bfloat16()
+    z2[0, :, length:] = (-50 * torch.randn(n, n - length, 128, generator=g)).bfloat16()
+    block = randomise(factories.pairformer_block(d_pair=128, triangle_model="af3"), seed=13).cuda()
+    block.set_backend("hip")
+    a = block(z.cuda(), mask.cuda()).cpu()
+    b = block(z2.cuda(), mask.cuda()).cpu()
+    assert torch.equal(a[0, :length, :length], b[0, :length, :length])
+
+
+def test_flash_core_large_logits_and_exact_masking():
+    """The core alone, against an fp32 torch softmax, with logits of several hundred nats
+    (the failure of a max-free softmax) and masked keys whose values must not matter."""
+    B, H, R, n = 1, 4, 3, 128
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(B, H, R, n, 32, generator=g)
+    k = torch.randn(B, H, R, n, 32, generator=g)
+    v = torch.randn(B, H, R, n, 32, generator=g)
+    bias = 300 * torch.randn(B, H, n, n, generator=g)  # log2 units: up to ~1000 nats
+    keep = torch.rand(n, generator=g) > 0.3
+    bias_m = torch.where(keep[None, None, None, :], bias, torch.tensor(float("-inf")))
+    qb, kb, vb = q.bfloat16(), k.bfloat16(), v.bfloat16()
+    bh = bias_m.half()
+    vt = vb.transpose(-1, -2).contiguous()
+    out = torch.zeros(B, R, n, H * 32, dtype=torch.bfloat16, device="cuda")
+    kernels.flash_attention_bias(qb.cuda(), kb.cuda(), vt.cuda(), bh.cuda(), out, rows_valid=R, n_valid=n)
+    logits = qb.float() @ kb.float().transpose(-1, -2) + bh.float()[:, :, None]  # [B,H,R,n,n] (log2)
+    w = torch.softmax(logits * 0.6931471805599453, dim=-1)
+    want = (w @ vb.float()).permute(0, 2, 3, 1, 4).reshape(B, R, n, H * 32)
+    got = out.cpu().float()
+    assert torch.isfinite(got).all()
+    _check(got, want.double(), None, "flash core, large logits")
+    v2 = vb.clone()
+    v2[..., ~keep, :] = 1e4
+    vt2 = v2.transpose(-1, -2).contiguous()
+    out2 = torch.zeros_like(out)
+    kernels.flash_attention_bias(qb.cuda(), kb.cuda(), vt2.cuda(), bh.cuda(), out2, rows_valid=R, n_valid=n)
+    assert torch.equal(out.cpu(), out2.cpu())
+
+
+def test_no_valid_key_gives_identity_update():
+    z, mask = _pair(64, 1, seed=31, lengths=[0])
+    m = randomise(factories.triangle_attention(128, 4, starting=True, model="af3"), seed=1).cuda()
+    m.set_backend("hip")
+    got = m(z.cuda(), mask.cuda()).cpu()
+    assert torch.isfinite(got.float()).all()
+    assert torch.equal(got, z)  # zero attention output -> zero update

@@ -1,0 +1,68 @@
+"""The C-ABI library on the CPU: it builds for gfx950, loads next to torch's HIP runtime and
+exports exactly what ``include/foldforge_amd.h`` declares. No kernel is launched here (no
+device); the workspace-size queries are pure host arithmetic and are checked against the
+layouts they describe.
+"""
+
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+
+from foldforge_amd import _native, build
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "foldforge_amd.h"
+
+
+def declared() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(ffk_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not build.LIBRARY.exists():
+        build.build()
+    return _native.lib()
+
+
+def test_header_and_binding_agree():
+    names = declared()
+    assert names, "no ffk_ entry point parsed from the header"
+    assert set(names) == set(_native.SIGNATURES), set(names) ^ set(_native.SIGNATURES)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    for name in declared():
+        assert hasattr(lib, name), name
+
+
+def test_version_and_error_text(lib):
+    assert lib.ffk_version() >= 100
+    assert isinstance(lib.ffk_last_error(), bytes)
+
+
+def test_workspace_sizes_follow_the_layouts(lib):
+    def up(x):
+        return (x + 255) // 256 * 256
+
+    b, n = 2, 300
+    np_ = 384
+    tm = lib.ffk_triangle_multiplication_workspace(b, n, 128, 128)
+    weights = up(4 * 128 * 128 * 2) + up(128 * 128 * 2) + up(128 * 128 * 2)
+    assert tm == weights + 3 * up(b * 128 * np_ * np_ * 2)
+    ta = lib.ffk_triangle_attention_workspace(b, n, 128, 4, 32)
+    weights = up(3 * 128 * 128 * 2) + up(32 * 128 * 2) + 2 * up(128 * 128 * 2)
+    qkv = 3 * up(b * 4 * np_ * np_ * 32 * 2)
+    assert ta == weights + qkv + up(b * 4 * np_ * np_ * 2) + up(b * n * n * 128 * 2)
+    assert lib.ffk_transition_workspace(128, 4) == 3 * up(4 * 128 * 128 * 2)
+    assert lib.ffk_triangle_multiplication_workspace(0, n, 128, 128) == 0
+
+
+def test_build_recipe_targets_gfx950_without_packed_fp32():
+    cmd = build.command()
+    assert "--offload-arch=gfx950" in cmd
+    assert "-packed-fp32-ops" in cmd
+    assert all(str(s).endswith(".hip") for s in build.sources())

@@ -1,0 +1,301 @@
+"""Pin the CPU oracle (``oracle/pairstack.py``) before trusting it.
+
+Checks, per function: the committed brute-force fixtures (``tests/golden``), fresh
+brute-force loops (``oracle/brute.py``), library routines that fix the maths
+(``torch.nn.functional.layer_norm``, ``scaled_dot_product_attention``), and invariants a
+plausible mistake breaks (outgoing/incoming transpose identity with swapped branches,
+softmax shift invariance, key-mask exactness, large-logit stability, the
+transposed-bias start/end identity). A planted mistake in the oracle must fail one of
+them: see ``test_a_planted_mistake_is_caught``.
+"""
+
+from __future__ import annotations
+
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import brute
+from oracle import pairstack as ps
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "pairstack_tiny.npz"
+F64 = torch.float64
+
+
+def _golden() -> dict[str, dict]:
+    data = np.load(GOLDEN)
+    cases: dict[str, dict] = {}
+    for key in data.files:
+        case, rest = key.split("/", 1)
+        entry = cases.setdefault(case, {"p": {}})
+        if rest.startswith("p/"):
+            entry["p"][rest[2:]] = torch.from_numpy(data[key])
+        else:
+            entry[rest] = torch.from_numpy(data[key])
+    return cases
+
+
+def _rand_params(shapes: dict[str, tuple[int, ...]], seed: int) -> dict[str, torch.Tensor]:
+    g = torch.Generator().manual_seed(seed)
+    out = {}
+    for name, shape in shapes.items():
+        noise = torch.randn(shape, generator=g, dtype=F64)
+        out[name] = 0.3 * noise if len(shape) > 1 else (1 + 0.1 * noise if name.endswith("weight") else 0.1 * noise)
+    return out
+
+
+def _tm_shapes(c: int, h: int) -> dict[str, tuple[int, ...]]:
+    return {"ln_pair.weight": (c,), "ln_pair.bias": (c,), "to_left.weight": (h, c),
+            "to_right.weight": (h, c), "to_left_gate.weight": (h, c), "to_right_gate.weight": (h, c),
+            "ln_out.weight": (h,), "ln_out.bias": (h,), "to_out.weight": (c, h), "to_gate.weight": (c, c)}
+
+
+def _ta_shapes(c: int, heads: int, d: int) -> dict[str, tuple[int, ...]]:
+    return {"ln_pair.weight": (c,), "ln_pair.bias": (c,), "to_bias.weight": (heads, c),
+            "to_query.weight": (heads * d, c), "to_key.weight": (heads * d, c),
+            "to_value.weight": (heads * d, c), "to_gate.weight": (heads * d, c),
+            "to_out.weight": (c, heads * d)}
+
+
+def _np(p: dict[str, torch.Tensor]) -> dict[str, np.ndarray]:
+    return {k: v.numpy() for k, v in p.items()}
+
+
+# ----------------------------------------------------------------------------- fixtures
+def test_golden_fixtures_match_the_oracle():
+    cases = _golden()
+    assert len(cases) == 8
+    for name, c in cases.items():
+        p = c["p"]
+        if name.startswith("trimul"):
+            got = ps.triangle_multiplication(c["z"], c["mask"], p, outgoing=name.endswith("out"), dtype=F64)
+        elif name.startswith("triattn"):
+            got = ps.triangle_attention(c["z"], c["mask"], p, starting="_start_" in name, n_head=2,
+                                        transposed_bias=name.endswith("tb"), dtype=F64)
+        elif name == "transition":
+            got = ps.transition(c["x"], p, dtype=F64)
+        else:
+            got = ps.attention_pair_bias(c["s"], c["z"], c["mask"], p, n_head=3, gate_bias=0.5, dtype=F64)
+        torch.testing.assert_close(got, c["expected"], rtol=1e-10, atol=1e-10, msg=name)
+
+
+def test_golden_fixtures_are_reproduced_by_the_brute_force():
+    import importlib.util
+
+    spec = importlib.util.spec_from_file_location("make_golden", GOLDEN.with_name("make_golden.py"))
+    mod = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mod)
+    fresh = mod.cases()
+    data = np.load(GOLDEN)
+    assert set(fresh) == set(data.files)
+    for k in data.files:
+        np.testing.assert_allclose(fresh[k], data[k], rtol=0, atol=1e-12, err_msg=k)
+
+
+# ----------------------------------------------------------------------------- LayerNorm
+def test_layer_norm_closed_form():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(7, 128, generator=g, dtype=F64) * 3 + 2
+    w = torch.randn(128, generator=g, dtype=F64)
+    b = torch.randn(128, generator=g, dtype=F64)
+    got = ps.layer_norm(x, w, b, 1e-5)
+    torch.testing.assert_close(got, F.layer_norm(x, (128,), w, b, 1e-5))
+    row = x[3]
+    mu = row.sum() / 128
+    var = ((row - mu) ** 2).sum() / 128
+    torch.testing.assert_close(got[3], (row - mu) / torch.sqrt(var + 1e-5) * w + b)
+    # no affine: zero mean, unit (biased) variance up to eps
+    y = ps.layer_norm(x, None, None, 0.0)
+    torch.testing.assert_close(y.mean(-1), torch.zeros(7, dtype=F64), atol=1e-12, rtol=0)
+    torch.testing.assert_close(y.var(-1, unbiased=False), torch.ones(7, dtype=F64))
+
+
+# ----------------------------------------------------------------------------- triangle multiplication
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_trimul_matches_brute_force(outgoing):
+    n, c, h = 6, 5, 3
+    p = _rand_params(_tm_shapes(c, h), 11)
+    g = torch.Generator().manual_seed(12)
+    z = torch.randn(2, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(2, n, dtype=torch.bool)
+    mask[1, -2:] = False
+    got = ps.triangle_multiplication(z, mask, p, outgoing=outgoing, dtype=F64)
+    want = brute.triangle_multiplication(z.numpy(), mask.numpy(), _np(p), outgoing=outgoing)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+
+
+def test_trimul_outgoing_is_incoming_on_the_transpose_with_branches_swapped():
+    n, c, h = 7, 6, 4
+    p = _rand_params(_tm_shapes(c, h), 21)
+    g = torch.Generator().manual_seed(22)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(1, n, dtype=torch.bool)
+    mask[0, 2] = False
+    swapped = dict(p)
+    swapped["to_left.weight"], swapped["to_right.weight"] = p["to_right.weight"], p["to_left.weight"]
+    swapped["to_left_gate.weight"], swapped["to_right_gate.weight"] = p["to_right_gate.weight"], p["to_left_gate.weight"]
+    a = ps.triangle_multiplication(z, mask, p, outgoing=True, dtype=F64)
+    b = ps.triangle_multiplication(z.transpose(1, 2), mask, swapped, outgoing=False, dtype=F64).transpose(1, 2)
+    torch.testing.assert_close(a, b)
+
+
+def test_trimul_masked_tokens_contribute_nothing():
+    n, c, h = 6, 5, 3
+    p = _rand_params(_tm_shapes(c, h), 31)
+    g = torch.Generator().manual_seed(32)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(1, n, dtype=torch.bool)
+    mask[0, 4:] = False
+    z2 = z.clone()
+    z2[0, 4:, :, :] = 1e3 * torch.randn(2, n, c, generator=g, dtype=F64)
+    z2[0, :, 4:, :] = -1e3
+    a = ps.triangle_multiplication(z, mask, p, outgoing=True, dtype=F64)
+    b = ps.triangle_multiplication(z2, mask, p, outgoing=True, dtype=F64)
+    torch.testing.assert_close(a[0, :4, :4], b[0, :4, :4], rtol=1e-12, atol=1e-12)
+
+
+# ----------------------------------------------------------------------------- triangle attention
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("transposed", [False, True])
+def test_triattn_matches_brute_force(starting, transposed):
+    n, c, heads, d = 6, 5, 2, 3
+    p = _rand_params(_ta_shapes(c, heads, d), 41)
+    g = torch.Generator().manual_seed(42)
+    z = torch.randn(2, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(2, n, dtype=torch.bool)
+    mask[0, 1] = False
+    mask[1, :] = False  # no valid key at all: the stated zero-output convention
+    got = ps.triangle_attention(z, mask, p, starting=starting, n_head=heads,
+                                transposed_bias=transposed, dtype=F64, row_chunk=2)
+    want = brute.triangle_attention(z.numpy(), mask.numpy(), _np(p), starting=starting,
+                                    n_head=heads, transposed_bias=transposed)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+
+
+def test_triattn_core_equals_sdpa_math():
+    g = torch.Generator().manual_seed(5)
+    q, k, v = (torch.randn(3, 4, 9, 8, generator=g, dtype=F64) for _ in range(3))
+    bias = torch.randn(1, 4, 9, 9, generator=g, dtype=F64)
+    keep = torch.ones(1, 1, 1, 9, dtype=torch.bool)
+    got = ps._masked_softmax_attention(q, k, v, bias, keep, 8**-0.5)
+    want = F.scaled_dot_product_attention(q, k, v, attn_mask=bias.expand(3, 4, 9, 9), scale=8**-0.5)
+    torch.testing.assert_close(got, want)
+
+
+def test_triattn_softmax_shift_invariance_and_mask_exactness():
+    g = torch.Generator().manual_seed(6)
+    q, k, v = (torch.randn(2, 4, 7, 8, generator=g, dtype=F64) for _ in range(3))
+    bias = torch.randn(1, 4, 7, 7, generator=g, dtype=F64)
+    keep = torch.tensor([True, True, False, True, False, True, True])[None, None, None, :]
+    base = ps._masked_softmax_attention(q, k, v, bias, keep, 0.3)
+    shifted = ps._masked_softmax_attention(q, k, v, bias + torch.randn(1, 4, 7, 1, generator=g, dtype=F64) * 50,
+                                           keep, 0.3)
+    torch.testing.assert_close(base, shifted)
+    # a masked key's value has no influence at all
+    v2 = v.clone()
+    v2[..., 2, :] = 1e6
+    v2[..., 4, :] = float("nan")
+    torch.testing.assert_close(ps._masked_softmax_attention(q, k, torch.nan_to_num(v2, nan=0.0), bias, keep, 0.3), base)
+
+
+def test_triattn_large_logits_stay_finite_and_match_brute_force():
+    n, c, heads, d = 5, 4, 2, 2
+    p = _rand_params(_ta_shapes(c, heads, d), 51)
+    p["to_bias.weight"] = p["to_bias.weight"] * 150.0  # logits of several hundred nats
+    g = torch.Generator().manual_seed(52)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(1, n, dtype=torch.bool)
+    got = ps.triangle_attention(z, mask, p, starting=True, n_head=heads, dtype=F64)
+    assert torch.isfinite(got).all()
+    want = brute.triangle_attention(z.numpy(), mask.numpy(), _np(p), starting=True, n_head=heads)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-10, atol=1e-10)
+
+
+def test_transposed_bias_ending_node_is_starting_node_on_the_transpose():
+    n, c, heads, d = 6, 5, 2, 3
+    p = _rand_params(_ta_shapes(c, heads, d), 61)
+    g = torch.Generator().manual_seed(62)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(1, n, dtype=torch.bool)
+    mask[0, 0] = False
+    end = ps.triangle_attention(z, mask, p, starting=False, n_head=heads, transposed_bias=True, dtype=F64)
+    start_t = ps.triangle_attention(z.transpose(1, 2), mask, p, starting=True, n_head=heads, dtype=F64)
+    torch.testing.assert_close(end, start_t.transpose(1, 2))
+    # the AF3 (un-transposed bias) ending node is a different function
+    af3 = ps.triangle_attention(z, mask, p, starting=False, n_head=heads, transposed_bias=False, dtype=F64)
+    assert (af3 - end).abs().max() > 1e-3
+
+
+# ----------------------------------------------------------------------------- transition / APB
+def test_transition_matches_brute_force_and_closed_form():
+    c = 6
+    p = _rand_params({"ln_in.weight": (c,), "ln_in.bias": (c,), "expand_a.weight": (4 * c, c),
+                      "expand_b.weight": (4 * c, c), "squeeze.weight": (c, 4 * c)}, 71)
+    g = torch.Generator().manual_seed(72)
+    x = torch.randn(2, 3, 4, c, generator=g, dtype=F64)
+    got = ps.transition(x, p, dtype=F64)
+    np.testing.assert_allclose(got.numpy(), brute.transition(x.numpy(), _np(p)), rtol=1e-11, atol=1e-11)
+    h = F.layer_norm(x, (c,), p["ln_in.weight"], p["ln_in.bias"], 1e-5)
+    a, b = h @ p["expand_a.weight"].T, h @ p["expand_b.weight"].T
+    torch.testing.assert_close(got, x + (a * torch.sigmoid(a) * b) @ p["squeeze.weight"].T)
+
+
+def test_attention_pair_bias_matches_brute_force():
+    n, cs, c, hs = 6, 8, 5, 2
+    p = _rand_params({"ln_single.weight": (cs,), "ln_single.bias": (cs,), "to_query.weight": (cs, cs),
+                      "to_query.bias": (cs,), "to_key.weight": (cs, cs), "to_value.weight": (cs, cs),
+                      "ln_pair.weight": (c,), "to_bias.weight": (hs, c), "to_gate.weight": (cs, cs),
+                      "to_out.weight": (cs, cs)}, 81)
+    g = torch.Generator().manual_seed(82)
+    s = torch.randn(2, n, cs, generator=g, dtype=F64)
+    z = torch.randn(2, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(2, n, dtype=torch.bool)
+    mask[0, -3:] = False
+    got = ps.attention_pair_bias(s, z, mask, p, n_head=hs, gate_bias=-1.0, dtype=F64)
+    want = brute.attention_pair_bias(s.numpy(), z.numpy(), mask.numpy(), _np(p), n_head=hs, gate_bias=-1.0)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+
+
+def test_block_is_the_composition_of_the_pinned_ops():
+    n, c, h, heads, d, cs, hs = 5, 6, 4, 2, 3, 6, 2
+    params = {}
+    for prefix, shapes, seed in (
+        ("tri_multi_outgoing", _tm_shapes(c, h), 1), ("tri_multi_incoming", _tm_shapes(c, h), 2),
+        ("tri_atten_starting", _ta_shapes(c, heads, d), 3), ("tri_atten_ending", _ta_shapes(c, heads, d), 4),
+    ):
+        params.update({f"{prefix}.{k}": v for k, v in _rand_params(shapes, seed).items()})
+    tr = {"ln_in.weight": (c,), "ln_in.bias": (c,), "expand_a.weight": (4 * c, c),
+          "expand_b.weight": (4 * c, c), "squeeze.weight": (c, 4 * c)}
+    params.update({f"transition_pair.{k}": v for k, v in _rand_params(tr, 5).items()})
+    g = torch.Generator().manual_seed(9)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(1, n, dtype=torch.bool)
+    mask[0, -1] = False
+    got = ps.pairformer_block(z, mask, params, n_head_pair=heads, dtype=F64)
+    x = z.numpy()
+    sub = lambda pre: {k[len(pre) + 1:]: v.numpy() for k, v in params.items() if k.startswith(pre + ".")}  # noqa: E731
+    x = brute.triangle_multiplication(x, mask.numpy(), sub("tri_multi_outgoing"), outgoing=True)
+    x = brute.triangle_multiplication(x, mask.numpy(), sub("tri_multi_incoming"), outgoing=False)
+    x = brute.triangle_attention(x, mask.numpy(), sub("tri_atten_starting"), starting=True, n_head=heads)
+    x = brute.triangle_attention(x, mask.numpy(), sub("tri_atten_ending"), starting=False, n_head=heads)
+    x = brute.transition(x, sub("transition_pair"))
+    np.testing.assert_allclose(got.numpy(), x, rtol=1e-10, atol=1e-10)
+
+
+def test_a_planted_mistake_is_caught(monkeypatch):
+    """A transposed operand planted in the oracle's contraction breaks the brute-force check."""
+    n, c, h = 5, 4, 3
+    p = _rand_params(_tm_shapes(c, h), 91)
+    g = torch.Generator().manual_seed(92)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(1, n, dtype=torch.bool)
+    want = brute.triangle_multiplication(z.numpy(), mask.numpy(), _np(p), outgoing=True)
+    real = ps.triangle_multiplication(z, mask, p, outgoing=True, dtype=F64)
+    np.testing.assert_allclose(real.numpy(), want, rtol=1e-11, atol=1e-11)
+    broken = dict(p)
+    broken["to_left.weight"], broken["to_right.weight"] = p["to_right.weight"], p["to_left.weight"]
+    wrong = ps.triangle_multiplication(z, mask, broken, outgoing=True, dtype=F64)
+    assert np.abs(wrong.numpy() - want).max() > 1e-3

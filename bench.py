@@ -88,7 +88,8 @@ def flash_roofline(n: int, length: int, reps: int) -> dict:
     vt = torch.randn(1, heads, n, d, np_, device="cuda", generator=g).bfloat16()
     bias = torch.randn(1, heads, np_, np_, device="cuda", generator=g)
     keep = torch.arange(np_, device="cuda") < length
-    bias = torch.where(keep[None, None, None, :], bias, torch.tensor(float("-inf"), device="cuda")).half()
+    bias = torch.where(keep[None, None, None, :], bias, torch.tensor(float("-inf"), device="cuda"))
+    bias = kernels.blocked_bias(bias)
     out = torch.empty(1, n, n, heads * d, device="cuda", dtype=torch.bfloat16)
 
     def launch():

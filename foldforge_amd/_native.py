@@ -42,8 +42,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ffk_flash_attention_bias": (
         c_int32,
         [c_void_p] * 5
-        + [c_int64, c_int32, c_int64, c_int64, c_int64, c_int64, c_int32, c_int64, c_int64,
-           c_int64, c_void_p],
+        + [c_int64, c_int32, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
+           c_void_p],
     ),
     "ffk_transition_workspace": (c_size_t, [c_int32, c_int32]),
     "ffk_transition": (

@@ -122,7 +122,7 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
 
 struct TriattnWs {
   bf16 *wqkv, *wb, *wg, *wo, *q, *k, *vt, *o;
-  f16* bias;
+  float* bias;
   size_t bytes;
 };
 TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d) {
@@ -137,7 +137,7 @@ TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d
   w.q = cv.take<bf16>((size_t)batch * heads * np * np * d);
   w.k = cv.take<bf16>((size_t)batch * heads * np * np * d);
   w.vt = cv.take<bf16>((size_t)batch * heads * np * np * d);
-  w.bias = cv.take<f16>((size_t)batch * heads * np * np);
+  w.bias = cv.take<float>((size_t)batch * heads * np * np);
   w.o = cv.take<bf16>((size_t)batch * n * n * hd);
   w.bytes = cv.used;
   return w;
@@ -318,15 +318,15 @@ int32_t ffk_triangle_attention(
 int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
                                  const void* bias, void* o, int64_t batch, int32_t heads,
                                  int64_t rows, int64_t n_pad, int64_t rows_valid,
-                                 int64_t n_valid, int32_t bias_key_major, int64_t o_sb,
-                                 int64_t o_sr, int64_t o_sj, void* stream) {
+                                 int64_t n_valid, int64_t o_sb, int64_t o_sr, int64_t o_sj,
+                                 void* stream) {
   if (int32_t s = check_device()) return s;
   if (!q || !k || !v_t || !bias || !o) return fail(FFK_ERR_INVALID, "flash_attention_bias: null tensor");
-  if (batch <= 0 || heads <= 0 || rows <= 0 || n_pad <= 0 || n_pad % 128 != 0)
-    return fail(FFK_ERR_INVALID, "flash_attention_bias: bad shape (n_pad %lld must be a positive multiple of 128)", (long long)n_pad);
+  if (batch <= 0 || heads <= 0 || rows <= 0 || n_pad <= 0 || n_pad % 128 != 0 || rows % 4 != 0)
+    return fail(FFK_ERR_INVALID, "flash_attention_bias: bad shape (n_pad %lld must be a positive multiple of 128, rows %lld of 4)", (long long)n_pad, (long long)rows);
   if (rows_valid < 0 || rows_valid > rows || n_valid < 0 || n_valid > n_pad)
     return fail(FFK_ERR_INVALID, "flash_attention_bias: valid extents exceed the padded shape");
-  if (batch * heads > 65535 || rows > 65535)
+  if ((n_pad + 255) / 256 * (rows / 4) * batch * heads > 0x7fffffffLL)
     return fail(FFK_ERR_INVALID, "flash_attention_bias: grid too large");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v_t) || !aligned16(bias))
     return fail(FFK_ERR_INVALID, "flash_attention_bias: q/k/v_t/bias must be 16-byte aligned");
@@ -336,7 +336,7 @@ int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
   f.q = static_cast<const bf16*>(q);
   f.k = static_cast<const bf16*>(k);
   f.vt = static_cast<const bf16*>(v_t);
-  f.bias = static_cast<const f16*>(bias);
+  f.bias = static_cast<const float*>(bias);
   f.o = static_cast<bf16*>(o);
   f.batch = batch;
   f.rows = rows;
@@ -347,7 +347,6 @@ int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
   f.o_sr = o_sr;
   f.o_sj = o_sj;
   f.heads = heads;
-  f.key_major = bias_key_major ? 1 : 0;
   if (rows_valid == 0 || n_valid == 0) return ok();
   launch_flash(f, static_cast<hipStream_t>(stream));
   return check_launch("flash_attention_bias");

@@ -61,6 +61,33 @@ __device__ __forceinline__ void mma_rows(const bf16* a_row, const bf16* b_row, i
   }
 }
 
+// The hardware deals workgroup w to XCD w % 8 (each XCD has its own L2). Renumber so that
+// every XCD receives one contiguous range of logical workgroup ids: neighbours in the
+// logical order (which share operands) then share an L2. Identity when total % 8 != 0.
+__device__ __forceinline__ uint32_t xcd_remap(uint32_t wg, uint32_t total) {
+  if (total % 8u != 0u) return wg;
+  return (wg % 8u) * (total / 8u) + wg / 8u;
+}
+
+// Smallest bf16-representable value >= x (x finite).
+__device__ __forceinline__ float bf16_ceil(float x) {
+  uint32_t u = __float_as_uint(x);
+  if ((u & 0xffffu) != 0u) u = (u & 0xffff0000u) + (x > 0.f ? 0x10000u : 0u);
+  return __uint_as_float(u);
+}
+
+// Combine x with the value of lane l ^ 32 (one v_permlane32_swap). After the swap of x
+// with itself each lane holds {x, partner} in the two results, in an order that depends
+// on the half, so only symmetric combinations are formed.
+__device__ __forceinline__ float pair_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Reduction over groups of 16 consecutive lanes.
 __device__ __forceinline__ float sum16(float v) {
   v += __shfl_xor(v, 8, 16);

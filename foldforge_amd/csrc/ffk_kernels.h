@@ -32,7 +32,7 @@ struct TriattnArgs {
   const bf16* wg;    // [128][128] to_gate
   const bf16* wo;    // [128][128] to_out
   bf16 *q, *k, *vt;  // [batch * heads][np][np][32], vt: [batch * heads][np][32][np]
-  f16* bias;         // [batch * heads][np][np]
+  float* bias;       // [batch * heads][np / 32][np / 32][2][32][16] blocked, see triattn.hip
   bf16* o;           // [batch][n][n][128] z-frame attention output
   bf16* out;
   int batch, n, np, heads, starting, transposed_bias, residual;
@@ -42,10 +42,10 @@ void launch_triattn(const TriattnArgs& a, hipStream_t stream);
 
 struct FlashArgs {
   const bf16 *q, *k, *vt;
-  const f16* bias;
+  const float* bias;  // blocked pair bias (log2 units, -inf at masked keys)
   bf16* o;
   int64_t batch, rows, np, rows_valid, n_valid, o_sb, o_sr, o_sj;
-  int heads, key_major;
+  int heads;
 };
 void launch_flash(const FlashArgs& a, hipStream_t stream);
 

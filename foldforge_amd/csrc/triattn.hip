@@ -3,21 +3,30 @@
 // Equations: src/foldforge/models/checkpoints/legacy/attention.py:108-163 with the masked
 // softmax of legacy/reference/attention.py:77-100. Three kernels per call:
 //   1. triattn_project  z -> LN_pair -> q (scaled by d^-1/2 log2 e), k, v^T and the pair
-//                       bias (log2 e scaled, fp16, -inf at masked keys). A tile is 128
+//                       bias (log2 e scaled, fp32, -inf at masked keys). A tile is 128
 //                       positions along one attention row: a row of z (starting) or a
-//                       column of z (ending), so every store is contiguous.
-//   2. flash_attn_bias  per (row, head, 128 queries): S^T = bias^T + K Q^T on MFMA (the
-//                       bias tile is the accumulator's initial value), online softmax in
-//                       fp32 with exp2, O^T += V^T P^T on MFMA. The N^3 H logits never
-//                       leave registers.
+//                       column of z (ending), so the q / k / v^T stores are contiguous. The
+//                       bias is written in the flash kernel's register order (below).
+//   2. flash_attn_bias  the attention core; the N^3 H logits never leave registers.
 //   3. triattn_output   out = z + (sigmoid(LN_pair(z) W_g^T) * o) W_out^T.
 // The gate is recomputed from z in kernel 3 rather than stored (z is read there for the
 // residual anyway).
 //
-// Flash layout (one wave = 32 queries): S^T is a 32 keys x 32 queries MFMA tile, so each
-// lane owns ONE query and 16 of the 32 keys: the softmax row max / sum are in-lane plus a
-// single exchange with lane l ^ 32. P^T comes out of the S^T accumulator already in the
-// B-operand order of the P V product; V^T rows are read with the matching key order.
+// Flash core (one wave = 32 queries of up to 4 attention rows; 8 waves per workgroup):
+//  * S^T (32 keys x 32 queries) is one MFMA accumulator. Its initial value is the pair-bias
+//    tile, loaded straight into the accumulator registers (fp32, stored by kernel 1 in
+//    exactly that register order: four 16-byte loads per lane, no VALU work), and shared
+//    by the 4 attention rows of the workgroup (the bias does not depend on the row).
+//  * The running offset m is subtracted by the matrix unit: a third k-step multiplies a
+//    constant 1 on the key side by -m on the query side (m kept bf16-representable).
+//  * Lazy softmax: the offset is fixed from the first tile that has a finite logit and
+//    only moved when a tile's exp2 sum overflows 2^64, so the common step is exp2,
+//    bf16 packing and a v_dot2 row sum: about one VALU op plus one exp per logit.
+//  * K and V^T tiles of the 4 rows are staged in LDS (64 keys per stage, double
+//    buffered) and shared by the 8 waves; V^T is stored with the keys of each 16-key
+//    group permuted so that a lane's 8 keys of the P V product are one 16-byte read.
+//  * Each lane owns one query; P^T comes out of the S^T accumulator already in the
+//    B-operand order of the P V product.
 #include <math.h>
 
 #include "ffk_device.h"
@@ -27,14 +36,27 @@ namespace ffk {
 
 constexpr int kTaTP = 128;  // projection tile (positions)
 constexpr int kTaTO = 64;   // output tile (positions)
-constexpr int kTaQ = 128;   // queries per flash workgroup
-constexpr int kTaK = 32;    // keys per flash step
+constexpr int kFR = 4;      // attention rows per flash workgroup (share the bias tile)
+constexpr int kFW = 8;      // waves per flash workgroup, 32 queries each
+constexpr int kFK = 64;     // keys per LDS stage
+constexpr int kKS = 40;     // LDS row stride (elements) of a K tile
+constexpr int kVS = 72;     // LDS row stride (elements) of a V^T tile
+constexpr float kLazyLimit = 1.8446744073709552e19f;  // 2^64
+
+// Index of bias entry (query, key) in the blocked layout
+//   [bh][query / 32][key / 32][g][query % 32][r] (16 fp32 per lane), key % 32 = 8(r/4) + 4g + r%4,
+// i.e. lane 32 g + query % 32 holds accumulator register r of the S^T tile.
+__device__ __forceinline__ int64_t bias_index(int64_t bh, int64_t nb, int64_t query, int64_t key) {
+  const int kk = (int)(key & 31);
+  const int a = kk >> 3, g = (kk >> 2) & 1, t = kk & 3;
+  return ((((bh * nb + (query >> 5)) * nb + (key >> 5)) * 2 + g) * 32 + (query & 31)) * 16 + 4 * a + t;
+}
 
 // grid (np / 128, np, batch); block 256.
 __global__ __launch_bounds__(256) void triattn_project(
     const bf16* __restrict__ z, const uint8_t* __restrict__ mask, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ wqkv, const bf16* __restrict__ wb,
-    bf16* __restrict__ qo, bf16* __restrict__ ko, bf16* __restrict__ vto, f16* __restrict__ bo,
+    bf16* __restrict__ qo, bf16* __restrict__ ko, bf16* __restrict__ vto, float* __restrict__ bo,
     int n, int np, int heads, int starting, int transposed_bias, float eps) {
   __shared__ __attribute__((aligned(16))) bf16 xh[kTaTP * kRow];
   __shared__ float keep[kTaTP];
@@ -54,8 +76,8 @@ __global__ __launch_bounds__(256) void triattn_project(
     }
   }
   ln_tile_128<kTaTP>(base, stride, valid, ln_w, ln_b, eps, xh, nullptr);
-  // The bias entry at tile position t is for key s0 + t (query-major layout) or for key r
-  // (key-major layout: the AF3 ending node, whose bias is not transposed).
+  // The bias entry at tile position t is (query r, key s0 + t), except for the AF3 ending
+  // node (bias from the un-transposed pair), where it is (query s0 + t, key r).
   const bool key_major = !starting && !transposed_bias;
   if (tid < kTaTP) {
     const int key = key_major ? r : s0 + tid;
@@ -66,7 +88,6 @@ __global__ __launch_bounds__(256) void triattn_project(
   const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int p0 = 32 * wave;  // this wave's 32 positions
   const bf16* xrow_li = xh + (p0 + li) * kRow;
-  const int64_t rowplane = (int64_t)np * np;
   // q, k: D[position][d] (A = x rows, B = weight rows); lane li holds channel d = li.
 #pragma unroll 1
   for (int t = 0; t < 2 * heads; ++t) {
@@ -92,103 +113,229 @@ __global__ __launch_bounds__(256) void triattn_project(
     f32x16 acc = zero16();
     mma_rows<128>(wb + (int64_t)li * 128, xrow_li, g, acc);
     const float kp = keep[p0 + li];
+    const int64_t nb = np / 32;
+    const int64_t s = s0 + p0 + li;
+    const int64_t query = key_major ? s : r;
+    const int64_t key = key_major ? r : s;
     if (g == 0) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         if (q < heads) {
           const float v = kp != 0.f ? acc[q] : -INFINITY;
-          bo[(((int64_t)b * heads + q) * np + r) * np + s0 + p0 + li] = (f16)v;
+          bo[bias_index((int64_t)b * heads + q, nb, query, key)] = v;
         }
       }
     }
   }
 }
 
-// grid (np / 128, rows, batch * heads); block 256 (4 waves x 32 queries).
-template <bool KEY_MAJOR>
-__global__ __launch_bounds__(256) void flash_attn_bias(
+struct __attribute__((aligned(16))) FlashLds {
+  bf16 k[2][kFR][kFK * kKS];
+  bf16 v[2][kFR][32 * kVS];
+};
+
+// Lazily-offset softmax step for one attention row: S holds bias + q.k - m for 32 keys
+// of this lane's query. Writes the bf16 P^T operands, accumulates the row sum and, when
+// needed (first finite tile, exp2 sum overflow), moves the offset m and rescales O / l.
+__device__ __forceinline__ void softmax_step(f32x16& S, float& m, float& l, bool& set, f32x16& O,
+                                             bf16x8& negm, int g, bf16x8& p0, bf16x8& p1) {
+  const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
+  float ts = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) {
+    const bf16x2 a = {(bf16)fast_exp2(S[i]), (bf16)fast_exp2(S[i + 1])};
+    const bf16x2 c = {(bf16)fast_exp2(S[i + 8]), (bf16)fast_exp2(S[i + 9])};
+    p0[i] = a[0];
+    p0[i + 1] = a[1];
+    p1[i] = c[0];
+    p1[i + 1] = c[1];
+    ts = __builtin_amdgcn_fdot2_f32_bf16(a, ones, ts, false);
+    ts = __builtin_amdgcn_fdot2_f32_bf16(c, ones, ts, false);
+  }
+  const bool bad = !set || !(ts < kLazyLimit);
+  if (__builtin_amdgcn_ballot_w64(bad) != 0) {
+    // exact tile maximum of this query (both lane halves hold its keys)
+    float tm = S[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) tm = fmaxf(tm, S[i]);
+    tm = pair_max(tm);
+    if (tm > -INFINITY && (!set || tm > 0.f)) {
+      const float mn = bf16_ceil(m + tm);
+      const float shift = mn - m;
+      const float alpha = fast_exp2(-shift);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        S[i] -= shift;
+        O[i] *= alpha;
+      }
+      l *= alpha;
+      m = mn;
+      set = true;
+      negm[0] = g == 0 ? (bf16)(-mn) : (bf16)0.f;
+    }
+    ts = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; i += 2) {
+      const bf16x2 a = {(bf16)fast_exp2(S[i]), (bf16)fast_exp2(S[i + 1])};
+      const bf16x2 c = {(bf16)fast_exp2(S[i + 8]), (bf16)fast_exp2(S[i + 9])};
+      p0[i] = a[0];
+      p0[i + 1] = a[1];
+      p1[i] = c[0];
+      p1[i + 1] = c[1];
+      ts = __builtin_amdgcn_fdot2_f32_bf16(a, ones, ts, false);
+      ts = __builtin_amdgcn_fdot2_f32_bf16(c, ones, ts, false);
+    }
+  }
+  l += ts;
+}
+
+// grid (ceil(np / 256) * (np / 4) * batch * heads) workgroups, renumbered per XCD;
+// block 512 = 8 waves x 32 queries, 4 attention rows.
+__global__ __launch_bounds__(512) void flash_attn_bias(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ vt,
-    const f16* __restrict__ bias, bf16* __restrict__ o, int heads, int64_t rows, int64_t np,
+    const float* __restrict__ bias, bf16* __restrict__ o, int heads, int64_t rows, int64_t np,
     int64_t rows_valid, int64_t n_valid, int64_t o_sb, int64_t o_sr, int64_t o_sj) {
-  const int64_t j0 = (int64_t)blockIdx.x * kTaQ;
-  const int64_t r = blockIdx.y;
-  if (r >= rows_valid || j0 >= n_valid) return;  // whole workgroup outside the output
-  const int64_t bh = blockIdx.z;
+  __shared__ FlashLds lds;
+  const uint32_t nqb = (uint32_t)((np + 32 * kFW - 1) / (32 * kFW));
+  const uint32_t nrg = (uint32_t)(rows / kFR);
+  const uint32_t total = gridDim.x;
+  const uint32_t wg = xcd_remap(blockIdx.x, total);
+  const uint32_t qb = wg % nqb;
+  const uint32_t rg = (wg / nqb) % nrg;
+  const int64_t bh = wg / (nqb * nrg);
+  const int64_t j0 = (int64_t)qb * 32 * kFW;
+  const int64_t r0 = (int64_t)rg * kFR;
+  if (r0 >= rows_valid || j0 >= n_valid) return;  // whole workgroup outside the output
   const int64_t bidx = bh / heads;
   const int h = (int)(bh % heads);
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
-  const int64_t j = j0 + 32 * wave + li;  // this lane's query
+  const int64_t jw = j0 + 32 * wave;  // first query of this wave
+  const bool active = jw < np;        // the last query block may be partial
+  const int64_t j = jw + li;
+  const int64_t nb = np / 32;
 
-  const bf16* qrow = q + ((bh * rows + r) * np + j) * 32;
-  const bf16x8 q0 = ld8(qrow + 8 * g), q1 = ld8(qrow + 16 + 8 * g);
-  const bf16* kbase = k + (bh * rows + r) * np * 32;
-  const bf16* vrow = vt + ((bh * rows + r) * 32 + li) * np;  // row d = li of V^T
-  const f16* bb = bias + bh * np * np;
-
-  float m = -INFINITY, l = 0.f;
-  f32x16 O = zero16();
-#pragma unroll 1
-  for (int64_t kb = 0; kb < np; kb += kTaK) {
-    f32x16 S;
-    if (!KEY_MAJOR) {
-      const f16* brow = bb + j * np + kb + 4 * g;
+  bf16x8 qa[kFR][2];
+  bf16x8 negm[kFR];
+  float m[kFR], l[kFR];
+  bool set[kFR];
+  f32x16 O[kFR];
+  const bf16x8 zero8 = {};
+  bf16x8 ones_k = zero8;
+  ones_k[0] = g == 0 ? (bf16)1.f : (bf16)0.f;
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const f16x4 v4 = *reinterpret_cast<const f16x4*>(brow + 8 * qd);
-#pragma unroll
-        for (int t = 0; t < 4; ++t) S[4 * qd + t] = (float)v4[t];
-      }
+  for (int rr = 0; rr < kFR; ++rr) {
+    if (active) {
+      const bf16* qrow = q + ((bh * rows + r0 + rr) * np + j) * 32;
+      qa[rr][0] = ld8(qrow + 8 * g);
+      qa[rr][1] = ld8(qrow + 16 + 8 * g);
     } else {
-#pragma unroll
-      for (int qq = 0; qq < 16; ++qq) S[qq] = (float)bb[(kb + acc_row(qq, g)) * np + j];
+      qa[rr][0] = zero8;
+      qa[rr][1] = zero8;
     }
-    const bf16* krow = kbase + (kb + li) * 32;
-    S = mfma32(ld8(krow + 8 * g), q0, S);
-    S = mfma32(ld8(krow + 16 + 8 * g), q1, S);
-
-    float tmax = S[0];
-#pragma unroll
-    for (int qq = 1; qq < 16; ++qq) tmax = fmaxf(tmax, S[qq]);
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-    const float mnew = fmaxf(m, tmax);
-    const float muse = mnew == -INFINITY ? 0.f : mnew;
-    const float alpha = fast_exp2(m - muse);
-    float ps = 0.f;
-    bf16x8 p0, p1;
-#pragma unroll
-    for (int qq = 0; qq < 8; ++qq) {
-      const float e0 = fast_exp2(S[qq] - muse);
-      const float e1 = fast_exp2(S[qq + 8] - muse);
-      ps += e0 + e1;
-      p0[qq] = (bf16)e0;
-      p1[qq] = (bf16)e1;
-    }
-    l = l * alpha + ps;
-#pragma unroll
-    for (int qq = 0; qq < 16; ++qq) O[qq] *= alpha;
-    m = mnew;
-    // V^T operand in the key order of p0 / p1: keys {4g..4g+3, 8+4g..8+4g+3} (+16).
-    const bf16* vk = vrow + kb + 4 * g;
-    const bf16x4 va = *reinterpret_cast<const bf16x4*>(vk);
-    const bf16x4 vb = *reinterpret_cast<const bf16x4*>(vk + 8);
-    const bf16x4 vc = *reinterpret_cast<const bf16x4*>(vk + 16);
-    const bf16x4 vd = *reinterpret_cast<const bf16x4*>(vk + 24);
-    const bf16x8 a0 = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
-    const bf16x8 a1 = {vc[0], vc[1], vc[2], vc[3], vd[0], vd[1], vd[2], vd[3]};
-    O = mfma32(a0, p0, O);
-    O = mfma32(a1, p1, O);
+    negm[rr] = zero8;
+    m[rr] = 0.f;
+    l[rr] = 0.f;
+    set[rr] = false;
+    O[rr] = zero16();
   }
-  l += __shfl_xor(l, 32, 64);
-  if (j >= n_valid) return;
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  bf16* dst = o + bidx * o_sb + r * o_sr + j * o_sj + h * 32;
+
+  // K / V^T staging: per stage 4 rows x (64 keys x 64 B of K + 32 d x 128 B of V^T)
+  // = 2048 chunks of 16 bytes, 4 per thread.
+  const bf16* kbase = k + (bh * rows + r0) * np * 32;
+  const bf16* vbase = vt + (bh * rows + r0) * 32 * np;
+  bf16x8 pre[4];
+  auto gload = [&](int64_t key0) {
 #pragma unroll
-  for (int qd = 0; qd < 4; ++qd) {
-    bf16x4 w;
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + 512 * u;
+      const int part = c >> 10, rr = (c >> 8) & 3, w = c & 255;
+      if (part == 0) {
+        const int key = w >> 2, d8 = w & 3;
+        pre[u] = ld8(kbase + ((int64_t)rr * np + key0 + key) * 32 + 8 * d8);
+      } else {
+        const int d = w >> 3, k8 = w & 7;
+        pre[u] = ld8(vbase + ((int64_t)rr * 32 + d) * np + key0 + 8 * k8);
+      }
+    }
+  };
+  auto sstore = [&](int sb) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) w[t] = (bf16)(O[4 * qd + t] * inv);
-    *reinterpret_cast<bf16x4*>(dst + 8 * qd + 4 * g) = w;
+    for (int u = 0; u < 4; ++u) {
+      const int c = tid + 512 * u;
+      const int part = c >> 10, rr = (c >> 8) & 3, w = c & 255;
+      if (part == 0) {
+        const int key = w >> 2, d8 = w & 3;
+        *reinterpret_cast<bf16x8*>(&lds.k[sb][rr][key * kKS + 8 * d8]) = pre[u];
+      } else {
+        const int d = w >> 3, k8 = w & 7;
+        // keys 8 k8 .. 8 k8 + 7: within their 16-key group the first four go to
+        // 4 h .. 4 h + 3 and the last four to 8 + 4 h .. (h = k8 & 1)
+        bf16* dst = &lds.v[sb][rr][d * kVS + 16 * (k8 >> 1) + 4 * (k8 & 1)];
+        const bf16x4 lo = {pre[u][0], pre[u][1], pre[u][2], pre[u][3]};
+        const bf16x4 hi = {pre[u][4], pre[u][5], pre[u][6], pre[u][7]};
+        *reinterpret_cast<bf16x4*>(dst) = lo;
+        *reinterpret_cast<bf16x4*>(dst + 8) = hi;
+      }
+    }
+  };
+
+  const float* bias_w = bias + ((bh * nb + (active ? jw / 32 : 0)) * nb) * 1024 + lane * 16;
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  const int64_t nstage = np / kFK;
+#pragma unroll 1
+  for (int64_t st = 0; st < nstage; ++st) {
+    const int sb = (int)(st & 1);
+    const bool more = st + 1 < nstage;
+    if (more) gload((st + 1) * kFK);
+    if (active) {
+#pragma unroll
+      for (int sub = 0; sub < 2; ++sub) {
+        const int64_t kb = st * 2 + sub;
+        f32x16 binit;
+        {
+          const f32x4* bp = reinterpret_cast<const f32x4*>(bias_w + kb * 1024);
+#pragma unroll
+          for (int v4 = 0; v4 < 4; ++v4) {
+            const f32x4 t = bp[v4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) binit[4 * v4 + e] = t[e];
+          }
+        }
+#pragma unroll
+        for (int rr = 0; rr < kFR; ++rr) {
+          const bf16* krow = &lds.k[sb][rr][(sub * 32 + li) * kKS];
+          f32x16 S = mfma32(ld8(krow + 8 * g), qa[rr][0], binit);
+          S = mfma32(ld8(krow + 16 + 8 * g), qa[rr][1], S);
+          S = mfma32(ones_k, negm[rr], S);
+          bf16x8 p0, p1;
+          softmax_step(S, m[rr], l[rr], set[rr], O[rr], negm[rr], g, p0, p1);
+          const bf16* vrow = &lds.v[sb][rr][li * kVS + sub * 32 + 8 * g];
+          O[rr] = mfma32(ld8(vrow), p0, O[rr]);
+          O[rr] = mfma32(ld8(vrow + 16), p1, O[rr]);
+        }
+      }
+    }
+    if (more) sstore(sb ^ 1);
+    __syncthreads();
+  }
+  if (!active) return;
+#pragma unroll
+  for (int rr = 0; rr < kFR; ++rr) {
+    const float lt = pair_sum(l[rr]);
+    const int64_t r = r0 + rr;
+    if (r >= rows_valid || j >= n_valid) continue;
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    bf16* dst = o + bidx * o_sb + r * o_sr + j * o_sj + h * 32;
+#pragma unroll
+    for (int qd = 0; qd < 4; ++qd) {
+      bf16x4 w;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) w[t] = (bf16)(O[rr][4 * qd + t] * inv);
+      *reinterpret_cast<bf16x4*>(dst + 8 * qd + 4 * g) = w;
+    }
   }
 }
 
@@ -237,16 +384,11 @@ __global__ __launch_bounds__(256) void triattn_output(
 }
 
 void launch_flash(const FlashArgs& a, hipStream_t stream) {
-  dim3 grid(a.np / kTaQ, a.rows, a.batch * a.heads);
-  if (a.key_major) {
-    flash_attn_bias<true><<<grid, 256, 0, stream>>>(a.q, a.k, a.vt, a.bias, a.o, a.heads, a.rows,
-                                                    a.np, a.rows_valid, a.n_valid, a.o_sb, a.o_sr,
-                                                    a.o_sj);
-  } else {
-    flash_attn_bias<false><<<grid, 256, 0, stream>>>(a.q, a.k, a.vt, a.bias, a.o, a.heads,
-                                                     a.rows, a.np, a.rows_valid, a.n_valid,
-                                                     a.o_sb, a.o_sr, a.o_sj);
-  }
+  const int64_t nqb = (a.np + 32 * kFW - 1) / (32 * kFW);
+  const int64_t blocks = nqb * (a.rows / kFR) * a.batch * a.heads;
+  flash_attn_bias<<<dim3((unsigned)blocks), 32 * kFW, 0, stream>>>(
+      a.q, a.k, a.vt, a.bias, a.o, a.heads, a.rows, a.np, a.rows_valid, a.n_valid, a.o_sb, a.o_sr,
+      a.o_sj);
 }
 
 void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
@@ -267,7 +409,6 @@ void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
   f.rows_valid = a.n;
   f.n_valid = a.n;
   f.heads = a.heads;
-  f.key_major = (!a.starting && !a.transposed_bias) ? 1 : 0;
   // o is written in the frame of z: row r of the attention is a row (starting) or a
   // column (ending) of z.
   const int64_t c = 128;

@@ -191,32 +191,43 @@ def transition(
     return out
 
 
+def blocked_bias(bias: Tensor) -> Tensor:
+    """``bias [B, H, Np, Np]`` (query, key; log2 units) -> the flash kernel's blocked fp32 layout
+    ``[B * H, Np/32, Np/32, 2, 32, 16]``: entry ``[.., qb, kb, g, li, r]`` is query ``32 qb + li``,
+    key ``32 kb + 8 (r // 4) + 4 g + r % 4``."""
+    b, h, n1, n2 = bias.shape
+    _need(n1 == n2 and n1 % 32 == 0, "bias must be [B, H, Np, Np] with Np % 32 == 0")
+    nb = n1 // 32
+    t = bias.float().reshape(b * h, nb, 32, nb, 4, 2, 4)  # [bh, qb, li, kb, a, g, t]
+    return t.permute(0, 1, 3, 5, 2, 4, 6).contiguous()
+
+
 def flash_attention_bias(
     q: Tensor,
     k: Tensor,
     v_t: Tensor,
-    bias: Tensor,
+    bias_blk: Tensor,
     out: Tensor,
     *,
     rows_valid: int,
     n_valid: int,
-    bias_key_major: bool = False,
 ) -> Tensor:
     """The flash core on prepared operands (see ``ffk_flash_attention_bias``).
 
     ``q, k [B, H, R, Np, 32]`` bf16 (q pre-scaled by ``d^-1/2 log2 e``),
-    ``v_t [B, H, R, 32, Np]`` bf16, ``bias [B, H, Np, Np]`` fp16 in log2 units;
+    ``v_t [B, H, R, 32, Np]`` bf16, ``bias_blk`` from :func:`blocked_bias`;
     ``out [B, R, n_valid, H * 32]`` bf16 receives ``o`` for rows < rows_valid.
     """
     batch, heads, rows, n_pad, d = q.shape
     _need(d == TRI_HEAD_DIM, f"head dim {d} (the kernel takes {TRI_HEAD_DIM})")
     _need(k.shape == q.shape and v_t.shape == (batch, heads, rows, d, n_pad), "q/k/v_t shapes")
-    _need(bias.shape == (batch, heads, n_pad, n_pad) and bias.dtype == torch.float16, "bias [B, H, Np, Np] fp16")
-    _need(all(t.is_contiguous() for t in (q, k, v_t, bias)), "operands must be contiguous")
+    _need(bias_blk.dtype == torch.float32 and bias_blk.numel() == batch * heads * n_pad * n_pad,
+          "bias_blk must be the blocked fp32 layout of [B, H, Np, Np]")
+    _need(all(t.is_contiguous() for t in (q, k, v_t, bias_blk)), "operands must be contiguous")
     _need(out.dtype == torch.bfloat16 and out.shape[-1] == heads * d, "out [..., H * 32] bf16")
     status = _native.lib().ffk_flash_attention_bias(
-        q.data_ptr(), k.data_ptr(), v_t.data_ptr(), bias.data_ptr(), out.data_ptr(),
-        batch, heads, rows, n_pad, rows_valid, n_valid, int(bias_key_major),
+        q.data_ptr(), k.data_ptr(), v_t.data_ptr(), bias_blk.data_ptr(), out.data_ptr(),
+        batch, heads, rows, n_pad, rows_valid, n_valid,
         out.stride(0), out.stride(1), out.stride(2), _stream(q.device),
     )
     _native.check(status, "flash_attention_bias")

@@ -96,21 +96,23 @@ int32_t ffk_triangle_attention(
 
 /*
  * Flash attention core with an additive pair bias, the building block of triangle
- * attention (and of the single track's attention with pair bias):
- *   o[b, h, r, j, :] = sum_k softmax_k(q[b,h,r,j,:] . k[b,h,r,k,:] + bias) v[b,h,r,k,:]
- * in the base-2 domain: q must already carry the softmax scale times log2(e), bias is
- * fp16 in log2 units with -inf at masked keys. Shapes: q, k [bh, rows, n_pad, 32] bf16;
- * v_t [bh, rows, 32, n_pad] bf16 (v transposed); bias [bh, n_pad, n_pad] f16 read as
- * bias[h][query][key] (bias_key_major = 0) or bias[h][key][query] (1); output bf16
- * written at o + b*o_sb + r*o_sr + j*o_sj + h*32 + d for r < rows_valid, j < n_valid.
- * n_pad must be a multiple of 128. Replaces the engine's triangle-attention kernel
- * (docs/engine-kernel-gaps.md:10-23 names its sm90 source); no reference C signature.
+ * attention:
+ *   o[b, r, j, h*32 + :] = sum_k softmax_k(q[b,h,r,j,:] . k[b,h,r,k,:] + bias[b,h,j,k]) v[b,h,r,k,:]
+ * in the base-2 domain: q must already carry the softmax scale times log2(e); bias is
+ * fp32 in log2 units with -inf at masked keys, in the blocked layout
+ *   bias_blk[b*heads + h][j / 32][k / 32][g][j % 32][r],  k % 32 = 8 (r / 4) + 4 g + r % 4
+ * (g in 0..1, r in 0..15): the register order of the kernel's 32 x 32 logit tiles.
+ * Shapes: q, k [batch * heads, rows, n_pad, 32] bf16; v_t [batch * heads, rows, 32, n_pad]
+ * bf16 (v transposed); output bf16 written at o + b*o_sb + r*o_sr + j*o_sj + h*32 + d for
+ * r < rows_valid, j < n_valid. n_pad must be a multiple of 128 and rows of 4. A query
+ * whose keys are all masked gets a zero output. Replaces the engine's triangle-attention
+ * kernel (docs/engine-kernel-gaps.md:10-23 names its sm90 source); no reference C signature.
  */
 int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
                                  const void* bias, void* o, int64_t batch, int32_t heads,
                                  int64_t rows, int64_t n_pad, int64_t rows_valid,
-                                 int64_t n_valid, int32_t bias_key_major, int64_t o_sb,
-                                 int64_t o_sr, int64_t o_sj, void* stream);
+                                 int64_t n_valid, int64_t o_sb, int64_t o_sr, int64_t o_sj,
+                                 void* stream);
 
 /*
  * Pair (or single) transition: x + squeeze(silu(expand_a(LN(x))) * expand_b(LN(x))),

@@ -121,20 +121,21 @@ def test_padding_is_bitwise_invisible_to_the_valid_region():
 def test_flash_core_large_logits_and_exact_masking():
     """The core alone, against an fp32 torch softmax, with logits of several hundred nats
     (the failure of a max-free softmax) and masked keys whose values must not matter."""
-    B, H, R, n = 1, 4, 3, 128
+    B, H, R, n = 1, 4, 4, 256
     g = torch.Generator().manual_seed(21)
     q = torch.randn(B, H, R, n, 32, generator=g)
     k = torch.randn(B, H, R, n, 32, generator=g)
     v = torch.randn(B, H, R, n, 32, generator=g)
     bias = 300 * torch.randn(B, H, n, n, generator=g)  # log2 units: up to ~1000 nats
     keep = torch.rand(n, generator=g) > 0.3
+    keep[:40] = False  # the first key tiles are fully masked: the offset is set later
     bias_m = torch.where(keep[None, None, None, :], bias, torch.tensor(float("-inf")))
     qb, kb, vb = q.bfloat16(), k.bfloat16(), v.bfloat16()
-    bh = bias_m.half()
     vt = vb.transpose(-1, -2).contiguous()
+    blk = kernels.blocked_bias(bias_m)
     out = torch.zeros(B, R, n, H * 32, dtype=torch.bfloat16, device="cuda")
-    kernels.flash_attention_bias(qb.cuda(), kb.cuda(), vt.cuda(), bh.cuda(), out, rows_valid=R, n_valid=n)
-    logits = qb.float() @ kb.float().transpose(-1, -2) + bh.float()[:, :, None]  # [B,H,R,n,n] (log2)
+    kernels.flash_attention_bias(qb.cuda(), kb.cuda(), vt.cuda(), blk.cuda(), out, rows_valid=R, n_valid=n)
+    logits = qb.float() @ kb.float().transpose(-1, -2) + bias_m[:, :, None]  # [B,H,R,n,n] (log2)
     w = torch.softmax(logits * 0.6931471805599453, dim=-1)
     want = (w @ vb.float()).permute(0, 2, 3, 1, 4).reshape(B, R, n, H * 32)
     got = out.cpu().float()
@@ -144,8 +145,29 @@ def test_flash_core_large_logits_and_exact_masking():
     v2[..., ~keep, :] = 1e4
     vt2 = v2.transpose(-1, -2).contiguous()
     out2 = torch.zeros_like(out)
-    kernels.flash_attention_bias(qb.cuda(), kb.cuda(), vt2.cuda(), bh.cuda(), out2, rows_valid=R, n_valid=n)
+    kernels.flash_attention_bias(qb.cuda(), kb.cuda(), vt2.cuda(), blk.cuda(), out2, rows_valid=R, n_valid=n)
     assert torch.equal(out.cpu(), out2.cpu())
+
+
+def test_flash_core_moderate_logits_and_partial_query_block():
+    """Unit-scale logits (the lazy offset never moves after the first tile), n = 384 so the
+    last 256-query block is half outside, and only some rows / queries are stored."""
+    B, H, R, n = 2, 4, 8, 384
+    g = torch.Generator().manual_seed(22)
+    q = (0.3 * torch.randn(B, H, R, n, 32, generator=g)).bfloat16()
+    k = torch.randn(B, H, R, n, 32, generator=g).bfloat16()
+    v = torch.randn(B, H, R, n, 32, generator=g).bfloat16()
+    bias = 2 * torch.randn(B, H, n, n, generator=g)
+    bias[1, :, :, 300:] = float("-inf")
+    rows_valid, n_valid = 6, 350
+    out = torch.zeros(B, R, n_valid, H * 32, dtype=torch.bfloat16, device="cuda")
+    kernels.flash_attention_bias(q.cuda(), k.cuda(), v.transpose(-1, -2).contiguous().cuda(),
+                                 kernels.blocked_bias(bias).cuda(), out, rows_valid=rows_valid, n_valid=n_valid)
+    w = torch.softmax((q.float() @ k.float().transpose(-1, -2) + bias[:, :, None]) * 0.6931471805599453, dim=-1)
+    want = (w @ v.float()).permute(0, 2, 3, 1, 4).reshape(B, R, n, H * 32)[:, :, :n_valid]
+    got = out.cpu().float()
+    _check(got[:, :rows_valid], want[:, :rows_valid].double(), None, "flash core, partial blocks")
+    assert (got[:, rows_valid:] == 0).all()
 
 
 def test_no_valid_key_gives_identity_update():

@@ -134,11 +134,9 @@ struct __attribute__((aligned(16))) FlashLds {
   bf16 v[2][kFR][32 * kVS];
 };
 
-// Lazily-offset softmax step for one attention row: S holds bias + q.k - m for 32 keys
-// of this lane's query. Writes the bf16 P^T operands, accumulates the row sum and, when
-// needed (first finite tile, exp2 sum overflow), moves the offset m and rescales O / l.
-__device__ __forceinline__ void softmax_step(f32x16& S, float& m, float& l, bool& set, f32x16& O,
-                                             bf16x8& negm, int g, bf16x8& p0, bf16x8& p1) {
+// exp2 of the 32 logits a lane holds for its query, packed into the bf16 P^T operands of
+// the P V product; returns the lane's partial row sum (v_dot2 over the packed pairs).
+__device__ __forceinline__ float exp_pack(const f32x16& S, bf16x8& p0, bf16x8& p1) {
   const bf16x2 ones = {(bf16)1.f, (bf16)1.f};
   float ts = 0.f;
 #pragma unroll
@@ -152,41 +150,34 @@ __device__ __forceinline__ void softmax_step(f32x16& S, float& m, float& l, bool
     ts = __builtin_amdgcn_fdot2_f32_bf16(a, ones, ts, false);
     ts = __builtin_amdgcn_fdot2_f32_bf16(c, ones, ts, false);
   }
-  const bool bad = !set || !(ts < kLazyLimit);
-  if (__builtin_amdgcn_ballot_w64(bad) != 0) {
-    // exact tile maximum of this query (both lane halves hold its keys)
-    float tm = S[0];
+  return ts;
+}
+
+// The lazy offset's slow path for one attention row (called by the whole wave when some
+// lane's query has no offset yet or its tile sum overflowed 2^64): move m to the tile's
+// maximum (rounded up to a bf16 value, so that the matrix unit subtracts it exactly),
+// rescale O and l, and redo the exponentials.
+__device__ __forceinline__ void rebase(f32x16& S, float& m, float& l, bool& set, f32x16& O,
+                                       bf16x8& negm, int g, bf16x8& p0, bf16x8& p1, float& ts) {
+  float tm = S[0];
 #pragma unroll
-    for (int i = 1; i < 16; ++i) tm = fmaxf(tm, S[i]);
-    tm = pair_max(tm);
-    if (tm > -INFINITY && (!set || tm > 0.f)) {
-      const float mn = bf16_ceil(m + tm);
-      const float shift = mn - m;
-      const float alpha = fast_exp2(-shift);
+  for (int i = 1; i < 16; ++i) tm = fmaxf(tm, S[i]);
+  tm = pair_max(tm);
+  if (tm > -INFINITY && (!set || tm > 0.f)) {
+    const float mn = bf16_ceil(m + tm);
+    const float shift = mn - m;
+    const float alpha = fast_exp2(-shift);
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        S[i] -= shift;
-        O[i] *= alpha;
-      }
-      l *= alpha;
-      m = mn;
-      set = true;
-      negm[0] = g == 0 ? (bf16)(-mn) : (bf16)0.f;
+    for (int i = 0; i < 16; ++i) {
+      S[i] -= shift;
+      O[i] *= alpha;
     }
-    ts = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; i += 2) {
-      const bf16x2 a = {(bf16)fast_exp2(S[i]), (bf16)fast_exp2(S[i + 1])};
-      const bf16x2 c = {(bf16)fast_exp2(S[i + 8]), (bf16)fast_exp2(S[i + 9])};
-      p0[i] = a[0];
-      p0[i + 1] = a[1];
-      p1[i] = c[0];
-      p1[i + 1] = c[1];
-      ts = __builtin_amdgcn_fdot2_f32_bf16(a, ones, ts, false);
-      ts = __builtin_amdgcn_fdot2_f32_bf16(c, ones, ts, false);
-    }
+    l *= alpha;
+    m = mn;
+    set = true;
+    negm[0] = g == 0 ? (bf16)(-mn) : (bf16)0.f;
   }
-  l += ts;
+  ts = exp_pack(S, p0, p1);
 }
 
 // grid (ceil(np / 256) * (np / 4) * batch * heads) workgroups, renumbered per XCD;
@@ -281,6 +272,17 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
   };
 
   const float* bias_w = bias + ((bh * nb + (active ? jw / 32 : 0)) * nb) * 1024 + lane * 16;
+  auto bias_tile = [&](int64_t kb, f32x16& t) {
+    const f32x4* bp = reinterpret_cast<const f32x4*>(bias_w + kb * 1024);
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const f32x4 x = bp[v4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[4 * v4 + e] = x[e];
+    }
+  };
+  f32x16 bcur;
+  if (active) bias_tile(0, bcur);
   gload(0);
   sstore(0);
   __syncthreads();
@@ -289,32 +291,53 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
   for (int64_t st = 0; st < nstage; ++st) {
     const int sb = (int)(st & 1);
     const bool more = st + 1 < nstage;
-    if (more) gload((st + 1) * kFK);
+    if (!active && more) gload((st + 1) * kFK);
     if (active) {
 #pragma unroll
       for (int sub = 0; sub < 2; ++sub) {
         const int64_t kb = st * 2 + sub;
-        f32x16 binit;
-        {
-          const f32x4* bp = reinterpret_cast<const f32x4*>(bias_w + kb * 1024);
+        // two rows at a time: S^T = bias + K Q^T - m, softmax, O^T += V^T P^T
 #pragma unroll
-          for (int v4 = 0; v4 < 4; ++v4) {
-            const f32x4 t = bp[v4];
+        for (int rp = 0; rp < kFR; rp += 2) {
+          f32x16 S[2];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) binit[4 * v4 + e] = t[e];
+          for (int u = 0; u < 2; ++u) {
+            const int rr = rp + u;
+            const bf16* krow = &lds.k[sb][rr][(sub * 32 + li) * kKS];
+            S[u] = mfma32(ld8(krow + 8 * g), qa[rr][0], bcur);
+            S[u] = mfma32(ld8(krow + 16 + 8 * g), qa[rr][1], S[u]);
+            S[u] = mfma32(ones_k, negm[rr], S[u]);
           }
-        }
+          // after the last rows' products the bias registers are free again: fetch the
+          // next step's tile now, so its latency hides behind this step's remaining work
+          if (rp + 2 == kFR && kb + 1 < nb) bias_tile(kb + 1, bcur);
+          // The next stage's K / V^T loads go out after this bias fetch, so that waiting
+          // for the bias never waits for them (memory counters retire in issue order).
+          if (rp + 2 == kFR && sub == 0 && more) gload((st + 1) * kFK);
+          bf16x8 p0[2], p1[2];
+          float ts[2];
+          bool any_bad = false;
 #pragma unroll
-        for (int rr = 0; rr < kFR; ++rr) {
-          const bf16* krow = &lds.k[sb][rr][(sub * 32 + li) * kKS];
-          f32x16 S = mfma32(ld8(krow + 8 * g), qa[rr][0], binit);
-          S = mfma32(ld8(krow + 16 + 8 * g), qa[rr][1], S);
-          S = mfma32(ones_k, negm[rr], S);
-          bf16x8 p0, p1;
-          softmax_step(S, m[rr], l[rr], set[rr], O[rr], negm[rr], g, p0, p1);
-          const bf16* vrow = &lds.v[sb][rr][li * kVS + sub * 32 + 8 * g];
-          O[rr] = mfma32(ld8(vrow), p0, O[rr]);
-          O[rr] = mfma32(ld8(vrow + 16), p1, O[rr]);
+          for (int u = 0; u < 2; ++u) {
+            ts[u] = exp_pack(S[u], p0[u], p1[u]);
+            any_bad |= !set[rp + u] || !(ts[u] < kLazyLimit);
+          }
+          if (__builtin_amdgcn_ballot_w64(any_bad) != 0) {
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+              const int rr = rp + u;
+              if (__builtin_amdgcn_ballot_w64(!set[rr] || !(ts[u] < kLazyLimit)) != 0)
+                rebase(S[u], m[rr], l[rr], set[rr], O[rr], negm[rr], g, p0[u], p1[u], ts[u]);
+            }
+          }
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int rr = rp + u;
+            l[rr] += ts[u];
+            const bf16* vrow = &lds.v[sb][rr][li * kVS + sub * 32 + 8 * g];
+            O[rr] = mfma32(ld8(vrow), p0[u], O[rr]);
+            O[rr] = mfma32(ld8(vrow + 16), p1[u], O[rr]);
+          }
         }
       }
     }
@@ -386,7 +409,7 @@ __global__ __launch_bounds__(256) void triattn_output(
 void launch_flash(const FlashArgs& a, hipStream_t stream) {
   const int64_t nqb = (a.np + 32 * kFW - 1) / (32 * kFW);
   const int64_t blocks = nqb * (a.rows / kFR) * a.batch * a.heads;
-  flash_attn_bias<<<dim3((unsigned)blocks), 32 * kFW, 0, stream>>>(
+  flash_attn_bias<<<dim3((unsigned)blocks), 64 * kFW, 0, stream>>>(
       a.q, a.k, a.vt, a.bias, a.o, a.heads, a.rows, a.np, a.rows_valid, a.n_valid, a.o_sb, a.o_sr,
       a.o_sj);
 }

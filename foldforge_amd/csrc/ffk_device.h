@@ -88,6 +88,19 @@ __device__ __forceinline__ float pair_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// A 32-row x 128-k slice of a K-contiguous bf16 weight matrix held in registers: entry kk
+// is this lane's MFMA operand for k = 16 kk .. 16 kk + 15 of row (first + lane % 32).
+struct WFrag {
+  bf16x8 k[8];
+};
+
+__device__ __forceinline__ void load_wfrag(WFrag& w, const bf16* __restrict__ W, int first_row,
+                                           int li, int g) {
+  const bf16* row = W + (int64_t)(first_row + li) * 128 + 8 * g;
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) w.k[kk] = ld8(row + 16 * kk);
+}
+
 // Reduction over groups of 16 consecutive lanes.
 __device__ __forceinline__ float sum16(float v) {
   v += __shfl_xor(v, 8, 16);
@@ -116,25 +129,27 @@ constexpr int kRow = 136;
 // fp32 affine) into LDS as bf16 [TM][kRow]. Position t lives at base + t * stride
 // (elements) and is real when t < valid; others are written as zeros. When raw is
 // non-null the un-normalised input is stored there too (same layout).
-// 256 threads: 16 lanes per position, 8 channels per lane, 16 positions per pass.
-template <int TM>
+// NT threads (256 or 512): 16 lanes per position, 8 channels per lane, NT / 16 positions
+// per pass.
+template <int TM, int NT = 256>
 __device__ __forceinline__ void ln_tile_128(const bf16* __restrict__ base, int64_t stride, int valid,
                                             const float* __restrict__ w, const float* __restrict__ b,
                                             float eps, bf16* xh, bf16* raw) {
   const int tid = threadIdx.x;
   const int sub = tid & 15;   // channel group: channels 8*sub .. 8*sub+7
-  const int pos0 = tid >> 4;  // 0..15
+  const int pos0 = tid >> 4;  // 0 .. NT / 16 - 1
   float wv[8], bv[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     wv[e] = w[8 * sub + e];
     bv[e] = b ? b[8 * sub + e] : 0.f;
   }
-  constexpr int kPass = TM / 16;
+  constexpr int kPer = NT / 16;
+  constexpr int kPass = TM / kPer;
   bf16x8 v[kPass];
 #pragma unroll
   for (int it = 0; it < kPass; ++it) {
-    const int t = pos0 + 16 * it;
+    const int t = pos0 + kPer * it;
     if (t < valid) {
       v[it] = ld8(base + (int64_t)t * stride + 8 * sub);
     } else {
@@ -144,7 +159,7 @@ __device__ __forceinline__ void ln_tile_128(const bf16* __restrict__ base, int64
   }
 #pragma unroll
   for (int it = 0; it < kPass; ++it) {
-    const int t = pos0 + 16 * it;
+    const int t = pos0 + kPer * it;
     float x[8];
     float s = 0.f;
 #pragma unroll

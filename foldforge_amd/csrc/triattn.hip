@@ -34,8 +34,6 @@
 
 namespace ffk {
 
-constexpr int kTaTP = 128;  // projection tile (positions)
-constexpr int kTaTO = 64;   // output tile (positions)
 constexpr int kFR = 4;      // attention rows per flash workgroup (share the bias tile)
 constexpr int kFW = 8;      // waves per flash workgroup, 32 queries each
 constexpr int kFK = 64;     // keys per LDS stage
@@ -52,78 +50,128 @@ __device__ __forceinline__ int64_t bias_index(int64_t bh, int64_t nb, int64_t qu
   return ((((bh * nb + (query >> 5)) * nb + (key >> 5)) * 2 + g) * 32 + (query & 31)) * 16 + 4 * a + t;
 }
 
-// grid (np / 128, np, batch); block 256.
-__global__ __launch_bounds__(256) void triattn_project(
+constexpr int kPT = 64;        // positions per projection / output tile
+constexpr int kQS = 32 + 8;     // LDS row stride of a staged [position][d] q / k tile
+constexpr int kVPS = kPT + 8;   // LDS row stride of a staged [d][position] v^T tile
+
+// Persistent, weight-stationary: tiles are (batch, row r of the padded grid, 64 positions
+// along the attention row); wave w owns head w (its q, k, v^T weight rows in registers)
+// and wave 0 also the pair bias (4 heads padded to 32 rows).
+__global__ __launch_bounds__(256, 2) void triattn_project(
     const bf16* __restrict__ z, const uint8_t* __restrict__ mask, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ wqkv, const bf16* __restrict__ wb,
     bf16* __restrict__ qo, bf16* __restrict__ ko, bf16* __restrict__ vto, float* __restrict__ bo,
-    int n, int np, int heads, int starting, int transposed_bias, float eps) {
-  __shared__ __attribute__((aligned(16))) bf16 xh[kTaTP * kRow];
-  __shared__ float keep[kTaTP];
-  const int s0 = blockIdx.x * kTaTP;
-  const int r = blockIdx.y;
-  const int b = blockIdx.z;
+    int batch, int n, int np, int heads, int starting, int transposed_bias, float eps) {
+  __shared__ __attribute__((aligned(16))) bf16 xh[kPT * kRow];
+  __shared__ __attribute__((aligned(16))) bf16 sq[4][kPT * kQS];
+  __shared__ __attribute__((aligned(16))) bf16 sk[4][kPT * kQS];
+  __shared__ __attribute__((aligned(16))) bf16 sv[4][32 * kVPS];
+  __shared__ float keep[kPT];
+  __shared__ __attribute__((aligned(16))) bf16 wbl[4 * 128];  // the (at most 4) bias rows
   const int tid = threadIdx.x;
-  const int valid = (r < n) ? max(0, min(kTaTP, n - s0)) : 0;
-  const bf16* base = z;
-  int64_t stride = 128;
-  if (valid > 0) {
-    if (starting) {
-      base = z + (((int64_t)b * n + r) * n + s0) * 128;
-    } else {
-      base = z + (((int64_t)b * n + s0) * n + r) * 128;
-      stride = (int64_t)n * 128;
-    }
+  const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const bool has_head = wave < heads;
+  WFrag wq, wk, wv;
+  if (has_head) {
+    load_wfrag(wq, wqkv, 32 * wave, li, g);
+    load_wfrag(wk, wqkv, 128 + 32 * wave, li, g);
+    load_wfrag(wv, wqkv, 256 + 32 * wave, li, g);
   }
-  ln_tile_128<kTaTP>(base, stride, valid, ln_w, ln_b, eps, xh, nullptr);
+  for (int e = tid; e < 4 * 128; e += 256) wbl[e] = wb[e];
   // The bias entry at tile position t is (query r, key s0 + t), except for the AF3 ending
   // node (bias from the un-transposed pair), where it is (query s0 + t, key r).
   const bool key_major = !starting && !transposed_bias;
-  if (tid < kTaTP) {
-    const int key = key_major ? r : s0 + tid;
-    keep[tid] = (key < n && mask[(int64_t)b * n + key] != 0) ? 1.f : 0.f;
-  }
-  __syncthreads();
-
-  const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
-  const int p0 = 32 * wave;  // this wave's 32 positions
-  const bf16* xrow_li = xh + (p0 + li) * kRow;
-  // q, k: D[position][d] (A = x rows, B = weight rows); lane li holds channel d = li.
+  const int nsb = np / kPT;
+  const int64_t nb = np / 32;
+  const int ntiles = batch * np * nsb;
 #pragma unroll 1
-  for (int t = 0; t < 2 * heads; ++t) {
-    const int hh = t % heads;
-    f32x16 acc = zero16();
-    mma_rows<128>(xrow_li, wqkv + (int64_t)(t * 32 + li) * 128, g, acc);
-    bf16* dst = (t < heads ? qo : ko) +
-                ((((int64_t)b * heads + hh) * np + r) * np + s0 + p0) * 32 + li;
-#pragma unroll
-    for (int q = 0; q < 16; ++q) dst[(int64_t)acc_row(q, g) * 32] = (bf16)acc[q];
-  }
-  // v^T: D[d][position] (A = weight rows, B = x rows); lane li holds position p0 + li.
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int sb = tile % nsb;
+    const int r = (tile / nsb) % np;
+    const int b = tile / (nsb * np);
+    const int s0 = sb * kPT;
+    const int valid = (r < n) ? max(0, min(kPT, n - s0)) : 0;
+    const bf16* base = z;
+    int64_t stride = 128;
+    if (valid > 0) {
+      if (starting) {
+        base = z + (((int64_t)b * n + r) * n + s0) * 128;
+      } else {
+        base = z + (((int64_t)b * n + s0) * n + r) * 128;
+        stride = (int64_t)n * 128;
+      }
+    }
+    __syncthreads();
+    ln_tile_128<kPT>(base, stride, valid, ln_w, ln_b, eps, xh, nullptr);
+    if (tid < kPT) {
+      const int key = key_major ? r : s0 + tid;
+      keep[tid] = (key < n && mask[(int64_t)b * n + key] != 0) ? 1.f : 0.f;
+    }
+    __syncthreads();
 #pragma unroll 1
-  for (int hh = 0; hh < heads; ++hh) {
-    f32x16 acc = zero16();
-    mma_rows<128>(wqkv + (int64_t)(2 * 128 + hh * 32 + li) * 128, xrow_li, g, acc);
-    bf16* dst = vto + ((((int64_t)b * heads + hh) * np + r) * 32) * np + s0 + p0 + li;
+    for (int pt = 0; pt < kPT / 32; ++pt) {
+      const bf16* xrow = xh + (pt * 32 + li) * kRow + 8 * g;
+      if (has_head) {
+        f32x16 aq = zero16(), ak = zero16(), av = zero16();
 #pragma unroll
-    for (int q = 0; q < 16; ++q) dst[(int64_t)acc_row(q, g) * np] = (bf16)acc[q];
-  }
-  // bias: D[head][position] with the head rows zero-padded to 32.
-  {
-    f32x16 acc = zero16();
-    mma_rows<128>(wb + (int64_t)li * 128, xrow_li, g, acc);
-    const float kp = keep[p0 + li];
-    const int64_t nb = np / 32;
-    const int64_t s = s0 + p0 + li;
-    const int64_t query = key_major ? s : r;
-    const int64_t key = key_major ? r : s;
-    if (g == 0) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        if (q < heads) {
-          const float v = kp != 0.f ? acc[q] : -INFINITY;
-          bo[bias_index((int64_t)b * heads + q, nb, query, key)] = v;
+        for (int kk = 0; kk < 8; ++kk) {
+          const bf16x8 x = ld8(xrow + 16 * kk);
+          aq = mfma32(x, wq.k[kk], aq);  // D[position][d]
+          ak = mfma32(x, wk.k[kk], ak);
+          av = mfma32(wv.k[kk], x, av);  // D[d][position]
         }
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int row = acc_row(q, g);
+          sq[wave][(pt * 32 + row) * kQS + li] = (bf16)aq[q];
+          sk[wave][(pt * 32 + row) * kQS + li] = (bf16)ak[q];
+          sv[wave][row * kVPS + pt * 32 + li] = (bf16)av[q];
+        }
+      }
+      if (wave == 0) {
+        f32x16 ab = zero16();
+        const bf16x8 zero8 = {};
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const bf16x8 wrow = li < 4 ? ld8(&wbl[li * 128 + 16 * kk + 8 * g]) : zero8;
+          ab = mfma32(wrow, ld8(xrow + 16 * kk), ab);
+        }
+        // D[head][position]: heads are rows 0..3 = registers 0..3 of lane group 0
+        const float kp = keep[pt * 32 + li];
+        const int64_t s = s0 + pt * 32 + li;
+        const int64_t query = key_major ? s : r;
+        const int64_t key = key_major ? r : s;
+        if (g == 0) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            if (q < heads) {
+              const float v = kp != 0.f ? ab[q] : -INFINITY;
+              bo[bias_index((int64_t)b * heads + q, nb, query, key)] = v;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+    if (has_head) {
+      const int64_t bh = (int64_t)b * heads + wave;
+      // q / k: 64 positions x 64 bytes, contiguous; 16-byte stores
+      bf16* qd = qo + ((bh * np + r) * np + s0) * 32;
+      bf16* kd = ko + ((bh * np + r) * np + s0) * 32;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int chunk = lane + 64 * u;
+        const int p = chunk >> 2, d8 = chunk & 3;
+        *reinterpret_cast<bf16x8*>(qd + p * 32 + 8 * d8) = ld8(&sq[wave][p * kQS + 8 * d8]);
+        *reinterpret_cast<bf16x8*>(kd + p * 32 + 8 * d8) = ld8(&sk[wave][p * kQS + 8 * d8]);
+      }
+      // v^T: 32 rows of d x 64 positions
+      bf16* vd = vto + ((bh * np + r) * 32) * np + s0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int chunk = lane + 64 * u;
+        const int d = chunk >> 3, p8 = chunk & 7;
+        *reinterpret_cast<bf16x8*>(vd + (int64_t)d * np + 8 * p8) = ld8(&sv[wave][d * kVPS + 8 * p8]);
       }
     }
   }
@@ -362,48 +410,93 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
   }
 }
 
-// out = z + (sigmoid(LN_pair(z) W_g^T) * o) W_out^T; grid (ceil(n / 64), n, batch).
-__global__ __launch_bounds__(256) void triattn_output(
+// out = z + (sigmoid(LN_pair(z) W_g^T) * o) W_out^T. Persistent over tiles of 64 positions
+// along a row of z; wave w owns gate channels and output channels 32 w .. 32 w + 31.
+__global__ __launch_bounds__(256, 2) void triattn_output(
     const bf16* __restrict__ z, const bf16* __restrict__ o, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ wg, const bf16* __restrict__ wo,
-    bf16* __restrict__ out, int n, int residual, float eps) {
-  __shared__ __attribute__((aligned(16))) bf16 zr[kTaTO * kRow];
-  __shared__ __attribute__((aligned(16))) bf16 xh[kTaTO * kRow];
-  __shared__ __attribute__((aligned(16))) bf16 y[kTaTO * kRow];
-  const int j0 = blockIdx.x * kTaTO, i = blockIdx.y, b = blockIdx.z;
+    bf16* __restrict__ out, int batch, int n, int residual, float eps) {
+  __shared__ __attribute__((aligned(16))) bf16 zr[kPT * kRow];  // raw z, then the output tile
+  __shared__ __attribute__((aligned(16))) bf16 xh[kPT * kRow];
+  __shared__ __attribute__((aligned(16))) bf16 ot[kPT * kRow];  // o, then sigmoid(gate) * o
   const int tid = threadIdx.x;
-  const int valid = min(kTaTO, n - j0);
-  const int64_t zoff = (((int64_t)b * n + i) * n + j0) * 128;
-  ln_tile_128<kTaTO>(z + zoff, 128, valid, ln_w, ln_b, eps, xh, zr);
-  __syncthreads();
   const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int f = 32 * wave + li;
+  WFrag fg, fo;
+  load_wfrag(fg, wg, 32 * wave, li, g);
+  load_wfrag(fo, wo, 32 * wave, li, g);
+  const int njb = (n + kPT - 1) / kPT;
+  const int ntiles = batch * n * njb;
 #pragma unroll 1
-  for (int pt = 0; pt < kTaTO / 32; ++pt) {
-    f32x16 ag = zero16();
-    mma_rows<128>(xh + (pt * 32 + li) * kRow, wg + f * 128, g, ag);
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int jb = tile % njb;
+    const int i = (tile / njb) % n;
+    const int b = tile / (njb * n);
+    const int j0 = jb * kPT;
+    const int valid = min(kPT, n - j0);
+    const int64_t zoff = (((int64_t)b * n + i) * n + j0) * 128;
+    __syncthreads();
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int p = pt * 32 + acc_row(q, g);
-      const float ov = p < valid ? (float)o[zoff + (int64_t)p * 128 + f] : 0.f;
-      y[p * kRow + f] = (bf16)(sigmoidf_(ag[q]) * ov);
+    for (int u = 0; u < 4; ++u) {
+      const int chunk = tid + 256 * u;
+      const int p = chunk >> 4, c8 = chunk & 15;
+      bf16x8 v = {};
+      if (p < valid) v = ld8(o + zoff + (int64_t)p * 128 + 8 * c8);
+      *reinterpret_cast<bf16x8*>(&ot[p * kRow + 8 * c8]) = v;
     }
-  }
-  __syncthreads();
-#pragma unroll 1
-  for (int pt = 0; pt < kTaTO / 32; ++pt) {
-    f32x16 ao = zero16();
-    mma_rows<128>(y + (pt * 32 + li) * kRow, wo + f * 128, g, ao);
+    ln_tile_128<kPT>(z + zoff, 128, valid, ln_w, ln_b, eps, xh, zr);
+    __syncthreads();
+    f32x16 ag[kPT / 32];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int p = pt * 32 + acc_row(q, g);
-      if (p < valid) {
+    for (int pt = 0; pt < kPT / 32; ++pt) {
+      const bf16* xrow = xh + (pt * 32 + li) * kRow + 8 * g;
+      ag[pt] = zero16();
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) ag[pt] = mfma32(ld8(xrow + 16 * kk), fg.k[kk], ag[pt]);
+    }
+    // gate times o, in place (each wave rewrites only its own 32 channels)
+#pragma unroll
+    for (int pt = 0; pt < kPT / 32; ++pt)
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int p = pt * 32 + acc_row(q, g);
+        ot[p * kRow + f] = (bf16)(sigmoidf_(ag[pt][q]) * (float)ot[p * kRow + f]);
+      }
+    __syncthreads();
+#pragma unroll
+    for (int pt = 0; pt < kPT / 32; ++pt) {
+      const bf16* yrow = ot + (pt * 32 + li) * kRow + 8 * g;
+      f32x16 ao = zero16();
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) ao = mfma32(ld8(yrow + 16 * kk), fo.k[kk], ao);
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int p = pt * 32 + acc_row(q, g);
         float val = ao[q];
         if (residual) val += (float)zr[p * kRow + f];
-        out[zoff + (int64_t)p * 128 + f] = (bf16)val;
+        zr[p * kRow + f] = (bf16)val;
       }
     }
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int chunk = tid + 256 * u;
+      const int p = chunk >> 4, c8 = chunk & 15;
+      if (p < valid)
+        *reinterpret_cast<bf16x8*>(out + zoff + (int64_t)p * 128 + 8 * c8) = ld8(&zr[p * kRow + 8 * c8]);
+    }
   }
+}
+
+static int persistent_grid(int ntiles, int per_cu) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    hipGetDevice(&dev);
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (cus <= 0) cus = 256;
+  }
+  return max(1, min(ntiles, cus * per_cu));
 }
 
 void launch_flash(const FlashArgs& a, hipStream_t stream) {
@@ -416,10 +509,10 @@ void launch_flash(const FlashArgs& a, hipStream_t stream) {
 
 void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
   const int np = a.np;
-  dim3 gp(np / kTaTP, np, a.batch);
-  triattn_project<<<gp, 256, 0, stream>>>(a.z, a.mask, a.ln_w, a.ln_b, a.wqkv, a.wb, a.q, a.k,
-                                          a.vt, a.bias, a.n, np, a.heads, a.starting,
-                                          a.transposed_bias, a.eps);
+  const int tiles_p = a.batch * np * (np / kPT);
+  triattn_project<<<persistent_grid(tiles_p, 2), 256, 0, stream>>>(
+      a.z, a.mask, a.ln_w, a.ln_b, a.wqkv, a.wb, a.q, a.k, a.vt, a.bias, a.batch, a.n, np,
+      a.heads, a.starting, a.transposed_bias, a.eps);
   FlashArgs f;
   f.q = a.q;
   f.k = a.k;
@@ -444,9 +537,9 @@ void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
     f.o_sj = (int64_t)a.n * c;
   }
   launch_flash(f, stream);
-  dim3 go((a.n + kTaTO - 1) / kTaTO, a.n, a.batch);
-  triattn_output<<<go, 256, 0, stream>>>(a.z, a.o, a.ln_w, a.ln_b, a.wg, a.wo, a.out, a.n,
-                                         a.residual, a.eps);
+  const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);
+  triattn_output<<<persistent_grid(tiles_o, 2), 256, 0, stream>>>(
+      a.z, a.o, a.ln_w, a.ln_b, a.wg, a.wo, a.out, a.batch, a.n, a.residual, a.eps);
 }
 
 }  // namespace ffk

@@ -7,6 +7,9 @@
 //                      columns of z, which stores A^T).
 //   2. trimul_contract P[bh] = X[bh] Y[bh]^T on MFMA, 128x128 tiles, LDS double buffer.
 //   3. trimul_output   LN_out(P) W_out^T * sigmoid(LN_pair(z) W_g^T) + z, channel-last.
+// Kernels 1 and 3 are persistent and weight-stationary: each wave keeps its 32-channel
+// slice of every projection in registers (one load per workgroup), loops over 64-position
+// tiles, and stages its results through LDS so that every global store is 16 bytes.
 // The output gate is recomputed from z in kernel 3 (z is read there for the residual
 // anyway) instead of being stored: 128 channels of gate would cost 2 x 67 MB of HBM
 // traffic at N = 512 against 8.6 GFLOP of MFMA work.
@@ -15,67 +18,93 @@
 
 namespace ffk {
 
-constexpr int kTrimulTP = 128;  // positions per projection tile
-constexpr int kTrimulTO = 64;   // positions per output tile
-constexpr int kCT = 128;        // contraction output tile
-constexpr int kCK = 32;         // contraction k step
-constexpr int kCKP = kCK + 8;   // LDS row stride of a contraction operand tile
+constexpr int kPT = 64;      // positions per projection / output tile
+constexpr int kPS = kPT + 8;  // LDS row stride of a [channel][position] staging tile
+constexpr int kCT = 128;      // contraction output tile
+constexpr int kCK = 32;       // contraction k step
+constexpr int kCKP = kCK + 8; // LDS row stride of a contraction operand tile
 
-// grid (np / 128, np, batch); block 256.
-// wp rows: [0,h) to_left, [h,2h) to_left_gate, [2h,3h) to_right, [3h,4h) to_right_gate.
-__global__ __launch_bounds__(256) void trimul_project(
+// Persistent: tiles are (batch, row r of the padded grid, 64 positions along s); grid is a
+// few workgroups per CU. wp rows: [0,h) to_left, [h,2h) to_left_gate, [2h,3h) to_right,
+// [3h,4h) to_right_gate. Wave w owns hidden channels 32 w .. 32 w + 31 of A and of B.
+__global__ __launch_bounds__(256, 2) void trimul_project(
     const bf16* __restrict__ z, const uint8_t* __restrict__ mask, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ wp, bf16* __restrict__ a_out,
-    bf16* __restrict__ b_out, int n, int np, int outgoing, float eps) {
-  __shared__ __attribute__((aligned(16))) bf16 xh[kTrimulTP * kRow];
-  __shared__ float pm[kTrimulTP];
+    bf16* __restrict__ b_out, int batch, int n, int np, int outgoing, float eps) {
   constexpr int H = 128;
-  const int s0 = blockIdx.x * kTrimulTP;
-  const int r = blockIdx.y;
-  const int b = blockIdx.z;
+  __shared__ __attribute__((aligned(16))) bf16 xh[kPT * kRow];
+  __shared__ __attribute__((aligned(16))) bf16 stage[4][2][32 * kPS];
+  __shared__ float pm[kPT];
   const int tid = threadIdx.x;
-  const int valid = (r < n) ? max(0, min(kTrimulTP, n - s0)) : 0;
-  const bf16* base = z;
-  int64_t stride = 128;
-  if (valid > 0) {
-    if (outgoing) {
-      base = z + (((int64_t)b * n + r) * n + s0) * 128;
-    } else {
-      base = z + (((int64_t)b * n + s0) * n + r) * 128;
-      stride = (int64_t)n * 128;
-    }
-  }
-  ln_tile_128<kTrimulTP>(base, stride, valid, ln_w, ln_b, eps, xh, nullptr);
-  if (tid < kTrimulTP) {
-    float m = 0.f;
-    if (tid < valid) {
-      const uint8_t* mb = mask + (int64_t)b * n;
-      m = (mb[r] != 0 && mb[s0 + tid] != 0) ? 1.f : 0.f;
-    }
-    pm[tid] = m;
-  }
-  __syncthreads();
-
   const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
-  const int p = 32 * wave + li;  // position of this lane (D column)
-  const bf16* xrow = xh + p * kRow;
-  const float m = pm[p];
+  WFrag wl, wlg, wr, wrg;
+  load_wfrag(wl, wp, 32 * wave, li, g);
+  load_wfrag(wlg, wp, H + 32 * wave, li, g);
+  load_wfrag(wr, wp, 2 * H + 32 * wave, li, g);
+  load_wfrag(wrg, wp, 3 * H + 32 * wave, li, g);
+  const int nsb = np / kPT;
   const int64_t plane = (int64_t)np * np;
-  const int64_t off = (int64_t)r * np + s0 + p;
+  const int ntiles = batch * np * nsb;
 #pragma unroll 1
-  for (int branch = 0; branch < 2; ++branch) {
-    bf16* dst = (branch == 0 ? a_out : b_out) + (int64_t)b * H * plane + off;
-#pragma unroll 1
-    for (int fc = 0; fc < H / 32; ++fc) {
-      const bf16* wv = wp + (int64_t)(branch * 2 * H + fc * 32 + li) * 128;
-      const bf16* wgt = wv + (int64_t)H * 128;
-      f32x16 av = zero16(), ag = zero16();
-      mma_rows<128>(wv, xrow, g, av);
-      mma_rows<128>(wgt, xrow, g, ag);
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int sb = tile % nsb;
+    const int r = (tile / nsb) % np;
+    const int b = tile / (nsb * np);
+    const int s0 = sb * kPT;
+    const int valid = (r < n) ? max(0, min(kPT, n - s0)) : 0;
+    const bf16* base = z;
+    int64_t stride = 128;
+    if (valid > 0) {
+      if (outgoing) {
+        base = z + (((int64_t)b * n + r) * n + s0) * 128;
+      } else {
+        base = z + (((int64_t)b * n + s0) * n + r) * 128;
+        stride = (int64_t)n * 128;
+      }
+    }
+    __syncthreads();  // the previous tile's LDS readers are done
+    ln_tile_128<kPT>(base, stride, valid, ln_w, ln_b, eps, xh, nullptr);
+    if (tid < kPT) {
+      float m = 0.f;
+      if (tid < valid) {
+        const uint8_t* mb = mask + (int64_t)b * n;
+        m = (mb[r] != 0 && mb[s0 + tid] != 0) ? 1.f : 0.f;
+      }
+      pm[tid] = m;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int pt = 0; pt < kPT / 32; ++pt) {
+      const bf16* xrow = xh + (pt * 32 + li) * kRow + 8 * g;
+      f32x16 al = zero16(), alg = zero16(), ar = zero16(), arg = zero16();
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        const bf16x8 x = ld8(xrow + 16 * kk);
+        al = mfma32(wl.k[kk], x, al);
+        alg = mfma32(wlg.k[kk], x, alg);
+        ar = mfma32(wr.k[kk], x, ar);
+        arg = mfma32(wrg.k[kk], x, arg);
+      }
+      // D[channel][position]: register q is channel acc_row(q, g), lane li position pt*32+li
+      const float m = pm[pt * 32 + li];
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
-        const int f = fc * 32 + acc_row(q, g);
-        dst[(int64_t)f * plane] = (bf16)(av[q] * m * sigmoidf_(ag[q]));
+        const int c = acc_row(q, g);
+        stage[wave][0][c * kPS + pt * 32 + li] = (bf16)(al[q] * m * sigmoidf_(alg[q]));
+        stage[wave][1][c * kPS + pt * 32 + li] = (bf16)(ar[q] * m * sigmoidf_(arg[q]));
+      }
+    }
+    __syncthreads();
+    // 32 channels x 64 positions of A and of B per wave: 16-byte stores, 8 positions each
+#pragma unroll
+    for (int o = 0; o < 2; ++o) {
+      bf16* dst = (o == 0 ? a_out : b_out) + ((int64_t)b * H + 32 * wave) * plane + (int64_t)r * np + s0;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int chunk = lane + 64 * u;
+        const int c = chunk >> 3, p8 = chunk & 7;
+        *reinterpret_cast<bf16x8*>(dst + (int64_t)c * plane + 8 * p8) =
+            ld8(&stage[wave][o][c * kPS + 8 * p8]);
       }
     }
   }
@@ -162,92 +191,141 @@ __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ 
 }
 
 // out[b,i,j,:] = z + (LN_out(P[b,:,i,j]) W_out^T) * sigmoid(LN_pair(z[b,i,j]) W_g^T).
-// grid (ceil(n / 64), n, batch); block 256.
-__global__ __launch_bounds__(256) void trimul_output(
+// Persistent over tiles of 64 positions along a row of z; wave w owns output channels
+// 32 w .. 32 w + 31 of both projections (weights in registers).
+__global__ __launch_bounds__(256, 2) void trimul_output(
     const bf16* __restrict__ z, const bf16* __restrict__ P, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const float* __restrict__ lno_w,
     const float* __restrict__ lno_b, const bf16* __restrict__ wg, const bf16* __restrict__ wo,
-    bf16* __restrict__ out, int n, int np, int residual, float eps) {
-  __shared__ __attribute__((aligned(16))) bf16 zr[kTrimulTO * kRow];
-  __shared__ __attribute__((aligned(16))) bf16 xh[kTrimulTO * kRow];
-  __shared__ __attribute__((aligned(16))) bf16 y[kTrimulTO * kRow];
-  __shared__ float red[4][kTrimulTO];
+    bf16* __restrict__ out, int batch, int n, int np, int residual, float eps) {
   constexpr int H = 128;
-  const int j0 = blockIdx.x * kTrimulTO, i = blockIdx.y, b = blockIdx.z;
+  __shared__ __attribute__((aligned(16))) bf16 zr[kPT * kRow];  // raw z, then the output tile
+  __shared__ __attribute__((aligned(16))) bf16 xh[kPT * kRow];
+  __shared__ __attribute__((aligned(16))) bf16 y[kPT * kRow];
+  __shared__ __attribute__((aligned(16))) bf16 pt_[H * kPS];    // P tile, [channel][position]
+  __shared__ float red[4][kPT];
+  __shared__ float lno[2][H];  // centre-norm affine, kept in LDS (not hoisted into registers)
   const int tid = threadIdx.x;
-  const int valid = min(kTrimulTO, n - j0);
-  const int64_t zoff = (((int64_t)b * n + i) * n + j0) * 128;
-  ln_tile_128<kTrimulTO>(z + zoff, 128, valid, ln_w, ln_b, eps, xh, zr);
-
-  // centre norm over the 128 hidden channels of P: wave q reads channels 32q..32q+31 of
-  // the 64 positions (each read is 64 consecutive positions of one channel plane).
-  {
-    const int pos = tid & 63, q = tid >> 6;
-    const int64_t plane = (int64_t)np * np;
-    const bf16* pp = P + ((int64_t)b * H + 32 * q) * plane + (int64_t)i * np + j0 + pos;
-    float v[32];
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      v[e] = pos < valid ? (float)pp[(int64_t)e * plane] : 0.f;
-      s += v[e];
-    }
-    red[q][pos] = s;
-    __syncthreads();
-    const float mean = (red[0][pos] + red[1][pos] + red[2][pos] + red[3][pos]) * (1.f / H);
-    float ss = 0.f;
-#pragma unroll
-    for (int e = 0; e < 32; ++e) {
-      v[e] -= mean;
-      ss += v[e] * v[e];
-    }
-    __syncthreads();
-    red[q][pos] = ss;
-    __syncthreads();
-    const float var = (red[0][pos] + red[1][pos] + red[2][pos] + red[3][pos]) * (1.f / H);
-    const float rstd = __builtin_amdgcn_rsqf(var + eps);
-#pragma unroll
-    for (int e8 = 0; e8 < 4; ++e8) {
-      bf16x8 o;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int c = 32 * q + 8 * e8 + e;
-        o[e] = (bf16)(v[8 * e8 + e] * rstd * lno_w[c] + lno_b[c]);
-      }
-      *reinterpret_cast<bf16x8*>(&y[pos * kRow + 32 * q + 8 * e8]) = o;
-    }
-  }
-  __syncthreads();
-
   const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int f = 32 * wave + li;  // output channel of this lane
+  if (tid < H) {
+    lno[0][tid] = lno_w[tid];
+    lno[1][tid] = lno_b[tid];
+  }
+  WFrag fg, fo;
+  load_wfrag(fg, wg, 32 * wave, li, g);
+  load_wfrag(fo, wo, 32 * wave, li, g);
+  const int njb = (n + kPT - 1) / kPT;
+  const int64_t plane = (int64_t)np * np;
+  const int ntiles = batch * n * njb;
 #pragma unroll 1
-  for (int pt = 0; pt < kTrimulTO / 32; ++pt) {
-    f32x16 ag = zero16(), ao = zero16();
-    mma_rows<128>(xh + (pt * 32 + li) * kRow, wg + f * 128, g, ag);
-    mma_rows<128>(y + (pt * 32 + li) * kRow, wo + f * H, g, ao);
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int jb = tile % njb;
+    const int i = (tile / njb) % n;
+    const int b = tile / (njb * n);
+    const int j0 = jb * kPT;
+    const int valid = min(kPT, n - j0);
+    const int64_t zoff = (((int64_t)b * n + i) * n + j0) * 128;
+    __syncthreads();
+    // P tile: 128 channels x 64 positions, 16-byte loads (positions j0.. are < np)
+    {
+      const bf16* pb = P + (int64_t)b * H * plane + (int64_t)i * np + j0;
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-      const int p = pt * 32 + acc_row(q, g);
-      if (p < valid) {
+      for (int u = 0; u < 4; ++u) {
+        const int chunk = tid + 256 * u;
+        const int c = chunk >> 3, p8 = chunk & 7;
+        *reinterpret_cast<bf16x8*>(&pt_[c * kPS + 8 * p8]) = ld8(pb + (int64_t)c * plane + 8 * p8);
+      }
+    }
+    ln_tile_128<kPT>(z + zoff, 128, valid, ln_w, ln_b, eps, xh, zr);
+    __syncthreads();
+    // centre norm over the 128 channels of each position: wave q sums channels 32q..32q+31
+    // (two-pass statistics; the column is re-read from LDS rather than held in registers)
+    {
+      const int pos = tid & 63, q = tid >> 6;
+      const bf16* col = &pt_[(32 * q) * kPS + pos];
+      float sacc = 0.f;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) sacc += (float)col[e * kPS];
+      red[q][pos] = sacc;
+      __syncthreads();
+      const float mean = (red[0][pos] + red[1][pos] + red[2][pos] + red[3][pos]) * (1.f / H);
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 32; ++e) {
+        const float d = (float)col[e * kPS] - mean;
+        ss += d * d;
+      }
+      __syncthreads();
+      red[q][pos] = ss;
+      __syncthreads();
+      const float var = (red[0][pos] + red[1][pos] + red[2][pos] + red[3][pos]) * (1.f / H);
+      const float rstd = __builtin_amdgcn_rsqf(var + eps);
+#pragma unroll
+      for (int e8 = 0; e8 < 4; ++e8) {
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int c = 32 * q + 8 * e8 + e;
+          o[e] = (bf16)(((float)col[(8 * e8 + e) * kPS] - mean) * rstd * lno[0][c] + lno[1][c]);
+        }
+        *reinterpret_cast<bf16x8*>(&y[pos * kRow + 32 * q + 8 * e8]) = o;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ptile = 0; ptile < kPT / 32; ++ptile) {
+      const bf16* xrow = xh + (ptile * 32 + li) * kRow + 8 * g;
+      const bf16* yrow = y + (ptile * 32 + li) * kRow + 8 * g;
+      f32x16 ag = zero16(), ao = zero16();
+#pragma unroll
+      for (int kk = 0; kk < 8; ++kk) {
+        ag = mfma32(ld8(xrow + 16 * kk), fg.k[kk], ag);
+        ao = mfma32(ld8(yrow + 16 * kk), fo.k[kk], ao);
+      }
+      // D[position][channel]: the output tile overwrites the raw z tile in LDS in place
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        const int p = ptile * 32 + acc_row(q, g);
         float val = ao[q] * sigmoidf_(ag[q]);
         if (residual) val += (float)zr[p * kRow + f];
-        out[zoff + (int64_t)p * 128 + f] = (bf16)val;
+        zr[p * kRow + f] = (bf16)val;
       }
+    }
+    __syncthreads();
+    // 64 positions x 256 bytes: 16-byte stores
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int chunk = tid + 256 * u;
+      const int p = chunk >> 4, c8 = chunk & 15;
+      if (p < valid)
+        *reinterpret_cast<bf16x8*>(out + zoff + (int64_t)p * 128 + 8 * c8) = ld8(&zr[p * kRow + 8 * c8]);
     }
   }
 }
 
+static int persistent_grid(int ntiles, int per_cu) {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0;
+    hipGetDevice(&dev);
+    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (cus <= 0) cus = 256;
+  }
+  return max(1, min(ntiles, cus * per_cu));
+}
+
 void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
   const int np = a.np;
-  dim3 gp(np / kTrimulTP, np, a.batch);
-  trimul_project<<<gp, 256, 0, stream>>>(a.z, a.mask, a.ln_w, a.ln_b, a.wp, a.A, a.B, a.n, np,
-                                         a.outgoing, a.eps);
+  const int tiles_p = a.batch * np * (np / kPT);
+  trimul_project<<<persistent_grid(tiles_p, 2), 256, 0, stream>>>(
+      a.z, a.mask, a.ln_w, a.ln_b, a.wp, a.A, a.B, a.batch, a.n, np, a.outgoing, a.eps);
   dim3 gc(np / kCT, np / kCT, a.batch * 128);
   trimul_contract<<<gc, 256, 0, stream>>>(a.A, a.B, a.P, np);
-  dim3 go((a.n + kTrimulTO - 1) / kTrimulTO, a.n, a.batch);
-  trimul_output<<<go, 256, 0, stream>>>(a.z, a.P, a.ln_w, a.ln_b, a.lno_w, a.lno_b, a.wg, a.wo,
-                                        a.out, a.n, np, a.residual, a.eps);
+  const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);
+  trimul_output<<<persistent_grid(tiles_o, 2), 256, 0, stream>>>(
+      a.z, a.P, a.ln_w, a.ln_b, a.lno_w, a.lno_b, a.wg, a.wo, a.out, a.batch, a.n, np,
+      a.residual, a.eps);
 }
 
 }  // namespace ffk

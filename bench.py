@@ -48,6 +48,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-runs", type=int, default=3)
+    ap.add_argument("--copy-reference-mb", type=int, default=0,
+                    help="also run a plain device copy of this many MiB (the HBM-counter calibration)")
     return ap.parse_args()
 
 
@@ -100,7 +102,8 @@ def flash_roofline(n: int, length: int, reps: int) -> dict:
     achieved = flops / (ms * 1e-3) / 1e12
     return {"bound": "mfma", "kernel": "flash_attn_bias", "achieved": round(achieved, 2),
             "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None, "us_per_launch": round(ms * 1e3, 2), "flop_per_launch": flops}
+            "traffic": recorded_traffic("flash_attn_bias_n512"), "us_per_launch": round(ms * 1e3, 2),
+            "flop_per_launch": flops}
 
 
 def layernorm_roofline(n: int, reps: int) -> dict:
@@ -117,6 +120,30 @@ def layernorm_roofline(n: int, reps: int) -> dict:
     return {"kernel": "layer_norm_bf16_128", "bound": "hbm", "achieved": round(gbs, 1),
             "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(gbs / PEAK_HBM_GBS, 4),
             "us_per_launch": round(ms * 1e3, 2), "bytes_per_launch": nbytes}
+
+
+def copy_reference(mib: int, reps: int = 3) -> dict:
+    """A plain device-to-device copy of known size: what the HBM read / write counters report
+    for it calibrates the counters of the kernels above (bytes per counted KiB)."""
+    import torch
+
+    src = torch.empty(mib << 20, dtype=torch.uint8, device="cuda").fill_(1)
+    dst = torch.empty_like(src)
+    ms = event_time_ms(lambda: dst.copy_(src), reps)
+    return {"bytes_each_way": mib << 20, "us_per_copy": round(ms * 1e3, 2),
+            "gbs": round(2.0 * (mib << 20) / (ms * 1e-3) / 1e9, 1)}
+
+
+def recorded_traffic(kernel: str) -> float | None:
+    """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter summary
+    (``profiles/<kernel>_traffic.md``, line ``traffic_bytes_per_launch: <n>``), else None."""
+    path = ROOT / "profiles" / f"{kernel}_traffic.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.strip().startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1])
+    return None
 
 
 def cpu_baseline(z, mask, state, gpu_out, runs: int) -> dict:
@@ -203,6 +230,7 @@ def main() -> int:
     print(f"flash core {roof['us_per_launch']} us {roof['achieved']} TFLOP/s; "
           f"layernorm {ln['us_per_launch']} us {ln['achieved']} GB/s", file=sys.stderr, flush=True)
     gpu_out = out.cpu()
+    copy = copy_reference(args.copy_reference_mb) if args.copy_reference_mb > 0 else None
 
     base = None
     if not args.no_cpu_baseline:
@@ -232,7 +260,7 @@ def main() -> int:
             "block_gflop": round(gflop, 1), "block_tflops": round(gflop / ms_per_step, 1),
         },
         "roofline": roof,
-        "kernels": {"layer_norm": ln},
+        "kernels": {"layer_norm": ln, **({"copy_reference": copy} if copy else {})},
         "cpu_baseline": base,
     }
     print(json.dumps(line), flush=True)

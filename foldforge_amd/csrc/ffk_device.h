@@ -125,46 +125,54 @@ __device__ __forceinline__ float wave_sum(float v) {
 // Row stride (elements) of a 128-channel bf16 tile in LDS: 16 bytes of padding per row.
 constexpr int kRow = 136;
 
-// Load TM positions of a 128-channel bf16 pair tile and LayerNorm them (fp32 statistics,
-// fp32 affine) into LDS as bf16 [TM][kRow]. Position t lives at base + t * stride
-// (elements) and is real when t < valid; others are written as zeros. When raw is
-// non-null the un-normalised input is stored there too (same layout).
-// NT threads (256 or 512): 16 lanes per position, 8 channels per lane, NT / 16 positions
-// per pass.
+// A tile of TM positions of a 128-channel bf16 pair tensor in registers, NT threads
+// (256 or 512): 16 lanes per position, 8 channels per lane, NT / 16 positions per pass.
 template <int TM, int NT = 256>
-__device__ __forceinline__ void ln_tile_128(const bf16* __restrict__ base, int64_t stride, int valid,
-                                            const float* __restrict__ w, const float* __restrict__ b,
-                                            float eps, bf16* xh, bf16* raw) {
-  const int tid = threadIdx.x;
-  const int sub = tid & 15;   // channel group: channels 8*sub .. 8*sub+7
-  const int pos0 = tid >> 4;  // 0 .. NT / 16 - 1
+struct LnTile {
+  static constexpr int kPer = NT / 16;
+  static constexpr int kPass = TM / kPer;
+  bf16x8 v[kPass];
+};
+
+// Issue the loads of a tile: position t lives at base + t * stride (elements) and is real
+// when t < valid; other positions read as zeros.
+template <int TM, int NT>
+__device__ __forceinline__ void ln_load(LnTile<TM, NT>& tile, const bf16* __restrict__ base,
+                                        int64_t stride, int valid) {
+  const int sub = threadIdx.x & 15, pos0 = threadIdx.x >> 4;
+#pragma unroll
+  for (int it = 0; it < LnTile<TM, NT>::kPass; ++it) {
+    const int t = pos0 + LnTile<TM, NT>::kPer * it;
+    if (t < valid) {
+      tile.v[it] = ld8(base + (int64_t)t * stride + 8 * sub);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tile.v[it][e] = (bf16)0.f;
+    }
+  }
+}
+
+// LayerNorm a loaded tile (fp32 statistics, fp32 affine) into LDS as bf16 [TM][kRow]; invalid
+// positions are written as zeros. When raw is non-null the input is stored there too.
+template <int TM, int NT>
+__device__ __forceinline__ void ln_finish(const LnTile<TM, NT>& tile, int valid,
+                                          const float* __restrict__ w, const float* __restrict__ b,
+                                          float eps, bf16* xh, bf16* raw) {
+  const int sub = threadIdx.x & 15, pos0 = threadIdx.x >> 4;
   float wv[8], bv[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     wv[e] = w[8 * sub + e];
     bv[e] = b ? b[8 * sub + e] : 0.f;
   }
-  constexpr int kPer = NT / 16;
-  constexpr int kPass = TM / kPer;
-  bf16x8 v[kPass];
 #pragma unroll
-  for (int it = 0; it < kPass; ++it) {
-    const int t = pos0 + kPer * it;
-    if (t < valid) {
-      v[it] = ld8(base + (int64_t)t * stride + 8 * sub);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[it][e] = (bf16)0.f;
-    }
-  }
-#pragma unroll
-  for (int it = 0; it < kPass; ++it) {
-    const int t = pos0 + kPer * it;
+  for (int it = 0; it < LnTile<TM, NT>::kPass; ++it) {
+    const int t = pos0 + LnTile<TM, NT>::kPer * it;
     float x[8];
     float s = 0.f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      x[e] = (float)v[it][e];
+      x[e] = (float)tile.v[it][e];
       s += x[e];
     }
     const float mean = sum16(s) * (1.f / 128.f);
@@ -180,8 +188,26 @@ __device__ __forceinline__ void ln_tile_128(const bf16* __restrict__ base, int64
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = real ? (bf16)(x[e] * rstd * wv[e] + bv[e]) : (bf16)0.f;
     *reinterpret_cast<bf16x8*>(xh + t * kRow + 8 * sub) = o;
-    if (raw) *reinterpret_cast<bf16x8*>(raw + t * kRow + 8 * sub) = v[it];
+    if (raw) *reinterpret_cast<bf16x8*>(raw + t * kRow + 8 * sub) = tile.v[it];
   }
+}
+
+// An opaque copy of a pointer: loads through it cannot be hoisted out of the enclosing loop
+// (used where keeping loop-invariant values in registers would cost occupancy).
+template <typename T>
+__device__ __forceinline__ const T* opaque(const T* p) {
+  asm volatile("" : "+s"(p));
+  return p;
+}
+
+// Load and LayerNorm in one step (see ln_load / ln_finish).
+template <int TM, int NT = 256>
+__device__ __forceinline__ void ln_tile_128(const bf16* __restrict__ base, int64_t stride, int valid,
+                                            const float* __restrict__ w, const float* __restrict__ b,
+                                            float eps, bf16* xh, bf16* raw) {
+  LnTile<TM, NT> tile;
+  ln_load(tile, base, stride, valid);
+  ln_finish(tile, valid, w, b, eps, xh, raw);
 }
 
 }  // namespace ffk

@@ -427,25 +427,45 @@ __global__ __launch_bounds__(256, 2) void triattn_output(
   load_wfrag(fo, wo, 32 * wave, li, g);
   const int njb = (n + kPT - 1) / kPT;
   const int ntiles = batch * n * njb;
-#pragma unroll 1
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  auto where = [&](int tile, int& valid) -> int64_t {
     const int jb = tile % njb;
     const int i = (tile / njb) % n;
     const int b = tile / (njb * n);
     const int j0 = jb * kPT;
-    const int valid = min(kPT, n - j0);
-    const int64_t zoff = (((int64_t)b * n + i) * n + j0) * 128;
-    __syncthreads();
+    valid = min(kPT, n - j0);
+    return (((int64_t)b * n + i) * n + j0) * 128;
+  };
+  // the next tile's z and o (64 positions x 128 channels), loaded during the current one
+  LnTile<kPT, 256> zt;
+  bf16x8 ov[4];
+  auto issue = [&](int tile) {
+    int valid;
+    const int64_t zoff = where(tile, valid);
+    ln_load(zt, z + zoff, 128, valid);
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       const int chunk = tid + 256 * u;
       const int p = chunk >> 4, c8 = chunk & 15;
       bf16x8 v = {};
       if (p < valid) v = ld8(o + zoff + (int64_t)p * 128 + 8 * c8);
-      *reinterpret_cast<bf16x8*>(&ot[p * kRow + 8 * c8]) = v;
+      ov[u] = v;
     }
-    ln_tile_128<kPT>(z + zoff, 128, valid, ln_w, ln_b, eps, xh, zr);
+  };
+  if ((int)blockIdx.x < ntiles) issue(blockIdx.x);
+#pragma unroll 1
+  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    int valid;
+    const int64_t zoff = where(tile, valid);
     __syncthreads();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int chunk = tid + 256 * u;
+      const int p = chunk >> 4, c8 = chunk & 15;
+      *reinterpret_cast<bf16x8*>(&ot[p * kRow + 8 * c8]) = ov[u];
+    }
+    ln_finish(zt, valid, ln_w, ln_b, eps, xh, zr);
+    __syncthreads();
+    if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);
     f32x16 ag[kPT / 32];
 #pragma unroll
     for (int pt = 0; pt < kPT / 32; ++pt) {

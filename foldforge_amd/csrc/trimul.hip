@@ -111,16 +111,21 @@ __global__ __launch_bounds__(256, 2) void trimul_project(
 }
 
 // P[bh][i][j] = sum_k X[bh][i][k] * Y[bh][j][k]; all planes [np][np] bf16, np % 128 == 0.
-// grid (np / 128, np / 128, batch * h); block 256 = 2 x 2 waves of 64 x 64.
+// grid: (np / 128)^2 * batch * h workgroups in one dimension, renumbered so that the tiles
+// of a channel plane (which share its X rows and Y rows) run on one XCD and hit one L2;
+// block 256 = 2 x 2 waves of 64 x 64.
 __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ X,
                                                        const bf16* __restrict__ Y,
                                                        bf16* __restrict__ P, int np) {
   __shared__ __attribute__((aligned(16))) bf16 xs[2][kCT * kCKP];
   __shared__ __attribute__((aligned(16))) bf16 ys[2][kCT * kCKP];
-  const int j0 = blockIdx.x * kCT, i0 = blockIdx.y * kCT;
+  const int nt = np / kCT;
+  const uint32_t wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t bh = wg / (nt * nt);
+  const int j0 = (int)(wg % nt) * kCT, i0 = (int)((wg / nt) % nt) * kCT;
   const int64_t plane = (int64_t)np * np;
-  const bf16* Xb = X + blockIdx.z * plane + (int64_t)i0 * np;
-  const bf16* Yb = Y + blockIdx.z * plane + (int64_t)j0 * np;
+  const bf16* Xb = X + bh * plane + (int64_t)i0 * np;
+  const bf16* Yb = Y + bh * plane + (int64_t)j0 * np;
   const int tid = threadIdx.x;
   // global -> LDS: a 128 x 32 tile is 512 chunks of 8 bf16; 2 per thread per operand.
   bf16x8 rx[2], ry[2];
@@ -176,7 +181,7 @@ __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ 
     __syncthreads();
     buf ^= 1;
   }
-  bf16* Pb = P + blockIdx.z * plane;
+  bf16* Pb = P + bh * plane;
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
@@ -218,27 +223,44 @@ __global__ __launch_bounds__(256, 2) void trimul_output(
   const int njb = (n + kPT - 1) / kPT;
   const int64_t plane = (int64_t)np * np;
   const int ntiles = batch * n * njb;
+  auto where = [&](int tile, int& b, int& i, int& j0, int& valid) {
+    const int jb = tile % njb;
+    i = (tile / njb) % n;
+    b = tile / (njb * n);
+    j0 = jb * kPT;
+    valid = min(kPT, n - j0);
+  };
+  // the next tile's z and P (128 channels x 64 positions), loaded during the current one
+  LnTile<kPT, 256> zt;
+  bf16x8 pv[4];
+  auto issue = [&](int tile) {
+    int b, i, j0, valid;
+    where(tile, b, i, j0, valid);
+    ln_load(zt, z + (((int64_t)b * n + i) * n + j0) * 128, 128, valid);
+    const bf16* pb = P + (int64_t)b * H * plane + (int64_t)i * np + j0;  // j0 + 63 < np
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int chunk = tid + 256 * u;
+      const int c = chunk >> 3, p8 = chunk & 7;
+      pv[u] = ld8(pb + (int64_t)c * plane + 8 * p8);
+    }
+  };
+  if ((int)blockIdx.x < ntiles) issue(blockIdx.x);
 #pragma unroll 1
   for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int jb = tile % njb;
-    const int i = (tile / njb) % n;
-    const int b = tile / (njb * n);
-    const int j0 = jb * kPT;
-    const int valid = min(kPT, n - j0);
+    int b, i, j0, valid;
+    where(tile, b, i, j0, valid);
     const int64_t zoff = (((int64_t)b * n + i) * n + j0) * 128;
     __syncthreads();
-    // P tile: 128 channels x 64 positions, 16-byte loads (positions j0.. are < np)
-    {
-      const bf16* pb = P + (int64_t)b * H * plane + (int64_t)i * np + j0;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int chunk = tid + 256 * u;
-        const int c = chunk >> 3, p8 = chunk & 7;
-        *reinterpret_cast<bf16x8*>(&pt_[c * kPS + 8 * p8]) = ld8(pb + (int64_t)c * plane + 8 * p8);
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int chunk = tid + 256 * u;
+      const int c = chunk >> 3, p8 = chunk & 7;
+      *reinterpret_cast<bf16x8*>(&pt_[c * kPS + 8 * p8]) = pv[u];
     }
-    ln_tile_128<kPT>(z + zoff, 128, valid, ln_w, ln_b, eps, xh, zr);
+    ln_finish(zt, valid, ln_w, ln_b, eps, xh, zr);
     __syncthreads();
+    if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);
     // centre norm over the 128 channels of each position: wave q sums channels 32q..32q+31
     // (two-pass statistics; the column is re-read from LDS rather than held in registers)
     {
@@ -320,8 +342,8 @@ void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
   const int tiles_p = a.batch * np * (np / kPT);
   trimul_project<<<persistent_grid(tiles_p, 2), 256, 0, stream>>>(
       a.z, a.mask, a.ln_w, a.ln_b, a.wp, a.A, a.B, a.batch, a.n, np, a.outgoing, a.eps);
-  dim3 gc(np / kCT, np / kCT, a.batch * 128);
-  trimul_contract<<<gc, 256, 0, stream>>>(a.A, a.B, a.P, np);
+  const int nt = np / kCT;
+  trimul_contract<<<dim3((unsigned)(nt * nt * a.batch * 128)), 256, 0, stream>>>(a.A, a.B, a.P, np);
   const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);
   trimul_output<<<persistent_grid(tiles_o, 2), 256, 0, stream>>>(
       a.z, a.P, a.ln_w, a.ln_b, a.lno_w, a.lno_b, a.wg, a.wo, a.out, a.batch, a.n, np,

@@ -49,6 +49,8 @@ int32_t device_state(int device) {
   return g_device_state[device];
 }
 
+int g_cu_count[kMaxDevices];
+
 int32_t check_device() {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
@@ -64,6 +66,22 @@ int32_t check_launch(const char* what) {
   if (e != hipSuccess) return fail(FFK_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
   return ok();
 }
+
+}  // namespace
+
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 256;
+  if (g_cu_count[dev] <= 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    g_cu_count[dev] = cus;
+  }
+  return g_cu_count[dev];
+}
+
+namespace {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
@@ -87,8 +105,10 @@ __global__ __launch_bounds__(256) void pack_bf16(PackJob job) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int s = 0; s < job.nseg; ++s) {
     const PackSeg sg = job.seg[s];
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < sg.n; i += stride)
-      sg.dst[i] = (bf16)(sg.src ? sg.src[i] * sg.scale : 0.f);
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < sg.n; i += stride) {
+      const int64_t j = sg.swap23 ? (i & ~int64_t(12)) | ((i & 4) << 1) | ((i & 8) >> 1) : i;
+      sg.dst[i] = (bf16)(sg.src ? sg.src[j] * sg.scale : 0.f);
+    }
   }
 }
 
@@ -144,15 +164,13 @@ TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d
 }
 
 struct TransitionWs {
-  bf16 *wa, *wb, *ws;
+  bf16* w;  // the three weights, packed chunk by chunk in the kernel's LDS image order
   size_t bytes;
 };
 TransitionWs transition_ws(void* ws, int d, int factor) {
   Carver cv{static_cast<char*>(ws)};
   TransitionWs w;
-  w.wa = cv.take<bf16>((size_t)factor * d * d);
-  w.wb = cv.take<bf16>((size_t)factor * d * d);
-  w.ws = cv.take<bf16>((size_t)factor * d * d);
+  w.w = cv.take<bf16>((size_t)3 * factor * d * d);
   w.bytes = cv.used;
   return w;
 }
@@ -376,20 +394,12 @@ int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
   if (rows == 0) return ok();
   const TransitionWs w = transition_ws(workspace, d, factor);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t m = (int64_t)factor * d * d;
-  PackJob job{};
-  job.seg[0] = {w_expand_a, w.wa, m, 1.f};
-  job.seg[1] = {w_expand_b, w.wb, m, 1.f};
-  job.seg[2] = {w_squeeze, w.ws, m, 1.f};
-  job.nseg = 3;
-  launch_pack(job, st);
+  launch_transition_pack(w_expand_a, w_expand_b, w_squeeze, w.w, st);
   TransitionArgs a;
   a.x = static_cast<const bf16*>(x);
   a.ln_w = ln_w;
   a.ln_b = ln_b;
-  a.wa = w.wa;
-  a.wb = w.wb;
-  a.ws = w.ws;
+  a.w = w.w;
   a.out = static_cast<bf16*>(out);
   a.rows = rows;
   a.residual = residual ? 1 : 0;

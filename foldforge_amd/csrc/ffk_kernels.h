@@ -52,12 +52,16 @@ void launch_flash(const FlashArgs& a, hipStream_t stream);
 struct TransitionArgs {
   const bf16* x;
   const float *ln_w, *ln_b;
-  const bf16 *wa, *wb, *ws;  // [4c][c], [4c][c], [c][4c]
+  const bf16* w;  // expand_a, expand_b, squeeze as written by launch_transition_pack
   bf16* out;
   int64_t rows;
   int residual;
   float eps;
 };
+// expand_a [4c][c], expand_b [4c][c], squeeze [c][4c] (fp32) -> the transition kernel's packed
+// bf16 weight stream (3 * 4c * c elements).
+void launch_transition_pack(const float* wa, const float* wb, const float* ws, bf16* dst,
+                            hipStream_t stream);
 void launch_transition(const TransitionArgs& a, hipStream_t stream);
 
 struct PackSeg {
@@ -65,12 +69,16 @@ struct PackSeg {
   bf16* dst;
   int64_t n;
   float scale;
+  int swap23;        // 1: dst[i] = src[i with index bits 2 and 3 exchanged]
 };
 struct PackJob {
   PackSeg seg[8];
   int nseg;
 };
 void launch_pack(const PackJob& job, hipStream_t stream);
+
+// Compute units of the current device (cached per device).
+int cu_count();
 
 void launch_layer_norm(const void* x, const float* w, const float* b, void* y, int64_t rows,
                        int cols, float eps, int dtype, hipStream_t stream);

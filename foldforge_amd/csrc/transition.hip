@@ -2,161 +2,335 @@
 //
 // Equations: src/foldforge/models/checkpoints/legacy/reference/transition.py:40-41 and
 // src/foldforge/modules/dense/diffusion_transformer.py:36-44 (SwiGLU). The 4c-wide hidden
-// layer never reaches HBM: x is read once and the output written once.
+// layer never leaves registers: x is read once and the output written once.
 //
-// Persistent over tiles of 128 positions; 8 waves per workgroup = 4 position groups of 32
-// x 2 halves. The 384 KB of bf16 weights are streamed through LDS in chunks of 64 hidden
-// channels (Wa, Wb rows and the matching Ws columns), each chunk shared by the four
-// position groups; the next chunk's loads are in flight while the current one is used.
-// Per chunk a wave computes a, b for its 32 positions x 32 hidden channels (the LN'd
-// operand stays in registers for the whole tile), writes silu(a) * b to LDS, and after a
-// barrier accumulates its 32 positions x 64 output channels over the chunk's 64 hidden
-// channels (the other half's h comes from the partner wave through LDS).
+// Persistent over tiles of 256 positions; 8 waves per workgroup (two per SIMD, so one wave's
+// silu VALU work overlaps the other's MFMAs). Wave w owns positions 32 w .. 32 w + 31 of the
+// tile for the whole tile:
+//   * its LN'd operand x^ (32 positions x 128 channels) sits in registers as the B operand;
+//   * the expand GEMMs are computed transposed, D = W_a,b (hidden x k) * x^ (k x positions),
+//     so a lane holds one position and 16 hidden channels of a 32-hidden block;
+//   * h = silu(a) * b, rounded to bf16, is then directly the B operand of the squeeze GEMM
+//     (k = hidden, in the order the accumulator registers hold it; the squeeze weight is
+//     packed in that same order);
+//   * the squeeze accumulates out^T (128 channels x 32 positions) in registers, initialised
+//     with the residual x, across all 512 hidden channels.
+// expand_a is packed pre-multiplied by -log2(e), so a' = -log2(e) a feeds exp2 directly and
+// h' = a' b / (1 + 2^a') = -log2(e) h; squeeze is packed pre-multiplied by -ln(2), which
+// undoes that factor (out = squeeze h = (-ln 2 squeeze) h').
+// Every global-to-LDS transfer is a direct LDS DMA (global_load_lds_dwordx4), so no VGPRs
+// stage data. The 384 KB of bf16 weights are packed once per call (pack_transition) into 16
+// contiguous 24 KB chunks of 32 hidden channels (expand_a rows, expand_b rows, squeeze
+// columns), each already in the byte order the kernel wants in LDS, so streaming a chunk is a
+// plain linear copy; chunks are double-buffered, one barrier per chunk, and the next tile's
+// raw x arrives behind the first chunk's compute. LDS tiles are unpadded and XOR-swizzled.
 #include "ffk_device.h"
 #include "ffk_kernels.h"
 
 namespace ffk {
 
-constexpr int kXT = 128;       // positions per tile
-constexpr int kXC = 64;        // hidden channels per chunk
-constexpr int kWS = 128 + 8;   // LDS row stride of a Wa / Wb chunk (K = 128)
-constexpr int kSS = kXC + 8;   // LDS row stride of a Ws chunk and of the h chunk (K = 64)
+constexpr int kXC = 32;   // hidden channels per chunk
 
-struct __attribute__((aligned(16))) TransitionLds {
-  bf16 xr[kXT * kRow];   // raw x (residual), then the output tile
-  bf16 xh[kXT * kRow];   // LN(x)
-  bf16 wa[kXC * kWS];    // expand_a rows of the chunk
-  bf16 wb[kXC * kWS];    // expand_b rows of the chunk
-  bf16 ws[128 * kSS];    // squeeze columns of the chunk, [out channel][hidden]
-  bf16 h[kXT * kSS];     // silu(a) * b of the chunk, [position][hidden]
+struct __attribute__((aligned(16))) TransitionChunk {
+  bf16 wa[kXC * 128];  // expand_a rows h0 .. h0 + 31, k = 0 .. 127 (16-byte pieces swizzled)
+  bf16 wb[kXC * 128];  // expand_b rows
+  bf16 ws[128 * kXC];  // squeeze [out channel][hidden h0 .. h0 + 31] (pieces swizzled)
 };
 
-// grid: persistent (one workgroup per CU); block 512.
-__global__ __launch_bounds__(512) void transition_128x4(
-    const bf16* __restrict__ x, const float* __restrict__ ln_w, const float* __restrict__ ln_b,
-    const bf16* __restrict__ wa, const bf16* __restrict__ wb, const bf16* __restrict__ ws,
-    bf16* __restrict__ out, int64_t rows, int residual, float eps) {
-  constexpr int C = 128, HID = 512;
-  __shared__ TransitionLds L;
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
-  const int pg = wave & 3;   // position group: positions 32 pg .. 32 pg + 31
-  const int hh = wave >> 2;  // hidden half of the chunk / output channel half
-  // chunk staging: 3 x 1024 chunks of 16 bytes (Wa, Wb: 64 rows x 16; Ws: 128 rows x 8)
-  bf16x8 pre[6];
-  auto gload = [&](int h0) {
-#pragma unroll
-    for (int u = 0; u < 6; ++u) {
-      const int c = tid + 512 * u;  // 0 .. 3071
-      const int part = c >> 10, w = c & 1023;
-      if (part < 2) {
-        const int row = w >> 4, k8 = w & 15;
-        pre[u] = ld8((part == 0 ? wa : wb) + (int64_t)(h0 + row) * C + 8 * k8);
-      } else {
-        const int row = w >> 3, k8 = w & 7;
-        pre[u] = ld8(ws + (int64_t)row * HID + h0 + 8 * k8);
-      }
-    }
-  };
-  auto sstore = [&]() {
-#pragma unroll
-    for (int u = 0; u < 6; ++u) {
-      const int c = tid + 512 * u;
-      const int part = c >> 10, w = c & 1023;
-      if (part < 2) {
-        const int row = w >> 4, k8 = w & 15;
-        *reinterpret_cast<bf16x8*>(&(part == 0 ? L.wa : L.wb)[row * kWS + 8 * k8]) = pre[u];
-      } else {
-        const int row = w >> 3, k8 = w & 7;
-        *reinterpret_cast<bf16x8*>(&L.ws[row * kSS + 8 * k8]) = pre[u];
-      }
-    }
-  };
+typedef __attribute__((address_space(3))) void lds_void;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-  const int64_t ntiles = (rows + kXT - 1) / kXT;
-#pragma unroll 1
-  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
-    const int64_t row0 = tile * kXT;
-    const int valid = (int)min<int64_t>(kXT, rows - row0);
-    gload(0);
-    __syncthreads();  // the previous tile's LDS readers are done
-    ln_tile_128<kXT, 512>(x + row0 * C, C, valid, ln_w, ln_b, eps, L.xh, L.xr);
-    sstore();
-    __syncthreads();
-    bf16x8 xf[8];
-    {
-      const bf16* xrow = L.xh + (32 * pg + li) * kRow + 8 * g;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) xf[kk] = ld8(xrow + 16 * kk);
+// gfx950 LDS: 64 banks of 4 bytes; a 16-byte-per-lane read serves 16 lanes per cycle.
+// Element offset of 16-byte piece k8 of row r in a 128-wide tile: pieces XOR-swizzled with
+// r % 16, so sixteen lanes reading sixteen consecutive rows (or the sixteen pieces of one
+// row) hit distinct banks.
+__device__ __forceinline__ int off128(int r, int k8) { return r * 128 + 8 * (k8 ^ (r & 15)); }
+// Same for the 32-wide squeeze chunk: 4 pieces per row, four consecutive rows fill the 64
+// banks, so the piece is swizzled with (r / 4) % 4.
+__device__ __forceinline__ int off32(int r, int p) { return r * 32 + 8 * (p ^ ((r >> 2) & 3)); }
+
+// One wave-wide LDS DMA: lane L copies 16 bytes from sbase + voff (bytes) to LDS byte address
+// m0 + 16 L; sbase and m0 are wave-uniform (scalar registers). Issued as inline assembly so
+// that the compiler's wait insertion does not treat every later LDS read as dependent on
+// it: each use is followed by an explicit s_waitcnt vmcnt before the data is read.
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+// Same for data read once (the pair tensor): non-temporal, so the stream does not evict the
+// weights from L2.
+__device__ __forceinline__ void dma16_stream(const void* sbase, uint32_t voff, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "{m0}"(m0)
+               : "memory");
+}
+// Wait until at most N vector-memory operations of this wave are in flight and its LDS
+// operations are done.
+template <int N>
+__device__ __forceinline__ void wait_vm_lds() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void*)p;
+}
+
+constexpr int kChunkElems = 3 * kXC * 128;  // 12288 bf16 = 24 KB per chunk
+
+// expand_a [512][128], expand_b [512][128], squeeze [128][512] (fp32) -> 16 chunks of the LDS
+// image TransitionChunk: expand rows with 16-byte pieces at off128 positions, squeeze rows
+// (output channels) holding the chunk's 32 hidden channels in accumulator order (inside each
+// 16-block: 0-3, 8-11, 4-7, 12-15) with pieces at off32 positions; scaled as described above.
+__global__ __launch_bounds__(256) void pack_transition(const float* __restrict__ wa,
+                                                       const float* __restrict__ wb,
+                                                       const float* __restrict__ ws,
+                                                       bf16* __restrict__ dst) {
+  constexpr int total = 16 * kChunkElems;
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
+    const int c = i / kChunkElems, rem = i % kChunkElems, part = rem >> 12, o = rem & 4095;
+    float v;
+    if (part < 2) {
+      const int r = o >> 7, slot = (o >> 3) & 15, e = o & 7;
+      const int src = (kXC * c + r) * 128 + 8 * (slot ^ (r & 15)) + e;
+      v = part == 0 ? -kLog2e * wa[src] : wb[src];
+    } else {
+      const int r = o >> 5, slot = (o >> 3) & 3, e = o & 7;
+      const int q = 8 * (slot ^ ((r >> 2) & 3)) + e;            // accumulator-order position
+      const int hid = (q & ~12) | ((q & 4) << 1) | ((q & 8) >> 1);  // its hidden channel
+      v = (-1.f / kLog2e) * ws[r * 512 + kXC * c + hid];
     }
-    f32x16 acc[2] = {zero16(), zero16()};  // output channels 64 hh + 32 t + li
-#pragma unroll 1
-    for (int h0 = 0; h0 < HID; h0 += kXC) {
-      const bool more = h0 + kXC < HID;
-      if (more) gload(h0 + kXC);
-      f32x16 aa = zero16(), ab = zero16();
-      const bf16* war = L.wa + (32 * hh + li) * kWS + 8 * g;
-      const bf16* wbr = L.wb + (32 * hh + li) * kWS + 8 * g;
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        aa = mfma32(xf[kk], ld8(war + 16 * kk), aa);
-        ab = mfma32(xf[kk], ld8(wbr + 16 * kk), ab);
-      }
-      // D[position][hidden]: lane li is hidden channel 32 hh + li of the chunk
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int p = 32 * pg + acc_row(q, g);
-        L.h[p * kSS + 32 * hh + li] = (bf16)(siluf_(aa[q]) * ab[q]);
-      }
-      __syncthreads();  // h complete for the chunk
-      const bf16* hrow = L.h + (32 * pg + li) * kSS + 8 * g;
-#pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const bf16* wsr = L.ws + (64 * hh + 32 * t + li) * kSS + 8 * g;
-#pragma unroll
-        for (int kk = 0; kk < kXC / 16; ++kk) acc[t] = mfma32(ld8(hrow + 16 * kk), ld8(wsr + 16 * kk), acc[t]);
-      }
-      __syncthreads();  // chunk weights and h consumed
-      if (more) {
-        sstore();
-        __syncthreads();
-      }
-    }
-    // D[position][out channel]: add the residual, stage the tile in place of raw x
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int c = 64 * hh + 32 * t + li;
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int p = 32 * pg + acc_row(q, g);
-        float v = acc[t][q];
-        if (residual) v += (float)L.xr[p * kRow + c];
-        L.xr[p * kRow + c] = (bf16)v;
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int chunk = tid + 512 * u;
-      const int p = chunk >> 4, c8 = chunk & 15;
-      if (p < valid)
-        *reinterpret_cast<bf16x8*>(out + (row0 + p) * C + 8 * c8) = ld8(&L.xr[p * kRow + 8 * c8]);
-    }
+    dst[i] = (bf16)v;
   }
 }
 
-void launch_transition(const TransitionArgs& a, hipStream_t stream) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    hipGetDevice(&dev);
-    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (cus <= 0) cus = 256;
+// This wave's share (24 / NW of the 24 one-KB pieces) of chunk c of the packed weights into
+// the chunk buffer at LDS byte address buf.
+template <int NW>
+__device__ __forceinline__ void weight_dma(const bf16* wpack, int c, uint32_t buf, int wave,
+                                           int lane) {
+  constexpr int per = 24 / NW;
+#pragma unroll
+  for (int u = 0; u < per; ++u) {
+    const int q = per * wave + u;
+    dma16(wpack + c * kChunkElems, 1024 * q + 16 * lane, buf + 1024 * q);
   }
-  const int64_t ntiles = (a.rows + kXT - 1) / kXT;
-  const int grid = (int)(ntiles < cus ? ntiles : cus);
-  transition_128x4<<<dim3(grid), 512, 0, stream>>>(a.x, a.ln_w, a.ln_b, a.wa, a.wb, a.ws, a.out,
-                                                   a.rows, a.residual, a.eps);
+}
+
+// One chunk: issue the DMA of the weights NB - 1 chunks ahead (and, in the first chunk of a
+// tile, of this wave's rows of the next tile's x), then expand (a', b) -> h' -> squeeze into
+// acc using cur.
+template <int NW, typename XDma>
+__device__ __forceinline__ void transition_chunk(const TransitionChunk* cur, uint32_t ahead_buf,
+                                                 int c_ahead, bool first, const XDma& xdma,
+                                                 const bf16* wpack, int wave, int lane,
+                                                 const bf16x8 (&xb)[8], f32x16 (&acc)[4]) {
+  const int g = lane >> 5, li = lane & 31;
+  weight_dma<NW>(wpack, c_ahead, ahead_buf, wave, lane);
+  f32x16 a = zero16(), b = zero16();
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) {
+    a = mfma32(ld8(&cur->wa[off128(li, 2 * kk + g)]), xb[kk], a);
+    b = mfma32(ld8(&cur->wb[off128(li, 2 * kk + g)]), xb[kk], b);
+  }
+  if (first) xdma();
+  // a', b: hidden h0 + 8 (r/4) + 4 g + r%4, position li. Slice s of h' (registers 8 s ..
+  // 8 s + 7) covers hidden 16 s + {4 g .. 4 g + 3, 8 + 4 g .. 8 + 4 g + 3}: the packed
+  // squeeze weight holds each 16-block as 0-3, 8-11 | 4-7, 12-15, so piece 2 s + g of an
+  // output row is exactly that k set.
+  bf16x8 hb[2];
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    hb[r >> 3][r & 7] = (bf16)(a[r] * b[r] * __builtin_amdgcn_rcpf(1.f + fast_exp2(a[r])));
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+#pragma unroll
+    for (int ot = 0; ot < 4; ++ot)
+      acc[ot] = mfma32(ld8(&cur->ws[off32(32 * ot + li, 2 * s + g)]), hb[s], acc[ot]);
+  }
+}
+
+// grid: persistent; block 64 NW (NW waves, 32 positions each, tile = 32 NW positions); NB
+// weight-chunk buffers. wpack: see pack_transition.
+template <int NW, int NB, int WG_PER_CU>
+__global__ __launch_bounds__(64 * NW, WG_PER_CU) void transition_swiglu(
+    const bf16* __restrict__ x, const float* __restrict__ ln_w, const float* __restrict__ ln_b,
+    const bf16* __restrict__ wpack, bf16* __restrict__ out, int64_t rows, int residual,
+    float eps) {
+  constexpr int C = 128, NCH = 512 / kXC, XT = 32 * NW;
+  __shared__ TransitionChunk W[NB];  // chunk k of the stream lives in W[k % NB]
+  __shared__ bf16 XR[XT * C];        // x tile: raw, then x^; wave w owns rows 32 w .. 32 w + 31
+  const int lane = threadIdx.x & 63, g = lane >> 5, li = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int sub = lane & 15, p16 = lane >> 4;  // LayerNorm layout: 16 lanes per position
+  const int rw = 32 * wave;                    // this wave's first tile row
+  const uint32_t w_lds = lds_addr(W), xr_lds = lds_addr(XR + rw * C);
+
+  const int64_t ntiles = (rows + XT - 1) / XT;
+  if ((int64_t)blockIdx.x >= ntiles) return;
+  // This wave's 32 rows of the tile at row0 straight into LDS: piece j = rows 4 j .. 4 j + 3,
+  // lane L fills bytes 16 L of it. Rows past the end re-read the last row (finite values,
+  // never stored: positions do not interact).
+  // (row0 < rows, so the scalar base is a real row and every offset is non-negative.)
+  auto x_dma = [&](int64_t row0) {
+    const bf16* base = x + row0 * C;
+    const int64_t last = rows - 1 - row0;  // >= 0
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int r = rw + 4 * j + (lane >> 4);  // tile row
+      const int rr = r < last ? r : (int)last;
+      dma16_stream(base, 256 * rr + 16 * ((lane & 15) ^ (r & 15)), xr_lds + 4 * j * 256);
+    }
+  };
+  x_dma((int64_t)blockIdx.x * XT);
+#pragma unroll
+  for (int b = 0; b < NB - 1; ++b) weight_dma<NW>(wpack, b, w_lds + b * sizeof(TransitionChunk), wave, lane);
+  int k = 0;  // position in the chunk stream (16 chunks per tile)
+
+#pragma unroll 1
+  for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+    const int64_t row0 = tile * XT;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // own x rows and chunk-0 pieces landed
+    __syncthreads();                                   // everyone's chunk-0 pieces landed
+    bf16x8 xv[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) xv[it] = ld8(&XR[off128(rw + 4 * it + p16, sub)]);
+    // out^T accumulators: acc[ot] = channels 32 ot + (8 (r/4) + 4 g + r%4), position li
+    f32x16 acc[4];
+#pragma unroll
+    for (int ot = 0; ot < 4; ++ot) {
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const bf16x4 v =
+            *reinterpret_cast<const bf16x4*>(&XR[off128(rw + li, 4 * ot + m) + 4 * g]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[ot][4 * m + e] = residual ? (float)v[e] : 0.f;
+      }
+    }
+    __syncthreads();
+    // LayerNorm (fp32 statistics and affine), written back over the raw rows; the affine is
+    // re-read per tile rather than held in registers through the chunk loop
+    float lw[8], lb[8];
+    {
+      const float* w_ = opaque(ln_w);
+      const float* b_ = opaque(ln_b);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        lw[e] = w_[8 * sub + e];
+        lb[e] = b_[8 * sub + e];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      float v[8];
+      float s = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] = (float)xv[it][e];
+        s += v[e];
+      }
+      const float mean = sum16(s) * (1.f / 128.f);
+      float q = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] -= mean;
+        q += v[e] * v[e];
+      }
+      const float rstd = __builtin_amdgcn_rsqf(sum16(q) * (1.f / 128.f) + eps);
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)(v[e] * rstd * lw[e] + lb[e]);
+      *reinterpret_cast<bf16x8*>(&XR[off128(rw + 4 * it + p16, sub)]) = o;
+    }
+    __syncthreads();
+    bf16x8 xb[8];  // B operand: position li, k = 16 kk + 8 g .. + 7
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) xb[kk] = ld8(&XR[off128(rw + li, 2 * kk + g)]);
+    // x^ must be in registers before the next tile's x overwrites its rows
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    // the last tile re-reads its own rows instead of a next tile's
+    const int64_t next0 = tile + gridDim.x < ntiles ? row0 + (int64_t)gridDim.x * XT : row0;
+    auto xdma = [&]() { x_dma(next0); };
+
+#pragma unroll 1
+    for (int c = 0; c < NCH; ++c, ++k) {
+      // chunks wrap around into the next tile; buffer (k + NB - 1) % NB was last read in
+      // chunk k - 1
+      transition_chunk<NW>(&W[k % NB], w_lds + ((k + NB - 1) % NB) * sizeof(TransitionChunk),
+                           (c + NB - 1) % NCH, c == 0, xdma, wpack, wave, lane, xb, acc);
+      // this wave's pieces of chunk k + 1 have landed (after them only the pieces of chunks up
+      // to k + NB - 1 and, in a tile's first chunk, the 8 x pieces were issued); the barrier
+      // then publishes every wave's pieces and retires the reads of W[k % NB]
+      constexpr int later = (NB - 2) * (24 / NW);
+      if (c == 0)
+        wait_vm_lds<later + 8>();
+      else
+        wait_vm_lds<later>();
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    }
+
+    // Store from registers: lanes l and l ^ 32 hold channels 8 m + 0..3 and 8 m + 4..7 of one
+    // position; one swap gives lane group 0 the 8 channels of m = 0, 2 and group 1 those of
+    // m = 1, 3, so every lane writes 16 contiguous bytes.
+    const int64_t r = row0 + rw + li;
+#pragma unroll
+    for (int ot = 0; ot < 4; ++ot) {
+#pragma unroll
+      for (int mp = 0; mp < 2; ++mp) {
+        uint32_t own[2][2];  // [m - 2 mp][dword]: channels 32 ot + 8 m + 4 g + 0..3
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int base = 4 * (2 * mp + t);
+#pragma unroll
+          for (int d = 0; d < 2; ++d) {
+            bf16x2 p;
+            p[0] = (bf16)acc[ot][base + 2 * d];
+            p[1] = (bf16)acc[ot][base + 2 * d + 1];
+            own[t][d] = __builtin_bit_cast(uint32_t, p);
+          }
+        }
+        uint32_t recv[2];
+#pragma unroll
+        for (int d = 0; d < 2; ++d) {
+          const uint32_t send = g ? own[0][d] : own[1][d];
+          const auto sw = __builtin_amdgcn_permlane32_swap(send, send, false, false);
+          recv[d] = g ? sw[0] : sw[1];
+        }
+        uint32_t v[4];
+        v[0] = g ? recv[0] : own[0][0];
+        v[1] = g ? recv[1] : own[0][1];
+        v[2] = g ? own[1][0] : recv[0];
+        v[3] = g ? own[1][1] : recv[1];
+        if (r < rows) {
+          const u32x4 o = {v[0], v[1], v[2], v[3]};
+          __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(out + r * C + 32 * ot +
+                                                                 8 * (2 * mp + g)));
+        }
+      }
+    }
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // no LDS write may land after exit
+}
+
+// Workgroup shape: kTransNW waves of 32 positions, kTransNB chunk buffers, kTransWG
+// workgroups per CU (LDS: kTransNB * 24 KB + kTransNW * 8 KB per workgroup).
+#ifndef FFK_TRANSITION_SHAPE
+#define FFK_TRANSITION_SHAPE 4, 2, 2
+#endif
+constexpr int kTransShape[3] = {FFK_TRANSITION_SHAPE};
+constexpr int kTransNW = kTransShape[0], kTransNB = kTransShape[1], kTransWG = kTransShape[2];
+static_assert(24 % kTransNW == 0 && kTransNB >= 2, "transition workgroup shape");
+
+void launch_transition_pack(const float* wa, const float* wb, const float* ws, bf16* dst,
+                            hipStream_t stream) {
+  pack_transition<<<dim3(192), 256, 0, stream>>>(wa, wb, ws, dst);
+}
+
+void launch_transition(const TransitionArgs& a, hipStream_t stream) {
+  constexpr int XT = 32 * kTransNW;
+  const int64_t ntiles = (a.rows + XT - 1) / XT;
+  const int64_t slots = (int64_t)cu_count() * kTransWG;
+  const int grid = (int)(ntiles < slots ? ntiles : slots);
+  transition_swiglu<kTransNW, kTransNB, kTransWG><<<dim3(grid), 64 * kTransNW, 0, stream>>>(
+      a.x, a.ln_w, a.ln_b, a.w, a.out, a.rows, a.residual, a.eps);
 }
 
 }  // namespace ffk

@@ -509,14 +509,7 @@ __global__ __launch_bounds__(256, 2) void triattn_output(
 }
 
 static int persistent_grid(int ntiles, int per_cu) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0;
-    hipGetDevice(&dev);
-    hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (cus <= 0) cus = 256;
-  }
-  return max(1, min(ntiles, cus * per_cu));
+  return max(1, min(ntiles, cu_count() * per_cu));
 }
 
 void launch_flash(const FlashArgs& a, hipStream_t stream) {

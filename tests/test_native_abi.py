@@ -62,7 +62,10 @@ def test_workspace_sizes_follow_the_layouts(lib):
 
 
 def test_build_recipe_targets_gfx950_without_packed_fp32():
-    cmd = build.command()
-    assert "--offload-arch=gfx950" in cmd
-    assert "-packed-fp32-ops" in cmd
-    assert all(str(s).endswith(".hip") for s in build.sources())
+    srcs = build.sources()
+    assert srcs and all(str(s).endswith(".hip") for s in srcs)
+    for src in srcs:
+        cmd = build.compile_command(src, src.with_suffix(".o"))
+        assert "--offload-arch=gfx950" in cmd
+        assert "-packed-fp32-ops" in cmd
+    assert "--offload-arch=gfx950" in build.link_command([s.with_suffix(".o") for s in srcs])

@@ -123,6 +123,7 @@ void launch_pack(const PackJob& job, hipStream_t stream) {
 
 struct TrimulWs {
   bf16 *wp, *wg, *wo, *A, *B, *P;
+  float* maskf;
   size_t bytes;
 };
 TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
@@ -136,6 +137,7 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
   w.A = cv.take<bf16>(plane);
   w.B = cv.take<bf16>(plane);
   w.P = cv.take<bf16>(plane);
+  w.maskf = cv.take<float>((size_t)batch * np);
   w.bytes = cv.used;
   return w;
 }
@@ -253,6 +255,7 @@ int32_t ffk_triangle_multiplication(
   a.A = w.A;
   a.B = w.B;
   a.P = w.P;
+  a.maskf = w.maskf;
   a.out = static_cast<bf16*>(out);
   a.batch = (int)batch;
   a.n = (int)n;

@@ -101,18 +101,29 @@ __device__ __forceinline__ void load_wfrag(WFrag& w, const bf16* __restrict__ W,
   for (int kk = 0; kk < 8; ++kk) w.k[kk] = ld8(row + 16 * kk);
 }
 
-// Reduction over groups of 16 consecutive lanes.
-__device__ __forceinline__ float sum16(float v) {
-  v += __shfl_xor(v, 8, 16);
-  v += __shfl_xor(v, 4, 16);
-  v += __shfl_xor(v, 2, 16);
-  v += __shfl_xor(v, 1, 16);
+// Lane permutes inside rows of 16 lanes (DPP, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+constexpr int kDppXor1 = 0xb1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4e;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <-> 7 - i within each 8
+constexpr int kDppMirror = 0x140;      // lane i <-> 15 - i within each 16
+
+// Sum over groups of 4 / 16 consecutive lanes (every lane of the group gets the total): pair
+// and quad sums by quad permutes, then the two quads of an 8 joined by the half-row mirror
+// and the two 8s of a 16 by the row mirror.
+__device__ __forceinline__ float sum4(float v) {
+  v += dpp_f<kDppXor1>(v);
+  v += dpp_f<kDppXor2>(v);
   return v;
 }
 
-__device__ __forceinline__ float sum4(float v) {
-  v += __shfl_xor(v, 2, 4);
-  v += __shfl_xor(v, 1, 4);
+__device__ __forceinline__ float sum16(float v) {
+  v = sum4(v);
+  v += dpp_f<kDppHalfMirror>(v);
+  v += dpp_f<kDppMirror>(v);
   return v;
 }
 
@@ -198,6 +209,80 @@ template <typename T>
 __device__ __forceinline__ const T* opaque(const T* p) {
   asm volatile("" : "+s"(p));
   return p;
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void*)p;
+}
+
+// gfx950 LDS: 64 banks of 4 bytes; a 16-byte-per-lane access serves 16 lanes per cycle.
+// Element offset of 16-byte piece k8 of row r in an unpadded 128-channel bf16 tile, pieces
+// XOR-swizzled with r % 16: sixteen lanes reading sixteen consecutive rows at one k (an MFMA
+// operand fetch) or the sixteen pieces of one row hit distinct banks.
+__device__ __forceinline__ int off128(int r, int k8) { return r * 128 + 8 * (k8 ^ (r & 15)); }
+
+// One wave-wide LDS DMA: lane L copies 16 bytes from sbase + voff (bytes) to LDS byte address
+// m0 + 16 L; sbase and m0 are wave-uniform. Issued as inline assembly so that the compiler's
+// wait insertion does not treat every later LDS read as dependent on it: each use is paired
+// with an explicit s_waitcnt vmcnt (vector-memory operations of a wave complete in order)
+// before the data is read, and a kernel waits for its last transfers before it exits.
+__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
+// Same for data read once (the pair tensor): non-temporal, so the stream does not evict
+// reused data (weights) from L2.
+__device__ __forceinline__ void dma16_stream(const void* sbase, uint32_t voff, uint32_t m0) {
+  asm volatile("global_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "{m0}"(m0)
+               : "memory");
+}
+// Wait until at most N vector-memory operations of this wave are in flight and its LDS
+// operations are done.
+template <int N>
+__device__ __forceinline__ void wait_vm_lds() {
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
+}
+
+// LayerNorm in place (fp32 statistics and affine) over the rows 0 .. TM - 1 of an off128
+// tile, NT threads, 16 lanes per row; rows >= valid become zeros.
+template <int TM, int NT>
+__device__ __forceinline__ void ln_inplace_swz(bf16* buf, int valid, const float* w, const float* b,
+                                               float eps) {
+  const int sub = threadIdx.x & 15, pos0 = threadIdx.x >> 4;
+  float wv[8], bv[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    wv[e] = w[8 * sub + e];
+    bv[e] = b ? b[8 * sub + e] : 0.f;
+  }
+#pragma unroll
+  for (int it = 0; it < TM / (NT / 16); ++it) {
+    const int t = pos0 + (NT / 16) * it;
+    bf16x8* p = reinterpret_cast<bf16x8*>(&buf[off128(t, sub)]);
+    const bf16x8 raw = *p;
+    float x[8];
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = (float)raw[e];
+      s += x[e];
+    }
+    const float mean = sum16(s) * (1.f / 128.f);
+    float q = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] -= mean;
+      q += x[e] * x[e];
+    }
+    const float rstd = __builtin_amdgcn_rsqf(sum16(q) * (1.f / 128.f) + eps);
+    bf16x8 o;
+    const bool real = t < valid;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = real ? (bf16)(x[e] * rstd * wv[e] + bv[e]) : (bf16)0.f;
+    *p = o;
+  }
 }
 
 // Load and LayerNorm in one step (see ln_load / ln_finish).

@@ -17,6 +17,7 @@ struct TrimulArgs {
   const bf16* wg;  // [c][c]
   const bf16* wo;  // [c][h]
   bf16 *A, *B, *P;  // [batch][h][np][np]
+  float* maskf;     // [batch][np] scratch: the key mask as 1 / 0, zero past n
   bf16* out;
   int batch, n, np, outgoing, residual;
   float eps;

@@ -37,41 +37,10 @@ struct __attribute__((aligned(16))) TransitionChunk {
   bf16 ws[128 * kXC];  // squeeze [out channel][hidden h0 .. h0 + 31] (pieces swizzled)
 };
 
-typedef __attribute__((address_space(3))) void lds_void;
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-// gfx950 LDS: 64 banks of 4 bytes; a 16-byte-per-lane read serves 16 lanes per cycle.
-// Element offset of 16-byte piece k8 of row r in a 128-wide tile: pieces XOR-swizzled with
-// r % 16, so sixteen lanes reading sixteen consecutive rows (or the sixteen pieces of one
-// row) hit distinct banks.
-__device__ __forceinline__ int off128(int r, int k8) { return r * 128 + 8 * (k8 ^ (r & 15)); }
-// Same for the 32-wide squeeze chunk: 4 pieces per row, four consecutive rows fill the 64
-// banks, so the piece is swizzled with (r / 4) % 4.
+// Element offset of 16-byte piece p of row r of the 32-wide squeeze chunk (the analogue of
+// off128: 4 pieces per row, four consecutive rows fill the 64 banks, so the piece is swizzled
+// with (r / 4) % 4).
 __device__ __forceinline__ int off32(int r, int p) { return r * 32 + 8 * (p ^ ((r >> 2) & 3)); }
-
-// One wave-wide LDS DMA: lane L copies 16 bytes from sbase + voff (bytes) to LDS byte address
-// m0 + 16 L; sbase and m0 are wave-uniform (scalar registers). Issued as inline assembly so
-// that the compiler's wait insertion does not treat every later LDS read as dependent on
-// it: each use is followed by an explicit s_waitcnt vmcnt before the data is read.
-__device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t m0) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
-}
-// Same for data read once (the pair tensor): non-temporal, so the stream does not evict the
-// weights from L2.
-__device__ __forceinline__ void dma16_stream(const void* sbase, uint32_t voff, uint32_t m0) {
-  asm volatile("global_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "{m0}"(m0)
-               : "memory");
-}
-// Wait until at most N vector-memory operations of this wave are in flight and its LDS
-// operations are done.
-template <int N>
-__device__ __forceinline__ void wait_vm_lds() {
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(lds_void*)p;
-}
 
 constexpr int kChunkElems = 3 * kXC * 128;  // 12288 bf16 = 24 KB per chunk
 

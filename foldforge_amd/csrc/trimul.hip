@@ -24,90 +24,130 @@ constexpr int kCT = 128;      // contraction output tile
 constexpr int kCK = 32;       // contraction k step
 constexpr int kCKP = kCK + 8; // LDS row stride of a contraction operand tile
 
-// Persistent: tiles are (batch, row r of the padded grid, 64 positions along s); grid is a
-// few workgroups per CU. wp rows: [0,h) to_left, [h,2h) to_left_gate, [2h,3h) to_right,
-// [3h,4h) to_right_gate. Wave w owns hidden channels 32 w .. 32 w + 31 of A and of B.
-__global__ __launch_bounds__(256, 2) void trimul_project(
-    const bf16* __restrict__ z, const uint8_t* __restrict__ mask, const float* __restrict__ ln_w,
+// Persistent: tiles are (batch, row r of the padded grid, 64 positions along s); one
+// workgroup of 8 waves per CU. wp rows: [0,h) to_left, [h,2h) to_left_gate, [2h,3h)
+// to_right, [3h,4h) to_right_gate. Wave w computes output o = w / 4 (0: A, 1: B) for hidden
+// channels 32 (w % 4) .. + 31, holding that slice of the projection and of its gate in
+// registers.
+// Memory stays busy through the compute: the z tiles stream through a ring of three LDS
+// buffers by LDS DMA, the fetch of tile t + 2 issued right after tile t's MFMAs, and the
+// stores of tile t are left in flight while tile t + 1 is normalised and projected (a wave
+// only waits for its own DMA pieces, never for its stores).
+__global__ __launch_bounds__(512, 2) void trimul_project(
+    const bf16* __restrict__ z, const float* __restrict__ maskf, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ wp, bf16* __restrict__ a_out,
     bf16* __restrict__ b_out, int batch, int n, int np, int outgoing, float eps) {
-  constexpr int H = 128;
-  __shared__ __attribute__((aligned(16))) bf16 xh[kPT * kRow];
-  __shared__ __attribute__((aligned(16))) bf16 stage[4][2][32 * kPS];
-  __shared__ float pm[kPT];
+  constexpr int H = 128, NB = 3;
+  __shared__ __attribute__((aligned(16))) bf16 zt[NB][kPT * 128];  // raw z, then LN(z) (off128)
+  __shared__ __attribute__((aligned(16))) bf16 stage[8][32 * kPS];  // [channel][position]
+  __shared__ float lnp[2][H];  // LayerNorm affine
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
-  WFrag wl, wlg, wr, wrg;
-  load_wfrag(wl, wp, 32 * wave, li, g);
-  load_wfrag(wlg, wp, H + 32 * wave, li, g);
-  load_wfrag(wr, wp, 2 * H + 32 * wave, li, g);
-  load_wfrag(wrg, wp, 3 * H + 32 * wave, li, g);
+  const int lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int o = wave >> 2, cb = wave & 3;  // output (A / B), channel block
+  if (tid < 2 * H) lnp[tid / H][tid % H] = (tid < H ? ln_w : ln_b)[tid % H];  // published by the first barrier
+  WFrag wv, wgt;
+  load_wfrag(wv, wp, 2 * H * o + 32 * cb, li, g);
+  load_wfrag(wgt, wp, 2 * H * o + H + 32 * cb, li, g);
   const int nsb = np / kPT;
   const int64_t plane = (int64_t)np * np;
   const int ntiles = batch * np * nsb;
-#pragma unroll 1
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  auto where = [&](int tile, int& b, int& r, int& s0, int& valid) {
     const int sb = tile % nsb;
-    const int r = (tile / nsb) % np;
-    const int b = tile / (nsb * np);
-    const int s0 = sb * kPT;
-    const int valid = (r < n) ? max(0, min(kPT, n - s0)) : 0;
+    r = (tile / nsb) % np;
+    b = tile / (nsb * np);
+    s0 = sb * kPT;
+    valid = (r < n) ? max(0, min(kPT, n - s0)) : 0;
+  };
+  // This wave's 2 one-KB pieces (positions 8 wave .. 8 wave + 7) of a tile's z rows into ring
+  // slot buf; positions past the end re-read a real row (zeroed by the LayerNorm). A tile
+  // index past the end issues the same two transfers for tile 0 (kept so that every wave
+  // always has the same number of transfers in flight).
+  auto z_dma = [&](int tile, int buf) {
+    int b, r, s0, valid;
+    where(tile < ntiles ? tile : 0, b, r, s0, valid);
     const bf16* base = z;
-    int64_t stride = 128;
+    uint32_t stride = 256;  // bytes between consecutive positions
     if (valid > 0) {
       if (outgoing) {
         base = z + (((int64_t)b * n + r) * n + s0) * 128;
       } else {
         base = z + (((int64_t)b * n + s0) * n + r) * 128;
-        stride = (int64_t)n * 128;
+        stride = (uint32_t)n * 256;
       }
     }
-    __syncthreads();  // the previous tile's LDS readers are done
-    ln_tile_128<kPT>(base, stride, valid, ln_w, ln_b, eps, xh, nullptr);
-    if (tid < kPT) {
-      float m = 0.f;
-      if (tid < valid) {
-        const uint8_t* mb = mask + (int64_t)b * n;
-        m = (mb[r] != 0 && mb[s0 + tid] != 0) ? 1.f : 0.f;
-      }
-      pm[tid] = m;
+    const int last = valid > 0 ? valid - 1 : 0;
+    const uint32_t dst = lds_addr(&zt[buf][0]);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int piece = 2 * wave + u, pos = 4 * piece + (lane >> 4);
+      const int pe = pos < last ? pos : last;
+      dma16_stream(base, pe * stride + 16 * ((lane & 15) ^ (pos & 15)), dst + 1024 * piece);
     }
+  };
+  const int step = gridDim.x;
+  z_dma(blockIdx.x, 0);
+  z_dma(blockIdx.x + step, 1);
+  int buf = 0, k = 0;
+#pragma unroll 1
+  for (int tile = blockIdx.x; tile < ntiles; tile += step, ++k, buf = buf == NB - 1 ? 0 : buf + 1) {
+    int b, r, s0, valid;
+    where(tile, b, r, s0, valid);
+    // this wave's pieces of the tile have landed: issued after them were tile + step's 2
+    // pieces, and from the second tile on the previous tile's 4 stores, and from the third
+    // on also the stores two tiles back and tile + 2 step's pieces
+    if (k == 0)
+      wait_vm_lds<2>();
+    else if (k == 1)
+      wait_vm_lds<6>();
+    else
+      wait_vm_lds<10>();
+    __syncthreads();  // everyone's pieces landed
+    bf16* xh = zt[buf];
+    ln_inplace_swz<kPT, 512>(xh, valid, lnp[0], lnp[1], eps);
     __syncthreads();
+    // pair mask m[r] m[s] (uniform addresses: scalar loads, which leave vmcnt alone)
+    const float* mrow = maskf + (int64_t)b * np;
+    const float mr = mrow[r];
+    const float* ms = mrow + s0;
+    bf16* st = stage[wave];
 #pragma unroll
     for (int pt = 0; pt < kPT / 32; ++pt) {
-      const bf16* xrow = xh + (pt * 32 + li) * kRow + 8 * g;
-      f32x16 al = zero16(), alg = zero16(), ar = zero16(), arg = zero16();
+      f32x16 av = zero16(), ag = zero16();
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {
-        const bf16x8 x = ld8(xrow + 16 * kk);
-        al = mfma32(wl.k[kk], x, al);
-        alg = mfma32(wlg.k[kk], x, alg);
-        ar = mfma32(wr.k[kk], x, ar);
-        arg = mfma32(wrg.k[kk], x, arg);
+        const bf16x8 x = ld8(&xh[off128(pt * 32 + li, 2 * kk + g)]);
+        av = mfma32(x, wv.k[kk], av);
+        ag = mfma32(x, wgt.k[kk], ag);
       }
-      // D[channel][position]: register q is channel acc_row(q, g), lane li position pt*32+li
-      const float m = pm[pt * 32 + li];
+      // D[position][channel]: register q is position pt*32 + acc_row(q, g), lane li channel
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int c = acc_row(q, g);
-        stage[wave][0][c * kPS + pt * 32 + li] = (bf16)(al[q] * m * sigmoidf_(alg[q]));
-        stage[wave][1][c * kPS + pt * 32 + li] = (bf16)(ar[q] * m * sigmoidf_(arg[q]));
+      for (int m4 = 0; m4 < 4; ++m4) {
+        const int p0 = pt * 32 + 8 * m4 + 4 * g;
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int pa = pt * 32 + 8 * m4 + e;  // uniform; lane group 1 takes pa + 4
+          const float mk = mr * (g ? ms[pa + 4] : ms[pa]);
+          v[e] = (bf16)(av[4 * m4 + e] * mk * sigmoidf_(ag[4 * m4 + e]));
+        }
+        *reinterpret_cast<bf16x4*>(&st[li * kPS + p0]) = v;
       }
     }
-    __syncthreads();
-    // 32 channels x 64 positions of A and of B per wave: 16-byte stores, 8 positions each
+    // ring slot buf + 2 was last read by the previous tile, before this tile's first barrier
+    z_dma(tile + 2 * step, buf == 0 ? 2 : buf - 1);
+    // the stage is this wave's own: LDS operations of a wave complete in order
+    __builtin_amdgcn_wave_barrier();
+    // 32 channels x 64 positions: 4 stores of 16 bytes per lane
+    bf16* dst = (o == 0 ? a_out : b_out) + ((int64_t)b * H + 32 * cb) * plane + (int64_t)r * np + s0;
 #pragma unroll
-    for (int o = 0; o < 2; ++o) {
-      bf16* dst = (o == 0 ? a_out : b_out) + ((int64_t)b * H + 32 * wave) * plane + (int64_t)r * np + s0;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int chunk = lane + 64 * u;
-        const int c = chunk >> 3, p8 = chunk & 7;
-        *reinterpret_cast<bf16x8*>(dst + (int64_t)c * plane + 8 * p8) =
-            ld8(&stage[wave][o][c * kPS + 8 * p8]);
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int chunk = lane + 64 * u;
+      const int c = chunk >> 3, p8 = chunk & 7;
+      *reinterpret_cast<bf16x8*>(dst + (int64_t)c * plane + 8 * p8) = ld8(&st[c * kPS + 8 * p8]);
     }
   }
+  wait_vm_lds<0>();  // no LDS write may land after exit
 }
 
 // P[bh][i][j] = sum_k X[bh][i][k] * Y[bh][j][k]; all planes [np][np] bf16, np % 128 == 0.
@@ -326,6 +366,17 @@ __global__ __launch_bounds__(256, 2) void trimul_output(
   }
 }
 
+// maskf[b][s] = key_mask[b][s] ? 1 : 0 for s < n, 0 for n <= s < np.
+__global__ __launch_bounds__(256) void trimul_mask(const uint8_t* __restrict__ mask,
+                                                   float* __restrict__ maskf, int batch, int n,
+                                                   int np) {
+  const int64_t total = (int64_t)batch * np;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t b = i / np, s = i % np;
+    maskf[i] = (s < n && mask[b * n + s] != 0) ? 1.f : 0.f;
+  }
+}
+
 static int persistent_grid(int ntiles, int per_cu) {
   return max(1, min(ntiles, cu_count() * per_cu));
 }
@@ -333,8 +384,11 @@ static int persistent_grid(int ntiles, int per_cu) {
 void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
   const int np = a.np;
   const int tiles_p = a.batch * np * (np / kPT);
-  trimul_project<<<persistent_grid(tiles_p, 2), 256, 0, stream>>>(
-      a.z, a.mask, a.ln_w, a.ln_b, a.wp, a.A, a.B, a.batch, a.n, np, a.outgoing, a.eps);
+  const int64_t mtotal = (int64_t)a.batch * np;
+  trimul_mask<<<dim3((unsigned)((mtotal + 255) / 256 < 1024 ? (mtotal + 255) / 256 : 1024)), 256, 0,
+                stream>>>(a.mask, a.maskf, a.batch, a.n, np);
+  trimul_project<<<persistent_grid(tiles_p, 1), 512, 0, stream>>>(
+      a.z, a.maskf, a.ln_w, a.ln_b, a.wp, a.A, a.B, a.batch, a.n, np, a.outgoing, a.eps);
   const int nt = np / kCT;
   trimul_contract<<<dim3((unsigned)(nt * nt * a.batch * 128)), 256, 0, stream>>>(a.A, a.B, a.P, np);
   const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);

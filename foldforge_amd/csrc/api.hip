@@ -234,11 +234,12 @@ int32_t ffk_triangle_multiplication(
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t hc = (int64_t)d_hidden * d_pair;
   PackJob job{};
+  // gate projections pre-multiplied by -log2(e): the kernels' sigmoid is 1 / (1 + 2^y)
   job.seg[0] = {w_left, w.wp, hc, 1.f};
-  job.seg[1] = {w_left_gate, w.wp + hc, hc, 1.f};
+  job.seg[1] = {w_left_gate, w.wp + hc, hc, -kLog2e};
   job.seg[2] = {w_right, w.wp + 2 * hc, hc, 1.f};
-  job.seg[3] = {w_right_gate, w.wp + 3 * hc, hc, 1.f};
-  job.seg[4] = {w_gate, w.wg, (int64_t)d_pair * d_pair, 1.f};
+  job.seg[3] = {w_right_gate, w.wp + 3 * hc, hc, -kLog2e};
+  job.seg[4] = {w_gate, w.wg, (int64_t)d_pair * d_pair, -kLog2e};
   job.seg[5] = {w_out, w.wo, (int64_t)d_pair * d_hidden, 1.f};
   job.nseg = 6;
   launch_pack(job, st);
@@ -305,7 +306,7 @@ int32_t ffk_triangle_attention(
   job.seg[2] = {w_value, w.wqkv + 2 * m, m, 1.f};
   job.seg[3] = {w_bias, w.wb, (int64_t)n_head * d_pair, kLog2e};
   job.seg[4] = {nullptr, w.wb + (int64_t)n_head * d_pair, (int64_t)(32 - n_head) * d_pair, 0.f};
-  job.seg[5] = {w_gate, w.wg, m, 1.f};
+  job.seg[5] = {w_gate, w.wg, m, -kLog2e};  // sigmoid(x) = 1 / (1 + 2^(-log2(e) x))
   job.seg[6] = {w_out, w.wo, m, 1.f};
   job.nseg = 7;
   launch_pack(job, st);

@@ -51,6 +51,11 @@ __device__ __forceinline__ float sigmoidf_(float x) {
 
 __device__ __forceinline__ float siluf_(float x) { return x * sigmoidf_(x); }
 
+// sigmoid(x) from y = -log2(e) x (gate weights packed pre-multiplied by -log2(e)).
+__device__ __forceinline__ float sigmoid_scaled(float y) {
+  return __builtin_amdgcn_rcpf(1.f + fast_exp2(y));
+}
+
 // acc += A(32 x K) * B(K x 32); a_row / b_row point at k = 0 of this lane's A row and
 // B column (lane l%32), K a multiple of 16.
 template <int K>
@@ -99,6 +104,15 @@ __device__ __forceinline__ void load_wfrag(WFrag& w, const bf16* __restrict__ W,
   const bf16* row = W + (int64_t)(first_row + li) * 128 + 8 * g;
 #pragma unroll
   for (int kk = 0; kk < 8; ++kk) w.k[kk] = ld8(row + 16 * kk);
+}
+
+// Force the loads of a fragment to complete here. Weight fragments are loaded once before a
+// persistent tile loop; without this the compiler's wait bookkeeping cannot prove them done at
+// the loop head and re-waits on them inside every iteration (down to vmcnt(0)), which also
+// drains every DMA and store the loop keeps in flight.
+__device__ __forceinline__ void settle(const WFrag& w) {
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk) asm volatile("" ::"v"(w.k[kk]));
 }
 
 // Lane permutes inside rows of 16 lanes (DPP, no LDS round trip).

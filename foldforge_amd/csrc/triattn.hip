@@ -76,6 +76,9 @@ __global__ __launch_bounds__(256, 2) void triattn_project(
     load_wfrag(wq, wqkv, 32 * wave, li, g);
     load_wfrag(wk, wqkv, 128 + 32 * wave, li, g);
     load_wfrag(wv, wqkv, 256 + 32 * wave, li, g);
+    settle(wq);
+    settle(wk);
+    settle(wv);
   }
   for (int e = tid; e < 4 * 128; e += 256) wbl[e] = wb[e];
   // The bias entry at tile position t is (query r, key s0 + t), except for the AF3 ending
@@ -425,6 +428,8 @@ __global__ __launch_bounds__(256, 2) void triattn_output(
   WFrag fg, fo;
   load_wfrag(fg, wg, 32 * wave, li, g);
   load_wfrag(fo, wo, 32 * wave, li, g);
+  settle(fg);
+  settle(fo);
   const int njb = (n + kPT - 1) / kPT;
   const int ntiles = batch * n * njb;
   auto where = [&](int tile, int& valid) -> int64_t {
@@ -480,7 +485,7 @@ __global__ __launch_bounds__(256, 2) void triattn_output(
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const int p = pt * 32 + acc_row(q, g);
-        ot[p * kRow + f] = (bf16)(sigmoidf_(ag[pt][q]) * (float)ot[p * kRow + f]);
+        ot[p * kRow + f] = (bf16)(sigmoid_scaled(ag[pt][q]) * (float)ot[p * kRow + f]);
       }
     __syncthreads();
 #pragma unroll

@@ -30,8 +30,7 @@ constexpr int kCKP = kCK + 8; // LDS row stride of a contraction operand tile
 // channels 32 (w % 4) .. + 31, holding that slice of the projection and of its gate in
 // registers.
 // Memory stays busy through the compute: the z tiles stream through a ring of three LDS
-// buffers by LDS DMA, the fetch of tile t + 2 issued right after tile t's MFMAs, and the
-// stores of tile t are left in flight while tile t + 1 is normalised and projected (a wave
+// buffers by LDS DMA, two tiles ahead, and the stores of a tile are left in flight (a wave
 // only waits for its own DMA pieces, never for its stores).
 __global__ __launch_bounds__(512, 2) void trimul_project(
     const bf16* __restrict__ z, const float* __restrict__ maskf, const float* __restrict__ ln_w,
@@ -49,6 +48,8 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
   WFrag wv, wgt;
   load_wfrag(wv, wp, 2 * H * o + 32 * cb, li, g);
   load_wfrag(wgt, wp, 2 * H * o + H + 32 * cb, li, g);
+  settle(wv);
+  settle(wgt);
   const int nsb = np / kPT;
   const int64_t plane = (int64_t)np * np;
   const int ntiles = batch * np * nsb;
@@ -86,30 +87,45 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
     }
   };
   const int step = gridDim.x;
+  if ((int)blockIdx.x >= ntiles) return;
+  // Software pipeline, one barrier per tile: after the barrier of tile k a wave issues the
+  // fetch of tile k + 2, projects and stores tile k (normalised in the previous step), then
+  // normalises tile k + 1 (fetched one step earlier) in its own ring slot, so LayerNorm work
+  // overlaps the other waves' MFMAs.
   z_dma(blockIdx.x, 0);
   z_dma(blockIdx.x + step, 1);
+  wait_vm_lds<2>();  // this wave's pieces of the first tile landed
+  __syncthreads();
+  {
+    int b, r, s0, valid;
+    where(blockIdx.x, b, r, s0, valid);
+    ln_inplace_swz<kPT, 512>(zt[0], valid, lnp[0], lnp[1], eps);
+  }
   int buf = 0, k = 0;
 #pragma unroll 1
   for (int tile = blockIdx.x; tile < ntiles; tile += step, ++k, buf = buf == NB - 1 ? 0 : buf + 1) {
     int b, r, s0, valid;
     where(tile, b, r, s0, valid);
-    // this wave's pieces of the tile have landed: issued after them were tile + step's 2
-    // pieces, and from the second tile on the previous tile's 4 stores, and from the third
-    // on also the stores two tiles back and tile + 2 step's pieces
+    const int nbuf = buf == NB - 1 ? 0 : buf + 1, fbuf = nbuf == NB - 1 ? 0 : nbuf + 1;
+    // this wave's pieces of tile + step have landed (issued after them: only the previous
+    // tile's 4 stores, none before the first step); the barrier publishes everyone's pieces
+    // and normalised rows and retires the previous tile's reads of ring slot fbuf
     if (k == 0)
-      wait_vm_lds<2>();
-    else if (k == 1)
-      wait_vm_lds<6>();
+      wait_vm_lds<0>();
     else
-      wait_vm_lds<10>();
-    __syncthreads();  // everyone's pieces landed
-    bf16* xh = zt[buf];
-    ln_inplace_swz<kPT, 512>(xh, valid, lnp[0], lnp[1], eps);
+      wait_vm_lds<4>();
     __syncthreads();
-    // pair mask m[r] m[s] (uniform addresses: scalar loads, which leave vmcnt alone)
+    z_dma(tile + 2 * step, fbuf);
+    const bf16* xh = zt[buf];
+    // pair mask m[r] m[s] (uniform addresses: scalar loads, which leave vmcnt alone); a tile
+    // whose 64 pairs are all real takes the unmasked epilogue
     const float* mrow = maskf + (int64_t)b * np;
     const float mr = mrow[r];
     const float* ms = mrow + s0;
+    float mall = mr;
+#pragma unroll
+    for (int i = 0; i < kPT; ++i) mall = fminf(mall, ms[i]);
+    const bool full = mall == 1.f;
     bf16* st = stage[wave];
 #pragma unroll
     for (int pt = 0; pt < kPT / 32; ++pt) {
@@ -121,21 +137,28 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
         ag = mfma32(x, wgt.k[kk], ag);
       }
       // D[position][channel]: register q is position pt*32 + acc_row(q, g), lane li channel
+      if (full) {
 #pragma unroll
-      for (int m4 = 0; m4 < 4; ++m4) {
-        const int p0 = pt * 32 + 8 * m4 + 4 * g;
-        bf16x4 v;
+        for (int m4 = 0; m4 < 4; ++m4) {
+          bf16x4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int pa = pt * 32 + 8 * m4 + e;  // uniform; lane group 1 takes pa + 4
-          const float mk = mr * (g ? ms[pa + 4] : ms[pa]);
-          v[e] = (bf16)(av[4 * m4 + e] * mk * sigmoidf_(ag[4 * m4 + e]));
+          for (int e = 0; e < 4; ++e) v[e] = (bf16)(av[4 * m4 + e] * sigmoid_scaled(ag[4 * m4 + e]));
+          *reinterpret_cast<bf16x4*>(&st[li * kPS + pt * 32 + 8 * m4 + 4 * g]) = v;
         }
-        *reinterpret_cast<bf16x4*>(&st[li * kPS + p0]) = v;
+      } else {
+#pragma unroll
+        for (int m4 = 0; m4 < 4; ++m4) {
+          bf16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int pa = pt * 32 + 8 * m4 + e;  // uniform; lane group 1 takes pa + 4
+            const float mk = mr * (g ? ms[pa + 4] : ms[pa]);
+            v[e] = (bf16)(av[4 * m4 + e] * mk * sigmoid_scaled(ag[4 * m4 + e]));
+          }
+          *reinterpret_cast<bf16x4*>(&st[li * kPS + pt * 32 + 8 * m4 + 4 * g]) = v;
+        }
       }
     }
-    // ring slot buf + 2 was last read by the previous tile, before this tile's first barrier
-    z_dma(tile + 2 * step, buf == 0 ? 2 : buf - 1);
     // the stage is this wave's own: LDS operations of a wave complete in order
     __builtin_amdgcn_wave_barrier();
     // 32 channels x 64 positions: 4 stores of 16 bytes per lane
@@ -145,6 +168,11 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
       const int chunk = lane + 64 * u;
       const int c = chunk >> 3, p8 = chunk & 7;
       *reinterpret_cast<bf16x8*>(dst + (int64_t)c * plane + 8 * p8) = ld8(&st[c * kPS + 8 * p8]);
+    }
+    if (tile + step < ntiles) {
+      int nb, nr, ns0, nvalid;
+      where(tile + step, nb, nr, ns0, nvalid);
+      ln_inplace_swz<kPT, 512>(zt[nbuf], nvalid, lnp[0], lnp[1], eps);
     }
   }
   wait_vm_lds<0>();  // no LDS write may land after exit
@@ -260,6 +288,8 @@ __global__ __launch_bounds__(256, 2) void trimul_output(
   WFrag fg, fo;
   load_wfrag(fg, wg, 32 * wave, li, g);
   load_wfrag(fo, wo, 32 * wave, li, g);
+  settle(fg);
+  settle(fo);
   const int njb = (n + kPT - 1) / kPT;
   const int64_t plane = (int64_t)np * np;
   const int ntiles = batch * n * njb;
@@ -349,7 +379,7 @@ __global__ __launch_bounds__(256, 2) void trimul_output(
 #pragma unroll
       for (int q = 0; q < 16; ++q) {
         const int p = ptile * 32 + acc_row(q, g);
-        float val = ao[q] * sigmoidf_(ag[q]);
+        float val = ao[q] * sigmoid_scaled(ag[q]);
         if (residual) val += (float)zr[p * kRow + f];
         zr[p * kRow + f] = (bf16)val;
       }

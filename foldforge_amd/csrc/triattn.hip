@@ -14,17 +14,18 @@
 //
 // Flash core (one wave = 32 queries of up to 4 attention rows; 8 waves per workgroup):
 //  * S^T (32 keys x 32 queries) is one MFMA accumulator. Its initial value is the pair-bias
-//    tile, loaded straight into the accumulator registers (fp32, stored by kernel 1 in
-//    exactly that register order: four 16-byte loads per lane, no VALU work), and shared
-//    by the 4 attention rows of the workgroup (the bias does not depend on the row).
+//    tile (fp32, stored by kernel 1 in the accumulator's register order), shared by the 4
+//    attention rows of the workgroup (the bias does not depend on the row).
 //  * The running offset m is subtracted by the matrix unit: a third k-step multiplies a
 //    constant 1 on the key side by -m on the query side (m kept bf16-representable).
 //  * Lazy softmax: the offset is fixed from the first tile that has a finite logit and
 //    only moved when a tile's exp2 sum overflows 2^64, so the common step is exp2,
 //    bf16 packing and a v_dot2 row sum: about one VALU op plus one exp per logit.
-//  * K and V^T tiles of the 4 rows are staged in LDS (64 keys per stage, double
-//    buffered) and shared by the 8 waves; V^T is stored with the keys of each 16-key
-//    group permuted so that a lane's 8 keys of the P V product are one 16-byte read.
+//  * Every operand tile reaches LDS by LDS DMA (no registers, no VALU): K and V^T of the 4
+//    rows in stages of 64 keys (double-buffered, shared by the 8 waves) and each wave's bias
+//    tiles (double-buffered), all one step ahead, with explicit waits on the wave's own
+//    transfers. V^T is stored by kernel 1 with the keys of each 16-key group permuted
+//    (0-3, 8-11, 4-7, 12-15), so that a lane's 8 keys of the P V product are one 16-byte read.
 //  * Each lane owns one query; P^T comes out of the S^T accumulator already in the
 //    B-operand order of the P V product.
 #include <math.h>
@@ -37,18 +38,23 @@ namespace ffk {
 constexpr int kFR = 4;      // attention rows per flash workgroup (share the bias tile)
 constexpr int kFW = 8;      // waves per flash workgroup, 32 queries each
 constexpr int kFK = 64;     // keys per LDS stage
-constexpr int kKS = 40;     // LDS row stride (elements) of a K tile
-constexpr int kVS = 72;     // LDS row stride (elements) of a V^T tile
 constexpr float kLazyLimit = 1.8446744073709552e19f;  // 2^64
 
 // Index of bias entry (query, key) in the blocked layout
-//   [bh][query / 32][key / 32][g][query % 32][r] (16 fp32 per lane), key % 32 = 8(r/4) + 4g + r%4,
-// i.e. lane 32 g + query % 32 holds accumulator register r of the S^T tile.
+//   [bh][query / 32][key / 32][v][lane][e] (a 32 x 32 tile = 1024 fp32),
+//   lane = 32 g + query % 32, key % 32 = 8 v + 4 g + e:
+// accumulator register 4 v + e of lane `lane` of the S^T tile; a lane's 4 registers of one v
+// are 16 contiguous bytes and consecutive lanes are consecutive, so a DMA'd tile reads back
+// from LDS without bank conflicts.
 __device__ __forceinline__ int64_t bias_index(int64_t bh, int64_t nb, int64_t query, int64_t key) {
   const int kk = (int)(key & 31);
-  const int a = kk >> 3, g = (kk >> 2) & 1, t = kk & 3;
-  return ((((bh * nb + (query >> 5)) * nb + (key >> 5)) * 2 + g) * 32 + (query & 31)) * 16 + 4 * a + t;
+  const int v = kk >> 3, g = (kk >> 2) & 1, e = kk & 3;
+  const int lane = 32 * g + (int)(query & 31);
+  return ((((bh * nb + (query >> 5)) * nb + (key >> 5)) * 4 + v) * 64 + lane) * 4 + e;
 }
+
+// Position of key index s inside its 16-key group as stored in v^T (bits 2 and 3 exchanged).
+__device__ __forceinline__ int vkey_slot(int s) { return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1); }
 
 constexpr int kPT = 64;        // positions per projection / output tile
 constexpr int kQS = 32 + 8;     // LDS row stride of a staged [position][d] q / k tile
@@ -128,7 +134,7 @@ __global__ __launch_bounds__(256, 2) void triattn_project(
           const int row = acc_row(q, g);
           sq[wave][(pt * 32 + row) * kQS + li] = (bf16)aq[q];
           sk[wave][(pt * 32 + row) * kQS + li] = (bf16)ak[q];
-          sv[wave][row * kVPS + pt * 32 + li] = (bf16)av[q];
+          sv[wave][row * kVPS + vkey_slot(pt * 32 + li)] = (bf16)av[q];
         }
       }
       if (wave == 0) {
@@ -181,9 +187,16 @@ __global__ __launch_bounds__(256, 2) void triattn_project(
 }
 
 struct __attribute__((aligned(16))) FlashLds {
-  bf16 k[2][kFR][kFK * kKS];
-  bf16 v[2][kFR][32 * kVS];
+  bf16 k[2][kFR][kFK * 32];   // [key][d], 16-byte pieces at koff
+  bf16 v[2][kFR][32 * kFK];   // [d][key], 16-byte pieces at voff
+  float bias[kFW][2][1024];   // per wave, two bias tiles (the blocked layout, copied as is)
 };
+
+// Element offsets of 16-byte piece p of K row `key` (4 pieces: 64 B, four rows fill the 64
+// banks) and of V^T row d (8 pieces: 128 B, two rows fill them), XOR-swizzled so that the
+// MFMA operand reads of 16 consecutive rows hit distinct banks.
+__device__ __forceinline__ int koff(int key, int p) { return key * 32 + 8 * (p ^ ((key >> 2) & 3)); }
+__device__ __forceinline__ int voff(int d, int p) { return d * kFK + 8 * (p ^ ((d >> 1) & 7)); }
 
 // exp2 of the 32 logits a lane holds for its query, packed into the bf16 P^T operands of
 // the P V product; returns the lane's partial row sum (v_dot2 over the packed pairs).
@@ -251,12 +264,49 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
   const int64_t bidx = bh / heads;
   const int h = (int)(bh % heads);
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t jw = j0 + 32 * wave;  // first query of this wave
   const bool active = jw < np;        // the last query block may be partial
   const int64_t j = jw + li;
   const int64_t nb = np / 32;
+  const int64_t nstage = np / kFK;
 
+  // Transfers (each one 1 KB LDS DMA per wave): stage s of K / V^T = 32 pieces, 4 per wave
+  // (piece P = 4 wave + u: part P / 16 (K, V^T), row (P / 4) % 4, quarter P % 4); bias tile
+  // kb of this wave = 4 pieces. Past the last stage / tile a transfer repeats a real one into
+  // a buffer that is no longer read, so every wave always has the same transfers in flight.
+  const bf16* kbase = k + (bh * rows + r0) * np * 32;
+  const bf16* vbase = vt + (bh * rows + r0) * 32 * np;
+  const uint32_t k_lds = lds_addr(&lds.k[0][0][0]), v_lds = lds_addr(&lds.v[0][0][0]);
+  auto kv_dma = [&](int64_t s, int buf) {
+    const int64_t key0 = (s < nstage ? s : nstage - 1) * kFK;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int P = 4 * wave + u, rr = (P >> 2) & 3, i = P & 3;  // wave-uniform
+      if (P < 16) {
+        const int key = 16 * i + (lane >> 2), p = (lane & 3) ^ ((key >> 2) & 3);
+        dma16(kbase, (uint32_t)((((int64_t)rr * np + key0 + key) * 32 + 8 * p) * 2),
+              k_lds + (uint32_t)(((buf * kFR + rr) * kFK * 32 + 16 * i * 32) * 2));
+      } else {
+        const int d = 8 * i + (lane >> 3), p = (lane & 7) ^ ((d >> 1) & 7);
+        dma16(vbase, (uint32_t)((((int64_t)rr * 32 + d) * np + key0 + 8 * p) * 2),
+              v_lds + (uint32_t)(((buf * kFR + rr) * 32 * kFK + 8 * i * kFK) * 2));
+      }
+    }
+  };
+  const float* bias_w = bias + (bh * nb + (active ? jw / 32 : 0)) * nb * 1024;
+  const uint32_t b_lds = lds_addr(&lds.bias[wave][0][0]);
+  auto bias_dma = [&](int64_t kb) {
+    const int64_t kt = kb < nb ? kb : nb - 1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(bias_w, (uint32_t)((kt * 1024 + 256 * i + 4 * lane) * 4),
+            b_lds + (uint32_t)(((kb & 1) * 1024 + 256 * i) * 4));
+  };
+
+  kv_dma(0, 0);
+  bias_dma(0);
   bf16x8 qa[kFR][2];
   bf16x8 negm[kFR];
   float m[kFR], l[kFR];
@@ -281,72 +331,37 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
     set[rr] = false;
     O[rr] = zero16();
   }
-
-  // K / V^T staging: per stage 4 rows x (64 keys x 64 B of K + 32 d x 128 B of V^T)
-  // = 2048 chunks of 16 bytes, 4 per thread.
-  const bf16* kbase = k + (bh * rows + r0) * np * 32;
-  const bf16* vbase = vt + (bh * rows + r0) * 32 * np;
-  bf16x8 pre[4];
-  auto gload = [&](int64_t key0) {
+  // the q loads complete here, not inside the key loop (see settle)
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = tid + 512 * u;
-      const int part = c >> 10, rr = (c >> 8) & 3, w = c & 255;
-      if (part == 0) {
-        const int key = w >> 2, d8 = w & 3;
-        pre[u] = ld8(kbase + ((int64_t)rr * np + key0 + key) * 32 + 8 * d8);
-      } else {
-        const int d = w >> 3, k8 = w & 7;
-        pre[u] = ld8(vbase + ((int64_t)rr * 32 + d) * np + key0 + 8 * k8);
-      }
-    }
-  };
-  auto sstore = [&](int sb) {
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int c = tid + 512 * u;
-      const int part = c >> 10, rr = (c >> 8) & 3, w = c & 255;
-      if (part == 0) {
-        const int key = w >> 2, d8 = w & 3;
-        *reinterpret_cast<bf16x8*>(&lds.k[sb][rr][key * kKS + 8 * d8]) = pre[u];
-      } else {
-        const int d = w >> 3, k8 = w & 7;
-        // keys 8 k8 .. 8 k8 + 7: within their 16-key group the first four go to
-        // 4 h .. 4 h + 3 and the last four to 8 + 4 h .. (h = k8 & 1)
-        bf16* dst = &lds.v[sb][rr][d * kVS + 16 * (k8 >> 1) + 4 * (k8 & 1)];
-        const bf16x4 lo = {pre[u][0], pre[u][1], pre[u][2], pre[u][3]};
-        const bf16x4 hi = {pre[u][4], pre[u][5], pre[u][6], pre[u][7]};
-        *reinterpret_cast<bf16x4*>(dst) = lo;
-        *reinterpret_cast<bf16x4*>(dst + 8) = hi;
-      }
-    }
-  };
-
-  const float* bias_w = bias + ((bh * nb + (active ? jw / 32 : 0)) * nb) * 1024 + lane * 16;
-  auto bias_tile = [&](int64_t kb, f32x16& t) {
-    const f32x4* bp = reinterpret_cast<const f32x4*>(bias_w + kb * 1024);
-#pragma unroll
-    for (int v4 = 0; v4 < 4; ++v4) {
-      const f32x4 x = bp[v4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) t[4 * v4 + e] = x[e];
-    }
-  };
-  f32x16 bcur;
-  if (active) bias_tile(0, bcur);
-  gload(0);
-  sstore(0);
+  for (int rr = 0; rr < kFR; ++rr) asm volatile("" ::"v"(qa[rr][0]), "v"(qa[rr][1]));
+  wait_vm_lds<0>();
   __syncthreads();
-  const int64_t nstage = np / kFK;
+
 #pragma unroll 1
   for (int64_t st = 0; st < nstage; ++st) {
     const int sb = (int)(st & 1);
-    const bool more = st + 1 < nstage;
-    if (!active && more) gload((st + 1) * kFK);
-    if (active) {
 #pragma unroll
-      for (int sub = 0; sub < 2; ++sub) {
-        const int64_t kb = st * 2 + sub;
+    for (int sub = 0; sub < 2; ++sub) {
+      const int64_t kb = st * 2 + sub;
+      // this wave's bias tile kb has landed: issued after it were only, in a second
+      // sub-step, the 4 pieces of the next K / V^T stage
+      if (sub == 0)
+        wait_vm_lds<0>();
+      else
+        wait_vm_lds<4>();
+      f32x16 bcur;
+      {
+        const float* bt = &lds.bias[wave][kb & 1][4 * lane];
+#pragma unroll
+        for (int v4 = 0; v4 < 4; ++v4) {
+          const f32x4 x = *reinterpret_cast<const f32x4*>(bt + 256 * v4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) bcur[4 * v4 + e] = x[e];
+        }
+      }
+      bias_dma(kb + 1);                      // into the other tile buffer, read last step
+      if (sub == 0) kv_dma(st + 1, sb ^ 1);  // the other stage buffer, read last stage
+      if (active) {
         // two rows at a time: S^T = bias + K Q^T - m, softmax, O^T += V^T P^T
 #pragma unroll
         for (int rp = 0; rp < kFR; rp += 2) {
@@ -354,17 +369,11 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const int rr = rp + u;
-            const bf16* krow = &lds.k[sb][rr][(sub * 32 + li) * kKS];
-            S[u] = mfma32(ld8(krow + 8 * g), qa[rr][0], bcur);
-            S[u] = mfma32(ld8(krow + 16 + 8 * g), qa[rr][1], S[u]);
+            const bf16* kt = lds.k[sb][rr];
+            S[u] = mfma32(ld8(kt + koff(sub * 32 + li, g)), qa[rr][0], bcur);
+            S[u] = mfma32(ld8(kt + koff(sub * 32 + li, 2 + g)), qa[rr][1], S[u]);
             S[u] = mfma32(ones_k, negm[rr], S[u]);
           }
-          // after the last rows' products the bias registers are free again: fetch the
-          // next step's tile now, so its latency hides behind this step's remaining work
-          if (rp + 2 == kFR && kb + 1 < nb) bias_tile(kb + 1, bcur);
-          // The next stage's K / V^T loads go out after this bias fetch, so that waiting
-          // for the bias never waits for them (memory counters retire in issue order).
-          if (rp + 2 == kFR && sub == 0 && more) gload((st + 1) * kFK);
           bf16x8 p0[2], p1[2];
           float ts[2];
           bool any_bad = false;
@@ -385,16 +394,20 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
           for (int u = 0; u < 2; ++u) {
             const int rr = rp + u;
             l[rr] += ts[u];
-            const bf16* vrow = &lds.v[sb][rr][li * kVS + sub * 32 + 8 * g];
-            O[rr] = mfma32(ld8(vrow), p0[u], O[rr]);
-            O[rr] = mfma32(ld8(vrow + 16), p1[u], O[rr]);
+            const bf16* vtile = lds.v[sb][rr];
+            O[rr] = mfma32(ld8(vtile + voff(li, 4 * sub + g)), p0[u], O[rr]);
+            O[rr] = mfma32(ld8(vtile + voff(li, 4 * sub + 2 + g)), p1[u], O[rr]);
           }
         }
       }
     }
-    if (more) sstore(sb ^ 1);
+    // this wave's pieces of the next stage have landed (only the 4 bias pieces of the
+    // second sub-step were issued after them); the barrier publishes everyone's and retires
+    // this stage's reads of the buffer the next transfers overwrite
+    wait_vm_lds<4>();
     __syncthreads();
   }
+  wait_vm_lds<0>();  // no LDS write may land after exit
   if (!active) return;
 #pragma unroll
   for (int rr = 0; rr < kFR; ++rr) {

@@ -193,13 +193,23 @@ def transition(
 
 def blocked_bias(bias: Tensor) -> Tensor:
     """``bias [B, H, Np, Np]`` (query, key; log2 units) -> the flash kernel's blocked fp32 layout
-    ``[B * H, Np/32, Np/32, 2, 32, 16]``: entry ``[.., qb, kb, g, li, r]`` is query ``32 qb + li``,
-    key ``32 kb + 8 (r // 4) + 4 g + r % 4``."""
+    ``[B * H, Np/32, Np/32, 4, 64, 4]``: entry ``[.., qb, kb, v, lane, e]`` with
+    ``lane = 32 g + li`` is query ``32 qb + li``, key ``32 kb + 8 v + 4 g + e``."""
     b, h, n1, n2 = bias.shape
     _need(n1 == n2 and n1 % 32 == 0, "bias must be [B, H, Np, Np] with Np % 32 == 0")
     nb = n1 // 32
-    t = bias.float().reshape(b * h, nb, 32, nb, 4, 2, 4)  # [bh, qb, li, kb, a, g, t]
-    return t.permute(0, 1, 3, 5, 2, 4, 6).contiguous()
+    t = bias.float().reshape(b * h, nb, 32, nb, 4, 2, 4)  # [bh, qb, li, kb, v, g, e]
+    return t.permute(0, 1, 3, 4, 5, 2, 6).reshape(b * h, nb, nb, 4, 64, 4).contiguous()
+
+
+def flash_v_layout(v_t: Tensor) -> Tensor:
+    """``v_t [..., 32, Np]`` -> the flash kernel's v^T layout: inside every group of 16 keys the
+    keys are stored in the order 0-3, 8-11, 4-7, 12-15 (index bits 2 and 3 exchanged)."""
+    n = v_t.shape[-1]
+    _need(n % 16 == 0, "the key count must be a multiple of 16")
+    idx = torch.arange(n, device=v_t.device)
+    perm = (idx & ~12) | ((idx & 4) << 1) | ((idx & 8) >> 1)
+    return v_t[..., perm].contiguous()
 
 
 def flash_attention_bias(
@@ -215,7 +225,8 @@ def flash_attention_bias(
     """The flash core on prepared operands (see ``ffk_flash_attention_bias``).
 
     ``q, k [B, H, R, Np, 32]`` bf16 (q pre-scaled by ``d^-1/2 log2 e``),
-    ``v_t [B, H, R, 32, Np]`` bf16, ``bias_blk`` from :func:`blocked_bias`;
+    ``v_t [B, H, R, 32, Np]`` bf16 from :func:`flash_v_layout`, ``bias_blk`` from
+    :func:`blocked_bias`;
     ``out [B, R, n_valid, H * 32]`` bf16 receives ``o`` for rows < rows_valid.
     """
     batch, heads, rows, n_pad, d = q.shape

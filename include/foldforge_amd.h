@@ -100,10 +100,11 @@ int32_t ffk_triangle_attention(
  *   o[b, r, j, h*32 + :] = sum_k softmax_k(q[b,h,r,j,:] . k[b,h,r,k,:] + bias[b,h,j,k]) v[b,h,r,k,:]
  * in the base-2 domain: q must already carry the softmax scale times log2(e); bias is
  * fp32 in log2 units with -inf at masked keys, in the blocked layout
- *   bias_blk[b*heads + h][j / 32][k / 32][g][j % 32][r],  k % 32 = 8 (r / 4) + 4 g + r % 4
- * (g in 0..1, r in 0..15): the register order of the kernel's 32 x 32 logit tiles.
+ *   bias_blk[b*heads + h][j / 32][k / 32][v][32 g + j % 32][e],  k % 32 = 8 v + 4 g + e
+ * (v in 0..3, g in 0..1, e in 0..3): the register order of the kernel's 32 x 32 logit tiles.
  * Shapes: q, k [batch * heads, rows, n_pad, 32] bf16; v_t [batch * heads, rows, 32, n_pad]
- * bf16 (v transposed); output bf16 written at o + b*o_sb + r*o_sr + j*o_sj + h*32 + d for
+ * bf16 (v transposed, the keys of every group of 16 stored in the order 0-3, 8-11, 4-7,
+ * 12-15); output bf16 written at o + b*o_sb + r*o_sr + j*o_sj + h*32 + d for
  * r < rows_valid, j < n_valid. n_pad must be a multiple of 128 and rows of 4. A query
  * whose keys are all masked gets a zero output. Replaces the engine's triangle-attention
  * kernel (docs/engine-kernel-gaps.md:10-23 names its sm90 source); no reference C signature.

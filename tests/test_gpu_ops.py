@@ -131,7 +131,7 @@ def test_flash_core_large_logits_and_exact_masking():
     keep[:40] = False  # the first key tiles are fully masked: the offset is set later
     bias_m = torch.where(keep[None, None, None, :], bias, torch.tensor(float("-inf")))
     qb, kb, vb = q.bfloat16(), k.bfloat16(), v.bfloat16()
-    vt = vb.transpose(-1, -2).contiguous()
+    vt = kernels.flash_v_layout(vb.transpose(-1, -2))
     blk = kernels.blocked_bias(bias_m)
     out = torch.zeros(B, R, n, H * 32, dtype=torch.bfloat16, device="cuda")
     kernels.flash_attention_bias(qb.cuda(), kb.cuda(), vt.cuda(), blk.cuda(), out, rows_valid=R, n_valid=n)
@@ -143,7 +143,7 @@ def test_flash_core_large_logits_and_exact_masking():
     _check(got, want.double(), None, "flash core, large logits")
     v2 = vb.clone()
     v2[..., ~keep, :] = 1e4
-    vt2 = v2.transpose(-1, -2).contiguous()
+    vt2 = kernels.flash_v_layout(v2.transpose(-1, -2))
     out2 = torch.zeros_like(out)
     kernels.flash_attention_bias(qb.cuda(), kb.cuda(), vt2.cuda(), blk.cuda(), out2, rows_valid=R, n_valid=n)
     assert torch.equal(out.cpu(), out2.cpu())
@@ -161,7 +161,7 @@ def test_flash_core_moderate_logits_and_partial_query_block():
     bias[1, :, :, 300:] = float("-inf")
     rows_valid, n_valid = 6, 350
     out = torch.zeros(B, R, n_valid, H * 32, dtype=torch.bfloat16, device="cuda")
-    kernels.flash_attention_bias(q.cuda(), k.cuda(), v.transpose(-1, -2).contiguous().cuda(),
+    kernels.flash_attention_bias(q.cuda(), k.cuda(), kernels.flash_v_layout(v.transpose(-1, -2)).cuda(),
                                  kernels.blocked_bias(bias).cuda(), out, rows_valid=rows_valid, n_valid=n_valid)
     w = torch.softmax((q.float() @ k.float().transpose(-1, -2) + bias[:, :, None]) * 0.6931471805599453, dim=-1)
     want = (w @ v.float()).permute(0, 2, 3, 1, 4).reshape(B, R, n, H * 32)[:, :, :n_valid]

@@ -268,11 +268,10 @@ __global__ __launch_bounds__(64 * NW, WG_PER_CU) void transition_swiglu(
         v[1] = g ? recv[1] : own[0][1];
         v[2] = g ? own[1][0] : recv[0];
         v[3] = g ? own[1][1] : recv[1];
-        if (r < rows) {
-          const u32x4 o = {v[0], v[1], v[2], v[3]};
-          __builtin_nontemporal_store(o, reinterpret_cast<u32x4*>(out + r * C + 32 * ot +
-                                                                 8 * (2 * mp + g)));
-        }
+        // (regular stores: L2 merges the eight 32-byte pieces of a row into full lines)
+        if (r < rows)
+          *reinterpret_cast<u32x4*>(out + r * C + 32 * ot + 8 * (2 * mp + g)) =
+              u32x4{v[0], v[1], v[2], v[3]};
       }
     }
   }

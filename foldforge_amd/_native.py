@@ -45,11 +45,21 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         + [c_int64, c_int32, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64,
            c_void_p],
     ),
-    "ffk_transition_workspace": (c_size_t, [c_int32, c_int32]),
+    "ffk_transition_workspace": (c_size_t, [c_int64, c_int32, c_int32]),
     "ffk_transition": (
         c_int32,
         [c_void_p] * 7
         + [c_void_p, c_size_t, c_int64, c_int32, c_int32, c_int32, c_float, c_void_p],
+    ),
+    "ffk_attention_pair_bias_workspace": (
+        c_size_t,
+        [c_int64, c_int64, c_int32, c_int32, c_int32],
+    ),
+    "ffk_attention_pair_bias": (
+        c_int32,
+        [c_void_p] * 15
+        + [c_size_t, c_int64, c_int64, c_int32, c_int32, c_int32, c_float, c_int32, c_float,
+           c_float, c_void_p],
     ),
 }
 

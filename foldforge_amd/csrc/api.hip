@@ -165,14 +165,48 @@ TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d
   return w;
 }
 
+// The fused kernel (d = 128, factor 4) takes the three weights packed chunk by chunk in its
+// LDS image order; other widths run LayerNorm -> expand (SwiGLU) -> squeeze through token
+// rows x = LN(x) [rows][d] and h [rows][factor d].
+bool transition_fused(int d, int factor) { return d == 128 && factor == 4; }
+
 struct TransitionWs {
-  bf16* w;  // the three weights, packed chunk by chunk in the kernel's LDS image order
+  bf16* w;
+  bf16 *x, *h;
   size_t bytes;
 };
-TransitionWs transition_ws(void* ws, int d, int factor) {
+TransitionWs transition_ws(void* ws, int64_t rows, int d, int factor) {
   Carver cv{static_cast<char*>(ws)};
-  TransitionWs w;
-  w.w = cv.take<bf16>((size_t)3 * factor * d * d);
+  TransitionWs w{};
+  if (transition_fused(d, factor)) {
+    w.w = cv.take<bf16>((size_t)3 * factor * d * d);
+  } else {
+    w.x = cv.take<bf16>((size_t)rows * d);
+    w.h = cv.take<bf16>((size_t)rows * factor * d);
+  }
+  w.bytes = cv.used;
+  return w;
+}
+
+int64_t pad32(int64_t n) { return (n + 31) / 32 * 32; }
+
+struct ApbWs {
+  bf16 *x, *q, *k, *vt, *gate, *og;
+  float* bias;
+  size_t bytes;
+};
+ApbWs apb_ws(void* ws, int64_t batch, int64_t n, int cs, int heads) {
+  Carver cv{static_cast<char*>(ws)};
+  const int64_t np = pad32(n);
+  const size_t tok = (size_t)batch * n * cs;
+  ApbWs w;
+  w.x = cv.take<bf16>(tok);
+  w.q = cv.take<bf16>(tok);
+  w.k = cv.take<bf16>(tok);
+  w.gate = cv.take<bf16>(tok);
+  w.og = cv.take<bf16>(tok);
+  w.vt = cv.take<bf16>((size_t)batch * cs * np);
+  w.bias = cv.take<float>((size_t)batch * heads * n * np);
   w.bytes = cv.used;
   return w;
 }
@@ -374,9 +408,9 @@ int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
   return check_launch("flash_attention_bias");
 }
 
-size_t ffk_transition_workspace(int32_t d, int32_t factor) {
-  if (d <= 0 || factor <= 0) return 0;
-  return transition_ws(nullptr, d, factor).bytes;
+size_t ffk_transition_workspace(int64_t rows, int32_t d, int32_t factor) {
+  if (rows < 0 || d <= 0 || factor <= 0) return 0;
+  return transition_ws(nullptr, rows, d, factor).bytes;
 }
 
 int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
@@ -385,19 +419,47 @@ int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
                        size_t workspace_bytes, int64_t rows, int32_t d, int32_t factor,
                        int32_t residual, float eps, void* stream) {
   if (int32_t s = check_device()) return s;
-  if (d != 128 || factor != 4)
-    return fail(FFK_ERR_INVALID, "transition: d=%d factor=%d (kernels take 128 x 4)", d, factor);
+  const bool fused = transition_fused(d, factor);
+  if (!fused && (d <= 0 || factor <= 0 || d % 64 != 0 || ((int64_t)factor * d) % 64 != 0))
+    return fail(FFK_ERR_INVALID, "transition: d=%d factor=%d (kernels take 128 x 4, or d and factor * d multiples of 64)", d, factor);
   if (rows < 0) return fail(FFK_ERR_INVALID, "transition: negative rows");
+  if (!fused && (rows + 31) / 32 > 0x7fffffffLL)
+    return fail(FFK_ERR_INVALID, "transition: %lld rows exceed the launch grid", (long long)rows);
   if (!x || !ln_w || !ln_b || !w_expand_a || !w_expand_b || !w_squeeze || !out)
     return fail(FFK_ERR_INVALID, "transition: null argument");
   if (!aligned16(x) || !aligned16(out))
     return fail(FFK_ERR_INVALID, "transition: x/out must be 16-byte aligned");
-  const TransitionWs need = transition_ws(nullptr, d, factor);
+  if (!fused && (!aligned16(w_expand_a) || !aligned16(w_expand_b) || !aligned16(w_squeeze)))
+    return fail(FFK_ERR_INVALID, "transition: weights must be 16-byte aligned");
+  const TransitionWs need = transition_ws(nullptr, rows, d, factor);
   if (!workspace || workspace_bytes < need.bytes || !aligned16(workspace))
     return fail(FFK_ERR_WORKSPACE, "transition: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
   if (rows == 0) return ok();
-  const TransitionWs w = transition_ws(workspace, d, factor);
+  const TransitionWs w = transition_ws(workspace, rows, d, factor);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!fused) {
+    launch_layer_norm(x, ln_w, ln_b, w.x, rows, d, eps, FFK_DTYPE_BF16, st);
+    RowGemmArgs g{};
+    g.x = w.x;
+    g.w0 = w_expand_a;
+    g.w1 = w_expand_b;
+    g.M = rows;
+    g.K = d;
+    g.O = 2 * factor * d;
+    g.h = w.h;
+    launch_row_gemm(g, kEpiSwiglu, st);
+    RowGemmArgs s{};
+    s.x = w.h;
+    s.w0 = w_squeeze;
+    s.M = rows;
+    s.K = factor * d;
+    s.O = d;
+    s.res = static_cast<const bf16*>(x);
+    s.out = static_cast<bf16*>(out);
+    s.residual = residual ? 1 : 0;
+    launch_row_gemm(s, kEpiResid, st);
+    return check_launch("transition");
+  }
   launch_transition_pack(w_expand_a, w_expand_b, w_squeeze, w.w, st);
   TransitionArgs a;
   a.x = static_cast<const bf16*>(x);
@@ -410,6 +472,109 @@ int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
   a.eps = eps;
   launch_transition(a, st);
   return check_launch("transition");
+}
+
+size_t ffk_attention_pair_bias_workspace(int64_t batch, int64_t n, int32_t d_single,
+                                         int32_t d_pair, int32_t n_head) {
+  if (batch <= 0 || n <= 0 || d_single <= 0 || d_pair <= 0 || n_head <= 0) return 0;
+  return apb_ws(nullptr, batch, n, d_single, n_head).bytes;
+}
+
+int32_t ffk_attention_pair_bias(
+    const void* s, const void* z, const uint8_t* key_mask, const float* ln_single_w,
+    const float* ln_single_b, const float* w_query, const float* b_query, const float* w_key,
+    const float* w_value, const float* ln_pair_w, const float* w_bias, const float* w_gate,
+    const float* w_out, void* out, void* workspace, size_t workspace_bytes, int64_t batch,
+    int64_t n, int32_t d_single, int32_t d_pair, int32_t n_head, float gate_bias,
+    int32_t residual, float eps_single, float eps_pair, void* stream) {
+  if (int32_t st = check_device()) return st;
+  if (d_pair != 128)
+    return fail(FFK_ERR_INVALID, "attention_pair_bias: d_pair=%d (kernels take 128)", d_pair);
+  if (n_head <= 0 || n_head > 32 || d_single <= 0 || d_single % 64 != 0 || d_single % n_head != 0 ||
+      (d_single / n_head) % 8 != 0 || d_single / n_head > 32)
+    return fail(FFK_ERR_INVALID, "attention_pair_bias: d_single=%d heads=%d (kernels take a multiple of 64 split into at most 32 heads of 8, 16, 24 or 32)", d_single, n_head);
+  if (batch <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "attention_pair_bias: empty shape");
+  if (batch > 65535 || n > (1 << 24))
+    return fail(FFK_ERR_INVALID, "attention_pair_bias: batch=%lld n=%lld exceed the launch grid", (long long)batch, (long long)n);
+  if (!s || !z || !key_mask || !ln_single_w || !ln_single_b || !w_query || !b_query || !w_key ||
+      !w_value || !ln_pair_w || !w_bias || !w_gate || !w_out || !out)
+    return fail(FFK_ERR_INVALID, "attention_pair_bias: null argument");
+  if (!aligned16(s) || !aligned16(z) || !aligned16(out))
+    return fail(FFK_ERR_INVALID, "attention_pair_bias: s/z/out must be 16-byte aligned");
+  if (!aligned16(w_query) || !aligned16(w_key) || !aligned16(w_value) || !aligned16(w_gate) ||
+      !aligned16(w_out))
+    return fail(FFK_ERR_INVALID, "attention_pair_bias: projection weights must be 16-byte aligned");
+  const ApbWs need = apb_ws(nullptr, batch, n, d_single, n_head);
+  if (!workspace || workspace_bytes < need.bytes || !aligned16(workspace))
+    return fail(FFK_ERR_WORKSPACE, "attention_pair_bias: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
+  const ApbWs w = apb_ws(workspace, batch, n, d_single, n_head);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t rows = batch * n;
+  const int64_t np = pad32(n);
+  const int dh = d_single / n_head;
+  launch_layer_norm(s, ln_single_w, ln_single_b, w.x, rows, d_single, eps_single, FFK_DTYPE_BF16, st);
+
+  RowGemmArgs p{};
+  p.x = w.x;
+  p.w0 = w_query;
+  p.w1 = w_key;
+  p.w2 = w_value;
+  p.w3 = w_gate;
+  p.M = rows;
+  p.K = d_single;
+  p.O = 4 * d_single;
+  p.q_bias = b_query;
+  p.q_scale = kLog2e / sqrtf((float)dh);
+  p.gate_bias = gate_bias;
+  p.q = w.q;
+  p.k = w.k;
+  p.vt = w.vt;
+  p.gate = w.gate;
+  p.n = (int)n;
+  p.np = (int)np;
+  p.heads = n_head;
+  p.dh = dh;
+  launch_row_gemm(p, kEpiApb, st);
+
+  PairBiasArgs pb;
+  pb.z = static_cast<const bf16*>(z);
+  pb.mask = key_mask;
+  pb.ln_w = ln_pair_w;
+  pb.w_bias = w_bias;
+  pb.bias = w.bias;
+  pb.tiles = batch * n * (np / 32);
+  pb.n = (int)n;
+  pb.np = (int)np;
+  pb.heads = n_head;
+  pb.eps = eps_pair;
+  launch_apb_pair_bias(pb, st);
+
+  ApbAttnArgs at;
+  at.q = w.q;
+  at.k = w.k;
+  at.vt = w.vt;
+  at.gate = w.gate;
+  at.bias = w.bias;
+  at.mask = key_mask;
+  at.og = w.og;
+  at.n = (int)n;
+  at.np = (int)np;
+  at.heads = n_head;
+  at.dh = dh;
+  at.cs = d_single;
+  launch_apb_attention(at, (int)batch, st);
+
+  RowGemmArgs o{};
+  o.x = w.og;
+  o.w0 = w_out;
+  o.M = rows;
+  o.K = d_single;
+  o.O = d_single;
+  o.res = static_cast<const bf16*>(s);
+  o.out = static_cast<bf16*>(out);
+  o.residual = residual ? 1 : 0;
+  launch_row_gemm(o, kEpiResid, st);
+  return check_launch("attention_pair_bias");
 }
 
 }  // extern "C"

@@ -65,6 +65,51 @@ void launch_transition_pack(const float* wa, const float* wb, const float* ws, b
                             hipStream_t stream);
 void launch_transition(const TransitionArgs& a, hipStream_t stream);
 
+// Token-row GEMM out[m][o] = sum_k W[o][k] x[m][k] (single track, single.hip) with one of
+// three epilogues. K % 64 == 0, O % 32 == 0; weights are the fp32 parameters.
+enum { kEpiApb = 0, kEpiSwiglu = 1, kEpiResid = 2 };
+struct RowGemmArgs {
+  const bf16* x;  // [M][K]
+  // kEpiApb: w0..w3 = to_query, to_key, to_value, to_gate ([cs][cs] each, O = 4 cs);
+  // kEpiSwiglu: w0 = expand_a, w1 = expand_b ([hid][K] each, O = 2 hid);
+  // kEpiResid: w0 = [O][K]
+  const float *w0, *w1, *w2, *w3;
+  int64_t M;
+  int K, O;
+  // kEpiApb: q = (x W_q^T + q_bias) * q_scale, k, v^T [batch][heads][dh][np] (keys permuted
+  // as in the attention kernel), gate = sigmoid(x W_g^T + gate_bias); q, k, gate [M][cs]
+  const float* q_bias;
+  float q_scale, gate_bias;
+  bf16 *q, *k, *vt, *gate;
+  int n, np, heads, dh;
+  bf16* h;  // kEpiSwiglu: [M][hid] = silu(a) * b
+  const bf16* res;  // kEpiResid: out = res + y (residual) or y
+  bf16* out;
+  int residual;
+};
+void launch_row_gemm(const RowGemmArgs& a, int epi, hipStream_t stream);
+
+struct PairBiasArgs {
+  const bf16* z;         // [batch][n][n][128]
+  const uint8_t* mask;   // [batch][n]
+  const float* ln_w;     // [128] pair-norm weight (the norm has no offset)
+  const float* w_bias;   // [heads][128]
+  float* bias;           // [batch][heads][n][np], log2 units, kMaskedLogit at masked keys
+  int64_t tiles;         // batch * n * np / 32
+  int n, np, heads;
+  float eps;
+};
+void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream);
+
+struct ApbAttnArgs {
+  const bf16 *q, *k, *vt, *gate;
+  const float* bias;
+  const uint8_t* mask;
+  bf16* og;  // [M][cs] gate * attention output
+  int n, np, heads, dh, cs;
+};
+void launch_apb_attention(const ApbAttnArgs& a, int batch, hipStream_t stream);
+
 struct PackSeg {
   const float* src;  // NULL: write zeros
   bf16* dst;

@@ -1,0 +1,395 @@
+// Single-track kernels: attention with pair bias and the wide (non-128) SwiGLU transition.
+//
+// Shapes: tokens m = b * n + i (M = batch * n rows), single width cs (a multiple of 64),
+// heads x dh with dh a multiple of 8 and at most 32. The pair input z is [batch, n, n, 128].
+//
+// Attention with pair bias (legacy/transformer.py:93-137 of the reference):
+//   x = LN_single(s); q = (x W_q^T + b_q), k = x W_k^T, v = x W_v^T, g = sigmoid(x W_g^T + gb)
+//   bias[h, i, j] = LN_pair(z[i, j]) . W_b[h]   (the pair norm has no offset)
+//   o = softmax_j(q_i . k_j / sqrt(dh) + bias[h, i, j]) over valid keys j, 0 for an empty row
+//   out = s + (g * o) W_out^T
+// is run as: LayerNorm (layernorm.hip) -> row_gemm<kEpiApb> (q, k, v^T, gate) ->
+// apb_pair_bias -> apb_attention (gate applied) -> row_gemm<kEpiResid>.
+// The wide transition is LayerNorm -> row_gemm<kEpiSwiglu> -> row_gemm<kEpiResid>.
+//
+// Logits are carried in log2 units: q is scaled by log2(e) / sqrt(dh) and the pair-bias
+// weights by log2(e), so the softmax uses exp2. Masked keys (and the padding keys past n)
+// get the finite logit kMaskedLogit: their weight is exactly 0 once any valid key is seen.
+#include "ffk_device.h"
+#include "ffk_kernels.h"
+
+namespace ffk {
+
+namespace {
+
+constexpr float kMaskedLogit = -1e30f;
+
+__device__ __forceinline__ bf16x8 zero8() {
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) r[e] = (bf16)0.f;
+  return r;
+}
+
+// 8 consecutive fp32 weights -> one bf16 MFMA operand.
+__device__ __forceinline__ bf16x8 cvt8(const float* p) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[e] = (bf16)a[e];
+    r[4 + e] = (bf16)b[e];
+  }
+  return r;
+}
+
+__device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float d) {
+  bf16x4 v;
+  v[0] = (bf16)a;
+  v[1] = (bf16)b;
+  v[2] = (bf16)c;
+  v[3] = (bf16)d;
+  *reinterpret_cast<bf16x4*>(p) = v;
+}
+
+// Position of key `key` inside the v^T rows: index bits 2 and 3 exchanged, so that the 8
+// consecutive positions a lane loads are the 8 keys its P^T operand holds.
+__device__ __forceinline__ int vkey_pos(int key) {
+  return (key & ~12) | ((key & 4) << 1) | ((key & 8) >> 1);
+}
+
+// ---------------------------------------------------------------------------- row GEMM
+// D[o][m] = sum_k W[o][k] X[m][k]: one wave computes a 32 (o) x 32 (m) tile, a workgroup
+// four o tiles of the same 32 rows of X. A = W rows (fp32 parameters converted to bf16 in
+// registers), B = X rows (bf16 tokens). k is consumed in groups of 64: for MFMA step t of a
+// group, lane half g supplies k = 64 kg + 32 g + 8 t + (0..7) of both operands, so every
+// lane streams 64 contiguous bytes of its X row and 128 of its W row per group.
+// Epilogue: lane (li, g) holds token m0 + li and outputs o = 32 ot + 8 v + 4 g + e
+// (acc[4 v + e]).
+template <int EPI>
+__global__ __launch_bounds__(256) void row_gemm(RowGemmArgs a) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
+  const int ot = blockIdx.y * 4 + wave;
+  if (ot * 32 >= a.O) return;
+  const int64_t m0 = (int64_t)blockIdx.x * 32;
+  const int64_t mr = min(m0 + li, a.M - 1);
+
+  const float* wr;
+  int seg = 0, cbase = 0;
+  if (EPI == kEpiApb) {
+    const int cs = a.O / 4;
+    seg = (ot * 32) / cs;
+    cbase = ot * 32 - seg * cs;
+    const float* base = seg == 0 ? a.w0 : seg == 1 ? a.w1 : seg == 2 ? a.w2 : a.w3;
+    wr = base + (int64_t)(cbase + li) * a.K;
+  } else if (EPI == kEpiSwiglu) {
+    // packed tile: rows 0-15 are expand_a rows 16 ot .., rows 16-31 the expand_b rows alike
+    wr = (li < 16 ? a.w0 : a.w1) + (int64_t)(ot * 16 + (li & 15)) * a.K;
+  } else {
+    wr = a.w0 + (int64_t)(ot * 32 + li) * a.K;
+  }
+  wr += 32 * g;
+  const bf16* xr = a.x + mr * a.K + 32 * g;
+
+  f32x16 acc = zero16();
+  for (int k0 = 0; k0 < a.K; k0 += 64) {
+    bf16x8 wf[4], xf[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      wf[t] = cvt8(wr + k0 + 8 * t);
+      xf[t] = ld8(xr + k0 + 8 * t);
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) acc = mfma32(wf[t], xf[t], acc);
+  }
+
+  const int64_t m = m0 + li;
+  if (m >= a.M) return;
+  if (EPI == kEpiApb) {
+    const int cs = a.O / 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = cbase + 8 * v + 4 * g;
+      float y0 = acc[4 * v], y1 = acc[4 * v + 1], y2 = acc[4 * v + 2], y3 = acc[4 * v + 3];
+      if (seg == 0) {
+        y0 = (y0 + a.q_bias[c]) * a.q_scale;
+        y1 = (y1 + a.q_bias[c + 1]) * a.q_scale;
+        y2 = (y2 + a.q_bias[c + 2]) * a.q_scale;
+        y3 = (y3 + a.q_bias[c + 3]) * a.q_scale;
+        store4(a.q + m * cs + c, y0, y1, y2, y3);
+      } else if (seg == 1) {
+        store4(a.k + m * cs + c, y0, y1, y2, y3);
+      } else if (seg == 2) {
+        const int64_t b = m / a.n;
+        const int key = (int)(m - b * a.n);
+        const int pos = vkey_pos(key);
+        const float ys[4] = {y0, y1, y2, y3};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int hh = (c + e) / a.dh, d = (c + e) - hh * a.dh;
+          a.vt[((b * a.heads + hh) * a.dh + d) * a.np + pos] = (bf16)ys[e];
+        }
+      } else {
+        const float nb = -kLog2e;
+        y0 = sigmoid_scaled((y0 + a.gate_bias) * nb);
+        y1 = sigmoid_scaled((y1 + a.gate_bias) * nb);
+        y2 = sigmoid_scaled((y2 + a.gate_bias) * nb);
+        y3 = sigmoid_scaled((y3 + a.gate_bias) * nb);
+        store4(a.gate + m * cs + c, y0, y1, y2, y3);
+      }
+    }
+  } else if (EPI == kEpiSwiglu) {
+    const int hid = a.O / 2;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float av = acc[4 * v + e], bv = acc[8 + 4 * v + e];
+        y[e] = av * sigmoid_scaled(-kLog2e * av) * bv;
+      }
+      store4(a.h + m * hid + ot * 16 + 8 * v + 4 * g, y[0], y[1], y[2], y[3]);
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = ot * 32 + 8 * v + 4 * g;
+      float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
+      if (a.residual) {
+        const bf16x4 r = *reinterpret_cast<const bf16x4*>(a.res + m * a.O + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] += (float)r[e];
+      }
+      store4(a.out + m * a.O + c, y[0], y[1], y[2], y[3]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------- pair bias
+// bias[b, h, i, j] = rstd_ij * (z_ij . W'_h - mean_ij * sum_c W'_h[c]) with
+// W'_h[c] = log2(e) * gamma[c] * W_b[h][c]; this equals LN_pair(z_ij) . W_b[h] * log2(e) for
+// the offset-free pair norm. z is exact in bf16 and W' is carried as a bf16 pair
+// hi + lo (two MFMA passes), so the bias keeps fp32 accuracy: its error does not grow with
+// the logit size (large pair logits would otherwise shift the softmax weights).
+// One wave handles a tile of 32 consecutive keys j of one (b, i): lane (li, g) loads its
+// row's channels 64 g .. 64 g + 63 (128 contiguous bytes), the statistics come from those
+// registers (two passes, halves joined across lane l ^ 32), and the heads x keys block is
+// one 32 x 32 MFMA tile (A = W' rows, B = the z rows; channel 64 g + 8 t + e feeds step t).
+__global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
+  __shared__ float wsum_s[4][32];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
+
+  bf16x8 wf[8], wl[8];
+  float rs = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int c = 64 * g + 8 * t + e;
+      const float v = li < a.heads ? kLog2e * a.ln_w[c] * a.w_bias[li * 128 + c] : 0.f;
+      wf[t][e] = (bf16)v;
+      wl[t][e] = (bf16)(v - (float)wf[t][e]);
+      rs += v;
+    }
+  }
+  rs = pair_sum(rs);
+  if (g == 0) wsum_s[wave][li] = rs;
+  __syncthreads();
+  float wsum[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) wsum[r] = wsum_s[wave][acc_row(r, g)];
+
+  const int n = a.n;
+  const int njt = a.np / 32;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < a.tiles; t += stride) {
+    const int64_t bi = t / njt;  // b * n + i
+    const int j0 = (int)(t - bi * njt) * 32;
+    const int j = min(j0 + li, n - 1);
+    const bf16* zr = a.z + (bi * n + j) * 128 + 64 * g;
+    bf16x8 zf[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) zf[u] = ld8(zr + 8 * u);
+    float s1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s1 += (float)zf[u][e];
+    const float mean = pair_sum(s1) * (1.f / 128.f);
+    float s2 = 0.f;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = (float)zf[u][e] - mean;
+        s2 += d * d;
+      }
+    const float rstd = __builtin_amdgcn_rsqf(pair_sum(s2) * (1.f / 128.f) + a.eps);
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = mfma32(wl[u], zf[u], acc);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc = mfma32(wf[u], zf[u], acc);
+
+    const int64_t b = bi / n;
+    const int64_t i = bi - b * n;
+    const int key = j0 + li;
+    const bool valid = key < n && a.mask[b * n + key] != 0;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int h = acc_row(r, g);
+      if (h < a.heads)
+        a.bias[((b * a.heads + h) * n + i) * a.np + key] =
+            valid ? rstd * (acc[r] - mean * wsum[r]) : kMaskedLogit;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------- attention
+// One workgroup per (32 queries, head, batch); its four waves split the key blocks
+// (wave w takes blocks w, w + 4, ...), run an online softmax each and are merged through LDS.
+// Per 32-key block: S^T = K Q^T + bias^T (A = k rows, B = q rows, the bias as the MFMA
+// accumulator input: lane (li, g) holds query li and keys 8 v + 4 g + e), then
+// O^T += V^T P^T (A = v^T rows in the permuted key order, B = this lane's 16 weights).
+__global__ __launch_bounds__(256) void apb_attention(ApbAttnArgs a) {
+  __shared__ float sm[4][32], sl[4][32];
+  __shared__ float so[3][64][16];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
+  const int q0 = blockIdx.x * 32, h = blockIdx.y, b = blockIdx.z;
+  const int n = a.n, dh = a.dh, cs = a.cs;
+
+  int any = 0;
+  for (int t = threadIdx.x; t < n; t += 256) any |= a.mask[(int64_t)b * n + t];
+  const bool empty = !__syncthreads_or(any);
+
+  const int qr = min(q0 + li, n - 1);
+  const bf16* qp = a.q + ((int64_t)b * n + qr) * cs + h * dh;
+  bf16x8 qf0 = zero8(), qf1 = zero8();
+  if (8 * g < dh) qf0 = ld8(qp + 8 * g);
+  if (16 + 8 * g < dh) qf1 = ld8(qp + 16 + 8 * g);
+  const float* bp = a.bias + (((int64_t)b * a.heads + h) * n + qr) * a.np + 4 * g;
+  const bf16* vp = a.vt + (((int64_t)b * a.heads + h) * dh + min(li, dh - 1)) * a.np + 8 * g;
+  const bf16* kbase = a.k + (int64_t)b * n * cs + h * dh;
+
+  float m = -INFINITY, l = 0.f;
+  f32x16 o = zero16();
+  const int nkb = a.np / 32;
+  for (int kb = wave; kb < nkb; kb += 4) {
+    const bf16* kp = kbase + (int64_t)min(kb * 32 + li, n - 1) * cs;
+    bf16x8 kf0 = zero8(), kf1 = zero8();
+    if (8 * g < dh) kf0 = ld8(kp + 8 * g);
+    if (16 + 8 * g < dh) kf1 = ld8(kp + 16 + 8 * g);
+    f32x16 s;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const f32x4 bb = *reinterpret_cast<const f32x4*>(bp + kb * 32 + 8 * v);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) s[4 * v + e] = bb[e];
+    }
+    bf16x8 vf0 = ld8(vp + kb * 32), vf1 = ld8(vp + kb * 32 + 16);
+    s = mfma32(kf0, qf0, s);
+    s = mfma32(kf1, qf1, s);
+
+    float bm = s[0];
+#pragma unroll
+    for (int r = 1; r < 16; ++r) bm = fmaxf(bm, s[r]);
+    bm = pair_max(bm);
+    const float mn = fmaxf(m, bm);
+    const float alpha = fast_exp2(m - mn);
+    m = mn;
+    float ps = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      s[r] = fast_exp2(s[r] - mn);
+      ps += s[r];
+    }
+    l = l * alpha + ps;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[r] *= alpha;
+
+    if (kb * 32 + 32 > n) {  // keys past n: their v^T entries were never written
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int key = kb * 32 + 4 * g + 8 * (j >> 2) + (j & 3);
+        if (key >= n) vf0[j] = (bf16)0.f;
+        if (key + 16 >= n) vf1[j] = (bf16)0.f;
+      }
+    }
+    bf16x8 p0, p1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      p0[j] = (bf16)s[j];
+      p1[j] = (bf16)s[8 + j];
+    }
+    o = mfma32(vf0, p0, o);
+    o = mfma32(vf1, p1, o);
+  }
+  l = pair_sum(l);
+
+  if (g == 0) {
+    sm[wave][li] = m;
+    sl[wave][li] = l;
+  }
+  __syncthreads();
+  const float mx = fmaxf(fmaxf(sm[0][li], sm[1][li]), fmaxf(sm[2][li], sm[3][li]));
+  float total = 0.f;
+#pragma unroll
+  for (int w = 0; w < 4; ++w) total += sl[w][li] * fast_exp2(sm[w][li] - mx);
+  const float f = empty ? 0.f : fast_exp2(m - mx) / total;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) o[r] *= f;
+  if (wave > 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) so[wave - 1][lane][r] = o[r];
+  }
+  __syncthreads();
+  if (wave != 0) return;
+#pragma unroll
+  for (int w = 0; w < 3; ++w)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[r] += so[w][lane][r];
+  const int qq = q0 + li;
+  if (qq >= n) return;
+  const int64_t row = ((int64_t)b * n + qq) * cs + h * dh;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int d0 = 8 * v + 4 * g;
+    if (d0 < dh) {
+      const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + row + d0);
+      store4(a.og + row + d0, o[4 * v] * (float)gv[0], o[4 * v + 1] * (float)gv[1],
+             o[4 * v + 2] * (float)gv[2], o[4 * v + 3] * (float)gv[3]);
+    }
+  }
+}
+
+dim3 gemm_grid(int64_t M, int O) {
+  return dim3((unsigned)((M + 31) / 32), (unsigned)((O + 127) / 128));
+}
+
+}  // namespace
+
+void launch_row_gemm(const RowGemmArgs& a, int epi, hipStream_t stream) {
+  const dim3 grid = gemm_grid(a.M, a.O);
+  if (epi == kEpiApb)
+    row_gemm<kEpiApb><<<grid, 256, 0, stream>>>(a);
+  else if (epi == kEpiSwiglu)
+    row_gemm<kEpiSwiglu><<<grid, 256, 0, stream>>>(a);
+  else
+    row_gemm<kEpiResid><<<grid, 256, 0, stream>>>(a);
+}
+
+void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream) {
+  int64_t blocks = (a.tiles + 15) / 16;  // about four tiles per wave
+  const int64_t cap = (int64_t)cu_count() * 8;
+  if (blocks > cap) blocks = cap;
+  if (blocks < 1) blocks = 1;
+  apb_pair_bias<<<dim3((unsigned)blocks), 256, 0, stream>>>(a);
+}
+
+void launch_apb_attention(const ApbAttnArgs& a, int batch, hipStream_t stream) {
+  apb_attention<<<dim3((unsigned)((a.n + 31) / 32), (unsigned)a.heads, (unsigned)batch), 256, 0,
+                  stream>>>(a);
+}
+
+}  // namespace ffk

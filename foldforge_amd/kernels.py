@@ -3,7 +3,8 @@
 The engine exposes ``layer_norm``, ``triangle_multiplicative_update``,
 ``triangle_attention`` and ``transition`` under ``miniworld_engine.kernels``
 (names: ``docs/guides/ENGINE-2.4.2.md:18-21`` of the reference; their signatures are
-not in the reference, so these are this library's own). Each function validates its
+not in the reference, so these are this library's own); ``attention_pair_bias`` serves
+the engine's ``single_attention`` op (``AttentionPairBias``).  Each function validates its
 tensors, allocates the output and the workspace with torch's allocator on the input's
 device, and calls the C-ABI on torch's current stream. There is no fallback: the
 module classes decide what to refuse (``unsupported``) before a call ever gets here.
@@ -170,24 +171,97 @@ def transition(
     eps: float = 1e-5,
     out: Tensor | None = None,
 ) -> Tensor:
-    """Fused SwiGLU transition of ``x [..., 128]`` bf16 (factor 4)."""
+    """SwiGLU transition of ``x [..., d]`` bf16: one fused kernel at d = 128 x 4, token-row
+    GEMMs (LayerNorm, expand with SwiGLU epilogue, squeeze + residual) at other widths."""
     _need(x.is_cuda and x.is_contiguous(), "x must be a contiguous device tensor")
     _need(x.dtype == torch.bfloat16, f"x must be bf16 (got {x.dtype})")
     d = x.shape[-1]
-    _need(d == PAIR_WIDTH, f"width {d} (the kernel takes {PAIR_WIDTH})")
     factor = expand_a.shape[0] // d
+    _need(transition_supported(d, factor),
+          f"width {d} x {factor} (the kernels take 128 x 4, or d and factor * d multiples of 64)")
+    _need(expand_a.shape == (factor * d, d) and expand_b.shape == (factor * d, d)
+          and squeeze.shape == (d, factor * d), "expand_a/expand_b [f d, d], squeeze [d, f d]")
     dev = x.device
     ps = [_param(t, dev, nm) for t, nm in zip(
         (ln_weight, ln_bias, expand_a, expand_b, squeeze),
         ("ln_weight", "ln_bias", "expand_a", "expand_b", "squeeze"))]
+    rows = x.numel() // d
     lib = _native.lib()
-    ws = _workspace(lib.ffk_transition_workspace(d, factor), dev)
+    ws = _workspace(lib.ffk_transition_workspace(rows, d, factor), dev)
     out = torch.empty_like(x) if out is None else out
     status = lib.ffk_transition(
         x.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(), ws.data_ptr(), ws.numel(),
-        x.numel() // d, d, factor, int(residual), float(eps), _stream(dev),
+        rows, d, factor, int(residual), float(eps), _stream(dev),
     )
     _native.check(status, "transition")
+    return out
+
+
+def transition_supported(d: int, factor: int) -> bool:
+    """Widths the transition kernels take."""
+    return (d == PAIR_WIDTH and factor == 4) or (d > 0 and factor > 0 and d % 64 == 0
+                                                 and (factor * d) % 64 == 0)
+
+
+def single_attention_heads_supported(d_single: int, n_head: int) -> bool:
+    """Single widths and head splits the attention-with-pair-bias kernels take."""
+    if n_head <= 0 or n_head > 32 or d_single <= 0 or d_single % 64 or d_single % n_head:
+        return False
+    dh = d_single // n_head
+    return dh % 8 == 0 and dh <= 32
+
+
+def attention_pair_bias(
+    s: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    *,
+    ln_single_weight: Tensor,
+    ln_single_bias: Tensor,
+    to_query: Tensor,
+    query_bias: Tensor,
+    to_key: Tensor,
+    to_value: Tensor,
+    ln_pair_weight: Tensor,
+    to_bias: Tensor,
+    to_gate: Tensor,
+    to_out: Tensor,
+    n_head: int,
+    gate_bias: float = 0.0,
+    residual: bool = True,
+    eps_single: float = 1e-5,
+    eps_pair: float = 1e-5,
+    out: Tensor | None = None,
+) -> Tensor:
+    """Single-track attention with pair bias: ``s [B, N, c_s]`` bf16 attends over tokens with
+    the bias ``LN_pair(z) . to_bias`` from ``z [B, N, N, 128]`` bf16, under the key mask."""
+    batch, n = _pair(z, mask)
+    _need(s.is_cuda and s.is_contiguous() and s.dtype == torch.bfloat16,
+          "s must be a contiguous bf16 device tensor")
+    _need(s.dim() == 3 and s.shape[:2] == z.shape[:2], f"s {tuple(s.shape)} does not match z")
+    cs = s.shape[-1]
+    _need(single_attention_heads_supported(cs, n_head),
+          f"single width {cs} with {n_head} heads (the kernels take a multiple of 64 split "
+          "into at most 32 heads of 8, 16, 24 or 32)")
+    dev = s.device
+    names = ("ln_single_weight", "ln_single_bias", "to_query", "query_bias", "to_key", "to_value",
+             "ln_pair_weight", "to_bias", "to_gate", "to_out")
+    tensors = (ln_single_weight, ln_single_bias, to_query, query_bias, to_key, to_value,
+               ln_pair_weight, to_bias, to_gate, to_out)
+    ps = [_param(t, dev, nm) for t, nm in zip(tensors, names)]
+    for t, nm in zip(ps, names):
+        if nm.startswith("to_") and nm != "to_bias":
+            _need(t.shape == (cs, cs), f"{nm} {tuple(t.shape)} (expected [{cs}, {cs}])")
+    _need(ps[7].shape == (n_head, PAIR_WIDTH), f"to_bias {tuple(ps[7].shape)}")
+    lib = _native.lib()
+    ws = _workspace(lib.ffk_attention_pair_bias_workspace(batch, n, cs, PAIR_WIDTH, n_head), dev)
+    out = torch.empty_like(s) if out is None else out
+    status = lib.ffk_attention_pair_bias(
+        s.data_ptr(), z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
+        ws.data_ptr(), ws.numel(), batch, n, cs, PAIR_WIDTH, n_head, float(gate_bias),
+        int(residual), float(eps_single), float(eps_pair), _stream(dev),
+    )
+    _native.check(status, "attention_pair_bias")
     return out
 
 

@@ -359,8 +359,11 @@ class Transition(EngineOp, MasterWeights, nn.Module):
             return reason
         if x.dtype != torch.bfloat16:
             return f"{x.dtype} activations (the kernel takes bf16)"
-        if self.d != 128 or self.n != 4:
-            return f"width {self.d} x {self.n} (the kernel takes 128 x 4)"
+        from foldforge_amd.kernels import transition_supported
+
+        if not transition_supported(self.d, self.n):
+            return (f"width {self.d} x {self.n} (the kernels take 128 x 4, or d and "
+                    "n * d multiples of 64)")
         return None
 
     def _forward_pytorch(self, x: Tensor, *, residual: bool = True) -> Tensor:
@@ -382,10 +385,8 @@ class Transition(EngineOp, MasterWeights, nn.Module):
 
 class AttentionPairBias(EngineOp, MasterWeights, nn.Module):
     """Single-track attention with pair bias, residual included
-    (``legacy/transformer.py:28-137``; parameters ``legacy/released.py:268-315``).
+    (``legacy/transformer.py:28-137``; parameters ``legacy/released.py:281-315``).
     The pair norm has no offset (a per-head constant is softmax-invariant)."""
-
-    backends = ("pytorch",)
 
     def __init__(self, d_single: int, d_pair: int, n_head: int = 16, gate_bias: float = 0.0,
                  backend: str = "pytorch") -> None:
@@ -401,11 +402,48 @@ class AttentionPairBias(EngineOp, MasterWeights, nn.Module):
         self.to_out = _linear(d_single, d_single)
         self._init_backend(backend)
 
+    def _unsupported_hip(self, s: Tensor, z: Tensor, mask: Tensor,
+                         extra_bias: Tensor | None = None) -> str | None:
+        reason = _pair_reason(z, mask) or hip_reason(s)
+        if reason is not None:
+            return reason
+        if s.dtype != torch.bfloat16:
+            return f"{s.dtype} single activations (the kernels take bf16)"
+        if s.dim() != 3 or s.shape[:2] != z.shape[:2] or s.shape[-1] != self.d_single:
+            return f"single shape {tuple(s.shape)} for pair {tuple(z.shape)}"
+        if z.shape[-1] != 128 or self.d_pair != 128:
+            return f"d_pair={z.shape[-1]} (the kernels take 128)"
+        from foldforge_amd.kernels import single_attention_heads_supported
+
+        if not single_attention_heads_supported(self.d_single, self.n_head):
+            return (f"d_single={self.d_single} heads={self.n_head} (the kernels take a multiple "
+                    "of 64 split into at most 32 heads of 8, 16, 24 or 32)")
+        if extra_bias is not None:
+            return "an extra attention bias is not in the hip kernels"
+        return None
+
     def _forward_pytorch(self, s: Tensor, z: Tensor, mask: Tensor, extra_bias: Tensor | None = None,
                          *, residual: bool = True) -> Tensor:
         if self.dead:
             return s if residual else torch.zeros_like(s)
         return torch_ops.attention_pair_bias(self, s, z, mask, extra_bias, residual=residual)
+
+    def _forward_hip(self, s: Tensor, z: Tensor, mask: Tensor, extra_bias: Tensor | None = None,
+                     *, residual: bool = True) -> Tensor:
+        if self.dead:
+            return s if residual else torch.zeros_like(s)
+        from foldforge_amd import kernels
+
+        return kernels.attention_pair_bias(
+            s.contiguous(), z.contiguous(), mask.contiguous(),
+            ln_single_weight=self.ln_single.weight, ln_single_bias=self.ln_single.bias,
+            to_query=self.to_query.weight, query_bias=self.to_query.bias,
+            to_key=self.to_key.weight, to_value=self.to_value.weight,
+            ln_pair_weight=self.ln_pair.weight, to_bias=self.to_bias.weight,
+            to_gate=self.to_gate.weight, to_out=self.to_out.weight, n_head=self.n_head,
+            gate_bias=self.gate_bias, residual=residual, eps_single=self.ln_single.eps,
+            eps_pair=self.ln_pair.eps,
+        )
 
 
 # ------------------------------------------------------------------------------------ block

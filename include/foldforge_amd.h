@@ -116,19 +116,46 @@ int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
                                  void* stream);
 
 /*
- * Pair (or single) transition: x + squeeze(silu(expand_a(LN(x))) * expand_b(LN(x))),
- * fully fused (the 4x hidden never reaches HBM). d = 128, factor = 4.
+ * Pair (or single) transition: x + squeeze(silu(expand_a(LN(x))) * expand_b(LN(x))) over
+ * `rows` token rows of width d. d = 128, factor = 4 runs one fused kernel (the 4x hidden
+ * never reaches HBM); other widths (d and factor * d multiples of 64, e.g. the single
+ * track's 384 x 4) run LayerNorm -> expand with SwiGLU epilogue -> squeeze + residual,
+ * keeping the hidden rows in the workspace.
  * Replaces: engine Transition.forward / `transition`
  * (src/foldforge/models/checkpoints/legacy/reference/transition.py:28-59,
  * engine parameters legacy/released.py:211-224; op name "transition",
  * src/foldforge/modules/engine/backends.py:51).
  */
-size_t ffk_transition_workspace(int32_t d, int32_t factor);
+size_t ffk_transition_workspace(int64_t rows, int32_t d, int32_t factor);
 int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
                        const float* w_expand_a, const float* w_expand_b,
                        const float* w_squeeze, void* out, void* workspace,
                        size_t workspace_bytes, int64_t rows, int32_t d, int32_t factor,
                        int32_t residual, float eps, void* stream);
+
+/*
+ * Single-track attention with pair bias, residual included:
+ *   x = LN_single(s); bias[h, i, j] = LN_pair(z[i, j]) . w_bias[h]  (pair norm without offset)
+ *   o_h = softmax_j((x w_query^T + b_query)_h . (x w_key^T)_h / sqrt(dh) + bias[h]) (x w_value^T)_h
+ *   out = s + (sigmoid(x w_gate^T + gate_bias) * o) w_out^T
+ * with the [batch, n] key mask (masked keys weigh exactly 0; a batch entry without a valid
+ * key gets o = 0). s, out [batch, n, d_single] bf16; z [batch, n, n, d_pair] bf16;
+ * d_pair = 128; d_single a multiple of 64 split into n_head <= 32 heads of dh = 8, 16, 24
+ * or 32 (the trunk: 384 = 16 x 24). `out` may alias `s`.
+ * Replaces: engine AttentionPairBias.forward, op name "single_attention"
+ * (src/foldforge/modules/engine/backends.py:50; equations
+ * src/foldforge/models/checkpoints/legacy/transformer.py:28-137 as called from
+ * legacy/pairformer.py:211-226; engine parameters legacy/released.py:281-315).
+ */
+size_t ffk_attention_pair_bias_workspace(int64_t batch, int64_t n, int32_t d_single,
+                                         int32_t d_pair, int32_t n_head);
+int32_t ffk_attention_pair_bias(
+    const void* s, const void* z, const uint8_t* key_mask, const float* ln_single_w,
+    const float* ln_single_b, const float* w_query, const float* b_query, const float* w_key,
+    const float* w_value, const float* ln_pair_w, const float* w_bias, const float* w_gate,
+    const float* w_out, void* out, void* workspace, size_t workspace_bytes, int64_t batch,
+    int64_t n, int32_t d_single, int32_t d_pair, int32_t n_head, float gate_bias,
+    int32_t residual, float eps_single, float eps_pair, void* stream);
 
 #ifdef __cplusplus
 }

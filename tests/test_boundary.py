@@ -53,9 +53,8 @@ def test_names_and_aliases():
 def test_serves_is_derived_from_the_classes():
     table = backends.SERVES
     assert set(table) == set(backends.OPS)
-    for op in ("trimul", "triangle_attention", "transition", "layernorm"):
+    for op in ("trimul", "triangle_attention", "transition", "layernorm", "single_attention"):
         assert table[op] == ("miniworld", "pytorch", "hip"), op
-    assert table["single_attention"] == ("pytorch",)
     assert table["opm"] == ()  # named, no class in this build
 
 
@@ -67,7 +66,9 @@ def test_choose_backend(monkeypatch):
     fake_gfx950(monkeypatch)
     assert backends.choose_backend("miniworld", Transition) == ("hip", None)
     assert backends.choose_backend("hip", TriangleMultiplication) == ("hip", None)
-    assert backends.choose_backend("miniworld", AttentionPairBias) == ("pytorch", None)
+    assert backends.choose_backend("miniworld", AttentionPairBias) == ("hip", None)
+    name, why = backends.choose_backend("cuda", AttentionPairBias)
+    assert name == "pytorch" and "no 'cuda' backend" in why
     name, why = backends.choose_backend("cuda", Transition)
     assert name == "pytorch" and "no 'cuda' backend" in why
     # another ROCm card: the hip kernels are gfx950 code objects
@@ -78,14 +79,14 @@ def test_choose_backend(monkeypatch):
 
 def test_plan_resolve_reports_refused_ops(monkeypatch, caplog):
     fake_gfx950(monkeypatch)
-    plan = backends.BackendPlan.make("pytorch", {"transition": "hip", "single_attention": "hip"})
+    plan = backends.BackendPlan.make("pytorch", {"transition": "hip", "single_attention": "cuda"})
     with caplog.at_level(logging.WARNING, logger="foldforge.backend"):
         plan.resolve()
     assert plan.of("transition") == "hip"
     assert plan.resolved["single_attention"].reason is not None
     assert plan.report()["fallbacks"].keys() == {"single_attention"}
     assert sum("single_attention" in r.message for r in caplog.records) == 1
-    strict = backends.BackendPlan.make("pytorch", {"single_attention": "hip"}, "error")
+    strict = backends.BackendPlan.make("pytorch", {"single_attention": "cuda"}, "error")
     with pytest.raises(backends.BackendUnsupportedError):
         strict.resolve()
 
@@ -154,7 +155,8 @@ def test_composite_children_are_set_one_by_one(monkeypatch):
     assert block.tri_multi_outgoing.backend == "hip"
     assert block.tri_atten_ending.backend == "hip"
     assert block.transition_pair.backend == "hip"
-    assert block.single_attention.backend == "pytorch"  # no hip kernel: not a refusal
+    assert block.single_attention.backend == "hip"
+    assert block.single_transition.backend == "hip"
     # widths outside the kernels (32 != 128) are refused per call even on a gfx950
     from foldforge_amd import modules
 

@@ -1,7 +1,7 @@
 """GPU: a whole Pairformer block and a short trunk through the drop-in boundary.
 
-``foldforge_amd.load(..., backend="miniworld")`` on a gfx950 must serve every pair op with
-the native ``hip`` backend (checked through the guard's host-call counters), and the
+``foldforge_amd.load(..., backend="miniworld")`` on a gfx950 must serve every op (pair and
+single track) with the native ``hip`` backend (checked through the guard's host-call counters), and the
 result must match the fp64 oracle: the block's update within rel-RMS 3e-2 on the valid
 pairs, the trunk's final pair and single within 5e-2. At the full N = 512 the
 size-independent properties are checked: finiteness, run-to-run bitwise determinism,
@@ -50,14 +50,13 @@ def test_block_update_matches_oracle():
     assert rr <= 3e-2
 
 
-def test_load_serves_every_pair_op_with_hip_and_matches_oracle():
+def test_load_serves_every_op_with_hip_and_matches_oracle():
     n = 96
     model = foldforge_amd.load(backend="miniworld", device="cuda", blocks=2, seed=1, d_single=384)
     report = model.foldforge_load_report["engine_backends"]
     backends_of = {name: r["backend"] for name, r in report["modules"].items()}
     for name, backend in backends_of.items():
-        if ".single_" not in name:
-            assert backend == "hip", (name, backend)
+        assert backend == "hip", (name, backend)
     g = torch.Generator().manual_seed(2)
     z = torch.randn(1, n, n, 128, generator=g).bfloat16()
     s = torch.randn(1, n, 384, generator=g).bfloat16()
@@ -66,10 +65,9 @@ def test_load_serves_every_pair_op_with_hip_and_matches_oracle():
     with torch.no_grad():
         pair, single = model(z.cuda(), mask.cuda(), s.cuda(), passes=1)
     served = serving.report_observations(model)["modules"]
-    pair_ops = {k: v for k, v in served.items() if ".single_" not in k}
-    hip_calls = sum(v["served_host_calls"].get("hip", 0) for v in pair_ops.values())
-    assert hip_calls == 2 * 5, served  # 5 pair ops per block served natively
-    assert all(not v["refused_host_calls"] for v in pair_ops.values())
+    hip_calls = sum(v["served_host_calls"].get("hip", 0) for v in served.values())
+    assert hip_calls == 2 * 7, served  # 5 pair + 2 single-track ops per block served natively
+    assert all(not v["refused_host_calls"] for v in served.values())
     state = model.state_dict()
     wz, ws = z, s
     for i in range(2):

@@ -17,7 +17,16 @@ Reported beside it, in the same JSON line:
   host's cores on the same block and input (1 warm-up, median of 3), with the GPU
   result's rel-RMS against it.
 
-``python bench.py [--steps K] [--warmup W] [--n 512] [--no-cpu-baseline]``; one GPU only.
+* ``trunk``: the 48-block trunk with its single track (c_s 384, 16 x 24 attention with
+  pair bias) at N = 512, all-ones mask, z and s ~N(0,1), 3 passes (144 block evaluations),
+  every op on ``hip``: ms per trunk run, ms per block, the single track's share, and the
+  residual-stream RMS after the last block.
+
+``python bench.py [--steps K] [--warmup W] [--n 512] [--no-cpu-baseline] [--no-trunk]``;
+one GPU only. ``--ladder`` instead prints one JSON line per length of the trunk's length
+ladder (N = 768 ... 2048 full trunks, then single blocks upward until the device is out of
+memory); ``--trunk-only`` prints the trunk line alone (with the engine ``pytorch``
+backend's trunk time beside it, and the fp32 CPU oracle's per-block time x 144).
 """
 
 from __future__ import annotations
@@ -50,6 +59,10 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--cpu-runs", type=int, default=3)
     ap.add_argument("--copy-reference-mb", type=int, default=0,
                     help="also run a plain device copy of this many MiB (the HBM-counter calibration)")
+    ap.add_argument("--no-trunk", action="store_true", help="skip the 48-block trunk measurement")
+    ap.add_argument("--trunk-only", action="store_true")
+    ap.add_argument("--ladder", action="store_true")
+    ap.add_argument("--ladder-max", type=int, default=16384)
     return ap.parse_args()
 
 
@@ -146,6 +159,157 @@ def recorded_traffic(kernel: str) -> float | None:
     return None
 
 
+TRUNK_BLOCKS, TRUNK_PASSES, D_SINGLE = 48, 3, 384
+
+
+def block_gflop(n: int, d_single: int = 0) -> float:
+    """Algorithmic GFLOP of one block: TriMul x2, TriAttn x2 (core + projections), pair
+    transition, and with a single track the attention with pair bias + single transition."""
+    c, h, hd = 128, 128, 128
+    trimul = 2 * n**3 * h + n * n * (8 * c * h + 2 * c * c + 2 * h * c)
+    triattn = 4 * n**3 * hd + n * n * (8 * c * hd + 2 * c * 4 + 2 * hd * c)
+    trans = n * n * (4 * c * 4 * c + 2 * 4 * c * c)
+    total = 2 * trimul + 2 * triattn + trans
+    if d_single:
+        cs = d_single
+        total += n * (8 * cs * cs + 2 * cs * cs) + 4 * n * n * cs + 2 * n * n * c * 16
+        total += n * (4 * cs * 4 * cs + 2 * 4 * cs * cs)
+    return total / 1e9
+
+
+def trunk_inputs(n: int, seed: int = 0):
+    import torch
+
+    g = torch.Generator().manual_seed(seed + 7)
+    z = torch.randn(1, n, n, 128, generator=g).bfloat16()
+    s = torch.randn(1, n, D_SINGLE, generator=g).bfloat16()
+    mask = torch.ones(1, n, dtype=torch.bool)
+    return z, s, mask
+
+
+def time_trunk(model, z, s, mask, runs: int, warmup: int = 1) -> tuple[float, object]:
+    """ms per trunk run (TRUNK_PASSES passes over the blocks) between HIP events."""
+    import torch
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            out = model(z, mask, s, passes=TRUNK_PASSES)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(runs):
+            out = model(z, mask, s, passes=TRUNK_PASSES)
+        end.record()
+        end.synchronize()
+    return start.elapsed_time(end) / runs, out
+
+
+def trunk_measure(n: int, runs: int, *, pytorch_too: bool = False, cpu_too: bool = False) -> dict:
+    """The 48-block trunk with its single track, every op on hip (guard: error)."""
+    import torch
+
+    import foldforge_amd
+
+    model = foldforge_amd.load(backend="miniworld", device="cuda", blocks=TRUNK_BLOCKS, seed=0,
+                               d_single=D_SINGLE, unsupported="error")
+    z_cpu, s_cpu, mask_cpu = trunk_inputs(n)
+    z, s, mask = z_cpu.cuda(), s_cpu.cuda(), mask_cpu.cuda()
+    ms, (pair, single) = time_trunk(model, z, s, mask, runs)
+    evals = TRUNK_BLOCKS * TRUNK_PASSES
+    blk = model.blocks[0]
+    with torch.no_grad():
+        zb = blk(z, mask)
+        apb_ms = event_time_ms(lambda: blk.single_attention(s, zb, mask), 20)
+        str_ms = event_time_ms(lambda: blk.single_transition(s), 20)
+    rms = lambda t: float(t.float().pow(2).mean().sqrt())  # noqa: E731
+    gf = block_gflop(n, D_SINGLE)
+    out = {
+        "workload": f"48-block Pairformer trunk with single track, N={n}, c_z=128, c_s={D_SINGLE}, "
+                    f"APB 16x24, {TRUNK_PASSES} passes ({evals} block evaluations), all-ones mask, "
+                    "z, s ~N(0,1), seeded random init (to_out/squeeze x0.25)",
+        "n": n, "ms_per_trunk": round(ms, 2), "ms_per_block": round(ms / evals, 4),
+        "trunk_tflops": round(gf * evals / ms, 1),
+        "single_track_us_per_block": {"attention_pair_bias": round(apb_ms * 1e3, 1),
+                                      "single_transition": round(str_ms * 1e3, 1)},
+        "final_rms": {"pair": round(rms(pair), 4), "single": round(rms(single), 4)},
+        "finite": bool(torch.isfinite(pair.float()).all() and torch.isfinite(single.float()).all()),
+    }
+    if pytorch_too:
+        ref = foldforge_amd.load(backend="pytorch", device="cuda", blocks=TRUNK_BLOCKS, seed=0,
+                                 d_single=D_SINGLE)
+        ms_ref, (pr, sr) = time_trunk(ref, z, s, mask, 1)
+        where = mask[:, :, None] & mask[:, None, :]
+        from oracle import pairstack as ps
+
+        out["pytorch_backend"] = {
+            "ms_per_trunk": round(ms_ref, 1),
+            "hip_speedup": round(ms_ref / ms, 2),
+            "hip_vs_pytorch_rel_rms": {"pair": round(ps.rel_rms(pair.cpu().double(), pr.cpu().double(),
+                                                                 where.cpu()), 5),
+                                       "single": round(ps.rel_rms(single.cpu().double(),
+                                                                  sr.cpu().double()), 5)},
+        }
+        del ref
+    if cpu_too:
+        from oracle import pairstack as ps
+
+        threads = min(16, os.cpu_count() or 1)
+        torch.set_num_threads(threads)
+        state = {k[len("blocks.0."):]: v.cpu() for k, v in model.state_dict().items()
+                 if k.startswith("blocks.0.")}
+        ps.pairformer_block(z_cpu, mask_cpu, state, s=s_cpu)
+        t0 = time.perf_counter()
+        ps.pairformer_block(z_cpu, mask_cpu, state, s=s_cpu)
+        per_block = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(per_block * evals, 1), "unit": "s per trunk run",
+                               "cores": threads, "kind": "port",
+                               "sample": f"one block with single track at N={n} (fp32 oracle, 1 warm-up, "
+                                         f"1 timed) x {evals}: an extrapolation"}
+    return out
+
+
+def ladder(max_n: int) -> list[dict]:
+    """Config 5: full trunks at N = 768 .. 2048, then single blocks (with single track) at
+    larger N until the device runs out of memory."""
+    import torch
+
+    import foldforge_amd
+
+    lines = []
+    for n in (768, 1024, 1536, 2048):
+        torch.cuda.empty_cache()
+        lines.append(trunk_measure(n, 1))
+        print(json.dumps({"ladder": lines[-1]}), flush=True)
+    model = foldforge_amd.load(backend="miniworld", device="cuda", blocks=1, seed=0,
+                               d_single=D_SINGLE, unsupported="error")
+    blk = model.blocks[0]
+    for n in (3072, 4096, 6144, 8192, 10240, 12288, 16384):
+        if n > max_n:
+            break
+        torch.cuda.empty_cache()
+        try:
+            z_cpu, s_cpu, mask_cpu = trunk_inputs(n)
+            z, s, mask = z_cpu.cuda(), s_cpu.cuda(), mask_cpu.cuda()
+            del z_cpu
+            with torch.no_grad():
+                blk(z, mask, s)
+                torch.cuda.synchronize()
+                ms = event_time_ms(lambda: blk(z, mask, s), 1)
+            peak = torch.cuda.max_memory_allocated() / 2**30
+            row = {"n": n, "ms_per_block": round(ms, 2),
+                   "block_tflops": round(block_gflop(n, D_SINGLE) / ms, 1),
+                   "ms_per_trunk_extrapolated": round(ms * TRUNK_BLOCKS * TRUNK_PASSES, 1),
+                   "peak_gib": round(peak, 1)}
+        except torch.cuda.OutOfMemoryError as exc:
+            row = {"n": n, "out_of_memory": str(exc).splitlines()[0][:160]}
+        lines.append(row)
+        print(json.dumps({"ladder": row}), flush=True)
+        z = s = mask = None
+        if "out_of_memory" in row:
+            break
+    return lines
+
+
 def cpu_baseline(z, mask, state, gpu_out, runs: int) -> dict:
     import platform
 
@@ -194,6 +358,13 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.ladder:
+        ladder(args.ladder_max)
+        return 0
+    if args.trunk_only:
+        print(json.dumps({"trunk": trunk_measure(512, max(1, args.steps // 10), pytorch_too=True,
+                                                 cpu_too=not args.no_cpu_baseline)}), flush=True)
+        return 0
     dev = torch.device("cuda:0")
     n = args.n
     length = real_length(n, args.seed)
@@ -237,9 +408,12 @@ def main() -> int:
         base = cpu_baseline(z_cpu, mask_cpu, block.state_dict(), gpu_out, args.cpu_runs)
         print(f"cpu baseline {base['value']} ms/block on {base['cores']} threads", file=sys.stderr, flush=True)
 
-    gflop = (2 * (2 * n**3 * 128 + n * n * (8 * 128 * 128 + 2 * 128 * 128 + 2 * 128 * 128))
-             + 2 * (4 * n**3 * 4 * 32 + n * n * (8 * 128 * 128 + 2 * 128 * 4 + 2 * 128 * 128))
-             + n * n * (4 * 128 * 512 + 2 * 512 * 128)) / 1e9
+    gflop = block_gflop(n)
+    trunk = None
+    if not args.no_trunk:
+        trunk = trunk_measure(512, 2)
+        print(f"trunk {trunk['ms_per_trunk']} ms ({trunk['ms_per_block']} ms/block)", file=sys.stderr,
+              flush=True)
     line = {
         "metric": METRIC,
         "value": round(ms_per_step, 4),
@@ -262,6 +436,7 @@ def main() -> int:
         "roofline": roof,
         "kernels": {"layer_norm": ln, **({"copy_reference": copy} if copy else {})},
         "cpu_baseline": base,
+        "trunk": trunk,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -269,36 +269,46 @@ def pairformer_block(
     transposed_bias: bool = False,
     eps: float = 1e-5,
     dtype: torch.dtype = torch.float32,
+    io_dtype: torch.dtype | None = None,
 ) -> Tensor | tuple[Tensor, Tensor]:
     """One sequential (AF3) Pairformer block (``legacy/pairformer.py:191-230``).
 
     ``z <- TM_out(z); z <- TM_in(z); z <- TA_start(z); z <- TA_end(z); z <- Tr(z)``;
     with a single track ``s <- APB(s, z); s <- Tr_s(s)``. ``params`` holds the
     block's engine keys (``tri_multi_outgoing.to_left.weight`` ...).
+
+    ``io_dtype`` (e.g. bf16) rounds the residual stream to that dtype after every op, as
+    an engine op returns ``x + f(x)`` in its input dtype (``README.md:143-145``; bf16
+    activations, ``src/foldforge/modules/engine/configure.py:73-99``); the arithmetic
+    inside each op stays in ``dtype``. None keeps the stream in ``dtype`` throughout.
     """
     kw = {"eps": eps, "dtype": dtype}
-    z = triangle_multiplication(
+
+    def io(t: Tensor) -> Tensor:
+        return t if io_dtype is None else t.to(io_dtype).to(dtype)
+
+    z = io(triangle_multiplication(
         z, mask, sub_params(params, "tri_multi_outgoing"), outgoing=True, **kw
-    )
-    z = triangle_multiplication(
+    ))
+    z = io(triangle_multiplication(
         z, mask, sub_params(params, "tri_multi_incoming"), outgoing=False, **kw
-    )
-    z = triangle_attention(
+    ))
+    z = io(triangle_attention(
         z, mask, sub_params(params, "tri_atten_starting"), starting=True,
         n_head=n_head_pair, transposed_bias=transposed_bias, **kw,
-    )
-    z = triangle_attention(
+    ))
+    z = io(triangle_attention(
         z, mask, sub_params(params, "tri_atten_ending"), starting=False,
         n_head=n_head_pair, transposed_bias=transposed_bias, **kw,
-    )
-    z = transition(z, sub_params(params, "transition_pair"), **kw)
+    ))
+    z = io(transition(z, sub_params(params, "transition_pair"), **kw))
     if s is None:
         return z
-    s = attention_pair_bias(
+    s = io(attention_pair_bias(
         s, z, mask, sub_params(params, "single_attention"), n_head=n_head_single,
         gate_bias=single_gate_bias, **kw,
-    )
-    s = transition(s, sub_params(params, "single_transition"), **kw)
+    ))
+    s = io(transition(s, sub_params(params, "single_transition"), **kw))
     return z, s
 
 

@@ -299,3 +299,24 @@ def test_a_planted_mistake_is_caught(monkeypatch):
     broken["to_left.weight"], broken["to_right.weight"] = p["to_right.weight"], p["to_left.weight"]
     wrong = ps.triangle_multiplication(z, mask, broken, outgoing=True, dtype=F64)
     assert np.abs(wrong.numpy() - want).max() > 1e-3
+
+
+def test_block_io_dtype_rounds_the_stream_between_ops():
+    n, c, h, heads, d = 5, 6, 4, 2, 3
+    params = {}
+    for prefix, shapes, seed in (
+        ("tri_multi_outgoing", _tm_shapes(c, h), 11), ("tri_multi_incoming", _tm_shapes(c, h), 12),
+        ("tri_atten_starting", _ta_shapes(c, heads, d), 13), ("tri_atten_ending", _ta_shapes(c, heads, d), 14),
+    ):
+        params.update({f"{prefix}.{k}": v for k, v in _rand_params(shapes, seed).items()})
+    tr = {"ln_in.weight": (c,), "ln_in.bias": (c,), "expand_a.weight": (4 * c, c),
+          "expand_b.weight": (4 * c, c), "squeeze.weight": (c, 4 * c)}
+    params.update({f"transition_pair.{k}": v for k, v in _rand_params(tr, 15).items()})
+    g = torch.Generator().manual_seed(16)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(1, n, dtype=torch.bool)
+    plain = ps.pairformer_block(z, mask, params, n_head_pair=heads, dtype=F64)
+    assert torch.equal(plain, ps.pairformer_block(z, mask, params, n_head_pair=heads, dtype=F64, io_dtype=None))
+    rounded = ps.pairformer_block(z, mask, params, n_head_pair=heads, dtype=F64, io_dtype=torch.bfloat16)
+    assert torch.equal(rounded, rounded.bfloat16().double())  # the stream leaves each op in bf16
+    assert 0 < ps.rel_rms(rounded, plain) < 2e-2

@@ -166,13 +166,13 @@ TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d
 }
 
 // The fused kernel (d = 128, factor 4) takes the three weights packed chunk by chunk in its
-// LDS image order; other widths run LayerNorm -> expand (SwiGLU) -> squeeze through token
-// rows x = LN(x) [rows][d] and h [rows][factor d].
+// LDS image order; other widths run expand (LayerNorm prologue, SwiGLU epilogue) -> squeeze
+// through the hidden rows h [rows][factor d] (fp32).
 bool transition_fused(int d, int factor) { return d == 128 && factor == 4; }
 
 struct TransitionWs {
   bf16* w;
-  bf16 *x, *h;
+  float* h;
   size_t bytes;
 };
 TransitionWs transition_ws(void* ws, int64_t rows, int d, int factor) {
@@ -181,8 +181,7 @@ TransitionWs transition_ws(void* ws, int64_t rows, int d, int factor) {
   if (transition_fused(d, factor)) {
     w.w = cv.take<bf16>((size_t)3 * factor * d * d);
   } else {
-    w.x = cv.take<bf16>((size_t)rows * d);
-    w.h = cv.take<bf16>((size_t)rows * factor * d);
+    w.h = cv.take<float>((size_t)rows * factor * d);
   }
   w.bytes = cv.used;
   return w;
@@ -191,8 +190,8 @@ TransitionWs transition_ws(void* ws, int64_t rows, int d, int factor) {
 int64_t pad32(int64_t n) { return (n + 31) / 32 * 32; }
 
 struct ApbWs {
-  bf16 *x, *q, *k, *vt, *gate, *og;
-  float* bias;
+  bf16 *q, *k, *vt, *gate;
+  float *og, *bias;
   size_t bytes;
 };
 ApbWs apb_ws(void* ws, int64_t batch, int64_t n, int cs, int heads) {
@@ -200,11 +199,10 @@ ApbWs apb_ws(void* ws, int64_t batch, int64_t n, int cs, int heads) {
   const int64_t np = pad32(n);
   const size_t tok = (size_t)batch * n * cs;
   ApbWs w;
-  w.x = cv.take<bf16>(tok);
   w.q = cv.take<bf16>(tok);
   w.k = cv.take<bf16>(tok);
   w.gate = cv.take<bf16>(tok);
-  w.og = cv.take<bf16>(tok);
+  w.og = cv.take<float>(tok);
   w.vt = cv.take<bf16>((size_t)batch * cs * np);
   w.bias = cv.take<float>((size_t)batch * heads * n * np);
   w.bytes = cv.used;
@@ -420,8 +418,8 @@ int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
                        int32_t residual, float eps, void* stream) {
   if (int32_t s = check_device()) return s;
   const bool fused = transition_fused(d, factor);
-  if (!fused && (d <= 0 || factor <= 0 || d % 64 != 0 || ((int64_t)factor * d) % 64 != 0))
-    return fail(FFK_ERR_INVALID, "transition: d=%d factor=%d (kernels take 128 x 4, or d and factor * d multiples of 64)", d, factor);
+  if (!fused && (d <= 0 || factor <= 0 || d % 64 != 0 || d > kLnGemmMaxK || ((int64_t)factor * d) % 64 != 0))
+    return fail(FFK_ERR_INVALID, "transition: d=%d factor=%d (kernels take 128 x 4, or d <= %d and factor * d multiples of 64)", d, factor, kLnGemmMaxK);
   if (rows < 0) return fail(FFK_ERR_INVALID, "transition: negative rows");
   if (!fused && (rows + 31) / 32 > 0x7fffffffLL)
     return fail(FFK_ERR_INVALID, "transition: %lld rows exceed the launch grid", (long long)rows);
@@ -438,18 +436,20 @@ int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
   const TransitionWs w = transition_ws(workspace, rows, d, factor);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (!fused) {
-    launch_layer_norm(x, ln_w, ln_b, w.x, rows, d, eps, FFK_DTYPE_BF16, st);
     RowGemmArgs g{};
-    g.x = w.x;
+    g.ln_x = static_cast<const bf16*>(x);
+    g.ln_w = ln_w;
+    g.ln_b = ln_b;
+    g.eps = eps;
     g.w0 = w_expand_a;
     g.w1 = w_expand_b;
     g.M = rows;
     g.K = d;
     g.O = 2 * factor * d;
-    g.h = w.h;
-    launch_row_gemm(g, kEpiSwiglu, st);
+    g.h32 = w.h;
+    launch_row_gemm(g, kEpiSwiglu, kXLn, st);
     RowGemmArgs s{};
-    s.x = w.h;
+    s.x32 = w.h;
     s.w0 = w_squeeze;
     s.M = rows;
     s.K = factor * d;
@@ -457,7 +457,7 @@ int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
     s.res = static_cast<const bf16*>(x);
     s.out = static_cast<bf16*>(out);
     s.residual = residual ? 1 : 0;
-    launch_row_gemm(s, kEpiResid, st);
+    launch_row_gemm(s, kEpiResid, kXF32, st);
     return check_launch("transition");
   }
   launch_transition_pack(w_expand_a, w_expand_b, w_squeeze, w.w, st);
@@ -490,9 +490,9 @@ int32_t ffk_attention_pair_bias(
   if (int32_t st = check_device()) return st;
   if (d_pair != 128)
     return fail(FFK_ERR_INVALID, "attention_pair_bias: d_pair=%d (kernels take 128)", d_pair);
-  if (n_head <= 0 || n_head > 32 || d_single <= 0 || d_single % 64 != 0 || d_single % n_head != 0 ||
-      (d_single / n_head) % 8 != 0 || d_single / n_head > 32)
-    return fail(FFK_ERR_INVALID, "attention_pair_bias: d_single=%d heads=%d (kernels take a multiple of 64 split into at most 32 heads of 8, 16, 24 or 32)", d_single, n_head);
+  if (n_head <= 0 || n_head > 32 || d_single <= 0 || d_single % 64 != 0 || d_single > kLnGemmMaxK ||
+      d_single % n_head != 0 || (d_single / n_head) % 8 != 0 || d_single / n_head > 32)
+    return fail(FFK_ERR_INVALID, "attention_pair_bias: d_single=%d heads=%d (kernels take a multiple of 64 up to %d split into at most 32 heads of 8, 16, 24 or 32)", d_single, n_head, kLnGemmMaxK);
   if (batch <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "attention_pair_bias: empty shape");
   if (batch > 65535 || n > (1 << 24))
     return fail(FFK_ERR_INVALID, "attention_pair_bias: batch=%lld n=%lld exceed the launch grid", (long long)batch, (long long)n);
@@ -512,10 +512,11 @@ int32_t ffk_attention_pair_bias(
   const int64_t rows = batch * n;
   const int64_t np = pad32(n);
   const int dh = d_single / n_head;
-  launch_layer_norm(s, ln_single_w, ln_single_b, w.x, rows, d_single, eps_single, FFK_DTYPE_BF16, st);
-
   RowGemmArgs p{};
-  p.x = w.x;
+  p.ln_x = static_cast<const bf16*>(s);
+  p.ln_w = ln_single_w;
+  p.ln_b = ln_single_b;
+  p.eps = eps_single;
   p.w0 = w_query;
   p.w1 = w_key;
   p.w2 = w_value;
@@ -534,7 +535,7 @@ int32_t ffk_attention_pair_bias(
   p.np = (int)np;
   p.heads = n_head;
   p.dh = dh;
-  launch_row_gemm(p, kEpiApb, st);
+  launch_row_gemm(p, kEpiApb, kXLn, st);
 
   PairBiasArgs pb;
   pb.z = static_cast<const bf16*>(z);
@@ -565,7 +566,7 @@ int32_t ffk_attention_pair_bias(
   launch_apb_attention(at, (int)batch, st);
 
   RowGemmArgs o{};
-  o.x = w.og;
+  o.x32 = w.og;
   o.w0 = w_out;
   o.M = rows;
   o.K = d_single;
@@ -573,7 +574,7 @@ int32_t ffk_attention_pair_bias(
   o.res = static_cast<const bf16*>(s);
   o.out = static_cast<bf16*>(out);
   o.residual = residual ? 1 : 0;
-  launch_row_gemm(o, kEpiResid, st);
+  launch_row_gemm(o, kEpiResid, kXF32, st);
   return check_launch("attention_pair_bias");
 }
 

@@ -66,10 +66,17 @@ void launch_transition_pack(const float* wa, const float* wb, const float* ws, b
 void launch_transition(const TransitionArgs& a, hipStream_t stream);
 
 // Token-row GEMM out[m][o] = sum_k W[o][k] x[m][k] (single track, single.hip) with one of
-// three epilogues. K % 64 == 0, O % 32 == 0; weights are the fp32 parameters.
+// three epilogues, x either LayerNorm(ln_x) (kXLn, K <= kLnGemmMaxK) or fp32 rows x32 (kXF32).
+// K % 64 == 0, O % 32 == 0; weights are the fp32 parameters. Pairs served: (kEpiApb, kXLn),
+// (kEpiSwiglu, kXLn), (kEpiResid, kXF32).
 enum { kEpiApb = 0, kEpiSwiglu = 1, kEpiResid = 2 };
+enum { kXLn = 0, kXF32 = 1 };
+constexpr int kLnGemmMaxK = 768;
 struct RowGemmArgs {
-  const bf16* x;  // [M][K]
+  const bf16* ln_x;             // kXLn: [M][K] rows to normalise with ln_w, ln_b, eps
+  const float *ln_w, *ln_b;
+  float eps;
+  const float* x32;             // kXF32: [M][K]
   // kEpiApb: w0..w3 = to_query, to_key, to_value, to_gate ([cs][cs] each, O = 4 cs);
   // kEpiSwiglu: w0 = expand_a, w1 = expand_b ([hid][K] each, O = 2 hid);
   // kEpiResid: w0 = [O][K]
@@ -82,12 +89,12 @@ struct RowGemmArgs {
   float q_scale, gate_bias;
   bf16 *q, *k, *vt, *gate;
   int n, np, heads, dh;
-  bf16* h;  // kEpiSwiglu: [M][hid] = silu(a) * b
+  float* h32;  // kEpiSwiglu: [M][hid] = silu(a) * b
   const bf16* res;  // kEpiResid: out = res + y (residual) or y
   bf16* out;
   int residual;
 };
-void launch_row_gemm(const RowGemmArgs& a, int epi, hipStream_t stream);
+void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream);
 
 struct PairBiasArgs {
   const bf16* z;         // [batch][n][n][128]
@@ -105,7 +112,7 @@ struct ApbAttnArgs {
   const bf16 *q, *k, *vt, *gate;
   const float* bias;
   const uint8_t* mask;
-  bf16* og;  // [M][cs] gate * attention output
+  float* og;  // [M][cs] gate * attention output
   int n, np, heads, dh, cs;
 };
 void launch_apb_attention(const ApbAttnArgs& a, int batch, hipStream_t stream);

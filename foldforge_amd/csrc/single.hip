@@ -60,20 +60,51 @@ __device__ __forceinline__ int vkey_pos(int key) {
 }
 
 // ---------------------------------------------------------------------------- row GEMM
-// D[o][m] = sum_k W[o][k] X[m][k]: one wave computes a 32 (o) x 32 (m) tile, a workgroup
-// four o tiles of the same 32 rows of X. A = W rows (fp32 parameters converted to bf16 in
-// registers), B = X rows (bf16 tokens). k is consumed in groups of 64: for MFMA step t of a
-// group, lane half g supplies k = 64 kg + 32 g + 8 t + (0..7) of both operands, so every
-// lane streams 64 contiguous bytes of its X row and 128 of its W row per group.
+// D[o][m] = sum_k W[o][k] X[m][k] over 32 rows of X per workgroup: A = W rows (fp32 parameters,
+// converted in registers), B = X rows. The workgroup's 8 waves cover NO output tiles of 32
+// with KS waves each (NO * KS = 8): the KS waves of a tile split k in groups of 64 (part p
+// takes groups p, p + KS, ...), keep the next group's global loads in flight while
+// multiplying the current one, and add their partial tiles through LDS; part 0 runs the
+// epilogue. For MFMA step t of a group, lane half g supplies k = 64 kg + 32 g + 8 t + (0..7)
+// of both operands.
+// Precision: activations enter as fp32 and are split into bf16 hi + lo (two MFMAs), so only
+// the weights are rounded to bf16.
+// X sources: kXLn = LayerNorm of bf16 rows (ln_x [M][K], statistics and affine in fp32, the
+// normalised tile staged in LDS once per workgroup as hi / lo rows); kXF32 = fp32 rows
+// streamed from x32 [M][K].
 // Epilogue: lane (li, g) holds token m0 + li and outputs o = 32 ot + 8 v + 4 g + e
 // (acc[4 v + e]).
-template <int EPI>
-__global__ __launch_bounds__(256) void row_gemm(RowGemmArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
-  const int ot = blockIdx.y * 4 + wave;
-  if (ot * 32 >= a.O) return;
+__device__ __forceinline__ void split8(const f32x4& a, const f32x4& b, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hi[e] = (bf16)a[e];
+    hi[4 + e] = (bf16)b[e];
+    lo[e] = (bf16)(a[e] - (float)hi[e]);
+    lo[4 + e] = (bf16)(b[e] - (float)hi[4 + e]);
+  }
+}
+
+constexpr int kGemmWaves = 8;
+
+size_t row_gemm_lds(int xsrc, int K, int no) {
+  const size_t red = (size_t)(kGemmWaves - no) * 64 * 16 * sizeof(float);
+  return xsrc == kXLn ? red + (size_t)2 * 32 * (K + 8) * sizeof(bf16) : red;
+}
+
+template <int EPI, int XSRC, int NO>
+__global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
+  constexpr int KS = kGemmWaves / NO;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  float* red = reinterpret_cast<float*>(smem);  // [NO][KS - 1][64][16]
+  bf16* xs_hi = reinterpret_cast<bf16*>(smem + (kGemmWaves - NO) * 64 * 16 * sizeof(float));
+  const int xstride = a.K + 8;  // [32][K + 8]: rows 16 bytes apart modulo 256, conflict-free
+  bf16* xs_lo = xs_hi + 32 * xstride;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, g = lane >> 5;
+  const int osub = wave / KS, part = wave % KS;
+  const int ot = blockIdx.y * NO + osub;
+  const bool active = ot * 32 < a.O;
   const int64_t m0 = (int64_t)blockIdx.x * 32;
-  const int64_t mr = min(m0 + li, a.M - 1);
+  const int G = a.K / 64;
 
   const float* wr;
   int seg = 0, cbase = 0;
@@ -90,22 +121,113 @@ __global__ __launch_bounds__(256) void row_gemm(RowGemmArgs a) {
     wr = a.w0 + (int64_t)(ot * 32 + li) * a.K;
   }
   wr += 32 * g;
-  const bf16* xr = a.x + mr * a.K + 32 * g;
+  const float* x32 = a.x32 + min(m0 + li, a.M - 1) * a.K + 32 * g;
 
   f32x16 acc = zero16();
-  for (int k0 = 0; k0 < a.K; k0 += 64) {
-    bf16x8 wf[4], xf[4];
+  f32x4 wc[8], wn[8], xc[8], xn[8];
+  auto fetch = [&](int kg, f32x4* w, f32x4* x) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      wf[t] = cvt8(wr + k0 + 8 * t);
-      xf[t] = ld8(xr + k0 + 8 * t);
+    for (int q = 0; q < 8; ++q) w[q] = *reinterpret_cast<const f32x4*>(wr + 64 * kg + 4 * q);
+    if (XSRC == kXF32) {
+#pragma unroll
+      for (int q = 0; q < 8; ++q) x[q] = *reinterpret_cast<const f32x4*>(x32 + 64 * kg + 4 * q);
     }
+  };
+  if (active && part < G) fetch(part, wc, xc);
+
+  if (XSRC == kXLn) {
+    // thread t normalises row t / 16, chunks (t % 16) + 16 i of 8 channels, held in registers;
+    // the 16 threads of a row are consecutive lanes, joined by DPP sums
+    constexpr int kMaxChunks = kLnGemmMaxK / 128;
+    const int r = tid >> 4, pc = tid & 15;
+    const int nc = a.K / 8;
+    const bf16* xr = a.ln_x + min(m0 + r, a.M - 1) * a.K;
+    bf16x8 xv[kMaxChunks];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) acc = mfma32(wf[t], xf[t], acc);
+    for (int i = 0; i < kMaxChunks; ++i)
+      if (pc + 16 * i < nc) xv[i] = ld8(xr + 8 * (pc + 16 * i));
+    float s1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i)
+      if (pc + 16 * i < nc)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s1 += (float)xv[i][e];
+    const float mean = sum16(s1) / (float)a.K;
+    float s2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i)
+      if (pc + 16 * i < nc)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = (float)xv[i][e] - mean;
+          s2 += d * d;
+        }
+    const float rstd = __builtin_amdgcn_rsqf(sum16(s2) / (float)a.K + a.eps);
+#pragma unroll
+    for (int i = 0; i < kMaxChunks; ++i) {
+      if (pc + 16 * i < nc) {
+        const int c = 8 * (pc + 16 * i);
+        const f32x4 w0 = *reinterpret_cast<const f32x4*>(a.ln_w + c);
+        const f32x4 w1 = *reinterpret_cast<const f32x4*>(a.ln_w + c + 4);
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(a.ln_b + c);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(a.ln_b + c + 4);
+        f32x4 y0, y1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          y0[e] = ((float)xv[i][e] - mean) * rstd * w0[e] + b0[e];
+          y1[e] = ((float)xv[i][4 + e] - mean) * rstd * w1[e] + b1[e];
+        }
+        bf16x8 hi, lo;
+        split8(y0, y1, hi, lo);
+        *reinterpret_cast<bf16x8*>(xs_hi + r * xstride + c) = hi;
+        *reinterpret_cast<bf16x8*>(xs_lo + r * xstride + c) = lo;
+      }
+    }
+    __syncthreads();
+  }
+
+  if (active) {
+    for (int kg = part; kg < G; kg += KS) {
+      const bool more = kg + KS < G;
+      if (more) fetch(kg + KS, wn, xn);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        bf16x8 whi, wlo, xhi, xlo;
+        split8(wc[2 * t], wc[2 * t + 1], whi, wlo);
+        if (XSRC == kXLn) {
+          const int k = 64 * kg + 32 * g + 8 * t;
+          xhi = *reinterpret_cast<const bf16x8*>(xs_hi + li * xstride + k);
+          xlo = *reinterpret_cast<const bf16x8*>(xs_lo + li * xstride + k);
+        } else {
+          split8(xc[2 * t], xc[2 * t + 1], xhi, xlo);
+        }
+        acc = mfma32(whi, xlo, acc);
+        acc = mfma32(whi, xhi, acc);
+      }
+      if (more) {
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          wc[q] = wn[q];
+          xc[q] = xn[q];
+        }
+      }
+    }
+  }
+  if (KS > 1) {
+    if (part > 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((osub * (KS - 1) + part - 1) * 64 + lane) * 16 + r] = acc[r];
+    }
+    __syncthreads();
+    if (part != 0) return;
+#pragma unroll
+    for (int w = 0; w < KS - 1; ++w)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[r] += red[((osub * (KS - 1) + w) * 64 + lane) * 16 + r];
   }
 
   const int64_t m = m0 + li;
-  if (m >= a.M) return;
+  if (!active || m >= a.M) return;
   if (EPI == kEpiApb) {
     const int cs = a.O / 4;
 #pragma unroll
@@ -143,13 +265,13 @@ __global__ __launch_bounds__(256) void row_gemm(RowGemmArgs a) {
     const int hid = a.O / 2;
 #pragma unroll
     for (int v = 0; v < 2; ++v) {
-      float y[4];
+      f32x4 y;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float av = acc[4 * v + e], bv = acc[8 + 4 * v + e];
         y[e] = av * sigmoid_scaled(-kLog2e * av) * bv;
       }
-      store4(a.h + m * hid + ot * 16 + 8 * v + 4 * g, y[0], y[1], y[2], y[3]);
+      *reinterpret_cast<f32x4*>(a.h32 + m * hid + ot * 16 + 8 * v + 4 * g) = y;
     }
   } else {
 #pragma unroll
@@ -179,38 +301,48 @@ __global__ __launch_bounds__(256) void row_gemm(RowGemmArgs a) {
 __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
   __shared__ float wsum_s[4][32];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
+  const int n = a.n;
+  const int njt = a.np / 32;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+
+  // Tiles are fetched one ahead (two register buffers used alternately); a fetch past the
+  // last tile re-reads the last tile, so every load stays inside z.
+  auto fetch = [&](bf16x8* zf, int64_t tile) {
+    const int64_t tt = tile < a.tiles ? tile : a.tiles - 1;
+    const int64_t bi = tt / njt;
+    const int j0 = (int)(tt - bi * njt) * 32;
+    const bf16* zr = a.z + (bi * n + min(j0 + li, n - 1)) * 128 + 64 * g;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) zf[u] = ld8(zr + 8 * u);
+  };
+  int64_t t = (int64_t)blockIdx.x * 4 + wave;
+  bf16x8 z0[8], z1[8];
+  fetch(z0, t);
 
   bf16x8 wf[8], wl[8];
   float rs = 0.f;
+  const float* wrow = a.w_bias + min(li, a.heads - 1) * 128 + 64 * g;
+  const float* lrow = a.ln_w + 64 * g;
+  const float keep = li < a.heads ? kLog2e : 0.f;
 #pragma unroll
-  for (int t = 0; t < 8; ++t) {
+  for (int u = 0; u < 8; ++u) {
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(wrow + 8 * u);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(wrow + 8 * u + 4);
+    const f32x4 l0 = *reinterpret_cast<const f32x4*>(lrow + 8 * u);
+    const f32x4 l1 = *reinterpret_cast<const f32x4*>(lrow + 8 * u + 4);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const int c = 64 * g + 8 * t + e;
-      const float v = li < a.heads ? kLog2e * a.ln_w[c] * a.w_bias[li * 128 + c] : 0.f;
-      wf[t][e] = (bf16)v;
-      wl[t][e] = (bf16)(v - (float)wf[t][e]);
+      const float v = keep * (e < 4 ? l0[e] * w0[e] : l1[e - 4] * w1[e - 4]);
+      wf[u][e] = (bf16)v;
+      wl[u][e] = (bf16)(v - (float)wf[u][e]);
       rs += v;
     }
   }
   rs = pair_sum(rs);
   if (g == 0) wsum_s[wave][li] = rs;
   __syncthreads();
-  float wsum[16];
-#pragma unroll
-  for (int r = 0; r < 16; ++r) wsum[r] = wsum_s[wave][acc_row(r, g)];
 
-  const int n = a.n;
-  const int njt = a.np / 32;
-  const int64_t stride = (int64_t)gridDim.x * 4;
-  for (int64_t t = (int64_t)blockIdx.x * 4 + wave; t < a.tiles; t += stride) {
-    const int64_t bi = t / njt;  // b * n + i
-    const int j0 = (int)(t - bi * njt) * 32;
-    const int j = min(j0 + li, n - 1);
-    const bf16* zr = a.z + (bi * n + j) * 128 + 64 * g;
-    bf16x8 zf[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) zf[u] = ld8(zr + 8 * u);
+  auto process = [&](const bf16x8* zf, int64_t tile) {
     float s1 = 0.f;
 #pragma unroll
     for (int u = 0; u < 8; ++u)
@@ -232,17 +364,27 @@ __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
 #pragma unroll
     for (int u = 0; u < 8; ++u) acc = mfma32(wf[u], zf[u], acc);
 
+    const int64_t bi = tile / njt;
+    const int key = (int)(tile - bi * njt) * 32 + li;
     const int64_t b = bi / n;
     const int64_t i = bi - b * n;
-    const int key = j0 + li;
     const bool valid = key < n && a.mask[b * n + key] != 0;
+    float* out = a.bias + (b * a.heads * n + i) * a.np + key;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int h = acc_row(r, g);
       if (h < a.heads)
-        a.bias[((b * a.heads + h) * n + i) * a.np + key] =
-            valid ? rstd * (acc[r] - mean * wsum[r]) : kMaskedLogit;
+        out[(int64_t)h * n * a.np] = valid ? rstd * (acc[r] - mean * wsum_s[wave][h]) : kMaskedLogit;
     }
+  };
+  while (t < a.tiles) {
+    fetch(z1, t + stride);
+    process(z0, t);
+    t += stride;
+    if (t >= a.tiles) break;
+    fetch(z0, t + stride);
+    process(z1, t);
+    t += stride;
   }
 }
 
@@ -357,26 +499,37 @@ __global__ __launch_bounds__(256) void apb_attention(ApbAttnArgs a) {
     const int d0 = 8 * v + 4 * g;
     if (d0 < dh) {
       const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + row + d0);
-      store4(a.og + row + d0, o[4 * v] * (float)gv[0], o[4 * v + 1] * (float)gv[1],
-             o[4 * v + 2] * (float)gv[2], o[4 * v + 3] * (float)gv[3]);
+      f32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = o[4 * v + e] * (float)gv[e];
+      *reinterpret_cast<f32x4*>(a.og + row + d0) = y;
     }
   }
 }
 
-dim3 gemm_grid(int64_t M, int O) {
-  return dim3((unsigned)((M + 31) / 32), (unsigned)((O + 127) / 128));
-}
-
 }  // namespace
 
-void launch_row_gemm(const RowGemmArgs& a, int epi, hipStream_t stream) {
-  const dim3 grid = gemm_grid(a.M, a.O);
-  if (epi == kEpiApb)
-    row_gemm<kEpiApb><<<grid, 256, 0, stream>>>(a);
-  else if (epi == kEpiSwiglu)
-    row_gemm<kEpiSwiglu><<<grid, 256, 0, stream>>>(a);
-  else
-    row_gemm<kEpiResid><<<grid, 256, 0, stream>>>(a);
+template <int EPI, int XSRC, int NO>
+void launch_row_gemm_t(const RowGemmArgs& a, hipStream_t stream) {
+  const int otiles = a.O / 32;
+  const dim3 grid((unsigned)((a.M + 31) / 32), (unsigned)((otiles + NO - 1) / NO));
+  const size_t lds = row_gemm_lds(XSRC, a.K, NO);
+  auto kernel = row_gemm<EPI, XSRC, NO>;
+  if (lds > 65536)  // beyond the default dynamic LDS size (K > 480 with the LayerNorm tile)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  kernel<<<grid, 64 * kGemmWaves, lds, stream>>>(a);
+}
+
+// Tile shapes: the LayerNorm-fed GEMMs give each workgroup several output tiles (the tile is
+// normalised once per workgroup), the fp32-fed ones split k 8 ways.
+void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream) {
+  if (epi == kEpiApb && xsrc == kXLn)
+    launch_row_gemm_t<kEpiApb, kXLn, 4>(a, stream);
+  else if (epi == kEpiSwiglu && xsrc == kXLn)
+    launch_row_gemm_t<kEpiSwiglu, kXLn, 8>(a, stream);
+  else if (epi == kEpiResid && xsrc == kXF32)
+    launch_row_gemm_t<kEpiResid, kXF32, 1>(a, stream);
 }
 
 void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream) {

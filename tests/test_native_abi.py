@@ -58,11 +58,11 @@ def test_workspace_sizes_follow_the_layouts(lib):
     qkv = 3 * up(b * 4 * np_ * np_ * 32 * 2)
     assert ta == weights + qkv + up(b * 4 * np_ * np_ * 4) + up(b * n * n * 128 * 2)
     assert lib.ffk_transition_workspace(1000, 128, 4) == 3 * up(4 * 128 * 128 * 2)
-    assert lib.ffk_transition_workspace(700, 384, 4) == up(700 * 384 * 2) + up(700 * 1536 * 2)
+    assert lib.ffk_transition_workspace(700, 384, 4) == up(700 * 1536 * 4)
     np32 = 320
     apb = lib.ffk_attention_pair_bias_workspace(b, n, 384, 128, 16)
     tokens = up(b * n * 384 * 2)
-    assert apb == 5 * tokens + up(b * 384 * np32 * 2) + up(b * 16 * n * np32 * 4)
+    assert apb == 3 * tokens + up(b * n * 384 * 4) + up(b * 384 * np32 * 2) + up(b * 16 * n * np32 * 4)
     assert lib.ffk_attention_pair_bias_workspace(b, 0, 384, 128, 16) == 0
     assert lib.ffk_triangle_multiplication_workspace(0, n, 128, 128) == 0
 

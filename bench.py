@@ -61,6 +61,8 @@ def parse() -> argparse.Namespace:
                     help="also run a plain device copy of this many MiB (the HBM-counter calibration)")
     ap.add_argument("--no-trunk", action="store_true", help="skip the 48-block trunk measurement")
     ap.add_argument("--trunk-only", action="store_true")
+    ap.add_argument("--no-reference-backend", action="store_true",
+                    help="with --trunk-only: skip the engine pytorch backend's trunk run")
     ap.add_argument("--ladder", action="store_true")
     ap.add_argument("--ladder-max", type=int, default=16384)
     return ap.parse_args()
@@ -287,10 +289,13 @@ def ladder(max_n: int) -> list[dict]:
         if n > max_n:
             break
         torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats()
         try:
-            z_cpu, s_cpu, mask_cpu = trunk_inputs(n)
-            z, s, mask = z_cpu.cuda(), s_cpu.cuda(), mask_cpu.cuda()
-            del z_cpu
+            # drawn on the device: the fp32 draw of z alone would need 4 N^2 128 bytes of host memory
+            g = torch.Generator(device="cuda").manual_seed(7)
+            z = torch.randn(1, n, n, 128, device="cuda", generator=g, dtype=torch.bfloat16)
+            s = torch.randn(1, n, D_SINGLE, device="cuda", generator=g, dtype=torch.bfloat16)
+            mask = torch.ones(1, n, dtype=torch.bool, device="cuda")
             with torch.no_grad():
                 blk(z, mask, s)
                 torch.cuda.synchronize()
@@ -362,7 +367,8 @@ def main() -> int:
         ladder(args.ladder_max)
         return 0
     if args.trunk_only:
-        print(json.dumps({"trunk": trunk_measure(512, max(1, args.steps // 10), pytorch_too=True,
+        print(json.dumps({"trunk": trunk_measure(512, max(1, args.steps // 10),
+                                                 pytorch_too=not args.no_reference_backend,
                                                  cpu_too=not args.no_cpu_baseline)}), flush=True)
         return 0
     dev = torch.device("cuda:0")

@@ -16,11 +16,15 @@
 //  * S^T (32 keys x 32 queries) is one MFMA accumulator. Its initial value is the pair-bias
 //    tile (fp32, stored by kernel 1 in the accumulator's register order), shared by the 4
 //    attention rows of the workgroup (the bias does not depend on the row).
-//  * The running offset m is subtracted by the matrix unit: a third k-step multiplies a
+//  * The softmax offset m is subtracted by the matrix unit: a third k-step multiplies a
 //    constant 1 on the key side by -m on the query side (m kept bf16-representable).
-//  * Lazy softmax: the offset is fixed from the first tile that has a finite logit and
-//    only moved when a tile's exp2 sum overflows 2^64, so the common step is exp2,
-//    bf16 packing and a v_dot2 row sum: about one VALU op plus one exp per logit.
+//  * Fixed-offset softmax: m is the row maximum of the first key tile (before the loop) and
+//    never moves, so the key loop has no branch at all: exp2, bf16 packing and a v_dot2 row
+//    sum, about one VALU op plus one exp per logit, and the compiler can interleave the rows'
+//    matrix and vector work freely. A row whose final sum leaves [2^-100, 2^100] (a later
+//    logit more than ~100 above m, or all its logits far below m) is recomputed exactly at
+//    the end with a two-pass softmax (true maximum first); the sum bound keeps every
+//    intermediate finite, so the check after the loop is sufficient.
 //  * Every operand tile reaches LDS by LDS DMA (no registers, no VALU): K and V^T of the 4
 //    rows in stages of 64 keys (double-buffered, shared by the 8 waves) and each wave's bias
 //    tiles (double-buffered), all one step ahead, with explicit waits on the wave's own
@@ -38,7 +42,8 @@ namespace ffk {
 constexpr int kFR = 4;      // attention rows per flash workgroup (share the bias tile)
 constexpr int kFW = 8;      // waves per flash workgroup, 32 queries each
 constexpr int kFK = 64;     // keys per LDS stage
-constexpr float kLazyLimit = 1.8446744073709552e19f;  // 2^64
+constexpr float kSumHigh = 1.2676506002282294e30f;  // 2^100
+constexpr float kSumLow = 7.888609052210118e-31f;    // 2^-100
 
 // Index of bias entry (query, key) in the blocked layout
 //   [bh][query / 32][key / 32][v][lane][e] (a 32 x 32 tile = 1024 fp32),
@@ -217,33 +222,6 @@ __device__ __forceinline__ float exp_pack(const f32x16& S, bf16x8& p0, bf16x8& p
   return ts;
 }
 
-// The lazy offset's slow path for one attention row (called by the whole wave when some
-// lane's query has no offset yet or its tile sum overflowed 2^64): move m to the tile's
-// maximum (rounded up to a bf16 value, so that the matrix unit subtracts it exactly),
-// rescale O and l, and redo the exponentials.
-__device__ __forceinline__ void rebase(f32x16& S, float& m, float& l, bool& set, f32x16& O,
-                                       bf16x8& negm, int g, bf16x8& p0, bf16x8& p1, float& ts) {
-  float tm = S[0];
-#pragma unroll
-  for (int i = 1; i < 16; ++i) tm = fmaxf(tm, S[i]);
-  tm = pair_max(tm);
-  if (tm > -INFINITY && (!set || tm > 0.f)) {
-    const float mn = bf16_ceil(m + tm);
-    const float shift = mn - m;
-    const float alpha = fast_exp2(-shift);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      S[i] -= shift;
-      O[i] *= alpha;
-    }
-    l *= alpha;
-    m = mn;
-    set = true;
-    negm[0] = g == 0 ? (bf16)(-mn) : (bf16)0.f;
-  }
-  ts = exp_pack(S, p0, p1);
-}
-
 // grid (ceil(np / 256) * (np / 4) * batch * heads) workgroups, renumbered per XCD;
 // block 512 = 8 waves x 32 queries, 4 attention rows.
 __global__ __launch_bounds__(512) void flash_attn_bias(
@@ -309,8 +287,7 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
   bias_dma(0);
   bf16x8 qa[kFR][2];
   bf16x8 negm[kFR];
-  float m[kFR], l[kFR];
-  bool set[kFR];
+  float l[kFR];
   f32x16 O[kFR];
   const bf16x8 zero8 = {};
   bf16x8 ones_k = zero8;
@@ -326,9 +303,7 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
       qa[rr][1] = zero8;
     }
     negm[rr] = zero8;
-    m[rr] = 0.f;
     l[rr] = 0.f;
-    set[rr] = false;
     O[rr] = zero16();
   }
   // the q loads complete here, not inside the key loop (see settle)
@@ -336,6 +311,31 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
   for (int rr = 0; rr < kFR; ++rr) asm volatile("" ::"v"(qa[rr][0]), "v"(qa[rr][1]));
   wait_vm_lds<0>();
   __syncthreads();
+
+  // offsets from the first key tile (bias + q.k), rounded up to a bf16 value so that the
+  // matrix unit subtracts them exactly; a row whose first tile is fully masked starts at 0
+  if (active) {
+    f32x16 b0;
+    const float* bt = &lds.bias[wave][0][4 * lane];
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(bt + 256 * v4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) b0[4 * v4 + e] = x[e];
+    }
+#pragma unroll
+    for (int rr = 0; rr < kFR; ++rr) {
+      const bf16* kt = lds.k[0][rr];
+      f32x16 S0 = mfma32(ld8(kt + koff(li, g)), qa[rr][0], b0);
+      S0 = mfma32(ld8(kt + koff(li, 2 + g)), qa[rr][1], S0);
+      float tm = S0[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) tm = fmaxf(tm, S0[i]);
+      tm = pair_max(tm);
+      const float m0 = tm > -INFINITY ? bf16_ceil(tm) : 0.f;
+      negm[rr][0] = g == 0 ? (bf16)(-m0) : (bf16)0.f;
+    }
+  }
 
 #pragma unroll 1
   for (int64_t st = 0; st < nstage; ++st) {
@@ -376,20 +376,8 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
           }
           bf16x8 p0[2], p1[2];
           float ts[2];
-          bool any_bad = false;
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            ts[u] = exp_pack(S[u], p0[u], p1[u]);
-            any_bad |= !set[rp + u] || !(ts[u] < kLazyLimit);
-          }
-          if (__builtin_amdgcn_ballot_w64(any_bad) != 0) {
-#pragma unroll
-            for (int u = 0; u < 2; ++u) {
-              const int rr = rp + u;
-              if (__builtin_amdgcn_ballot_w64(!set[rr] || !(ts[u] < kLazyLimit)) != 0)
-                rebase(S[u], m[rr], l[rr], set[rr], O[rr], negm[rr], g, p0[u], p1[u], ts[u]);
-            }
-          }
+          for (int u = 0; u < 2; ++u) ts[u] = exp_pack(S[u], p0[u], p1[u]);
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
             const int rr = rp + u;
@@ -409,9 +397,54 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
   }
   wait_vm_lds<0>();  // no LDS write may land after exit
   if (!active) return;
+
+  // Exact two-pass softmax of one attention row for this wave's 32 queries, reading K, V^T
+  // and the bias tiles straight from global memory (the rare path: rows whose sums left the
+  // safe range of the fixed offset).
+  auto exact_row = [&](int rr, f32x16& Orow, float& lrow) {
+    const bf16* krow = kbase + (int64_t)rr * np * 32 + li * 32;
+    const bf16* vrow = vbase + (int64_t)rr * 32 * np + (int64_t)li * np;
+    auto logits = [&](int64_t kb) {
+      f32x16 st;
+#pragma unroll
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(bias_w + kb * 1024 + 256 * v4 + 4 * lane);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) st[4 * v4 + e] = x[e];
+      }
+      st = mfma32(ld8(krow + kb * 32 * 32 + 8 * g), qa[rr][0], st);
+      return mfma32(ld8(krow + kb * 32 * 32 + 16 + 8 * g), qa[rr][1], st);
+    };
+    float mx = -INFINITY;
+    for (int64_t kb = 0; kb < nb; ++kb) {
+      const f32x16 st = logits(kb);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, st[i]);
+    }
+    mx = pair_max(mx);
+    const float off = mx > -INFINITY ? mx : 0.f;
+    f32x16 o = zero16();
+    float ls = 0.f;
+    for (int64_t kb = 0; kb < nb; ++kb) {
+      f32x16 st = logits(kb);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) st[i] -= off;
+      bf16x8 p0, p1;
+      ls += exp_pack(st, p0, p1);
+      o = mfma32(ld8(vrow + kb * 32 + 8 * g), p0, o);
+      o = mfma32(ld8(vrow + kb * 32 + 16 + 8 * g), p1, o);
+    }
+    Orow = o;
+    lrow = ls;
+  };
+
 #pragma unroll
   for (int rr = 0; rr < kFR; ++rr) {
-    const float lt = pair_sum(l[rr]);
+    float lt = pair_sum(l[rr]);
+    if (__builtin_amdgcn_ballot_w64(!(lt < kSumHigh) || !(lt > kSumLow)) != 0) {
+      exact_row(rr, O[rr], l[rr]);
+      lt = pair_sum(l[rr]);
+    }
     const int64_t r = r0 + rr;
     if (r >= rows_valid || j >= n_valid) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;

@@ -16,15 +16,16 @@
 //  * S^T (32 keys x 32 queries) is one MFMA accumulator. Its initial value is the pair-bias
 //    tile (fp32, stored by kernel 1 in the accumulator's register order), shared by the 4
 //    attention rows of the workgroup (the bias does not depend on the row).
-//  * The softmax offset m is subtracted by the matrix unit: a third k-step multiplies a
-//    constant 1 on the key side by -m on the query side (m kept bf16-representable).
-//  * Fixed-offset softmax: m is the row maximum of the first key tile (before the loop) and
-//    never moves, so the key loop has no branch at all: exp2, bf16 packing and a v_dot2 row
-//    sum, about one VALU op plus one exp per logit, and the compiler can interleave the rows'
-//    matrix and vector work freely. A row whose final sum leaves [2^-100, 2^100] (a later
-//    logit more than ~100 above m, or all its logits far below m) is recomputed exactly at
-//    the end with a two-pass softmax (true maximum first); the sum bound keeps every
-//    intermediate finite, so the check after the loop is sufficient.
+//  * Fixed-offset softmax: one offset m per query, shared by the wave's 4 rows, is the
+//    largest bias of the first key tile (computed before the loop from the bias alone, so
+//    padded rows cannot change a valid row's rounding) and never moves. It is subtracted
+//    from the bias tile once per key block (the accumulator's initial value), so the key
+//    loop has no branch and no extra work per row: two MFMAs, exp2, bf16 packing and a
+//    v_dot2 row sum, about one VALU op plus one exp per logit, and the compiler can
+//    interleave the rows' matrix and vector work freely. A row whose final sum leaves
+//    [2^-100, 2^100] (logits more than ~100 log2 units above m, or all of them that far
+//    below) is recomputed exactly at the end with a two-pass softmax (true maximum first);
+//    the sum bound keeps every intermediate finite, so the check after the loop suffices.
 //  * Every operand tile reaches LDS by LDS DMA (no registers, no VALU): K and V^T of the 4
 //    rows in stages of 64 keys (double-buffered, shared by the 8 waves) and each wave's bias
 //    tiles (double-buffered), all one step ahead, with explicit waits on the wave's own
@@ -286,12 +287,9 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
   kv_dma(0, 0);
   bias_dma(0);
   bf16x8 qa[kFR][2];
-  bf16x8 negm[kFR];
   float l[kFR];
   f32x16 O[kFR];
   const bf16x8 zero8 = {};
-  bf16x8 ones_k = zero8;
-  ones_k[0] = g == 0 ? (bf16)1.f : (bf16)0.f;
 #pragma unroll
   for (int rr = 0; rr < kFR; ++rr) {
     if (active) {
@@ -302,7 +300,6 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
       qa[rr][0] = zero8;
       qa[rr][1] = zero8;
     }
-    negm[rr] = zero8;
     l[rr] = 0.f;
     O[rr] = zero16();
   }
@@ -312,29 +309,21 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
   wait_vm_lds<0>();
   __syncthreads();
 
-  // offsets from the first key tile (bias + q.k), rounded up to a bf16 value so that the
-  // matrix unit subtracts them exactly; a row whose first tile is fully masked starts at 0
+  // one offset per query, shared by the wave's rows: the largest bias of the first key tile
+  // (0 when that tile is fully masked). It depends on the bias row alone, so no row of the
+  // workgroup (a padded one included) can change another row's rounding.
+  float msh = 0.f;
   if (active) {
-    f32x16 b0;
     const float* bt = &lds.bias[wave][0][4 * lane];
+    float tm = -INFINITY;
 #pragma unroll
     for (int v4 = 0; v4 < 4; ++v4) {
       const f32x4 x = *reinterpret_cast<const f32x4*>(bt + 256 * v4);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) b0[4 * v4 + e] = x[e];
+      for (int e = 0; e < 4; ++e) tm = fmaxf(tm, x[e]);
     }
-#pragma unroll
-    for (int rr = 0; rr < kFR; ++rr) {
-      const bf16* kt = lds.k[0][rr];
-      f32x16 S0 = mfma32(ld8(kt + koff(li, g)), qa[rr][0], b0);
-      S0 = mfma32(ld8(kt + koff(li, 2 + g)), qa[rr][1], S0);
-      float tm = S0[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) tm = fmaxf(tm, S0[i]);
-      tm = pair_max(tm);
-      const float m0 = tm > -INFINITY ? bf16_ceil(tm) : 0.f;
-      negm[rr][0] = g == 0 ? (bf16)(-m0) : (bf16)0.f;
-    }
+    tm = pair_max(tm);
+    msh = tm > -INFINITY ? tm : 0.f;
   }
 
 #pragma unroll 1
@@ -356,13 +345,13 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
         for (int v4 = 0; v4 < 4; ++v4) {
           const f32x4 x = *reinterpret_cast<const f32x4*>(bt + 256 * v4);
 #pragma unroll
-          for (int e = 0; e < 4; ++e) bcur[4 * v4 + e] = x[e];
+          for (int e = 0; e < 4; ++e) bcur[4 * v4 + e] = x[e] - msh;
         }
       }
       bias_dma(kb + 1);                      // into the other tile buffer, read last step
       if (sub == 0) kv_dma(st + 1, sb ^ 1);  // the other stage buffer, read last stage
       if (active) {
-        // two rows at a time: S^T = bias + K Q^T - m, softmax, O^T += V^T P^T
+        // two rows at a time: S^T = (bias - m) + K Q^T, softmax, O^T += V^T P^T
 #pragma unroll
         for (int rp = 0; rp < kFR; rp += 2) {
           f32x16 S[2];
@@ -372,7 +361,6 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
             const bf16* kt = lds.k[sb][rr];
             S[u] = mfma32(ld8(kt + koff(sub * 32 + li, g)), qa[rr][0], bcur);
             S[u] = mfma32(ld8(kt + koff(sub * 32 + li, 2 + g)), qa[rr][1], S[u]);
-            S[u] = mfma32(ones_k, negm[rr], S[u]);
           }
           bf16x8 p0[2], p1[2];
           float ts[2];

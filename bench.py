@@ -76,11 +76,13 @@ def real_length(n: int, seed: int) -> int:
     return int(torch.randint(lo, n + 1, (1,), generator=g).item())
 
 
-def event_time_ms(fn, reps: int) -> float:
-    """Average ms of ``fn`` over ``reps`` launches between two events on the current stream."""
+def event_time_ms(fn, reps: int, warm: int = 1) -> float:
+    """Average ms of ``fn`` over ``reps`` launches between two events on the current stream,
+    after ``warm`` untimed launches."""
     import torch
 
-    fn()
+    for _ in range(max(1, warm)):
+        fn()
     torch.cuda.synchronize()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     start.record()
@@ -112,7 +114,7 @@ def flash_roofline(n: int, length: int, reps: int) -> dict:
     def launch():
         kernels.flash_attention_bias(q, k, vt, bias, out, rows_valid=n, n_valid=n)
 
-    ms = event_time_ms(launch, reps)
+    ms = event_time_ms(launch, reps, warm=max(50, reps))  # steady clocks, as inside a block
     flops = 4.0 * n**3 * heads * d
     achieved = flops / (ms * 1e-3) / 1e12
     return {"bound": "mfma", "kernel": "flash_attn_bias", "achieved": round(achieved, 2),
@@ -129,7 +131,7 @@ def layernorm_roofline(n: int, reps: int) -> dict:
     x = torch.randn(n * n, 128, device="cuda").bfloat16()
     w = torch.ones(128, device="cuda")
     b = torch.zeros(128, device="cuda")
-    ms = event_time_ms(lambda: kernels.layer_norm(x, w, b, 1e-5), reps)
+    ms = event_time_ms(lambda: kernels.layer_norm(x, w, b, 1e-5), reps, warm=max(50, reps))
     nbytes = 2.0 * n * n * 128 * 2
     gbs = nbytes / (ms * 1e-3) / 1e9
     return {"kernel": "layer_norm_bf16_128", "bound": "hbm", "achieved": round(gbs, 1),

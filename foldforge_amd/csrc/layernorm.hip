@@ -2,38 +2,25 @@
 //
 // Reference: the engine LayerNorm (src/foldforge/modules/engine/modules.py:230-238) and the
 // torch.nn.LayerNorm of the legacy graph (legacy/attention.py:90). HBM-bound: the 128-wide
-// bf16 path streams 16-byte vectors, 16 lanes per row, 4 rows in flight per lane, and keeps
-// the row in registers between the two statistics passes (exact two-pass variance).
+// bf16 path is persistent (four 256-thread workgroups per CU), streams 16-byte vectors with 16
+// lanes per row and 8 rows per lane, fetches the next 128 rows of a workgroup while it
+// normalises the current ones (two register buffers used alternately), and keeps each row in
+// registers between the two statistics passes (exact two-pass variance).
 #include "ffk_device.h"
 #include "ffk_kernels.h"
 
 namespace ffk {
 
-constexpr int kLnRowsPerBlock = 64;  // 16 rows per pass x 4 passes
+constexpr int kLnRowsPerLane = 8;
+constexpr int kLnRowsPerBlock = 16 * kLnRowsPerLane;  // 16 rows per pass (16 lanes each)
 
-// bf16 rows of exactly 128 channels. grid ceil(rows / 64); block 256.
-__global__ __launch_bounds__(256) void layer_norm_bf16_128(const bf16* __restrict__ x,
-                                                           const float* __restrict__ w,
-                                                           const float* __restrict__ b,
-                                                           bf16* __restrict__ y, int64_t rows,
-                                                           float eps) {
-  const int tid = threadIdx.x;
-  const int sub = tid & 15;
-  const int64_t row0 = (int64_t)blockIdx.x * kLnRowsPerBlock + (tid >> 4);
-  float wv[8], bv[8];
+// Normalise and store the rows row0 + 16 it (it < kLnRowsPerLane) whose 8-channel slices
+// `sub` this lane holds in v; rows at or past `rows` are skipped.
+__device__ __forceinline__ void ln_rows_compute(const bf16x8 (&v)[kLnRowsPerLane], int64_t row0, int64_t rows,
+                                                const float (&wv)[8], const float (&bv)[8],
+                                                bf16* __restrict__ y, int sub, float eps) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    wv[e] = w ? w[8 * sub + e] : 1.f;
-    bv[e] = b ? b[8 * sub + e] : 0.f;
-  }
-  bf16x8 v[4];
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int64_t row = row0 + 16 * it;
-    if (row < rows) v[it] = ld8(x + row * 128 + 8 * sub);
-  }
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
+  for (int it = 0; it < kLnRowsPerLane; ++it) {
     const int64_t row = row0 + 16 * it;
     float xv[8];
     float s = 0.f;
@@ -56,6 +43,43 @@ __global__ __launch_bounds__(256) void layer_norm_bf16_128(const bf16* __restric
       for (int e = 0; e < 8; ++e) o[e] = (bf16)(xv[e] * rstd * wv[e] + bv[e]);
       *reinterpret_cast<bf16x8*>(y + row * 128 + 8 * sub) = o;
     }
+  }
+}
+
+// bf16 rows of exactly 128 channels. grid min(ceil(rows / 128), 4 per CU); block 256.
+__global__ __launch_bounds__(256) void layer_norm_bf16_128(const bf16* __restrict__ x,
+                                                           const float* __restrict__ w,
+                                                           const float* __restrict__ b,
+                                                           bf16* __restrict__ y, int64_t rows,
+                                                           float eps) {
+  const int tid = threadIdx.x;
+  const int sub = tid & 15;
+  float wv[8], bv[8];
+  auto load = [&](bf16x8 (&v)[kLnRowsPerLane], int64_t row0) {
+#pragma unroll
+    for (int it = 0; it < kLnRowsPerLane; ++it) {
+      const int64_t row = row0 + 16 * it;
+      if (row < rows) v[it] = ld8(x + row * 128 + 8 * sub);
+    }
+  };
+  const int64_t step = (int64_t)gridDim.x * kLnRowsPerBlock;
+  int64_t row0 = (int64_t)blockIdx.x * kLnRowsPerBlock + (tid >> 4);
+  bf16x8 va[kLnRowsPerLane], vb[kLnRowsPerLane];
+  load(va, row0);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    wv[e] = w ? w[8 * sub + e] : 1.f;
+    bv[e] = b ? b[8 * sub + e] : 0.f;
+  }
+  // row0 - tid / 16 is the workgroup's first row: the loop condition is uniform
+  while (row0 - (tid >> 4) < rows) {
+    load(vb, row0 + step);
+    ln_rows_compute(va, row0, rows, wv, bv, y, sub, eps);
+    row0 += step;
+    if (row0 - (tid >> 4) >= rows) break;
+    load(va, row0 + step);
+    ln_rows_compute(vb, row0, rows, wv, bv, y, sub, eps);
+    row0 += step;
   }
 }
 
@@ -92,7 +116,8 @@ __global__ __launch_bounds__(256) void layer_norm_rows(const T* __restrict__ x,
 void launch_layer_norm(const void* x, const float* w, const float* b, void* y, int64_t rows,
                        int cols, float eps, int dtype, hipStream_t stream) {
   if (dtype == 0 && cols == 128) {
-    const int64_t blocks = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+    int64_t blocks = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
+    if (blocks > (int64_t)cu_count() * 4) blocks = (int64_t)cu_count() * 4;
     layer_norm_bf16_128<<<dim3((unsigned)blocks), 256, 0, stream>>>(
         static_cast<const bf16*>(x), w, b, static_cast<bf16*>(y), rows, eps);
     return;

@@ -26,7 +26,8 @@ Reported beside it, in the same JSON line:
 one GPU only. ``--ladder`` instead prints one JSON line per length of the trunk's length
 ladder (N = 768 ... 2048 full trunks, then single blocks upward until the device is out of
 memory); ``--trunk-only`` prints the trunk line alone (with the engine ``pytorch``
-backend's trunk time beside it, and the fp32 CPU oracle's per-block time x 144).
+backend's trunk time beside it, the fp32 CPU oracle's per-block time x 144, and the trunk
+replayed as one captured graph at N = 128 and 512).
 """
 
 from __future__ import annotations
@@ -272,6 +273,27 @@ def trunk_measure(n: int, runs: int, *, pytorch_too: bool = False, cpu_too: bool
     return out
 
 
+def graph_measure(n: int, runs: int = 3) -> dict:
+    """The 48 x 3 trunk run eagerly and as one captured graph (foldforge_amd.execution)."""
+    import torch
+
+    import foldforge_amd
+    from foldforge_amd.execution import capture_trunk
+
+    model = foldforge_amd.load(backend="miniworld", device="cuda", blocks=TRUNK_BLOCKS, seed=0,
+                               d_single=D_SINGLE, unsupported="error")
+    z_cpu, s_cpu, mask_cpu = trunk_inputs(n)
+    z, s, mask = z_cpu.cuda(), s_cpu.cuda(), mask_cpu.cuda()
+    eager_ms, (pe, se) = time_trunk(model, z, s, mask, runs)
+    graph = capture_trunk(model, z, mask, s, passes=TRUNK_PASSES)
+    graph_ms = event_time_ms(lambda: graph(z, mask, s), runs, warm=1)
+    pg, sg = graph(z, mask, s)
+    torch.cuda.synchronize()
+    return {"n": n, "eager_ms_per_trunk": round(eager_ms, 2), "graph_ms_per_trunk": round(graph_ms, 2),
+            "graph_speedup": round(eager_ms / graph_ms, 2),
+            "graph_equals_eager": bool(torch.equal(pg, pe) and torch.equal(sg, se))}
+
+
 def ladder(max_n: int) -> list[dict]:
     """Config 5: full trunks at N = 768 .. 2048, then single blocks (with single track) at
     larger N until the device runs out of memory."""
@@ -369,9 +391,10 @@ def main() -> int:
         ladder(args.ladder_max)
         return 0
     if args.trunk_only:
-        print(json.dumps({"trunk": trunk_measure(512, max(1, args.steps // 10),
-                                                 pytorch_too=not args.no_reference_backend,
-                                                 cpu_too=not args.no_cpu_baseline)}), flush=True)
+        trunk = trunk_measure(512, max(1, args.steps // 10), pytorch_too=not args.no_reference_backend,
+                              cpu_too=not args.no_cpu_baseline)
+        trunk["graph"] = [graph_measure(n) for n in (128, 512)]
+        print(json.dumps({"trunk": trunk}), flush=True)
         return 0
     dev = torch.device("cuda:0")
     n = args.n

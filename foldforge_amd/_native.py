@@ -51,6 +51,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 7
         + [c_void_p, c_size_t, c_int64, c_int32, c_int32, c_int32, c_float, c_void_p],
     ),
+    "ffk_msa_pair_weighted_averaging_workspace": (
+        c_size_t,
+        [c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32],
+    ),
+    "ffk_msa_pair_weighted_averaging": (
+        c_int32,
+        [c_void_p] * 12
+        + [c_size_t, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32,
+           c_float, c_float, c_void_p],
+    ),
     "ffk_attention_pair_bias_workspace": (
         c_size_t,
         [c_int64, c_int64, c_int32, c_int32, c_int32],

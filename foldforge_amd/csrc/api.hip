@@ -189,6 +189,27 @@ TransitionWs transition_ws(void* ws, int64_t rows, int d, int factor) {
 
 int64_t pad32(int64_t n) { return (n + 31) / 32 * 32; }
 
+int64_t pad64(int64_t n) { return (n + 63) / 64 * 64; }
+
+struct PwaWs {
+  bf16 *vt, *gate, *w;
+  float *logits, *og;
+  size_t bytes;
+};
+PwaWs pwa_ws(void* ws, int64_t batch, int64_t depth, int64_t n, int heads, int dh) {
+  Carver cv{static_cast<char*>(ws)};
+  const int64_t np = pad64(n);
+  const size_t tok = (size_t)batch * depth * n * heads * dh;
+  PwaWs w;
+  w.vt = cv.take<bf16>((size_t)batch * heads * depth * dh * np);
+  w.gate = cv.take<bf16>(tok);
+  w.logits = cv.take<float>((size_t)batch * heads * n * np);
+  w.w = cv.take<bf16>((size_t)batch * heads * n * np);
+  w.og = cv.take<float>(tok);
+  w.bytes = cv.used;
+  return w;
+}
+
 struct ApbWs {
   bf16 *q, *k, *vt, *gate;
   float *og, *bias;
@@ -576,6 +597,109 @@ int32_t ffk_attention_pair_bias(
   o.residual = residual ? 1 : 0;
   launch_row_gemm(o, kEpiResid, kXF32, st);
   return check_launch("attention_pair_bias");
+}
+
+size_t ffk_msa_pair_weighted_averaging_workspace(int64_t batch, int64_t depth, int64_t n,
+                                                  int32_t d_msa, int32_t d_pair, int32_t n_head,
+                                                  int32_t d_head) {
+  if (batch <= 0 || depth <= 0 || n <= 0 || d_msa <= 0 || d_pair <= 0 || n_head <= 0 || d_head <= 0)
+    return 0;
+  return pwa_ws(nullptr, batch, depth, n, n_head, d_head).bytes;
+}
+
+int32_t ffk_msa_pair_weighted_averaging(
+    const void* m, const void* z, const uint8_t* key_mask, const float* ln_msa_w,
+    const float* ln_msa_b, const float* ln_pair_w, const float* w_bias, const float* w_value,
+    const float* w_gate, const float* w_out, void* out, void* workspace, size_t workspace_bytes,
+    int64_t batch, int64_t depth, int64_t n, int32_t d_msa, int32_t d_pair, int32_t n_head,
+    int32_t d_head, int32_t residual, float eps_msa, float eps_pair, void* stream) {
+  if (int32_t st = check_device()) return st;
+  const int64_t hd = (int64_t)n_head * d_head;
+  if (d_pair != 128)
+    return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: d_pair=%d (kernels take 128)", d_pair);
+  if (d_msa <= 0 || d_msa % 64 != 0 || d_msa > kLnGemmMaxK || n_head <= 0 || n_head > 32 ||
+      d_head <= 0 || d_head % 4 != 0 || hd % 64 != 0)
+    return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: d_msa=%d heads=%d x %d (kernels take d_msa a multiple of 64 up to %d, at most 32 heads, d_head a multiple of 4, heads * d_head a multiple of 64)", d_msa, n_head, d_head, kLnGemmMaxK);
+  if (batch <= 0 || depth <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: empty shape");
+  if (batch * n_head > 65535 || (n + 63) / 64 > 65535 || (depth * d_head + 127) / 128 > 0x7fffffffLL)
+    return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: shape exceeds the launch grid");
+  if (!m || !z || !key_mask || !ln_msa_w || !ln_msa_b || !ln_pair_w || !w_bias || !w_value ||
+      !w_gate || !w_out || !out)
+    return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: null argument");
+  if (!aligned16(m) || !aligned16(z) || !aligned16(out) || !aligned16(w_value) ||
+      !aligned16(w_gate) || !aligned16(w_out))
+    return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: m/z/out and the projection weights must be 16-byte aligned");
+  const PwaWs need = pwa_ws(nullptr, batch, depth, n, n_head, d_head);
+  if (!workspace || workspace_bytes < need.bytes || !aligned16(workspace))
+    return fail(FFK_ERR_WORKSPACE, "msa_pair_weighted_averaging: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
+  const PwaWs w = pwa_ws(workspace, batch, depth, n, n_head, d_head);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t rows = batch * depth * n;
+  const int64_t np = pad64(n);
+
+  RowGemmArgs p{};
+  p.ln_x = static_cast<const bf16*>(m);
+  p.ln_w = ln_msa_w;
+  p.ln_b = ln_msa_b;
+  p.eps = eps_msa;
+  p.w0 = w_value;
+  p.w1 = w_gate;
+  p.M = rows;
+  p.K = d_msa;
+  p.O = (int)(2 * hd);
+  p.vt = w.vt;
+  p.gate = w.gate;
+  p.n = (int)n;
+  p.np = (int)np;
+  p.heads = n_head;
+  p.dh = d_head;
+  p.depth = (int)depth;
+  launch_row_gemm(p, kEpiPwa, kXLn, st);
+
+  PairBiasArgs pb;
+  pb.z = static_cast<const bf16*>(z);
+  pb.mask = key_mask;
+  pb.ln_w = ln_pair_w;
+  pb.w_bias = w_bias;
+  pb.bias = w.logits;
+  pb.tiles = batch * n * (np / 32);
+  pb.n = (int)n;
+  pb.np = (int)np;
+  pb.heads = n_head;
+  pb.eps = eps_pair;
+  launch_apb_pair_bias(pb, st);
+
+  PwaSoftmaxArgs sm;
+  sm.logits = w.logits;
+  sm.w = w.w;
+  sm.rows = batch * n_head * n;
+  sm.np = (int)np;
+  launch_pwa_softmax(sm, st);
+
+  PwaAverageArgs av;
+  av.vt = w.vt;
+  av.w = w.w;
+  av.gate = w.gate;
+  av.og = w.og;
+  av.batch = (int)batch;
+  av.heads = n_head;
+  av.depth = (int)depth;
+  av.n = (int)n;
+  av.np = (int)np;
+  av.dh = d_head;
+  launch_pwa_average(av, st);
+
+  RowGemmArgs o{};
+  o.x32 = w.og;
+  o.w0 = w_out;
+  o.M = rows;
+  o.K = (int)hd;
+  o.O = d_msa;
+  o.res = static_cast<const bf16*>(m);
+  o.out = static_cast<bf16*>(out);
+  o.residual = residual ? 1 : 0;
+  launch_row_gemm(o, kEpiResid, kXF32, st);
+  return check_launch("msa_pair_weighted_averaging");
 }
 
 }  // extern "C"

@@ -69,7 +69,7 @@ void launch_transition(const TransitionArgs& a, hipStream_t stream);
 // three epilogues, x either LayerNorm(ln_x) (kXLn, K <= kLnGemmMaxK) or fp32 rows x32 (kXF32).
 // K % 64 == 0, O % 32 == 0; weights are the fp32 parameters. Pairs served: (kEpiApb, kXLn),
 // (kEpiSwiglu, kXLn), (kEpiResid, kXF32).
-enum { kEpiApb = 0, kEpiSwiglu = 1, kEpiResid = 2 };
+enum { kEpiApb = 0, kEpiSwiglu = 1, kEpiResid = 2, kEpiPwa = 3 };
 enum { kXLn = 0, kXF32 = 1 };
 constexpr int kLnGemmMaxK = 768;
 struct RowGemmArgs {
@@ -89,6 +89,9 @@ struct RowGemmArgs {
   float q_scale, gate_bias;
   bf16 *q, *k, *vt, *gate;
   int n, np, heads, dh;
+  // kEpiPwa: w0 = to_value, w1 = to_gate ([hd][K] each, O = 2 hd); tokens m = (b S + s) n + j;
+  // v^T [batch][heads][S][dh][np] (bf16, keys contiguous), gate = sigmoid(x W_g^T) [M][hd]
+  int depth;
   float* h32;  // kEpiSwiglu: [M][hid] = silu(a) * b
   const bf16* res;  // kEpiResid: out = res + y (residual) or y
   bf16* out;
@@ -116,6 +119,25 @@ struct ApbAttnArgs {
   int n, np, heads, dh, cs;
 };
 void launch_apb_attention(const ApbAttnArgs& a, int batch, hipStream_t stream);
+
+// MSA pair-weighted averaging (msa.hip): the softmax over keys of the pair logits and the
+// weighted average of every MSA row's values.
+struct PwaSoftmaxArgs {
+  const float* logits;  // [batch][heads][n][np] (log2 units, masked keys very negative)
+  bf16* w;              // [batch][heads][n][np] softmax weights, 0 at masked / padding keys
+  int64_t rows;         // batch * heads * n
+  int np;
+};
+void launch_pwa_softmax(const PwaSoftmaxArgs& a, hipStream_t stream);
+
+struct PwaAverageArgs {
+  const bf16* vt;    // [batch][heads][S][dh][np]
+  const bf16* w;     // [batch][heads][n][np]
+  const bf16* gate;  // [batch][S][n][heads dh]
+  float* og;         // [batch][S][n][heads dh] = gate * sum_j w[h][i][j] v[s][j][h]
+  int batch, heads, depth, n, np, dh;
+};
+void launch_pwa_average(const PwaAverageArgs& a, hipStream_t stream);
 
 struct PackSeg {
   const float* src;  // NULL: write zeros

@@ -114,6 +114,11 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
     cbase = ot * 32 - seg * cs;
     const float* base = seg == 0 ? a.w0 : seg == 1 ? a.w1 : seg == 2 ? a.w2 : a.w3;
     wr = base + (int64_t)(cbase + li) * a.K;
+  } else if (EPI == kEpiPwa) {
+    const int hd = a.O / 2;
+    seg = (ot * 32) / hd;
+    cbase = ot * 32 - seg * hd;
+    wr = (seg == 0 ? a.w0 : a.w1) + (int64_t)(cbase + li) * a.K;
   } else if (EPI == kEpiSwiglu) {
     // packed tile: rows 0-15 are expand_a rows 16 ot .., rows 16-31 the expand_b rows alike
     wr = (li < 16 ? a.w0 : a.w1) + (int64_t)(ot * 16 + (li & 15)) * a.K;
@@ -259,6 +264,26 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
         y2 = sigmoid_scaled((y2 + a.gate_bias) * nb);
         y3 = sigmoid_scaled((y3 + a.gate_bias) * nb);
         store4(a.gate + m * cs + c, y0, y1, y2, y3);
+      }
+    }
+  } else if (EPI == kEpiPwa) {
+    const int hd = a.O / 2;
+    const int64_t bs = m / a.n;  // b S + s
+    const int j = (int)(m - bs * a.n);
+    const int64_t b = bs / a.depth, srow = bs - b * a.depth;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = cbase + 8 * v + 4 * g;  // 4 channels of one head (dh % 4 == 0)
+      float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
+      if (seg == 0) {
+        const int hh = c / a.dh, d0 = c - hh * a.dh;
+        bf16* dst = a.vt + (((b * a.heads + hh) * a.depth + srow) * a.dh + d0) * a.np + j;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[(int64_t)e * a.np] = (bf16)y[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = sigmoid_scaled(-kLog2e * y[e]);
+        store4(a.gate + m * hd + c, y[0], y[1], y[2], y[3]);
       }
     }
   } else if (EPI == kEpiSwiglu) {
@@ -530,6 +555,8 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
     launch_row_gemm_t<kEpiSwiglu, kXLn, 8>(a, stream);
   else if (epi == kEpiResid && xsrc == kXF32)
     launch_row_gemm_t<kEpiResid, kXF32, 1>(a, stream);
+  else if (epi == kEpiPwa && xsrc == kXLn)
+    launch_row_gemm_t<kEpiPwa, kXLn, 4>(a, stream);
 }
 
 void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream) {

@@ -4,7 +4,8 @@ The engine exposes ``layer_norm``, ``triangle_multiplicative_update``,
 ``triangle_attention`` and ``transition`` under ``miniworld_engine.kernels``
 (names: ``docs/guides/ENGINE-2.4.2.md:18-21`` of the reference; their signatures are
 not in the reference, so these are this library's own); ``attention_pair_bias`` serves
-the engine's ``single_attention`` op (``AttentionPairBias``).  Each function validates its
+the engine's ``single_attention`` op (``AttentionPairBias``) and
+``msa_pair_weighted_averaging`` its ``msa_pwa`` op (``MSAPairWeightedAveraging``). Each function validates its
 tensors, allocates the output and the workspace with torch's allocator on the input's
 device, and calls the C-ABI on torch's current stream. There is no fallback: the
 module classes decide what to refuse (``unsupported``) before a call ever gets here.
@@ -262,6 +263,65 @@ def attention_pair_bias(
         int(residual), float(eps_single), float(eps_pair), _stream(dev),
     )
     _native.check(status, "attention_pair_bias")
+    return out
+
+
+def msa_pair_weighted_averaging_supported(d_msa: int, n_head: int, d_head: int) -> bool:
+    """MSA widths and head splits the pair-weighted averaging kernels take."""
+    return (0 < d_msa <= 768 and d_msa % 64 == 0 and 0 < n_head <= 32 and d_head > 0
+            and d_head % 4 == 0 and (n_head * d_head) % 64 == 0)
+
+
+def msa_pair_weighted_averaging(
+    m: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    *,
+    ln_msa_weight: Tensor,
+    ln_msa_bias: Tensor,
+    ln_pair_weight: Tensor,
+    to_bias: Tensor,
+    to_value: Tensor,
+    to_gate: Tensor,
+    to_out: Tensor,
+    n_head: int,
+    residual: bool = True,
+    eps_msa: float = 1e-5,
+    eps_pair: float = 1e-5,
+    out: Tensor | None = None,
+) -> Tensor:
+    """MSA pair-weighted averaging of ``m [B, S, N, c_m]`` bf16 with the weights
+    ``softmax_j(LN_pair(z) . to_bias)`` from ``z [B, N, N, 128]`` bf16, under the key mask."""
+    batch, n = _pair(z, mask)
+    _need(m.is_cuda and m.is_contiguous() and m.dtype == torch.bfloat16,
+          "m must be a contiguous bf16 device tensor")
+    _need(m.dim() == 4 and m.shape[0] == batch and m.shape[2] == n,
+          f"m {tuple(m.shape)} does not match z {tuple(z.shape)}")
+    depth, cm = m.shape[1], m.shape[3]
+    hd = to_value.shape[0]
+    _need(hd % n_head == 0, f"hidden {hd} is not a multiple of {n_head} heads")
+    dh = hd // n_head
+    _need(msa_pair_weighted_averaging_supported(cm, n_head, dh),
+          f"d_msa={cm} heads={n_head} x {dh} (the kernels take d_msa a multiple of 64 up to 768, "
+          "at most 32 heads of a multiple of 4, heads x d_head a multiple of 64)")
+    dev = m.device
+    names = ("ln_msa_weight", "ln_msa_bias", "ln_pair_weight", "to_bias", "to_value", "to_gate",
+             "to_out")
+    ps = [_param(t, dev, nm) for t, nm in zip(
+        (ln_msa_weight, ln_msa_bias, ln_pair_weight, to_bias, to_value, to_gate, to_out), names)]
+    _need(ps[3].shape == (n_head, PAIR_WIDTH), f"to_bias {tuple(ps[3].shape)}")
+    _need(ps[4].shape == (hd, cm) and ps[5].shape == (hd, cm) and ps[6].shape == (cm, hd),
+          "to_value / to_gate [H d, c_m], to_out [c_m, H d]")
+    lib = _native.lib()
+    ws = _workspace(lib.ffk_msa_pair_weighted_averaging_workspace(batch, depth, n, cm, PAIR_WIDTH,
+                                                                  n_head, dh), dev)
+    out = torch.empty_like(m) if out is None else out
+    status = lib.ffk_msa_pair_weighted_averaging(
+        m.data_ptr(), z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
+        ws.data_ptr(), ws.numel(), batch, depth, n, cm, PAIR_WIDTH, n_head, dh, int(residual),
+        float(eps_msa), float(eps_pair), _stream(dev),
+    )
+    _native.check(status, "msa_pair_weighted_averaging")
     return out
 
 

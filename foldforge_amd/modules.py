@@ -446,6 +446,65 @@ class AttentionPairBias(EngineOp, MasterWeights, nn.Module):
         )
 
 
+# ------------------------------------------------------------------------------------ MSA stack
+class MSAPairWeightedAveraging(EngineOp, MasterWeights, nn.Module):
+    """MSA pair-weighted averaging, residual included (``legacy/attention.py:174-229``;
+    parameters ``legacy/released.py:253-278``): every MSA row is averaged over the keys with
+    one set of softmax weights per head taken from the pair. The pair norm has no offset
+    (a per-head constant is softmax-invariant). ``d_hidden`` is the per-head value width
+    (default ``d_msa // n_head``, the legacy ``value_dim``)."""
+
+    def __init__(self, d_msa: int, d_pair: int, n_head: int = 8, d_hidden: int | None = None,
+                 p_drop: float = 0.0, backend: str = "pytorch") -> None:
+        nn.Module.__init__(self)
+        dh = d_msa // n_head if d_hidden is None else d_hidden
+        self.d_msa, self.d_pair, self.n_head, self.d_hidden, self.p_drop = d_msa, d_pair, n_head, dh, p_drop
+        self.ln_msa = LayerNorm(d_msa)
+        self.ln_pair = LayerNorm(d_pair, bias=False)
+        self.to_bias = _linear(d_pair, n_head)
+        self.to_value = _linear(d_msa, n_head * dh)
+        self.to_gate = _linear(d_msa, n_head * dh)
+        self.to_out = _linear(n_head * dh, d_msa)
+        self._init_backend(backend)
+
+    def _unsupported_hip(self, m: Tensor, z: Tensor, mask: Tensor) -> str | None:
+        reason = _pair_reason(z, mask) or hip_reason(m)
+        if reason is not None:
+            return reason
+        if m.dtype != torch.bfloat16:
+            return f"{m.dtype} MSA activations (the kernels take bf16)"
+        if m.dim() != 4 or m.shape[0] != z.shape[0] or m.shape[2] != z.shape[1] or m.shape[3] != self.d_msa:
+            return f"MSA shape {tuple(m.shape)} for pair {tuple(z.shape)}"
+        if z.shape[-1] != 128 or self.d_pair != 128:
+            return f"d_pair={z.shape[-1]} (the kernels take 128)"
+        from foldforge_amd.kernels import msa_pair_weighted_averaging_supported
+
+        if not msa_pair_weighted_averaging_supported(self.d_msa, self.n_head, self.d_hidden):
+            return (f"d_msa={self.d_msa} heads={self.n_head} x {self.d_hidden} (the kernels take "
+                    "d_msa a multiple of 64 up to 768, at most 32 heads of a multiple of 4, "
+                    "heads x d_head a multiple of 64)")
+        return None
+
+    def _forward_pytorch(self, m: Tensor, z: Tensor, mask: Tensor, *, residual: bool = True) -> Tensor:
+        if self.dead:
+            return m if residual else torch.zeros_like(m)
+        return torch_ops.msa_pair_weighted_averaging(self, m, z, mask, residual=residual)
+
+    def _forward_hip(self, m: Tensor, z: Tensor, mask: Tensor, *, residual: bool = True) -> Tensor:
+        if self.dead:
+            return m if residual else torch.zeros_like(m)
+        from foldforge_amd import kernels
+
+        return kernels.msa_pair_weighted_averaging(
+            m.contiguous(), z.contiguous(), mask.contiguous(),
+            ln_msa_weight=self.ln_msa.weight, ln_msa_bias=self.ln_msa.bias,
+            ln_pair_weight=self.ln_pair.weight, to_bias=self.to_bias.weight,
+            to_value=self.to_value.weight, to_gate=self.to_gate.weight, to_out=self.to_out.weight,
+            n_head=self.n_head, residual=residual, eps_msa=self.ln_msa.eps,
+            eps_pair=self.ln_pair.eps,
+        )
+
+
 # ------------------------------------------------------------------------------------ block
 @dataclass(frozen=True)
 class PairformerConfig:

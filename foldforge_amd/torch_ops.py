@@ -6,7 +6,8 @@ reference). It runs on whatever device its inputs are on, computes in fp32 from 
 parameters and returns the input dtype. Equations: the reference's legacy statements
 (``legacy/reference/triangle.py:39-49``, ``legacy/attention.py:108-163``,
 ``legacy/reference/attention.py:77-100``, ``legacy/reference/transition.py:40-41``,
-``legacy/transformer.py:93-137``), under the engine's ``[B, N]`` key mask.
+``legacy/transformer.py:93-137``, ``legacy/attention.py:203-223``), under the engine's
+``[B, N]`` key mask.
 """
 
 from __future__ import annotations
@@ -130,3 +131,23 @@ def attention_pair_bias(m, s: Tensor, z: Tensor, mask: Tensor, extra_bias: Tenso
     gate = torch.sigmoid(_lin(x, m.to_gate.weight) + m.gate_bias)
     y = _lin(gate * o, m.to_out.weight)
     return (x0 + y if residual else y).to(dtype)
+
+
+def msa_pair_weighted_averaging(m_, msa: Tensor, z: Tensor, mask: Tensor, *,
+                                residual: bool = True) -> Tensor:
+    """``m_``: an MSAPairWeightedAveraging module; ``msa [B, S, N, c_m]``, ``z [B, N, N, c_z]``,
+    key mask ``[B, N]`` (``legacy/attention.py:203-223``)."""
+    dtype = msa.dtype
+    m = msa.float()
+    batch, depth, n, _ = m.shape
+    heads = m_.n_head
+    x = _ln(m, m_.ln_msa.weight, m_.ln_msa.bias, m_.ln_msa.eps)
+    zn = _ln(z.float(), m_.ln_pair.weight, None, m_.ln_pair.eps)
+    logits = torch.einsum("bijc,hc->bhij", zn, m_.to_bias.weight.float())
+    keep = mask.to(torch.bool)
+    w = logits.masked_fill(~keep[:, None, None, :], MASK_VALUE).softmax(dim=-1)
+    v = _lin(x, m_.to_value.weight).reshape(batch, depth, n, heads, -1)
+    o = torch.einsum("bhij,bsjhc->bsihc", w, v).reshape(batch, depth, n, -1)
+    o = torch.where((~keep.any(dim=-1))[:, None, None, None], torch.zeros_like(o), o)
+    y = _lin(torch.sigmoid(_lin(x, m_.to_gate.weight)) * o, m_.to_out.weight)
+    return (m + y if residual else y).to(dtype)

@@ -157,6 +157,32 @@ int32_t ffk_attention_pair_bias(
     int64_t n, int32_t d_single, int32_t d_pair, int32_t n_head, float gate_bias,
     int32_t residual, float eps_single, float eps_pair, void* stream);
 
+/*
+ * MSA pair-weighted averaging, residual included:
+ *   x = LN_msa(m); w[h, i, :] = softmax_j(LN_pair(z)[i, j] . w_bias[h]) over valid keys j
+ *   (pair norm without offset; the same weights for every MSA row);
+ *   o[s, i, h] = sum_j w[h, i, j] (x w_value^T)[s, j, h];
+ *   out = m + (sigmoid(x w_gate^T) * o) w_out^T.
+ * m, out [batch, depth, n, d_msa] bf16 (depth = MSA rows); z [batch, n, n, d_pair] bf16;
+ * key_mask [batch, n] (a column is a key when any MSA row has it); a batch element without a
+ * valid key gets a zero update. d_pair = 128; d_msa a multiple of 64 up to 768; at most 32
+ * heads of d_head (a multiple of 4), n_head * d_head a multiple of 64 (AF3: 8 x 8). `out`
+ * may alias `m`.
+ * Replaces: engine MSAPairWeightedAveraging.forward, op name "msa_pwa"
+ * (src/foldforge/modules/engine/backends.py:49; equations
+ * src/foldforge/models/checkpoints/legacy/attention.py:174-229; engine parameters
+ * legacy/released.py:253-278; called as graph.py:302).
+ */
+size_t ffk_msa_pair_weighted_averaging_workspace(int64_t batch, int64_t depth, int64_t n,
+                                                  int32_t d_msa, int32_t d_pair, int32_t n_head,
+                                                  int32_t d_head);
+int32_t ffk_msa_pair_weighted_averaging(
+    const void* m, const void* z, const uint8_t* key_mask, const float* ln_msa_w,
+    const float* ln_msa_b, const float* ln_pair_w, const float* w_bias, const float* w_value,
+    const float* w_gate, const float* w_out, void* out, void* workspace, size_t workspace_bytes,
+    int64_t batch, int64_t depth, int64_t n, int32_t d_msa, int32_t d_pair, int32_t n_head,
+    int32_t d_head, int32_t residual, float eps_msa, float eps_pair, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

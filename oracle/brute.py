@@ -9,7 +9,8 @@ numpy fp64 arrays; every loop is explicit. Sizes must stay tiny (N <= 8).
 Equations (reference paths as in ``oracle/pairstack.py``):
 ``legacy/reference/triangle.py:39-49``, ``legacy/attention.py:108-163``,
 ``legacy/reference/attention.py:96-101``, ``legacy/reference/transition.py:40-41``,
-``legacy/transformer.py:93-137``.
+``legacy/transformer.py:93-137``, ``legacy/attention.py:203-223`` (MSA pair-weighted
+averaging).
 """
 
 from __future__ import annotations
@@ -183,4 +184,36 @@ def attention_pair_bias(s, z, mask, p, *, n_head: int, gate_bias: float = 0.0,
             y = _matvec(p["to_out.weight"], gated)
             for ch in range(cs):
                 out[b, i, ch] += y[ch]
+    return out
+
+
+def msa_pair_weighted_averaging(m, z, mask, p, *, n_head: int, eps: float = 1e-5):
+    """MSA pair-weighted averaging, fp64 loops: one softmax over keys j per (head, query i),
+    shared by every MSA row s."""
+    batch, depth, n, cm = m.shape
+    hd = len(p["to_value.weight"])
+    d = hd // n_head
+    out = np.array(m, dtype=np.float64, copy=True)
+    for b in range(batch):
+        any_key = any(bool(mask[b, k]) for k in range(n))
+        w = [[None] * n for _ in range(n_head)]
+        for i in range(n):
+            zb = [_matvec(p["to_bias.weight"], layer_norm_vec(z[b, i, j], p["ln_pair.weight"], None, eps))
+                  for j in range(n)]
+            for h in range(n_head):
+                w[h][i] = _softmax_row([zb[j][h] if bool(mask[b, j]) else MASK_VALUE for j in range(n)])
+        for s in range(depth):
+            x = [layer_norm_vec(m[b, s, j], p["ln_msa.weight"], p["ln_msa.bias"], eps) for j in range(n)]
+            v = [_matvec(p["to_value.weight"], xj) for xj in x]
+            for i in range(n):
+                g = _matvec(p["to_gate.weight"], x[i])
+                o = [0.0] * hd
+                for h in range(n_head):
+                    for c in range(d):
+                        f = h * d + c
+                        o[f] = sum(w[h][i][j] * v[j][f] for j in range(n)) if any_key else 0.0
+                gated = [_sigmoid(g[f]) * o[f] for f in range(hd)]
+                y = _matvec(p["to_out.weight"], gated)
+                for ch in range(cm):
+                    out[b, s, i, ch] += y[ch]
     return out

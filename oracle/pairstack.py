@@ -34,6 +34,9 @@ Reference equations followed (paths relative to the reference tree):
   ``legacy/pairformer.py:204-229`` (engine names ``legacy/released.py:281-315``;
   the pair norm's offset is dropped, ``released.py:268-270``).
 * Block: the sequential AF3 order of ``legacy/pairformer.py:191-230``.
+* MSA pair-weighted averaging: ``legacy/attention.py:174-229`` (``MSAAttention``; engine
+  names ``legacy/released.py:253-278``, the pair norm's offset dropped), called with the
+  engine's column key mask ``[B, N]`` (``src/foldforge/modules/engine/graph.py:295-305``).
 
 The engine takes a ``[B, N]`` key mask (``src/foldforge/modules/engine/graph.py:214-218``)
 where the legacy graph takes the outer-product pair mask; the two agree on valid
@@ -249,6 +252,42 @@ def attention_pair_bias(
     o = torch.where(empty[:, None, None], torch.zeros_like(o), o)
     gate = torch.sigmoid(x @ _p(params, "to_gate.weight", dtype).T + gate_bias)
     return s + (gate * o) @ _p(params, "to_out.weight", dtype).T
+
+
+def msa_pair_weighted_averaging(
+    m: Tensor,
+    z: Tensor,
+    mask: Tensor,
+    params: Params,
+    *,
+    n_head: int,
+    eps: float = 1e-5,
+    dtype: torch.dtype = torch.float32,
+) -> Tensor:
+    """MSA pair-weighted averaging (``legacy/attention.py:203-223``), residual included.
+
+    ``m [B, S, N, c_m]``, ``z [B, N, N, c_z]``, key mask ``[B, N]``:
+    ``x = LN_msa(m)``; ``w[h, i, :] = softmax_j(LN_pair(z)[i, j] . W_b[h])`` over valid keys j
+    (one set of weights for every MSA row); ``o[s, i, h] = sum_j w[h, i, j] v[s, j, h]`` with
+    ``v = x W_v^T``; ``m + (sigmoid(x W_g^T) * o) W_out^T``. A batch element without a valid key
+    gets a zero update.
+    """
+    m = m.detach().to("cpu", dtype)
+    z = z.detach().to("cpu", dtype)
+    batch, depth, n, cm = m.shape
+    x = layer_norm(m, _p(params, "ln_msa.weight", dtype), _p(params, "ln_msa.bias", dtype), eps)
+    hd = params["to_value.weight"].shape[0]
+    d = hd // n_head
+    zn = layer_norm(z, _p(params, "ln_pair.weight", dtype), None, eps)
+    logits = torch.einsum("bijc,hc->bhij", zn, _p(params, "to_bias.weight", dtype))
+    keep = mask.to("cpu", torch.bool)[:, None, None, :]
+    w = torch.softmax(logits.masked_fill(~keep, MASK_VALUE), dim=-1)
+    v = (x @ _p(params, "to_value.weight", dtype).T).reshape(batch, depth, n, n_head, d)
+    o = torch.einsum("bhij,bsjhc->bsihc", w, v).reshape(batch, depth, n, hd)
+    empty = ~mask.to("cpu", torch.bool).any(dim=-1)
+    o = torch.where(empty[:, None, None, None], torch.zeros_like(o), o)
+    gate = torch.sigmoid(x @ _p(params, "to_gate.weight", dtype).T)
+    return m + (gate * o) @ _p(params, "to_out.weight", dtype).T
 
 
 def sub_params(params: Params, prefix: str) -> dict[str, Tensor]:

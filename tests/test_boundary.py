@@ -20,6 +20,7 @@ from foldforge_amd import backends, factories, graph, policy, serving
 from foldforge_amd.modules import (
     AttentionPairBias,
     BackendUnsupported,
+    MSAPairWeightedAveraging,
     MasterWeights,
     PairformerBlock,
     Transition,
@@ -215,7 +216,8 @@ def test_engine_state_dict_keys():
 
 
 def test_dead_flag_and_identity():
-    for cls in (Transition, TriangleAttention, TriangleMultiplication, AttentionPairBias):
+    for cls in (Transition, TriangleAttention, TriangleMultiplication, AttentionPairBias,
+                MSAPairWeightedAveraging):
         assert cls.dead is False
     module = factories.transition(16, 2, precision="fp32").eval()
     module.dead = True
@@ -262,6 +264,24 @@ def test_pytorch_backend_triattn_matches_oracle(starting, model):
     want = ps.triangle_attention(x, mask, m.state_dict(), starting=starting, n_head=4,
                                  transposed_bias=m.transposed_bias, dtype=torch.float64)
     torch.testing.assert_close(_valid(got.double(), mask), _valid(want, mask), atol=2e-5, rtol=2e-5)
+
+
+def test_msa_pair_weighted_averaging_class_contract_and_pytorch_backend():
+    m = randomise(factories.msa_pair_weighted_averaging(64, 32, 8, precision="fp32"), 6)
+    keys = set(m.state_dict())
+    assert {"ln_msa.weight", "ln_msa.bias", "ln_pair.weight", "to_bias.weight", "to_value.weight",
+            "to_gate.weight", "to_out.weight"} == keys  # no pair-norm offset
+    assert m.to_value.weight.shape == (64, 64) and m.d_hidden == 8
+    assert backends.op_of(m) == "msa_pwa"
+    torch.manual_seed(7)
+    msa = torch.randn(1, 3, 7, 64)
+    z = torch.randn(1, 7, 7, 32)
+    mask = torch.ones(1, 7, dtype=torch.bool)
+    mask[0, -2:] = False
+    got = m(msa, z, mask)
+    want = ps.msa_pair_weighted_averaging(msa, z, mask, m.state_dict(), n_head=8, dtype=torch.float64)
+    torch.testing.assert_close(got.double(), want, atol=2e-5, rtol=2e-5)
+    torch.testing.assert_close(m(msa, z, mask), msa + m.delta(msa, z, mask))
 
 
 def test_pytorch_backend_block_and_run_block_match_oracle():

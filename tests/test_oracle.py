@@ -259,6 +259,50 @@ def test_attention_pair_bias_matches_brute_force():
     np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
 
 
+def _pwa_params(cm: int, c: int, heads: int, d: int, seed: int) -> dict[str, torch.Tensor]:
+    return _rand_params({"ln_msa.weight": (cm,), "ln_msa.bias": (cm,), "ln_pair.weight": (c,),
+                         "to_bias.weight": (heads, c), "to_value.weight": (heads * d, cm),
+                         "to_gate.weight": (heads * d, cm), "to_out.weight": (cm, heads * d)}, seed)
+
+
+def test_msa_pair_weighted_averaging_matches_brute_force():
+    depth, n, cm, c, heads, d = 3, 5, 6, 4, 2, 3
+    p = _pwa_params(cm, c, heads, d, 91)
+    g = torch.Generator().manual_seed(92)
+    m = torch.randn(2, depth, n, cm, generator=g, dtype=F64)
+    z = torch.randn(2, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(2, n, dtype=torch.bool)
+    mask[0, 1] = mask[0, 4] = False
+    mask[1, :] = False  # no valid key: zero update
+    got = ps.msa_pair_weighted_averaging(m, z, mask, p, n_head=heads, dtype=F64)
+    want = brute.msa_pair_weighted_averaging(m.numpy(), z.numpy(), mask.numpy(), _np(p), n_head=heads)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+    assert torch.equal(got[1], m[1])
+
+
+def test_msa_pair_weighted_averaging_closed_forms():
+    """Zero pair logits give the plain mean of the values over the valid keys; the weights do
+    not depend on the MSA row, so permuting MSA rows permutes the update."""
+    depth, n, cm, c, heads, d = 4, 6, 8, 4, 2, 4
+    p = _pwa_params(cm, c, heads, d, 93)
+    p["to_bias.weight"] = torch.zeros(heads, c, dtype=F64)
+    g = torch.Generator().manual_seed(94)
+    m = torch.randn(1, depth, n, cm, generator=g, dtype=F64)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    mask = torch.tensor([[True, False, True, True, False, True]])
+    got = ps.msa_pair_weighted_averaging(m, z, mask, p, n_head=heads, dtype=F64)
+    x = F.layer_norm(m, (cm,), p["ln_msa.weight"], p["ln_msa.bias"], 1e-5)
+    v = x @ p["to_value.weight"].T
+    mean = v[:, :, mask[0]].mean(dim=2, keepdim=True)
+    want = m + (torch.sigmoid(x @ p["to_gate.weight"].T) * mean) @ p["to_out.weight"].T
+    torch.testing.assert_close(got, want)
+    perm = torch.tensor([2, 0, 3, 1])
+    p2 = _pwa_params(cm, c, heads, d, 95)
+    a = ps.msa_pair_weighted_averaging(m, z, mask, p2, n_head=heads, dtype=F64)
+    b = ps.msa_pair_weighted_averaging(m[:, perm], z, mask, p2, n_head=heads, dtype=F64)
+    torch.testing.assert_close(b, a[:, perm])
+
+
 def test_block_is_the_composition_of_the_pinned_ops():
     n, c, h, heads, d, cs, hs = 5, 6, 4, 2, 3, 6, 2
     params = {}

@@ -65,6 +65,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--no-reference-backend", action="store_true",
                     help="with --trunk-only: skip the engine pytorch backend's trunk run")
     ap.add_argument("--ladder", action="store_true")
+    ap.add_argument("--msa", action="store_true",
+                    help="time the MSA-stack ops at L = 256 / 384 tokens, 512 MSA rows")
     ap.add_argument("--ladder-max", type=int, default=16384)
     return ap.parse_args()
 
@@ -294,6 +296,35 @@ def graph_measure(n: int, runs: int = 3) -> dict:
             "graph_equals_eager": bool(torch.equal(pg, pe) and torch.equal(sg, se))}
 
 
+def msa_measure(reps: int = 20) -> dict:
+    """MSA pair-weighted averaging at the reference's op-table shapes: L = 256 / 384 tokens,
+    512 MSA rows, AF3 widths (c_m 64, c_z 128, 8 heads x 8), bf16; hip and the engine pytorch
+    backend on the same GPU."""
+    import torch
+
+    from foldforge_amd import factories
+    from foldforge_amd.trunk import randomise
+
+    out = {"workload": "MSA pair-weighted averaging, 512 MSA rows, c_m=64, c_z=128, 8 heads x 8, "
+                       "all-ones mask, bf16, seeded random init", "rows": []}
+    mod = randomise(factories.msa_pair_weighted_averaging(64, 128, 8), seed=0).cuda()
+    for n in (256, 384):
+        g = torch.Generator().manual_seed(n)
+        m = torch.randn(1, 512, n, 64, generator=g).bfloat16().cuda()
+        z = torch.randn(1, n, n, 128, generator=g).bfloat16().cuda()
+        mask = torch.ones(1, n, dtype=torch.bool, device="cuda")
+        row = {"n": n}
+        with torch.no_grad():
+            for backend in ("hip", "pytorch"):
+                mod.set_backend(backend)
+                row[f"{backend}_ms"] = round(event_time_ms(lambda: mod(m, z, mask), reps, warm=5), 4)
+        gflop = (2 * 512 * n * 64 * 128 + 2 * n * n * 64 * 512 + 2 * 512 * n * 64 * 64 + 2 * n * n * 128 * 8) / 1e9
+        row["gflop"] = round(gflop, 2)
+        row["hip_tflops"] = round(gflop / row["hip_ms"], 1)
+        out["rows"].append(row)
+    return out
+
+
 def ladder(max_n: int) -> list[dict]:
     """Config 5: full trunks at N = 768 .. 2048, then single blocks (with single track) at
     larger N until the device runs out of memory."""
@@ -389,6 +420,9 @@ def main() -> int:
         return 1
     if args.ladder:
         ladder(args.ladder_max)
+        return 0
+    if args.msa:
+        print(json.dumps({"msa": msa_measure(args.steps)}), flush=True)
         return 0
     if args.trunk_only:
         trunk = trunk_measure(512, max(1, args.steps // 10), pytorch_too=not args.no_reference_backend,

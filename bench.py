@@ -7,6 +7,10 @@ node (4 heads x 32), pair transition (x4) -- on z [1, 512, 512, 128] bf16 ~N(0,1
 parameters (seeded init), ragged padding: the real length is drawn from U{300..512}
 (seed 0) and the key mask zeroes the padded tokens. Inputs are resident in HBM before
 the timed region; every step runs the full block through the native ``hip`` backend.
+After the W warm-up steps, untimed steps continue until ``--settle-ms`` (500) of wall
+time has passed since the first warm-up step: an idle MI355X needs a few hundred ms of
+load to reach its steady clock, and a timed region of 20 blocks (~25 ms) started from a
+cold clock has measured up to 2.8x slow. ``config.clock_settle`` reports those steps.
 
 Reported beside it, in the same JSON line:
 * ``roofline``: the triangle-attention flash core (the block's dominant MFMA kernel),
@@ -53,6 +57,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--settle-ms", type=float, default=500.0,
+                    help="after the warm-up steps, keep running untimed steps until this much wall "
+                         "time has passed since the first one (the GPU clock ramps up under load)")
     ap.add_argument("--n", type=int, default=512)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--kernel-reps", type=int, default=20)
@@ -305,23 +312,29 @@ def msa_measure(reps: int = 20) -> dict:
     from foldforge_amd import factories
     from foldforge_amd.trunk import randomise
 
-    out = {"workload": "MSA pair-weighted averaging, 512 MSA rows, c_m=64, c_z=128, 8 heads x 8, "
-                       "all-ones mask, bf16, seeded random init", "rows": []}
-    mod = randomise(factories.msa_pair_weighted_averaging(64, 128, 8), seed=0).cuda()
-    for n in (256, 384):
-        g = torch.Generator().manual_seed(n)
-        m = torch.randn(1, 512, n, 64, generator=g).bfloat16().cuda()
-        z = torch.randn(1, n, n, 128, generator=g).bfloat16().cuda()
-        mask = torch.ones(1, n, dtype=torch.bool, device="cuda")
-        row = {"n": n}
-        with torch.no_grad():
-            for backend in ("hip", "pytorch"):
-                mod.set_backend(backend)
-                row[f"{backend}_ms"] = round(event_time_ms(lambda: mod(m, z, mask), reps, warm=5), 4)
-        gflop = (2 * 512 * n * 64 * 128 + 2 * n * n * 64 * 512 + 2 * 512 * n * 64 * 64 + 2 * n * n * 128 * 8) / 1e9
-        row["gflop"] = round(gflop, 2)
-        row["hip_tflops"] = round(gflop / row["hip_ms"], 1)
-        out["rows"].append(row)
+    out = {"workload": "MSA pair-weighted averaging, 512 MSA rows, c_m=64, c_z=128, 8 heads x "
+                       "d_head (8: AF3; 32: the reference's op-table cell), all-ones mask, bf16, "
+                       "seeded random init", "rows": []}
+    depth, cm, heads = 512, 64, 8
+    for dh in (8, 32):
+        mod = randomise(factories.msa_pair_weighted_averaging(cm, 128, heads, dh), seed=0).cuda()
+        hd = heads * dh
+        for n in (256, 384):
+            g = torch.Generator().manual_seed(n)
+            m = torch.randn(1, depth, n, cm, generator=g).bfloat16().cuda()
+            z = torch.randn(1, n, n, 128, generator=g).bfloat16().cuda()
+            mask = torch.ones(1, n, dtype=torch.bool, device="cuda")
+            row = {"n": n, "d_head": dh}
+            with torch.no_grad():
+                for backend in ("hip", "pytorch"):
+                    mod.set_backend(backend)
+                    row[f"{backend}_ms"] = round(
+                        event_time_ms(lambda: mod(m, z, mask), reps, warm=max(50, reps)), 4)
+            gflop = (2 * depth * n * cm * 2 * hd + 2 * n * n * hd * depth + 2 * depth * n * hd * cm
+                     + 2 * n * n * 128 * heads) / 1e9
+            row["gflop"] = round(gflop, 2)
+            row["hip_tflops"] = round(gflop / row["hip_ms"], 1)
+            out["rows"].append(row)
     return out
 
 
@@ -444,9 +457,17 @@ def main() -> int:
     z, mask = z_cpu.to(dev), mask_cpu.to(dev)
 
     with torch.no_grad():
+        t_warm = time.perf_counter()
         for _ in range(args.warmup):
             out = block(z, mask)
         torch.cuda.synchronize()
+        settle_steps = 0
+        while (time.perf_counter() - t_warm) * 1e3 < args.settle_ms:
+            for _ in range(10):
+                out = block(z, mask)
+            settle_steps += 10
+            torch.cuda.synchronize()
+        settle_ms = (time.perf_counter() - t_warm) * 1e3
         start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t0 = time.perf_counter()
         start.record()
@@ -497,6 +518,7 @@ def main() -> int:
                         "c_z=128, trimul hidden 128, triangle attention 4x32, transition x4, batch 1",
             "n_tokens": n, "real_length": length, "batch": 1, "c_z": 128,
             "block_gflop": round(gflop, 1), "block_tflops": round(gflop / ms_per_step, 1),
+            "clock_settle": {"untimed_steps_after_warmup": settle_steps, "ms": round(settle_ms, 1)},
         },
         "roofline": roof,
         "kernels": {"layer_norm": ln, **({"copy_reference": copy} if copy else {})},

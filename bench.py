@@ -338,6 +338,37 @@ def msa_measure(reps: int = 20) -> dict:
     return out
 
 
+def opm_measure(reps: int = 20) -> dict:
+    """Outer product mean at the reference's op-table shapes: L = 256 / 384 tokens, 512 MSA
+    rows, c_m 64, 32 x 32 outer products, c_z 128, AF3 form (n + 1e-3 divisor, bias before
+    the divide), 90% of the MSA entries real; hip and the engine pytorch backend."""
+    import torch
+
+    from foldforge_amd import factories
+    from foldforge_amd.trunk import randomise
+
+    out = {"workload": "outer product mean, 512 MSA rows, c_m=64, hidden 32, c_z=128, AF3 divisor, "
+                       "90% of MSA entries real, bf16, seeded random init", "rows": []}
+    depth, cm = 512, 64
+    mod = randomise(factories.outer_product_mean(cm, 128, 32, count_offset=1e-3,
+                                                 normalize_before_proj=False), seed=0).cuda()
+    for n in (256, 384):
+        g = torch.Generator().manual_seed(n)
+        m = torch.randn(1, depth, n, cm, generator=g).bfloat16().cuda()
+        rows = (torch.rand(1, depth, n, generator=g) < 0.9).cuda()
+        row = {"n": n}
+        with torch.no_grad():
+            for backend in ("hip", "pytorch"):
+                mod.set_backend(backend)
+                row[f"{backend}_ms"] = round(
+                    event_time_ms(lambda: mod(m, rows), reps, warm=max(50, reps)), 4)
+        gflop = (2 * depth * n * n * 32 * 32 + 2 * n * n * 1024 * 128 + 2 * depth * n * cm * 64) / 1e9
+        row["gflop"] = round(gflop, 2)
+        row["hip_tflops"] = round(gflop / row["hip_ms"], 1)
+        out["rows"].append(row)
+    return out
+
+
 def ladder(max_n: int) -> list[dict]:
     """Config 5: full trunks at N = 768 .. 2048, then single blocks (with single track) at
     larger N until the device runs out of memory."""
@@ -435,7 +466,7 @@ def main() -> int:
         ladder(args.ladder_max)
         return 0
     if args.msa:
-        print(json.dumps({"msa": msa_measure(args.steps)}), flush=True)
+        print(json.dumps({"msa": msa_measure(args.steps), "opm": opm_measure(args.steps)}), flush=True)
         return 0
     if args.trunk_only:
         trunk = trunk_measure(512, max(1, args.steps // 10), pytorch_too=not args.no_reference_backend,

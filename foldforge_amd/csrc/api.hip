@@ -210,6 +210,24 @@ PwaWs pwa_ws(void* ws, int64_t batch, int64_t depth, int64_t n, int heads, int d
   return w;
 }
 
+struct OpmWs {
+  bf16 *lt, *rt, *mt, *wp;
+  float* count;
+  size_t bytes;
+};
+OpmWs opm_ws(void* ws, int64_t batch, int64_t depth, int64_t n, int cz) {
+  Carver cv{static_cast<char*>(ws)};
+  const int64_t sp = pad32(depth);
+  OpmWs w;
+  w.lt = cv.take<bf16>((size_t)batch * n * 32 * sp);
+  w.rt = cv.take<bf16>((size_t)batch * n * 32 * sp);
+  w.mt = cv.take<bf16>((size_t)batch * n * sp);
+  w.count = cv.take<float>((size_t)batch * n * n);
+  w.wp = cv.take<bf16>((size_t)cz * 1024);
+  w.bytes = cv.used;
+  return w;
+}
+
 struct ApbWs {
   bf16 *q, *k, *vt, *gate;
   float *og, *bias;
@@ -700,6 +718,90 @@ int32_t ffk_msa_pair_weighted_averaging(
   o.residual = residual ? 1 : 0;
   launch_row_gemm(o, kEpiResid, kXF32, st);
   return check_launch("msa_pair_weighted_averaging");
+}
+
+size_t ffk_outer_product_mean_workspace(int64_t batch, int64_t depth, int64_t n, int32_t d_msa,
+                                        int32_t d_hidden, int32_t d_pair) {
+  if (batch <= 0 || depth <= 0 || n <= 0 || d_msa <= 0 || d_hidden <= 0 || d_pair <= 0) return 0;
+  return opm_ws(nullptr, batch, depth, n, d_pair).bytes;
+}
+
+int32_t ffk_outer_product_mean(
+    const void* m, const uint8_t* rows_mask, const float* ln_w, const float* ln_b,
+    const float* w_left, const float* b_left, const float* w_right, const float* b_right,
+    const float* w_out, const float* b_out, const void* residual, void* out, void* workspace,
+    size_t workspace_bytes, int64_t batch, int64_t depth, int64_t n, int32_t d_msa,
+    int32_t d_hidden, int32_t d_pair, float eps, float count_offset,
+    int32_t normalize_before_proj, void* stream) {
+  if (int32_t st = check_device()) return st;
+  if (d_hidden != 32 || d_pair != 128)
+    return fail(FFK_ERR_INVALID, "outer_product_mean: d_hidden=%d d_pair=%d (kernels take 32 and 128)", d_hidden, d_pair);
+  if (d_msa <= 0 || d_msa % 64 != 0 || d_msa > kLnGemmMaxK)
+    return fail(FFK_ERR_INVALID, "outer_product_mean: d_msa=%d (kernels take a multiple of 64 up to %d)", d_msa, kLnGemmMaxK);
+  if (batch <= 0 || depth <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "outer_product_mean: empty shape");
+  const int64_t sp = pad32(depth);
+  const int64_t nt = (n + 7) / 8;
+  if (batch > 65535 || (n + 31) / 32 > 65535 || nt * nt * batch > 0x7fffffffLL ||
+      batch * n * sp / 32 > 0x7fffffffLL || n * n > 0x7fffffffLL)
+    return fail(FFK_ERR_INVALID, "outer_product_mean: shape exceeds the launch grid");
+  if (!m || !rows_mask || !ln_w || !ln_b || !w_left || !w_right || !w_out || !b_out || !out)
+    return fail(FFK_ERR_INVALID, "outer_product_mean: null argument");
+  if (!aligned16(m) || !aligned16(out) || !aligned16(w_left) || !aligned16(w_right) ||
+      !aligned16(b_out) || (residual && !aligned16(residual)))
+    return fail(FFK_ERR_INVALID, "outer_product_mean: m/out/residual, the projection weights and the output bias must be 16-byte aligned");
+  const OpmWs need = opm_ws(nullptr, batch, depth, n, d_pair);
+  if (!workspace || workspace_bytes < need.bytes || !aligned16(workspace))
+    return fail(FFK_ERR_WORKSPACE, "outer_product_mean: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
+  const OpmWs w = opm_ws(workspace, batch, depth, n, d_pair);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  RowGemmArgs p{};
+  p.ln_x = static_cast<const bf16*>(m);
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.eps = eps;
+  p.w0 = w_left;
+  p.w1 = w_right;
+  p.bias0 = b_left;
+  p.bias1 = b_right;
+  p.M = batch * n * sp;
+  p.K = d_msa;
+  p.O = 64;
+  p.n = (int)n;
+  p.depth = (int)depth;
+  p.sp = (int)sp;
+  p.rows_mask = rows_mask;
+  p.lt = w.lt;
+  p.rt = w.rt;
+  p.mt = w.mt;
+  launch_row_gemm(p, kEpiOpm, kXLn, st);
+
+  OpmCountArgs c;
+  c.mt = w.mt;
+  c.count = w.count;
+  c.batch = (int)batch;
+  c.n = (int)n;
+  c.sp = (int)sp;
+  launch_opm_count(c, st);
+
+  launch_opm_pack(w_out, w.wp, d_pair, st);
+
+  OpmContractArgs o;
+  o.lt = w.lt;
+  o.rt = w.rt;
+  o.wp = w.wp;
+  o.bias = b_out;
+  o.count = w.count;
+  o.res = static_cast<const bf16*>(residual);
+  o.out = static_cast<bf16*>(out);
+  o.batch = (int)batch;
+  o.n = (int)n;
+  o.sp = (int)sp;
+  o.cz = d_pair;
+  o.count_offset = count_offset;
+  o.normalize_before_proj = normalize_before_proj ? 1 : 0;
+  launch_opm_contract(o, st);
+  return check_launch("outer_product_mean");
 }
 
 }  // extern "C"

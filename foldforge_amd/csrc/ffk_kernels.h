@@ -68,8 +68,8 @@ void launch_transition(const TransitionArgs& a, hipStream_t stream);
 // Token-row GEMM out[m][o] = sum_k W[o][k] x[m][k] (single track, single.hip) with one of
 // three epilogues, x either LayerNorm(ln_x) (kXLn, K <= kLnGemmMaxK) or fp32 rows x32 (kXF32).
 // K % 64 == 0, O % 32 == 0; weights are the fp32 parameters. Pairs served: (kEpiApb, kXLn),
-// (kEpiSwiglu, kXLn), (kEpiResid, kXF32).
-enum { kEpiApb = 0, kEpiSwiglu = 1, kEpiResid = 2, kEpiPwa = 3 };
+// (kEpiSwiglu, kXLn), (kEpiResid, kXF32), (kEpiPwa, kXLn), (kEpiOpm, kXLn).
+enum { kEpiApb = 0, kEpiSwiglu = 1, kEpiResid = 2, kEpiPwa = 3, kEpiOpm = 4 };
 enum { kXLn = 0, kXF32 = 1 };
 constexpr int kLnGemmMaxK = 768;
 struct RowGemmArgs {
@@ -92,6 +92,15 @@ struct RowGemmArgs {
   // kEpiPwa: w0 = to_value, w1 = to_gate ([hd][K] each, O = 2 hd); tokens m = (b S + s) n + j;
   // v^T [batch][heads][S][dh][np] (bf16, keys contiguous), gate = sigmoid(x W_g^T) [M][hd]
   int depth;
+  // kEpiOpm: w0 = to_left, w1 = to_right ([32][K] each, O = 64), bias0 / bias1 their biases
+  // (NULL: none). Logical rows m = (b n + j) sp + s (s < sp, sp % 32 == 0) read MSA row
+  // (b depth + s) n + j; rows with s >= depth, or masked in rows_mask [batch][depth][n],
+  // project to 0. Outputs: lt / rt [batch][n][32][sp] (bf16, MSA rows contiguous) and mt
+  // [batch][n][sp] (bf16 0 / 1, the row mask transposed).
+  const uint8_t* rows_mask;
+  const float *bias0, *bias1;
+  bf16 *lt, *rt, *mt;
+  int sp;
   float* h32;  // kEpiSwiglu: [M][hid] = silu(a) * b
   const bf16* res;  // kEpiResid: out = res + y (residual) or y
   bf16* out;
@@ -138,6 +147,32 @@ struct PwaAverageArgs {
   int batch, heads, depth, n, np, dh;
 };
 void launch_pwa_average(const PwaAverageArgs& a, hipStream_t stream);
+
+// Outer product mean (opm.hip). For every pair (i, j): o[(c, e)] = sum_s l[s][i][c] r[s][j][e]
+// over the MSA rows, out = (o W^T scale1 + bias) scale2 with the count n_ij = sum_s
+// m[s][i] m[s][j]: divisor d = n_ij + count_offset (count_offset >= 0) or max(n_ij, 1)
+// (count_offset < 0); normalize_before_proj: scale1 = 1 / d, scale2 = 1, else scale1 = 1,
+// scale2 = 1 / d. Optional residual: out = res + value.
+struct OpmCountArgs {
+  const bf16* mt;  // [batch][n][sp]
+  float* count;    // [batch][n][n]
+  int batch, n, sp;
+};
+void launch_opm_count(const OpmCountArgs& a, hipStream_t stream);
+// to_out.weight [c_z][32 * 32] fp32 (column c * 32 + e) -> the contraction's bf16 order.
+void launch_opm_pack(const float* w, bf16* wp, int cz, hipStream_t stream);
+struct OpmContractArgs {
+  const bf16 *lt, *rt;   // [batch][n][32][sp]
+  const bf16* wp;        // [c_z][1024] from launch_opm_pack
+  const float* bias;     // [c_z]
+  const float* count;    // [batch][n][n]
+  const bf16* res;       // [batch][n][n][c_z] or NULL
+  bf16* out;             // [batch][n][n][c_z]
+  int batch, n, sp, cz;
+  float count_offset;
+  int normalize_before_proj;
+};
+void launch_opm_contract(const OpmContractArgs& a, hipStream_t stream);
 
 struct PackSeg {
   const float* src;  // NULL: write zeros

@@ -44,15 +44,6 @@ __device__ __forceinline__ bf16x8 cvt8(const float* p) {
   return r;
 }
 
-__device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float d) {
-  bf16x4 v;
-  v[0] = (bf16)a;
-  v[1] = (bf16)b;
-  v[2] = (bf16)c;
-  v[3] = (bf16)d;
-  *reinterpret_cast<bf16x4*>(p) = v;
-}
-
 // Position of key `key` inside the v^T rows: index bits 2 and 3 exchanged, so that the 8
 // consecutive positions a lane loads are the 8 keys its P^T operand holds.
 __device__ __forceinline__ int vkey_pos(int key) {
@@ -91,6 +82,16 @@ size_t row_gemm_lds(int xsrc, int K, int no) {
   return xsrc == kXLn ? red + (size_t)2 * 32 * (K + 8) * sizeof(bf16) : red;
 }
 
+// kEpiOpm: the MSA row read by logical row m = (b n + j) sp + s (rows past the depth repeat
+// the last one; their projection is zeroed).
+__device__ inline int64_t opm_msa_row(const RowGemmArgs& a, int64_t m) {
+  const int64_t bj = m / a.sp;
+  const int s = min((int)(m - bj * a.sp), a.depth - 1);
+  const int64_t b = bj / a.n;
+  const int j = (int)(bj - b * a.n);
+  return (b * a.depth + s) * a.n + j;
+}
+
 template <int EPI, int XSRC, int NO>
 __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
   constexpr int KS = kGemmWaves / NO;
@@ -114,7 +115,7 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
     cbase = ot * 32 - seg * cs;
     const float* base = seg == 0 ? a.w0 : seg == 1 ? a.w1 : seg == 2 ? a.w2 : a.w3;
     wr = base + (int64_t)(cbase + li) * a.K;
-  } else if (EPI == kEpiPwa) {
+  } else if (EPI == kEpiPwa || EPI == kEpiOpm) {
     const int hd = a.O / 2;
     seg = (ot * 32) / hd;
     cbase = ot * 32 - seg * hd;
@@ -146,7 +147,7 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
     constexpr int kMaxChunks = kLnGemmMaxK / 128;
     const int r = tid >> 4, pc = tid & 15;
     const int nc = a.K / 8;
-    const bf16* xr = a.ln_x + min(m0 + r, a.M - 1) * a.K;
+    const bf16* xr = a.ln_x + (EPI == kEpiOpm ? opm_msa_row(a, m0 + r) : min(m0 + r, a.M - 1)) * a.K;
     bf16x8 xv[kMaxChunks];
 #pragma unroll
     for (int i = 0; i < kMaxChunks; ++i)
@@ -286,6 +287,22 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
         store4(a.gate + m * hd + c, y[0], y[1], y[2], y[3]);
       }
     }
+  } else if (EPI == kEpiOpm) {
+    const int64_t bj = m / a.sp;
+    const int s = (int)(m - bj * a.sp);
+    const int64_t b = bj / a.n;
+    const int j = (int)(bj - b * a.n);
+    const float keep = s < a.depth && a.rows_mask[(b * a.depth + s) * a.n + j] ? 1.f : 0.f;
+    const float* bias = seg == 0 ? a.bias0 : a.bias1;
+    bf16* dst = (seg == 0 ? a.lt : a.rt) + bj * 32 * a.sp + s;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = 8 * v + 4 * g + e;
+        dst[(int64_t)c * a.sp] = (bf16)((acc[4 * v + e] + (bias ? bias[c] : 0.f)) * keep);
+      }
+    if (seg == 0 && g == 0) a.mt[bj * a.sp + s] = (bf16)keep;
   } else if (EPI == kEpiSwiglu) {
     const int hid = a.O / 2;
 #pragma unroll
@@ -560,6 +577,8 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
     launch_row_gemm_t<kEpiResid, kXF32, 1>(a, stream);
   else if (epi == kEpiPwa && xsrc == kXLn)
     launch_row_gemm_t<kEpiPwa, kXLn, 8>(a, stream);
+  else if (epi == kEpiOpm && xsrc == kXLn)
+    launch_row_gemm_t<kEpiOpm, kXLn, 2>(a, stream);
 }
 
 void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream) {

@@ -5,7 +5,8 @@ The engine exposes ``layer_norm``, ``triangle_multiplicative_update``,
 (names: ``docs/guides/ENGINE-2.4.2.md:18-21`` of the reference; their signatures are
 not in the reference, so these are this library's own); ``attention_pair_bias`` serves
 the engine's ``single_attention`` op (``AttentionPairBias``) and
-``msa_pair_weighted_averaging`` its ``msa_pwa`` op (``MSAPairWeightedAveraging``). Each function validates its
+``msa_pair_weighted_averaging`` its ``msa_pwa`` op (``MSAPairWeightedAveraging``) and
+``outer_product_mean`` its ``opm`` op (``OuterProductMean``). Each function validates its
 tensors, allocates the output and the workspace with torch's allocator on the input's
 device, and calls the C-ABI on torch's current stream. There is no fallback: the
 module classes decide what to refuse (``unsupported``) before a call ever gets here.
@@ -322,6 +323,72 @@ def msa_pair_weighted_averaging(
         float(eps_msa), float(eps_pair), _stream(dev),
     )
     _native.check(status, "msa_pair_weighted_averaging")
+    return out
+
+
+def outer_product_mean_supported(d_msa: int, d_hidden: int, d_pair: int) -> bool:
+    """Widths the outer-product-mean kernels take."""
+    return 0 < d_msa <= 768 and d_msa % 64 == 0 and d_hidden == 32 and d_pair == PAIR_WIDTH
+
+
+def outer_product_mean(
+    m: Tensor,
+    rows_mask: Tensor,
+    *,
+    ln_weight: Tensor,
+    ln_bias: Tensor,
+    to_left: Tensor,
+    to_right: Tensor,
+    to_out: Tensor,
+    to_out_bias: Tensor,
+    left_bias: Tensor | None = None,
+    right_bias: Tensor | None = None,
+    residual: Tensor | None = None,
+    count_offset: float | None = 1e-3,
+    normalize_before_proj: bool = False,
+    eps: float = 1e-5,
+    out: Tensor | None = None,
+) -> Tensor:
+    """Outer product mean of ``m [B, S, N, c_m]`` bf16 under the MSA row mask
+    ``rows_mask [B, S, N]`` bool -> ``[B, N, N, 128]`` bf16 (plus ``residual`` when given).
+    ``count_offset`` None divides by ``max(n, 1)``, a number by ``n + count_offset``."""
+    _need(m.is_cuda and m.is_contiguous() and m.dtype == torch.bfloat16,
+          "m must be a contiguous bf16 device tensor")
+    _need(m.dim() == 4, f"m must be [B, S, N, c_m] (got {tuple(m.shape)})")
+    batch, depth, n, cm = m.shape
+    _need(rows_mask.dtype == torch.bool and tuple(rows_mask.shape) == (batch, depth, n)
+          and rows_mask.device == m.device and rows_mask.is_contiguous(),
+          "rows_mask must be a contiguous bool device tensor [B, S, N]")
+    hidden = to_left.shape[0]
+    cz = to_out.shape[0]
+    _need(outer_product_mean_supported(cm, hidden, cz),
+          f"d_msa={cm} d_hidden={hidden} d_pair={cz} (the kernels take d_msa a multiple of 64 "
+          "up to 768, d_hidden 32, d_pair 128)")
+    _need(depth > 0 and n > 0 and batch > 0, "empty MSA")
+    dev = m.device
+    names = ("ln_weight", "ln_bias", "to_left", "to_right", "to_out", "to_out_bias")
+    ln_w, ln_b, wl, wr, wo, bo = (_param(t, dev, nm) for t, nm in zip(
+        (ln_weight, ln_bias, to_left, to_right, to_out, to_out_bias), names))
+    _need(wl.shape == (hidden, cm) and wr.shape == (hidden, cm), "to_left / to_right [32, c_m]")
+    _need(wo.shape == (cz, hidden * hidden) and bo.shape == (cz,), "to_out [128, 1024] + bias [128]")
+    bl = None if left_bias is None else _param(left_bias, dev, "left_bias")
+    br = None if right_bias is None else _param(right_bias, dev, "right_bias")
+    if residual is not None:
+        _need(residual.dtype == torch.bfloat16 and residual.is_contiguous()
+              and tuple(residual.shape) == (batch, n, n, cz) and residual.device == dev,
+              "residual must be a contiguous bf16 [B, N, N, 128] device tensor")
+    lib = _native.lib()
+    ws = _workspace(lib.ffk_outer_product_mean_workspace(batch, depth, n, cm, hidden, cz), dev)
+    out = torch.empty(batch, n, n, cz, dtype=torch.bfloat16, device=dev) if out is None else out
+    status = lib.ffk_outer_product_mean(
+        m.data_ptr(), rows_mask.data_ptr(), ln_w.data_ptr(), ln_b.data_ptr(), wl.data_ptr(),
+        None if bl is None else bl.data_ptr(), wr.data_ptr(), None if br is None else br.data_ptr(),
+        wo.data_ptr(), bo.data_ptr(), None if residual is None else residual.data_ptr(),
+        out.data_ptr(), ws.data_ptr(), ws.numel(), batch, depth, n, cm, hidden, cz, float(eps),
+        -1.0 if count_offset is None else float(count_offset), int(normalize_before_proj),
+        _stream(dev),
+    )
+    _native.check(status, "outer_product_mean")
     return out
 
 

@@ -505,6 +505,93 @@ class MSAPairWeightedAveraging(EngineOp, MasterWeights, nn.Module):
         )
 
 
+class OuterProductMean(EngineOp, MasterWeights, nn.Module):
+    """Outer product mean, the raw MSA-to-pair update (``legacy/primitives.py:40-136``,
+    ``legacy/reference/attention.py:57-74``; engine factory ``modules/engine/modules.py:184-210``;
+    parameters ``legacy/released.py:227-251``). The forward returns the update alone, or
+    ``residual + update`` when ``residual=`` is given (the model owns the residual,
+    ``graph.py:303``).
+
+    ``l, r = mask * (LN(m) W^T + b)``; ``o[i, j] = sum_s l[s, i] (x) r[s, j]`` (left channel
+    major); ``n[i, j] = sum_s mask[s, i] mask[s, j]``; divisor ``n + count_offset`` or, with
+    ``count_offset=None``, ``max(n, 1)``. ``normalize_before_proj=False`` is AF3's
+    ``(o W^T + b) / d``, ``True`` is ``(o / d) W^T + b``. ``groups > 1`` (Chai-1) takes the
+    products within each of ``groups`` channel groups, normalises them with ``product_norm``
+    and divides by nothing; ``d_hidden`` is the total width of all groups.
+    """
+
+    def __init__(self, d_msa: int, d_pair: int, d_hidden: int = 32, *,
+                 normalize_before_proj: bool = True, projection_bias: bool = False,
+                 groups: int = 1, product_norm_eps: float = 0.1, count_offset: float | None = None,
+                 backend: str = "pytorch") -> None:
+        nn.Module.__init__(self)
+        if d_hidden % groups != 0:
+            raise ValueError(f"d_hidden={d_hidden} is not a multiple of groups={groups}")
+        if count_offset is not None and count_offset < 0:
+            raise ValueError(f"count_offset={count_offset} must be >= 0 (or None for the clamp)")
+        self.d_msa, self.d_pair, self.d_hidden, self.groups = d_msa, d_pair, d_hidden, groups
+        self.normalize_before_proj, self.count_offset = normalize_before_proj, count_offset
+        k = d_hidden // groups
+        self.ln_msa = LayerNorm(d_msa)
+        self.to_left = _linear(d_msa, d_hidden, bias=projection_bias)
+        self.to_right = _linear(d_msa, d_hidden, bias=projection_bias)
+        self.to_out = _linear(groups * k * k, d_pair, bias=True)
+        if groups > 1:
+            self.product_norm = LayerNorm(groups * k * k, eps=product_norm_eps)
+        self._init_backend(backend)
+
+    def _unsupported_hip(self, m: Tensor, mask: Tensor, residual: Tensor | None = None) -> str | None:
+        reason = hip_reason(m, mask)
+        if reason is not None:
+            return reason
+        if self.groups != 1:
+            return f"groups={self.groups} (the kernels take one group)"
+        if m.dtype != torch.bfloat16:
+            return f"{m.dtype} MSA activations (the kernels take bf16)"
+        if m.dim() != 4 or m.shape[3] != self.d_msa:
+            return f"MSA shape {tuple(m.shape)} (expected [B, S, N, {self.d_msa}])"
+        if mask.dtype != torch.bool or tuple(mask.shape) != tuple(m.shape[:3]):
+            return f"row mask {tuple(mask.shape)} {mask.dtype} (expected bool {tuple(m.shape[:3])})"
+        if min(m.shape[:3]) == 0:
+            return "empty MSA"
+        if residual is not None and (residual.dtype != torch.bfloat16
+                                     or tuple(residual.shape) != (m.shape[0], m.shape[2], m.shape[2], self.d_pair)):
+            return f"residual {tuple(residual.shape)} {residual.dtype}"
+        from foldforge_amd.kernels import outer_product_mean_supported
+
+        if not outer_product_mean_supported(self.d_msa, self.d_hidden, self.d_pair):
+            return (f"d_msa={self.d_msa} d_hidden={self.d_hidden} d_pair={self.d_pair} (the kernels "
+                    "take d_msa a multiple of 64 up to 768, d_hidden 32, d_pair 128)")
+        return None
+
+    def _forward_pytorch(self, m: Tensor, mask: Tensor, residual: Tensor | None = None) -> Tensor:
+        if self.dead:
+            return residual if residual is not None else torch.zeros(
+                *m.shape[:1], m.shape[2], m.shape[2], self.d_pair, dtype=m.dtype, device=m.device)
+        return torch_ops.outer_product_mean(self, m, mask, residual=residual)
+
+    def _forward_hip(self, m: Tensor, mask: Tensor, residual: Tensor | None = None) -> Tensor:
+        if self.dead:
+            return self._forward_pytorch(m, mask, residual)
+        from foldforge_amd import kernels
+
+        return kernels.outer_product_mean(
+            m.contiguous(), mask.contiguous(), ln_weight=self.ln_msa.weight,
+            ln_bias=self.ln_msa.bias, to_left=self.to_left.weight, to_right=self.to_right.weight,
+            to_out=self.to_out.weight, to_out_bias=self.to_out.bias, left_bias=self.to_left.bias,
+            right_bias=self.to_right.bias,
+            residual=None if residual is None else residual.contiguous(),
+            count_offset=self.count_offset, normalize_before_proj=self.normalize_before_proj,
+            eps=self.ln_msa.eps,
+        )
+
+    def delta(self, m: Tensor, mask: Tensor, residual: Tensor | None = None) -> Tensor:
+        """The update alone (what the forward returns without ``residual``)."""
+        reason = self.unsupported(m, mask)
+        backend = "pytorch" if reason is not None else self.backend
+        return getattr(self, f"_forward_{backend}")(m, mask)
+
+
 # ------------------------------------------------------------------------------------ block
 @dataclass(frozen=True)
 class PairformerConfig:

@@ -151,3 +151,31 @@ def msa_pair_weighted_averaging(m_, msa: Tensor, z: Tensor, mask: Tensor, *,
     o = torch.where((~keep.any(dim=-1))[:, None, None, None], torch.zeros_like(o), o)
     y = _lin(torch.sigmoid(_lin(x, m_.to_gate.weight)) * o, m_.to_out.weight)
     return (m + y if residual else y).to(dtype)
+
+
+def outer_product_mean(m_, msa: Tensor, mask: Tensor, *, residual: Tensor | None = None) -> Tensor:
+    """``m_``: an OuterProductMean module; ``msa [B, S, N, c_m]``, row mask ``[B, S, N]``
+    (``legacy/primitives.py:80-136``, ``legacy/reference/attention.py:57-74``)."""
+    dtype = msa.dtype
+    batch, depth, n, _ = msa.shape
+    x = _ln(msa.float(), m_.ln_msa.weight, m_.ln_msa.bias, m_.ln_msa.eps)
+    keep = mask.to(torch.float32)
+    left = _lin(x, m_.to_left.weight, m_.to_left.bias) * keep[..., None]
+    right = _lin(x, m_.to_right.weight, m_.to_right.bias) * keep[..., None]
+    if m_.groups == 1:
+        o = torch.einsum("bsic,bsje->bijce", left, right).reshape(batch, n, n, -1)
+        count = torch.einsum("bsi,bsj->bij", keep, keep)[..., None]
+        d = count.clamp_min(1.0) if m_.count_offset is None else count + m_.count_offset
+        if m_.normalize_before_proj:
+            y = _lin(o / d, m_.to_out.weight, m_.to_out.bias)
+        else:
+            y = _lin(o, m_.to_out.weight, m_.to_out.bias) / d
+    else:
+        g = m_.groups
+        o = torch.einsum("bsigc,bsjge->bijgce", left.unflatten(-1, (g, -1)),
+                         right.unflatten(-1, (g, -1))).reshape(batch, n, n, -1)
+        pn = m_.product_norm
+        y = _lin(_ln(o, pn.weight, pn.bias, pn.eps), m_.to_out.weight, m_.to_out.bias)
+    if residual is not None:
+        y = residual.float() + y
+    return y.to(dtype)

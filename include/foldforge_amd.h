@@ -183,6 +183,35 @@ int32_t ffk_msa_pair_weighted_averaging(
     int64_t batch, int64_t depth, int64_t n, int32_t d_msa, int32_t d_pair, int32_t n_head,
     int32_t d_head, int32_t residual, float eps_msa, float eps_pair, void* stream);
 
+/* Outer product mean (the MSA-to-pair update), raw or added to a residual.
+ * m [batch][depth][n][d_msa] bf16, rows_mask [batch][depth][n] (0 / 1 bytes: which MSA
+ * entries are real), residual (NULL, or [batch][n][n][d_pair] bf16; may alias out),
+ * out [batch][n][n][d_pair] bf16:
+ *   l = mask (LN(m) W_left^T + b_left), r = mask (LN(m) W_right^T + b_right)  (d_hidden each)
+ *   o[i][j] = sum_s l[s][i] (x) r[s][j]  (flattened left-channel-major: c * d_hidden + e)
+ *   count[i][j] = sum_s mask[s][i] mask[s][j]
+ *   d = count + count_offset (count_offset >= 0: AF3's n + 1e-3) or max(count, 1) (< 0)
+ *   out = residual + ((o W_out^T + b_out) / d)        normalize_before_proj = 0
+ *   out = residual + ((o / d) W_out^T + b_out)        normalize_before_proj = 1
+ * Weights fp32: w_left / w_right [d_hidden][d_msa], b_left / b_right [d_hidden] or NULL,
+ * w_out [d_pair][d_hidden^2], b_out [d_pair]. Served: d_hidden 32, d_pair 128, d_msa a
+ * multiple of 64 up to 768, depth >= 1; anything else returns FFK_ERR_INVALID.
+ * Replaces: engine OuterProductMean.forward, op name "opm"
+ * (src/foldforge/modules/engine/backends.py:48; factory modules.py:184-210; equations
+ * src/foldforge/models/checkpoints/legacy/primitives.py:40-136 and
+ * legacy/reference/attention.py:57-74; engine parameters legacy/released.py:227-251; called as
+ * graph.py:303).
+ */
+size_t ffk_outer_product_mean_workspace(int64_t batch, int64_t depth, int64_t n, int32_t d_msa,
+                                        int32_t d_hidden, int32_t d_pair);
+int32_t ffk_outer_product_mean(
+    const void* m, const uint8_t* rows_mask, const float* ln_w, const float* ln_b,
+    const float* w_left, const float* b_left, const float* w_right, const float* b_right,
+    const float* w_out, const float* b_out, const void* residual, void* out, void* workspace,
+    size_t workspace_bytes, int64_t batch, int64_t depth, int64_t n, int32_t d_msa,
+    int32_t d_hidden, int32_t d_pair, float eps, float count_offset,
+    int32_t normalize_before_proj, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

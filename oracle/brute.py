@@ -10,7 +10,7 @@ Equations (reference paths as in ``oracle/pairstack.py``):
 ``legacy/reference/triangle.py:39-49``, ``legacy/attention.py:108-163``,
 ``legacy/reference/attention.py:96-101``, ``legacy/reference/transition.py:40-41``,
 ``legacy/transformer.py:93-137``, ``legacy/attention.py:203-223`` (MSA pair-weighted
-averaging).
+averaging), ``legacy/primitives.py:80-156`` (outer product mean).
 """
 
 from __future__ import annotations
@@ -216,4 +216,53 @@ def msa_pair_weighted_averaging(m, z, mask, p, *, n_head: int, eps: float = 1e-5
                 y = _matvec(p["to_out.weight"], gated)
                 for ch in range(cm):
                     out[b, s, i, ch] += y[ch]
+    return out
+
+
+def outer_product_mean(m, rows_mask, p, *, count_offset=1e-3, normalize_before_proj=False,
+                       groups: int = 1, eps: float = 1e-5, product_norm_eps: float = 0.1):
+    """Outer product mean (raw update), fp64 loops. ``to_out.weight`` column ``g K K + c K + e``
+    multiplies the product of left channel ``g K + c`` and right channel ``g K + e``."""
+    batch, depth, n, _ = m.shape
+    hidden = len(p["to_left.weight"])
+    k = hidden // groups
+    cz = len(p["to_out.weight"])
+    bl, br = p.get("to_left.bias"), p.get("to_right.bias")
+    out = np.zeros((batch, n, n, cz))
+    for b in range(batch):
+        left = [[None] * n for _ in range(depth)]
+        right = [[None] * n for _ in range(depth)]
+        for s in range(depth):
+            for i in range(n):
+                x = layer_norm_vec(m[b, s, i], p["ln_msa.weight"], p["ln_msa.bias"], eps)
+                keep = 1.0 if bool(rows_mask[b, s, i]) else 0.0
+                lv = _matvec(p["to_left.weight"], x)
+                rv = _matvec(p["to_right.weight"], x)
+                left[s][i] = [keep * (lv[c] + (bl[c] if bl is not None else 0.0)) for c in range(hidden)]
+                right[s][i] = [keep * (rv[c] + (br[c] if br is not None else 0.0)) for c in range(hidden)]
+        for i in range(n):
+            for j in range(n):
+                o = [0.0] * (groups * k * k)
+                for g in range(groups):
+                    for c in range(k):
+                        for e in range(k):
+                            o[g * k * k + c * k + e] = sum(left[s][i][g * k + c] * right[s][j][g * k + e]
+                                                           for s in range(depth))
+                if groups > 1:
+                    o = layer_norm_vec(o, p["product_norm.weight"], p["product_norm.bias"], product_norm_eps)
+                    y = _matvec(p["to_out.weight"], o)
+                    for f in range(cz):
+                        out[b, i, j, f] = y[f] + p["to_out.bias"][f]
+                    continue
+                cnt = sum((1.0 if bool(rows_mask[b, s, i]) else 0.0) * (1.0 if bool(rows_mask[b, s, j]) else 0.0)
+                          for s in range(depth))
+                d = max(cnt, 1.0) if count_offset is None else cnt + count_offset
+                if normalize_before_proj:
+                    y = _matvec(p["to_out.weight"], [v / d for v in o])
+                    for f in range(cz):
+                        out[b, i, j, f] = y[f] + p["to_out.bias"][f]
+                else:
+                    y = _matvec(p["to_out.weight"], o)
+                    for f in range(cz):
+                        out[b, i, j, f] = (y[f] + p["to_out.bias"][f]) / d
     return out

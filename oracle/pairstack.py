@@ -37,6 +37,10 @@ Reference equations followed (paths relative to the reference tree):
 * MSA pair-weighted averaging: ``legacy/attention.py:174-229`` (``MSAAttention``; engine
   names ``legacy/released.py:253-278``, the pair norm's offset dropped), called with the
   engine's column key mask ``[B, N]`` (``src/foldforge/modules/engine/graph.py:295-305``).
+* Outer product mean: ``legacy/primitives.py:80-156`` and
+  ``legacy/reference/attention.py:57-74`` (AF3's released contraction and divisor), with the
+  engine's forms (``src/foldforge/modules/engine/modules.py:184-210``) and names
+  (``legacy/released.py:227-251``); returns the raw update.
 
 The engine takes a ``[B, N]`` key mask (``src/foldforge/modules/engine/graph.py:214-218``)
 where the legacy graph takes the outer-product pair mask; the two agree on valid
@@ -288,6 +292,65 @@ def msa_pair_weighted_averaging(
     o = torch.where(empty[:, None, None, None], torch.zeros_like(o), o)
     gate = torch.sigmoid(x @ _p(params, "to_gate.weight", dtype).T)
     return m + (gate * o) @ _p(params, "to_out.weight", dtype).T
+
+
+def outer_product_mean(
+    m: Tensor,
+    rows_mask: Tensor,
+    params: Params,
+    *,
+    count_offset: float | None = 1e-3,
+    normalize_before_proj: bool = False,
+    groups: int = 1,
+    eps: float = 1e-5,
+    product_norm_eps: float = 0.1,
+    dtype: torch.dtype = torch.float32,
+) -> Tensor:
+    """Outer product mean, the raw update ``[B, N, N, c_z]`` (no residual).
+
+    Follows the dense module of ``legacy/primitives.py:80-136`` one batch element at a time,
+    with the engine's ``to_out.weight [c_z, G K K]`` turned back into the released
+    ``output_w [(G,) K, K, c_z]`` (the inverse of ``legacy/released.py:248``):
+    ``left / right = mask * (LN(m) W^T + b)`` (``primitives.py:83-86``); ungrouped, AF3's
+    contraction and divisor of ``legacy/reference/attention.py:71-74`` (``count_offset`` =
+    AF3's 1e-3, bias before the divide), the clamp ``max(n, 1)`` when ``count_offset`` is
+    None, and the bias after the divide for ``normalize_before_proj`` (``primitives.py:
+    123-132``); grouped (``primitives.py:138-156``): products within each group, summed over
+    the MSA rows, ``product_norm``, projection, no divide.
+    """
+    m = m.detach().to("cpu", dtype)
+    keep_all = rows_mask.detach().to("cpu", dtype)
+    batch, depth, n, _ = m.shape
+    x = layer_norm(m, _p(params, "ln_msa.weight", dtype), _p(params, "ln_msa.bias", dtype), eps)
+    wl, wr = _p(params, "to_left.weight", dtype), _p(params, "to_right.weight", dtype)
+    bl = _p(params, "to_left.bias", dtype) if "to_left.bias" in params else None
+    br = _p(params, "to_right.bias", dtype) if "to_right.bias" in params else None
+    wo, bo = _p(params, "to_out.weight", dtype), _p(params, "to_out.bias", dtype)
+    cz = wo.shape[0]
+    k = wl.shape[0] // groups
+    out = []
+    for b in range(batch):
+        mask = keep_all[b][..., None]  # [S, N, 1]
+        left = x[b] @ wl.T + (0 if bl is None else bl)
+        right = x[b] @ wr.T + (0 if br is None else br)
+        left, right = mask * left, mask * right
+        if groups > 1:
+            lg, rg = left.unflatten(-1, (groups, k)), right.unflatten(-1, (groups, k))
+            product = torch.einsum("sigk,sjgl->ijgkl", lg, rg).flatten(-3)
+            product = layer_norm(product, _p(params, "product_norm.weight", dtype),
+                                 _p(params, "product_norm.bias", dtype), product_norm_eps)
+            out.append(product @ wo.T.reshape(groups * k * k, cz) + bo)
+            continue
+        output_w = wo.T.reshape(k, k, cz)
+        outer = torch.einsum("acb,ade->dceb", left.permute(0, 2, 1), right)
+        output = torch.einsum("dceb,cef->dbf", outer, output_w)
+        norm = torch.einsum("abc,adc->bdc", mask, mask)
+        divisor = norm.clamp_min(1.0) if count_offset is None else norm + count_offset
+        if normalize_before_proj:
+            out.append(output.permute(1, 0, 2) / divisor + bo)
+        else:
+            out.append((output + bo).permute(1, 0, 2) / divisor)
+    return torch.stack(out)
 
 
 def sub_params(params: Params, prefix: str) -> dict[str, Tensor]:

@@ -54,9 +54,10 @@ def test_names_and_aliases():
 def test_serves_is_derived_from_the_classes():
     table = backends.SERVES
     assert set(table) == set(backends.OPS)
-    for op in ("trimul", "triangle_attention", "transition", "layernorm", "single_attention"):
+    for op in ("trimul", "triangle_attention", "transition", "layernorm", "single_attention",
+               "msa_pwa", "opm"):
         assert table[op] == ("miniworld", "pytorch", "hip"), op
-    assert table["opm"] == ()  # named, no class in this build
+    assert table["dit_blocks"] == ()  # named, no class in this build
 
 
 def test_choose_backend(monkeypatch):
@@ -282,6 +283,50 @@ def test_msa_pair_weighted_averaging_class_contract_and_pytorch_backend():
     want = ps.msa_pair_weighted_averaging(msa, z, mask, m.state_dict(), n_head=8, dtype=torch.float64)
     torch.testing.assert_close(got.double(), want, atol=2e-5, rtol=2e-5)
     torch.testing.assert_close(m(msa, z, mask), msa + m.delta(msa, z, mask))
+
+
+@pytest.mark.parametrize("form", [
+    dict(count_offset=1e-3, normalize_before_proj=False),
+    dict(count_offset=None, normalize_before_proj=True, projection_bias=True),
+    dict(count_offset=None, normalize_before_proj=False, groups=2),
+])
+def test_outer_product_mean_class_contract_and_pytorch_backend(form):
+    groups = form.get("groups", 1)
+    hidden = 8 if groups > 1 else 4
+    m = randomise(factories.outer_product_mean(16, 24, hidden, precision="fp32", **form), 8)
+    keys = set(m.state_dict())
+    want_keys = {"ln_msa.weight", "ln_msa.bias", "to_left.weight", "to_right.weight",
+                 "to_out.weight", "to_out.bias"}
+    if form.get("projection_bias"):
+        want_keys |= {"to_left.bias", "to_right.bias"}
+    if groups > 1:
+        want_keys |= {"product_norm.weight", "product_norm.bias"}
+    assert keys == want_keys
+    k = hidden // groups
+    assert m.to_out.weight.shape == (24, groups * k * k)
+    assert backends.op_of(m) == "opm"
+    torch.manual_seed(9)
+    msa = torch.randn(2, 5, 7, 16)
+    rows = torch.rand(2, 5, 7) > 0.3
+    rows[1, :, -1] = False
+    got = m(msa, rows)
+    oracle_form = {k_: v for k_, v in form.items() if k_ != "projection_bias"}
+    want = ps.outer_product_mean(msa, rows, m.state_dict(), dtype=torch.float64, **oracle_form)
+    torch.testing.assert_close(got.double(), want, atol=2e-5, rtol=2e-5)
+    pair = torch.randn(2, 7, 7, 24)
+    torch.testing.assert_close(m(msa, rows, residual=pair), pair + m.delta(msa, rows))
+    assert m.unsupported(msa, rows) is None  # pytorch serves every form
+
+
+def test_outer_product_mean_hip_refusals():
+    m = factories.outer_product_mean(64, 128, 32, groups=1)
+    m.set_backend("hip")
+    msa = torch.randn(1, 3, 5, 64).bfloat16()
+    rows = torch.ones(1, 3, 5, dtype=torch.bool)
+    assert "device" in (m.unsupported(msa, rows) or "")  # a CPU tensor is not served
+    g = factories.outer_product_mean(64, 128, 32, groups=4)
+    g.set_backend("hip")
+    assert g.unsupported(msa, rows) is not None
 
 
 def test_pytorch_backend_block_and_run_block_match_oracle():

@@ -64,6 +64,10 @@ def test_workspace_sizes_follow_the_layouts(lib):
     tokens = up(b * n * 384 * 2)
     assert apb == 3 * tokens + up(b * n * 384 * 4) + up(b * 384 * np32 * 2) + up(b * 16 * n * np32 * 4)
     assert lib.ffk_attention_pair_bias_workspace(b, 0, 384, 128, 16) == 0
+    depth, sp = 45, 64
+    opm = lib.ffk_outer_product_mean_workspace(b, depth, n, 64, 32, 128)
+    assert opm == 2 * up(b * n * 32 * sp * 2) + up(b * n * sp * 2) + up(b * n * n * 4) + up(128 * 1024 * 2)
+    assert lib.ffk_outer_product_mean_workspace(b, 0, n, 64, 32, 128) == 0
     assert lib.ffk_triangle_multiplication_workspace(0, n, 128, 128) == 0
 
 

@@ -303,6 +303,85 @@ def test_msa_pair_weighted_averaging_closed_forms():
     torch.testing.assert_close(b, a[:, perm])
 
 
+def _opm_params(cm: int, hidden: int, cz: int, seed: int, *, groups: int = 1,
+                bias: bool = False) -> dict[str, torch.Tensor]:
+    k = hidden // groups
+    shapes = {"ln_msa.weight": (cm,), "ln_msa.bias": (cm,), "to_left.weight": (hidden, cm),
+              "to_right.weight": (hidden, cm), "to_out.weight": (cz, groups * k * k),
+              "to_out.bias": (cz,)}
+    if bias:
+        shapes |= {"to_left.bias": (hidden,), "to_right.bias": (hidden,)}
+    if groups > 1:
+        shapes |= {"product_norm.weight": (groups * k * k,), "product_norm.bias": (groups * k * k,)}
+    return _rand_params(shapes, seed)
+
+
+def _opm_inputs(batch: int, depth: int, n: int, cm: int, seed: int):
+    g = torch.Generator().manual_seed(seed)
+    m = torch.randn(batch, depth, n, cm, generator=g, dtype=F64)
+    rows = torch.rand(batch, depth, n, generator=g) > 0.25
+    rows[:, 0] = True
+    return m, rows
+
+
+@pytest.mark.parametrize("form", [
+    dict(count_offset=1e-3, normalize_before_proj=False),
+    dict(count_offset=None, normalize_before_proj=False),
+    dict(count_offset=None, normalize_before_proj=True),
+    dict(count_offset=1e-3, normalize_before_proj=True),
+    dict(count_offset=None, normalize_before_proj=False, groups=2),
+])
+@pytest.mark.parametrize("bias", [False, True])
+def test_outer_product_mean_matches_brute_force(form, bias):
+    depth, n, cm, hidden, cz = 3, 4, 6, 4, 5
+    groups = form.get("groups", 1)
+    p = _opm_params(cm, hidden, cz, 101, groups=groups, bias=bias)
+    m, rows = _opm_inputs(2, depth, n, cm, 102)
+    rows[1, :, 2] = False  # a token with no MSA entry: count 0
+    got = ps.outer_product_mean(m, rows, p, dtype=F64, **form)
+    want = brute.outer_product_mean(m.numpy(), rows.numpy(), _np(p), **form)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+
+
+def test_outer_product_mean_closed_forms():
+    """A mean over MSA rows: with the divisor n (offset 0) repeating every MSA row leaves the
+    output unchanged and a masked row adds nothing; one MSA row gives the outer product of its
+    two projections, flattened left channel first (a single nonzero output weight picks
+    left channel c times right channel e); the AF3 form puts the bias before the divide."""
+    depth, n, cm, hidden, cz = 3, 5, 8, 4, 3
+    p = _opm_params(cm, hidden, cz, 103)
+    m, rows = _opm_inputs(1, depth, n, cm, 104)
+    mean = dict(count_offset=0.0, normalize_before_proj=True)
+    base = ps.outer_product_mean(m, rows, p, dtype=F64, **mean)
+    twice = ps.outer_product_mean(torch.cat([m, m], 1), torch.cat([rows, rows], 1), p,
+                                  dtype=F64, **mean)
+    torch.testing.assert_close(twice, base)
+    # the AF3 form divides the bias too: repeating the rows scales the bias term by 1 / 2
+    af3_1 = ps.outer_product_mean(m, rows, p, count_offset=0.0, dtype=F64)
+    af3_2 = ps.outer_product_mean(torch.cat([m, m], 1), torch.cat([rows, rows], 1), p,
+                                  count_offset=0.0, dtype=F64)
+    count = torch.einsum("bsi,bsj->bij", rows.double(), rows.double())[..., None]
+    torch.testing.assert_close(af3_1 - af3_2, p["to_out.bias"] / (2 * count))
+    extra = torch.zeros(1, 1, n, dtype=torch.bool)
+    padded = ps.outer_product_mean(torch.cat([m, torch.randn(1, 1, n, cm, dtype=F64)], 1),
+                                   torch.cat([rows, extra], 1), p, dtype=F64, **mean)
+    torch.testing.assert_close(padded, base)
+
+    one = torch.ones(1, 1, n, dtype=torch.bool)
+    x = F.layer_norm(m[:, :1], (cm,), p["ln_msa.weight"], p["ln_msa.bias"], 1e-5)[0, 0]
+    left, right = x @ p["to_left.weight"].T, x @ p["to_right.weight"].T
+    c, e = 1, 3
+    q = dict(p)
+    q["to_out.weight"] = torch.zeros(cz, hidden * hidden, dtype=F64)
+    q["to_out.weight"][0, c * hidden + e] = 1.0
+    q["to_out.bias"] = torch.zeros(cz, dtype=F64)
+    got = ps.outer_product_mean(m[:, :1], one, q, count_offset=0.0, dtype=F64)[0, :, :, 0]
+    torch.testing.assert_close(got, torch.outer(left[:, c], right[:, e]))
+    af3 = ps.outer_product_mean(m[:, :1], one, p, count_offset=1e-3, dtype=F64)
+    plain = ps.outer_product_mean(m[:, :1], one, p, count_offset=0.0, dtype=F64)
+    torch.testing.assert_close(af3, plain / (1 + 1e-3))
+
+
 def test_block_is_the_composition_of_the_pinned_ops():
     n, c, h, heads, d, cs, hs = 5, 6, 4, 2, 3, 6, 2
     params = {}

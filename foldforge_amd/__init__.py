@@ -14,12 +14,15 @@ __version__ = "0.1.0"
 
 def load(name: str = "pairformer-trunk", checkpoint=None, *, backend: str = "miniworld",
          dtype=None, device="cuda", blocks: int = 48, seed: int = 0, d_single: int = 384,
-         engine_ops=None, unsupported: str = "fallback", out_scale: float | None = 0.25):
+         engine_ops=None, unsupported: str = "fallback", out_scale: float | None = 0.25,
+         family: str = "alphafold3"):
     """A configured trunk on ``device`` with ``backend`` applied to every op module.
 
-    ``checkpoint``: a ``.safetensors`` file or a weights-only torch state dict in the
-    engine's keys (``blocks.<i>.tri_multi_outgoing.to_left.weight`` ...); without one the
-    parameters are seeded random init (:func:`foldforge_amd.trunk.randomise`).
+    ``checkpoint``: a miniworld-format file (``*.miniworld.pt`` of ``family``; a whole-model
+    file contributes its ``evoformer.trunk_pairformer.<i>`` blocks), a ``.safetensors`` file or
+    a weights-only torch state dict in the trunk's keys
+    (``blocks.<i>.tri_multi_outgoing.to_left.weight`` ...); without one the parameters are
+    seeded random init (:func:`foldforge_amd.trunk.randomise`).
     """
     import torch
 
@@ -37,13 +40,23 @@ def load(name: str = "pairformer-trunk", checkpoint=None, *, backend: str = "min
         randomise(model, seed, out_scale=out_scale)
     else:
         path = str(checkpoint)
-        if path.endswith(".safetensors"):
+        if path.endswith(".miniworld.pt"):
+            from foldforge_amd import checkpoint as ckpt
+
+            blob = ckpt.read(path)
+            whole = any(k.startswith(ckpt.TRUNK_PREFIX + ".") for k in blob["state_dict"])
+            ckpt.load_into(model, blob, family=family,
+                           prefix=ckpt.TRUNK_PREFIX if whole else None,
+                           renumber_as="blocks" if whole else None)
+            state = None
+        elif path.endswith(".safetensors"):
             from safetensors.torch import load_file
 
             state = load_file(path)
         else:
             state = torch.load(path, map_location="cpu", weights_only=True)
-        model.load_state_dict(state, strict=True)
+        if state is not None:
+            model.load_state_dict(state, strict=True)
     device = torch.device(device)
     configure_model(model, dtype, device)
     plan.resolve(device)

@@ -684,3 +684,80 @@ class PairformerBlock(MasterWeights, nn.Module):
             s = self.single_attention(single, source, key_mask, bias)
             s = self.single_transition(s)
         return pair_out, s
+
+
+class MSABlock(MasterWeights, nn.Module):
+    """One MSA-stack block composed of the op classes (the reference's engine graph builds it
+    the same way, ``src/foldforge/modules/engine/graph.py:240-340``; the engine has no MSA
+    block class): outer product mean -> MSA pair-weighted averaging -> MSA transition (or the
+    Boltz order, ``msa_first``), then the pair track (two triangle multiplications, two
+    triangle attentions when ``with_pair_attention``, the transition). Every part owns its
+    residual except the outer product mean, whose raw update is added here. ``parallel`` is
+    Chai-1's block (every update of a stage reads the stage's input, ``graph.py:316-340``).
+
+    ``block(msa [M, L, c_m], pair [L, L, c_z], msa_mask [M, L], pair_mask [L, L])`` ->
+    ``(msa, pair)``: unbatched, like the reference's block; MSA rows are real where
+    ``msa_mask > 0``, a token column is a key when any row has it, and the token mask is the
+    pair mask's diagonal.
+    """
+
+    backends = ("pytorch",)
+
+    def __init__(self, c_msa: int, c_pair: int, n_heads_pair: int = 4, *,
+                 msa_value_dim: int | None = None, with_pair_attention: bool = True,
+                 triangle_model: str = "af3", msa_first: bool = False, parallel: bool = False,
+                 opm_channel: int = 32, opm_groups: int = 1, opm_projection_bias: bool = False,
+                 opm_normalize_before_proj: bool = False,
+                 opm_count_offset: float | None = 1e-3) -> None:
+        super().__init__()
+        if parallel and msa_first:
+            raise ValueError("a parallel MSA block runs the outer product mean first")
+        self.msa_first, self.parallel, self.with_pair_attention = msa_first, parallel, with_pair_attention
+        self.outer_product_mean = OuterProductMean(
+            c_msa, c_pair, opm_channel * opm_groups, groups=opm_groups,
+            projection_bias=opm_projection_bias, normalize_before_proj=opm_normalize_before_proj,
+            count_offset=None if opm_groups > 1 else opm_count_offset)
+        self.msa_attention1 = MSAPairWeightedAveraging(c_msa, c_pair, 8, msa_value_dim)
+        self.msa_transition = Transition(c_msa, 4)
+        self.triangle_multiplication_outgoing = TriangleMultiplication(c_pair, outgoing=True)
+        self.triangle_multiplication_incoming = TriangleMultiplication(c_pair, outgoing=False)
+        if with_pair_attention:
+            self.pair_attention1 = TriangleAttention(c_pair, n_heads_pair, starting=True, model=triangle_model)
+            self.pair_attention2 = TriangleAttention(c_pair, n_heads_pair, starting=False, model=triangle_model)
+        self.pair_transition = Transition(c_pair, 4)
+        self.backend = "pytorch"
+
+    def children_ops(self) -> list[nn.Module]:
+        return [m for m in self.children() if isinstance(m, EngineOp)]
+
+    def set_backend(self, name: str) -> None:
+        self.backend = "pytorch"
+        for m in self.children_ops():
+            m.set_backend(name if name in m.backends else "pytorch")
+
+    def forward(self, msa: Tensor, pair: Tensor, msa_mask: Tensor, pair_mask: Tensor):
+        m, z = msa[None], pair[None]
+        rows = (msa_mask > 0)[None].contiguous()
+        columns = (msa_mask.max(dim=0).values > 0)[None].contiguous()
+        tokens = (pair_mask.diagonal(dim1=-2, dim2=-1) > 0)[None].contiguous()
+        if self.parallel:
+            z = self.outer_product_mean(m, rows, residual=z)
+            m = m + self.msa_attention1.delta(m, z, columns) + self.msa_transition.delta(m)
+            z = z + (self.triangle_multiplication_outgoing.delta(z, tokens)
+                     + self.triangle_multiplication_incoming.delta(z, tokens)
+                     + self.pair_transition.delta(z))
+            if self.with_pair_attention:
+                z = z + self.pair_attention1.delta(z, tokens) + self.pair_attention2.delta(z, tokens)
+            return m[0], z[0]
+        if self.msa_first:
+            m = self.msa_transition(self.msa_attention1(m, z, columns))
+        z = self.outer_product_mean(m, rows, residual=z)
+        if not self.msa_first:
+            m = self.msa_transition(self.msa_attention1(m, z, columns))
+        z = self.triangle_multiplication_outgoing(z, tokens)
+        z = self.triangle_multiplication_incoming(z, tokens)
+        if self.with_pair_attention:
+            z = self.pair_attention1(z, tokens)
+            z = self.pair_attention2(z, tokens)
+        z = self.pair_transition(z)
+        return m[0], z[0]

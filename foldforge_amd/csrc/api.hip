@@ -639,7 +639,8 @@ int32_t ffk_msa_pair_weighted_averaging(
       d_head <= 0 || d_head % 4 != 0 || hd % 64 != 0)
     return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: d_msa=%d heads=%d x %d (kernels take d_msa a multiple of 64 up to %d, at most 32 heads, d_head a multiple of 4, heads * d_head a multiple of 64)", d_msa, n_head, d_head, kLnGemmMaxK);
   if (batch <= 0 || depth <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: empty shape");
-  if (batch * n_head > 65535 || (n + 63) / 64 > 65535 || (depth * d_head + 127) / 128 > 0x7fffffffLL)
+  if ((depth * d_head + 127) / 128 * ((n + 127) / 128) * batch * n_head > 0x7fffffffLL ||
+      batch * n_head * n > 0x7fffffffLL * 4)
     return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: shape exceeds the launch grid");
   if (!m || !z || !key_mask || !ln_msa_w || !ln_msa_b || !ln_pair_w || !w_bias || !w_value ||
       !w_gate || !w_out || !out)

@@ -52,64 +52,117 @@ __global__ __launch_bounds__(256) void pwa_softmax(PwaSoftmaxArgs a) {
   }
 }
 
-// grid (ceil(S dh / 128), ceil(n / 64), batch * heads); block 256: wave w computes rows
-// 32 w .. 32 w + 31 of the workgroup's 128 (s, c) rows for its 64 queries (two 32 x 32 MFMA
-// tiles sharing the A operand). A = v^T rows, B = weight rows, both key-contiguous; keys are
-// consumed in groups of 64, lane half g taking keys 64 kg + 32 g + 8 t .. + 7 for step t.
-// Epilogue: lane (li, g) holds query q0 + li (or + 32) and rows r = r0 + 8 v + 4 g + e, i.e.
-// (s, c) = (r / dh, r % dh): four consecutive channels of one MSA row.
+constexpr int kPT = 128;         // output tile: 128 (s, c) rows x 128 queries
+constexpr int kPK = 32;          // keys per LDS stage
+constexpr int kPKP = kPK + 8;    // LDS row stride (80 B: conflict-free 16-byte reads)
+
+// Per (batch, head): O[(s, c)][i] = sum_j v^T[(s, c)][j] w[i][j], an NT GEMM with both operands
+// key-contiguous. grid: ceil(S dh / 128) * ceil(n / 128) * batch * heads workgroups (renumbered
+// so that neighbours share an XCD's L2), block 256 = 2 x 2 waves of 64 x 64; operands staged
+// through LDS 32 keys at a time (register prefetch, double buffer, one barrier per stage).
+// v^T is not written at keys >= n: those operand entries are zeroed as they are staged.
+// Epilogue: lane (li, g) holds query q0' + li and rows r = r0' + 8 v + 4 g + e, i.e.
+// (s, c) = (r / dh, r % dh): four consecutive channels of one MSA row (dh % 4 == 0).
 __global__ __launch_bounds__(256) void pwa_average(PwaAverageArgs a) {
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
-  const int64_t bh = blockIdx.z;
+  __shared__ __attribute__((aligned(16))) bf16 xs[2][kPT * kPKP];
+  __shared__ __attribute__((aligned(16))) bf16 ys[2][kPT * kPKP];
+  const int rows = a.depth * a.dh, n = a.n, np = a.np;
+  const int rt = (rows + kPT - 1) / kPT, qt = (n + kPT - 1) / kPT;
+  const uint32_t wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t bh = wg / ((uint32_t)rt * qt);
+  const int rem = (int)(wg - bh * rt * qt);
+  const int r0 = (rem / qt) * kPT, q0 = (rem % qt) * kPT;
   const int64_t b = bh / a.heads;
   const int h = (int)(bh - b * a.heads);
-  const int rows = a.depth * a.dh, n = a.n, np = a.np;
-  const int r0 = blockIdx.x * 128 + 32 * wave;
-  if (r0 >= rows) return;  // no barrier in this kernel
-  const int q0 = blockIdx.y * 64;
-  const bf16* arow = a.vt + (bh * rows + min(r0 + li, rows - 1)) * np + 32 * g;
-  const bf16* b0row = a.w + (bh * n + min(q0 + li, n - 1)) * np + 32 * g;
-  const bf16* b1row = a.w + (bh * n + min(q0 + 32 + li, n - 1)) * np + 32 * g;
-  f32x16 acc0 = zero16(), acc1 = zero16();
-  for (int k0 = 0; k0 < np; k0 += 64) {
-    bf16x8 af[4], bf0[4], bf1[4];
+  const bf16* X = a.vt + bh * rows * (int64_t)np;
+  const bf16* Y = a.w + bh * n * (int64_t)np;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, g = lane >> 5;
+
+  const bf16* xsrc[2];
+  const bf16* ysrc[2];
+  int soff[2], kcol[2];
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      af[t] = ld8(arow + k0 + 8 * t);
-      bf0[t] = ld8(b0row + k0 + 8 * t);
-      bf1[t] = ld8(b1row + k0 + 8 * t);
+  for (int u = 0; u < 2; ++u) {
+    const int c = tid + 256 * u;
+    const int row = c >> 2, kc = (c & 3) * 8;
+    xsrc[u] = X + (int64_t)min(r0 + row, rows - 1) * np + kc;
+    ysrc[u] = Y + (int64_t)min(q0 + row, n - 1) * np + kc;
+    soff[u] = row * kPKP + kc;
+    kcol[u] = kc;
+  }
+  bf16x8 rx[2], ry[2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      rx[u] = ld8(xsrc[u] + k0);
+      ry[u] = ld8(ysrc[u] + k0);
     }
-    if (k0 + 64 > n) {  // keys past n: their v^T entries were never written
+    if (k0 + kPK > n) {
 #pragma unroll
-      for (int t = 0; t < 4; ++t)
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          if (k0 + 32 * g + 8 * t + e >= n) af[t][e] = (bf16)0.f;
+          if (k0 + kcol[u] + e >= n) rx[u][e] = (bf16)0.f;
     }
+  };
+  auto sstore = [&](int buf) {
 #pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      acc0 = mfma32(af[t], bf0[t], acc0);
-      acc1 = mfma32(af[t], bf1[t], acc1);
+    for (int u = 0; u < 2; ++u) {
+      *reinterpret_cast<bf16x8*>(&xs[buf][soff[u]]) = rx[u];
+      *reinterpret_cast<bf16x8*>(&ys[buf][soff[u]]) = ry[u];
     }
+  };
+  const int wm = wave >> 1, wn = wave & 1;
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = zero16();
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  int buf = 0;
+#pragma unroll 1
+  for (int k0 = 0; k0 < np; k0 += kPK) {
+    const bool more = k0 + kPK < np;
+    if (more) gload(k0 + kPK);
+#pragma unroll
+    for (int kk = 0; kk < kPK; kk += 16) {
+      bf16x8 av[2], bv[2];
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi) av[mi] = ld8(&xs[buf][(wm * 64 + mi * 32 + li) * kPKP + kk + 8 * g]);
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) bv[ni] = ld8(&ys[buf][(wn * 64 + ni * 32 + li) * kPKP + kk + 8 * g]);
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma32(av[mi], bv[ni], acc[mi][ni]);
+    }
+    if (more) sstore(buf ^ 1);
+    __syncthreads();
+    buf ^= 1;
   }
+
   const int hd = a.heads * a.dh;
 #pragma unroll
-  for (int half = 0; half < 2; ++half) {
-    const f32x16& acc = half == 0 ? acc0 : acc1;
-    const int q = q0 + 32 * half + li;
+  for (int ni = 0; ni < 2; ++ni) {
+    const int q = q0 + wn * 64 + ni * 32 + li;
     if (q >= n) continue;
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int r = r0 + 8 * v + 4 * g;
-      if (r >= rows) continue;
-      const int s = r / a.dh, c = r - s * a.dh;
-      const int64_t off = ((b * a.depth + s) * n + q) * hd + h * a.dh + c;
-      const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + off);
-      f32x4 y;
+    for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = acc[4 * v + e] * (float)gv[e];
-      *reinterpret_cast<f32x4*>(a.og + off) = y;
-    }
+      for (int v = 0; v < 4; ++v) {
+        const int r = r0 + wm * 64 + mi * 32 + 8 * v + 4 * g;
+        if (r >= rows) continue;
+        const int s = r / a.dh, c = r - s * a.dh;
+        const int64_t off = ((b * a.depth + s) * n + q) * hd + h * a.dh + c;
+        const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + off);
+        f32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = acc[mi][ni][4 * v + e] * (float)gv[e];
+        *reinterpret_cast<f32x4*>(a.og + off) = y;
+      }
   }
 }
 
@@ -120,10 +173,8 @@ void launch_pwa_softmax(const PwaSoftmaxArgs& a, hipStream_t stream) {
 }
 
 void launch_pwa_average(const PwaAverageArgs& a, hipStream_t stream) {
-  const int rows = a.depth * a.dh;
-  pwa_average<<<dim3((unsigned)((rows + 127) / 128), (unsigned)((a.n + 63) / 64),
-                     (unsigned)(a.batch * a.heads)),
-                256, 0, stream>>>(a);
+  const int64_t rt = ((int64_t)a.depth * a.dh + kPT - 1) / kPT, qt = (a.n + kPT - 1) / kPT;
+  pwa_average<<<dim3((unsigned)(rt * qt * a.batch * a.heads)), 256, 0, stream>>>(a);
 }
 
 }  // namespace ffk

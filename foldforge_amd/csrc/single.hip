@@ -565,16 +565,24 @@ void launch_row_gemm_t(const RowGemmArgs& a, hipStream_t stream) {
 
 // Tile shapes: the LayerNorm-fed GEMMs give each workgroup several output tiles (the tile is
 // normalised once per workgroup); the fp32-fed ones split k 8 ways when k is long, and give the
-// waves separate output tiles when it is a single group or two.
+// waves separate output tiles when k has fewer groups than waves.
 void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream) {
   if (epi == kEpiApb && xsrc == kXLn)
     launch_row_gemm_t<kEpiApb, kXLn, 4>(a, stream);
   else if (epi == kEpiSwiglu && xsrc == kXLn)
     launch_row_gemm_t<kEpiSwiglu, kXLn, 8>(a, stream);
-  else if (epi == kEpiResid && xsrc == kXF32 && a.K <= 128)
-    launch_row_gemm_t<kEpiResid, kXF32, 8>(a, stream);
-  else if (epi == kEpiResid && xsrc == kXF32)
-    launch_row_gemm_t<kEpiResid, kXF32, 1>(a, stream);
+  else if (epi == kEpiResid && xsrc == kXF32) {
+    // k split into KS parts of whole 64-wide groups with none left idle (8 from 6 groups up)
+    const int groups = a.K / 64;
+    if (groups >= 6)
+      launch_row_gemm_t<kEpiResid, kXF32, 1>(a, stream);
+    else if (groups >= 4)
+      launch_row_gemm_t<kEpiResid, kXF32, 2>(a, stream);
+    else if (groups >= 2)
+      launch_row_gemm_t<kEpiResid, kXF32, 4>(a, stream);
+    else
+      launch_row_gemm_t<kEpiResid, kXF32, 8>(a, stream);
+  }
   else if (epi == kEpiPwa && xsrc == kXLn)
     launch_row_gemm_t<kEpiPwa, kXLn, 8>(a, stream);
   else if (epi == kEpiOpm && xsrc == kXLn)

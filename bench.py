@@ -74,6 +74,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--ladder", action="store_true")
     ap.add_argument("--msa", action="store_true",
                     help="time the MSA-stack ops at L = 256 / 384 tokens, 512 MSA rows")
+    ap.add_argument("--shapes", action="store_true",
+                    help="time the template-stack and confidence-head shapes of the block")
     ap.add_argument("--ladder-max", type=int, default=16384)
     return ap.parse_args()
 
@@ -369,6 +371,47 @@ def opm_measure(reps: int = 20) -> dict:
     return out
 
 
+def shapes_measure(reps: int = 10) -> dict:
+    """The same block at its other shapes: AF3's template stack (pair 64, triangle attention
+    4 x 16, hidden 64, transition x 2; 4 templates batched) and the confidence head's block
+    (pair 128 with the single track, 5 samples batched), both at N = 384; ms per block on hip
+    and on the engine pytorch backend (same GPU)."""
+    import torch
+
+    from foldforge_amd import factories
+    from foldforge_amd.policy import guard
+    from foldforge_amd.trunk import randomise
+
+    n = 384
+    out = {"n": n, "rows": []}
+    cases = (
+        ("template stack block (AF3): pair 64, 4 x 16 heads, hidden 64, transition x2, 4 templates",
+         dict(d_pair=64, triangle_model="af3", d_hidden_tri_attention=16, pair_transition_n=2), 4, 64, 0),
+        ("confidence head block (AF3): pair 128 + single 384, 5 samples",
+         dict(d_pair=128, triangle_model="af3", d_single=384), 5, 128, 384),
+    )
+    for name, kwargs, batch, c, cs in cases:
+        block = randomise(factories.pairformer_block(**kwargs), seed=1, out_scale=0.25).cuda()
+        g = torch.Generator(device="cuda").manual_seed(2)
+        z = torch.randn(batch, n, n, c, device="cuda", generator=g).bfloat16()
+        mask = torch.ones(batch, n, dtype=torch.bool, device="cuda")
+        s = torch.randn(batch, n, cs, device="cuda", generator=g).bfloat16() if cs else None
+        args = (z, mask) if s is None else (z, mask, s)
+        row = {"workload": name, "batch": batch}
+        with torch.no_grad():
+            for backend in ("hip", "pytorch"):
+                block.set_backend(backend)
+                if backend == "hip":
+                    for m in block.children_ops():
+                        guard(m, "error")
+                row[f"{backend}_ms"] = round(event_time_ms(lambda: block(*args), reps, warm=max(20, reps)), 3)
+        row["hip_speedup"] = round(row["pytorch_ms"] / row["hip_ms"], 2)
+        out["rows"].append(row)
+        del block, z, s
+        torch.cuda.empty_cache()
+    return out
+
+
 def ladder(max_n: int) -> list[dict]:
     """Config 5: full trunks at N = 768 .. 2048, then single blocks (with single track) at
     larger N until the device runs out of memory."""
@@ -464,6 +507,9 @@ def main() -> int:
         return 1
     if args.ladder:
         ladder(args.ladder_max)
+        return 0
+    if args.shapes:
+        print(json.dumps({"shapes": shapes_measure(args.steps)}), flush=True)
         return 0
     if args.msa:
         print(json.dumps({"msa": msa_measure(args.steps), "opm": opm_measure(args.steps)}), flush=True)

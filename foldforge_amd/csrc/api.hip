@@ -121,16 +121,30 @@ void launch_pack(const PackJob& job, hipStream_t stream) {
 // ---------------------------------------------------------------------------------------
 // workspace layouts (shared by the size queries and the entry points)
 
+// The fused kernels serve the AF3 trunk widths; other widths run the generic path
+// (token-row GEMMs + the plane contraction).
+bool trimul_fused(int c, int h) { return c == 128 && h == 128; }
+bool triattn_fused(int c, int heads, int d) { return c == 128 && heads == 4 && d == 32; }
+
 struct TrimulWs {
-  bf16 *wp, *wg, *wo, *A, *B, *P;
-  float* maskf;
+  bf16 *wp, *wg, *wo, *A, *B, *P, *Pt;
+  float *maskf, *y32;
   size_t bytes;
 };
 TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
   Carver cv{static_cast<char*>(ws)};
   const int64_t np = pad128(n);
   const size_t plane = (size_t)batch * h * np * np;
-  TrimulWs w;
+  TrimulWs w{};
+  if (!trimul_fused(c, h)) {
+    w.A = cv.take<bf16>(plane);
+    w.B = cv.take<bf16>(plane);
+    w.P = cv.take<bf16>(plane);
+    w.Pt = cv.take<bf16>((size_t)batch * n * n * h);
+    w.y32 = cv.take<float>((size_t)batch * n * n * c);
+    w.bytes = cv.used;
+    return w;
+  }
   w.wp = cv.take<bf16>((size_t)4 * h * c);
   w.wg = cv.take<bf16>((size_t)c * c);
   w.wo = cv.take<bf16>((size_t)c * h);
@@ -142,16 +156,30 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
   return w;
 }
 
+int64_t pad32(int64_t n);
+
 struct TriattnWs {
-  bf16 *wqkv, *wb, *wg, *wo, *q, *k, *vt, *o;
-  float* bias;
+  bf16 *wqkv, *wb, *wg, *wo, *q, *k, *vt, *o, *gate;
+  float *bias, *og;
   size_t bytes;
 };
 TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d) {
   Carver cv{static_cast<char*>(ws)};
   const int64_t np = pad128(n);
   const int hd = heads * d;
-  TriattnWs w;
+  TriattnWs w{};
+  if (!triattn_fused(c, heads, d)) {
+    const int64_t np32 = pad32(n);
+    const size_t tok = (size_t)batch * n * n * hd;
+    w.q = cv.take<bf16>(tok);
+    w.k = cv.take<bf16>(tok);
+    w.gate = cv.take<bf16>(tok);
+    w.vt = cv.take<bf16>((size_t)batch * n * hd * np32);
+    w.bias = cv.take<float>((size_t)batch * heads * n * np32);
+    w.og = cv.take<float>(tok);
+    w.bytes = cv.used;
+    return w;
+  }
   w.wqkv = cv.take<bf16>((size_t)3 * hd * c);
   w.wb = cv.take<bf16>((size_t)32 * c);
   w.wg = cv.take<bf16>((size_t)hd * c);
@@ -288,8 +316,10 @@ int32_t ffk_triangle_multiplication(
     size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_pair, int32_t d_hidden,
     int32_t outgoing, int32_t residual, float eps, void* stream) {
   if (int32_t s = check_device()) return s;
-  if (d_pair != 128 || d_hidden != 128)
-    return fail(FFK_ERR_INVALID, "triangle_multiplication: d_pair=%d d_hidden=%d (kernels take 128/128)", d_pair, d_hidden);
+  const bool fused = trimul_fused(d_pair, d_hidden);
+  if (!fused && (d_pair <= 0 || d_pair % 64 != 0 || d_pair > 256 || d_hidden <= 0 ||
+                 d_hidden % 64 != 0 || d_hidden > kLnGemmMaxK))
+    return fail(FFK_ERR_INVALID, "triangle_multiplication: d_pair=%d d_hidden=%d (kernels take 128/128, or d_pair a multiple of 64 up to 256 with d_hidden a multiple of 64 up to %d)", d_pair, d_hidden, kLnGemmMaxK);
   if (batch <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "triangle_multiplication: empty shape");
   if (batch * 128 > 65535 || pad128(n) > 65535)
     return fail(FFK_ERR_INVALID, "triangle_multiplication: batch=%lld n=%lld exceed the launch grid", (long long)batch, (long long)n);
@@ -303,6 +333,58 @@ int32_t ffk_triangle_multiplication(
     return fail(FFK_ERR_WORKSPACE, "triangle_multiplication: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
   const TrimulWs w = trimul_ws(workspace, batch, n, d_pair, d_hidden);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (!fused) {
+    if (batch * d_hidden * (pad128(n) / 128) * (pad128(n) / 128) > 0x7fffffffLL)
+      return fail(FFK_ERR_INVALID, "triangle_multiplication: shape exceeds the launch grid");
+    const int64_t np = pad128(n);
+    RowGemmArgs p{};
+    p.ln_x = static_cast<const bf16*>(z);
+    p.ln_w = ln_pair_w;
+    p.ln_b = ln_pair_b;
+    p.eps = eps;
+    p.w0 = w_left;
+    p.w1 = w_right;
+    p.w2 = w_left_gate;
+    p.w3 = w_right_gate;
+    p.M = batch * np * np;
+    p.K = d_pair;
+    p.O = 4 * d_hidden;
+    p.n = (int)n;
+    p.npm = (int)np;
+    p.tmap = outgoing ? kMapGridOut : kMapGridIn;
+    p.mask = key_mask;
+    p.pa = w.A;
+    p.pb = w.B;
+    launch_row_gemm(p, kEpiTrimul, kXLn, st);
+    launch_trimul_contract(w.A, w.B, w.P, batch * d_hidden, (int)np, st);
+    launch_planes_to_rows(w.P, w.Pt, (int)batch, d_hidden, (int)n, (int)np, st);
+    RowGemmArgs o{};
+    o.ln_x = w.Pt;
+    o.ln_w = ln_out_w;
+    o.ln_b = ln_out_b;
+    o.eps = eps;
+    o.w0 = w_out;
+    o.M = batch * n * n;
+    o.K = d_hidden;
+    o.O = d_pair;
+    o.h32 = w.y32;
+    launch_row_gemm(o, kEpiStore32, kXLn, st);
+    RowGemmArgs f{};
+    f.ln_x = static_cast<const bf16*>(z);
+    f.ln_w = ln_pair_w;
+    f.ln_b = ln_pair_b;
+    f.eps = eps;
+    f.w0 = w_gate;
+    f.M = batch * n * n;
+    f.K = d_pair;
+    f.O = d_pair;
+    f.y32 = w.y32;
+    f.res = static_cast<const bf16*>(z);
+    f.out = static_cast<bf16*>(out);
+    f.residual = residual ? 1 : 0;
+    launch_row_gemm(f, kEpiGateResid, kXLn, st);
+    return check_launch("triangle_multiplication");
+  }
   const int64_t hc = (int64_t)d_hidden * d_pair;
   PackJob job{};
   // gate projections pre-multiplied by -log2(e): the kernels' sigmoid is 1 / (1 + 2^y)
@@ -353,8 +435,10 @@ int32_t ffk_triangle_attention(
     int32_t d_head, int32_t starting, int32_t transposed_bias, int32_t residual, float eps,
     void* stream) {
   if (int32_t s = check_device()) return s;
-  if (d_pair != 128 || d_head != 32 || n_head != 4)
-    return fail(FFK_ERR_INVALID, "triangle_attention: d_pair=%d heads=%d x %d (kernels take 128, 4 x 32)", d_pair, n_head, d_head);
+  const bool fused = triattn_fused(d_pair, n_head, d_head);
+  if (!fused && (!(d_pair == 64 || d_pair == 128 || d_pair == 256) || n_head <= 0 || n_head > 32 ||
+                 d_head <= 0 || d_head % 8 != 0 || d_head > 32 || (n_head * d_head) % 64 != 0))
+    return fail(FFK_ERR_INVALID, "triangle_attention: d_pair=%d heads=%d x %d (kernels take 128 with 4 x 32, or d_pair 64 / 128 / 256 with at most 32 heads of 8 to 32 channels, heads x d_head a multiple of 64)", d_pair, n_head, d_head);
   if (batch <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "triangle_attention: empty shape");
   if (batch * n_head > 65535 || pad128(n) > 65535)
     return fail(FFK_ERR_INVALID, "triangle_attention: batch=%lld n=%lld exceed the launch grid", (long long)batch, (long long)n);
@@ -369,6 +453,81 @@ int32_t ffk_triangle_attention(
   const TriattnWs w = triattn_ws(workspace, batch, n, d_pair, n_head, d_head);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int hd = n_head * d_head;
+  if (!fused) {
+    if (batch * n > 65535 || batch * n * n * hd / 32 > 0x7fffffffLL * 8)
+      return fail(FFK_ERR_INVALID, "triangle_attention: batch * n = %lld exceeds the launch grid", (long long)(batch * n));
+    const int64_t np32 = pad32(n);
+    // q, k, v^T, gate of every pair row (the transposed pair for the ending node)
+    RowGemmArgs p{};
+    p.ln_x = static_cast<const bf16*>(z);
+    p.ln_w = ln_pair_w;
+    p.ln_b = ln_pair_b;
+    p.eps = eps;
+    p.w0 = w_query;
+    p.w1 = w_key;
+    p.w2 = w_value;
+    p.w3 = w_gate;
+    p.M = batch * n * n;
+    p.K = d_pair;
+    p.O = 4 * hd;
+    p.q_bias = nullptr;
+    p.q_scale = kLog2e / sqrtf((float)d_head);
+    p.gate_bias = 0.f;
+    p.q = w.q;
+    p.k = w.k;
+    p.vt = w.vt;
+    p.gate = w.gate;
+    p.n = (int)n;
+    p.np = (int)np32;
+    p.heads = n_head;
+    p.dh = d_head;
+    p.tmap = starting ? kMapIdentity : kMapPairT;
+    launch_row_gemm(p, kEpiApb, kXLn, st);
+    // the pair bias from the un-transposed pair (the OpenFold lineage's ending node: the
+    // transposed one); the norm's offset adds one constant per head, which the softmax cancels
+    PairBiasArgs pb;
+    pb.z = static_cast<const bf16*>(z);
+    pb.mask = key_mask;
+    pb.ln_w = ln_pair_w;
+    pb.w_bias = w_bias;
+    pb.bias = w.bias;
+    pb.tiles = batch * n * (np32 / 32);
+    pb.n = (int)n;
+    pb.np = (int)np32;
+    pb.heads = n_head;
+    pb.eps = eps;
+    pb.c = d_pair;
+    pb.transposed = !starting && transposed_bias ? 1 : 0;
+    launch_apb_pair_bias(pb, st);
+    ApbAttnArgs at;
+    at.q = w.q;
+    at.k = w.k;
+    at.vt = w.vt;
+    at.gate = w.gate;
+    at.bias = w.bias;
+    at.mask = key_mask;
+    at.og = w.og;
+    at.n = (int)n;
+    at.np = (int)np32;
+    at.heads = n_head;
+    at.dh = d_head;
+    at.cs = hd;
+    at.rows_per_bias = (int)n;
+    launch_apb_attention(at, (int)(batch * n), st);
+    RowGemmArgs o{};
+    o.x32 = w.og;
+    o.w0 = w_out;
+    o.M = batch * n * n;
+    o.K = hd;
+    o.O = d_pair;
+    o.n = (int)n;
+    o.tmap = starting ? kMapIdentity : kMapPairT;
+    o.res = static_cast<const bf16*>(z);
+    o.out = static_cast<bf16*>(out);
+    o.residual = residual ? 1 : 0;
+    launch_row_gemm(o, kEpiResid, kXF32, st);
+    return check_launch("triangle_attention");
+  }
   const int64_t m = (int64_t)hd * d_pair;
   const float qscale = kLog2e / sqrtf((float)d_head);
   PackJob job{};
@@ -587,6 +746,8 @@ int32_t ffk_attention_pair_bias(
   pb.np = (int)np;
   pb.heads = n_head;
   pb.eps = eps_pair;
+  pb.c = 128;
+  pb.transposed = 0;
   launch_apb_pair_bias(pb, st);
 
   ApbAttnArgs at;
@@ -602,6 +763,7 @@ int32_t ffk_attention_pair_bias(
   at.heads = n_head;
   at.dh = dh;
   at.cs = d_single;
+  at.rows_per_bias = 1;
   launch_apb_attention(at, (int)batch, st);
 
   RowGemmArgs o{};
@@ -686,6 +848,8 @@ int32_t ffk_msa_pair_weighted_averaging(
   pb.np = (int)np;
   pb.heads = n_head;
   pb.eps = eps_pair;
+  pb.c = 128;
+  pb.transposed = 0;
   launch_apb_pair_bias(pb, st);
 
   PwaSoftmaxArgs sm;

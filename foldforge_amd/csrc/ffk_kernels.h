@@ -23,6 +23,9 @@ struct TrimulArgs {
   float eps;
 };
 void launch_trimul(const TrimulArgs& a, hipStream_t stream);
+// P[p] = X[p] Y[p]^T for `planes` planes of [np][np] bf16 (np % 128 == 0).
+void launch_trimul_contract(const bf16* A, const bf16* B, bf16* P, int64_t planes, int np,
+                            hipStream_t stream);
 
 struct TriattnArgs {
   const bf16* z;
@@ -69,7 +72,21 @@ void launch_transition(const TransitionArgs& a, hipStream_t stream);
 // three epilogues, x either LayerNorm(ln_x) (kXLn, K <= kLnGemmMaxK) or fp32 rows x32 (kXF32).
 // K % 64 == 0, O % 32 == 0; weights are the fp32 parameters. Pairs served: (kEpiApb, kXLn),
 // (kEpiSwiglu, kXLn), (kEpiResid, kXF32), (kEpiPwa, kXLn), (kEpiOpm, kXLn).
-enum { kEpiApb = 0, kEpiSwiglu = 1, kEpiResid = 2, kEpiPwa = 3, kEpiOpm = 4 };
+enum {
+  kEpiApb = 0,
+  kEpiSwiglu = 1,
+  kEpiResid = 2,
+  kEpiPwa = 3,
+  kEpiOpm = 4,
+  kEpiTrimul = 5,     // gated, masked left / right projections into channel planes
+  kEpiStore32 = 6,    // h32 = y (fp32)
+  kEpiGateResid = 7,  // out = res + y32 * sigmoid(y) (or y32 * sigmoid(y))
+};
+// Row maps (RowGemmArgs.tmap): the input row read for logical row m, and the rows the epilogue
+// of kEpiResid writes. kMapPairT: m = (b n + r) n + j reads row (b n + j) n + r (the
+// transposed pair); kMapGridOut / kMapGridIn: m = (b npm + i) npm + k over the padded grid
+// reads pair row (b n + i) n + k / (b n + k) n + i (clamped past n).
+enum { kMapIdentity = 0, kMapPairT = 1, kMapGridOut = 2, kMapGridIn = 3 };
 enum { kXLn = 0, kXF32 = 1 };
 constexpr int kLnGemmMaxK = 768;
 struct RowGemmArgs {
@@ -101,7 +118,14 @@ struct RowGemmArgs {
   const float *bias0, *bias1;
   bf16 *lt, *rt, *mt;
   int sp;
-  float* h32;  // kEpiSwiglu: [M][hid] = silu(a) * b
+  // kEpiTrimul: w0..w3 = to_left, to_right, to_left_gate, to_right_gate ([hid][K], O = 4 hid),
+  // tiles packed as 16 projection rows + their 16 gate rows; rows on the padded grid (kMapGrid*);
+  // pa / pb [batch][hid][npm][npm] = proj * mask_i mask_k * sigmoid(gate), 0 past n.
+  const uint8_t* mask;
+  bf16 *pa, *pb;
+  int tmap, npm;
+  const float* y32;  // kEpiGateResid: [M][O]
+  float* h32;  // kEpiSwiglu: [M][hid] = silu(a) * b; kEpiStore32: [M][O] = y
   const bf16* res;  // kEpiResid: out = res + y (residual) or y
   bf16* out;
   int residual;
@@ -117,6 +141,8 @@ struct PairBiasArgs {
   int64_t tiles;         // batch * n * np / 32
   int n, np, heads;
   float eps;
+  int c;                 // pair width: 64, 128 or 256
+  int transposed;        // 1: the logit of (query i, key j) comes from z[b, j, i]
 };
 void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream);
 
@@ -126,8 +152,13 @@ struct ApbAttnArgs {
   const uint8_t* mask;
   float* og;  // [M][cs] gate * attention output
   int n, np, heads, dh, cs;
+  int rows_per_bias;  // attention batches sharing one bias and key mask (pair rows: n; else 1)
 };
 void launch_apb_attention(const ApbAttnArgs& a, int batch, hipStream_t stream);
+
+// Channel planes P [batch][hid][np][np] -> token rows Pt [batch][n][n][hid] (bf16).
+void launch_planes_to_rows(const bf16* planes, bf16* rows, int batch, int hid, int n, int np,
+                           hipStream_t stream);
 
 // MSA pair-weighted averaging (msa.hip): the softmax over keys of the pair logits and the
 // weighted average of every MSA row's values.

@@ -82,6 +82,23 @@ size_t row_gemm_lds(int xsrc, int K, int no) {
   return xsrc == kXLn ? red + (size_t)2 * 32 * (K + 8) * sizeof(bf16) : red;
 }
 
+// The input row of logical row m under the row map a.tmap (see kMap* in ffk_kernels.h).
+__device__ inline int64_t mapped_row(const RowGemmArgs& a, int64_t m) {
+  if (a.tmap == kMapPairT) {
+    const int64_t nn = (int64_t)a.n * a.n;
+    const int64_t b = m / nn, rem = m - b * nn;
+    const int r = (int)(rem / a.n), j = (int)(rem - (int64_t)r * a.n);
+    return (b * a.n + j) * a.n + r;
+  }
+  if (a.tmap == kMapGridOut || a.tmap == kMapGridIn) {
+    const int64_t gg = (int64_t)a.npm * a.npm;
+    const int64_t b = m / gg, rem = m - b * gg;
+    const int i = min((int)(rem / a.npm), a.n - 1), k = min((int)(rem % a.npm), a.n - 1);
+    return a.tmap == kMapGridOut ? (b * a.n + i) * a.n + k : (b * a.n + k) * a.n + i;
+  }
+  return min(m, a.M - 1);
+}
+
 // kEpiOpm: the MSA row read by logical row m = (b n + j) sp + s (rows past the depth repeat
 // the last one; their projection is zeroed).
 __device__ inline int64_t opm_msa_row(const RowGemmArgs& a, int64_t m) {
@@ -120,6 +137,14 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
     seg = (ot * 32) / hd;
     cbase = ot * 32 - seg * hd;
     wr = (seg == 0 ? a.w0 : a.w1) + (int64_t)(cbase + li) * a.K;
+  } else if (EPI == kEpiTrimul) {
+    // packed tile: rows 0-15 are projection rows cbase .. cbase + 15 of one side, rows 16-31 the
+    // matching gate rows
+    const int tps = a.O / 64;  // tiles per side: hid / 16
+    seg = ot / tps;
+    cbase = (ot - seg * tps) * 16;
+    const float* base = li < 16 ? (seg == 0 ? a.w0 : a.w1) : (seg == 0 ? a.w2 : a.w3);
+    wr = base + (int64_t)(cbase + (li & 15)) * a.K;
   } else if (EPI == kEpiSwiglu) {
     // packed tile: rows 0-15 are expand_a rows 16 ot .., rows 16-31 the expand_b rows alike
     wr = (li < 16 ? a.w0 : a.w1) + (int64_t)(ot * 16 + (li & 15)) * a.K;
@@ -127,7 +152,7 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
     wr = a.w0 + (int64_t)(ot * 32 + li) * a.K;
   }
   wr += 32 * g;
-  const float* x32 = a.x32 + min(m0 + li, a.M - 1) * a.K + 32 * g;
+  const float* x32 = a.x32 + mapped_row(a, m0 + li) * a.K + 32 * g;
 
   f32x16 acc = zero16();
   f32x4 wc[8], wn[8], xc[8], xn[8];
@@ -147,7 +172,7 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
     constexpr int kMaxChunks = kLnGemmMaxK / 128;
     const int r = tid >> 4, pc = tid & 15;
     const int nc = a.K / 8;
-    const bf16* xr = a.ln_x + (EPI == kEpiOpm ? opm_msa_row(a, m0 + r) : min(m0 + r, a.M - 1)) * a.K;
+    const bf16* xr = a.ln_x + (EPI == kEpiOpm ? opm_msa_row(a, m0 + r) : mapped_row(a, m0 + r)) * a.K;
     bf16x8 xv[kMaxChunks];
 #pragma unroll
     for (int i = 0; i < kMaxChunks; ++i)
@@ -241,10 +266,16 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
       const int c = cbase + 8 * v + 4 * g;
       float y0 = acc[4 * v], y1 = acc[4 * v + 1], y2 = acc[4 * v + 2], y3 = acc[4 * v + 3];
       if (seg == 0) {
-        y0 = (y0 + a.q_bias[c]) * a.q_scale;
-        y1 = (y1 + a.q_bias[c + 1]) * a.q_scale;
-        y2 = (y2 + a.q_bias[c + 2]) * a.q_scale;
-        y3 = (y3 + a.q_bias[c + 3]) * a.q_scale;
+        if (a.q_bias) {
+          y0 += a.q_bias[c];
+          y1 += a.q_bias[c + 1];
+          y2 += a.q_bias[c + 2];
+          y3 += a.q_bias[c + 3];
+        }
+        y0 *= a.q_scale;
+        y1 *= a.q_scale;
+        y2 *= a.q_scale;
+        y3 *= a.q_scale;
         store4(a.q + m * cs + c, y0, y1, y2, y3);
       } else if (seg == 1) {
         store4(a.k + m * cs + c, y0, y1, y2, y3);
@@ -303,6 +334,46 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
         dst[(int64_t)c * a.sp] = (bf16)((acc[4 * v + e] + (bias ? bias[c] : 0.f)) * keep);
       }
     if (seg == 0 && g == 0) a.mt[bj * a.sp + s] = (bf16)keep;
+  } else if (EPI == kEpiTrimul) {
+    const int hid = a.O / 4;
+    const int64_t gg = (int64_t)a.npm * a.npm;
+    const int64_t b = m / gg, rem = m - b * gg;
+    const int i = (int)(rem / a.npm), k = (int)(rem - (int64_t)i * a.npm);
+    // the pair mask m_i m_k is symmetric: the same for (i, k) and the transposed read (k, i)
+    const float keep = i < a.n && k < a.n && a.mask[b * a.n + i] && a.mask[b * a.n + k] ? 1.f : 0.f;
+    bf16* plane = (seg == 0 ? a.pa : a.pb) + b * hid * gg + rem;
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = cbase + 8 * v + 4 * g + e;
+        const float proj = acc[4 * v + e] * keep;  // masked before the gate, as the reference
+        plane[(int64_t)c * gg] = (bf16)(proj * sigmoid_scaled(-kLog2e * acc[8 + 4 * v + e]));
+      }
+  } else if (EPI == kEpiStore32) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = ot * 32 + 8 * v + 4 * g;
+      f32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = acc[4 * v + e];
+      *reinterpret_cast<f32x4*>(a.h32 + m * a.O + c) = y;
+    }
+  } else if (EPI == kEpiGateResid) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = ot * 32 + 8 * v + 4 * g;
+      const f32x4 yv = *reinterpret_cast<const f32x4*>(a.y32 + m * a.O + c);
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = yv[e] * sigmoid_scaled(-kLog2e * acc[4 * v + e]);
+      if (a.residual) {
+        const bf16x4 r = *reinterpret_cast<const bf16x4*>(a.res + m * a.O + c);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] += (float)r[e];
+      }
+      store4(a.out + m * a.O + c, y[0], y[1], y[2], y[3]);
+    }
   } else if (EPI == kEpiSwiglu) {
     const int hid = a.O / 2;
 #pragma unroll
@@ -340,7 +411,9 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
 // row's channels 64 g .. 64 g + 63 (128 contiguous bytes), the statistics come from those
 // registers (two passes, halves joined across lane l ^ 32), and the heads x keys block is
 // one 32 x 32 MFMA tile (A = W' rows, B = the z rows; channel 64 g + 8 t + e feeds step t).
+template <int C>
 __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
+  constexpr int kU = C / 16;  // 8-channel chunks per lane (each lane half holds C / 2)
   __shared__ float wsum_s[4][32];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
   const int n = a.n;
@@ -353,21 +426,27 @@ __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
     const int64_t tt = tile < a.tiles ? tile : a.tiles - 1;
     const int64_t bi = tt / njt;
     const int j0 = (int)(tt - bi * njt) * 32;
-    const bf16* zr = a.z + (bi * n + min(j0 + li, n - 1)) * 128 + 64 * g;
+    const int key = min(j0 + li, n - 1);
+    int64_t row = bi * n + key;  // pair position (query i, key): z[b, i, key]
+    if (a.transposed) {          // z[b, key, i]
+      const int64_t b = bi / n;
+      row = (b * n + key) * n + (bi - b * n);
+    }
+    const bf16* zr = a.z + row * C + (C / 2) * g;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) zf[u] = ld8(zr + 8 * u);
+    for (int u = 0; u < kU; ++u) zf[u] = ld8(zr + 8 * u);
   };
   int64_t t = (int64_t)blockIdx.x * 4 + wave;
-  bf16x8 z0[8], z1[8];
+  bf16x8 z0[kU], z1[kU];
   fetch(z0, t);
 
-  bf16x8 wf[8], wl[8];
+  bf16x8 wf[kU], wl[kU];
   float rs = 0.f;
-  const float* wrow = a.w_bias + min(li, a.heads - 1) * 128 + 64 * g;
-  const float* lrow = a.ln_w + 64 * g;
+  const float* wrow = a.w_bias + min(li, a.heads - 1) * C + (C / 2) * g;
+  const float* lrow = a.ln_w + (C / 2) * g;
   const float keep = li < a.heads ? kLog2e : 0.f;
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
+  for (int u = 0; u < kU; ++u) {
     const f32x4 w0 = *reinterpret_cast<const f32x4*>(wrow + 8 * u);
     const f32x4 w1 = *reinterpret_cast<const f32x4*>(wrow + 8 * u + 4);
     const f32x4 l0 = *reinterpret_cast<const f32x4*>(lrow + 8 * u);
@@ -387,24 +466,24 @@ __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
   auto process = [&](const bf16x8* zf, int64_t tile) {
     float s1 = 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kU; ++u)
 #pragma unroll
       for (int e = 0; e < 8; ++e) s1 += (float)zf[u][e];
-    const float mean = pair_sum(s1) * (1.f / 128.f);
+    const float mean = pair_sum(s1) * (1.f / C);
     float s2 = 0.f;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < kU; ++u)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float d = (float)zf[u][e] - mean;
         s2 += d * d;
       }
-    const float rstd = __builtin_amdgcn_rsqf(pair_sum(s2) * (1.f / 128.f) + a.eps);
+    const float rstd = __builtin_amdgcn_rsqf(pair_sum(s2) * (1.f / C) + a.eps);
     f32x16 acc = zero16();
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc = mfma32(wl[u], zf[u], acc);
+    for (int u = 0; u < kU; ++u) acc = mfma32(wl[u], zf[u], acc);
 #pragma unroll
-    for (int u = 0; u < 8; ++u) acc = mfma32(wf[u], zf[u], acc);
+    for (int u = 0; u < kU; ++u) acc = mfma32(wf[u], zf[u], acc);
 
     const int64_t bi = tile / njt;
     const int key = (int)(tile - bi * njt) * 32 + li;
@@ -443,8 +522,9 @@ __global__ __launch_bounds__(256) void apb_attention(ApbAttnArgs a) {
   const int q0 = blockIdx.x * 32, h = blockIdx.y, b = blockIdx.z;
   const int n = a.n, dh = a.dh, cs = a.cs;
 
+  const int bb = b / a.rows_per_bias;  // the batch element of the bias and the key mask
   int any = 0;
-  for (int t = threadIdx.x; t < n; t += 256) any |= a.mask[(int64_t)b * n + t];
+  for (int t = threadIdx.x; t < n; t += 256) any |= a.mask[(int64_t)bb * n + t];
   const bool empty = !__syncthreads_or(any);
 
   const int qr = min(q0 + li, n - 1);
@@ -452,7 +532,7 @@ __global__ __launch_bounds__(256) void apb_attention(ApbAttnArgs a) {
   bf16x8 qf0 = zero8(), qf1 = zero8();
   if (8 * g < dh) qf0 = ld8(qp + 8 * g);
   if (16 + 8 * g < dh) qf1 = ld8(qp + 16 + 8 * g);
-  const float* bp = a.bias + (((int64_t)b * a.heads + h) * n + qr) * a.np + 4 * g;
+  const float* bp = a.bias + (((int64_t)bb * a.heads + h) * n + qr) * a.np + 4 * g;
   const bf16* vp = a.vt + (((int64_t)b * a.heads + h) * dh + min(li, dh - 1)) * a.np + 8 * g;
   const bf16* kbase = a.k + (int64_t)b * n * cs + h * dh;
 
@@ -587,6 +667,24 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
     launch_row_gemm_t<kEpiPwa, kXLn, 8>(a, stream);
   else if (epi == kEpiOpm && xsrc == kXLn)
     launch_row_gemm_t<kEpiOpm, kXLn, 2>(a, stream);
+  else if (epi == kEpiTrimul && xsrc == kXLn)
+    launch_row_gemm_t<kEpiTrimul, kXLn, 8>(a, stream);
+  else if (epi == kEpiStore32 && xsrc == kXLn) {
+    if (a.O >= 256)
+      launch_row_gemm_t<kEpiStore32, kXLn, 8>(a, stream);
+    else if (a.O >= 128)
+      launch_row_gemm_t<kEpiStore32, kXLn, 4>(a, stream);
+    else
+      launch_row_gemm_t<kEpiStore32, kXLn, 2>(a, stream);
+  } else if (epi == kEpiGateResid && xsrc == kXLn) {
+    // one workgroup column (O <= 256): a workgroup owns its rows, so out may alias the input
+    if (a.O > 128)
+      launch_row_gemm_t<kEpiGateResid, kXLn, 8>(a, stream);
+    else if (a.O > 64)
+      launch_row_gemm_t<kEpiGateResid, kXLn, 4>(a, stream);
+    else
+      launch_row_gemm_t<kEpiGateResid, kXLn, 2>(a, stream);
+  }
 }
 
 void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream) {
@@ -594,7 +692,12 @@ void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream) {
   const int64_t cap = (int64_t)cu_count() * 8;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
-  apb_pair_bias<<<dim3((unsigned)blocks), 256, 0, stream>>>(a);
+  if (a.c == 64)
+    apb_pair_bias<64><<<dim3((unsigned)blocks), 256, 0, stream>>>(a);
+  else if (a.c == 256)
+    apb_pair_bias<256><<<dim3((unsigned)blocks), 256, 0, stream>>>(a);
+  else
+    apb_pair_bias<128><<<dim3((unsigned)blocks), 256, 0, stream>>>(a);
 }
 
 void launch_apb_attention(const ApbAttnArgs& a, int batch, hipStream_t stream) {

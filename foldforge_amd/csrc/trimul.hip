@@ -427,4 +427,10 @@ void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
       a.residual, a.eps);
 }
 
+void launch_trimul_contract(const bf16* A, const bf16* B, bf16* P, int64_t planes, int np,
+                            hipStream_t stream) {
+  const int64_t nt = np / kCT;
+  trimul_contract<<<dim3((unsigned)(nt * nt * planes)), 256, 0, stream>>>(A, B, P, np);
+}
+
 }  // namespace ffk

@@ -48,11 +48,29 @@ def _workspace(nbytes: int, device: torch.device) -> Tensor:
     return torch.empty(max(int(nbytes), 256), dtype=torch.uint8, device=device)
 
 
-def _pair(z: Tensor, mask: Tensor) -> tuple[int, int]:
+def trimul_supported(d_pair: int, d_hidden: int) -> bool:
+    """Widths of the triangle-multiplication kernels: the fused AF3 trunk kernels (128 / 128)
+    or the generic path (pair a multiple of 64 up to 256, hidden a multiple of 64 up to 768)."""
+    return (d_pair, d_hidden) == (128, 128) or (
+        0 < d_pair <= 256 and d_pair % 64 == 0 and 0 < d_hidden <= 768 and d_hidden % 64 == 0)
+
+
+def triangle_attention_supported(d_pair: int, n_head: int, d_head: int, transposed_bias: bool) -> bool:
+    """Shapes of the triangle-attention kernels: the fused AF3 trunk kernels (128, 4 x 32) or
+    the generic path (pair 64 / 128 / 256, at most 32 heads of 8 to 32 channels with
+    heads x d_head a multiple of 64); both take either bias orientation."""
+    if (d_pair, n_head, d_head) == (128, 4, 32):
+        return True
+    return (d_pair in (64, 128, 256) and 0 < n_head <= 32 and 0 < d_head <= 32 and d_head % 8 == 0
+            and (n_head * d_head) % 64 == 0)
+
+
+def _pair(z: Tensor, mask: Tensor, width: int | None = PAIR_WIDTH) -> tuple[int, int]:
     _need(z.is_cuda, "z must be a device tensor")
     _need(z.dtype == torch.bfloat16, f"z must be bf16 (got {z.dtype})")
     _need(z.dim() == 4 and z.shape[1] == z.shape[2], f"z must be [B, N, N, c] (got {tuple(z.shape)})")
-    _need(z.shape[3] == PAIR_WIDTH, f"pair width {z.shape[3]} (the kernels take {PAIR_WIDTH})")
+    if width is not None:
+        _need(z.shape[3] == width, f"pair width {z.shape[3]} (the kernels take {width})")
     _need(z.is_contiguous(), "z must be contiguous")
     _need(mask.dtype == torch.bool and mask.shape == z.shape[:2], "mask must be bool [B, N]")
     _need(mask.device == z.device and mask.is_contiguous(), "mask must be a contiguous device tensor")
@@ -98,8 +116,9 @@ def triangle_multiplicative_update(
     eps: float = 1e-5,
     out: Tensor | None = None,
 ) -> Tensor:
-    """Triangle multiplication (outgoing / incoming) of ``z [B, N, N, 128]`` bf16 under the key mask."""
-    batch, n = _pair(z, mask)
+    """Triangle multiplication (outgoing / incoming) of ``z [B, N, N, c]`` bf16 under the key mask."""
+    batch, n = _pair(z, mask, width=None)
+    c = z.shape[3]
     dev = z.device
     names = ("ln_pair_weight", "ln_pair_bias", "to_left", "to_right", "to_left_gate",
              "to_right_gate", "ln_out_weight", "ln_out_bias", "to_out", "to_gate")
@@ -107,13 +126,15 @@ def triangle_multiplicative_update(
         (ln_pair_weight, ln_pair_bias, to_left, to_right, to_left_gate, to_right_gate,
          ln_out_weight, ln_out_bias, to_out, to_gate), names)]
     hidden = to_left.shape[0]
-    _need(to_left.shape == (hidden, PAIR_WIDTH), f"to_left {tuple(to_left.shape)}")
+    _need(to_left.shape == (hidden, c), f"to_left {tuple(to_left.shape)}")
+    _need(trimul_supported(c, hidden), f"d_pair={c} d_hidden={hidden} (the kernels take 128 / 128, "
+          "or a pair width a multiple of 64 up to 256 with a hidden width a multiple of 64 up to 768)")
     lib = _native.lib()
-    ws = _workspace(lib.ffk_triangle_multiplication_workspace(batch, n, PAIR_WIDTH, hidden), dev)
+    ws = _workspace(lib.ffk_triangle_multiplication_workspace(batch, n, c, hidden), dev)
     out = torch.empty_like(z) if out is None else out
     status = lib.ffk_triangle_multiplication(
         z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
-        ws.data_ptr(), ws.numel(), batch, n, PAIR_WIDTH, hidden, int(outgoing), int(residual),
+        ws.data_ptr(), ws.numel(), batch, n, c, hidden, int(outgoing), int(residual),
         float(eps), _stream(dev),
     )
     _native.check(status, "triangle_multiplicative_update")
@@ -139,8 +160,9 @@ def triangle_attention(
     eps: float = 1e-5,
     out: Tensor | None = None,
 ) -> Tensor:
-    """Triangle attention around the starting / ending node of ``z [B, N, N, 128]`` bf16."""
-    batch, n = _pair(z, mask)
+    """Triangle attention around the starting / ending node of ``z [B, N, N, c]`` bf16."""
+    batch, n = _pair(z, mask, width=None)
+    c = z.shape[3]
     dev = z.device
     ps = [_param(t, dev, nm) for t, nm in zip(
         (ln_pair_weight, ln_pair_bias, to_bias, to_query, to_key, to_value, to_gate, to_out),
@@ -149,12 +171,17 @@ def triangle_attention(
     hd = to_query.shape[0]
     _need(hd % n_head == 0, f"hidden {hd} is not a multiple of {n_head} heads")
     d = hd // n_head
+    _need(triangle_attention_supported(c, n_head, d, transposed_bias),
+          f"d_pair={c} heads={n_head} x {d} (the kernels take 128 with 4 x 32, or pair 64 / 128 / "
+          "256 with at most 32 heads of 8 to 32 channels, heads x d_head a multiple of 64)")
+    if (c, n_head, d) != (128, 4, 32):
+        _need(batch * n <= 65535, f"batch x n = {batch * n} exceeds the launch grid")
     lib = _native.lib()
-    ws = _workspace(lib.ffk_triangle_attention_workspace(batch, n, PAIR_WIDTH, n_head, d), dev)
+    ws = _workspace(lib.ffk_triangle_attention_workspace(batch, n, c, n_head, d), dev)
     out = torch.empty_like(z) if out is None else out
     status = lib.ffk_triangle_attention(
         z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
-        ws.data_ptr(), ws.numel(), batch, n, PAIR_WIDTH, n_head, d, int(starting),
+        ws.data_ptr(), ws.numel(), batch, n, c, n_head, d, int(starting),
         int(transposed_bias), int(residual), float(eps), _stream(dev),
     )
     _native.check(status, "triangle_attention")

@@ -214,8 +214,11 @@ class TriangleMultiplication(EngineOp, MasterWeights, nn.Module):
         reason = _pair_reason(x, mask)
         if reason is not None:
             return reason
-        if x.shape[-1] != 128 or self.d_hidden != 128:
-            return f"d_pair={x.shape[-1]} d_hidden={self.d_hidden} (the kernels take 128/128)"
+        from foldforge_amd.kernels import trimul_supported
+
+        if x.shape[-1] != self.d_pair or not trimul_supported(self.d_pair, self.d_hidden):
+            return (f"d_pair={x.shape[-1]} d_hidden={self.d_hidden} (the kernels take 128 / 128, or a "
+                    "pair width a multiple of 64 up to 256 with a hidden width a multiple of 64 up to 768)")
         if self.divide_by_length:
             return "the length-divided (RF3) contraction is not in the hip kernels"
         return None
@@ -302,9 +305,16 @@ class TriangleAttention(EngineOp, MasterWeights, nn.Module):
         reason = _pair_reason(x, mask)
         if reason is not None:
             return reason
-        if x.shape[-1] != 128 or self.n_head != 4 or self.d_hidden != 128:
-            return (f"d_pair={x.shape[-1]} heads={self.n_head} hidden={self.d_hidden} "
-                    "(the kernels take 128, 4 x 32)")
+        from foldforge_amd.kernels import triangle_attention_supported
+
+        d = self.d_hidden // self.n_head
+        if (x.shape[-1] != self.d_pair or self.d_hidden % self.n_head
+                or not triangle_attention_supported(self.d_pair, self.n_head, d, self.transposed_bias)):
+            return (f"d_pair={x.shape[-1]} heads={self.n_head} hidden={self.d_hidden} (the kernels "
+                    "take 128 with 4 x 32, or pair 64 / 128 / 256 with at most 32 heads of 8 to 32 "
+                    "channels, heads x d_head a multiple of 64)")
+        if (self.d_pair, self.n_head, d) != (128, 4, 32) and x.shape[0] * x.shape[1] > 65535:
+            return f"batch x n = {x.shape[0] * x.shape[1]} exceeds the launch grid"
         return None
 
     def _forward_pytorch(self, x: Tensor, mask: Tensor, *, residual: bool = True) -> Tensor:

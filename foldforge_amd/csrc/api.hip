@@ -245,7 +245,7 @@ struct OpmWs {
 };
 OpmWs opm_ws(void* ws, int64_t batch, int64_t depth, int64_t n, int cz) {
   Carver cv{static_cast<char*>(ws)};
-  const int64_t sp = pad32(depth);
+  const int64_t sp = pad64(depth);
   OpmWs w;
   w.lt = cv.take<bf16>((size_t)batch * n * 32 * sp);
   w.rt = cv.take<bf16>((size_t)batch * n * 32 * sp);
@@ -578,7 +578,7 @@ int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
     return fail(FFK_ERR_INVALID, "flash_attention_bias: bad shape (n_pad %lld must be a positive multiple of 128, rows %lld of 4)", (long long)n_pad, (long long)rows);
   if (rows_valid < 0 || rows_valid > rows || n_valid < 0 || n_valid > n_pad)
     return fail(FFK_ERR_INVALID, "flash_attention_bias: valid extents exceed the padded shape");
-  if ((n_pad + 255) / 256 * (rows / 4) * batch * heads > 0x7fffffffLL)
+  if ((n_pad + 127) / 128 * (rows / 4) * batch * heads > 0x7fffffffLL)
     return fail(FFK_ERR_INVALID, "flash_attention_bias: grid too large");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v_t) || !aligned16(bias))
     return fail(FFK_ERR_INVALID, "flash_attention_bias: q/k/v_t/bias must be 16-byte aligned");
@@ -904,7 +904,7 @@ int32_t ffk_outer_product_mean(
   if (d_msa <= 0 || d_msa % 64 != 0 || d_msa > kLnGemmMaxK)
     return fail(FFK_ERR_INVALID, "outer_product_mean: d_msa=%d (kernels take a multiple of 64 up to %d)", d_msa, kLnGemmMaxK);
   if (batch <= 0 || depth <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "outer_product_mean: empty shape");
-  const int64_t sp = pad32(depth);
+  const int64_t sp = pad64(depth);
   const int64_t nt = (n + 7) / 8;
   if (batch > 65535 || (n + 31) / 32 > 65535 || nt * nt * batch > 0x7fffffffLL ||
       batch * n * sp / 32 > 0x7fffffffLL || n * n > 0x7fffffffLL)

@@ -9,7 +9,8 @@
 //   normalize-before-projection form is (o / d) W_out^T + b.
 // The C-ABI (api.hip) runs:
 //   row_gemm<kEpiOpm, kXLn> (single.hip): LayerNorm + both projections, masked, stored with
-//     the MSA rows contiguous (l^T, r^T [batch][n][32][sp]) and the mask transposed
+//     the MSA rows contiguous (l^T, r^T [batch][n][32][sp], sp = depth padded to 64) and the
+//     mask transposed
 //   opm_count: n[i, j] as a 0/1 GEMM over the MSA rows (exact in fp32)
 //   opm_pack: W_out rounded to bf16 in the contraction's k order
 //   opm_contract: per workgroup a tile of 8 x 8 tokens: the 256 x 256 outer-product block
@@ -25,8 +26,10 @@ namespace {
 constexpr int kOpmC = 32;                   // channels per side (d_hidden)
 constexpr int kOpmT = 8;                    // tokens per tile side
 constexpr int kOpmRows = kOpmT * kOpmC;     // (token, channel) rows of one operand tile
-constexpr int kOpmKC = 32;                  // MSA rows per LDS stage
-constexpr int kOpmKS = kOpmKC + 8;          // LDS row stride of a stage (80 B: conflict-free reads)
+constexpr int kOpmKC = 32;                  // MSA rows per LDS stage (the MSA padding is 64)
+constexpr int kOpmKS = kOpmKC + 8;          // LDS row stride of a stage (conflict-free reads)
+constexpr int kOpmCPR = kOpmKC / 8;         // 16-byte chunks per operand row and stage
+constexpr int kOpmPT = kOpmRows * kOpmCPR / 512;  // chunks per thread and operand
 constexpr int kOpmPairs = kOpmT * kOpmT;    // pairs per tile
 constexpr int kOpmK2 = kOpmC * kOpmC;       // 1024: the projection's k
 constexpr int kOpmOS = kOpmK2 + 8;          // LDS row stride of a pair's outer product
@@ -85,30 +88,30 @@ __global__ __launch_bounds__(512) void opm_contract(OpmContractArgs a) {
   const int i0 = ti * kOpmT, j0 = tj * kOpmT;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, g = lane >> 5;
 
-  // global -> LDS: an operand stage is 256 rows x 32 MSA rows = 1024 chunks of 8 bf16
-  const bf16* xsrc[2];
-  const bf16* ysrc[2];
-  int soff[2];
+  // global -> LDS: an operand stage is 256 rows x kOpmKC MSA rows in chunks of 8 bf16
+  const bf16* xsrc[kOpmPT];
+  const bf16* ysrc[kOpmPT];
+  int soff[kOpmPT];
 #pragma unroll
-  for (int u = 0; u < 2; ++u) {
+  for (int u = 0; u < kOpmPT; ++u) {
     const int c = tid + 512 * u;
-    const int row = c >> 2, kc = (c & 3) * 8;
+    const int row = c / kOpmCPR, kc = (c % kOpmCPR) * 8;
     const int ti_tok = min(i0 + (row >> 5), n - 1), tj_tok = min(j0 + (row >> 5), n - 1);
     xsrc[u] = a.lt + ((b * n + ti_tok) * kOpmC + (row & 31)) * sp + kc;
     ysrc[u] = a.rt + ((b * n + tj_tok) * kOpmC + (row & 31)) * sp + kc;
     soff[u] = row * kOpmKS + kc;
   }
-  bf16x8 rx[2], ry[2];
+  bf16x8 rx[kOpmPT], ry[kOpmPT];
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kOpmPT; ++u) {
       rx[u] = ld8(xsrc[u] + k0);
       ry[u] = ld8(ysrc[u] + k0);
     }
   };
   auto sstore = [&](int buf) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < kOpmPT; ++u) {
       *reinterpret_cast<bf16x8*>(xs + buf * kOpmRows * kOpmKS + soff[u]) = rx[u];
       *reinterpret_cast<bf16x8*>(ys + buf * kOpmRows * kOpmKS + soff[u]) = ry[u];
     }

@@ -41,8 +41,10 @@
 namespace ffk {
 
 constexpr int kFR = 4;      // attention rows per flash workgroup (share the bias tile)
-constexpr int kFW = 8;      // waves per flash workgroup, 32 queries each
-constexpr int kFK = 64;     // keys per LDS stage
+constexpr int kFW = 4;      // waves per flash workgroup, 32 queries each (two workgroups per
+                            // CU: the waves sharing a SIMD belong to different workgroups, so
+                            // their barriers do not hold them in step)
+constexpr int kFK = 32;     // keys per LDS stage
 constexpr float kSumHigh = 1.2676506002282294e30f;  // 2^100
 constexpr float kSumLow = 7.888609052210118e-31f;    // 2^-100
 
@@ -199,10 +201,10 @@ struct __attribute__((aligned(16))) FlashLds {
 };
 
 // Element offsets of 16-byte piece p of K row `key` (4 pieces: 64 B, four rows fill the 64
-// banks) and of V^T row d (8 pieces: 128 B, two rows fill them), XOR-swizzled so that the
-// MFMA operand reads of 16 consecutive rows hit distinct banks.
+// banks) and of V^T row d (4 pieces of a 32-key stage), XOR-swizzled so that the MFMA operand
+// reads of 16 consecutive rows hit distinct banks.
 __device__ __forceinline__ int koff(int key, int p) { return key * 32 + 8 * (p ^ ((key >> 2) & 3)); }
-__device__ __forceinline__ int voff(int d, int p) { return d * kFK + 8 * (p ^ ((d >> 1) & 7)); }
+__device__ __forceinline__ int voff(int d, int p) { return d * kFK + 8 * (p ^ ((d >> 2) & 3)); }
 
 // exp2 of the 32 logits a lane holds for its query, packed into the bf16 P^T operands of
 // the P V product; returns the lane's partial row sum (v_dot2 over the packed pairs).
@@ -224,8 +226,8 @@ __device__ __forceinline__ float exp_pack(const f32x16& S, bf16x8& p0, bf16x8& p
 }
 
 // grid (ceil(np / 256) * (np / 4) * batch * heads) workgroups, renumbered per XCD;
-// block 512 = 8 waves x 32 queries, 4 attention rows.
-__global__ __launch_bounds__(512) void flash_attn_bias(
+// block 256 = 4 waves x 32 queries, 4 attention rows.
+__global__ __launch_bounds__(256, 2) void flash_attn_bias(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ vt,
     const float* __restrict__ bias, bf16* __restrict__ o, int heads, int64_t rows, int64_t np,
     int64_t rows_valid, int64_t n_valid, int64_t o_sb, int64_t o_sr, int64_t o_sj) {
@@ -251,8 +253,8 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
   const int64_t nb = np / 32;
   const int64_t nstage = np / kFK;
 
-  // Transfers (each one 1 KB LDS DMA per wave): stage s of K / V^T = 32 pieces, 4 per wave
-  // (piece P = 4 wave + u: part P / 16 (K, V^T), row (P / 4) % 4, quarter P % 4); bias tile
+  // Transfers (each one 1 KB LDS DMA per wave): stage s of K / V^T = 16 pieces, 4 per wave
+  // (piece P = 4 wave + u: part P / 8 (K, V^T), row (P / 2) % 4, half P % 2); bias tile
   // kb of this wave = 4 pieces. Past the last stage / tile a transfer repeats a real one into
   // a buffer that is no longer read, so every wave always has the same transfers in flight.
   const bf16* kbase = k + (bh * rows + r0) * np * 32;
@@ -262,15 +264,15 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
     const int64_t key0 = (s < nstage ? s : nstage - 1) * kFK;
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int P = 4 * wave + u, rr = (P >> 2) & 3, i = P & 3;  // wave-uniform
-      if (P < 16) {
+      const int P = 4 * wave + u, rr = (P >> 1) & 3, i = P & 1;  // wave-uniform
+      if (P < 8) {
         const int key = 16 * i + (lane >> 2), p = (lane & 3) ^ ((key >> 2) & 3);
         dma16(kbase, (uint32_t)((((int64_t)rr * np + key0 + key) * 32 + 8 * p) * 2),
               k_lds + (uint32_t)(((buf * kFR + rr) * kFK * 32 + 16 * i * 32) * 2));
       } else {
-        const int d = 8 * i + (lane >> 3), p = (lane & 7) ^ ((d >> 1) & 7);
+        const int d = 16 * i + (lane >> 2), p = (lane & 3) ^ ((d >> 2) & 3);
         dma16(vbase, (uint32_t)((((int64_t)rr * 32 + d) * np + key0 + 8 * p) * 2),
-              v_lds + (uint32_t)(((buf * kFR + rr) * 32 * kFK + 8 * i * kFK) * 2));
+              v_lds + (uint32_t)(((buf * kFR + rr) * 32 * kFK + 16 * i * kFK) * 2));
       }
     }
   };
@@ -329,57 +331,50 @@ __global__ __launch_bounds__(512) void flash_attn_bias(
 #pragma unroll 1
   for (int64_t st = 0; st < nstage; ++st) {
     const int sb = (int)(st & 1);
+    // this wave's bias tile st and everyone's K / V^T stage st have landed (waited for and
+    // published at the end of the last stage)
+    wait_vm_lds<0>();
+    f32x16 bcur;
+    {
+      const float* bt = &lds.bias[wave][st & 1][4 * lane];
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      const int64_t kb = st * 2 + sub;
-      // this wave's bias tile kb has landed: issued after it were only, in a second
-      // sub-step, the 4 pieces of the next K / V^T stage
-      if (sub == 0)
-        wait_vm_lds<0>();
-      else
-        wait_vm_lds<4>();
-      f32x16 bcur;
-      {
-        const float* bt = &lds.bias[wave][kb & 1][4 * lane];
+      for (int v4 = 0; v4 < 4; ++v4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(bt + 256 * v4);
 #pragma unroll
-        for (int v4 = 0; v4 < 4; ++v4) {
-          const f32x4 x = *reinterpret_cast<const f32x4*>(bt + 256 * v4);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) bcur[4 * v4 + e] = x[e] - msh;
-        }
+        for (int e = 0; e < 4; ++e) bcur[4 * v4 + e] = x[e] - msh;
       }
-      bias_dma(kb + 1);                      // into the other tile buffer, read last step
-      if (sub == 0) kv_dma(st + 1, sb ^ 1);  // the other stage buffer, read last stage
-      if (active) {
-        // two rows at a time: S^T = (bias - m) + K Q^T, softmax, O^T += V^T P^T
+    }
+    kv_dma(st + 1, sb ^ 1);  // the other stage buffer, read last stage
+    bias_dma(st + 1);        // the other tile buffer, read last stage (issued last: see below)
+    if (active) {
+      // two rows at a time: S^T = (bias - m) + K Q^T, softmax, O^T += V^T P^T
 #pragma unroll
-        for (int rp = 0; rp < kFR; rp += 2) {
-          f32x16 S[2];
+      for (int rp = 0; rp < kFR; rp += 2) {
+        f32x16 S[2];
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int rr = rp + u;
-            const bf16* kt = lds.k[sb][rr];
-            S[u] = mfma32(ld8(kt + koff(sub * 32 + li, g)), qa[rr][0], bcur);
-            S[u] = mfma32(ld8(kt + koff(sub * 32 + li, 2 + g)), qa[rr][1], S[u]);
-          }
-          bf16x8 p0[2], p1[2];
-          float ts[2];
+        for (int u = 0; u < 2; ++u) {
+          const int rr = rp + u;
+          const bf16* kt = lds.k[sb][rr];
+          S[u] = mfma32(ld8(kt + koff(li, g)), qa[rr][0], bcur);
+          S[u] = mfma32(ld8(kt + koff(li, 2 + g)), qa[rr][1], S[u]);
+        }
+        bf16x8 p0[2], p1[2];
+        float ts[2];
 #pragma unroll
-          for (int u = 0; u < 2; ++u) ts[u] = exp_pack(S[u], p0[u], p1[u]);
+        for (int u = 0; u < 2; ++u) ts[u] = exp_pack(S[u], p0[u], p1[u]);
 #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int rr = rp + u;
-            l[rr] += ts[u];
-            const bf16* vtile = lds.v[sb][rr];
-            O[rr] = mfma32(ld8(vtile + voff(li, 4 * sub + g)), p0[u], O[rr]);
-            O[rr] = mfma32(ld8(vtile + voff(li, 4 * sub + 2 + g)), p1[u], O[rr]);
-          }
+        for (int u = 0; u < 2; ++u) {
+          const int rr = rp + u;
+          l[rr] += ts[u];
+          const bf16* vtile = lds.v[sb][rr];
+          O[rr] = mfma32(ld8(vtile + voff(li, g)), p0[u], O[rr]);
+          O[rr] = mfma32(ld8(vtile + voff(li, 2 + g)), p1[u], O[rr]);
         }
       }
     }
-    // this wave's pieces of the next stage have landed (only the 4 bias pieces of the
-    // second sub-step were issued after them); the barrier publishes everyone's and retires
-    // this stage's reads of the buffer the next transfers overwrite
+    // this wave's pieces of the next K / V^T stage have landed (only its 4 bias pieces, issued
+    // after them, may still be in flight); the barrier publishes everyone's and retires this
+    // stage's reads of the buffer the next transfers overwrite
     wait_vm_lds<4>();
     __syncthreads();
   }

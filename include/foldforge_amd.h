@@ -58,7 +58,9 @@ int32_t ffk_layer_norm(const void* x, const float* weight, const float* bias, vo
 /*
  * Triangle multiplicative update, outgoing (outgoing = 1) or incoming (0), including
  * the LayerNorm + gated projections prologue and the centre norm + output projection +
- * output gate epilogue. d_pair = d_hidden = 128.
+ * output gate epilogue. d_pair = d_hidden = 128 runs the fused kernels; other widths (d_pair
+ * a multiple of 64 up to 256, d_hidden a multiple of 64 up to 768: the template stack's)
+ * run the generic path with a larger workspace.
  * Replaces: engine TriangleMultiplication.forward / `triangle_multiplicative_update`
  * (equations src/foldforge/models/checkpoints/legacy/reference/triangle.py:19-49,
  * engine parameters legacy/released.py:135-173; op name "trimul",
@@ -77,8 +79,10 @@ int32_t ffk_triangle_multiplication(
 /*
  * Triangle attention around the starting (starting = 1) or ending (0) node: LayerNorm,
  * pair bias, q/k/v/gate projections, flash attention with key mask, gate, output
- * projection. d_pair = 128, n_head * d_head = 128, d_head = 32. transposed_bias = 1
- * takes the ending node's bias from the transposed pair (OpenFold lineage).
+ * projection. d_pair = 128 with 4 heads x 32 runs the fused kernels; d_pair 64 / 128 / 256
+ * with at most 32 heads of 8 to 32 channels (n_head * d_head a multiple of 64, batch * n at
+ * most 65535) runs the generic path. transposed_bias = 1 takes the ending node's bias from
+ * the transposed pair (OpenFold lineage).
  * Replaces: engine TriangleAttention(AF3).forward / `triangle_attention`
  * (src/foldforge/models/checkpoints/legacy/attention.py:108-163,
  * legacy/reference/attention.py:77-100; engine parameters legacy/released.py:176-208;

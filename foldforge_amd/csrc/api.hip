@@ -103,19 +103,33 @@ struct Carver {
 
 __global__ __launch_bounds__(256) void pack_bf16(PackJob job) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t first = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   for (int s = 0; s < job.nseg; ++s) {
     const PackSeg sg = job.seg[s];
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < sg.n; i += stride) {
+    for (int64_t i = first; i < sg.n; i += stride) {
       const int64_t j = sg.swap23 ? (i & ~int64_t(12)) | ((i & 4) << 1) | ((i & 8) >> 1) : i;
       sg.dst[i] = (bf16)(sg.src ? sg.src[j] * sg.scale : 0.f);
+    }
+  }
+  if (job.mask) {
+    const int64_t total = (int64_t)job.batch * job.np;
+    for (int64_t i = first; i < total; i += stride) {
+      const int64_t b = i / job.np, s = i - b * job.np;
+      job.maskf[i] = s < job.n && job.mask[b * job.n + s] != 0 ? 1.f : 0.f;
     }
   }
 }
 
 }  // namespace
 
+// One thread per element of the largest segment (at most 1024 workgroups): the weights of one
+// op are a few hundred thousand values, a latency-bound pass either way.
 void launch_pack(const PackJob& job, hipStream_t stream) {
-  pack_bf16<<<dim3(64), 256, 0, stream>>>(job);
+  int64_t most = job.mask ? (int64_t)job.batch * job.np : 0;
+  for (int s = 0; s < job.nseg; ++s) most = job.seg[s].n > most ? job.seg[s].n : most;
+  int64_t blocks = (most + 255) / 256;
+  blocks = blocks < 1 ? 1 : blocks > 1024 ? 1024 : blocks;
+  pack_bf16<<<dim3((unsigned)blocks), 256, 0, stream>>>(job);
 }
 
 // ---------------------------------------------------------------------------------------
@@ -395,6 +409,11 @@ int32_t ffk_triangle_multiplication(
   job.seg[4] = {w_gate, w.wg, (int64_t)d_pair * d_pair, -kLog2e};
   job.seg[5] = {w_out, w.wo, (int64_t)d_pair * d_hidden, 1.f};
   job.nseg = 6;
+  job.mask = key_mask;
+  job.maskf = w.maskf;
+  job.batch = (int)batch;
+  job.n = (int)n;
+  job.np = (int)pad128(n);
   launch_pack(job, st);
   TrimulArgs a;
   a.z = static_cast<const bf16*>(z);

@@ -215,6 +215,11 @@ struct PackSeg {
 struct PackJob {
   PackSeg seg[8];
   int nseg;
+  // optional: the key mask as fp32 rows maskf[b][s] = mask[b][s] ? 1 : 0 (s < n), 0 for
+  // n <= s < np (mask NULL: none)
+  const uint8_t* mask;
+  float* maskf;
+  int batch, n, np;
 };
 void launch_pack(const PackJob& job, hipStream_t stream);
 

@@ -396,17 +396,6 @@ __global__ __launch_bounds__(256, 2) void trimul_output(
   }
 }
 
-// maskf[b][s] = key_mask[b][s] ? 1 : 0 for s < n, 0 for n <= s < np.
-__global__ __launch_bounds__(256) void trimul_mask(const uint8_t* __restrict__ mask,
-                                                   float* __restrict__ maskf, int batch, int n,
-                                                   int np) {
-  const int64_t total = (int64_t)batch * np;
-  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-    const int64_t b = i / np, s = i % np;
-    maskf[i] = (s < n && mask[b * n + s] != 0) ? 1.f : 0.f;
-  }
-}
-
 static int persistent_grid(int ntiles, int per_cu) {
   return max(1, min(ntiles, cu_count() * per_cu));
 }
@@ -414,9 +403,6 @@ static int persistent_grid(int ntiles, int per_cu) {
 void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
   const int np = a.np;
   const int tiles_p = a.batch * np * (np / kPT);
-  const int64_t mtotal = (int64_t)a.batch * np;
-  trimul_mask<<<dim3((unsigned)((mtotal + 255) / 256 < 1024 ? (mtotal + 255) / 256 : 1024)), 256, 0,
-                stream>>>(a.mask, a.maskf, a.batch, a.n, np);
   trimul_project<<<persistent_grid(tiles_p, 1), 512, 0, stream>>>(
       a.z, a.maskf, a.ln_w, a.ln_b, a.wp, a.A, a.B, a.batch, a.n, np, a.outgoing, a.eps);
   const int nt = np / kCT;

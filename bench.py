@@ -71,6 +71,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--trunk-only", action="store_true")
     ap.add_argument("--no-reference-backend", action="store_true",
                     help="with --trunk-only: skip the engine pytorch backend's trunk run")
+    ap.add_argument("--no-graph", action="store_true",
+                    help="with --trunk-only: skip the captured-graph replays (N = 128 and 512)")
     ap.add_argument("--ladder", action="store_true")
     ap.add_argument("--msa", action="store_true",
                     help="time the MSA-stack ops at L = 256 / 384 tokens, 512 MSA rows")
@@ -517,7 +519,8 @@ def main() -> int:
     if args.trunk_only:
         trunk = trunk_measure(512, max(1, args.steps // 10), pytorch_too=not args.no_reference_backend,
                               cpu_too=not args.no_cpu_baseline)
-        trunk["graph"] = [graph_measure(n) for n in (128, 512)]
+        if not args.no_graph:
+            trunk["graph"] = [graph_measure(n) for n in (128, 512)]
         print(json.dumps({"trunk": trunk}), flush=True)
         return 0
     dev = torch.device("cuda:0")

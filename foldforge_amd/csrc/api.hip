@@ -174,7 +174,7 @@ int64_t pad32(int64_t n);
 
 struct TriattnWs {
   bf16 *wqkv, *wb, *wg, *wo, *q, *k, *vt, *o, *gate;
-  float *bias, *og;
+  float *bias, *og, *maskf;
   size_t bytes;
 };
 TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d) {
@@ -203,6 +203,7 @@ TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d
   w.vt = cv.take<bf16>((size_t)batch * heads * np * np * d);
   w.bias = cv.take<float>((size_t)batch * heads * np * np);
   w.o = cv.take<bf16>((size_t)batch * n * n * hd);
+  w.maskf = cv.take<float>((size_t)batch * np);
   w.bytes = cv.used;
   return w;
 }
@@ -558,10 +559,16 @@ int32_t ffk_triangle_attention(
   job.seg[5] = {w_gate, w.wg, m, -kLog2e};  // sigmoid(x) = 1 / (1 + 2^(-log2(e) x))
   job.seg[6] = {w_out, w.wo, m, 1.f};
   job.nseg = 7;
+  job.mask = key_mask;
+  job.maskf = w.maskf;
+  job.batch = (int)batch;
+  job.n = (int)n;
+  job.np = (int)pad128(n);
   launch_pack(job, st);
   TriattnArgs a;
   a.z = static_cast<const bf16*>(z);
   a.mask = key_mask;
+  a.maskf = w.maskf;
   a.ln_w = ln_pair_w;
   a.ln_b = ln_pair_b;
   a.wqkv = w.wqkv;

@@ -262,6 +262,10 @@ __device__ __forceinline__ void dma16_stream(const void* sbase, uint32_t voff, u
   asm volatile("global_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "{m0}"(m0)
                : "memory");
 }
+// Same for 4 bytes per lane: lane L copies sbase + voff to LDS byte address m0 + 4 L.
+__device__ __forceinline__ void dma4(const void* sbase, uint32_t voff, uint32_t m0) {
+  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+}
 // Wait until at most N vector-memory operations of this wave are in flight and its LDS
 // operations are done.
 template <int N>

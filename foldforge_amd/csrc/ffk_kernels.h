@@ -30,6 +30,7 @@ void launch_trimul_contract(const bf16* A, const bf16* B, bf16* P, int64_t plane
 struct TriattnArgs {
   const bf16* z;
   const uint8_t* mask;
+  const float* maskf;  // [batch][np] key mask as 1 / 0, zero past n
   const float *ln_w, *ln_b;
   const bf16* wqkv;  // [3 * 128][128], query rows carry d^-1/2 * log2(e)
   const bf16* wb;    // [32][128], rows < heads carry log2(e) * to_bias, others zero

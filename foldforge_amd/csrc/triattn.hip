@@ -61,137 +61,211 @@ __device__ __forceinline__ int64_t bias_index(int64_t bh, int64_t nb, int64_t qu
   return ((((bh * nb + (query >> 5)) * nb + (key >> 5)) * 4 + v) * 64 + lane) * 4 + e;
 }
 
-// Position of key index s inside its 16-key group as stored in v^T (bits 2 and 3 exchanged).
-__device__ __forceinline__ int vkey_slot(int s) { return (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1); }
-
 constexpr int kPT = 64;        // positions per projection / output tile
-constexpr int kQS = 32 + 8;     // LDS row stride of a staged [position][d] q / k tile
-constexpr int kVPS = kPT + 8;   // LDS row stride of a staged [d][position] v^T tile
 
-// Persistent, weight-stationary: tiles are (batch, row r of the padded grid, 64 positions
-// along the attention row); wave w owns head w (its q, k, v^T weight rows in registers)
-// and wave 0 also the pair bias (4 heads padded to 32 rows).
-__global__ __launch_bounds__(256, 2) void triattn_project(
-    const bf16* __restrict__ z, const uint8_t* __restrict__ mask, const float* __restrict__ ln_w,
+// Persistent, weight-stationary, one barrier per tile. Tiles are (batch, row r of the padded
+// grid, 64 positions along the attention row). Waves 0-3 hold the query and key rows of
+// head w, waves 4-7 the value rows of head w - 4; waves 4 and 5 also project the pair bias
+// of the tile's first and second 32 positions (4 heads padded to 32 rows). The z tiles
+// arrive by LDS DMA two tiles ahead in a three-slot ring and are normalised in place one
+// tile ahead, so the LayerNorm and the loads overlap the MFMAs and stores of other waves.
+// Each wave stages its outputs in LDS of its own and writes 16 bytes per lane: q and k as
+// 64-byte position rows, v^T as 128-byte runs of the 64 positions of one channel.
+__global__ __launch_bounds__(512, 2) void triattn_project(
+    const bf16* __restrict__ z, const float* __restrict__ maskf, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ wqkv, const bf16* __restrict__ wb,
     bf16* __restrict__ qo, bf16* __restrict__ ko, bf16* __restrict__ vto, float* __restrict__ bo,
-    int batch, int n, int np, int heads, int starting, int transposed_bias, float eps) {
-  __shared__ __attribute__((aligned(16))) bf16 xh[kPT * kRow];
-  __shared__ __attribute__((aligned(16))) bf16 sq[4][kPT * kQS];
-  __shared__ __attribute__((aligned(16))) bf16 sk[4][kPT * kQS];
-  __shared__ __attribute__((aligned(16))) bf16 sv[4][32 * kVPS];
-  __shared__ float keep[kPT];
-  __shared__ __attribute__((aligned(16))) bf16 wbl[4 * 128];  // the (at most 4) bias rows
+    int batch, int n, int np, int starting, int transposed_bias, float eps) {
+  constexpr int NB = 3, H = 4;
+  __shared__ __attribute__((aligned(16))) bf16 zt[NB][kPT * 128];  // raw z, then LN(z) (off128)
+  __shared__ __attribute__((aligned(16))) bf16 sqk[4][32 * 32];    // [position][d], q then k
+  __shared__ __attribute__((aligned(16))) bf16 svt[4][32 * kPT];   // [d][key slot]
+  __shared__ __attribute__((aligned(16))) float keep[NB][kPT];     // key mask per position
+  __shared__ __attribute__((aligned(16))) bf16 wbl[H * 128];       // the pair-bias rows
+  __shared__ float lnp[2][128];                                    // LayerNorm affine
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
-  const bool has_head = wave < heads;
-  WFrag wq, wk, wv;
-  if (has_head) {
-    load_wfrag(wq, wqkv, 32 * wave, li, g);
-    load_wfrag(wk, wqkv, 128 + 32 * wave, li, g);
-    load_wfrag(wv, wqkv, 256 + 32 * wave, li, g);
-    settle(wq);
-    settle(wk);
-    settle(wv);
+  const int lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const bool qk = wave < 4;
+  const int head = wave & 3;
+  if (tid < 256) lnp[tid >> 7][tid & 127] = (tid < 128 ? ln_w : ln_b)[tid & 127];
+  for (int e = tid; e < H * 128; e += 512) wbl[e] = wb[e];  // published by the first barrier
+  WFrag w0, w1;
+  load_wfrag(w0, wqkv, qk ? 32 * head : 256 + 32 * head, li, g);
+  settle(w0);
+  if (qk) {
+    load_wfrag(w1, wqkv, 128 + 32 * head, li, g);
+    settle(w1);
   }
-  for (int e = tid; e < 4 * 128; e += 256) wbl[e] = wb[e];
   // The bias entry at tile position t is (query r, key s0 + t), except for the AF3 ending
   // node (bias from the un-transposed pair), where it is (query s0 + t, key r).
   const bool key_major = !starting && !transposed_bias;
   const int nsb = np / kPT;
   const int64_t nb = np / 32;
   const int ntiles = batch * np * nsb;
-#pragma unroll 1
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  auto where = [&](int tile, int& b, int& r, int& s0, int& valid) {
     const int sb = tile % nsb;
-    const int r = (tile / nsb) % np;
-    const int b = tile / (nsb * np);
-    const int s0 = sb * kPT;
-    const int valid = (r < n) ? max(0, min(kPT, n - s0)) : 0;
+    r = (tile / nsb) % np;
+    b = tile / (nsb * np);
+    s0 = sb * kPT;
+    valid = (r < n) ? max(0, min(kPT, n - s0)) : 0;
+  };
+  // This wave's 2 one-KB pieces (positions 8 wave .. 8 wave + 7) of a tile's z rows into ring
+  // slot buf (positions past the end re-read a real row, zeroed by the LayerNorm); wave 7
+  // also fetches the tile's 64 key-mask values. A tile index past the end fetches tile 0
+  // again, so that every wave always has the same number of transfers in flight.
+  auto z_dma = [&](int tile, int buf) {
+    int b, r, s0, valid;
+    where(tile < ntiles ? tile : 0, b, r, s0, valid);
     const bf16* base = z;
-    int64_t stride = 128;
+    uint32_t stride = 256;  // bytes between consecutive positions
     if (valid > 0) {
       if (starting) {
         base = z + (((int64_t)b * n + r) * n + s0) * 128;
       } else {
         base = z + (((int64_t)b * n + s0) * n + r) * 128;
-        stride = (int64_t)n * 128;
+        stride = (uint32_t)n * 256;
       }
     }
-    __syncthreads();
-    ln_tile_128<kPT>(base, stride, valid, ln_w, ln_b, eps, xh, nullptr);
-    if (tid < kPT) {
-      const int key = key_major ? r : s0 + tid;
-      keep[tid] = (key < n && mask[(int64_t)b * n + key] != 0) ? 1.f : 0.f;
+    const int last = valid > 0 ? valid - 1 : 0;
+    const uint32_t dst = lds_addr(&zt[buf][0]);
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int piece = 2 * wave + u, pos = 4 * piece + (lane >> 4);
+      const int pe = pos < last ? pos : last;
+      dma16_stream(base, pe * stride + 16 * ((lane & 15) ^ (pos & 15)), dst + 1024 * piece);
     }
-    __syncthreads();
+    if (wave == 7) {
+      const float* mrow = maskf + (int64_t)b * np + (key_major ? r : s0);
+      dma4(mrow, key_major ? 0u : 4u * lane, lds_addr(&keep[buf][0]));
+    }
+  };
+  const int step = gridDim.x;
+  if ((int)blockIdx.x >= ntiles) return;
+  z_dma(blockIdx.x, 0);
+  z_dma(blockIdx.x + step, 1);
+  if (wave == 7)
+    wait_vm_lds<3>();  // this wave's transfers of the first tile landed
+  else
+    wait_vm_lds<2>();
+  __syncthreads();
+  {
+    int b, r, s0, valid;
+    where(blockIdx.x, b, r, s0, valid);
+    ln_inplace_swz<kPT, 512>(zt[0], valid, lnp[0], lnp[1], eps);
+  }
+  const int sw = (li >> 2) & 3;  // 16-byte column swizzle of a staged q / k row
+  const int swv = (li >> 1) & 7;  // of a staged v^T row
+  int buf = 0, k = 0;
 #pragma unroll 1
-    for (int pt = 0; pt < kPT / 32; ++pt) {
-      const bf16* xrow = xh + (pt * 32 + li) * kRow + 8 * g;
-      if (has_head) {
-        f32x16 aq = zero16(), ak = zero16(), av = zero16();
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const bf16x8 x = ld8(xrow + 16 * kk);
-          aq = mfma32(x, wq.k[kk], aq);  // D[position][d]
-          ak = mfma32(x, wk.k[kk], ak);
-          av = mfma32(wv.k[kk], x, av);  // D[d][position]
-        }
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-          const int row = acc_row(q, g);
-          sq[wave][(pt * 32 + row) * kQS + li] = (bf16)aq[q];
-          sk[wave][(pt * 32 + row) * kQS + li] = (bf16)ak[q];
-          sv[wave][row * kVPS + vkey_slot(pt * 32 + li)] = (bf16)av[q];
-        }
-      }
-      if (wave == 0) {
-        f32x16 ab = zero16();
-        const bf16x8 zero8 = {};
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk) {
-          const bf16x8 wrow = li < 4 ? ld8(&wbl[li * 128 + 16 * kk + 8 * g]) : zero8;
-          ab = mfma32(wrow, ld8(xrow + 16 * kk), ab);
-        }
-        // D[head][position]: heads are rows 0..3 = registers 0..3 of lane group 0
-        const float kp = keep[pt * 32 + li];
-        const int64_t s = s0 + pt * 32 + li;
-        const int64_t query = key_major ? s : r;
-        const int64_t key = key_major ? r : s;
-        if (g == 0) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            if (q < heads) {
-              const float v = kp != 0.f ? ab[q] : -INFINITY;
-              bo[bias_index((int64_t)b * heads + q, nb, query, key)] = v;
-            }
-          }
-        }
-      }
-    }
+  for (int tile = blockIdx.x; tile < ntiles; tile += step, ++k, buf = buf == NB - 1 ? 0 : buf + 1) {
+    int b, r, s0, valid;
+    where(tile, b, r, s0, valid);
+    const int nbuf = buf == NB - 1 ? 0 : buf + 1, fbuf = nbuf == NB - 1 ? 0 : nbuf + 1;
+    // this wave's transfers of tile + step have landed (issued after them: only the previous
+    // tile's stores, 8 on waves 0-5 and 4 on waves 6-7); the barrier publishes everyone's
+    // pieces and normalised rows and retires the previous tile's reads of ring slot fbuf
+    if (k == 0)
+      wait_vm_lds<0>();
+    else if (wave < 6)
+      wait_vm_lds<8>();
+    else
+      wait_vm_lds<4>();
     __syncthreads();
-    if (has_head) {
-      const int64_t bh = (int64_t)b * heads + wave;
-      // q / k: 64 positions x 64 bytes, contiguous; 16-byte stores
+    z_dma(tile + 2 * step, fbuf);
+    const bf16* xh = zt[buf];
+    const int64_t bh = (int64_t)b * H + head;
+    if (qk) {
+      bf16* st = sqk[head];
       bf16* qd = qo + ((bh * np + r) * np + s0) * 32;
       bf16* kd = ko + ((bh * np + r) * np + s0) * 32;
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int chunk = lane + 64 * u;
-        const int p = chunk >> 2, d8 = chunk & 3;
-        *reinterpret_cast<bf16x8*>(qd + p * 32 + 8 * d8) = ld8(&sq[wave][p * kQS + 8 * d8]);
-        *reinterpret_cast<bf16x8*>(kd + p * 32 + 8 * d8) = ld8(&sk[wave][p * kQS + 8 * d8]);
+      for (int pt = 0; pt < kPT / 32; ++pt) {
+        f32x16 aq = zero16(), ak = zero16();
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) {
+          const bf16x8 x = ld8(&xh[off128(pt * 32 + li, 2 * kk + g)]);
+          aq = mfma32(w0.k[kk], x, aq);  // D[d][position]: lane position li, register d
+          ak = mfma32(w1.k[kk], x, ak);
+        }
+#pragma unroll
+        for (int which = 0; which < 2; ++which) {
+          const f32x16& acc = which ? ak : aq;
+          // d = 8 j + 4 g + e: row li, 16-byte column j (swizzled), 8 bytes at 4 g
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            bf16x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = (bf16)acc[4 * j + e];
+            *reinterpret_cast<bf16x4*>(&st[li * 32 + 8 * (j ^ sw) + 4 * g]) = v;
+          }
+          // the stage is this wave's own: LDS operations of a wave complete in order
+          __builtin_amdgcn_wave_barrier();
+          bf16* dst = (which ? kd : qd) + pt * 32 * 32;
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int chunk = lane + 64 * u;
+            const int p = chunk >> 2, c = chunk & 3;
+            *reinterpret_cast<bf16x8*>(dst + p * 32 + 8 * c) = ld8(&st[p * 32 + 8 * (c ^ ((p >> 2) & 3))]);
+          }
+          __builtin_amdgcn_wave_barrier();
+        }
       }
-      // v^T: 32 rows of d x 64 positions
+    } else {
+      bf16* st = svt[head];
+#pragma unroll
+      for (int pt = 0; pt < kPT / 32; ++pt) {
+        f32x16 av = zero16();
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+          av = mfma32(ld8(&xh[off128(pt * 32 + li, 2 * kk + g)]), w0.k[kk], av);  // D[position][d]
+        // position 8 j + 4 g + e sits at key slot 16 (j >> 1) + 8 g + 4 (j & 1) + e: row d = li,
+        // 16-byte column 4 pt + 2 (j >> 1) + g (swizzled), 8 bytes at 4 (j & 1)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          bf16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = (bf16)av[4 * j + e];
+          const int c = 4 * pt + 2 * (j >> 1) + g;
+          *reinterpret_cast<bf16x4*>(&st[li * kPT + 8 * (c ^ swv) + 4 * (j & 1)]) = v;
+        }
+        if (wave == 4 + pt) {
+          f32x16 ab = zero16();
+          const bf16x8 zero8 = {};
+#pragma unroll
+          for (int kk = 0; kk < 8; ++kk) {
+            const bf16x8 wrow = li < H ? ld8(&wbl[li * 128 + 16 * kk + 8 * g]) : zero8;
+            ab = mfma32(wrow, ld8(&xh[off128(pt * 32 + li, 2 * kk + g)]), ab);
+          }
+          // D[head][position]: heads are rows 0..3 = registers 0..3 of lane group 0
+          const float kp = keep[buf][pt * 32 + li];
+          const int64_t s = s0 + pt * 32 + li;
+          const int64_t query = key_major ? s : r;
+          const int64_t key = key_major ? r : s;
+          if (g == 0) {
+#pragma unroll
+            for (int q = 0; q < H; ++q)
+              bo[bias_index((int64_t)b * H + q, nb, query, key)] = kp != 0.f ? ab[q] : -INFINITY;
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      // 32 rows of d x 64 key slots: 128 contiguous bytes per row
       bf16* vd = vto + ((bh * np + r) * 32) * np + s0;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int chunk = lane + 64 * u;
-        const int d = chunk >> 3, p8 = chunk & 7;
-        *reinterpret_cast<bf16x8*>(vd + (int64_t)d * np + 8 * p8) = ld8(&sv[wave][d * kVPS + 8 * p8]);
+        const int d = chunk >> 3, c = chunk & 7;
+        *reinterpret_cast<bf16x8*>(vd + (int64_t)d * np + 8 * c) = ld8(&st[d * kPT + 8 * (c ^ ((d >> 1) & 7))]);
       }
     }
+    if (tile + step < ntiles) {
+      int nb2, nr, ns0, nvalid;
+      where(tile + step, nb2, nr, ns0, nvalid);
+      ln_inplace_swz<kPT, 512>(zt[nbuf], nvalid, lnp[0], lnp[1], eps);
+    }
   }
+  wait_vm_lds<0>();  // no LDS write may land after exit
 }
 
 struct __attribute__((aligned(16))) FlashLds {
@@ -557,9 +631,9 @@ void launch_flash(const FlashArgs& a, hipStream_t stream) {
 void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
   const int np = a.np;
   const int tiles_p = a.batch * np * (np / kPT);
-  triattn_project<<<persistent_grid(tiles_p, 2), 256, 0, stream>>>(
-      a.z, a.mask, a.ln_w, a.ln_b, a.wqkv, a.wb, a.q, a.k, a.vt, a.bias, a.batch, a.n, np,
-      a.heads, a.starting, a.transposed_bias, a.eps);
+  triattn_project<<<persistent_grid(tiles_p, 1), 512, 0, stream>>>(
+      a.z, a.maskf, a.ln_w, a.ln_b, a.wqkv, a.wb, a.q, a.k, a.vt, a.bias, a.batch, a.n, np,
+      a.starting, a.transposed_bias, a.eps);
   FlashArgs f;
   f.q = a.q;
   f.k = a.k;

@@ -273,11 +273,12 @@ __device__ __forceinline__ void wait_vm_lds() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
 }
 
-// LayerNorm in place (fp32 statistics and affine) over the rows 0 .. TM - 1 of an off128
-// tile, NT threads, 16 lanes per row; rows >= valid become zeros.
+// LayerNorm (fp32 statistics and affine) of the rows 0 .. TM - 1 of an off128 tile src into
+// the off128 tile dst (which may be src), NT threads, 16 lanes per row; rows >= valid become
+// zeros.
 template <int TM, int NT>
-__device__ __forceinline__ void ln_inplace_swz(bf16* buf, int valid, const float* w, const float* b,
-                                               float eps) {
+__device__ __forceinline__ void ln_swz(const bf16* src, bf16* dst, int valid, const float* w,
+                                       const float* b, float eps) {
   const int sub = threadIdx.x & 15, pos0 = threadIdx.x >> 4;
   float wv[8], bv[8];
 #pragma unroll
@@ -288,8 +289,7 @@ __device__ __forceinline__ void ln_inplace_swz(bf16* buf, int valid, const float
 #pragma unroll
   for (int it = 0; it < TM / (NT / 16); ++it) {
     const int t = pos0 + (NT / 16) * it;
-    bf16x8* p = reinterpret_cast<bf16x8*>(&buf[off128(t, sub)]);
-    const bf16x8 raw = *p;
+    const bf16x8 raw = *reinterpret_cast<const bf16x8*>(&src[off128(t, sub)]);
     float x[8];
     float s = 0.f;
 #pragma unroll
@@ -309,8 +309,13 @@ __device__ __forceinline__ void ln_inplace_swz(bf16* buf, int valid, const float
     const bool real = t < valid;
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = real ? (bf16)(x[e] * rstd * wv[e] + bv[e]) : (bf16)0.f;
-    *p = o;
+    *reinterpret_cast<bf16x8*>(&dst[off128(t, sub)]) = o;
   }
+}
+template <int TM, int NT>
+__device__ __forceinline__ void ln_inplace_swz(bf16* buf, int valid, const float* w, const float* b,
+                                               float eps) {
+  ln_swz<TM, NT>(buf, buf, valid, w, b, eps);
 }
 
 // Load and LayerNorm in one step (see ln_load / ln_finish).

@@ -516,21 +516,31 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
   }
 }
 
-// out = z + (sigmoid(LN_pair(z) W_g^T) * o) W_out^T. Persistent over tiles of 64 positions
-// along a row of z; wave w owns gate channels and output channels 32 w .. 32 w + 31.
-__global__ __launch_bounds__(256, 2) void triattn_output(
+// out = z + (sigmoid(LN(z) W_g^T) * o) W_out^T over tiles of 64 consecutive pairs of one z row
+// (z, o and out share the [b][i][j][128] layout, so a tile is 16 contiguous KB of each).
+// Persistent, one workgroup of 8 waves per CU; wave w owns output channels 32 (w & 3) ..
+// + 31 of positions 32 (w >> 2) .. + 31, for the gate and for the output projection. z and o
+// tiles arrive by LDS DMA two tiles ahead (three-slot rings); LN(z) of the next tile is
+// computed during the current one. A step: the gate times o, in place in the o slot; LN of
+// the next tile; a barrier; the output projection plus the residual, in place in the z slot,
+// and the stores (16 bytes per lane, 64-byte runs per position).
+__global__ __launch_bounds__(512, 2) void triattn_output(
     const bf16* __restrict__ z, const bf16* __restrict__ o, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ wg, const bf16* __restrict__ wo,
     bf16* __restrict__ out, int batch, int n, int residual, float eps) {
-  __shared__ __attribute__((aligned(16))) bf16 zr[kPT * kRow];  // raw z, then the output tile
-  __shared__ __attribute__((aligned(16))) bf16 xh[kPT * kRow];
-  __shared__ __attribute__((aligned(16))) bf16 ot[kPT * kRow];  // o, then sigmoid(gate) * o
+  constexpr int NB = 3;
+  __shared__ __attribute__((aligned(16))) bf16 zs[NB][kPT * 128];  // raw z, then out (off128)
+  __shared__ __attribute__((aligned(16))) bf16 os[NB][kPT * 128];  // o, then gate * o (off128)
+  __shared__ __attribute__((aligned(16))) bf16 xh[2][kPT * 128];   // LN(z) (off128)
+  __shared__ float lnp[2][128];
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
-  const int f = 32 * wave + li;
+  const int lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cb = wave & 3, pt = wave >> 2;
+  if (tid < 256) lnp[tid >> 7][tid & 127] = (tid < 128 ? ln_w : ln_b)[tid & 127];
   WFrag fg, fo;
-  load_wfrag(fg, wg, 32 * wave, li, g);
-  load_wfrag(fo, wo, 32 * wave, li, g);
+  load_wfrag(fg, wg, 32 * cb, li, g);
+  load_wfrag(fo, wo, 32 * cb, li, g);
   settle(fg);
   settle(fo);
   const int njb = (n + kPT - 1) / kPT;
@@ -543,77 +553,101 @@ __global__ __launch_bounds__(256, 2) void triattn_output(
     valid = min(kPT, n - j0);
     return (((int64_t)b * n + i) * n + j0) * 128;
   };
-  // the next tile's z and o (64 positions x 128 channels), loaded during the current one
-  LnTile<kPT, 256> zt;
-  bf16x8 ov[4];
-  auto issue = [&](int tile) {
+  // This wave's 2 one-KB pieces of the tile's z and of its o into ring slot buf (positions
+  // past the end re-read the last real one); a tile index past the end fetches tile 0 again,
+  // so every wave always has the same number of transfers in flight.
+  auto dma = [&](int tile, int buf) {
     int valid;
-    const int64_t zoff = where(tile, valid);
-    ln_load(zt, z + zoff, 128, valid);
+    const int64_t off = where(tile < ntiles ? tile : 0, valid);
+    const uint32_t dz = lds_addr(&zs[buf][0]), dov = lds_addr(&os[buf][0]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int chunk = tid + 256 * u;
-      const int p = chunk >> 4, c8 = chunk & 15;
-      bf16x8 v = {};
-      if (p < valid) v = ld8(o + zoff + (int64_t)p * 128 + 8 * c8);
-      ov[u] = v;
+    for (int u = 0; u < 2; ++u) {
+      const int piece = 2 * wave + u, pos = 4 * piece + (lane >> 4);
+      const int pe = pos < valid ? pos : valid - 1;
+      const uint32_t voff = pe * 256 + 16 * ((lane & 15) ^ (pos & 15));
+      dma16_stream(z + off, voff, dz + 1024 * piece);
+      dma16_stream(o + off, voff, dov + 1024 * piece);
     }
   };
-  if ((int)blockIdx.x < ntiles) issue(blockIdx.x);
-#pragma unroll 1
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  const int step = gridDim.x;
+  if ((int)blockIdx.x >= ntiles) return;
+  dma(blockIdx.x, 0);
+  dma(blockIdx.x + step, 1);
+  wait_vm_lds<4>();  // this wave's transfers of the first tile landed
+  __syncthreads();
+  {
     int valid;
-    const int64_t zoff = where(tile, valid);
+    where(blockIdx.x, valid);
+    ln_swz<kPT, 512>(zs[0], xh[0], valid, lnp[0], lnp[1], eps);
+  }
+  const int p0 = 32 * pt + li;  // this lane's position in both products
+  int buf = 0, k = 0, prev_valid = kPT;
+#pragma unroll 1
+  for (int tile = blockIdx.x; tile < ntiles; tile += step, ++k, buf = buf == NB - 1 ? 0 : buf + 1) {
+    int valid;
+    const int64_t off = where(tile, valid);
+    const int nbuf = buf == NB - 1 ? 0 : buf + 1, fbuf = nbuf == NB - 1 ? 0 : nbuf + 1;
+    // this wave's transfers of tile + step have landed (issued after them: the previous
+    // tile's 2 stores, fewer for a partial tile); the barrier publishes everyone's pieces and
+    // LN(z), and retires the previous tile's accesses to ring slot fbuf
+    if (k == 0 || prev_valid < kPT)
+      wait_vm_lds<0>();
+    else
+      wait_vm_lds<2>();
     __syncthreads();
+    dma(tile + 2 * step, fbuf);
+    // gate: D[channel][position], lane position p0, registers channels 32 cb + 8 j + 4 g + e
+    {
+      const bf16* xr = xh[k & 1];
+      f32x16 ag = zero16();
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int chunk = tid + 256 * u;
-      const int p = chunk >> 4, c8 = chunk & 15;
-      *reinterpret_cast<bf16x8*>(&ot[p * kRow + 8 * c8]) = ov[u];
-    }
-    ln_finish(zt, valid, ln_w, ln_b, eps, xh, zr);
-    __syncthreads();
-    if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);
-    f32x16 ag[kPT / 32];
+      for (int kk = 0; kk < 8; ++kk) ag = mfma32(fg.k[kk], ld8(&xr[off128(p0, 2 * kk + g)]), ag);
+      bf16* orow = os[buf];
 #pragma unroll
-    for (int pt = 0; pt < kPT / 32; ++pt) {
-      const bf16* xrow = xh + (pt * 32 + li) * kRow + 8 * g;
-      ag[pt] = zero16();
+      for (int j = 0; j < 4; ++j) {
+        bf16x4* po = reinterpret_cast<bf16x4*>(&orow[off128(p0, 4 * cb + j) + 4 * g]);
+        const bf16x4 ov = *po;
+        bf16x4 v;
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) ag[pt] = mfma32(ld8(xrow + 16 * kk), fg.k[kk], ag[pt]);
-    }
-    // gate times o, in place (each wave rewrites only its own 32 channels)
-#pragma unroll
-    for (int pt = 0; pt < kPT / 32; ++pt)
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int p = pt * 32 + acc_row(q, g);
-        ot[p * kRow + f] = (bf16)(sigmoid_scaled(ag[pt][q]) * (float)ot[p * kRow + f]);
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)(sigmoid_scaled(ag[4 * j + e]) * (float)ov[e]);
+        *po = v;
       }
+    }
+    if (tile + step < ntiles) {
+      int nvalid;
+      where(tile + step, nvalid);
+      ln_swz<kPT, 512>(zs[nbuf], xh[(k + 1) & 1], nvalid, lnp[0], lnp[1], eps);
+    }
     __syncthreads();
-#pragma unroll
-    for (int pt = 0; pt < kPT / 32; ++pt) {
-      const bf16* yrow = ot + (pt * 32 + li) * kRow + 8 * g;
+    // output projection: D[channel][position] over the gated o of all 128 channels
+    {
+      const bf16* gr = os[buf];
       f32x16 ao = zero16();
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk) ao = mfma32(ld8(yrow + 16 * kk), fo.k[kk], ao);
+      for (int kk = 0; kk < 8; ++kk) ao = mfma32(fo.k[kk], ld8(&gr[off128(p0, 2 * kk + g)]), ao);
+      bf16* zrow = zs[buf];
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int p = pt * 32 + acc_row(q, g);
-        float val = ao[q];
-        if (residual) val += (float)zr[p * kRow + f];
-        zr[p * kRow + f] = (bf16)val;
+      for (int j = 0; j < 4; ++j) {
+        bf16x4* pz = reinterpret_cast<bf16x4*>(&zrow[off128(p0, 4 * cb + j) + 4 * g]);
+        const bf16x4 zv = *pz;
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)(ao[4 * j + e] + (residual ? (float)zv[e] : 0.f));
+        *pz = v;
+      }
+      // the block is this wave's own: LDS operations of a wave complete in order
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int chunk = lane + 64 * u;
+        const int p = 32 * pt + (chunk >> 2), c = 4 * cb + (chunk & 3);
+        if (p < valid)
+          *reinterpret_cast<bf16x8*>(out + off + (int64_t)p * 128 + 8 * c) = ld8(&zrow[off128(p, c)]);
       }
     }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int chunk = tid + 256 * u;
-      const int p = chunk >> 4, c8 = chunk & 15;
-      if (p < valid)
-        *reinterpret_cast<bf16x8*>(out + zoff + (int64_t)p * 128 + 8 * c8) = ld8(&zr[p * kRow + 8 * c8]);
-    }
+    prev_valid = valid;
   }
+  wait_vm_lds<0>();  // no LDS write may land after exit
 }
 
 static int persistent_grid(int ntiles, int per_cu) {
@@ -659,7 +693,7 @@ void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
   }
   launch_flash(f, stream);
   const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);
-  triattn_output<<<persistent_grid(tiles_o, 2), 256, 0, stream>>>(
+  triattn_output<<<persistent_grid(tiles_o, 1), 512, 0, stream>>>(
       a.z, a.o, a.ln_w, a.ln_b, a.wg, a.wo, a.out, a.batch, a.n, a.residual, a.eps);
 }
 

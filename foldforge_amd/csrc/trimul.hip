@@ -263,31 +263,35 @@ __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ 
     }
 }
 
-// out[b,i,j,:] = z + (LN_out(P[b,:,i,j]) W_out^T) * sigmoid(LN_pair(z[b,i,j]) W_g^T).
-// Persistent over tiles of 64 positions along a row of z; wave w owns output channels
-// 32 w .. 32 w + 31 of both projections (weights in registers).
-__global__ __launch_bounds__(256, 2) void trimul_output(
+// out[b,i,j,:] = z + (LN_out(P[b,:,i,j]) W_out^T) * sigmoid(LN_pair(z[b,i,j]) W_g^T) over tiles
+// of 64 consecutive pairs of one z row. Persistent, one workgroup of 8 waves per CU; wave w
+// owns output channels 32 (w & 3) .. + 31 of positions 32 (w >> 2) .. + 31 in both
+// projections. z tiles (64 positions x 256 bytes) and P tiles (128 channel rows x 128 bytes)
+// arrive by LDS DMA two tiles ahead in three-slot rings. Two barriers per tile, and the
+// normalisations run ahead of the products: during tile k the workgroup normalises P of
+// tile k (statistics gathered over the two previous phases), projects and stores tile k,
+// and for tile k + 1 computes LN(z), the gate and both passes of P's statistics.
+__global__ __launch_bounds__(512, 2) void trimul_output(
     const bf16* __restrict__ z, const bf16* __restrict__ P, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const float* __restrict__ lno_w,
     const float* __restrict__ lno_b, const bf16* __restrict__ wg, const bf16* __restrict__ wo,
     bf16* __restrict__ out, int batch, int n, int np, int residual, float eps) {
-  constexpr int H = 128;
-  __shared__ __attribute__((aligned(16))) bf16 zr[kPT * kRow];  // raw z, then the output tile
-  __shared__ __attribute__((aligned(16))) bf16 xh[kPT * kRow];
-  __shared__ __attribute__((aligned(16))) bf16 y[kPT * kRow];
-  __shared__ __attribute__((aligned(16))) bf16 pt_[H * kPS];    // P tile, [channel][position]
-  __shared__ float red[4][kPT];
-  __shared__ float lno[2][H];  // centre-norm affine, kept in LDS (not hoisted into registers)
+  constexpr int H = 128, NB = 3;
+  __shared__ __attribute__((aligned(16))) bf16 zs[NB][kPT * 128];  // raw z, then out (off128)
+  __shared__ __attribute__((aligned(16))) bf16 ps[NB][H * kPT];    // P, [channel][position]
+  __shared__ __attribute__((aligned(16))) bf16 xh[kPT * 128];      // LN(z) (off128)
+  __shared__ __attribute__((aligned(16))) bf16 y[kPT * 128];       // LN_out(P) (off128)
+  __shared__ float red[2][2][8][kPT];  // [tile parity][sum, centred squares][wave][position]
+  __shared__ float lnp[4][H];          // LN_pair and LN_out affine
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, g = lane >> 5, li = lane & 31;
-  const int f = 32 * wave + li;  // output channel of this lane
-  if (tid < H) {
-    lno[0][tid] = lno_w[tid];
-    lno[1][tid] = lno_b[tid];
-  }
+  const int lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int cb = wave & 3, pt = wave >> 2;
+  const float* const lsrc[4] = {ln_w, ln_b, lno_w, lno_b};
+  lnp[tid >> 7][tid & 127] = lsrc[tid >> 7][tid & 127];  // published by the first barrier
   WFrag fg, fo;
-  load_wfrag(fg, wg, 32 * wave, li, g);
-  load_wfrag(fo, wo, 32 * wave, li, g);
+  load_wfrag(fg, wg, 32 * cb, li, g);
+  load_wfrag(fo, wo, 32 * cb, li, g);
   settle(fg);
   settle(fo);
   const int njb = (n + kPT - 1) / kPT;
@@ -300,100 +304,148 @@ __global__ __launch_bounds__(256, 2) void trimul_output(
     j0 = jb * kPT;
     valid = min(kPT, n - j0);
   };
-  // the next tile's z and P (128 channels x 64 positions), loaded during the current one
-  LnTile<kPT, 256> zt;
-  bf16x8 pv[4];
-  auto issue = [&](int tile) {
+  // This wave's 2 one-KB pieces of the tile's z (positions past the end re-read the last
+  // real one) and 2 of its P (8 channel rows each; j0 + 63 < np) into ring slot buf; a tile
+  // index past the end fetches tile 0 again, so every wave always has the same number of
+  // transfers in flight.
+  auto dma = [&](int tile, int buf) {
     int b, i, j0, valid;
-    where(tile, b, i, j0, valid);
-    ln_load(zt, z + (((int64_t)b * n + i) * n + j0) * 128, 128, valid);
-    const bf16* pb = P + (int64_t)b * H * plane + (int64_t)i * np + j0;  // j0 + 63 < np
+    where(tile < ntiles ? tile : 0, b, i, j0, valid);
+    const bf16* zb = z + (((int64_t)b * n + i) * n + j0) * 128;
+    const uint32_t dz = lds_addr(&zs[buf][0]), dp = lds_addr(&ps[buf][0]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int chunk = tid + 256 * u;
-      const int c = chunk >> 3, p8 = chunk & 7;
-      pv[u] = ld8(pb + (int64_t)c * plane + 8 * p8);
+    for (int u = 0; u < 2; ++u) {
+      const int piece = 2 * wave + u, pos = 4 * piece + (lane >> 4);
+      const int pe = pos < valid ? pos : valid - 1;
+      dma16_stream(zb, pe * 256 + 16 * ((lane & 15) ^ (pos & 15)), dz + 1024 * piece);
+      const bf16* pb = P + ((int64_t)b * H + 8 * piece) * plane + (int64_t)i * np + j0;
+      dma16_stream(pb, (uint32_t)((lane >> 3) * plane * 2) + 16 * (lane & 7), dp + 1024 * piece);
     }
   };
-  if ((int)blockIdx.x < ntiles) issue(blockIdx.x);
+  // P statistics of this thread's 16 channels 16 wave .. + 15 at position `lane`
+  auto p_sum = [&](int buf, int par) {
+    const bf16* col = &ps[buf][(16 * wave) * kPT + lane];
+    float sacc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) sacc += (float)col[e * kPT];
+    red[par][0][wave][lane] = sacc;
+  };
+  auto p_mean = [&](int par) {
+    float m = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) m += red[par][0][q][lane];
+    return m * (1.f / H);
+  };
+  auto p_centred = [&](int buf, int par) {
+    const bf16* col = &ps[buf][(16 * wave) * kPT + lane];
+    const float mean = p_mean(par);
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const float d = (float)col[e * kPT] - mean;
+      ss += d * d;
+    }
+    red[par][1][wave][lane] = ss;
+  };
+  auto p_normalise = [&](int buf, int par) {
+    const bf16* col = &ps[buf][(16 * wave) * kPT + lane];
+    const float mean = p_mean(par);
+    float var = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) var += red[par][1][q][lane];
+    const float rstd = __builtin_amdgcn_rsqf(var * (1.f / H) + eps);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int c = 16 * wave + 8 * h + e;
+        o[e] = (bf16)(((float)col[(8 * h + e) * kPT] - mean) * rstd * lnp[2][c] + lnp[3][c]);
+      }
+      *reinterpret_cast<bf16x8*>(&y[off128(lane, 2 * wave + h)]) = o;
+    }
+  };
+  const int p0 = 32 * pt + li;  // this lane's position in both products
+  // gate: D[channel][position], lane position p0, registers channels 32 cb + 8 j + 4 g + e
+  auto gate = [&]() {
+    f32x16 ag = zero16();
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) ag = mfma32(fg.k[kk], ld8(&xh[off128(p0, 2 * kk + g)]), ag);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) ag[r] = sigmoid_scaled(ag[r]);
+    return ag;
+  };
+  const int step = gridDim.x;
+  if ((int)blockIdx.x >= ntiles) return;
+  dma(blockIdx.x, 0);
+  dma(blockIdx.x + step, 1);
+  wait_vm_lds<4>();  // this wave's transfers of the first tile landed
+  __syncthreads();
+  {
+    int b, i, j0, valid;
+    where(blockIdx.x, b, i, j0, valid);
+    ln_swz<kPT, 512>(zs[0], xh, valid, lnp[0], lnp[1], eps);
+    p_sum(0, 0);
+  }
+  __syncthreads();
+  f32x16 sg = gate();
+  p_centred(0, 0);
+  int buf = 0, k = 0, prev_valid = kPT;
 #pragma unroll 1
-  for (int tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
+  for (int tile = blockIdx.x; tile < ntiles; tile += step, ++k, buf = buf == NB - 1 ? 0 : buf + 1) {
     int b, i, j0, valid;
     where(tile, b, i, j0, valid);
-    const int64_t zoff = (((int64_t)b * n + i) * n + j0) * 128;
+    const int nbuf = buf == NB - 1 ? 0 : buf + 1, fbuf = nbuf == NB - 1 ? 0 : nbuf + 1;
+    const bool has_next = tile + step < ntiles;
+    // this wave's transfers of tile + step have landed (issued after them: the previous
+    // tile's 2 stores, fewer for a partial tile); the barrier publishes everyone's pieces,
+    // LN(z) and statistics, and retires the previous tile's accesses to ring slot fbuf
+    if (k == 0 || prev_valid < kPT)
+      wait_vm_lds<0>();
+    else
+      wait_vm_lds<2>();
     __syncthreads();
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int chunk = tid + 256 * u;
-      const int c = chunk >> 3, p8 = chunk & 7;
-      *reinterpret_cast<bf16x8*>(&pt_[c * kPS + 8 * p8]) = pv[u];
+    dma(tile + 2 * step, fbuf);
+    p_normalise(buf, k & 1);
+    if (has_next) {
+      int nb, ni, nj0, nvalid;
+      where(tile + step, nb, ni, nj0, nvalid);
+      ln_swz<kPT, 512>(zs[nbuf], xh, nvalid, lnp[0], lnp[1], eps);
+      p_sum(nbuf, (k + 1) & 1);
     }
-    ln_finish(zt, valid, ln_w, ln_b, eps, xh, zr);
     __syncthreads();
-    if (tile + (int)gridDim.x < ntiles) issue(tile + gridDim.x);
-    // centre norm over the 128 channels of each position: wave q sums channels 32q..32q+31
-    // (two-pass statistics; the column is re-read from LDS rather than held in registers)
     {
-      const int pos = tid & 63, q = tid >> 6;
-      const bf16* col = &pt_[(32 * q) * kPS + pos];
-      float sacc = 0.f;
+      f32x16 ao = zero16();
 #pragma unroll
-      for (int e = 0; e < 32; ++e) sacc += (float)col[e * kPS];
-      red[q][pos] = sacc;
-      __syncthreads();
-      const float mean = (red[0][pos] + red[1][pos] + red[2][pos] + red[3][pos]) * (1.f / H);
-      float ss = 0.f;
+      for (int kk = 0; kk < 8; ++kk) ao = mfma32(fo.k[kk], ld8(&y[off128(p0, 2 * kk + g)]), ao);
+      bf16* zrow = zs[buf];
 #pragma unroll
-      for (int e = 0; e < 32; ++e) {
-        const float d = (float)col[e * kPS] - mean;
-        ss += d * d;
+      for (int j = 0; j < 4; ++j) {
+        bf16x4* pz = reinterpret_cast<bf16x4*>(&zrow[off128(p0, 4 * cb + j) + 4 * g]);
+        const bf16x4 zv = *pz;
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)(ao[4 * j + e] * sg[4 * j + e] + (residual ? (float)zv[e] : 0.f));
+        *pz = v;
       }
-      __syncthreads();
-      red[q][pos] = ss;
-      __syncthreads();
-      const float var = (red[0][pos] + red[1][pos] + red[2][pos] + red[3][pos]) * (1.f / H);
-      const float rstd = __builtin_amdgcn_rsqf(var + eps);
+      // the block is this wave's own: LDS operations of a wave complete in order
+      __builtin_amdgcn_wave_barrier();
+      bf16* dst = out + (((int64_t)b * n + i) * n + j0) * 128;
 #pragma unroll
-      for (int e8 = 0; e8 < 4; ++e8) {
-        bf16x8 o;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int c = 32 * q + 8 * e8 + e;
-          o[e] = (bf16)(((float)col[(8 * e8 + e) * kPS] - mean) * rstd * lno[0][c] + lno[1][c]);
-        }
-        *reinterpret_cast<bf16x8*>(&y[pos * kRow + 32 * q + 8 * e8]) = o;
+      for (int u = 0; u < 2; ++u) {
+        const int chunk = lane + 64 * u;
+        const int p = 32 * pt + (chunk >> 2), c = 4 * cb + (chunk & 3);
+        if (p < valid)
+          *reinterpret_cast<bf16x8*>(dst + (int64_t)p * 128 + 8 * c) = ld8(&zrow[off128(p, c)]);
       }
     }
-    __syncthreads();
-#pragma unroll
-    for (int ptile = 0; ptile < kPT / 32; ++ptile) {
-      const bf16* xrow = xh + (ptile * 32 + li) * kRow + 8 * g;
-      const bf16* yrow = y + (ptile * 32 + li) * kRow + 8 * g;
-      f32x16 ag = zero16(), ao = zero16();
-#pragma unroll
-      for (int kk = 0; kk < 8; ++kk) {
-        ag = mfma32(ld8(xrow + 16 * kk), fg.k[kk], ag);
-        ao = mfma32(ld8(yrow + 16 * kk), fo.k[kk], ao);
-      }
-      // D[position][channel]: the output tile overwrites the raw z tile in LDS in place
-#pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int p = ptile * 32 + acc_row(q, g);
-        float val = ao[q] * sigmoid_scaled(ag[q]);
-        if (residual) val += (float)zr[p * kRow + f];
-        zr[p * kRow + f] = (bf16)val;
-      }
+    if (has_next) {
+      sg = gate();
+      p_centred(nbuf, (k + 1) & 1);
     }
-    __syncthreads();
-    // 64 positions x 256 bytes: 16-byte stores
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int chunk = tid + 256 * u;
-      const int p = chunk >> 4, c8 = chunk & 15;
-      if (p < valid)
-        *reinterpret_cast<bf16x8*>(out + zoff + (int64_t)p * 128 + 8 * c8) = ld8(&zr[p * kRow + 8 * c8]);
-    }
+    prev_valid = valid;
   }
+  wait_vm_lds<0>();  // no LDS write may land after exit
 }
 
 static int persistent_grid(int ntiles, int per_cu) {
@@ -408,7 +460,7 @@ void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
   const int nt = np / kCT;
   trimul_contract<<<dim3((unsigned)(nt * nt * a.batch * 128)), 256, 0, stream>>>(a.A, a.B, a.P, np);
   const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);
-  trimul_output<<<persistent_grid(tiles_o, 2), 256, 0, stream>>>(
+  trimul_output<<<persistent_grid(tiles_o, 1), 512, 0, stream>>>(
       a.z, a.P, a.ln_w, a.ln_b, a.lno_w, a.lno_b, a.wg, a.wo, a.out, a.batch, a.n, np,
       a.residual, a.eps);
 }

@@ -101,17 +101,18 @@ struct Carver {
   }
 };
 
+// Workgroup row y converts segment y (the row past the last segment converts the mask), so
+// the segments' loads are in flight together rather than one segment after another.
 __global__ __launch_bounds__(256) void pack_bf16(PackJob job) {
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   const int64_t first = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  for (int s = 0; s < job.nseg; ++s) {
-    const PackSeg sg = job.seg[s];
+  if ((int)blockIdx.y < job.nseg) {
+    const PackSeg sg = job.seg[blockIdx.y];
     for (int64_t i = first; i < sg.n; i += stride) {
       const int64_t j = sg.swap23 ? (i & ~int64_t(12)) | ((i & 4) << 1) | ((i & 8) >> 1) : i;
       sg.dst[i] = (bf16)(sg.src ? sg.src[j] * sg.scale : 0.f);
     }
-  }
-  if (job.mask) {
+  } else if (job.mask) {
     const int64_t total = (int64_t)job.batch * job.np;
     for (int64_t i = first; i < total; i += stride) {
       const int64_t b = i / job.np, s = i - b * job.np;
@@ -122,14 +123,16 @@ __global__ __launch_bounds__(256) void pack_bf16(PackJob job) {
 
 }  // namespace
 
-// One thread per element of the largest segment (at most 1024 workgroups): the weights of one
-// op are a few hundred thousand values, a latency-bound pass either way.
+// Grid: one row of workgroups per segment (plus one for the mask), each row as wide as the
+// largest segment needs (at most 1024 workgroups); the weights of one op are a few hundred
+// thousand values, a latency-bound pass either way.
 void launch_pack(const PackJob& job, hipStream_t stream) {
   int64_t most = job.mask ? (int64_t)job.batch * job.np : 0;
   for (int s = 0; s < job.nseg; ++s) most = job.seg[s].n > most ? job.seg[s].n : most;
   int64_t blocks = (most + 255) / 256;
   blocks = blocks < 1 ? 1 : blocks > 1024 ? 1024 : blocks;
-  pack_bf16<<<dim3((unsigned)blocks), 256, 0, stream>>>(job);
+  const unsigned rows = (unsigned)job.nseg + (job.mask ? 1u : 0u);
+  pack_bf16<<<dim3((unsigned)blocks, rows < 1 ? 1u : rows), 256, 0, stream>>>(job);
 }
 
 // ---------------------------------------------------------------------------------------

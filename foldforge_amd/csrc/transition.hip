@@ -289,7 +289,7 @@ static_assert(24 % kTransNW == 0 && kTransNB >= 2, "transition workgroup shape")
 
 void launch_transition_pack(const float* wa, const float* wb, const float* ws, bf16* dst,
                             hipStream_t stream) {
-  pack_transition<<<dim3(192), 256, 0, stream>>>(wa, wb, ws, dst);
+  pack_transition<<<dim3(16 * kChunkElems / 256), 256, 0, stream>>>(wa, wb, ws, dst);  // one element per thread
 }
 
 void launch_transition(const TransitionArgs& a, hipStream_t stream) {

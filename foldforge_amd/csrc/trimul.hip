@@ -185,8 +185,11 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
 __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ X,
                                                        const bf16* __restrict__ Y,
                                                        bf16* __restrict__ P, int np) {
-  __shared__ __attribute__((aligned(16))) bf16 xs[2][kCT * kCKP];
-  __shared__ __attribute__((aligned(16))) bf16 ys[2][kCT * kCKP];
+  // operand tiles during the k loop, then the output tile [128][kCT + 8] for the stores
+  __shared__ __attribute__((aligned(16))) bf16 smem[4 * kCT * kCKP];
+  static_assert(kCT * (kCT + 8) <= 4 * kCT * kCKP, "output tile exceeds the operand tiles");
+  bf16 (*xs)[kCT * kCKP] = reinterpret_cast<bf16 (*)[kCT * kCKP]>(smem);
+  bf16 (*ys)[kCT * kCKP] = reinterpret_cast<bf16 (*)[kCT * kCKP]>(smem + 2 * kCT * kCKP);
   const int nt = np / kCT;
   const uint32_t wg = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t bh = wg / (nt * nt);
@@ -240,27 +243,40 @@ __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ 
 #pragma unroll
       for (int ni = 0; ni < 2; ++ni)
         bv[ni] = ld8(&ys[buf][(wn * 64 + ni * 32 + li) * kCKP + kk + 8 * g]);
+      // D[j][i]: lane li is row i, its registers 4 t .. 4 t + 3 columns 8 t + 4 g + 0 .. 3
 #pragma unroll
       for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma32(av[mi], bv[ni], acc[mi][ni]);
+        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma32(bv[ni], av[mi], acc[mi][ni]);
     }
     if (more) sstore(buf ^ 1);
     __syncthreads();
     buf ^= 1;
   }
-  bf16* Pb = P + bh * plane;
+  // the k loop ended with a barrier: the operand tiles are free for the output tile
+  constexpr int kOS = kCT + 8;
 #pragma unroll
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) {
-      const int j = j0 + wn * 64 + ni * 32 + li;
+      const int i = wm * 64 + mi * 32 + li;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        const int i = i0 + wm * 64 + mi * 32 + acc_row(q, g);
-        Pb[(int64_t)i * np + j] = (bf16)acc[mi][ni][q];
+      for (int t = 0; t < 4; ++t) {
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)acc[mi][ni][4 * t + e];
+        *reinterpret_cast<bf16x4*>(&smem[i * kOS + wn * 64 + ni * 32 + 8 * t + 4 * g]) = v;
       }
     }
+  __syncthreads();
+  // 128 rows x 256 bytes: 16-byte stores, 16 lanes per row
+  bf16* Pb = P + bh * plane + (int64_t)i0 * np + j0;
+#pragma unroll
+  for (int u = 0; u < kCT * kCT / 8 / 256; ++u) {
+    const int chunk = tid + 256 * u;
+    const int row = chunk >> 4, c = chunk & 15;
+    *reinterpret_cast<bf16x8*>(Pb + (int64_t)row * np + 8 * c) = ld8(&smem[row * kOS + 8 * c]);
+  }
 }
 
 // out[b,i,j,:] = z + (LN_out(P[b,:,i,j]) W_out^T) * sigmoid(LN_pair(z[b,i,j]) W_g^T) over tiles

@@ -279,6 +279,111 @@ __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ 
   }
 }
 
+// The same product with 256 x 256 output tiles for np % 256 == 0: 8 waves of 128 x 64, the
+// operand tiles (256 rows x 32 k of X and of Y, 32 KB a stage) arrive by LDS DMA in a
+// four-stage ring, three stages ahead, so a plane's operands are read twice rather than
+// four times and the loads of three k steps are in flight behind the MFMAs. Operand rows
+// are 64 bytes with their 16-byte pieces XOR-swizzled by (row / 4) % 4, so the sixteen rows
+// of an MFMA fragment fetch hit distinct banks. The ring then holds the output tile for the
+// stores (rows of 512 bytes, pieces swizzled by row % 16).
+constexpr int kBT = 256;                    // output tile
+constexpr int kBStages = 4;
+constexpr int kBStage = 2 * kBT * kCK;      // bf16 per stage (X then Y)
+__global__ __launch_bounds__(512, 2) void trimul_contract256(const bf16* __restrict__ X,
+                                                             const bf16* __restrict__ Y,
+                                                             bf16* __restrict__ P, int np) {
+  __shared__ __attribute__((aligned(16))) bf16 smem[kBStages * kBStage];  // 128 KB
+  static_assert(kBT * kBT <= kBStages * kBStage, "output tile exceeds the ring");
+  const int nt = np / kBT;
+  const uint32_t wg = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t bh = wg / (nt * nt);
+  const int j0 = (int)(wg % nt) * kBT, i0 = (int)((wg / nt) % nt) * kBT;
+  const int64_t plane = (int64_t)np * np;
+  const bf16* Xb = X + bh * plane + (int64_t)i0 * np;
+  const bf16* Yb = Y + bh * plane + (int64_t)j0 * np;
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int wm = wave >> 2, wn = wave & 3;  // rows 128 wm .., columns 64 wn ..
+  // this wave's 4 one-KB pieces of stage s (pieces 0-15 of X, 16-31 of Y, 16 rows each)
+  auto stage_dma = [&](int s) {
+    const uint32_t base = lds_addr(&smem[(s % kBStages) * kBStage]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int piece = 4 * wave + u, half = piece >> 4;
+      const int row = 16 * (piece & 15) + (lane >> 2);
+      const int c = (lane & 3) ^ ((row >> 2) & 3);
+      const bf16* src = (half ? Yb : Xb) + s * kCK;
+      dma16(src, (uint32_t)(row * np * 2 + 16 * c), base + 1024 * piece);
+    }
+  };
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int c = 0; c < 2; ++c) acc[a][c] = zero16();
+  const int nk = np / kCK;
+  stage_dma(0);
+  if (nk > 1) stage_dma(1);
+  if (nk > 2) stage_dma(2);
+#pragma unroll 1
+  for (int s = 0; s < nk; ++s) {
+    // this wave's pieces of stage s landed (the later stages' transfers may be in flight)
+    if (s + 2 < nk)
+      wait_vm_lds<8>();
+    else if (s + 1 < nk)
+      wait_vm_lds<4>();
+    else
+      wait_vm_lds<0>();
+    __syncthreads();  // everyone's pieces of stage s; stage s - 1's slot is free
+    if (s + 3 < nk) stage_dma(s + 3);
+    const bf16* xs = &smem[(s % kBStages) * kBStage];
+    const bf16* ys = xs + kBT * kCK;
+#pragma unroll
+    for (int kk = 0; kk < kCK / 16; ++kk) {
+      bf16x8 av[4], bv[2];
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi) {
+        const int r = 128 * wm + 32 * mi + li;
+        av[mi] = ld8(&xs[r * kCK + 8 * ((2 * kk + g) ^ ((r >> 2) & 3))]);
+      }
+#pragma unroll
+      for (int ni = 0; ni < 2; ++ni) {
+        const int r = 64 * wn + 32 * ni + li;
+        bv[ni] = ld8(&ys[r * kCK + 8 * ((2 * kk + g) ^ ((r >> 2) & 3))]);
+      }
+      // D[j][i]: lane li is row i, its registers 4 t .. 4 t + 3 columns 8 t + 4 g + 0 .. 3
+#pragma unroll
+      for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma32(bv[ni], av[mi], acc[mi][ni]);
+    }
+  }
+  __syncthreads();  // every wave's last fragment reads are done: the ring holds the output
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      const int i = 128 * wm + 32 * mi + li;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = (bf16)acc[mi][ni][4 * t + e];
+        const int c = (64 * wn + 32 * ni + 8 * t) >> 3;  // 16-byte piece of the row
+        *reinterpret_cast<bf16x4*>(&smem[i * kBT + 8 * (c ^ (i & 15)) + 4 * g]) = v;
+      }
+    }
+  __syncthreads();
+  bf16* Pb = P + bh * plane + (int64_t)i0 * np + j0;
+#pragma unroll 4
+  for (int u = 0; u < kBT * kBT / 8 / 512; ++u) {
+    const int chunk = tid + 512 * u;
+    const int row = chunk >> 5, c = chunk & 31;
+    *reinterpret_cast<bf16x8*>(Pb + (int64_t)row * np + 8 * c) = ld8(&smem[row * kBT + 8 * (c ^ (row & 15))]);
+  }
+}
+
 // out[b,i,j,:] = z + (LN_out(P[b,:,i,j]) W_out^T) * sigmoid(LN_pair(z[b,i,j]) W_g^T) over tiles
 // of 64 consecutive pairs of one z row. Persistent, one workgroup of 8 waves per CU; wave w
 // owns output channels 32 (w & 3) .. + 31 of positions 32 (w >> 2) .. + 31 in both
@@ -473,8 +578,7 @@ void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
   const int tiles_p = a.batch * np * (np / kPT);
   trimul_project<<<persistent_grid(tiles_p, 1), 512, 0, stream>>>(
       a.z, a.maskf, a.ln_w, a.ln_b, a.wp, a.A, a.B, a.batch, a.n, np, a.outgoing, a.eps);
-  const int nt = np / kCT;
-  trimul_contract<<<dim3((unsigned)(nt * nt * a.batch * 128)), 256, 0, stream>>>(a.A, a.B, a.P, np);
+  launch_trimul_contract(a.A, a.B, a.P, (int64_t)a.batch * 128, np, stream);
   const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);
   trimul_output<<<persistent_grid(tiles_o, 1), 512, 0, stream>>>(
       a.z, a.P, a.ln_w, a.ln_b, a.lno_w, a.lno_b, a.wg, a.wo, a.out, a.batch, a.n, np,
@@ -483,6 +587,11 @@ void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
 
 void launch_trimul_contract(const bf16* A, const bf16* B, bf16* P, int64_t planes, int np,
                             hipStream_t stream) {
+  if (np % kBT == 0) {
+    const int64_t nt = np / kBT;
+    trimul_contract256<<<dim3((unsigned)(nt * nt * planes)), 512, 0, stream>>>(A, B, P, np);
+    return;
+  }
   const int64_t nt = np / kCT;
   trimul_contract<<<dim3((unsigned)(nt * nt * planes)), 256, 0, stream>>>(A, B, P, np);
 }

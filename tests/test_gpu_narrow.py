@@ -69,6 +69,17 @@ def test_trimul_generic_widths_match_oracle(outgoing, c, h, n, lengths):
     torch.testing.assert_close(full.float(), z.float() + got.float(), atol=3e-2, rtol=1e-2)
 
 
+def test_trimul_generic_width_256_tile_contraction():
+    """A padded width of 256: the contraction takes its 256 x 256 tiles."""
+    n, c, h = 230, 64, 64
+    z, mask = _pair(n, c, [230, 177], seed=21)
+    m = randomise(factories.triangle_multiplication(c, outgoing=False, d_hidden=h), seed=22).cuda()
+    m.set_backend("hip")
+    got = m.delta(z.cuda(), mask.cuda()).cpu()
+    want = ps.triangle_multiplication(z, mask, m.state_dict(), outgoing=False, dtype=torch.float64) - z.double()
+    _check(got, want, _pairs(mask), "trimul c=64 h=64 incoming n=230")
+
+
 @pytest.mark.parametrize("starting", [True, False])
 @pytest.mark.parametrize("model", ["af3", "protenix"])
 @pytest.mark.parametrize("c,heads,d", [(64, 4, 16), (64, 4, 32), (128, 8, 16), (256, 4, 32)])

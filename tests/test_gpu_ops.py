@@ -68,7 +68,7 @@ def test_layer_norm_matches_oracle():
 
 
 @pytest.mark.parametrize("outgoing", [True, False])
-@pytest.mark.parametrize("n,lengths", [(64, None), (100, [77]), (130, [130, 41])])
+@pytest.mark.parametrize("n,lengths", [(64, None), (100, [77]), (130, [130, 41]), (256, [256, 203])])
 def test_trimul_matches_oracle(outgoing, n, lengths):
     batch = len(lengths) if lengths else 1
     z, mask = _pair(n, batch, seed=n, lengths=lengths)

@@ -113,10 +113,22 @@ __global__ __launch_bounds__(256) void pack_bf16(PackJob job) {
       sg.dst[i] = (bf16)(sg.src ? sg.src[j] * sg.scale : 0.f);
     }
   } else if (job.mask) {
-    const int64_t total = (int64_t)job.batch * job.np;
-    for (int64_t i = first; i < total; i += stride) {
-      const int64_t b = i / job.np, s = i - b * job.np;
-      job.maskf[i] = s < job.n && job.mask[b * job.n + s] != 0 ? 1.f : 0.f;
+    // one workgroup per batch element: its mask row, and the number of key stages up to the
+    // last real key
+    __shared__ int last;
+    for (int b = blockIdx.x; b < job.batch; b += gridDim.x) {
+      if (threadIdx.x == 0) last = -1;
+      __syncthreads();
+      int mine = -1;
+      for (int s = threadIdx.x; s < job.np; s += blockDim.x) {
+        const bool real = s < job.n && job.mask[(int64_t)b * job.n + s] != 0;
+        job.maskf[(int64_t)b * job.np + s] = real ? 1.f : 0.f;
+        if (real) mine = s;
+      }
+      if (mine >= 0) atomicMax(&last, mine);
+      __syncthreads();
+      if (threadIdx.x == 0 && job.kstages) job.kstages[b] = (last + 32) / 32;
+      __syncthreads();
     }
   }
 }
@@ -127,7 +139,7 @@ __global__ __launch_bounds__(256) void pack_bf16(PackJob job) {
 // largest segment needs (at most 1024 workgroups); the weights of one op are a few hundred
 // thousand values, a latency-bound pass either way.
 void launch_pack(const PackJob& job, hipStream_t stream) {
-  int64_t most = job.mask ? (int64_t)job.batch * job.np : 0;
+  int64_t most = job.mask ? (int64_t)job.batch * 256 : 0;  // the mask row: a workgroup per batch
   for (int s = 0; s < job.nseg; ++s) most = job.seg[s].n > most ? job.seg[s].n : most;
   int64_t blocks = (most + 255) / 256;
   blocks = blocks < 1 ? 1 : blocks > 1024 ? 1024 : blocks;
@@ -178,6 +190,7 @@ int64_t pad32(int64_t n);
 struct TriattnWs {
   bf16 *wqkv, *wb, *wg, *wo, *q, *k, *vt, *o, *gate;
   float *bias, *og, *maskf;
+  int* kst;
   size_t bytes;
 };
 TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d) {
@@ -207,6 +220,7 @@ TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d
   w.bias = cv.take<float>((size_t)batch * heads * np * np);
   w.o = cv.take<bf16>((size_t)batch * n * n * hd);
   w.maskf = cv.take<float>((size_t)batch * np);
+  w.kst = cv.take<int>((size_t)batch);
   w.bytes = cv.used;
   return w;
 }
@@ -567,6 +581,7 @@ int32_t ffk_triangle_attention(
   job.nseg = 7;
   job.mask = key_mask;
   job.maskf = w.maskf;
+  job.kstages = w.kst;
   job.batch = (int)batch;
   job.n = (int)n;
   job.np = (int)pad128(n);
@@ -575,6 +590,7 @@ int32_t ffk_triangle_attention(
   a.z = static_cast<const bf16*>(z);
   a.mask = key_mask;
   a.maskf = w.maskf;
+  a.kstages = w.kst;
   a.ln_w = ln_pair_w;
   a.ln_b = ln_pair_b;
   a.wqkv = w.wqkv;
@@ -631,6 +647,7 @@ int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
   f.o_sr = o_sr;
   f.o_sj = o_sj;
   f.heads = heads;
+  f.kstages = nullptr;
   if (rows_valid == 0 || n_valid == 0) return ok();
   launch_flash(f, static_cast<hipStream_t>(stream));
   return check_launch("flash_attention_bias");

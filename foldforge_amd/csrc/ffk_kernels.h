@@ -38,6 +38,7 @@ struct TriattnArgs {
   const bf16* wo;    // [128][128] to_out
   bf16 *q, *k, *vt;  // [batch * heads][np][np][32], vt: [batch * heads][np][32][np]
   float* bias;       // [batch * heads][np / 32][np / 32][2][32][16] blocked, see triattn.hip
+  const int* kstages;  // [batch] key stages holding a real key (written by the weight packing)
   bf16* o;           // [batch][n][n][128] z-frame attention output
   bf16* out;
   int batch, n, np, heads, starting, transposed_bias, residual;
@@ -51,6 +52,9 @@ struct FlashArgs {
   bf16* o;
   int64_t batch, rows, np, rows_valid, n_valid, o_sb, o_sr, o_sj;
   int heads;
+  // optional [batch] key-stage counts: the stages past them hold only masked keys (bias
+  // -inf), which add exact zeros, and are skipped (NULL: every stage runs)
+  const int* kstages;
 };
 void launch_flash(const FlashArgs& a, hipStream_t stream);
 
@@ -220,6 +224,9 @@ struct PackJob {
   // n <= s < np (mask NULL: none)
   const uint8_t* mask;
   float* maskf;
+  // optional with the mask: kstages[b] = the number of 32-key stages up to the last real key
+  // of batch element b (0 when it has none)
+  int* kstages;
   int batch, n, np;
 };
 void launch_pack(const PackJob& job, hipStream_t stream);

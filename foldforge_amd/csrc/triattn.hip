@@ -304,7 +304,8 @@ __device__ __forceinline__ float exp_pack(const f32x16& S, bf16x8& p0, bf16x8& p
 __global__ __launch_bounds__(256, 2) void flash_attn_bias(
     const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ vt,
     const float* __restrict__ bias, bf16* __restrict__ o, int heads, int64_t rows, int64_t np,
-    int64_t rows_valid, int64_t n_valid, int64_t o_sb, int64_t o_sr, int64_t o_sj) {
+    int64_t rows_valid, int64_t n_valid, int64_t o_sb, int64_t o_sr, int64_t o_sj,
+    const int* __restrict__ kstages) {
   __shared__ FlashLds lds;
   const uint32_t nqb = (uint32_t)((np + 32 * kFW - 1) / (32 * kFW));
   const uint32_t nrg = (uint32_t)(rows / kFR);
@@ -326,6 +327,9 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
   const int64_t j = jw + li;
   const int64_t nb = np / 32;
   const int64_t nstage = np / kFK;
+  // key stages past the batch element's last real key hold bias -inf only: exp2 gives exact
+  // zeros there, so leaving them out changes no bit of l or O
+  const int64_t nrun = kstages ? min(nstage, ((int64_t)kstages[bidx] * 32 + kFK - 1) / kFK) : nstage;
 
   // Transfers (each one 1 KB LDS DMA per wave): stage s of K / V^T = 16 pieces, 4 per wave
   // (piece P = 4 wave + u: part P / 8 (K, V^T), row (P / 2) % 4, half P % 2); bias tile
@@ -403,7 +407,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
   }
 
 #pragma unroll 1
-  for (int64_t st = 0; st < nstage; ++st) {
+  for (int64_t st = 0; st < nrun; ++st) {
     const int sb = (int)(st & 1);
     // this wave's bias tile st and everyone's K / V^T stage st have landed (waited for and
     // published at the end of the last stage)
@@ -659,7 +663,7 @@ void launch_flash(const FlashArgs& a, hipStream_t stream) {
   const int64_t blocks = nqb * (a.rows / kFR) * a.batch * a.heads;
   flash_attn_bias<<<dim3((unsigned)blocks), 64 * kFW, 0, stream>>>(
       a.q, a.k, a.vt, a.bias, a.o, a.heads, a.rows, a.np, a.rows_valid, a.n_valid, a.o_sb, a.o_sr,
-      a.o_sj);
+      a.o_sj, a.kstages);
 }
 
 void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
@@ -680,6 +684,7 @@ void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
   f.rows_valid = a.n;
   f.n_valid = a.n;
   f.heads = a.heads;
+  f.kstages = a.kstages;
   // o is written in the frame of z: row r of the attention is a row (starting) or a
   // column (ending) of z.
   const int64_t c = 128;

@@ -56,7 +56,7 @@ def test_workspace_sizes_follow_the_layouts(lib):
     ta = lib.ffk_triangle_attention_workspace(b, n, 128, 4, 32)
     weights = up(3 * 128 * 128 * 2) + up(32 * 128 * 2) + 2 * up(128 * 128 * 2)
     qkv = 3 * up(b * 4 * np_ * np_ * 32 * 2)
-    assert ta == weights + qkv + up(b * 4 * np_ * np_ * 4) + up(b * n * n * 128 * 2) + up(b * np_ * 4)
+    assert ta == weights + qkv + up(b * 4 * np_ * np_ * 4) + up(b * n * n * 128 * 2) + up(b * np_ * 4) + up(b * 4)
     assert lib.ffk_transition_workspace(1000, 128, 4) == 3 * up(4 * 128 * 128 * 2)
     assert lib.ffk_transition_workspace(700, 384, 4) == up(700 * 1536 * 4)
     np32 = 320

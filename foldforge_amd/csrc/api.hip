@@ -158,6 +158,7 @@ bool triattn_fused(int c, int heads, int d) { return c == 128 && heads == 4 && d
 struct TrimulWs {
   bf16 *wp, *wg, *wo, *A, *B, *P, *Pt;
   float *maskf, *y32;
+  int* kst;
   size_t bytes;
 };
 TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
@@ -181,6 +182,7 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
   w.B = cv.take<bf16>(plane);
   w.P = cv.take<bf16>(plane);
   w.maskf = cv.take<float>((size_t)batch * np);
+  w.kst = cv.take<int>((size_t)batch);
   w.bytes = cv.used;
   return w;
 }
@@ -432,6 +434,7 @@ int32_t ffk_triangle_multiplication(
   job.nseg = 6;
   job.mask = key_mask;
   job.maskf = w.maskf;
+  job.kstages = w.kst;
   job.batch = (int)batch;
   job.n = (int)n;
   job.np = (int)pad128(n);
@@ -450,6 +453,7 @@ int32_t ffk_triangle_multiplication(
   a.B = w.B;
   a.P = w.P;
   a.maskf = w.maskf;
+  a.kstages = w.kst;
   a.out = static_cast<bf16*>(out);
   a.batch = (int)batch;
   a.n = (int)n;

@@ -18,14 +18,18 @@ struct TrimulArgs {
   const bf16* wo;  // [c][h]
   bf16 *A, *B, *P;  // [batch][h][np][np]
   float* maskf;     // [batch][np] scratch: the key mask as 1 / 0, zero past n
+  const int* kstages;  // [batch] 32-wide k stages up to the last real key (NULL: all)
   bf16* out;
   int batch, n, np, outgoing, residual;
   float eps;
 };
 void launch_trimul(const TrimulArgs& a, hipStream_t stream);
-// P[p] = X[p] Y[p]^T for `planes` planes of [np][np] bf16 (np % 128 == 0).
+// P[p] = X[p] Y[p]^T for `planes` planes of [np][np] bf16 (np % 128 == 0). With kstages, plane
+// p runs only the first kstages[p / planes_per_batch] k stages of 32 (the operands are zero past
+// them, so the product is unchanged).
 void launch_trimul_contract(const bf16* A, const bf16* B, bf16* P, int64_t planes, int np,
-                            hipStream_t stream);
+                            hipStream_t stream, const int* kstages = nullptr,
+                            int planes_per_batch = 1);
 
 struct TriattnArgs {
   const bf16* z;

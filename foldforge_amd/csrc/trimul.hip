@@ -184,7 +184,9 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
 // block 256 = 2 x 2 waves of 64 x 64.
 __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ X,
                                                        const bf16* __restrict__ Y,
-                                                       bf16* __restrict__ P, int np) {
+                                                       bf16* __restrict__ P, int np,
+                                                       const int* __restrict__ kstages,
+                                                       int planes_per_batch) {
   // operand tiles during the k loop, then the output tile [128][kCT + 8] for the stores
   __shared__ __attribute__((aligned(16))) bf16 smem[4 * kCT * kCKP];
   static_assert(kCT * (kCT + 8) <= 4 * kCT * kCKP, "output tile exceeds the operand tiles");
@@ -197,6 +199,8 @@ __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ 
   const int64_t plane = (int64_t)np * np;
   const bf16* Xb = X + bh * plane + (int64_t)i0 * np;
   const bf16* Yb = Y + bh * plane + (int64_t)j0 * np;
+  // k past the batch element's last real key: zero operands, left out
+  const int kend = kstages ? min(np, kstages[bh / planes_per_batch] * kCK) : np;
   const int tid = threadIdx.x;
   // global -> LDS: a 128 x 32 tile is 512 chunks of 8 bf16; 2 per thread per operand.
   bf16x8 rx[2], ry[2];
@@ -231,8 +235,8 @@ __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ 
   __syncthreads();
   int buf = 0;
 #pragma unroll 1
-  for (int k0 = 0; k0 < np; k0 += kCK) {
-    const bool more = k0 + kCK < np;
+  for (int k0 = 0; k0 < kend; k0 += kCK) {
+    const bool more = k0 + kCK < kend;
     if (more) gload(k0 + kCK);
 #pragma unroll
     for (int kk = 0; kk < kCK; kk += 16) {
@@ -291,7 +295,9 @@ constexpr int kBStages = 4;
 constexpr int kBStage = 2 * kBT * kCK;      // bf16 per stage (X then Y)
 __global__ __launch_bounds__(512, 2) void trimul_contract256(const bf16* __restrict__ X,
                                                              const bf16* __restrict__ Y,
-                                                             bf16* __restrict__ P, int np) {
+                                                             bf16* __restrict__ P, int np,
+                                                             const int* __restrict__ kstages,
+                                                             int planes_per_batch) {
   __shared__ __attribute__((aligned(16))) bf16 smem[kBStages * kBStage];  // 128 KB
   static_assert(kBT * kBT <= kBStages * kBStage, "output tile exceeds the ring");
   const int nt = np / kBT;
@@ -322,8 +328,9 @@ __global__ __launch_bounds__(512, 2) void trimul_contract256(const bf16* __restr
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int c = 0; c < 2; ++c) acc[a][c] = zero16();
-  const int nk = np / kCK;
-  stage_dma(0);
+  // k stages past the batch element's last real key: zero operands, left out
+  const int nk = kstages ? min(np / kCK, kstages[bh / planes_per_batch]) : np / kCK;
+  if (nk > 0) stage_dma(0);
   if (nk > 1) stage_dma(1);
   if (nk > 2) stage_dma(2);
 #pragma unroll 1
@@ -578,7 +585,7 @@ void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
   const int tiles_p = a.batch * np * (np / kPT);
   trimul_project<<<persistent_grid(tiles_p, 1), 512, 0, stream>>>(
       a.z, a.maskf, a.ln_w, a.ln_b, a.wp, a.A, a.B, a.batch, a.n, np, a.outgoing, a.eps);
-  launch_trimul_contract(a.A, a.B, a.P, (int64_t)a.batch * 128, np, stream);
+  launch_trimul_contract(a.A, a.B, a.P, (int64_t)a.batch * 128, np, stream, a.kstages, 128);
   const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);
   trimul_output<<<persistent_grid(tiles_o, 1), 512, 0, stream>>>(
       a.z, a.P, a.ln_w, a.ln_b, a.lno_w, a.lno_b, a.wg, a.wo, a.out, a.batch, a.n, np,
@@ -586,14 +593,16 @@ void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
 }
 
 void launch_trimul_contract(const bf16* A, const bf16* B, bf16* P, int64_t planes, int np,
-                            hipStream_t stream) {
+                            hipStream_t stream, const int* kstages, int planes_per_batch) {
   if (np % kBT == 0) {
     const int64_t nt = np / kBT;
-    trimul_contract256<<<dim3((unsigned)(nt * nt * planes)), 512, 0, stream>>>(A, B, P, np);
+    trimul_contract256<<<dim3((unsigned)(nt * nt * planes)), 512, 0, stream>>>(
+        A, B, P, np, kstages, planes_per_batch);
     return;
   }
   const int64_t nt = np / kCT;
-  trimul_contract<<<dim3((unsigned)(nt * nt * planes)), 256, 0, stream>>>(A, B, P, np);
+  trimul_contract<<<dim3((unsigned)(nt * nt * planes)), 256, 0, stream>>>(A, B, P, np, kstages,
+                                                                        planes_per_batch);
 }
 
 }  // namespace ffk

@@ -52,7 +52,7 @@ def test_workspace_sizes_follow_the_layouts(lib):
     np_ = 384
     tm = lib.ffk_triangle_multiplication_workspace(b, n, 128, 128)
     weights = up(4 * 128 * 128 * 2) + up(128 * 128 * 2) + up(128 * 128 * 2)
-    assert tm == weights + 3 * up(b * 128 * np_ * np_ * 2) + up(b * np_ * 4)
+    assert tm == weights + 3 * up(b * 128 * np_ * np_ * 2) + up(b * np_ * 4) + up(b * 4)
     ta = lib.ffk_triangle_attention_workspace(b, n, 128, 4, 32)
     weights = up(3 * 128 * 128 * 2) + up(32 * 128 * 2) + 2 * up(128 * 128 * 2)
     qkv = 3 * up(b * 4 * np_ * np_ * 32 * 2)

@@ -43,6 +43,28 @@ __device__ __forceinline__ int acc_row(int r, int g) { return 8 * (r >> 2) + 4 *
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
+// Stores of intermediates that the next kernel reads once. Bit k of FFK_NT_MASK makes family k
+// use non-temporal (streaming) stores: 1 projections (A, B, q, k, v^T), 2 contraction (P),
+// 4 output kernels (z), 8 flash core (o).
+#ifndef FFK_NT_MASK
+#define FFK_NT_MASK 5
+#endif
+constexpr int kNtProject = 1, kNtContract = 2, kNtOutput = 4, kNtFlash = 8;
+template <int Family>
+__device__ __forceinline__ void st16(bf16* p, bf16x8 v) {
+  if constexpr ((FFK_NT_MASK & Family) != 0)
+    __builtin_nontemporal_store(v, reinterpret_cast<bf16x8*>(p));
+  else
+    *reinterpret_cast<bf16x8*>(p) = v;
+}
+template <int Family>
+__device__ __forceinline__ void st8(bf16* p, bf16x4 v) {
+  if constexpr ((FFK_NT_MASK & Family) != 0)
+    __builtin_nontemporal_store(v, reinterpret_cast<bf16x4*>(p));
+  else
+    *reinterpret_cast<bf16x4*>(p) = v;
+}
+
 // Four values rounded to bf16, one 8-byte store.
 __device__ __forceinline__ void store4(bf16* p, float a, float b, float c, float d) {
   bf16x4 v;

@@ -2,16 +2,19 @@
 //
 // Reference: the engine LayerNorm (src/foldforge/modules/engine/modules.py:230-238) and the
 // torch.nn.LayerNorm of the legacy graph (legacy/attention.py:90). HBM-bound: the 128-wide
-// bf16 path is persistent (four 256-thread workgroups per CU), streams 16-byte vectors with 16
-// lanes per row and 8 rows per lane, fetches the next 128 rows of a workgroup while it
-// normalises the current ones (two register buffers used alternately), and keeps each row in
-// registers between the two statistics passes (exact two-pass variance).
+// bf16 path streams 16-byte vectors with 16 lanes per row and 2 rows per lane (32 rows per
+// 256-thread workgroup, up to 32 workgroups per CU, so a pair tensor of up to 262144 rows is
+// one pass of workgroups and larger ones loop), fetches a workgroup's next rows while it
+// normalises the current ones (two register buffers used alternately), keeps each row in
+// registers between the two statistics passes (exact two-pass variance) and writes the output
+// with non-temporal stores (measured at N = 512: 22.5 -> 19.6 us against 8 rows per lane, four
+// persistent workgroups per CU and regular stores).
 #include "ffk_device.h"
 #include "ffk_kernels.h"
 
 namespace ffk {
 
-constexpr int kLnRowsPerLane = 8;
+constexpr int kLnRowsPerLane = 2;
 constexpr int kLnRowsPerBlock = 16 * kLnRowsPerLane;  // 16 rows per pass (16 lanes each)
 
 // Normalise and store the rows row0 + 16 it (it < kLnRowsPerLane) whose 8-channel slices
@@ -41,12 +44,12 @@ __device__ __forceinline__ void ln_rows_compute(const bf16x8 (&v)[kLnRowsPerLane
       bf16x8 o;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (bf16)(xv[e] * rstd * wv[e] + bv[e]);
-      *reinterpret_cast<bf16x8*>(y + row * 128 + 8 * sub) = o;
+      __builtin_nontemporal_store(o, reinterpret_cast<bf16x8*>(y + row * 128 + 8 * sub));
     }
   }
 }
 
-// bf16 rows of exactly 128 channels. grid min(ceil(rows / 128), 4 per CU); block 256.
+// bf16 rows of exactly 128 channels. grid min(ceil(rows / 32), 32 per CU); block 256.
 __global__ __launch_bounds__(256) void layer_norm_bf16_128(const bf16* __restrict__ x,
                                                            const float* __restrict__ w,
                                                            const float* __restrict__ b,
@@ -66,10 +69,20 @@ __global__ __launch_bounds__(256) void layer_norm_bf16_128(const bf16* __restric
   int64_t row0 = (int64_t)blockIdx.x * kLnRowsPerBlock + (tid >> 4);
   bf16x8 va[kLnRowsPerLane], vb[kLnRowsPerLane];
   load(va, row0);
+  // one uniform branch per pointer (a per-element select compiles to a branch per load)
+  if (w != nullptr) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    wv[e] = w ? w[8 * sub + e] : 1.f;
-    bv[e] = b ? b[8 * sub + e] : 0.f;
+    for (int e = 0; e < 8; ++e) wv[e] = w[8 * sub + e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) wv[e] = 1.f;
+  }
+  if (b != nullptr) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bv[e] = b[8 * sub + e];
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bv[e] = 0.f;
   }
   // row0 - tid / 16 is the workgroup's first row: the loop condition is uniform
   while (row0 - (tid >> 4) < rows) {
@@ -117,7 +130,7 @@ void launch_layer_norm(const void* x, const float* w, const float* b, void* y, i
                        int cols, float eps, int dtype, hipStream_t stream) {
   if (dtype == 0 && cols == 128) {
     int64_t blocks = (rows + kLnRowsPerBlock - 1) / kLnRowsPerBlock;
-    if (blocks > (int64_t)cu_count() * 4) blocks = (int64_t)cu_count() * 4;
+    if (blocks > (int64_t)cu_count() * 32) blocks = (int64_t)cu_count() * 32;
     layer_norm_bf16_128<<<dim3((unsigned)blocks), 256, 0, stream>>>(
         static_cast<const bf16*>(x), w, b, static_cast<bf16*>(y), rows, eps);
     return;

@@ -206,7 +206,7 @@ __global__ __launch_bounds__(512, 2) void triattn_project(
           for (int u = 0; u < 2; ++u) {
             const int chunk = lane + 64 * u;
             const int p = chunk >> 2, c = chunk & 3;
-            *reinterpret_cast<bf16x8*>(dst + p * 32 + 8 * c) = ld8(&st[p * 32 + 8 * (c ^ ((p >> 2) & 3))]);
+            st16<kNtProject>(dst + p * 32 + 8 * c, ld8(&st[p * 32 + 8 * (c ^ ((p >> 2) & 3))]));
           }
           __builtin_amdgcn_wave_barrier();
         }
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(512, 2) void triattn_project(
       for (int u = 0; u < 4; ++u) {
         const int chunk = lane + 64 * u;
         const int d = chunk >> 3, c = chunk & 7;
-        *reinterpret_cast<bf16x8*>(vd + (int64_t)d * np + 8 * c) = ld8(&st[d * kPT + 8 * (c ^ ((d >> 1) & 7))]);
+        st16<kNtProject>(vd + (int64_t)d * np + 8 * c, ld8(&st[d * kPT + 8 * (c ^ ((d >> 1) & 7))]));
       }
     }
     if (tile + step < ntiles) {
@@ -515,7 +515,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
       bf16x4 w;
 #pragma unroll
       for (int t = 0; t < 4; ++t) w[t] = (bf16)(O[rr][4 * qd + t] * inv);
-      *reinterpret_cast<bf16x4*>(dst + 8 * qd + 4 * g) = w;
+      st8<kNtFlash>(dst + 8 * qd + 4 * g, w);
     }
   }
 }
@@ -646,7 +646,7 @@ __global__ __launch_bounds__(512, 2) void triattn_output(
         const int chunk = lane + 64 * u;
         const int p = 32 * pt + (chunk >> 2), c = 4 * cb + (chunk & 3);
         if (p < valid)
-          *reinterpret_cast<bf16x8*>(out + off + (int64_t)p * 128 + 8 * c) = ld8(&zrow[off128(p, c)]);
+          st16<kNtOutput>(out + off + (int64_t)p * 128 + 8 * c, ld8(&zrow[off128(p, c)]));
       }
     }
     prev_valid = valid;

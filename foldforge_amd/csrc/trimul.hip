@@ -167,7 +167,7 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
     for (int u = 0; u < 4; ++u) {
       const int chunk = lane + 64 * u;
       const int c = chunk >> 3, p8 = chunk & 7;
-      *reinterpret_cast<bf16x8*>(dst + (int64_t)c * plane + 8 * p8) = ld8(&st[c * kPS + 8 * p8]);
+      st16<kNtProject>(dst + (int64_t)c * plane + 8 * p8, ld8(&st[c * kPS + 8 * p8]));
     }
     if (tile + step < ntiles) {
       int nb, nr, ns0, nvalid;
@@ -279,7 +279,7 @@ __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ 
   for (int u = 0; u < kCT * kCT / 8 / 256; ++u) {
     const int chunk = tid + 256 * u;
     const int row = chunk >> 4, c = chunk & 15;
-    *reinterpret_cast<bf16x8*>(Pb + (int64_t)row * np + 8 * c) = ld8(&smem[row * kOS + 8 * c]);
+    st16<kNtContract>(Pb + (int64_t)row * np + 8 * c, ld8(&smem[row * kOS + 8 * c]));
   }
 }
 
@@ -387,7 +387,7 @@ __global__ __launch_bounds__(512, 2) void trimul_contract256(const bf16* __restr
   for (int u = 0; u < kBT * kBT / 8 / 512; ++u) {
     const int chunk = tid + 512 * u;
     const int row = chunk >> 5, c = chunk & 31;
-    *reinterpret_cast<bf16x8*>(Pb + (int64_t)row * np + 8 * c) = ld8(&smem[row * kBT + 8 * (c ^ (row & 15))]);
+    st16<kNtContract>(Pb + (int64_t)row * np + 8 * c, ld8(&smem[row * kBT + 8 * (c ^ (row & 15))]));
   }
 }
 
@@ -564,7 +564,7 @@ __global__ __launch_bounds__(512, 2) void trimul_output(
         const int chunk = lane + 64 * u;
         const int p = 32 * pt + (chunk >> 2), c = 4 * cb + (chunk & 3);
         if (p < valid)
-          *reinterpret_cast<bf16x8*>(dst + (int64_t)p * 128 + 8 * c) = ld8(&zrow[off128(p, c)]);
+          st16<kNtOutput>(dst + (int64_t)p * 128 + 8 * c, ld8(&zrow[off128(p, c)]));
       }
     }
     if (has_next) {

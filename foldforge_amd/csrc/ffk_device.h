@@ -47,7 +47,7 @@ __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<
 // use non-temporal (streaming) stores: 1 projections (A, B, q, k, v^T), 2 contraction (P),
 // 4 output kernels (z), 8 flash core (o).
 #ifndef FFK_NT_MASK
-#define FFK_NT_MASK 5
+#define FFK_NT_MASK 4
 #endif
 constexpr int kNtProject = 1, kNtContract = 2, kNtOutput = 4, kNtFlash = 8;
 template <int Family>

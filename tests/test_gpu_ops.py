@@ -67,6 +67,21 @@ def test_layer_norm_matches_oracle():
         _check(got, want, None, f"layer_norm {rows}x{cols} {dtype}")
 
 
+def test_layer_norm_multi_pass_and_no_affine():
+    # more rows than one pass of the 128-wide kernel's workgroups (32 rows each, at most 32 per
+    # CU), with a ragged tail; and the null weight / bias pointers of the C-ABI
+    g = torch.Generator().manual_seed(2)
+    rows = 32 * 32 * torch.cuda.get_device_properties(0).multi_processor_count * 2 + 37
+    x = torch.randn(rows, 128, generator=g).bfloat16()
+    w = 1 + 0.1 * torch.randn(128, generator=g)
+    b = 0.05 * torch.randn(128, generator=g)
+    got = kernels.layer_norm(x.cuda(), w.cuda(), b.cuda(), 1e-5).cpu()
+    _check(got, ps.layer_norm(x.double(), w.double(), b.double(), 1e-5), None, f"layer_norm {rows}x128")
+    x = x[:4099]
+    got = kernels.layer_norm(x.cuda(), None, None, 1e-5).cpu()
+    _check(got, ps.layer_norm(x.double(), None, None, 1e-5), None, "layer_norm without affine")
+
+
 @pytest.mark.parametrize("outgoing", [True, False])
 @pytest.mark.parametrize("n,lengths", [(64, None), (100, [77]), (130, [130, 41]), (256, [256, 203])])
 def test_trimul_matches_oracle(outgoing, n, lengths):

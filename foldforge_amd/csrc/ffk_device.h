@@ -45,7 +45,10 @@ __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<
 
 // Stores of intermediates that the next kernel reads once. Bit k of FFK_NT_MASK makes family k
 // use non-temporal (streaming) stores: 1 projections (A, B, q, k, v^T), 2 contraction (P),
-// 4 output kernels (z), 8 flash core (o).
+// 4 output kernels (z), 8 flash core (o). Only the output kernels stream by default: streaming
+// the projections' outputs sped a ragged N = 512 block up by 2% but slowed a full-mask trunk by
+// 2% (their consumers then read from HBM instead of the last-level cache), and streaming P or o
+// (the flash core writes 8-byte pieces) cost 3-20%.
 #ifndef FFK_NT_MASK
 #define FFK_NT_MASK 4
 #endif

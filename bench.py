@@ -210,6 +210,52 @@ def block_gflop(n: int, d_single: int = 0) -> float:
     return total / 1e9
 
 
+def op_gflop(n: int, keys: int | None = None) -> dict[str, float]:
+    """GFLOP of each pair op of one block at N = n. ``keys`` (the key stages the kernels run on a
+    ragged input: the 32-key stages up to the last real key) shortens the contraction and the
+    attention core; None counts all n (the algorithmic work)."""
+    c, h, hd = 128, 128, 128
+    k = n if keys is None else keys
+    trimul = 2 * n * n * k * h + n * n * (8 * c * h + 2 * c * c + 2 * h * c)
+    triattn = 4 * n * n * k * hd + n * n * (8 * c * hd + 2 * c * 4 + 2 * hd * c)
+    trans = n * n * (4 * c * 4 * c + 2 * 4 * c * c)
+    return {"trimul_outgoing": trimul / 1e9, "trimul_incoming": trimul / 1e9,
+            "triattn_starting": triattn / 1e9, "triattn_ending": triattn / 1e9, "transition": trans / 1e9}
+
+
+def key_extent(n: int, length: int) -> int:
+    """Keys the contraction and the flash core run over: 32-key stages up to the last real key."""
+    return min(n, (length + 31) // 32 * 32)
+
+
+#: The reference's per-op times for this block (engine ``cuda`` backend, H100 80GB, bf16, AF3
+#: widths, L = 384; docs/archive/BACKENDS-engine-2.3.md:257-262): not MI355X numbers, shown
+#: beside ours for scale only.
+REFERENCE_H100_MS_384 = {"trimul_outgoing": 0.52, "triattn_starting": 0.28, "transition": 0.11}
+
+OP_ATTRS = (("trimul_outgoing", "tri_multi_outgoing"), ("trimul_incoming", "tri_multi_incoming"),
+            ("triattn_starting", "tri_atten_starting"), ("triattn_ending", "tri_atten_ending"),
+            ("transition", "transition_pair"))
+
+
+def op_times(block, z, mask, length: int, reps: int) -> dict:
+    """ms of each pair op of ``block`` (whole op: LayerNorm, projections, core, gate, output,
+    residual) between HIP events, with its executed TFLOP/s, and the block's own ms."""
+    import torch
+
+    n = z.shape[1]
+    gf = op_gflop(n, key_extent(n, length))
+    ops = {}
+    with torch.no_grad():
+        for name, attr in OP_ATTRS:
+            op = getattr(block, attr)
+            call = (lambda: op(z)) if name == "transition" else (lambda: op(z, mask))
+            ms = event_time_ms(call, reps, warm=max(20, reps))
+            ops[name] = {"ms": round(ms, 4), "tflops_executed": round(gf[name] / ms, 1)}
+        block_ms = event_time_ms(lambda: block(z, mask), reps, warm=max(10, reps))
+    return {"ops": ops, "ms_per_block": round(block_ms, 4), "sum_of_ops_ms": round(sum(o["ms"] for o in ops.values()), 4)}
+
+
 def trunk_inputs(n: int, seed: int = 0):
     import torch
 
@@ -395,8 +441,7 @@ def shapes_measure(reps: int = 10) -> dict:
     and on the engine pytorch backend (same GPU)."""
     import torch
 
-    from foldforge_amd import factories
-    from foldforge_amd.policy import guard
+    from foldforge_amd import dispatch, factories
     from foldforge_amd.trunk import randomise
 
     n = 384
@@ -418,9 +463,7 @@ def shapes_measure(reps: int = 10) -> dict:
         with torch.no_grad():
             for backend in ("hip", "pytorch"):
                 block.set_backend(backend)
-                if backend == "hip":
-                    for m in block.children_ops():
-                        guard(m, "error")
+                dispatch.set_refusal(block, "error" if backend == "hip" else None)
                 row[f"{backend}_ms"] = round(event_time_ms(lambda: block(*args), reps, warm=max(20, reps)), 3)
         row["hip_speedup"] = round(row["pytorch_ms"] / row["hip_ms"], 2)
         out["rows"].append(row)
@@ -474,37 +517,86 @@ def ladder(max_n: int) -> list[dict]:
     return lines
 
 
-def cpu_baseline(z, mask, state, gpu_out, runs: int) -> dict:
+def _cpu_ops(z, mask, state, runs: int) -> tuple[dict, float, object]:
+    """The fp32 oracle's block on the CPU, op by op: median ms of each op over ``runs`` runs
+    after one warm-up, the median block ms, and the block's output."""
+    from oracle import pairstack as ps
+
+    sub = lambda prefix: ps.sub_params(state, prefix)  # noqa: E731
+    steps = (
+        ("trimul_outgoing", lambda x: ps.triangle_multiplication(x, mask, sub("tri_multi_outgoing"), outgoing=True)),
+        ("trimul_incoming", lambda x: ps.triangle_multiplication(x, mask, sub("tri_multi_incoming"), outgoing=False)),
+        ("triattn_starting", lambda x: ps.triangle_attention(x, mask, sub("tri_atten_starting"), starting=True, n_head=4)),
+        ("triattn_ending", lambda x: ps.triangle_attention(x, mask, sub("tri_atten_ending"), starting=False, n_head=4)),
+        ("transition", lambda x: ps.transition(x, sub("transition_pair"))),
+    )
+    times: dict[str, list[float]] = {name: [] for name, _ in steps}
+    blocks, out = [], None
+    for r in range(runs + 1):
+        x = z.float()
+        t_block = time.perf_counter()
+        for name, fn in steps:
+            t0 = time.perf_counter()
+            x = fn(x)
+            if r:
+                times[name].append(time.perf_counter() - t0)
+        if r:
+            blocks.append(time.perf_counter() - t_block)
+        out = x
+    ops = {name: round(statistics.median(t) * 1e3, 1) for name, t in times.items()}
+    return ops, statistics.median(blocks) * 1e3, out
+
+
+def cpu_model() -> str:
     import platform
 
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(z, mask, state, gpu_out, runs: int, small: dict | None = None) -> dict:
+    """The fp32 CPU oracle on the host's cores (at most 16 threads, the box's CPU share):
+    the timed workload's block op by op, the N = 384 block (``small``: z, mask, state) op by op,
+    and the single triangle-attention op at z [1, 128, 128, 128] (the reference's CPU case)."""
     import torch
 
     from oracle import pairstack as ps
 
     threads = min(16, os.cpu_count() or 1)
     torch.set_num_threads(threads)
-    ps.pairformer_block(z, mask, state)  # warm-up
-    times = []
-    out = None
-    for _ in range(runs):
-        t0 = time.perf_counter()
-        out = ps.pairformer_block(z, mask, state)
-        times.append(time.perf_counter() - t0)
+    ops, block_ms, out = _cpu_ops(z, mask, state, runs)
     where = mask[:, :, None] & mask[:, None, :]
     rr = ps.rel_rms(gpu_out.double() - z.double(), out.double() - z.double(), where)
-    cpu = platform.processor() or platform.machine()
-    try:
-        for line in Path("/proc/cpuinfo").read_text().splitlines():
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(statistics.median(times) * 1e3, 1), "unit": "ms per block",
-            "cores": threads, "kind": "port",
-            "sample": f"the full timed workload: one block at N={z.shape[1]}, fp32, oracle/pairstack.py, "
-                      f"median of {runs} after 1 warm-up; {cpu}",
-            "gpu_vs_cpu_update_rel_rms": round(rr, 5)}
+    result = {"value": round(block_ms, 1), "unit": "ms per block",
+              "cores": threads, "kind": "port",
+              "sample": f"the full timed workload: one block at N={z.shape[1]}, fp32, oracle/pairstack.py, "
+                        f"op by op, median of {runs} after 1 warm-up; {threads} threads of {cpu_model()}",
+              "ops_ms": ops, "gpu_vs_cpu_update_rel_rms": round(rr, 5)}
+    if small is not None:
+        ops384, block384, _ = _cpu_ops(small["z"], small["mask"], small["state"], runs)
+        result["n384"] = {"ms_per_block": round(block384, 1), "ops_ms": ops384}
+    # the single triangle-attention op (starting node) on z [1, 128, 128, 128] fp32, 4 x 32 heads,
+    # all-ones mask, seed 0 (the reference's CPU-runnable case)
+    from foldforge_amd import factories
+    from foldforge_amd.trunk import randomise
+
+    ta = randomise(factories.triangle_attention(128, 4, starting=True, model="af3", precision="fp32"), seed=0)
+    params = {k: v.float() for k, v in ta.state_dict().items()}
+    z1 = torch.randn(1, 128, 128, 128, generator=torch.Generator().manual_seed(0))
+    m1 = torch.ones(1, 128, dtype=torch.bool)
+    ps.triangle_attention(z1, m1, params, starting=True, n_head=4)
+    times = []
+    for _ in range(max(3, runs)):
+        t0 = time.perf_counter()
+        ps.triangle_attention(z1, m1, params, starting=True, n_head=4)
+        times.append(time.perf_counter() - t0)
+    result["triattn_op_n128_fp32_ms"] = round(statistics.median(times) * 1e3, 2)
+    return result
 
 
 def main() -> int:
@@ -515,8 +607,7 @@ def main() -> int:
         return 2
     import torch
 
-    from foldforge_amd import factories, serving
-    from foldforge_amd.policy import guard
+    from foldforge_amd import dispatch, factories
     from foldforge_amd.trunk import randomise
 
     if not torch.cuda.is_available():
@@ -547,8 +638,7 @@ def main() -> int:
     mask_cpu[0, length:] = False
     block = randomise(factories.pairformer_block(d_pair=128, triangle_model="af3"), seed=args.seed).to(dev)
     block.set_backend("hip")
-    for m in block.children_ops():
-        guard(m, "error")  # a refused call would raise instead of running torch ops
+    dispatch.set_refusal(block, "error")  # a refused call would raise instead of running torch ops
     z, mask = z_cpu.to(dev), mask_cpu.to(dev)
 
     with torch.no_grad():
@@ -572,10 +662,21 @@ def main() -> int:
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
     ms_per_step = start.elapsed_time(end) / args.steps
-    served = serving.report_observations(block)["modules"]
-    hip_calls = sum(v["served_host_calls"].get("hip", 0) for v in served.values())
+    hip_calls = dispatch.served_count(block, "hip")
     print(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step (wall {wall * 1e3 / args.steps:.3f}); "
           f"hip op calls {hip_calls}", file=sys.stderr, flush=True)
+
+    per_op = op_times(block, z, mask, length, args.kernel_reps)
+    g384 = torch.Generator().manual_seed(args.seed + 1)
+    z384_cpu = torch.randn(1, 384, 384, 128, generator=g384).bfloat16()
+    mask384_cpu = torch.ones(1, 384, dtype=torch.bool)
+    block384 = randomise(factories.pairformer_block(d_pair=128, triangle_model="af3"), seed=args.seed + 1).to(dev)
+    block384.set_backend("hip")
+    dispatch.set_refusal(block384, "error")
+    per_op_384 = op_times(block384, z384_cpu.to(dev), mask384_cpu.to(dev), 384, args.kernel_reps)
+    per_op_384["reference_h100_engine_cuda_ms"] = REFERENCE_H100_MS_384
+    print(f"N=384 block {per_op_384['ms_per_block']} ms; ops " +
+          ", ".join(f"{k} {v['ms']}" for k, v in per_op_384["ops"].items()), file=sys.stderr, flush=True)
 
     roof = flash_roofline(n, length, args.kernel_reps)
     ln = layernorm_roofline(n, args.kernel_reps)
@@ -586,15 +687,26 @@ def main() -> int:
 
     base = None
     if not args.no_cpu_baseline:
-        base = cpu_baseline(z_cpu, mask_cpu, block.state_dict(), gpu_out, args.cpu_runs)
+        small = {"z": z384_cpu, "mask": mask384_cpu,
+                 "state": {k: v.cpu() for k, v in block384.state_dict().items()}}
+        base = cpu_baseline(z_cpu, mask_cpu, {k: v.cpu() for k, v in block.state_dict().items()},
+                            gpu_out, args.cpu_runs, small)
         print(f"cpu baseline {base['value']} ms/block on {base['cores']} threads", file=sys.stderr, flush=True)
 
     gflop = block_gflop(n)
+    gflop_run = sum(op_gflop(n, key_extent(n, length)).values())
     trunk = None
+    ladder_rows = None
     if not args.no_trunk:
         trunk = trunk_measure(512, 2)
         print(f"trunk {trunk['ms_per_trunk']} ms ({trunk['ms_per_block']} ms/block)", file=sys.stderr,
               flush=True)
+        ladder_rows = []
+        for ln_ in (768, 1024):
+            torch.cuda.empty_cache()
+            row = trunk_measure(ln_, 1)
+            ladder_rows.append({k: row[k] for k in ("n", "ms_per_trunk", "ms_per_block", "trunk_tflops", "finite")})
+            print(f"ladder N={ln_}: trunk {row['ms_per_trunk']} ms", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC,
         "value": round(ms_per_step, 4),
@@ -613,12 +725,17 @@ def main() -> int:
                         "c_z=128, trimul hidden 128, triangle attention 4x32, transition x4, batch 1",
             "n_tokens": n, "real_length": length, "batch": 1, "c_z": 128,
             "block_gflop": round(gflop, 1), "block_tflops": round(gflop / ms_per_step, 1),
+            "block_gflop_executed": round(gflop_run, 1),
+            "block_tflops_executed": round(gflop_run / ms_per_step, 1),
+            "key_extent_executed": key_extent(n, length),
             "clock_settle": {"untimed_steps_after_warmup": settle_steps, "ms": round(settle_ms, 1)},
         },
         "roofline": roof,
         "kernels": {"layer_norm": ln, **({"copy_reference": copy} if copy else {})},
         "cpu_baseline": base,
+        "ops": {"n512_ragged": per_op, "n384": per_op_384},
         "trunk": trunk,
+        "ladder": ladder_rows,
     }
     print(json.dumps(line), flush=True)
     return 0

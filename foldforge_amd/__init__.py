@@ -26,15 +26,14 @@ def load(name: str = "pairformer-trunk", checkpoint=None, *, backend: str = "min
     """
     import torch
 
-    from foldforge_amd.backends import BackendPlan
-    from foldforge_amd.graph import configure_model
-    from foldforge_amd.policy import apply_plan
+    from foldforge_amd import dispatch
+    from foldforge_amd.adapter import place
     from foldforge_amd.trunk import PairformerTrunk, randomise
 
     if name != "pairformer-trunk":
         raise ValueError(f"unknown model {name!r}; this build serves 'pairformer-trunk'")
     dtype = torch.bfloat16 if dtype is None else dtype
-    plan = BackendPlan.make(backend, engine_ops, unsupported)
+    plan = dispatch.Plan.of(backend, engine_ops, unsupported)
     model = PairformerTrunk(blocks, d_single=d_single)
     if checkpoint is None:
         randomise(model, seed, out_scale=out_scale)
@@ -58,8 +57,8 @@ def load(name: str = "pairformer-trunk", checkpoint=None, *, backend: str = "min
         if state is not None:
             model.load_state_dict(state, strict=True)
     device = torch.device(device)
-    configure_model(model, dtype, device)
-    plan.resolve(device)
-    model.foldforge_load_report = {"engine_backends": {"plan": plan.report(),
-                                                       "modules": apply_plan(model, plan, device)}}
+    place(model, dtype, device)
+    picks = plan.resolve(dispatch.device_arch(device))
+    model.foldforge_load_report = {"engine_backends": {"plan": plan.summary(picks),
+                                                       "modules": dispatch.install(model, plan, device)}}
     return model

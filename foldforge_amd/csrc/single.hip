@@ -83,7 +83,10 @@ size_t row_gemm_lds(int xsrc, int K, int no) {
 }
 
 // The input row of logical row m under the row map a.tmap (see kMap* in ffk_kernels.h).
+// The last workgroup's rows past M (the grid covers M rounded up to 32) read row M - 1: they
+// are never stored, and an unclamped transposed map would read past the end of the input.
 __device__ inline int64_t mapped_row(const RowGemmArgs& a, int64_t m) {
+  m = min(m, a.M - 1);
   if (a.tmap == kMapPairT) {
     const int64_t nn = (int64_t)a.n * a.n;
     const int64_t b = m / nn, rem = m - b * nn;
@@ -96,12 +99,13 @@ __device__ inline int64_t mapped_row(const RowGemmArgs& a, int64_t m) {
     const int i = min((int)(rem / a.npm), a.n - 1), k = min((int)(rem % a.npm), a.n - 1);
     return a.tmap == kMapGridOut ? (b * a.n + i) * a.n + k : (b * a.n + k) * a.n + i;
   }
-  return min(m, a.M - 1);
+  return m;
 }
 
 // kEpiOpm: the MSA row read by logical row m = (b n + j) sp + s (rows past the depth repeat
 // the last one; their projection is zeroed).
 __device__ inline int64_t opm_msa_row(const RowGemmArgs& a, int64_t m) {
+  m = min(m, a.M - 1);
   const int64_t bj = m / a.sp;
   const int s = min((int)(m - bj * a.sp), a.depth - 1);
   const int64_t b = bj / a.n;

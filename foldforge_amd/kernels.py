@@ -25,6 +25,16 @@ TRI_HEADS = 4
 TRI_HEAD_DIM = 32
 
 
+#: The device type the kernels run on. Host-side argument checks compare against it, so a
+#: CPU test can exercise them by pointing it at "cpu" (nothing reaches the library then:
+#: every such test expects a ValueError before the native call).
+DEVICE_TYPE = "cuda"
+
+
+def _on_device(t: Tensor) -> bool:
+    return t.device.type == DEVICE_TYPE
+
+
 def _ptr(t: Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
@@ -38,10 +48,26 @@ def _need(cond: bool, message: str) -> None:
         raise ValueError(message)
 
 
-def _param(t: Tensor, device: torch.device, name: str) -> Tensor:
+def _param(t: Tensor, device: torch.device, name: str, shape: tuple[int, ...] | None = None) -> Tensor:
+    """An fp32 parameter on ``device`` of exactly ``shape``: the C-ABI receives no sizes for
+    parameters, so a wrong shape must stop here, not as an out-of-bounds device read."""
+    _need(isinstance(t, Tensor), f"{name} is missing")
     _need(t.device == device, f"{name} is on {t.device}, expected {device}")
     _need(t.dtype == torch.float32, f"{name} must be fp32 (got {t.dtype})")
+    if shape is not None:
+        _need(tuple(t.shape) == tuple(shape), f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
     return t.contiguous()
+
+
+def _output(out: Tensor | None, shape: tuple[int, ...], dtype: torch.dtype, device: torch.device) -> Tensor:
+    """The caller's ``out=`` tensor (checked: it is written through a raw pointer) or a new one."""
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    _need(tuple(out.shape) == tuple(shape), f"out has shape {tuple(out.shape)}, expected {tuple(shape)}")
+    _need(out.dtype == dtype, f"out must be {dtype} (got {out.dtype})")
+    _need(out.device == device, f"out is on {out.device}, expected {device}")
+    _need(out.is_contiguous(), "out must be contiguous")
+    return out
 
 
 def _workspace(nbytes: int, device: torch.device) -> Tensor:
@@ -66,7 +92,7 @@ def triangle_attention_supported(d_pair: int, n_head: int, d_head: int, transpos
 
 
 def _pair(z: Tensor, mask: Tensor, width: int | None = PAIR_WIDTH) -> tuple[int, int]:
-    _need(z.is_cuda, "z must be a device tensor")
+    _need(_on_device(z), "z must be a device tensor")
     _need(z.dtype == torch.bfloat16, f"z must be bf16 (got {z.dtype})")
     _need(z.dim() == 4 and z.shape[1] == z.shape[2], f"z must be [B, N, N, c] (got {tuple(z.shape)})")
     if width is not None:
@@ -79,14 +105,14 @@ def _pair(z: Tensor, mask: Tensor, width: int | None = PAIR_WIDTH) -> tuple[int,
 
 def layer_norm(x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: float = 1e-5) -> Tensor:
     """LayerNorm over the last axis (fp32 statistics and affine), returned in ``x.dtype``."""
-    _need(x.is_cuda and x.is_contiguous(), "x must be a contiguous device tensor")
+    _need(_on_device(x) and x.is_contiguous(), "x must be a contiguous device tensor")
     _need(x.dtype in (torch.bfloat16, torch.float32), f"x must be bf16 or fp32 (got {x.dtype})")
     cols = x.shape[-1]
     for t, name in ((weight, "weight"), (bias, "bias")):
         if t is not None:
             _need(t.numel() == cols, f"{name} has {t.numel()} entries for {cols} channels")
-    weight = None if weight is None else _param(weight, x.device, "weight")
-    bias = None if bias is None else _param(bias, x.device, "bias")
+    weight = None if weight is None else _param(weight, x.device, "weight", (cols,))
+    bias = None if bias is None else _param(bias, x.device, "bias", (cols,))
     y = torch.empty_like(x)
     dtype = 0 if x.dtype == torch.bfloat16 else 1
     status = _native.lib().ffk_layer_norm(
@@ -120,18 +146,18 @@ def triangle_multiplicative_update(
     batch, n = _pair(z, mask, width=None)
     c = z.shape[3]
     dev = z.device
-    names = ("ln_pair_weight", "ln_pair_bias", "to_left", "to_right", "to_left_gate",
-             "to_right_gate", "ln_out_weight", "ln_out_bias", "to_out", "to_gate")
-    ps = [_param(t, dev, nm) for t, nm in zip(
-        (ln_pair_weight, ln_pair_bias, to_left, to_right, to_left_gate, to_right_gate,
-         ln_out_weight, ln_out_bias, to_out, to_gate), names)]
     hidden = to_left.shape[0]
-    _need(to_left.shape == (hidden, c), f"to_left {tuple(to_left.shape)}")
     _need(trimul_supported(c, hidden), f"d_pair={c} d_hidden={hidden} (the kernels take 128 / 128, "
           "or a pair width a multiple of 64 up to 256 with a hidden width a multiple of 64 up to 768)")
+    spec = (("ln_pair_weight", ln_pair_weight, (c,)), ("ln_pair_bias", ln_pair_bias, (c,)),
+            ("to_left", to_left, (hidden, c)), ("to_right", to_right, (hidden, c)),
+            ("to_left_gate", to_left_gate, (hidden, c)), ("to_right_gate", to_right_gate, (hidden, c)),
+            ("ln_out_weight", ln_out_weight, (hidden,)), ("ln_out_bias", ln_out_bias, (hidden,)),
+            ("to_out", to_out, (c, hidden)), ("to_gate", to_gate, (c, c)))
+    ps = [_param(t, dev, nm, shape) for nm, t, shape in spec]
+    out = _output(out, tuple(z.shape), torch.bfloat16, dev)
     lib = _native.lib()
     ws = _workspace(lib.ffk_triangle_multiplication_workspace(batch, n, c, hidden), dev)
-    out = torch.empty_like(z) if out is None else out
     status = lib.ffk_triangle_multiplication(
         z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
         ws.data_ptr(), ws.numel(), batch, n, c, hidden, int(outgoing), int(residual),
@@ -164,21 +190,22 @@ def triangle_attention(
     batch, n = _pair(z, mask, width=None)
     c = z.shape[3]
     dev = z.device
-    ps = [_param(t, dev, nm) for t, nm in zip(
-        (ln_pair_weight, ln_pair_bias, to_bias, to_query, to_key, to_value, to_gate, to_out),
-        ("ln_pair_weight", "ln_pair_bias", "to_bias", "to_query", "to_key", "to_value",
-         "to_gate", "to_out"))]
     hd = to_query.shape[0]
-    _need(hd % n_head == 0, f"hidden {hd} is not a multiple of {n_head} heads")
+    _need(n_head > 0 and hd % n_head == 0, f"hidden {hd} is not a multiple of {n_head} heads")
+    spec = (("ln_pair_weight", ln_pair_weight, (c,)), ("ln_pair_bias", ln_pair_bias, (c,)),
+            ("to_bias", to_bias, (n_head, c)), ("to_query", to_query, (hd, c)),
+            ("to_key", to_key, (hd, c)), ("to_value", to_value, (hd, c)),
+            ("to_gate", to_gate, (hd, c)), ("to_out", to_out, (c, hd)))
+    ps = [_param(t, dev, nm, shape) for nm, t, shape in spec]
     d = hd // n_head
     _need(triangle_attention_supported(c, n_head, d, transposed_bias),
           f"d_pair={c} heads={n_head} x {d} (the kernels take 128 with 4 x 32, or pair 64 / 128 / "
           "256 with at most 32 heads of 8 to 32 channels, heads x d_head a multiple of 64)")
     if (c, n_head, d) != (128, 4, 32):
         _need(batch * n <= 65535, f"batch x n = {batch * n} exceeds the launch grid")
+    out = _output(out, tuple(z.shape), torch.bfloat16, dev)
     lib = _native.lib()
     ws = _workspace(lib.ffk_triangle_attention_workspace(batch, n, c, n_head, d), dev)
-    out = torch.empty_like(z) if out is None else out
     status = lib.ffk_triangle_attention(
         z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
         ws.data_ptr(), ws.numel(), batch, n, c, n_head, d, int(starting),
@@ -202,7 +229,7 @@ def transition(
 ) -> Tensor:
     """SwiGLU transition of ``x [..., d]`` bf16: one fused kernel at d = 128 x 4, token-row
     GEMMs (LayerNorm, expand with SwiGLU epilogue, squeeze + residual) at other widths."""
-    _need(x.is_cuda and x.is_contiguous(), "x must be a contiguous device tensor")
+    _need(_on_device(x) and x.is_contiguous(), "x must be a contiguous device tensor")
     _need(x.dtype == torch.bfloat16, f"x must be bf16 (got {x.dtype})")
     d = x.shape[-1]
     factor = expand_a.shape[0] // d
@@ -211,13 +238,14 @@ def transition(
     _need(expand_a.shape == (factor * d, d) and expand_b.shape == (factor * d, d)
           and squeeze.shape == (d, factor * d), "expand_a/expand_b [f d, d], squeeze [d, f d]")
     dev = x.device
-    ps = [_param(t, dev, nm) for t, nm in zip(
-        (ln_weight, ln_bias, expand_a, expand_b, squeeze),
-        ("ln_weight", "ln_bias", "expand_a", "expand_b", "squeeze"))]
+    spec = (("ln_weight", ln_weight, (d,)), ("ln_bias", ln_bias, (d,)),
+            ("expand_a", expand_a, (factor * d, d)), ("expand_b", expand_b, (factor * d, d)),
+            ("squeeze", squeeze, (d, factor * d)))
+    ps = [_param(t, dev, nm, shape) for nm, t, shape in spec]
     rows = x.numel() // d
+    out = _output(out, tuple(x.shape), torch.bfloat16, dev)
     lib = _native.lib()
     ws = _workspace(lib.ffk_transition_workspace(rows, d, factor), dev)
-    out = torch.empty_like(x) if out is None else out
     status = lib.ffk_transition(
         x.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(), ws.data_ptr(), ws.numel(),
         rows, d, factor, int(residual), float(eps), _stream(dev),
@@ -265,7 +293,7 @@ def attention_pair_bias(
     """Single-track attention with pair bias: ``s [B, N, c_s]`` bf16 attends over tokens with
     the bias ``LN_pair(z) . to_bias`` from ``z [B, N, N, 128]`` bf16, under the key mask."""
     batch, n = _pair(z, mask)
-    _need(s.is_cuda and s.is_contiguous() and s.dtype == torch.bfloat16,
+    _need(_on_device(s) and s.is_contiguous() and s.dtype == torch.bfloat16,
           "s must be a contiguous bf16 device tensor")
     _need(s.dim() == 3 and s.shape[:2] == z.shape[:2], f"s {tuple(s.shape)} does not match z")
     cs = s.shape[-1]
@@ -273,18 +301,15 @@ def attention_pair_bias(
           f"single width {cs} with {n_head} heads (the kernels take a multiple of 64 split "
           "into at most 32 heads of 8, 16, 24 or 32)")
     dev = s.device
-    names = ("ln_single_weight", "ln_single_bias", "to_query", "query_bias", "to_key", "to_value",
-             "ln_pair_weight", "to_bias", "to_gate", "to_out")
-    tensors = (ln_single_weight, ln_single_bias, to_query, query_bias, to_key, to_value,
-               ln_pair_weight, to_bias, to_gate, to_out)
-    ps = [_param(t, dev, nm) for t, nm in zip(tensors, names)]
-    for t, nm in zip(ps, names):
-        if nm.startswith("to_") and nm != "to_bias":
-            _need(t.shape == (cs, cs), f"{nm} {tuple(t.shape)} (expected [{cs}, {cs}])")
-    _need(ps[7].shape == (n_head, PAIR_WIDTH), f"to_bias {tuple(ps[7].shape)}")
+    spec = (("ln_single_weight", ln_single_weight, (cs,)), ("ln_single_bias", ln_single_bias, (cs,)),
+            ("to_query", to_query, (cs, cs)), ("query_bias", query_bias, (cs,)),
+            ("to_key", to_key, (cs, cs)), ("to_value", to_value, (cs, cs)),
+            ("ln_pair_weight", ln_pair_weight, (PAIR_WIDTH,)), ("to_bias", to_bias, (n_head, PAIR_WIDTH)),
+            ("to_gate", to_gate, (cs, cs)), ("to_out", to_out, (cs, cs)))
+    ps = [_param(t, dev, nm, shape) for nm, t, shape in spec]
+    out = _output(out, tuple(s.shape), torch.bfloat16, dev)
     lib = _native.lib()
     ws = _workspace(lib.ffk_attention_pair_bias_workspace(batch, n, cs, PAIR_WIDTH, n_head), dev)
-    out = torch.empty_like(s) if out is None else out
     status = lib.ffk_attention_pair_bias(
         s.data_ptr(), z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
         ws.data_ptr(), ws.numel(), batch, n, cs, PAIR_WIDTH, n_head, float(gate_bias),
@@ -321,7 +346,7 @@ def msa_pair_weighted_averaging(
     """MSA pair-weighted averaging of ``m [B, S, N, c_m]`` bf16 with the weights
     ``softmax_j(LN_pair(z) . to_bias)`` from ``z [B, N, N, 128]`` bf16, under the key mask."""
     batch, n = _pair(z, mask)
-    _need(m.is_cuda and m.is_contiguous() and m.dtype == torch.bfloat16,
+    _need(_on_device(m) and m.is_contiguous() and m.dtype == torch.bfloat16,
           "m must be a contiguous bf16 device tensor")
     _need(m.dim() == 4 and m.shape[0] == batch and m.shape[2] == n,
           f"m {tuple(m.shape)} does not match z {tuple(z.shape)}")
@@ -333,17 +358,14 @@ def msa_pair_weighted_averaging(
           f"d_msa={cm} heads={n_head} x {dh} (the kernels take d_msa a multiple of 64 up to 768, "
           "at most 32 heads of a multiple of 4, heads x d_head a multiple of 64)")
     dev = m.device
-    names = ("ln_msa_weight", "ln_msa_bias", "ln_pair_weight", "to_bias", "to_value", "to_gate",
-             "to_out")
-    ps = [_param(t, dev, nm) for t, nm in zip(
-        (ln_msa_weight, ln_msa_bias, ln_pair_weight, to_bias, to_value, to_gate, to_out), names)]
-    _need(ps[3].shape == (n_head, PAIR_WIDTH), f"to_bias {tuple(ps[3].shape)}")
-    _need(ps[4].shape == (hd, cm) and ps[5].shape == (hd, cm) and ps[6].shape == (cm, hd),
-          "to_value / to_gate [H d, c_m], to_out [c_m, H d]")
+    spec = (("ln_msa_weight", ln_msa_weight, (cm,)), ("ln_msa_bias", ln_msa_bias, (cm,)),
+            ("ln_pair_weight", ln_pair_weight, (PAIR_WIDTH,)), ("to_bias", to_bias, (n_head, PAIR_WIDTH)),
+            ("to_value", to_value, (hd, cm)), ("to_gate", to_gate, (hd, cm)), ("to_out", to_out, (cm, hd)))
+    ps = [_param(t, dev, nm, shape) for nm, t, shape in spec]
+    out = _output(out, tuple(m.shape), torch.bfloat16, dev)
     lib = _native.lib()
     ws = _workspace(lib.ffk_msa_pair_weighted_averaging_workspace(batch, depth, n, cm, PAIR_WIDTH,
                                                                   n_head, dh), dev)
-    out = torch.empty_like(m) if out is None else out
     status = lib.ffk_msa_pair_weighted_averaging(
         m.data_ptr(), z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
         ws.data_ptr(), ws.numel(), batch, depth, n, cm, PAIR_WIDTH, n_head, dh, int(residual),
@@ -379,7 +401,7 @@ def outer_product_mean(
     """Outer product mean of ``m [B, S, N, c_m]`` bf16 under the MSA row mask
     ``rows_mask [B, S, N]`` bool -> ``[B, N, N, 128]`` bf16 (plus ``residual`` when given).
     ``count_offset`` None divides by ``max(n, 1)``, a number by ``n + count_offset``."""
-    _need(m.is_cuda and m.is_contiguous() and m.dtype == torch.bfloat16,
+    _need(_on_device(m) and m.is_contiguous() and m.dtype == torch.bfloat16,
           "m must be a contiguous bf16 device tensor")
     _need(m.dim() == 4, f"m must be [B, S, N, c_m] (got {tuple(m.shape)})")
     batch, depth, n, cm = m.shape
@@ -393,20 +415,19 @@ def outer_product_mean(
           "up to 768, d_hidden 32, d_pair 128)")
     _need(depth > 0 and n > 0 and batch > 0, "empty MSA")
     dev = m.device
-    names = ("ln_weight", "ln_bias", "to_left", "to_right", "to_out", "to_out_bias")
-    ln_w, ln_b, wl, wr, wo, bo = (_param(t, dev, nm) for t, nm in zip(
-        (ln_weight, ln_bias, to_left, to_right, to_out, to_out_bias), names))
-    _need(wl.shape == (hidden, cm) and wr.shape == (hidden, cm), "to_left / to_right [32, c_m]")
-    _need(wo.shape == (cz, hidden * hidden) and bo.shape == (cz,), "to_out [128, 1024] + bias [128]")
-    bl = None if left_bias is None else _param(left_bias, dev, "left_bias")
-    br = None if right_bias is None else _param(right_bias, dev, "right_bias")
+    spec = (("ln_weight", ln_weight, (cm,)), ("ln_bias", ln_bias, (cm,)),
+            ("to_left", to_left, (hidden, cm)), ("to_right", to_right, (hidden, cm)),
+            ("to_out", to_out, (cz, hidden * hidden)), ("to_out_bias", to_out_bias, (cz,)))
+    ln_w, ln_b, wl, wr, wo, bo = (_param(t, dev, nm, shape) for nm, t, shape in spec)
+    bl = None if left_bias is None else _param(left_bias, dev, "left_bias", (hidden,))
+    br = None if right_bias is None else _param(right_bias, dev, "right_bias", (hidden,))
     if residual is not None:
         _need(residual.dtype == torch.bfloat16 and residual.is_contiguous()
               and tuple(residual.shape) == (batch, n, n, cz) and residual.device == dev,
               "residual must be a contiguous bf16 [B, N, N, 128] device tensor")
+    out = _output(out, (batch, n, n, cz), torch.bfloat16, dev)
     lib = _native.lib()
     ws = _workspace(lib.ffk_outer_product_mean_workspace(batch, depth, n, cm, hidden, cz), dev)
-    out = torch.empty(batch, n, n, cz, dtype=torch.bfloat16, device=dev) if out is None else out
     status = lib.ffk_outer_product_mean(
         m.data_ptr(), rows_mask.data_ptr(), ln_w.data_ptr(), ln_b.data_ptr(), wl.data_ptr(),
         None if bl is None else bl.data_ptr(), wr.data_ptr(), None if br is None else br.data_ptr(),
@@ -463,7 +484,13 @@ def flash_attention_bias(
     _need(bias_blk.dtype == torch.float32 and bias_blk.numel() == batch * heads * n_pad * n_pad,
           "bias_blk must be the blocked fp32 layout of [B, H, Np, Np]")
     _need(all(t.is_contiguous() for t in (q, k, v_t, bias_blk)), "operands must be contiguous")
-    _need(out.dtype == torch.bfloat16 and out.shape[-1] == heads * d, "out [..., H * 32] bf16")
+    _need(out.dtype == torch.bfloat16 and out.dim() == 4 and out.shape[-1] == heads * d,
+          "out must be bf16 [B, R, n_valid, H * 32]")
+    _need(out.device == q.device and out.stride(3) == 1, "out must be on q's device with unit channel stride")
+    _need(0 <= rows_valid <= rows and 0 <= n_valid <= n_pad, "valid extents exceed the operands")
+    _need(out.shape[0] >= batch and out.shape[1] >= rows_valid and out.shape[2] >= n_valid,
+          f"out {tuple(out.shape)} does not cover [{batch}, {rows_valid}, {n_valid}, {heads * d}]")
+    _need(all(t.device == q.device for t in (k, v_t, bias_blk)), "operands must share q's device")
     status = _native.lib().ffk_flash_attention_bias(
         q.data_ptr(), k.data_ptr(), v_t.data_ptr(), bias_blk.data_ptr(), out.data_ptr(),
         batch, heads, rows, n_pad, rows_valid, n_valid,

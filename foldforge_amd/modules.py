@@ -7,8 +7,10 @@ keep their contract (``src/foldforge/modules/engine/policy.py:85-101``,
 
 * ``backends`` (class attribute), ``backend``, ``set_backend(name)``;
 * ``unsupported(*args) -> str | None``: whether the CURRENT backend takes the call,
-  asked before the call; ``forward`` raises :class:`BackendUnsupported` for a call
-  outside the backend's range (the engine never falls back; FoldForge's guard does);
+  asked before the call; ``forward`` and ``delta`` raise :class:`BackendUnsupported` for a
+  call outside the backend's range (the engine never falls back; FoldForge's guard does,
+  and so does a module given the refusal policy ``"fallback"`` by
+  :func:`foldforge_amd.dispatch.install`);
 * ``_forward_<backend>(*args)`` for every listed backend;
 * residual-owning forwards (``x + f(x)``) and ``delta(*args)`` for the bare update;
 * ``dead = False`` class attribute; a dead module returns its input unchanged;
@@ -28,7 +30,7 @@ from typing import Any
 import torch
 from torch import nn
 
-from foldforge_amd import torch_ops
+from foldforge_amd import dispatch, torch_ops
 
 Tensor = torch.Tensor
 
@@ -90,10 +92,19 @@ class MasterWeights:
 
 
 class EngineOp:
-    """Backend dispatch of one op class (mixed into an ``nn.Module``)."""
+    """Backend dispatch of one op class (mixed into an ``nn.Module``).
+
+    A call goes to ``_forward_<backend>``. When the backend refuses it (``unsupported``
+    returns a reason) the module's ``refusal_policy`` decides: ``None`` (the engine's own
+    behaviour) raises :class:`BackendUnsupported`; ``"error"`` raises
+    :class:`foldforge_amd.dispatch.BackendUnsupportedError`; ``"fallback"`` runs ``pytorch``
+    and logs the reason once. ``forward`` and ``delta`` take the same route, so a refused
+    call never changes backend silently. Every call is counted in the module's ledger.
+    """
 
     backends: tuple[str, ...] = ("pytorch", "hip")
     dead: bool = False
+    refusal_policy: str | None = None
 
     def _init_backend(self, backend: str) -> None:
         self.backend = "pytorch"
@@ -112,17 +123,22 @@ class EngineOp:
             return None
         return getattr(self, f"_unsupported_{self.backend}")(*args, **kwargs)
 
+    def _route(self, args: tuple, kwargs: dict) -> str:
+        """The backend this call runs on (refusals handled by the policy, the call counted)."""
+        backend = self.backend
+        if backend != "pytorch":
+            reason = self.unsupported(*args, **kwargs)
+            if reason is not None:
+                backend = dispatch.on_refusal(self, reason, BackendUnsupported)  # type: ignore[arg-type]
+        dispatch.note_call(self, backend)  # type: ignore[arg-type]
+        return backend
+
     def forward(self, *args: Any, **kwargs: Any) -> Any:
-        reason = self.unsupported(*args, **kwargs)
-        if reason is not None:
-            raise BackendUnsupported(f"{type(self).__name__} backend {self.backend!r}: {reason}")
-        return getattr(self, f"_forward_{self.backend}")(*args, **kwargs)
+        return getattr(self, f"_forward_{self._route(args, kwargs)}")(*args, **kwargs)
 
     def delta(self, *args: Any, **kwargs: Any) -> Tensor:
         """The bare update ``f(x)`` (the forward returns ``x + f(x)``)."""
-        reason = self.unsupported(*args, **kwargs)
-        backend = "pytorch" if reason is not None else self.backend
-        return getattr(self, f"_forward_{backend}")(*args, residual=False, **kwargs)
+        return getattr(self, f"_forward_{self._route(args, kwargs)}")(*args, residual=False, **kwargs)
 
 
 def _linear(d_in: int, d_out: int, bias: bool = False) -> nn.Linear:
@@ -597,9 +613,7 @@ class OuterProductMean(EngineOp, MasterWeights, nn.Module):
 
     def delta(self, m: Tensor, mask: Tensor, residual: Tensor | None = None) -> Tensor:
         """The update alone (what the forward returns without ``residual``)."""
-        reason = self.unsupported(m, mask)
-        backend = "pytorch" if reason is not None else self.backend
-        return getattr(self, f"_forward_{backend}")(m, mask)
+        return getattr(self, f"_forward_{self._route((m, mask), {})}")(m, mask)
 
 
 # ------------------------------------------------------------------------------------ block
@@ -670,13 +684,12 @@ class PairformerBlock(MasterWeights, nn.Module):
                 bias: Tensor | None = None):
         c = self.config
         if c.parallel:
+            # every pair update reads the block's input (legacy/pairformer.py:176-190)
             z0 = pair
             upd = self.tri_multi_outgoing.delta(z0, key_mask) + self.tri_multi_incoming.delta(z0, key_mask)
-            upd = upd + self.transition_pair.delta(z0)
-            z1 = z0 + upd
             if c.use_triangle_attention:
-                z1 = z1 + self.tri_atten_starting.delta(z1, key_mask) + self.tri_atten_ending.delta(z1, key_mask)
-            pair_out = z1
+                upd = upd + self.tri_atten_starting.delta(z0, key_mask) + self.tri_atten_ending.delta(z0, key_mask)
+            pair_out = z0 + upd + self.transition_pair.delta(z0)
         else:
             z = self.tri_multi_outgoing(pair, key_mask)
             z = self.tri_multi_incoming(z, key_mask)

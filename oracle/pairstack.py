@@ -372,12 +372,16 @@ def pairformer_block(
     eps: float = 1e-5,
     dtype: torch.dtype = torch.float32,
     io_dtype: torch.dtype | None = None,
+    parallel: bool = False,
 ) -> Tensor | tuple[Tensor, Tensor]:
-    """One sequential (AF3) Pairformer block (``legacy/pairformer.py:191-230``).
+    """One Pairformer block: the sequential AF3 order (``legacy/pairformer.py:191-230``) or,
+    with ``parallel``, the schedule of ``legacy/pairformer.py:176-190`` and ``:208-226``.
 
-    ``z <- TM_out(z); z <- TM_in(z); z <- TA_start(z); z <- TA_end(z); z <- Tr(z)``;
-    with a single track ``s <- APB(s, z); s <- Tr_s(s)``. ``params`` holds the
-    block's engine keys (``tri_multi_outgoing.to_left.weight`` ...).
+    Sequential: ``z <- TM_out(z); z <- TM_in(z); z <- TA_start(z); z <- TA_end(z); z <- Tr(z)``;
+    with a single track ``s <- APB(s, z); s <- Tr_s(s)``.
+    Parallel: every update reads the block's input ``z0`` (``s0``):
+    ``z = z0 + (dTM_out + dTM_in + dTA_start + dTA_end) + dTr``, ``s = s0 + dAPB(s0, z0) +
+    dTr_s(s0)``. ``params`` holds the block's engine keys (``tri_multi_outgoing.to_left.weight`` ...).
 
     ``io_dtype`` (e.g. bf16) rounds the residual stream to that dtype after every op, as
     an engine op returns ``x + f(x)`` in its input dtype (``README.md:143-145``; bf16
@@ -388,6 +392,22 @@ def pairformer_block(
 
     def io(t: Tensor) -> Tensor:
         return t if io_dtype is None else t.to(io_dtype).to(dtype)
+
+    if parallel:
+        z0 = z.to(dtype)
+        upd = (triangle_multiplication(z, mask, sub_params(params, "tri_multi_outgoing"), outgoing=True, **kw) - z0) \
+            + (triangle_multiplication(z, mask, sub_params(params, "tri_multi_incoming"), outgoing=False, **kw) - z0)
+        for name, starting in (("tri_atten_starting", True), ("tri_atten_ending", False)):
+            if f"{name}.to_bias.weight" in params:
+                upd = upd + (triangle_attention(z, mask, sub_params(params, name), starting=starting,
+                                                n_head=n_head_pair, transposed_bias=transposed_bias, **kw) - z0)
+        z_out = io(z0 + upd + (transition(z, sub_params(params, "transition_pair"), **kw) - z0))
+        if s is None:
+            return z_out
+        s0 = s.to(dtype)
+        ds = attention_pair_bias(s, z, mask, sub_params(params, "single_attention"), n_head=n_head_single,
+                                 gate_bias=single_gate_bias, **kw) - s0
+        return z_out, io(s0 + ds + (transition(s, sub_params(params, "single_transition"), **kw) - s0))
 
     z = io(triangle_multiplication(
         z, mask, sub_params(params, "tri_multi_outgoing"), outgoing=True, **kw

@@ -18,7 +18,7 @@ def pytest_configure(config: pytest.Config) -> None:
 
 @pytest.fixture(autouse=True)
 def _fresh_log_state():
-    from foldforge_amd import policy
+    from foldforge_amd import dispatch
 
-    policy.forget_logged_refusals()
+    dispatch.forget_announcements()
     yield

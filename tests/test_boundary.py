@@ -1,6 +1,6 @@
-"""The drop-in boundary on the CPU: backend names and policy, the guard with its fallback and
-error policy, factories and precision, dead modules, the residual contract, and the
-``pytorch`` backend against the oracle.
+"""The drop-in boundary on the CPU: backend names and plans, the refusal policies (engine
+error, fallback, error), the parity helpers of the GPU tests, factories and precision, dead
+modules, the residual contract, and the ``pytorch`` backend against the oracle.
 
 Mirrors the reference's ``tests/kernels/test_backends.py``, ``test_engine_factories.py``,
 ``tests/models/test_dead_modules.py:97-136`` and ``test_released_conversions.py`` (the
@@ -16,7 +16,7 @@ import pytest
 import torch
 from torch import nn
 
-from foldforge_amd import backends, factories, graph, policy, serving
+from foldforge_amd import adapter, dispatch, factories
 from foldforge_amd.modules import (
     AttentionPairBias,
     BackendUnsupported,
@@ -32,65 +32,69 @@ from foldforge_amd.modules import (
 )
 from foldforge_amd.trunk import PairformerTrunk, randomise
 from oracle import pairstack as ps
+from tests.hip_calls import hip_delta, hip_forward
 
 
 def fake_gfx950(monkeypatch):
-    monkeypatch.setattr(backends, "capability", lambda _d: "gfx950")
+    monkeypatch.setattr(dispatch, "device_arch", lambda _d=None: "gfx950")
 
 
 def test_names_and_aliases():
-    assert set(backends.ENGINE_BACKENDS) >= {"pytorch", "hip", "cuda", "triton", "anthropic", "cueq"}
-    assert "miniworld" in backends.BACKENDS
+    assert set(dispatch.BACKEND_NAMES) >= {"pytorch", "hip", "cuda", "triton", "anthropic", "cueq"}
+    assert "miniworld" in dispatch.REQUESTABLE and "cuequivariance" in dispatch.REQUESTABLE
     with pytest.raises(ValueError, match="Unknown backend"):
-        backends.BackendPlan.make("magma")
+        dispatch.Plan.of("magma")
     with pytest.raises(ValueError, match="unknown op"):
-        backends.validate_ops({"nope": "pytorch"})
+        dispatch.check_ops({"nope": "pytorch"})
     with pytest.raises(ValueError, match="unknown backend"):
-        backends.validate_ops({"trimul": "nope"})
+        dispatch.check_ops({"trimul": "nope"})
     with pytest.raises(ValueError, match="engine.unsupported"):
-        backends.BackendPlan.make("pytorch", unsupported="ignore")
+        dispatch.Plan.of("pytorch", unsupported="ignore")
+    with pytest.raises(ValueError, match="Unknown backend"):
+        dispatch.pick("magma", Transition, "gfx950")
 
 
 def test_serves_is_derived_from_the_classes():
-    table = backends.SERVES
-    assert set(table) == set(backends.OPS)
+    table = dispatch.SERVES
+    assert set(table) == set(dispatch.OP_NAMES)
     for op in ("trimul", "triangle_attention", "transition", "layernorm", "single_attention",
                "msa_pwa", "opm"):
         assert table[op] == ("miniworld", "pytorch", "hip"), op
     assert table["dit_blocks"] == ()  # named, no class in this build
 
 
-def test_choose_backend(monkeypatch):
-    monkeypatch.setattr(backends, "capability", lambda _d: None)
-    assert backends.choose_backend("miniworld", Transition) == ("pytorch", None)
-    name, why = backends.choose_backend("hip", Transition)
+def test_pick():
+    assert dispatch.pick("miniworld", Transition, None) == ("pytorch", None)
+    name, why = dispatch.pick("hip", Transition, None)
     assert name == "pytorch" and "gfx950" in why
-    fake_gfx950(monkeypatch)
-    assert backends.choose_backend("miniworld", Transition) == ("hip", None)
-    assert backends.choose_backend("hip", TriangleMultiplication) == ("hip", None)
-    assert backends.choose_backend("miniworld", AttentionPairBias) == ("hip", None)
-    name, why = backends.choose_backend("cuda", AttentionPairBias)
-    assert name == "pytorch" and "no 'cuda' backend" in why
-    name, why = backends.choose_backend("cuda", Transition)
-    assert name == "pytorch" and "no 'cuda' backend" in why
+    assert dispatch.pick("miniworld", Transition, "gfx950") == ("hip", None)
+    assert dispatch.pick("hip", TriangleMultiplication, "gfx950") == ("hip", None)
+    assert dispatch.pick("miniworld", AttentionPairBias, "gfx950") == ("hip", None)
+    assert dispatch.pick("pytorch", AttentionPairBias, "gfx950") == ("pytorch", None)
+    for cls in (AttentionPairBias, Transition):
+        name, why = dispatch.pick("cuda", cls, "gfx950")
+        assert name == "pytorch" and "no 'cuda' backend" in why
+    name, why = dispatch.pick("cuequivariance", Transition, "gfx950")
+    assert name == "pytorch" and "'cueq'" in why
     # another ROCm card: the hip kernels are gfx950 code objects
-    monkeypatch.setattr(backends, "capability", lambda _d: "gfx942")
-    assert backends.choose_backend("miniworld", Transition) == ("pytorch", None)
-    assert backends.choose_backend("hip", Transition)[0] == "pytorch"
+    assert dispatch.pick("miniworld", Transition, "gfx942") == ("pytorch", None)
+    assert dispatch.pick("hip", Transition, "gfx942")[0] == "pytorch"
 
 
-def test_plan_resolve_reports_refused_ops(monkeypatch, caplog):
-    fake_gfx950(monkeypatch)
-    plan = backends.BackendPlan.make("pytorch", {"transition": "hip", "single_attention": "cuda"})
+def test_plan_resolve_reports_refused_ops(caplog):
+    plan = dispatch.Plan.of("pytorch", {"transition": "hip", "single_attention": "cuda"})
+    assert plan.requested("transition") == "hip" and plan.requested("trimul") == "pytorch"
     with caplog.at_level(logging.WARNING, logger="foldforge.backend"):
-        plan.resolve()
-    assert plan.of("transition") == "hip"
-    assert plan.resolved["single_attention"].reason is not None
-    assert plan.report()["fallbacks"].keys() == {"single_attention"}
+        picks = plan.resolve("gfx950")
+    assert picks["transition"] == ("hip", None)
+    assert picks["single_attention"].reason is not None
+    summary = plan.summary(picks)
+    assert summary["fallbacks"].keys() == {"single_attention"}
+    assert summary["ops"]["trimul"] == "pytorch"
     assert sum("single_attention" in r.message for r in caplog.records) == 1
-    strict = backends.BackendPlan.make("pytorch", {"single_attention": "cuda"}, "error")
-    with pytest.raises(backends.BackendUnsupportedError):
-        strict.resolve()
+    strict = dispatch.Plan.of("pytorch", {"single_attention": "cuda"}, "error")
+    with pytest.raises(dispatch.BackendUnsupportedError):
+        strict.resolve("gfx950")
 
 
 class _Model(nn.Module):
@@ -106,45 +110,95 @@ def _x(batch: int = 1) -> torch.Tensor:
     return torch.randn(batch, 4, 16)
 
 
-def test_apply_plan_sets_the_backend_per_module_and_guards(monkeypatch):
+def test_install_sets_the_backend_per_module(monkeypatch):
     fake_gfx950(monkeypatch)
     model = _Model()
-    choices = policy.apply_plan(model, backends.BackendPlan.make("miniworld", {"trimul": "pytorch"}))
+    placed = dispatch.install(model, dispatch.Plan.of("miniworld", {"trimul": "pytorch"}))
     assert model.transition.backend == "hip"
     assert model.norm.backend == "hip"
     assert model.trimul.backend == "pytorch"
-    assert choices["transition"]["backend"] == "hip"
-    assert choices["trimul"]["op"] == "trimul"
+    assert model.trimul.ln_pair.backend == "pytorch"  # an op's own sub-modules are its business
+    assert placed["transition"]["backend"] == "hip"
+    assert placed["trimul"]["op"] == "trimul"
+    assert set(placed) == {"transition", "trimul", "norm"}
 
 
-def test_unsupported_call_falls_back_once_and_logs_once(monkeypatch, caplog):
+def test_without_a_policy_a_refused_call_raises_in_forward_and_delta(monkeypatch):
+    """The engine's own contract: a module outside its backend's range never falls back."""
+    fake_gfx950(monkeypatch)
+    m = factories.transition(16, 2, precision="fp32")
+    m.set_backend("hip")
+    assert m.unsupported(_x()) is not None  # a CPU tensor is outside the hip backend
+    with pytest.raises(BackendUnsupported):
+        m(_x())
+    with pytest.raises(BackendUnsupported):
+        m.delta(_x())
+    assert dispatch.ledger_of(m).served == {}
+
+
+def test_parity_helpers_fail_when_hip_refuses(monkeypatch):
+    """The GPU parity tests call through these helpers; a refusal must fail them."""
+    m = factories.transition(16, 2, precision="fp32")
+    m.set_backend("hip")
+    monkeypatch.setattr(type(m), "_unsupported_hip", lambda self, x: "planted refusal")
+    with pytest.raises(AssertionError, match="planted refusal"):
+        hip_delta(m, _x())
+    with pytest.raises(AssertionError, match="planted refusal"):
+        hip_forward(m, _x())
+    m.refusal_policy = "fallback"  # even a module that would fall back fails the helper
+    with pytest.raises(AssertionError, match="refused"):
+        hip_delta(m, _x())
+    m.set_backend("pytorch")
+    with pytest.raises(AssertionError, match="not hip"):
+        hip_delta(m, _x())
+
+
+def test_parity_helpers_count_a_served_call(monkeypatch):
+    m = factories.transition(16, 2, precision="fp32")
+    m.set_backend("hip")
+    monkeypatch.setattr(type(m), "_unsupported_hip", lambda self, x: None)
+    monkeypatch.setattr(type(m), "_forward_hip", lambda self, x, residual=True: x * 0 + 7)
+    assert torch.equal(hip_delta(m, _x()), torch.full((1, 4, 16), 7.0))
+    assert dispatch.ledger_of(m).served["hip"] == 1
+    monkeypatch.setattr(type(m), "_route", lambda self, a, k: "hip")  # a route that forgets to count
+    with pytest.raises(AssertionError, match="did not serve"):
+        hip_delta(m, _x())
+
+
+def test_fallback_policy_runs_pytorch_once_logged(monkeypatch, caplog):
     fake_gfx950(monkeypatch)
     model = _Model()
     expected = Transition.forward(model.transition, _x())  # pytorch backend
-    policy.apply_plan(model, backends.BackendPlan.make("hip"))
+    dispatch.install(model, dispatch.Plan.of("hip"))
+    dispatch.clear_ledgers(model)
     assert model.transition.backend == "hip"
-    # a CPU tensor is outside the hip backend's range: the op raises, the guard falls back
-    assert model.transition.unsupported(_x()) is not None
-    with pytest.raises(BackendUnsupported):
-        Transition.forward(model.transition, _x())
     with caplog.at_level(logging.WARNING, logger="foldforge.backend"):
         first = model.transition(_x())
         second = model.transition(_x())
+        third = model.transition.delta(_x())
     torch.testing.assert_close(first, expected)
     torch.testing.assert_close(second, expected)
-    assert model.transition.backend == "hip"  # restored after the call
-    assert sum("refuses a call" in r.message for r in caplog.records) == 1
-    stats = serving.report_observations(model)["modules"]["transition"]
-    assert stats["served_host_calls"] == {"pytorch": 2}
-    assert len(stats["refused_host_calls"]) == 1
+    torch.testing.assert_close(_x() + third, expected)
+    assert model.transition.backend == "hip"  # the module keeps its backend
+    assert sum("refused a call" in r.message for r in caplog.records) == 1
+    entry = dispatch.ledger_report(model)["transition"]
+    assert entry["served"] == {"pytorch": 3}
+    assert sum(entry["refused"].values()) == 3 and len(entry["refused"]) == 1
+    assert dispatch.served_count(model, "hip") == 0
+    dispatch.clear_ledgers(model)
+    assert dispatch.ledger_report(model)["transition"]["served"] == {}
 
 
-def test_unsupported_error_policy_raises(monkeypatch):
+def test_error_policy_raises(monkeypatch):
     fake_gfx950(monkeypatch)
     model = _Model()
-    policy.apply_plan(model, backends.BackendPlan.make("hip", unsupported="error"))
-    with pytest.raises(backends.BackendUnsupportedError, match=r"engine.unsupported: error"):
+    dispatch.install(model, dispatch.Plan.of("hip", unsupported="error"))
+    with pytest.raises(dispatch.BackendUnsupportedError, match=r"engine.unsupported: error"):
         model.transition(_x())
+    with pytest.raises(dispatch.BackendUnsupportedError):
+        model.transition.delta(_x())
+    with pytest.raises(dispatch.BackendUnsupportedError, match="no 'cuda' backend"):
+        dispatch.install(_Model(), dispatch.Plan.of("cuda", unsupported="error"))
 
 
 def test_composite_children_are_set_one_by_one(monkeypatch):
@@ -152,7 +206,7 @@ def test_composite_children_are_set_one_by_one(monkeypatch):
     block = factories.pairformer_block(d_pair=32, triangle_model="af3", d_single=64,
                                        n_head_single=4, precision="fp32")
     holder = nn.ModuleList([block])
-    policy.apply_plan(holder, backends.BackendPlan.make("miniworld"))
+    dispatch.install(holder, dispatch.Plan.of("miniworld"))
     assert block.backend == "pytorch"
     assert block.tri_multi_outgoing.backend == "hip"
     assert block.tri_atten_ending.backend == "hip"
@@ -273,7 +327,7 @@ def test_msa_pair_weighted_averaging_class_contract_and_pytorch_backend():
     assert {"ln_msa.weight", "ln_msa.bias", "ln_pair.weight", "to_bias.weight", "to_value.weight",
             "to_gate.weight", "to_out.weight"} == keys  # no pair-norm offset
     assert m.to_value.weight.shape == (64, 64) and m.d_hidden == 8
-    assert backends.op_of(m) == "msa_pwa"
+    assert dispatch.op_name(m) == "msa_pwa"
     torch.manual_seed(7)
     msa = torch.randn(1, 3, 7, 64)
     z = torch.randn(1, 7, 7, 32)
@@ -304,7 +358,7 @@ def test_outer_product_mean_class_contract_and_pytorch_backend(form):
     assert keys == want_keys
     k = hidden // groups
     assert m.to_out.weight.shape == (24, groups * k * k)
-    assert backends.op_of(m) == "opm"
+    assert dispatch.op_name(m) == "opm"
     torch.manual_seed(9)
     msa = torch.randn(2, 5, 7, 16)
     rows = torch.rand(2, 5, 7) > 0.3
@@ -339,7 +393,7 @@ def test_pytorch_backend_block_and_run_block_match_oracle():
     tokens = torch.ones(n)
     tokens[-2:] = 0
     pair_mask = tokens[:, None] * tokens[None, :]
-    got_pair, got_single = graph.run_block(block, pair, pair_mask, single.clone(), tokens)
+    got_pair, got_single = adapter.run_block(block, pair, pair_mask, single.clone(), tokens)
     mask = (tokens > 0)[None]
     want_pair, want_single = ps.pairformer_block(pair[None], mask, block.state_dict(), n_head_pair=4,
                                                  s=single[None], n_head_single=4, dtype=torch.float64)
@@ -364,3 +418,22 @@ def test_trunk_runs_passes_on_cpu():
     pair, single = trunk(z, mask, s, passes=2, on_block=lambda p, i, *_: seen.append((p, i)))
     assert seen == [(0, 0), (0, 1), (1, 0), (1, 1)]
     assert torch.isfinite(pair).all() and torch.isfinite(single).all()
+
+
+def test_parallel_block_matches_the_oracle_schedule():
+    """``parallel=True`` (Chai-1 / RF3): every pair update and both single updates read the
+    block's input (``legacy/pairformer.py:176-190,208-226``)."""
+    block = randomise(factories.pairformer_block(d_pair=32, triangle_model="af3", d_single=48,
+                                                 n_head_single=4, parallel=True, precision="fp32"), 11)
+    torch.manual_seed(12)
+    z = torch.randn(2, 7, 7, 32)
+    s = torch.randn(2, 7, 48)
+    mask = torch.ones(2, 7, dtype=torch.bool)
+    mask[1, -2:] = False
+    got_z, got_s = block(z, mask, s)
+    want_z, want_s = ps.pairformer_block(z, mask, block.state_dict(), n_head_pair=4, s=s, n_head_single=4,
+                                         dtype=torch.float64, parallel=True)
+    torch.testing.assert_close(_valid(got_z.double(), mask), _valid(want_z, mask), atol=1e-4, rtol=1e-4)
+    torch.testing.assert_close(got_s.double()[mask], want_s[mask], atol=1e-4, rtol=1e-4)
+    seq_z = ps.pairformer_block(z, mask, block.state_dict(), n_head_pair=4, dtype=torch.float64)
+    assert (_valid(seq_z, mask) - _valid(want_z, mask)).abs().max() > 1e-2  # the schedules differ

@@ -1,7 +1,7 @@
 """GPU: a whole Pairformer block and a short trunk through the drop-in boundary.
 
 ``foldforge_amd.load(..., backend="miniworld")`` on a gfx950 must serve every op (pair and
-single track) with the native ``hip`` backend (checked through the guard's host-call counters), and the
+single track) with the native ``hip`` backend (checked through the modules' call ledgers), and the
 result must match the fp64 oracle: the block's update within rel-RMS 3e-2 on the valid
 pairs, the trunk's final pair and single within 5e-2. At the full N = 512 the
 size-independent properties are checked: finiteness, run-to-run bitwise determinism,
@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import foldforge_amd
-from foldforge_amd import factories, serving
+from foldforge_amd import dispatch, factories
 from foldforge_amd.trunk import randomise
 from oracle import pairstack as ps
 
@@ -64,10 +64,10 @@ def test_load_serves_every_op_with_hip_and_matches_oracle():
     mask[0, 90:] = False
     with torch.no_grad():
         pair, single = model(z.cuda(), mask.cuda(), s.cuda(), passes=1)
-    served = serving.report_observations(model)["modules"]
-    hip_calls = sum(v["served_host_calls"].get("hip", 0) for v in served.values())
+    served = dispatch.ledger_report(model)
+    hip_calls = dispatch.served_count(model, "hip")
     assert hip_calls == 2 * 7, served  # 5 pair + 2 single-track ops per block served natively
-    assert all(not v["refused_host_calls"] for v in served.values())
+    assert all(not v["refused"] for v in served.values())
     state = model.state_dict()
     wz, ws = z, s
     for i in range(2):

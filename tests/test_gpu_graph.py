@@ -1,8 +1,10 @@
-"""GPU: a captured trunk pass replays exactly what the eager pass computes.
+"""GPU: a captured trunk pass replays exactly what the eager pass computes, and that is the
+oracle's result.
 
 The graph is replayed several times with different inputs copied in, with eager work and
 host synchronisations between the replays; every replay must equal the eager run on the same
-inputs bitwise (the kernels are deterministic and take no state from earlier calls).
+inputs bitwise (the kernels are deterministic and take no state from earlier calls), and one
+replay is compared with the fp64 oracle run through the same blocks and passes.
 """
 
 from __future__ import annotations
@@ -12,6 +14,7 @@ import torch
 
 import foldforge_amd
 from foldforge_amd.execution import capture_trunk
+from oracle import pairstack as ps
 
 pytestmark = pytest.mark.gpu
 
@@ -51,6 +54,28 @@ def test_captured_trunk_pass_replays_the_eager_pass():
         assert torch.equal(got_s, want_s), f"single differs (seed {seed})"
         # eager work between replays, as a program around the graph would do
         _ = (want_z.float() * 2).sum().item()
+        if seed == 3:
+            _against_the_oracle(model, (z, mask, s), (got_z, got_s), passes=2)
+
+
+def _against_the_oracle(model, inputs, outputs, *, passes: int):
+    """The replay's change of pair and single over ``passes`` passes against the fp64 oracle's
+    (valid pairs / tokens): within the trunk bar for a few block evaluations, 5e-2."""
+    z, mask, s = (t.cpu() for t in inputs)
+    state = {k: v.cpu() for k, v in model.state_dict().items()}
+    blocks = len(model.blocks)
+    subs = [{k[len(f"blocks.{i}."):]: v for k, v in state.items() if k.startswith(f"blocks.{i}.")}
+            for i in range(blocks)]
+    fz, fs = z.double(), s.double()
+    for _ in range(passes):
+        for sub in subs:
+            fz, fs = ps.pairformer_block(fz, mask, sub, n_head_pair=4, s=fs, n_head_single=16, dtype=torch.float64)
+    pairs = mask[:, :, None] & mask[:, None, :]
+    got_z, got_s = (t.cpu().double() for t in outputs)
+    rz = ps.rel_rms(got_z - z.double(), fz - z.double(), pairs)
+    rs = ps.rel_rms(got_s - s.double(), fs - s.double(), mask)
+    print(f"replay vs fp64 oracle: pair change rel_rms={rz:.3e} single change rel_rms={rs:.3e}", flush=True)
+    assert rz <= 5e-2 and rs <= 5e-2
 
 
 def test_captured_pair_only_trunk():

@@ -14,6 +14,7 @@ import torch
 from foldforge_amd import factories
 from foldforge_amd.trunk import randomise
 from oracle import pairstack as ps
+from tests.hip_calls import hip_delta, hip_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -62,11 +63,11 @@ def test_msa_pair_weighted_averaging_matches_oracle(cm, heads, dh, depth, n, len
     msa, z, mask = _inputs(depth, n, cm, lengths, seed=n + cm + heads)
     mod = _pwa(cm, heads, dh, seed=cm + heads)
     assert mod.unsupported(msa.cuda(), z.cuda(), mask.cuda()) is None
-    got = mod.delta(msa.cuda(), z.cuda(), mask.cuda()).cpu()
+    got = hip_delta(mod, msa.cuda(), z.cuda(), mask.cuda()).cpu()
     want = ps.msa_pair_weighted_averaging(msa, z, mask, mod.state_dict(), n_head=heads,
                                           dtype=torch.float64) - msa.double()
     _check(got, want, f"msa_pwa c_m={cm} heads={heads}x{mod.d_hidden} S={depth} n={n} lengths={lengths}")
-    full = mod(msa.cuda(), z.cuda(), mask.cuda()).cpu()
+    full = hip_forward(mod, msa.cuda(), z.cuda(), mask.cuda()).cpu()
     _check(full, want + msa.double(), "msa_pwa residual")
 
 
@@ -74,12 +75,12 @@ def test_msa_pair_weighted_averaging_masking_is_exact_and_empty_rows_are_zero():
     depth, n, length = 4, 96, 61
     msa, z, mask = _inputs(depth, n, 64, [length, 0], seed=11)
     mod = _pwa(64, 8, None, seed=12)
-    a = mod.delta(msa.cuda(), z.cuda(), mask.cuda()).cpu()
+    a = hip_delta(mod, msa.cuda(), z.cuda(), mask.cuda()).cpu()
     msa2, z2 = msa.clone(), z.clone()
     msa2[0, :, length:] = 5.0
     z2[0, length:] = -4.0
     z2[0, :, length:] = 9.0
-    b = mod.delta(msa2.cuda(), z2.cuda(), mask.cuda()).cpu()
+    b = hip_delta(mod, msa2.cuda(), z2.cuda(), mask.cuda()).cpu()
     assert torch.equal(a[0, :, :length], b[0, :, :length])
     assert torch.equal(a[1], torch.zeros_like(a[1]))  # no valid key: zero update
 

@@ -12,10 +12,10 @@ from __future__ import annotations
 import pytest
 import torch
 
-from foldforge_amd import factories
-from foldforge_amd.policy import guard
+from foldforge_amd import dispatch, factories
 from foldforge_amd.trunk import randomise
 from oracle import pairstack as ps
+from tests.hip_calls import hip_delta, hip_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -62,7 +62,7 @@ def test_trimul_generic_widths_match_oracle(outgoing, c, h, n, lengths):
     m = randomise(factories.triangle_multiplication(c, outgoing=outgoing, d_hidden=h), seed=c + h).cuda()
     m.set_backend("hip")
     assert m.unsupported(z.cuda(), mask.cuda()) is None
-    got = m.delta(z.cuda(), mask.cuda()).cpu()
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
     want = ps.triangle_multiplication(z, mask, m.state_dict(), outgoing=outgoing, dtype=torch.float64) - z.double()
     _check(got, want, _pairs(mask), f"trimul c={c} h={h} outgoing={outgoing} n={n}")
     full = m(z.cuda(), mask.cuda()).cpu()
@@ -75,7 +75,7 @@ def test_trimul_generic_width_256_tile_contraction():
     z, mask = _pair(n, c, [230, 177], seed=21)
     m = randomise(factories.triangle_multiplication(c, outgoing=False, d_hidden=h), seed=22).cuda()
     m.set_backend("hip")
-    got = m.delta(z.cuda(), mask.cuda()).cpu()
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
     want = ps.triangle_multiplication(z, mask, m.state_dict(), outgoing=False, dtype=torch.float64) - z.double()
     _check(got, want, _pairs(mask), "trimul c=64 h=64 incoming n=230")
 
@@ -90,7 +90,7 @@ def test_triattn_generic_widths_match_oracle(starting, model, c, heads, d, n, le
                                                d_hidden=heads * d), seed=c + d).cuda()
     m.set_backend("hip")
     assert m.unsupported(z.cuda(), mask.cuda()) is None
-    got = m.delta(z.cuda(), mask.cuda()).cpu()
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
     want = ps.triangle_attention(z, mask, m.state_dict(), starting=starting, n_head=heads,
                                  transposed_bias=m.transposed_bias, dtype=torch.float64) - z.double()
     _check(got, want, _pairs(mask), f"triattn c={c} {heads}x{d} {model} starting={starting} n={n}")
@@ -105,11 +105,11 @@ def test_generic_path_masking_is_exact(op):
     else:
         m = randomise(factories.triangle_attention(c, 4, starting=False, model="af3", d_hidden=64), seed=4).cuda()
     m.set_backend("hip")
-    a = m.delta(z.cuda(), mask.cuda()).cpu()
+    a = hip_delta(m, z.cuda(), mask.cuda()).cpu()
     z2 = z.clone()
     z2[0, length:] = 3.0
     z2[0, :, length:] = -5.0
-    b = m.delta(z2.cuda(), mask.cuda()).cpu()
+    b = hip_delta(m, z2.cuda(), mask.cuda()).cpu()
     assert torch.equal(a[0, :length, :length], b[0, :length, :length])
 
 
@@ -122,8 +122,7 @@ def test_template_stack_block_runs_on_the_kernels():
     block = randomise(factories.pairformer_block(d_pair=c, triangle_model="af3", d_hidden_tri_attention=16,
                                                  pair_transition_n=2), seed=9).cuda()
     block.set_backend("hip")
-    for m in block.children_ops():
-        guard(m, "error")
+    dispatch.set_refusal(block, "error")
     with torch.no_grad():
         got = block(z.cuda(), mask.cuda()).cpu()
     want = ps.pairformer_block(z, mask, block.state_dict(), n_head_pair=4, dtype=torch.float64)

@@ -15,6 +15,7 @@ import torch
 from foldforge_amd import factories
 from foldforge_amd.trunk import randomise
 from oracle import pairstack as ps
+from tests.hip_calls import hip_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -69,13 +70,12 @@ def test_outer_product_mean_matches_oracle(form, batch, depth, n, cm):
     m, rows = _inputs(batch, depth, n, cm, seed=depth + n + cm)
     mod = _opm(cm, seed=n, **FORMS[form])
     mc, rc = m.cuda(), rows.cuda()
-    assert mod.unsupported(mc, rc) is None
-    got = mod(mc, rc).cpu()
+    got = hip_forward(mod, mc, rc).cpu()
     oracle_form = {k: v for k, v in FORMS[form].items() if k != "projection_bias"}
     want = ps.outer_product_mean(m, rows, mod.state_dict(), dtype=torch.float64, **oracle_form)
     _check(got, want, f"opm {form} B={batch} S={depth} n={n} c_m={cm}")
     pair = torch.randn(batch, n, n, 128, generator=torch.Generator().manual_seed(3)).bfloat16()
-    full = mod(mc, rc, residual=pair.cuda()).cpu()
+    full = hip_forward(mod, mc, rc, residual=pair.cuda()).cpu()
     _check(full, want + pair.double(), f"opm {form} residual")
 
 
@@ -84,7 +84,7 @@ def test_outer_product_mean_masked_entries_do_not_leak_and_empty_tokens_use_the_
     m, rows = _inputs(batch, depth, n, cm, seed=5, keep=0.6)
     rows[0, :, 13] = False  # a token without any MSA entry: count 0, divisor max(0, 1)
     mod = _opm(cm, seed=6, count_offset=None, normalize_before_proj=False)
-    a = mod(m.cuda(), rows.cuda()).cpu()
+    a = hip_forward(mod, m.cuda(), rows.cuda()).cpu()
     m2 = m.clone()
     m2[~rows] = 7.0
     b = mod(m2.cuda(), rows.cuda()).cpu()

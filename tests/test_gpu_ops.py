@@ -16,6 +16,7 @@ import torch
 from foldforge_amd import factories, kernels
 from foldforge_amd.trunk import randomise
 from oracle import pairstack as ps
+from tests.hip_calls import hip_delta, hip_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -89,10 +90,10 @@ def test_trimul_matches_oracle(outgoing, n, lengths):
     z, mask = _pair(n, batch, seed=n, lengths=lengths)
     m = randomise(factories.triangle_multiplication(128, outgoing=outgoing), seed=n).cuda()
     m.set_backend("hip")
-    got = m.delta(z.cuda(), mask.cuda()).cpu()
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
     want = ps.triangle_multiplication(z, mask, m.state_dict(), outgoing=outgoing, dtype=torch.float64) - z.double()
     _check(got, want, _pairs(mask), f"trimul outgoing={outgoing} n={n}")
-    full = m(z.cuda(), mask.cuda()).cpu()
+    full = hip_forward(m, z.cuda(), mask.cuda()).cpu()
     torch.testing.assert_close(full.float(), (z.float() + got.float()), atol=3e-2, rtol=1e-2)
 
 
@@ -104,7 +105,7 @@ def test_triattn_matches_oracle(starting, model, n, lengths):
     z, mask = _pair(n, batch, seed=7 * n, lengths=lengths)
     m = randomise(factories.triangle_attention(128, 4, starting=starting, model=model), seed=n).cuda()
     m.set_backend("hip")
-    got = m.delta(z.cuda(), mask.cuda()).cpu()
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
     want = ps.triangle_attention(z, mask, m.state_dict(), starting=starting, n_head=4,
                                  transposed_bias=m.transposed_bias, dtype=torch.float64) - z.double()
     _check(got, want, _pairs(mask), f"triattn starting={starting} {model} n={n}")
@@ -114,7 +115,7 @@ def test_transition_matches_oracle():
     z, _ = _pair(72, 2, seed=3)
     m = randomise(factories.transition(128, 4), seed=5).cuda()
     m.set_backend("hip")
-    got = m.delta(z.cuda()).cpu()
+    got = hip_delta(m, z.cuda()).cpu()
     want = ps.transition(z, m.state_dict(), dtype=torch.float64) - z.double()
     _check(got, want, None, "transition")
 
@@ -189,6 +190,6 @@ def test_no_valid_key_gives_identity_update():
     z, mask = _pair(64, 1, seed=31, lengths=[0])
     m = randomise(factories.triangle_attention(128, 4, starting=True, model="af3"), seed=1).cuda()
     m.set_backend("hip")
-    got = m(z.cuda(), mask.cuda()).cpu()
+    got = hip_forward(m, z.cuda(), mask.cuda()).cpu()
     assert torch.isfinite(got.float()).all()
     assert torch.equal(got, z)  # zero attention output -> zero update

@@ -16,6 +16,7 @@ import torch
 from foldforge_amd import factories, modules
 from foldforge_amd.trunk import randomise
 from oracle import pairstack as ps
+from tests.hip_calls import hip_delta, hip_forward
 
 pytestmark = pytest.mark.gpu
 
@@ -66,7 +67,7 @@ def test_attention_pair_bias_matches_oracle(cs, heads, n, lengths):
     s, z, mask = _inputs(n, cs, lengths, seed=n + cs)
     m = _apb(cs, heads, gate_bias=0.5, seed=cs + heads)
     assert m.unsupported(s.cuda(), z.cuda(), mask.cuda()) is None
-    got = m.delta(s.cuda(), z.cuda(), mask.cuda()).cpu()
+    got = hip_delta(m, s.cuda(), z.cuda(), mask.cuda()).cpu()
     want = ps.attention_pair_bias(s, z, mask, m.state_dict(), n_head=heads, gate_bias=0.5,
                                   dtype=torch.float64) - s.double()
     _check(got, want, f"attention_pair_bias cs={cs} heads={heads} n={n} lengths={lengths}")
@@ -78,12 +79,12 @@ def test_attention_pair_bias_masking_is_exact_and_empty_rows_are_zero():
     n, length = 96, 61
     s, z, mask = _inputs(n, 384, [length, 0], seed=11)
     m = _apb(384, 16, gate_bias=0.0, seed=12)
-    a = m.delta(s.cuda(), z.cuda(), mask.cuda()).cpu()
+    a = hip_delta(m, s.cuda(), z.cuda(), mask.cuda()).cpu()
     s2, z2 = s.clone(), z.clone()
     s2[0, length:] = 5.0
     z2[0, length:] = -4.0
     z2[0, :, length:] = 9.0
-    b = m.delta(s2.cuda(), z2.cuda(), mask.cuda()).cpu()
+    b = hip_delta(m, s2.cuda(), z2.cuda(), mask.cuda()).cpu()
     assert torch.equal(a[0, :length], b[0, :length])
     assert torch.equal(a[1], torch.zeros_like(a[1]))  # no valid key: zero update
     out = m(s.cuda(), z.cuda(), mask.cuda()).cpu()
@@ -96,7 +97,7 @@ def test_attention_pair_bias_large_logits_stay_finite():
     m = _apb(384, 16, gate_bias=0.0, seed=22)
     with torch.no_grad():
         m.to_bias.weight.mul_(40.0)  # pair logits of several hundred nats
-    got = m.delta(s.cuda(), z.cuda(), mask.cuda()).cpu()
+    got = hip_delta(m, s.cuda(), z.cuda(), mask.cuda()).cpu()
     assert torch.isfinite(got.float()).all()
     want = ps.attention_pair_bias(s, z, mask, m.state_dict(), n_head=16, dtype=torch.float64) - s.double()
     _check(got, want, "attention_pair_bias large logits")
@@ -109,7 +110,7 @@ def test_wide_transition_matches_oracle(d, factor, shape):
     m = randomise(factories.transition(d, factor), seed=d).cuda()
     m.set_backend("hip")
     assert m.unsupported(x.cuda()) is None
-    got = m.delta(x.cuda()).cpu()
+    got = hip_delta(m, x.cuda()).cpu()
     want = ps.transition(x, m.state_dict(), dtype=torch.float64) - x.double()
     _check(got, want, f"transition d={d} x{factor} rows={shape}")
     full = m(x.cuda()).cpu()

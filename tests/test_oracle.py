@@ -408,6 +408,52 @@ def test_block_is_the_composition_of_the_pinned_ops():
     np.testing.assert_allclose(got.numpy(), x, rtol=1e-10, atol=1e-10)
 
 
+def test_parallel_block_is_the_sum_of_updates_on_the_block_input():
+    """The parallel schedule (``legacy/pairformer.py:176-190``, single ``:208-226``): every
+    update is computed by the brute-force loops from the block's input and added once. The
+    schedule that feeds the triangle attentions the already-updated pair must differ."""
+    n, c, h, heads, d, cs, hs = 5, 6, 4, 2, 3, 8, 2
+    params = {}
+    for prefix, shapes, seed in (
+        ("tri_multi_outgoing", _tm_shapes(c, h), 21), ("tri_multi_incoming", _tm_shapes(c, h), 22),
+        ("tri_atten_starting", _ta_shapes(c, heads, d), 23), ("tri_atten_ending", _ta_shapes(c, heads, d), 24),
+    ):
+        params.update({f"{prefix}.{k}": v for k, v in _rand_params(shapes, seed).items()})
+    tr = lambda w: {"ln_in.weight": (w,), "ln_in.bias": (w,), "expand_a.weight": (4 * w, w),  # noqa: E731
+                    "expand_b.weight": (4 * w, w), "squeeze.weight": (w, 4 * w)}
+    params.update({f"transition_pair.{k}": v for k, v in _rand_params(tr(c), 25).items()})
+    params.update({f"single_transition.{k}": v for k, v in _rand_params(tr(cs), 26).items()})
+    apb = {"ln_single.weight": (cs,), "ln_single.bias": (cs,), "to_query.weight": (cs, cs),
+           "to_query.bias": (cs,), "to_key.weight": (cs, cs), "to_value.weight": (cs, cs),
+           "ln_pair.weight": (c,), "to_bias.weight": (hs, c), "to_gate.weight": (cs, cs),
+           "to_out.weight": (cs, cs)}
+    params.update({f"single_attention.{k}": v for k, v in _rand_params(apb, 27).items()})
+    g = torch.Generator().manual_seed(28)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    s = torch.randn(1, n, cs, generator=g, dtype=F64)
+    mask = torch.ones(1, n, dtype=torch.bool)
+    mask[0, -1] = False
+    got_z, got_s = ps.pairformer_block(z, mask, params, n_head_pair=heads, s=s, n_head_single=hs,
+                                       dtype=F64, parallel=True)
+    x, m = z.numpy(), mask.numpy()
+    sub = lambda pre: {k[len(pre) + 1:]: v.numpy() for k, v in params.items() if k.startswith(pre + ".")}  # noqa: E731
+    tm = (brute.triangle_multiplication(x, m, sub("tri_multi_outgoing"), outgoing=True) - x
+          + brute.triangle_multiplication(x, m, sub("tri_multi_incoming"), outgoing=False) - x)
+    ta = lambda y: (brute.triangle_attention(y, m, sub("tri_atten_starting"), starting=True, n_head=heads) - y  # noqa: E731
+                    + brute.triangle_attention(y, m, sub("tri_atten_ending"), starting=False, n_head=heads) - y)
+    tr_pair = brute.transition(x, sub("transition_pair")) - x
+    want_z = x + tm + ta(x) + tr_pair
+    np.testing.assert_allclose(got_z.numpy(), want_z, rtol=1e-10, atol=1e-10)
+    sv = s.numpy()
+    want_s = (sv + (brute.attention_pair_bias(sv, x, m, sub("single_attention"), n_head=hs) - sv)
+              + (brute.transition(sv, sub("single_transition")) - sv))
+    np.testing.assert_allclose(got_s.numpy(), want_s, rtol=1e-10, atol=1e-10)
+    # the mistake of feeding the attentions the pair after the other updates is visible
+    z1 = x + tm + tr_pair
+    wrong = z1 + ta(z1)
+    assert np.abs(wrong - want_z)[0][np.outer(m[0], m[0])].max() > 1e-3
+
+
 def test_a_planted_mistake_is_caught(monkeypatch):
     """A transposed operand planted in the oracle's contraction breaks the brute-force check."""
     n, c, h = 5, 4, 3

@@ -51,6 +51,15 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 7
         + [c_void_p, c_size_t, c_int64, c_int32, c_int32, c_int32, c_float, c_void_p],
     ),
+    "ffk_layer_norm_linear": (
+        c_int32,
+        [c_void_p] * 6 + [c_int64, c_int32, c_int32, c_int32, c_int32, c_float, c_void_p],
+    ),
+    "ffk_swiglu_ffn_workspace": (c_size_t, [c_int64, c_int32]),
+    "ffk_swiglu_ffn": (
+        c_int32,
+        [c_void_p] * 7 + [c_size_t, c_int64, c_int32, c_int32, c_void_p],
+    ),
     "ffk_msa_pair_weighted_averaging_workspace": (
         c_size_t,
         [c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32],

@@ -310,6 +310,68 @@ ApbWs apb_ws(void* ws, int64_t batch, int64_t n, int cs, int heads) {
   return w;
 }
 
+// Argument checks shared by the transition entry points (not the workspace).
+int32_t transition_check(const void* x, const float* ln_w, const float* ln_b, const float* wa,
+                         const float* wb, const float* wsq, const void* out, int64_t rows, int d,
+                         int factor) {
+  const bool fused = transition_fused(d, factor);
+  if (!fused && (d <= 0 || factor <= 0 || d % 64 != 0 || d > kLnGemmMaxK || ((int64_t)factor * d) % 64 != 0))
+    return fail(FFK_ERR_INVALID, "transition: d=%d factor=%d (kernels take 128 x 4, or d <= %d and factor * d multiples of 64)", d, factor, kLnGemmMaxK);
+  if (rows < 0) return fail(FFK_ERR_INVALID, "transition: negative rows");
+  if (!fused && (rows + 31) / 32 > 0x7fffffffLL)
+    return fail(FFK_ERR_INVALID, "transition: %lld rows exceed the launch grid", (long long)rows);
+  if (!x || !ln_w || !ln_b || !wa || !wb || !wsq || !out)
+    return fail(FFK_ERR_INVALID, "transition: null argument");
+  if (!aligned16(x) || !aligned16(out))
+    return fail(FFK_ERR_INVALID, "transition: x/out must be 16-byte aligned");
+  if (!fused && (!aligned16(wa) || !aligned16(wb) || !aligned16(wsq)))
+    return fail(FFK_ERR_INVALID, "transition: weights must be 16-byte aligned");
+  return FFK_OK;
+}
+
+// The launches of one transition call on a carved workspace.
+int32_t transition_run(const TransitionWs& w, const void* x, const float* ln_w, const float* ln_b,
+                       const float* wa, const float* wb, const float* wsq, void* out, int64_t rows,
+                       int d, int factor, int residual, float eps, hipStream_t st) {
+  if (!transition_fused(d, factor)) {
+    RowGemmArgs g{};
+    g.ln_x = static_cast<const bf16*>(x);
+    g.ln_w = ln_w;
+    g.ln_b = ln_b;
+    g.eps = eps;
+    g.w0 = wa;
+    g.w1 = wb;
+    g.M = rows;
+    g.K = d;
+    g.O = 2 * factor * d;
+    g.h32 = w.h;
+    launch_row_gemm(g, kEpiSwiglu, kXLn, st);
+    RowGemmArgs s{};
+    s.x32 = w.h;
+    s.w0 = wsq;
+    s.M = rows;
+    s.K = factor * d;
+    s.O = d;
+    s.res = static_cast<const bf16*>(x);
+    s.out = static_cast<bf16*>(out);
+    s.residual = residual ? 1 : 0;
+    launch_row_gemm(s, kEpiResid, kXF32, st);
+    return check_launch("transition");
+  }
+  launch_transition_pack(wa, wb, wsq, w.w, st);
+  TransitionArgs a;
+  a.x = static_cast<const bf16*>(x);
+  a.ln_w = ln_w;
+  a.ln_b = ln_b;
+  a.w = w.w;
+  a.out = static_cast<bf16*>(out);
+  a.rows = rows;
+  a.residual = residual ? 1 : 0;
+  a.eps = eps;
+  launch_transition(a, st);
+  return check_launch("transition");
+}
+
 }  // namespace ffk
 
 using namespace ffk;
@@ -668,61 +730,94 @@ int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
                        size_t workspace_bytes, int64_t rows, int32_t d, int32_t factor,
                        int32_t residual, float eps, void* stream) {
   if (int32_t s = check_device()) return s;
-  const bool fused = transition_fused(d, factor);
-  if (!fused && (d <= 0 || factor <= 0 || d % 64 != 0 || d > kLnGemmMaxK || ((int64_t)factor * d) % 64 != 0))
-    return fail(FFK_ERR_INVALID, "transition: d=%d factor=%d (kernels take 128 x 4, or d <= %d and factor * d multiples of 64)", d, factor, kLnGemmMaxK);
-  if (rows < 0) return fail(FFK_ERR_INVALID, "transition: negative rows");
-  if (!fused && (rows + 31) / 32 > 0x7fffffffLL)
-    return fail(FFK_ERR_INVALID, "transition: %lld rows exceed the launch grid", (long long)rows);
-  if (!x || !ln_w || !ln_b || !w_expand_a || !w_expand_b || !w_squeeze || !out)
-    return fail(FFK_ERR_INVALID, "transition: null argument");
-  if (!aligned16(x) || !aligned16(out))
-    return fail(FFK_ERR_INVALID, "transition: x/out must be 16-byte aligned");
-  if (!fused && (!aligned16(w_expand_a) || !aligned16(w_expand_b) || !aligned16(w_squeeze)))
-    return fail(FFK_ERR_INVALID, "transition: weights must be 16-byte aligned");
+  if (int32_t s = transition_check(x, ln_w, ln_b, w_expand_a, w_expand_b, w_squeeze, out, rows, d, factor))
+    return s;
   const TransitionWs need = transition_ws(nullptr, rows, d, factor);
   if (!workspace || workspace_bytes < need.bytes || !aligned16(workspace))
     return fail(FFK_ERR_WORKSPACE, "transition: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
   if (rows == 0) return ok();
-  const TransitionWs w = transition_ws(workspace, rows, d, factor);
+  return transition_run(transition_ws(workspace, rows, d, factor), x, ln_w, ln_b, w_expand_a, w_expand_b,
+                        w_squeeze, out, rows, d, factor, residual, eps, static_cast<hipStream_t>(stream));
+}
+
+int32_t ffk_layer_norm_linear(const void* x, const float* ln_w, const float* ln_b,
+                              const float* weight, const float* bias, void* y, int64_t rows,
+                              int32_t d_in, int32_t d_out, int32_t activation, int32_t out_dtype,
+                              float eps, void* stream) {
+  if (int32_t s = check_device()) return s;
+  if (!x || !weight || !y) return fail(FFK_ERR_INVALID, "layer_norm_linear: null tensor");
+  if (rows < 0 || d_in <= 0 || d_in % 64 != 0 || d_in > kLnGemmMaxK || d_out <= 0 || d_out % 32 != 0)
+    return fail(FFK_ERR_INVALID, "layer_norm_linear: rows=%lld d_in=%d d_out=%d (d_in a multiple of 64 up to %d, d_out a multiple of 32)",
+                (long long)rows, d_in, d_out, kLnGemmMaxK);
+  if (activation < FFK_ACT_NONE || activation > FFK_ACT_RELU)
+    return fail(FFK_ERR_INVALID, "layer_norm_linear: unknown activation %d", activation);
+  if (out_dtype != FFK_DTYPE_BF16 && out_dtype != FFK_DTYPE_F32)
+    return fail(FFK_ERR_INVALID, "layer_norm_linear: unknown output dtype %d", out_dtype);
+  if ((rows + 31) / 32 > 0x7fffffffLL) return fail(FFK_ERR_INVALID, "layer_norm_linear: too many rows");
+  if (!aligned16(x) || !aligned16(y) || !aligned16(weight) || (ln_w && !aligned16(ln_w)) ||
+      (ln_b && !aligned16(ln_b)))
+    return fail(FFK_ERR_INVALID, "layer_norm_linear: x, y, weight and the norm affine must be 16-byte aligned");
+  if (rows == 0) return ok();
+  RowGemmArgs g{};
+  g.ln_x = static_cast<const bf16*>(x);
+  g.ln_w = ln_w;
+  g.ln_b = ln_b;
+  g.eps = eps;
+  g.w0 = weight;
+  g.M = rows;
+  g.K = d_in;
+  g.O = d_out;
+  g.bias_out = bias;
+  g.act = activation;
+  g.y_f32 = out_dtype == FFK_DTYPE_F32 ? 1 : 0;
+  g.y = y;
+  launch_row_gemm(g, kEpiLinear, kXLn, static_cast<hipStream_t>(stream));
+  return check_launch("layer_norm_linear");
+}
+
+size_t ffk_swiglu_ffn_workspace(int64_t rows, int32_t hidden) {
+  if (rows < 0 || hidden <= 0) return 0;
+  return up256((size_t)rows * hidden * sizeof(float));
+}
+
+int32_t ffk_swiglu_ffn(const void* x, const float* w_a, const float* w_b, const float* w_out,
+                       const void* residual, void* out, void* workspace, size_t workspace_bytes,
+                       int64_t rows, int32_t d, int32_t hidden, void* stream) {
+  if (int32_t s = check_device()) return s;
+  if (!x || !w_a || !w_b || !w_out || !out) return fail(FFK_ERR_INVALID, "swiglu_ffn: null argument");
+  if (rows < 0 || d <= 0 || d % 64 != 0 || d > kLnGemmMaxK || hidden <= 0 || hidden % 64 != 0)
+    return fail(FFK_ERR_INVALID, "swiglu_ffn: rows=%lld d=%d hidden=%d (d a multiple of 64 up to %d, hidden a multiple of 64)",
+                (long long)rows, d, hidden, kLnGemmMaxK);
+  if ((rows + 31) / 32 > 0x7fffffffLL) return fail(FFK_ERR_INVALID, "swiglu_ffn: too many rows");
+  if (!aligned16(x) || !aligned16(out) || !aligned16(w_a) || !aligned16(w_b) || !aligned16(w_out) ||
+      (residual && !aligned16(residual)))
+    return fail(FFK_ERR_INVALID, "swiglu_ffn: tensors must be 16-byte aligned");
+  const size_t need = ffk_swiglu_ffn_workspace(rows, hidden);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(FFK_ERR_WORKSPACE, "swiglu_ffn: workspace %zu bytes < %zu", workspace_bytes, need);
+  if (rows == 0) return ok();
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (!fused) {
-    RowGemmArgs g{};
-    g.ln_x = static_cast<const bf16*>(x);
-    g.ln_w = ln_w;
-    g.ln_b = ln_b;
-    g.eps = eps;
-    g.w0 = w_expand_a;
-    g.w1 = w_expand_b;
-    g.M = rows;
-    g.K = d;
-    g.O = 2 * factor * d;
-    g.h32 = w.h;
-    launch_row_gemm(g, kEpiSwiglu, kXLn, st);
-    RowGemmArgs s{};
-    s.x32 = w.h;
-    s.w0 = w_squeeze;
-    s.M = rows;
-    s.K = factor * d;
-    s.O = d;
-    s.res = static_cast<const bf16*>(x);
-    s.out = static_cast<bf16*>(out);
-    s.residual = residual ? 1 : 0;
-    launch_row_gemm(s, kEpiResid, kXF32, st);
-    return check_launch("transition");
-  }
-  launch_transition_pack(w_expand_a, w_expand_b, w_squeeze, w.w, st);
-  TransitionArgs a;
-  a.x = static_cast<const bf16*>(x);
-  a.ln_w = ln_w;
-  a.ln_b = ln_b;
-  a.w = w.w;
-  a.out = static_cast<bf16*>(out);
-  a.rows = rows;
-  a.residual = residual ? 1 : 0;
-  a.eps = eps;
-  launch_transition(a, st);
-  return check_launch("transition");
+  RowGemmArgs g{};
+  g.ln_x = static_cast<const bf16*>(x);
+  g.ln_plain = 1;
+  g.w0 = w_a;
+  g.w1 = w_b;
+  g.M = rows;
+  g.K = d;
+  g.O = 2 * hidden;
+  g.h32 = static_cast<float*>(workspace);
+  launch_row_gemm(g, kEpiSwiglu, kXLn, st);
+  RowGemmArgs s{};
+  s.x32 = static_cast<const float*>(workspace);
+  s.w0 = w_out;
+  s.M = rows;
+  s.K = hidden;
+  s.O = d;
+  s.res = static_cast<const bf16*>(residual);
+  s.out = static_cast<bf16*>(out);
+  s.residual = residual ? 1 : 0;
+  launch_row_gemm(s, kEpiResid, kXF32, st);
+  return check_launch("swiglu_ffn");
 }
 
 size_t ffk_attention_pair_bias_workspace(int64_t batch, int64_t n, int32_t d_single,

@@ -80,7 +80,8 @@ void launch_transition(const TransitionArgs& a, hipStream_t stream);
 // Token-row GEMM out[m][o] = sum_k W[o][k] x[m][k] (single track, single.hip) with one of
 // three epilogues, x either LayerNorm(ln_x) (kXLn, K <= kLnGemmMaxK) or fp32 rows x32 (kXF32).
 // K % 64 == 0, O % 32 == 0; weights are the fp32 parameters. Pairs served: (kEpiApb, kXLn),
-// (kEpiSwiglu, kXLn), (kEpiResid, kXF32), (kEpiPwa, kXLn), (kEpiOpm, kXLn).
+// (kEpiSwiglu, kXLn), (kEpiResid, kXF32), (kEpiPwa, kXLn), (kEpiOpm, kXLn), (kEpiTrimul, kXLn),
+// (kEpiStore32, kXLn), (kEpiGateResid, kXLn), (kEpiLinear, kXLn).
 enum {
   kEpiApb = 0,
   kEpiSwiglu = 1,
@@ -90,7 +91,10 @@ enum {
   kEpiTrimul = 5,     // gated, masked left / right projections into channel planes
   kEpiStore32 = 6,    // h32 = y (fp32)
   kEpiGateResid = 7,  // out = res + y32 * sigmoid(y) (or y32 * sigmoid(y))
+  kEpiLinear = 8,     // y = act(W x + bias_out), bf16 or fp32 rows [M][O]
 };
+// kEpiLinear activations (the C-ABI's FFK_ACT_* values)
+enum { kActNone = 0, kActSigmoid = 1, kActSilu = 2, kActRelu = 3 };
 // Row maps (RowGemmArgs.tmap): the input row read for logical row m, and the rows the epilogue
 // of kEpiResid writes. kMapPairT: m = (b n + r) n + j reads row (b n + j) n + r (the
 // transposed pair); kMapGridOut / kMapGridIn: m = (b npm + i) npm + k over the padded grid
@@ -100,8 +104,9 @@ enum { kXLn = 0, kXF32 = 1 };
 constexpr int kLnGemmMaxK = 768;
 struct RowGemmArgs {
   const bf16* ln_x;             // kXLn: [M][K] rows to normalise with ln_w, ln_b, eps
-  const float *ln_w, *ln_b;
+  const float *ln_w, *ln_b;     // NULL: weight 1 / offset 0
   float eps;
+  int ln_plain;                 // kXLn with 1: the rows enter as they are (no normalisation)
   const float* x32;             // kXF32: [M][K]
   // kEpiApb: w0..w3 = to_query, to_key, to_value, to_gate ([cs][cs] each, O = 4 cs);
   // kEpiSwiglu: w0 = expand_a, w1 = expand_b ([hid][K] each, O = 2 hid);
@@ -138,6 +143,9 @@ struct RowGemmArgs {
   const bf16* res;  // kEpiResid: out = res + y (residual) or y
   bf16* out;
   int residual;
+  const float* bias_out;  // kEpiLinear: [O] or NULL
+  int act, y_f32;         // kEpiLinear: kAct*, 1 = fp32 rows
+  void* y;                // kEpiLinear: [M][O]
 };
 void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream);
 

@@ -187,7 +187,7 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
       if (pc + 16 * i < nc)
 #pragma unroll
         for (int e = 0; e < 8; ++e) s1 += (float)xv[i][e];
-    const float mean = sum16(s1) / (float)a.K;
+    const float mean = a.ln_plain ? 0.f : sum16(s1) / (float)a.K;
     float s2 = 0.f;
 #pragma unroll
     for (int i = 0; i < kMaxChunks; ++i)
@@ -197,15 +197,17 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
           const float d = (float)xv[i][e] - mean;
           s2 += d * d;
         }
-    const float rstd = __builtin_amdgcn_rsqf(sum16(s2) / (float)a.K + a.eps);
+    const float rstd = a.ln_plain ? 1.f : __builtin_amdgcn_rsqf(sum16(s2) / (float)a.K + a.eps);
+    const f32x4 one4 = {1.f, 1.f, 1.f, 1.f}, zero4 = {0.f, 0.f, 0.f, 0.f};
+    const bool has_w = a.ln_w != nullptr && !a.ln_plain, has_b = a.ln_b != nullptr && !a.ln_plain;
 #pragma unroll
     for (int i = 0; i < kMaxChunks; ++i) {
       if (pc + 16 * i < nc) {
         const int c = 8 * (pc + 16 * i);
-        const f32x4 w0 = *reinterpret_cast<const f32x4*>(a.ln_w + c);
-        const f32x4 w1 = *reinterpret_cast<const f32x4*>(a.ln_w + c + 4);
-        const f32x4 b0 = *reinterpret_cast<const f32x4*>(a.ln_b + c);
-        const f32x4 b1 = *reinterpret_cast<const f32x4*>(a.ln_b + c + 4);
+        const f32x4 w0 = has_w ? *reinterpret_cast<const f32x4*>(a.ln_w + c) : one4;
+        const f32x4 w1 = has_w ? *reinterpret_cast<const f32x4*>(a.ln_w + c + 4) : one4;
+        const f32x4 b0 = has_b ? *reinterpret_cast<const f32x4*>(a.ln_b + c) : zero4;
+        const f32x4 b1 = has_b ? *reinterpret_cast<const f32x4*>(a.ln_b + c + 4) : zero4;
         f32x4 y0, y1;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -377,6 +379,29 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
         for (int e = 0; e < 4; ++e) y[e] += (float)r[e];
       }
       store4(a.out + m * a.O + c, y[0], y[1], y[2], y[3]);
+    }
+  } else if (EPI == kEpiLinear) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = ot * 32 + 8 * v + 4 * g;
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t = acc[4 * v + e] + (a.bias_out ? a.bias_out[c + e] : 0.f);
+        if (a.act == kActSigmoid)
+          t = sigmoid_scaled(-kLog2e * t);
+        else if (a.act == kActSilu)
+          t = t * sigmoid_scaled(-kLog2e * t);
+        else if (a.act == kActRelu)
+          t = fmaxf(t, 0.f);
+        y[e] = t;
+      }
+      if (a.y_f32) {
+        const f32x4 yv = {y[0], y[1], y[2], y[3]};
+        *reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + m * a.O + c) = yv;
+      } else {
+        store4(static_cast<bf16*>(a.y) + m * a.O + c, y[0], y[1], y[2], y[3]);
+      }
     }
   } else if (EPI == kEpiSwiglu) {
     const int hid = a.O / 2;
@@ -680,6 +705,13 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
       launch_row_gemm_t<kEpiStore32, kXLn, 4>(a, stream);
     else
       launch_row_gemm_t<kEpiStore32, kXLn, 2>(a, stream);
+  } else if (epi == kEpiLinear && xsrc == kXLn) {
+    if (a.O >= 256)
+      launch_row_gemm_t<kEpiLinear, kXLn, 8>(a, stream);
+    else if (a.O >= 128)
+      launch_row_gemm_t<kEpiLinear, kXLn, 4>(a, stream);
+    else
+      launch_row_gemm_t<kEpiLinear, kXLn, 2>(a, stream);
   } else if (epi == kEpiGateResid && xsrc == kXLn) {
     // one workgroup column (O <= 256): a workgroup owns its rows, so out may alias the input
     if (a.O > 128)

@@ -1,9 +1,9 @@
 """Functional entry points of the HIP kernels, named after the engine's kernel functions.
 
-The engine exposes ``layer_norm``, ``triangle_multiplicative_update``,
-``triangle_attention`` and ``transition`` under ``miniworld_engine.kernels``
-(names: ``docs/guides/ENGINE-2.4.2.md:18-21`` of the reference; their signatures are
-not in the reference, so these are this library's own); ``attention_pair_bias`` serves
+The engine exposes ``layer_norm``, ``layer_norm_linear``, ``swiglu_ffn``,
+``triangle_multiplicative_update``, ``triangle_attention`` and ``transition_layer`` under
+``miniworld_engine.kernels`` (names: ``docs/guides/ENGINE-2.4.2.md:18-21`` of the reference;
+their signatures are not in the reference, so these are this library's own); ``attention_pair_bias`` serves
 the engine's ``single_attention`` op (``AttentionPairBias``) and
 ``msa_pair_weighted_averaging`` its ``msa_pwa`` op (``MSAPairWeightedAveraging``) and
 ``outer_product_mean`` its ``opm`` op (``OuterProductMean``). Each function validates its
@@ -121,6 +121,69 @@ def layer_norm(x: Tensor, weight: Tensor | None, bias: Tensor | None, eps: float
     )
     _native.check(status, "layer_norm")
     return y
+
+
+#: ``layer_norm_linear`` activations -> the C-ABI's FFK_ACT_* values
+ACTIVATIONS = {"none": 0, "sigmoid": 1, "silu": 2, "relu": 3}
+
+
+def layer_norm_linear(x: Tensor, ln_weight: Tensor | None, ln_bias: Tensor | None, weight: Tensor,
+                      bias: Tensor | None = None, *, activation: str = "none",
+                      out_dtype: torch.dtype = torch.bfloat16, eps: float = 1e-5,
+                      out: Tensor | None = None) -> Tensor:
+    """``act(LN(x) W^T + b)`` over the last axis of ``x [..., d_in]`` bf16 (the engine's
+    ``layer_norm_linear``): fp32 statistics, ``weight [d_out, d_in]`` fp32, ``bias [d_out]``,
+    output ``[..., d_out]`` in ``out_dtype`` (bf16 or fp32). d_in a multiple of 64 up to 768,
+    d_out a multiple of 32."""
+    _need(_on_device(x) and x.is_contiguous(), "x must be a contiguous device tensor")
+    _need(x.dtype == torch.bfloat16, f"x must be bf16 (got {x.dtype})")
+    _need(activation in ACTIVATIONS, f"activation must be one of {sorted(ACTIVATIONS)}")
+    _need(out_dtype in (torch.bfloat16, torch.float32), f"out_dtype must be bf16 or fp32 (got {out_dtype})")
+    d_in = x.shape[-1]
+    _need(weight.dim() == 2, f"weight must be [d_out, d_in] (got {tuple(weight.shape)})")
+    d_out = weight.shape[0]
+    _need(d_in % 64 == 0 and 0 < d_in <= 768 and d_out % 32 == 0 and d_out > 0,
+          f"d_in={d_in} d_out={d_out} (the kernel takes d_in a multiple of 64 up to 768, d_out a multiple of 32)")
+    dev = x.device
+    w = _param(weight, dev, "weight", (d_out, d_in))
+    lw = None if ln_weight is None else _param(ln_weight, dev, "ln_weight", (d_in,))
+    lb = None if ln_bias is None else _param(ln_bias, dev, "ln_bias", (d_in,))
+    b = None if bias is None else _param(bias, dev, "bias", (d_out,))
+    out = _output(out, (*x.shape[:-1], d_out), out_dtype, dev)
+    status = _native.lib().ffk_layer_norm_linear(
+        x.data_ptr(), _ptr(lw), _ptr(lb), w.data_ptr(), _ptr(b), out.data_ptr(), x.numel() // d_in,
+        d_in, d_out, ACTIVATIONS[activation], 0 if out_dtype == torch.bfloat16 else 1, float(eps),
+        _stream(dev))
+    _native.check(status, "layer_norm_linear")
+    return out
+
+
+def swiglu_ffn(x: Tensor, w_a: Tensor, w_b: Tensor, w_out: Tensor, residual: Tensor | None = None, *,
+               out: Tensor | None = None) -> Tensor:
+    """``(silu(x W_a^T) * (x W_b^T)) W_out^T`` (+ ``residual``) over the last axis of
+    ``x [..., d]`` bf16 (the engine's ``swiglu_ffn``): ``w_a, w_b [hidden, d]``,
+    ``w_out [d, hidden]`` fp32; d a multiple of 64 up to 768, hidden a multiple of 64."""
+    _need(_on_device(x) and x.is_contiguous(), "x must be a contiguous device tensor")
+    _need(x.dtype == torch.bfloat16, f"x must be bf16 (got {x.dtype})")
+    d = x.shape[-1]
+    hidden = w_a.shape[0]
+    _need(d % 64 == 0 and 0 < d <= 768 and hidden % 64 == 0 and hidden > 0,
+          f"d={d} hidden={hidden} (the kernel takes d a multiple of 64 up to 768, hidden a multiple of 64)")
+    dev = x.device
+    wa = _param(w_a, dev, "w_a", (hidden, d))
+    wb = _param(w_b, dev, "w_b", (hidden, d))
+    wo = _param(w_out, dev, "w_out", (d, hidden))
+    if residual is not None:
+        _need(residual.dtype == torch.bfloat16 and residual.shape == x.shape and residual.device == dev
+              and residual.is_contiguous(), "residual must be a contiguous bf16 tensor shaped like x")
+    out = _output(out, tuple(x.shape), torch.bfloat16, dev)
+    rows = x.numel() // d
+    lib = _native.lib()
+    ws = _workspace(lib.ffk_swiglu_ffn_workspace(rows, hidden), dev)
+    status = lib.ffk_swiglu_ffn(x.data_ptr(), wa.data_ptr(), wb.data_ptr(), wo.data_ptr(), _ptr(residual),
+                                out.data_ptr(), ws.data_ptr(), ws.numel(), rows, d, hidden, _stream(dev))
+    _native.check(status, "swiglu_ffn")
+    return out
 
 
 def triangle_multiplicative_update(
@@ -252,6 +315,10 @@ def transition(
     )
     _native.check(status, "transition")
     return out
+
+
+#: the engine's name for the transition kernel (``docs/guides/ENGINE-2.4.2.md:19``)
+transition_layer = transition
 
 
 def transition_supported(d: int, factor: int) -> bool:

@@ -36,6 +36,11 @@ extern "C" {
 #define FFK_DTYPE_BF16 0
 #define FFK_DTYPE_F32 1
 
+#define FFK_ACT_NONE 0    /* y = t */
+#define FFK_ACT_SIGMOID 1 /* y = 1 / (1 + exp(-t)) */
+#define FFK_ACT_SILU 2    /* y = t / (1 + exp(-t)) */
+#define FFK_ACT_RELU 3    /* y = max(t, 0) */
+
 /* Library version (major * 10000 + minor * 100 + patch). */
 int32_t ffk_version(void);
 
@@ -54,6 +59,38 @@ int32_t ffk_device_supported(int32_t device);
  */
 int32_t ffk_layer_norm(const void* x, const float* weight, const float* bias, void* y,
                        int64_t rows, int32_t cols, float eps, int32_t dtype, void* stream);
+
+/*
+ * LayerNorm fused into a linear projection, with a bias and an activation epilogue:
+ *   y[r, :] = act(LN(x[r, :]) W^T + bias)
+ * x [rows, d_in] bf16; LN with fp32 statistics, ln_w / ln_b fp32 [d_in] (either may be NULL:
+ * weight 1, offset 0); weight fp32 [d_out, d_in] (the engine Linear's own tensor, rounded to
+ * bf16 for the matrix cores; the normalised rows keep fp32 precision as a bf16 hi + lo pair);
+ * bias fp32 [d_out] or NULL; y [rows, d_out] in out_dtype (FFK_DTYPE_BF16 or FFK_DTYPE_F32);
+ * activation one of FFK_ACT_*. d_in a multiple of 64 up to 768, d_out a multiple of 32.
+ * Replaces: `miniworld_engine.kernels.layernorm_linear.interface.layer_norm_linear`
+ * (docs/guides/ENGINE-2.4.2.md:21; the reference holds no signature for it). The pair ops
+ * below fuse this prologue into their own projection kernels.
+ */
+int32_t ffk_layer_norm_linear(const void* x, const float* ln_w, const float* ln_b,
+                              const float* weight, const float* bias, void* y, int64_t rows,
+                              int32_t d_in, int32_t d_out, int32_t activation, int32_t out_dtype,
+                              float eps, void* stream);
+
+/*
+ * SwiGLU feed-forward on token rows, no normalisation:
+ *   out[r, :] = residual[r, :] + (silu(x[r, :] w_a^T) * (x[r, :] w_b^T)) w_out^T
+ * (residual NULL: the bare update). x, residual, out [rows, d] bf16 (out may alias x or the
+ * residual); w_a, w_b fp32 [hidden, d], w_out fp32 [d, hidden]; the hidden rows stay fp32 in
+ * the workspace (ffk_swiglu_ffn_workspace bytes). d a multiple of 64 up to 768, hidden a
+ * multiple of 64. The transition is x + swiglu_ffn(LN(x)).
+ * Replaces: `miniworld_engine.kernels.swiglu_ffn` (docs/guides/ENGINE-2.4.2.md:18; no
+ * signature in the reference).
+ */
+size_t ffk_swiglu_ffn_workspace(int64_t rows, int32_t hidden);
+int32_t ffk_swiglu_ffn(const void* x, const float* w_a, const float* w_b, const float* w_out,
+                       const void* residual, void* out, void* workspace, size_t workspace_bytes,
+                       int64_t rows, int32_t d, int32_t hidden, void* stream);
 
 /*
  * Triangle multiplicative update, outgoing (outgoing = 1) or incoming (0), including

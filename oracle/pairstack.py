@@ -83,6 +83,40 @@ def layer_norm(
     return y
 
 
+def layer_norm_linear(
+    x: Tensor, ln_w: Tensor | None, ln_b: Tensor | None, weight: Tensor, bias: Tensor | None = None,
+    *, activation: str = "none", eps: float = 1e-5, dtype: torch.dtype = torch.float32,
+) -> Tensor:
+    """``act(LN(x) W^T + b)``: the LayerNorm-fed projection every pair op starts with
+    (``legacy/reference/triangle.py:39-43``, ``legacy/attention.py:111-124``), as one function
+    (the engine's ``layer_norm_linear``, ``docs/guides/ENGINE-2.4.2.md:21``)."""
+    h = layer_norm(x.to(dtype), None if ln_w is None else ln_w.to(dtype),
+                   None if ln_b is None else ln_b.to(dtype), eps)
+    y = h @ weight.to(dtype).T
+    if bias is not None:
+        y = y + bias.to(dtype)
+    if activation == "sigmoid":
+        return torch.sigmoid(y)
+    if activation == "silu":
+        return y * torch.sigmoid(y)
+    if activation == "relu":
+        return y.clamp_min(0)
+    if activation != "none":
+        raise ValueError(f"unknown activation {activation!r}")
+    return y
+
+
+def swiglu_ffn(x: Tensor, w_a: Tensor, w_b: Tensor, w_out: Tensor, residual: Tensor | None = None,
+               *, dtype: torch.dtype = torch.float32) -> Tensor:
+    """``(silu(x W_a^T) * (x W_b^T)) W_out^T`` (+ ``residual``): the transition's body without its
+    LayerNorm (``legacy/reference/transition.py:40-41``; the engine's ``swiglu_ffn``,
+    ``docs/guides/ENGINE-2.4.2.md:18``)."""
+    h = x.to(dtype)
+    a = h @ w_a.to(dtype).T
+    y = (a * torch.sigmoid(a) * (h @ w_b.to(dtype).T)) @ w_out.to(dtype).T
+    return y if residual is None else residual.to(dtype) + y
+
+
 def _pair_mask(mask: Tensor, dtype: torch.dtype) -> Tensor:
     m = mask.to("cpu", dtype)
     return m[:, :, None] * m[:, None, :]

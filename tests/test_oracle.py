@@ -489,3 +489,46 @@ def test_block_io_dtype_rounds_the_stream_between_ops():
     rounded = ps.pairformer_block(z, mask, params, n_head_pair=heads, dtype=F64, io_dtype=torch.bfloat16)
     assert torch.equal(rounded, rounded.bfloat16().double())  # the stream leaves each op in bf16
     assert 0 < ps.rel_rms(rounded, plain) < 2e-2
+
+
+@pytest.mark.parametrize("activation", ["none", "sigmoid", "silu", "relu"])
+@pytest.mark.parametrize("affine", [True, False])
+def test_layer_norm_linear_matches_brute_force(activation, affine):
+    """Row by row: the brute-force LayerNorm, a mat-vec, the activation's closed form."""
+    import math
+
+    g = torch.Generator().manual_seed(61)
+    x = torch.randn(7, 12, generator=g, dtype=F64) * 2 + 0.3
+    w = torch.randn(5, 12, generator=g, dtype=F64) * 0.4
+    b = torch.randn(5, generator=g, dtype=F64) * 0.1
+    lw = 1 + 0.1 * torch.randn(12, generator=g, dtype=F64) if affine else None
+    lb = 0.1 * torch.randn(12, generator=g, dtype=F64) if affine else None
+    got = ps.layer_norm_linear(x, lw, lb, w, b, activation=activation, dtype=F64)
+    act = {"none": lambda t: t, "sigmoid": lambda t: 1 / (1 + math.exp(-t)),
+           "silu": lambda t: t / (1 + math.exp(-t)), "relu": lambda t: max(t, 0.0)}[activation]
+    for r in range(7):
+        h = brute.layer_norm_vec(x[r].numpy(), None if lw is None else lw.numpy(),
+                                 None if lb is None else lb.numpy(), 1e-5)
+        y = brute._matvec(w.numpy(), h)
+        want = [act(y[o] + float(b[o])) for o in range(5)]
+        np.testing.assert_allclose(got[r].numpy(), want, rtol=1e-12, atol=1e-12)
+    if activation == "none" and affine:
+        torch.testing.assert_close(got, F.linear(F.layer_norm(x, (12,), lw, lb, 1e-5), w, b))
+
+
+def test_swiglu_ffn_is_the_transition_without_its_norm():
+    """``x + swiglu_ffn(LN(x))`` equals the brute-force transition, which pins the SwiGLU body."""
+    c = 8
+    p = _rand_params({"ln_in.weight": (c,), "ln_in.bias": (c,), "expand_a.weight": (4 * c, c),
+                      "expand_b.weight": (4 * c, c), "squeeze.weight": (c, 4 * c)}, 62)
+    g = torch.Generator().manual_seed(63)
+    x = torch.randn(2, 5, c, generator=g, dtype=F64)
+    h = ps.layer_norm(x, p["ln_in.weight"], p["ln_in.bias"], 1e-5)
+    got = ps.swiglu_ffn(h, p["expand_a.weight"], p["expand_b.weight"], p["squeeze.weight"], residual=x, dtype=F64)
+    want = brute.transition(x.numpy(), _np(p))
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+    bare = ps.swiglu_ffn(h, p["expand_a.weight"], p["expand_b.weight"], p["squeeze.weight"], dtype=F64)
+    torch.testing.assert_close(bare + x, got)
+    # the gate branches are not interchangeable: swapping expand_a and expand_b changes the result
+    swapped = ps.swiglu_ffn(h, p["expand_b.weight"], p["expand_a.weight"], p["squeeze.weight"], dtype=F64)
+    assert (swapped - bare).abs().max() > 1e-3

@@ -51,6 +51,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p] * 7
         + [c_void_p, c_size_t, c_int64, c_int32, c_int32, c_int32, c_float, c_void_p],
     ),
+    "ffk_transition_noalloc": (
+        c_int32,
+        [c_void_p] * 7 + [c_int64, c_int32, c_int32, c_int32, c_float, c_void_p],
+    ),
     "ffk_layer_norm_linear": (
         c_int32,
         [c_void_p] * 6 + [c_int64, c_int32, c_int32, c_int32, c_int32, c_float, c_void_p],

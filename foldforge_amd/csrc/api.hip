@@ -9,6 +9,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
 
 #include "foldforge_amd.h"
@@ -329,7 +330,7 @@ int32_t transition_check(const void* x, const float* ln_w, const float* ln_b, co
   return FFK_OK;
 }
 
-// The launches of one transition call on a carved workspace.
+// The launches of one transition call on a carved workspace (caller's or the static scratch).
 int32_t transition_run(const TransitionWs& w, const void* x, const float* ln_w, const float* ln_b,
                        const float* wa, const float* wb, const float* wsq, void* out, int64_t rows,
                        int d, int factor, int residual, float eps, hipStream_t st) {
@@ -372,6 +373,41 @@ int32_t transition_run(const TransitionWs& w, const void* x, const float* ln_w, 
   return check_launch("transition");
 }
 
+}  // namespace ffk
+
+// ---------------------------------------------------------------------------------------
+// Static scratch of ffk_transition_noalloc, for callers that cannot allocate device memory.
+// Each device holds its own copy of this array for the life of the process. In host code its
+// name is only a stand-in, not a device address: the address of a device's copy comes from
+// hipGetSymbolAddress, looked up once per device with that device current, and only that
+// address is handed to kernels. Calls on one device share the array, so calls that overlap
+// in time on one device (different streams, other threads) race; nothing in it has to start
+// at zero (every launch writes what it later reads).
+constexpr size_t kNoAllocScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace ffk {
+namespace {
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxDevices];
+}  // namespace
+
+int32_t noalloc_scratch(void** address) {
+  int dev = -1;
+  const hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(FFK_ERR_HIP, "hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return fail(FFK_ERR_DEVICE, "device %d beyond the library's table", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_address[dev]) {
+    void* p = nullptr;
+    const hipError_t r = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (r != hipSuccess || !p)
+      return fail(FFK_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", dev, hipGetErrorString(r));
+    g_scratch_address[dev] = p;
+  }
+  *address = g_scratch_address[dev];
+  return FFK_OK;
+}
 }  // namespace ffk
 
 using namespace ffk;
@@ -737,6 +773,24 @@ int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
     return fail(FFK_ERR_WORKSPACE, "transition: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
   if (rows == 0) return ok();
   return transition_run(transition_ws(workspace, rows, d, factor), x, ln_w, ln_b, w_expand_a, w_expand_b,
+                        w_squeeze, out, rows, d, factor, residual, eps, static_cast<hipStream_t>(stream));
+}
+
+int32_t ffk_transition_noalloc(const void* x, const float* ln_w, const float* ln_b,
+                               const float* w_expand_a, const float* w_expand_b,
+                               const float* w_squeeze, void* out, int64_t rows, int32_t d,
+                               int32_t factor, int32_t residual, float eps, void* stream) {
+  if (int32_t s = check_device()) return s;
+  if (int32_t s = transition_check(x, ln_w, ln_b, w_expand_a, w_expand_b, w_squeeze, out, rows, d, factor))
+    return s;
+  const size_t need = transition_ws(nullptr, rows, d, factor).bytes;
+  if (need > kNoAllocScratchBytes)
+    return fail(FFK_ERR_WORKSPACE, "transition_noalloc: d=%d factor=%d rows=%lld needs %zu bytes of scratch; the static scratch holds %zu (use ffk_transition with a workspace)",
+                d, factor, (long long)rows, need, kNoAllocScratchBytes);
+  if (rows == 0) return ok();
+  void* base = nullptr;
+  if (int32_t s = noalloc_scratch(&base)) return s;
+  return transition_run(transition_ws(base, rows, d, factor), x, ln_w, ln_b, w_expand_a, w_expand_b,
                         w_squeeze, out, rows, d, factor, residual, eps, static_cast<hipStream_t>(stream));
 }
 

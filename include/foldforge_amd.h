@@ -175,6 +175,22 @@ int32_t ffk_transition(const void* x, const float* ln_w, const float* ln_b,
                        int32_t residual, float eps, void* stream);
 
 /*
+ * ffk_transition without a workspace argument and without any device allocation: the
+ * scratch (packed weights, or the hidden rows of the other widths) lives in a static
+ * 4 MiB device array of the library, one per device, held until the process ends. Same
+ * arguments, kernels and results as ffk_transition. Calls whose scratch would exceed 4 MiB
+ * return FFK_ERR_WORKSPACE: d = 128 x 4 always fits (384 KiB of packed weights); other widths
+ * fit while rows * factor * d * 4 bytes <= 4 MiB (e.g. the single track's 384 x 4 up to 682
+ * rows). Calls on one device share the array: calls that overlap in time on one device race.
+ * No counterpart in the reference: for callers that cannot allocate device memory (code under
+ * graph capture, fixed serving loops, harnesses that forbid hipMalloc).
+ */
+int32_t ffk_transition_noalloc(const void* x, const float* ln_w, const float* ln_b,
+                               const float* w_expand_a, const float* w_expand_b,
+                               const float* w_squeeze, void* out, int64_t rows, int32_t d,
+                               int32_t factor, int32_t residual, float eps, void* stream);
+
+/*
  * Single-track attention with pair bias, residual included:
  *   x = LN_single(s); bias[h, i, j] = LN_pair(z[i, j]) . w_bias[h]  (pair norm without offset)
  *   o_h = softmax_j((x w_query^T + b_query)_h . (x w_key^T)_h / sqrt(dh) + bias[h]) (x w_value^T)_h

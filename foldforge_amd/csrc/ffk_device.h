@@ -109,6 +109,32 @@ __device__ __forceinline__ uint32_t xcd_remap(uint32_t wg, uint32_t total) {
   return (wg % 8u) * (total / 8u) + wg / 8u;
 }
 
+// A persistent workgroup's tile in a (batch, row, block) grid, tile = (b * rows + r) * nblk +
+// blk. The walk advances by the grid stride with adds and carries: the stride is split into
+// the same three digits once, so the tile loop does no integer division (a runtime 32-bit
+// division is a long scalar sequence, and a tile loop needs the digits of three tiles).
+struct TileAt {
+  int blk, r, b;
+};
+__device__ __forceinline__ TileAt tile_at(int tile, int nblk, int rows) {
+  TileAt t;
+  t.blk = tile % nblk;
+  t.r = (tile / nblk) % rows;
+  t.b = tile / (nblk * rows);
+  return t;
+}
+// t + step, where step = tile_at(stride, nblk, rows) (each digit below its radix).
+__device__ __forceinline__ TileAt tile_add(TileAt t, const TileAt& step, int nblk, int rows) {
+  t.blk += step.blk;
+  int carry = t.blk >= nblk ? 1 : 0;
+  t.blk -= carry * nblk;
+  t.r += step.r + carry;
+  carry = t.r >= rows ? 1 : 0;
+  t.r -= carry * rows;
+  t.b += step.b + carry;
+  return t;
+}
+
 // Smallest bf16-representable value >= x (x finite).
 __device__ __forceinline__ float bf16_ceil(float x) {
   uint32_t u = __float_as_uint(x);

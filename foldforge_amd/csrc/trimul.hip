@@ -39,6 +39,8 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
   constexpr int H = 128, NB = 3;
   __shared__ __attribute__((aligned(16))) bf16 zt[NB][kPT * 128];  // raw z, then LN(z) (off128)
   __shared__ __attribute__((aligned(16))) bf16 stage[8][32 * kPS];  // [channel][position]
+  __shared__ __attribute__((aligned(16))) float msk[NB][8][kPT];    // token mask m[s0 + t], per wave
+  __shared__ float mrw[NB][8];                                      // token mask m[r], per wave
   __shared__ float lnp[2][H];  // LayerNorm affine
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;
@@ -52,28 +54,24 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
   settle(wgt);
   const int nsb = np / kPT;
   const int64_t plane = (int64_t)np * np;
-  const int ntiles = batch * np * nsb;
-  auto where = [&](int tile, int& b, int& r, int& s0, int& valid) {
-    const int sb = tile % nsb;
-    r = (tile / nsb) % np;
-    b = tile / (nsb * np);
-    s0 = sb * kPT;
-    valid = (r < n) ? max(0, min(kPT, n - s0)) : 0;
-  };
-  // This wave's 2 one-KB pieces (positions 8 wave .. 8 wave + 7) of a tile's z rows into ring
-  // slot buf; positions past the end re-read a real row (zeroed by the LayerNorm). A tile
-  // index past the end issues the same two transfers for tile 0 (kept so that every wave
-  // always has the same number of transfers in flight).
-  auto z_dma = [&](int tile, int buf) {
-    int b, r, s0, valid;
-    where(tile < ntiles ? tile : 0, b, r, s0, valid);
+  auto valid_of = [&](const TileAt& t) { return t.r < n ? max(0, min(kPT, n - t.blk * kPT)) : 0; };
+  // This wave's 2 one-KB pieces (positions 8 wave .. 8 wave + 7) of a tile's z rows and its
+  // own copies of the tile's token-mask values m[s0 + t] (one float per lane) and m[r] (lane
+  // 0) into ring slot buf; positions past the end re-read a real row (zeroed by the
+  // LayerNorm). A tile past the end issues the same transfers for tile 0 (kept so that every
+  // wave always has the same number of transfers in flight). The mask travels by LDS DMA
+  // like z: an ordinary load here would be a vector load (the DMAs' memory clobbers rule out
+  // scalar loads), and waiting for it would drain every transfer in flight.
+  auto z_dma = [&](TileAt t, int buf) {
+    if (t.b >= batch) t = TileAt{0, 0, 0};
+    const int s0 = t.blk * kPT, valid = valid_of(t);
     const bf16* base = z;
     uint32_t stride = 256;  // bytes between consecutive positions
     if (valid > 0) {
       if (outgoing) {
-        base = z + (((int64_t)b * n + r) * n + s0) * 128;
+        base = z + (((int64_t)t.b * n + t.r) * n + s0) * 128;
       } else {
-        base = z + (((int64_t)b * n + s0) * n + r) * 128;
+        base = z + (((int64_t)t.b * n + s0) * n + t.r) * 128;
         stride = (uint32_t)n * 256;
       }
     }
@@ -85,29 +83,30 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
       const int pe = pos < last ? pos : last;
       dma16_stream(base, pe * stride + 16 * ((lane & 15) ^ (pos & 15)), dst + 1024 * piece);
     }
+    const float* mb = maskf + (int64_t)t.b * np;
+    dma4(mb + s0, 4u * lane, lds_addr(&msk[buf][wave][0]));
+    if (lane == 0) dma4(mb + t.r, 0u, lds_addr(&mrw[buf][wave]));
   };
-  const int step = gridDim.x;
-  if ((int)blockIdx.x >= ntiles) return;
+  if ((int)blockIdx.x >= batch * np * nsb) return;
+  const TileAt stride = tile_at(gridDim.x, nsb, np);
+  TileAt cur = tile_at(blockIdx.x, nsb, np);
+  TileAt nxt = tile_add(cur, stride, nsb, np);
+  TileAt far = tile_add(nxt, stride, nsb, np);
   // Software pipeline, one barrier per tile: after the barrier of tile k a wave issues the
   // fetch of tile k + 2, projects and stores tile k (normalised in the previous step), then
   // normalises tile k + 1 (fetched one step earlier) in its own ring slot, so LayerNorm work
   // overlaps the other waves' MFMAs.
-  z_dma(blockIdx.x, 0);
-  z_dma(blockIdx.x + step, 1);
-  wait_vm_lds<2>();  // this wave's pieces of the first tile landed
+  z_dma(cur, 0);
+  z_dma(nxt, 1);
+  wait_vm_lds<4>();  // this wave's transfers of the first tile landed
   __syncthreads();
-  {
-    int b, r, s0, valid;
-    where(blockIdx.x, b, r, s0, valid);
-    ln_inplace_swz<kPT, 512>(zt[0], valid, lnp[0], lnp[1], eps);
-  }
+  ln_inplace_swz<kPT, 512>(zt[0], valid_of(cur), lnp[0], lnp[1], eps);
   int buf = 0, k = 0;
 #pragma unroll 1
-  for (int tile = blockIdx.x; tile < ntiles; tile += step, ++k, buf = buf == NB - 1 ? 0 : buf + 1) {
-    int b, r, s0, valid;
-    where(tile, b, r, s0, valid);
+  for (; cur.b < batch; ++k, buf = buf == NB - 1 ? 0 : buf + 1) {
+    const int b = cur.b, r = cur.r, s0 = cur.blk * kPT;
     const int nbuf = buf == NB - 1 ? 0 : buf + 1, fbuf = nbuf == NB - 1 ? 0 : nbuf + 1;
-    // this wave's pieces of tile + step have landed (issued after them: only the previous
+    // this wave's transfers of tile + step have landed (issued after them: only the previous
     // tile's 4 stores, none before the first step); the barrier publishes everyone's pieces
     // and normalised rows and retires the previous tile's reads of ring slot fbuf
     if (k == 0)
@@ -115,17 +114,13 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
     else
       wait_vm_lds<4>();
     __syncthreads();
-    z_dma(tile + 2 * step, fbuf);
+    z_dma(far, fbuf);
     const bf16* xh = zt[buf];
-    // pair mask m[r] m[s] (uniform addresses: scalar loads, which leave vmcnt alone); a tile
-    // whose 64 pairs are all real takes the unmasked epilogue
-    const float* mrow = maskf + (int64_t)b * np;
-    const float mr = mrow[r];
-    const float* ms = mrow + s0;
-    float mall = mr;
-#pragma unroll
-    for (int i = 0; i < kPT; ++i) mall = fminf(mall, ms[i]);
-    const bool full = mall == 1.f;
+    // pair mask m[r] m[s]: lane t holds m[s0 + t]; a tile whose 64 pairs are all real takes
+    // the unmasked epilogue
+    const float mr = mrw[buf][wave];
+    const float ms = msk[buf][wave][lane];
+    const bool full = mr == 1.f && __builtin_amdgcn_ballot_w64(ms != 1.f) == 0;
     bf16* st = stage[wave];
 #pragma unroll
     for (int pt = 0; pt < kPT / 32; ++pt) {
@@ -152,7 +147,9 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int pa = pt * 32 + 8 * m4 + e;  // uniform; lane group 1 takes pa + 4
-            const float mk = mr * (g ? ms[pa + 4] : ms[pa]);
+            const float m0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ms), pa));
+            const float m1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ms), pa + 4));
+            const float mk = mr * (g ? m1 : m0);
             v[e] = (bf16)(av[4 * m4 + e] * mk * sigmoid_scaled(ag[4 * m4 + e]));
           }
           *reinterpret_cast<bf16x4*>(&st[li * kPS + pt * 32 + 8 * m4 + 4 * g]) = v;
@@ -169,11 +166,10 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
       const int c = chunk >> 3, p8 = chunk & 7;
       st16<kNtProject>(dst + (int64_t)c * plane + 8 * p8, ld8(&st[c * kPS + 8 * p8]));
     }
-    if (tile + step < ntiles) {
-      int nb, nr, ns0, nvalid;
-      where(tile + step, nb, nr, ns0, nvalid);
-      ln_inplace_swz<kPT, 512>(zt[nbuf], nvalid, lnp[0], lnp[1], eps);
-    }
+    if (nxt.b < batch) ln_inplace_swz<kPT, 512>(zt[nbuf], valid_of(nxt), lnp[0], lnp[1], eps);
+    cur = nxt;
+    nxt = far;
+    far = tile_add(far, stride, nsb, np);
   }
   wait_vm_lds<0>();  // no LDS write may land after exit
 }

@@ -27,17 +27,18 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "ffk_triangle_multiplication": (
         c_int32,
         [c_void_p] * 13
-        + [c_void_p, c_size_t, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_float, c_void_p],
+        + [c_void_p, c_size_t, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32,
+           c_float, c_void_p],
     ),
     "ffk_triangle_attention_workspace": (
         c_size_t,
-        [c_int64, c_int64, c_int32, c_int32, c_int32],
+        [c_int64, c_int64, c_int32, c_int32, c_int32, c_int32],
     ),
     "ffk_triangle_attention": (
         c_int32,
-        [c_void_p] * 11
+        [c_void_p] * 15
         + [c_void_p, c_size_t, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32,
-           c_int32, c_float, c_void_p],
+           c_int32, c_int32, c_float, c_void_p],
     ),
     "ffk_flash_attention_bias": (
         c_int32,

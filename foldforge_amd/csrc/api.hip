@@ -158,7 +158,7 @@ bool triattn_fused(int c, int heads, int d) { return c == 128 && heads == 4 && d
 
 struct TrimulWs {
   bf16 *wp, *wg, *wo, *A, *B, *P, *Pt;
-  float *maskf, *y32;
+  float *maskf, *y32, *eps_out;
   int* kst;
   size_t bytes;
 };
@@ -167,6 +167,7 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
   const int64_t np = pad128(n);
   const size_t plane = (size_t)batch * h * np * np;
   TrimulWs w{};
+  w.eps_out = cv.take<float>(1);  // the centre norm's epsilon of a length-divided call
   if (!trimul_fused(c, h)) {
     w.A = cv.take<bf16>(plane);
     w.B = cv.take<bf16>(plane);
@@ -191,16 +192,18 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
 int64_t pad32(int64_t n);
 
 struct TriattnWs {
-  bf16 *wqkv, *wb, *wg, *wo, *q, *k, *vt, *o, *gate;
+  bf16 *wqkv, *wb, *wg, *wo, *wo_t, *q, *k, *vt, *o, *gate, *tbuf;
   float *bias, *og, *maskf;
   int* kst;
   size_t bytes;
 };
-TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d) {
+TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d, int form) {
   Carver cv{static_cast<char*>(ws)};
   const int64_t np = pad128(n);
   const int hd = heads * d;
   TriattnWs w{};
+  // the untransposed and dual forms stage one z-frame update before the transposed add
+  if (form != kTriattnStandard) w.tbuf = cv.take<bf16>((size_t)batch * n * n * c);
   if (!triattn_fused(c, heads, d)) {
     const int64_t np32 = pad32(n);
     const size_t tok = (size_t)batch * n * n * hd;
@@ -217,6 +220,7 @@ TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d
   w.wb = cv.take<bf16>((size_t)32 * c);
   w.wg = cv.take<bf16>((size_t)hd * c);
   w.wo = cv.take<bf16>((size_t)c * hd);
+  if (form == kTriattnDual) w.wo_t = cv.take<bf16>((size_t)c * hd);
   w.q = cv.take<bf16>((size_t)batch * heads * np * np * d);
   w.k = cv.take<bf16>((size_t)batch * heads * np * np * d);
   w.vt = cv.take<bf16>((size_t)batch * heads * np * np * d);
@@ -446,7 +450,7 @@ int32_t ffk_triangle_multiplication(
     const float* w_right_gate, const float* ln_out_w, const float* ln_out_b,
     const float* w_out, const float* w_gate, void* out, void* workspace,
     size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_pair, int32_t d_hidden,
-    int32_t outgoing, int32_t residual, float eps, void* stream) {
+    int32_t outgoing, int32_t residual, int32_t length_divided, float eps, void* stream) {
   if (int32_t s = check_device()) return s;
   const bool fused = trimul_fused(d_pair, d_hidden);
   if (!fused && (d_pair <= 0 || d_pair % 64 != 0 || d_pair > 256 || d_hidden <= 0 ||
@@ -465,6 +469,8 @@ int32_t ffk_triangle_multiplication(
     return fail(FFK_ERR_WORKSPACE, "triangle_multiplication: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
   const TrimulWs w = trimul_ws(workspace, batch, n, d_pair, d_hidden);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (length_divided) launch_length_eps(key_mask, (int)batch, (int)n, eps, w.eps_out, st);
+  const float* eps_out = length_divided ? w.eps_out : nullptr;
   // the output kernel addresses 8 channel planes from one base with 32-bit byte offsets
   if (fused && 7 * 2 * pad128(n) * pad128(n) > 0xffffffffLL)
     return fail(FFK_ERR_INVALID, "triangle_multiplication: n=%lld exceeds the fused kernels' plane offsets", (long long)n);
@@ -498,6 +504,7 @@ int32_t ffk_triangle_multiplication(
     o.ln_w = ln_out_w;
     o.ln_b = ln_out_b;
     o.eps = eps;
+    o.eps_dev = eps_out;
     o.w0 = w_out;
     o.M = batch * n * n;
     o.K = d_hidden;
@@ -559,28 +566,36 @@ int32_t ffk_triangle_multiplication(
   a.outgoing = outgoing ? 1 : 0;
   a.residual = residual ? 1 : 0;
   a.eps = eps;
+  a.eps_out = eps_out;
   launch_trimul(a, st);
   return check_launch("triangle_multiplication");
 }
 
 size_t ffk_triangle_attention_workspace(int64_t batch, int64_t n, int32_t d_pair,
-                                        int32_t n_head, int32_t d_head) {
+                                        int32_t n_head, int32_t d_head, int32_t output_form) {
   if (batch <= 0 || n <= 0 || d_pair <= 0 || n_head <= 0 || d_head <= 0) return 0;
-  return triattn_ws(nullptr, batch, n, d_pair, n_head, d_head).bytes;
+  if (output_form < kTriattnStandard || output_form > kTriattnDual) return 0;
+  return triattn_ws(nullptr, batch, n, d_pair, n_head, d_head, output_form).bytes;
 }
 
 int32_t ffk_triangle_attention(
     const void* z, const uint8_t* key_mask, const float* ln_pair_w, const float* ln_pair_b,
     const float* w_bias, const float* w_query, const float* w_key, const float* w_value,
-    const float* w_gate, const float* w_out, void* out, void* workspace,
+    const float* w_gate, const float* w_out, const float* b_gate, const float* b_out,
+    const float* w_out_t, const float* b_out_t, void* out, void* workspace,
     size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_pair, int32_t n_head,
-    int32_t d_head, int32_t starting, int32_t transposed_bias, int32_t residual, float eps,
-    void* stream) {
+    int32_t d_head, int32_t starting, int32_t transposed_bias, int32_t output_form,
+    int32_t residual, float eps, void* stream) {
   if (int32_t s = check_device()) return s;
+  if (output_form < kTriattnStandard || output_form > kTriattnDual)
+    return fail(FFK_ERR_INVALID, "triangle_attention: output_form %d (0 standard, 1 untransposed, 2 dual)", output_form);
+  if ((output_form == kTriattnDual) != (w_out_t != nullptr))
+    return fail(FFK_ERR_INVALID, "triangle_attention: w_out_t is required by, and only by, the dual output form");
+  if (b_out_t && !w_out_t) return fail(FFK_ERR_INVALID, "triangle_attention: b_out_t without w_out_t");
   const bool fused = triattn_fused(d_pair, n_head, d_head);
   if (!fused && (!(d_pair == 64 || d_pair == 128 || d_pair == 256) || n_head <= 0 || n_head > 32 ||
-                 d_head <= 0 || d_head % 8 != 0 || d_head > 32 || (n_head * d_head) % 64 != 0))
-    return fail(FFK_ERR_INVALID, "triangle_attention: d_pair=%d heads=%d x %d (kernels take 128 with 4 x 32, or d_pair 64 / 128 / 256 with at most 32 heads of 8 to 32 channels, heads x d_head a multiple of 64)", d_pair, n_head, d_head);
+                 d_head <= 0 || d_head % 8 != 0 || d_head > 64 || (n_head * d_head) % 64 != 0))
+    return fail(FFK_ERR_INVALID, "triangle_attention: d_pair=%d heads=%d x %d (kernels take 128 with 4 x 32, or d_pair 64 / 128 / 256 with at most 32 heads of 8 to 64 channels, heads x d_head a multiple of 64)", d_pair, n_head, d_head);
   if (batch <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "triangle_attention: empty shape");
   if (batch * n_head > 65535 || pad128(n) > 65535)
     return fail(FFK_ERR_INVALID, "triangle_attention: batch=%lld n=%lld exceed the launch grid", (long long)batch, (long long)n);
@@ -589,12 +604,14 @@ int32_t ffk_triangle_attention(
     return fail(FFK_ERR_INVALID, "triangle_attention: null argument");
   if (!aligned16(z) || !aligned16(out))
     return fail(FFK_ERR_INVALID, "triangle_attention: z/out must be 16-byte aligned");
-  const TriattnWs need = triattn_ws(nullptr, batch, n, d_pair, n_head, d_head);
+  const TriattnWs need = triattn_ws(nullptr, batch, n, d_pair, n_head, d_head, output_form);
   if (!workspace || workspace_bytes < need.bytes || !aligned16(workspace))
     return fail(FFK_ERR_WORKSPACE, "triangle_attention: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
-  const TriattnWs w = triattn_ws(workspace, batch, n, d_pair, n_head, d_head);
+  const TriattnWs w = triattn_ws(workspace, batch, n, d_pair, n_head, d_head, output_form);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int hd = n_head * d_head;
+  // the ending node's untransposed update is the starting orientation's: nothing to turn
+  const int form = output_form == kTriattnUntransposed && starting ? kTriattnStandard : output_form;
   if (!fused) {
     if (batch * n > 65535 || batch * n * n * hd / 32 > 0x7fffffffLL * 8)
       return fail(FFK_ERR_INVALID, "triangle_attention: batch * n = %lld exceeds the launch grid", (long long)(batch * n));
@@ -615,6 +632,7 @@ int32_t ffk_triangle_attention(
     p.q_bias = nullptr;
     p.q_scale = kLog2e / sqrtf((float)d_head);
     p.gate_bias = 0.f;
+    p.gate_b = b_gate;
     p.q = w.q;
     p.k = w.k;
     p.vt = w.vt;
@@ -656,18 +674,34 @@ int32_t ffk_triangle_attention(
     at.cs = hd;
     at.rows_per_bias = (int)n;
     launch_apb_attention(at, (int)(batch * n), st);
-    RowGemmArgs o{};
-    o.x32 = w.og;
-    o.w0 = w_out;
-    o.M = batch * n * n;
-    o.K = hd;
-    o.O = d_pair;
-    o.n = (int)n;
-    o.tmap = starting ? kMapIdentity : kMapPairT;
-    o.res = static_cast<const bf16*>(z);
-    o.out = static_cast<bf16*>(out);
-    o.residual = residual ? 1 : 0;
-    launch_row_gemm(o, kEpiResid, kXF32, st);
+    // the output projection of the gated values into dst (z frame), with the residual or not
+    auto project = [&](const float* wo, const float* bo, bf16* dst, int res) {
+      RowGemmArgs o{};
+      o.x32 = w.og;
+      o.w0 = wo;
+      o.bias_out = bo;
+      o.M = batch * n * n;
+      o.K = hd;
+      o.O = d_pair;
+      o.n = (int)n;
+      o.tmap = starting ? kMapIdentity : kMapPairT;
+      o.res = static_cast<const bf16*>(z);
+      o.out = dst;
+      o.residual = res;
+      launch_row_gemm(o, kEpiResid, kXF32, st);
+    };
+    bf16* dst = static_cast<bf16*>(out);
+    if (form == kTriattnUntransposed) {
+      project(w_out, b_out, w.tbuf, 0);
+      launch_pair_add_transposed(residual ? static_cast<const bf16*>(z) : nullptr, w.tbuf, dst,
+                                 batch, (int)n, d_pair, st);
+    } else if (form == kTriattnDual) {
+      project(w_out_t, b_out_t, w.tbuf, 0);
+      project(w_out, b_out, dst, residual ? 1 : 0);
+      launch_pair_add_transposed(dst, w.tbuf, dst, batch, (int)n, d_pair, st);
+    } else {
+      project(w_out, b_out, dst, residual ? 1 : 0);
+    }
     return check_launch("triangle_attention");
   }
   const int64_t m = (int64_t)hd * d_pair;
@@ -680,7 +714,8 @@ int32_t ffk_triangle_attention(
   job.seg[4] = {nullptr, w.wb + (int64_t)n_head * d_pair, (int64_t)(32 - n_head) * d_pair, 0.f};
   job.seg[5] = {w_gate, w.wg, m, -kLog2e};  // sigmoid(x) = 1 / (1 + 2^(-log2(e) x))
   job.seg[6] = {w_out, w.wo, m, 1.f};
-  job.nseg = 7;
+  job.seg[7] = {w_out_t, w.wo_t, form == kTriattnDual ? m : 0, 1.f};
+  job.nseg = 8;
   job.mask = key_mask;
   job.maskf = w.maskf;
   job.kstages = w.kst;
@@ -704,6 +739,12 @@ int32_t ffk_triangle_attention(
   a.vt = w.vt;
   a.bias = w.bias;
   a.o = w.o;
+  a.bg = b_gate;
+  a.bo = b_out;
+  a.form = form;
+  a.wo_t = w.wo_t;
+  a.bo_t = b_out_t;
+  a.tbuf = w.tbuf;
   a.out = static_cast<bf16*>(out);
   a.batch = (int)batch;
   a.n = (int)n;

@@ -22,8 +22,13 @@ struct TrimulArgs {
   bf16* out;
   int batch, n, np, outgoing, residual;
   float eps;
+  const float* eps_out;  // device epsilon of the centre norm (NULL: eps)
 };
 void launch_trimul(const TrimulArgs& a, hipStream_t stream);
+// eps_out[0] = eps * L^2 for the length-divided contraction, L the number of positions real in
+// any batch element (at least 1), from the key mask [batch][n].
+void launch_length_eps(const uint8_t* mask, int batch, int n, float eps, float* eps_out,
+                       hipStream_t stream);
 // P[p] = X[p] Y[p]^T for `planes` planes of [np][np] bf16 (np % 128 == 0). With kstages, plane
 // p runs only the first kstages[p / planes_per_batch] k stages of 32 (the operands are zero past
 // them, so the product is unchanged).
@@ -44,11 +49,24 @@ struct TriattnArgs {
   float* bias;       // [batch * heads][np / 32][np / 32][2][32][16] blocked, see triattn.hip
   const int* kstages;  // [batch] key stages holding a real key (written by the weight packing)
   bf16* o;           // [batch][n][n][128] z-frame attention output
+  const float *bg, *bo;  // gate / output projection biases [128] (NULL: none)
+  int form;          // kTriattn*: how the update reaches out
+  const bf16* wo_t;  // kTriattnDual: the second output projection [128][128] and its bias
+  const float* bo_t;
+  bf16* tbuf;        // kTriattnUntransposed / kTriattnDual: [batch][n][n][128] update scratch
   bf16* out;
   int batch, n, np, heads, starting, transposed_bias, residual;
   float eps;
 };
+// Output forms: the z-frame update (AF3 and its descendants); the update transposed (Chai-1's
+// trunk, ending node); the update plus the transpose of a second projection's (Chai-1's
+// confidence head).
+enum { kTriattnStandard = 0, kTriattnUntransposed = 1, kTriattnDual = 2 };
 void launch_triattn(const TriattnArgs& a, hipStream_t stream);
+// out[b][i][j][:] = (base ? base[b][i][j][:] : 0) + t[b][j][i][:] for c channels (c % 8 == 0);
+// base may be out, t may not.
+void launch_pair_add_transposed(const bf16* base, const bf16* t, bf16* out, int64_t batch, int n,
+                                int c, hipStream_t stream);
 
 struct FlashArgs {
   const bf16 *q, *k, *vt;
@@ -106,6 +124,7 @@ struct RowGemmArgs {
   const bf16* ln_x;             // kXLn: [M][K] rows to normalise with ln_w, ln_b, eps
   const float *ln_w, *ln_b;     // NULL: weight 1 / offset 0
   float eps;
+  const float* eps_dev;         // kXLn: device epsilon, read in place of eps (NULL: eps)
   int ln_plain;                 // kXLn with 1: the rows enter as they are (no normalisation)
   const float* x32;             // kXF32: [M][K]
   // kEpiApb: w0..w3 = to_query, to_key, to_value, to_gate ([cs][cs] each, O = 4 cs);
@@ -118,6 +137,7 @@ struct RowGemmArgs {
   // as in the attention kernel), gate = sigmoid(x W_g^T + gate_bias); q, k, gate [M][cs]
   const float* q_bias;
   float q_scale, gate_bias;
+  const float* gate_b;          // kEpiApb: per-channel gate bias [cs] (NULL: none)
   bf16 *q, *k, *vt, *gate;
   int n, np, heads, dh;
   // kEpiPwa: w0 = to_value, w1 = to_gate ([hd][K] each, O = 2 hd); tokens m = (b S + s) n + j;
@@ -140,10 +160,10 @@ struct RowGemmArgs {
   int tmap, npm;
   const float* y32;  // kEpiGateResid: [M][O]
   float* h32;  // kEpiSwiglu: [M][hid] = silu(a) * b; kEpiStore32: [M][O] = y
-  const bf16* res;  // kEpiResid: out = res + y (residual) or y
+  const bf16* res;  // kEpiResid: out = res + y (residual) or y, y with bias_out when set
   bf16* out;
   int residual;
-  const float* bias_out;  // kEpiLinear: [O] or NULL
+  const float* bias_out;  // kEpiLinear, kEpiResid: [O] or NULL
   int act, y_f32;         // kEpiLinear: kAct*, 1 = fp32 rows
   void* y;                // kEpiLinear: [M][O]
 };

@@ -46,6 +46,33 @@ __global__ __launch_bounds__(256) void planes_to_rows(const bf16* __restrict__ p
 
 }  // namespace
 
+// out[b][i][j][:] = (base ? base[b][i][j][:] : 0) + t[b][j][i][:]: one thread per 8 channels
+// of one output position, so every read and write is 16 contiguous bytes and each output
+// entry is read (from base) and written by the same thread (base may be out).
+__global__ __launch_bounds__(256) void pair_add_transposed(const bf16* base,
+                                                           const bf16* __restrict__ t, bf16* out,
+                                                           int64_t batch, int n, int c) {
+  const int c8 = c / 8;
+  const int64_t nn = (int64_t)n * n, total = batch * nn * c8;
+  for (int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x; idx < total;
+       idx += (int64_t)gridDim.x * 256) {
+    const int64_t pos = idx / c8;
+    const int ch = (int)(idx - pos * c8) * 8;
+    const int64_t b = pos / nn, r = pos - b * nn;
+    const int i = (int)(r / n), j = (int)(r - (int64_t)i * n);
+    const bf16x8 tv = ld8(t + ((b * n + j) * n + i) * c + ch);
+    bf16x8 y;
+    if (base) {
+      const bf16x8 bv = ld8(base + pos * c + ch);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = (bf16)((float)bv[e] + (float)tv[e]);
+    } else {
+      y = tv;
+    }
+    *reinterpret_cast<bf16x8*>(out + pos * c + ch) = y;
+  }
+}
+
 void launch_planes_to_rows(const bf16* planes, bf16* rows, int batch, int hid, int n, int np,
                            hipStream_t stream) {
   const size_t lds = (size_t)hid * (kRowTile + 2) * sizeof(bf16);
@@ -54,6 +81,15 @@ void launch_planes_to_rows(const bf16* planes, bf16* rows, int batch, int hid, i
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   planes_to_rows<<<dim3((unsigned)((n + kRowTile - 1) / kRowTile), (unsigned)n, (unsigned)batch),
                    256, lds, stream>>>(planes, rows, hid, n, np);
+}
+
+void launch_pair_add_transposed(const bf16* base, const bf16* t, bf16* out, int64_t batch, int n,
+                                int c, hipStream_t stream) {
+  const int64_t total = batch * n * n * (c / 8);
+  int64_t blocks = (total + 255) / 256;
+  const int64_t cap = (int64_t)cu_count() * 16;
+  blocks = blocks < 1 ? 1 : blocks > cap ? cap : blocks;
+  pair_add_transposed<<<dim3((unsigned)blocks), 256, 0, stream>>>(base, t, out, batch, n, c);
 }
 
 }  // namespace ffk

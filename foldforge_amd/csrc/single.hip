@@ -197,7 +197,8 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
           const float d = (float)xv[i][e] - mean;
           s2 += d * d;
         }
-    const float rstd = a.ln_plain ? 1.f : __builtin_amdgcn_rsqf(sum16(s2) / (float)a.K + a.eps);
+    const float eps = a.eps_dev ? *a.eps_dev : a.eps;
+    const float rstd = a.ln_plain ? 1.f : __builtin_amdgcn_rsqf(sum16(s2) / (float)a.K + eps);
     const f32x4 one4 = {1.f, 1.f, 1.f, 1.f}, zero4 = {0.f, 0.f, 0.f, 0.f};
     const bool has_w = a.ln_w != nullptr && !a.ln_plain, has_b = a.ln_b != nullptr && !a.ln_plain;
 #pragma unroll
@@ -297,6 +298,12 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
         }
       } else {
         const float nb = -kLog2e;
+        if (a.gate_b) {
+          y0 += a.gate_b[c];
+          y1 += a.gate_b[c + 1];
+          y2 += a.gate_b[c + 2];
+          y3 += a.gate_b[c + 3];
+        }
         y0 = sigmoid_scaled((y0 + a.gate_bias) * nb);
         y1 = sigmoid_scaled((y1 + a.gate_bias) * nb);
         y2 = sigmoid_scaled((y2 + a.gate_bias) * nb);
@@ -420,6 +427,10 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
     for (int v = 0; v < 4; ++v) {
       const int c = ot * 32 + 8 * v + 4 * g;
       float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
+      if (a.bias_out) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] += a.bias_out[c + e];
+      }
       if (a.residual) {
         const bf16x4 r = *reinterpret_cast<const bf16x4*>(a.res + m * a.O + c);
 #pragma unroll
@@ -544,9 +555,12 @@ __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
 // Per 32-key block: S^T = K Q^T + bias^T (A = k rows, B = q rows, the bias as the MFMA
 // accumulator input: lane (li, g) holds query li and keys 8 v + 4 g + e), then
 // O^T += V^T P^T (A = v^T rows in the permuted key order, B = this lane's 16 weights).
+// DT 32-channel tiles of the head (DT = 2: heads of 40 to 64 channels): DT 32 x 32 output
+// tiles, 2 DT MFMAs of the logits per key block.
+template <int DT>
 __global__ __launch_bounds__(256) void apb_attention(ApbAttnArgs a) {
   __shared__ float sm[4][32], sl[4][32];
-  __shared__ float so[3][64][16];
+  __shared__ float so[3][64][16 * DT];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
   const int q0 = blockIdx.x * 32, h = blockIdx.y, b = blockIdx.z;
   const int n = a.n, dh = a.dh, cs = a.cs;
@@ -558,31 +572,41 @@ __global__ __launch_bounds__(256) void apb_attention(ApbAttnArgs a) {
 
   const int qr = min(q0 + li, n - 1);
   const bf16* qp = a.q + ((int64_t)b * n + qr) * cs + h * dh;
-  bf16x8 qf0 = zero8(), qf1 = zero8();
-  if (8 * g < dh) qf0 = ld8(qp + 8 * g);
-  if (16 + 8 * g < dh) qf1 = ld8(qp + 16 + 8 * g);
+  bf16x8 qf[2 * DT];
+#pragma unroll
+  for (int f = 0; f < 2 * DT; ++f) qf[f] = 16 * f + 8 * g < dh ? ld8(qp + 16 * f + 8 * g) : zero8();
   const float* bp = a.bias + (((int64_t)bb * a.heads + h) * n + qr) * a.np + 4 * g;
-  const bf16* vp = a.vt + (((int64_t)b * a.heads + h) * dh + min(li, dh - 1)) * a.np + 8 * g;
+  const bf16* vp[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t)
+    vp[t] = a.vt + (((int64_t)b * a.heads + h) * dh + min(32 * t + li, dh - 1)) * a.np + 8 * g;
   const bf16* kbase = a.k + (int64_t)b * n * cs + h * dh;
 
   float m = -INFINITY, l = 0.f;
-  f32x16 o = zero16();
+  f32x16 o[DT];
+#pragma unroll
+  for (int t = 0; t < DT; ++t) o[t] = zero16();
   const int nkb = a.np / 32;
   for (int kb = wave; kb < nkb; kb += 4) {
     const bf16* kp = kbase + (int64_t)min(kb * 32 + li, n - 1) * cs;
-    bf16x8 kf0 = zero8(), kf1 = zero8();
-    if (8 * g < dh) kf0 = ld8(kp + 8 * g);
-    if (16 + 8 * g < dh) kf1 = ld8(kp + 16 + 8 * g);
+    bf16x8 kf[2 * DT];
+#pragma unroll
+    for (int f = 0; f < 2 * DT; ++f) kf[f] = 16 * f + 8 * g < dh ? ld8(kp + 16 * f + 8 * g) : zero8();
     f32x16 s;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const f32x4 bb = *reinterpret_cast<const f32x4*>(bp + kb * 32 + 8 * v);
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(bp + kb * 32 + 8 * v);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) s[4 * v + e] = bb[e];
+      for (int e = 0; e < 4; ++e) s[4 * v + e] = bv[e];
     }
-    bf16x8 vf0 = ld8(vp + kb * 32), vf1 = ld8(vp + kb * 32 + 16);
-    s = mfma32(kf0, qf0, s);
-    s = mfma32(kf1, qf1, s);
+    bf16x8 vf[DT][2];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      vf[t][0] = ld8(vp[t] + kb * 32);
+      vf[t][1] = ld8(vp[t] + kb * 32 + 16);
+    }
+#pragma unroll
+    for (int f = 0; f < 2 * DT; ++f) s = mfma32(kf[f], qf[f], s);
 
     float bm = s[0];
 #pragma unroll
@@ -599,15 +623,19 @@ __global__ __launch_bounds__(256) void apb_attention(ApbAttnArgs a) {
     }
     l = l * alpha + ps;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[r] *= alpha;
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] *= alpha;
 
     if (kb * 32 + 32 > n) {  // keys past n: their v^T entries were never written
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int key = kb * 32 + 4 * g + 8 * (j >> 2) + (j & 3);
-        if (key >= n) vf0[j] = (bf16)0.f;
-        if (key + 16 >= n) vf1[j] = (bf16)0.f;
-      }
+      for (int t = 0; t < DT; ++t)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int key = kb * 32 + 4 * g + 8 * (j >> 2) + (j & 3);
+          if (key >= n) vf[t][0][j] = (bf16)0.f;
+          if (key + 16 >= n) vf[t][1][j] = (bf16)0.f;
+        }
     }
     bf16x8 p0, p1;
 #pragma unroll
@@ -615,8 +643,11 @@ __global__ __launch_bounds__(256) void apb_attention(ApbAttnArgs a) {
       p0[j] = (bf16)s[j];
       p1[j] = (bf16)s[8 + j];
     }
-    o = mfma32(vf0, p0, o);
-    o = mfma32(vf1, p1, o);
+#pragma unroll
+    for (int t = 0; t < DT; ++t) {
+      o[t] = mfma32(vf[t][0], p0, o[t]);
+      o[t] = mfma32(vf[t][1], p1, o[t]);
+    }
   }
   l = pair_sum(l);
 
@@ -631,31 +662,39 @@ __global__ __launch_bounds__(256) void apb_attention(ApbAttnArgs a) {
   for (int w = 0; w < 4; ++w) total += sl[w][li] * fast_exp2(sm[w][li] - mx);
   const float f = empty ? 0.f : fast_exp2(m - mx) / total;
 #pragma unroll
-  for (int r = 0; r < 16; ++r) o[r] *= f;
+  for (int t = 0; t < DT; ++t)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[t][r] *= f;
   if (wave > 0) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) so[wave - 1][lane][r] = o[r];
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) so[wave - 1][lane][16 * t + r] = o[t][r];
   }
   __syncthreads();
   if (wave != 0) return;
 #pragma unroll
   for (int w = 0; w < 3; ++w)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) o[r] += so[w][lane][r];
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[t][r] += so[w][lane][16 * t + r];
   const int qq = q0 + li;
   if (qq >= n) return;
   const int64_t row = ((int64_t)b * n + qq) * cs + h * dh;
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int d0 = 8 * v + 4 * g;
-    if (d0 < dh) {
-      const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + row + d0);
-      f32x4 y;
+  for (int t = 0; t < DT; ++t)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = o[4 * v + e] * (float)gv[e];
-      *reinterpret_cast<f32x4*>(a.og + row + d0) = y;
+    for (int v = 0; v < 4; ++v) {
+      const int d0 = 32 * t + 8 * v + 4 * g;
+      if (d0 < dh) {
+        const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + row + d0);
+        f32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = o[t][4 * v + e] * (float)gv[e];
+        *reinterpret_cast<f32x4*>(a.og + row + d0) = y;
+      }
     }
-  }
 }
 
 }  // namespace
@@ -737,8 +776,11 @@ void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream) {
 }
 
 void launch_apb_attention(const ApbAttnArgs& a, int batch, hipStream_t stream) {
-  apb_attention<<<dim3((unsigned)((a.n + 31) / 32), (unsigned)a.heads, (unsigned)batch), 256, 0,
-                  stream>>>(a);
+  const dim3 grid((unsigned)((a.n + 31) / 32), (unsigned)a.heads, (unsigned)batch);
+  if (a.dh > 32)
+    apb_attention<2><<<grid, 256, 0, stream>>>(a);
+  else
+    apb_attention<1><<<grid, 256, 0, stream>>>(a);
 }
 
 }  // namespace ffk

@@ -531,17 +531,23 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
 __global__ __launch_bounds__(512, 2) void triattn_output(
     const bf16* __restrict__ z, const bf16* __restrict__ o, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ wg, const bf16* __restrict__ wo,
-    bf16* __restrict__ out, int batch, int n, int residual, float eps) {
+    const float* __restrict__ bg, const float* __restrict__ bo, bf16* __restrict__ out,
+    int batch, int n, int residual, float eps) {
   constexpr int NB = 3;
   __shared__ __attribute__((aligned(16))) bf16 zs[NB][kPT * 128];  // raw z, then out (off128)
   __shared__ __attribute__((aligned(16))) bf16 os[NB][kPT * 128];  // o, then gate * o (off128)
   __shared__ __attribute__((aligned(16))) bf16 xh[2][kPT * 128];   // LN(z) (off128)
   __shared__ float lnp[2][128];
+  __shared__ float pbias[2][128];  // gate bias (times -log2 e, as the packed gate), output bias
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int cb = wave & 3, pt = wave >> 2;
   if (tid < 256) lnp[tid >> 7][tid & 127] = (tid < 128 ? ln_w : ln_b)[tid & 127];
+  if (tid >= 256) {  // published by the first barrier; absent biases are zeros
+    const int c = tid & 127;
+    pbias[(tid >> 7) & 1][c] = tid < 384 ? (bg ? -kLog2e * bg[c] : 0.f) : (bo ? bo[c] : 0.f);
+  }
   WFrag fg, fo;
   load_wfrag(fg, wg, 32 * cb, li, g);
   load_wfrag(fo, wo, 32 * cb, li, g);
@@ -613,7 +619,8 @@ __global__ __launch_bounds__(512, 2) void triattn_output(
         const bf16x4 ov = *po;
         bf16x4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (bf16)(sigmoid_scaled(ag[4 * j + e]) * (float)ov[e]);
+        for (int e = 0; e < 4; ++e)
+          v[e] = (bf16)(sigmoid_scaled(ag[4 * j + e] + pbias[0][32 * cb + 8 * j + 4 * g + e]) * (float)ov[e]);
         *po = v;
       }
     }
@@ -636,7 +643,8 @@ __global__ __launch_bounds__(512, 2) void triattn_output(
         const bf16x4 zv = *pz;
         bf16x4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = (bf16)(ao[4 * j + e] + (residual ? (float)zv[e] : 0.f));
+        for (int e = 0; e < 4; ++e)
+          v[e] = (bf16)(ao[4 * j + e] + pbias[1][32 * cb + 8 * j + 4 * g + e] + (residual ? (float)zv[e] : 0.f));
         *pz = v;
       }
       // the block is this wave's own: LDS operations of a wave complete in order
@@ -698,8 +706,21 @@ void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
   }
   launch_flash(f, stream);
   const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);
-  triattn_output<<<persistent_grid(tiles_o, 1), 512, 0, stream>>>(
-      a.z, a.o, a.ln_w, a.ln_b, a.wg, a.wo, a.out, a.batch, a.n, a.residual, a.eps);
+  auto output = [&](const bf16* wo, const float* bo, bf16* dst, int residual) {
+    triattn_output<<<persistent_grid(tiles_o, 1), 512, 0, stream>>>(
+        a.z, a.o, a.ln_w, a.ln_b, a.wg, wo, a.bg, bo, dst, a.batch, a.n, residual, a.eps);
+  };
+  if (a.form == kTriattnUntransposed) {
+    // the update in the attention's orientation: the z-frame update, transposed
+    output(a.wo, a.bo, a.tbuf, 0);
+    launch_pair_add_transposed(a.residual ? a.z : nullptr, a.tbuf, a.out, a.batch, a.n, 128, stream);
+  } else if (a.form == kTriattnDual) {
+    output(a.wo_t, a.bo_t, a.tbuf, 0);
+    output(a.wo, a.bo, a.out, a.residual);
+    launch_pair_add_transposed(a.out, a.tbuf, a.out, a.batch, a.n, 128, stream);
+  } else {
+    output(a.wo, a.bo, a.out, a.residual);
+  }
 }
 
 }  // namespace ffk

@@ -399,7 +399,8 @@ __global__ __launch_bounds__(512, 2) void trimul_output(
     const bf16* __restrict__ z, const bf16* __restrict__ P, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const float* __restrict__ lno_w,
     const float* __restrict__ lno_b, const bf16* __restrict__ wg, const bf16* __restrict__ wo,
-    bf16* __restrict__ out, int batch, int n, int np, int residual, float eps) {
+    bf16* __restrict__ out, int batch, int n, int np, int residual, float eps,
+    const float* __restrict__ eps_out_dev) {
   constexpr int H = 128, NB = 3;
   __shared__ __attribute__((aligned(16))) bf16 zs[NB][kPT * 128];  // raw z, then out (off128)
   __shared__ __attribute__((aligned(16))) bf16 ps[NB][H * kPT];    // P, [channel][position]
@@ -413,6 +414,8 @@ __global__ __launch_bounds__(512, 2) void trimul_output(
   const int cb = wave & 3, pt = wave >> 2;
   const float* const lsrc[4] = {ln_w, ln_b, lno_w, lno_b};
   lnp[tid >> 7][tid & 127] = lsrc[tid >> 7][tid & 127];  // published by the first barrier
+  // the centre norm's epsilon: a device value when the contraction is length-divided
+  const float eps_out = eps_out_dev ? *eps_out_dev : eps;
   WFrag fg, fo;
   load_wfrag(fg, wg, 32 * cb, li, g);
   load_wfrag(fo, wo, 32 * cb, li, g);
@@ -477,7 +480,7 @@ __global__ __launch_bounds__(512, 2) void trimul_output(
     float var = 0.f;
 #pragma unroll
     for (int q = 0; q < 8; ++q) var += red[par][1][q][lane];
-    const float rstd = __builtin_amdgcn_rsqf(var * (1.f / H) + eps);
+    const float rstd = __builtin_amdgcn_rsqf(var * (1.f / H) + eps_out);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       bf16x8 o;
@@ -585,7 +588,36 @@ void launch_trimul(const TrimulArgs& a, hipStream_t stream) {
   const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);
   trimul_output<<<persistent_grid(tiles_o, 1), 512, 0, stream>>>(
       a.z, a.P, a.ln_w, a.ln_b, a.lno_w, a.lno_b, a.wg, a.wo, a.out, a.batch, a.n, np,
-      a.residual, a.eps);
+      a.residual, a.eps, a.eps_out);
+}
+
+// eps_out[0] = eps * L^2, L = max(1, the number of positions j < n real in any batch element).
+// RoseTTAFold3 divides the contraction by L before the centre LayerNorm
+// (src/foldforge/models/checkpoints/legacy/routing.py:33-55 with
+// legacy/reference/triangle.py:46-48); LN(P / L) with eps is LN(P) with eps L^2, so the
+// kernels keep P as it is and take this epsilon. One workgroup; no host read of L.
+__global__ __launch_bounds__(256) void length_eps(const uint8_t* __restrict__ mask, int batch,
+                                                  int n, float eps, float* __restrict__ eps_out) {
+  __shared__ int total;
+  if (threadIdx.x == 0) total = 0;
+  __syncthreads();
+  int count = 0;
+  for (int j = threadIdx.x; j < n; j += 256) {
+    bool any = false;
+    for (int b = 0; b < batch && !any; ++b) any = mask[(int64_t)b * n + j] != 0;
+    count += any ? 1 : 0;
+  }
+  atomicAdd(&total, count);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const float l = (float)(total > 1 ? total : 1);
+    eps_out[0] = eps * l * l;
+  }
+}
+
+void launch_length_eps(const uint8_t* mask, int batch, int n, float eps, float* eps_out,
+                       hipStream_t stream) {
+  length_eps<<<1, 256, 0, stream>>>(mask, batch, n, eps, eps_out);
 }
 
 void launch_trimul_contract(const bf16* A, const bf16* B, bf16* P, int64_t planes, int np,

@@ -83,11 +83,12 @@ def trimul_supported(d_pair: int, d_hidden: int) -> bool:
 
 def triangle_attention_supported(d_pair: int, n_head: int, d_head: int, transposed_bias: bool) -> bool:
     """Shapes of the triangle-attention kernels: the fused AF3 trunk kernels (128, 4 x 32) or
-    the generic path (pair 64 / 128 / 256, at most 32 heads of 8 to 32 channels with
-    heads x d_head a multiple of 64); both take either bias orientation."""
+    the generic path (pair 64 / 128 / 256, at most 32 heads of 8 to 64 channels with
+    heads x d_head a multiple of 64: the template stacks' and Chai-1's 4 x 64 on pair 256);
+    both take either bias orientation and every output form."""
     if (d_pair, n_head, d_head) == (128, 4, 32):
         return True
-    return (d_pair in (64, 128, 256) and 0 < n_head <= 32 and 0 < d_head <= 32 and d_head % 8 == 0
+    return (d_pair in (64, 128, 256) and 0 < n_head <= 32 and 0 < d_head <= 64 and d_head % 8 == 0
             and (n_head * d_head) % 64 == 0)
 
 
@@ -202,10 +203,15 @@ def triangle_multiplicative_update(
     to_gate: Tensor,
     outgoing: bool,
     residual: bool = True,
+    length_divided: bool = False,
     eps: float = 1e-5,
     out: Tensor | None = None,
 ) -> Tensor:
-    """Triangle multiplication (outgoing / incoming) of ``z [B, N, N, c]`` bf16 under the key mask."""
+    """Triangle multiplication (outgoing / incoming) of ``z [B, N, N, c]`` bf16 under the key mask.
+
+    ``length_divided``: RoseTTAFold3's exact form, the contraction divided by the number of
+    positions real in any batch element before the centre norm
+    (``src/foldforge/models/checkpoints/legacy/routing.py:33-55``); the count stays on the device."""
     batch, n = _pair(z, mask, width=None)
     c = z.shape[3]
     dev = z.device
@@ -224,7 +230,7 @@ def triangle_multiplicative_update(
     status = lib.ffk_triangle_multiplication(
         z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
         ws.data_ptr(), ws.numel(), batch, n, c, hidden, int(outgoing), int(residual),
-        float(eps), _stream(dev),
+        int(length_divided), float(eps), _stream(dev),
     )
     _native.check(status, "triangle_multiplicative_update")
     return out
@@ -244,35 +250,49 @@ def triangle_attention(
     to_out: Tensor,
     n_head: int,
     starting: bool,
+    gate_bias: Tensor | None = None,
+    out_bias: Tensor | None = None,
+    to_out_t: Tensor | None = None,
+    out_t_bias: Tensor | None = None,
     transposed_bias: bool = False,
+    untransposed_output: bool = False,
     residual: bool = True,
     eps: float = 1e-5,
     out: Tensor | None = None,
 ) -> Tensor:
-    """Triangle attention around the starting / ending node of ``z [B, N, N, c]`` bf16."""
+    """Triangle attention around the starting / ending node of ``z [B, N, N, c]`` bf16.
+
+    ``gate_bias`` / ``out_bias``: RoseTTAFold3's projection biases. ``untransposed_output``:
+    Chai-1's trunk, the ending node's update not turned back. ``to_out_t`` (+ ``out_t_bias``):
+    Chai-1's confidence head, a second output projection added transposed over the pair axes."""
     batch, n = _pair(z, mask, width=None)
     c = z.shape[3]
     dev = z.device
     hd = to_query.shape[0]
     _need(n_head > 0 and hd % n_head == 0, f"hidden {hd} is not a multiple of {n_head} heads")
+    _need(out_t_bias is None or to_out_t is not None, "out_t_bias needs to_out_t")
     spec = (("ln_pair_weight", ln_pair_weight, (c,)), ("ln_pair_bias", ln_pair_bias, (c,)),
             ("to_bias", to_bias, (n_head, c)), ("to_query", to_query, (hd, c)),
             ("to_key", to_key, (hd, c)), ("to_value", to_value, (hd, c)),
             ("to_gate", to_gate, (hd, c)), ("to_out", to_out, (c, hd)))
     ps = [_param(t, dev, nm, shape) for nm, t, shape in spec]
+    extra = (("gate_bias", gate_bias, (hd,)), ("out_bias", out_bias, (c,)),
+             ("to_out_t", to_out_t, (c, hd)), ("out_t_bias", out_t_bias, (c,)))
+    opt = [None if t is None else _param(t, dev, nm, shape) for nm, t, shape in extra]
+    form = 2 if to_out_t is not None else 1 if untransposed_output else 0
     d = hd // n_head
     _need(triangle_attention_supported(c, n_head, d, transposed_bias),
           f"d_pair={c} heads={n_head} x {d} (the kernels take 128 with 4 x 32, or pair 64 / 128 / "
-          "256 with at most 32 heads of 8 to 32 channels, heads x d_head a multiple of 64)")
+          "256 with at most 32 heads of 8 to 64 channels, heads x d_head a multiple of 64)")
     if (c, n_head, d) != (128, 4, 32):
         _need(batch * n <= 65535, f"batch x n = {batch * n} exceeds the launch grid")
     out = _output(out, tuple(z.shape), torch.bfloat16, dev)
     lib = _native.lib()
-    ws = _workspace(lib.ffk_triangle_attention_workspace(batch, n, c, n_head, d), dev)
+    ws = _workspace(lib.ffk_triangle_attention_workspace(batch, n, c, n_head, d, form), dev)
     status = lib.ffk_triangle_attention(
-        z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
-        ws.data_ptr(), ws.numel(), batch, n, c, n_head, d, int(starting),
-        int(transposed_bias), int(residual), float(eps), _stream(dev),
+        z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), *(_ptr(t) for t in opt),
+        out.data_ptr(), ws.data_ptr(), ws.numel(), batch, n, c, n_head, d, int(starting),
+        int(transposed_bias), form, int(residual), float(eps), _stream(dev),
     )
     _native.check(status, "triangle_attention")
     return out

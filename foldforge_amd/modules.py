@@ -235,8 +235,6 @@ class TriangleMultiplication(EngineOp, MasterWeights, nn.Module):
         if x.shape[-1] != self.d_pair or not trimul_supported(self.d_pair, self.d_hidden):
             return (f"d_pair={x.shape[-1]} d_hidden={self.d_hidden} (the kernels take 128 / 128, or a "
                     "pair width a multiple of 64 up to 256 with a hidden width a multiple of 64 up to 768)")
-        if self.divide_by_length:
-            return "the length-divided (RF3) contraction is not in the hip kernels"
         return None
 
     def _forward_pytorch(self, x: Tensor, mask: Tensor, *, residual: bool = True) -> Tensor:
@@ -256,27 +254,35 @@ class TriangleMultiplication(EngineOp, MasterWeights, nn.Module):
             to_left_gate=self.to_left_gate.weight, to_right_gate=self.to_right_gate.weight,
             ln_out_weight=self.ln_out.weight, ln_out_bias=self.ln_out.bias,
             to_out=self.to_out.weight, to_gate=self.to_gate.weight,
-            outgoing=self.outgoing, residual=residual, eps=self.ln_pair.eps,
+            outgoing=self.outgoing, residual=residual, length_divided=self.divide_by_length,
+            eps=self.ln_pair.eps,
         )
 
 
 class TriangleMultiplicationRF3(TriangleMultiplication):
     """RoseTTAFold3's exact form: the contraction divided by the real length
-    (``legacy/routing.py:33-41``). Served by the pytorch backend only."""
+    (``legacy/routing.py:33-55``, ``legacy/reference/triangle.py:46-48``)."""
 
     divide_by_length = True
 
 
-#: ``TriangleAttention(model=...)`` key -> whether the ending node takes its bias from the
-#: transposed pair (the OpenFold lineage; ``src/foldforge/modules/dense/spec.py:116-125``).
-TRIANGLE_ATTENTION_MODELS: dict[str, bool] = {
-    "af3": False,
-    "openfold3": False,
-    "intellifold2": False,
-    "openfold3_preview2": True,
-    "protenix": True,
-    "boltz2": True,
-    "opendde": True,
+#: ``TriangleAttention(model=...)`` key -> the key's class. The lineages differ in four places
+#: (``src/foldforge/modules/dense/spec.py``): the ending node's bias from the transposed pair
+#: (the OpenFold lineage, ``:116-125``), gate and output projection biases (RoseTTAFold3,
+#: ``:437,645``), the ending node's update added without turning it back (Chai-1's trunk,
+#: ``:463-470,716``) and a second, transposed output projection (Chai-1's confidence head,
+#: ``:476-478,694``).
+TRIANGLE_ATTENTION_MODELS: dict[str, str] = {
+    "af3": "TriangleAttentionAF3",
+    "openfold3": "TriangleAttentionAF3",
+    "intellifold2": "TriangleAttentionAF3",
+    "openfold3_preview2": "TriangleAttentionOpenFold",
+    "protenix": "TriangleAttentionOpenFold",
+    "boltz2": "TriangleAttentionOpenFold",
+    "opendde": "TriangleAttentionOpenFold",
+    "rf3": "TriangleAttentionRF3",
+    "chai1": "TriangleAttentionChai1",
+    "chai1_confidence": "TriangleAttentionChai1Confidence",
 }
 
 
@@ -284,11 +290,16 @@ class TriangleAttention(EngineOp, MasterWeights, nn.Module):
     """Triangle attention around the starting / ending node, residual included
     (``legacy/attention.py:60-171``; parameters ``legacy/released.py:176-208``).
 
-    ``TriangleAttention(..., model=key)`` builds the key's class (``TriangleAttentionAF3`` or
-    ``TriangleAttentionOpenFold``). ``d_hidden`` is the total hidden width (default ``d_pair``).
+    ``TriangleAttention(..., model=key)`` builds the key's class (``TRIANGLE_ATTENTION_MODELS``).
+    ``d_hidden`` is the total hidden width (default ``d_pair``). The class attributes name the
+    lineage's form: ``transposed_bias``, ``projection_bias`` (``to_gate`` / ``to_out`` carry
+    biases), ``untransposed_output`` and ``dual_output`` (``to_out_t``).
     """
 
     transposed_bias = False
+    projection_bias = False
+    untransposed_output = False
+    dual_output = False
 
     def __new__(cls, *args: Any, **kwargs: Any):
         if cls is TriangleAttention:
@@ -298,7 +309,7 @@ class TriangleAttention(EngineOp, MasterWeights, nn.Module):
                     f"no triangle attention class for model {model!r} in this build "
                     f"(known: {', '.join(TRIANGLE_ATTENTION_MODELS)})"
                 )
-            cls = TriangleAttentionOpenFold if TRIANGLE_ATTENTION_MODELS[model] else TriangleAttentionAF3
+            cls = globals()[TRIANGLE_ATTENTION_MODELS[model]]
         return super().__new__(cls)
 
     def __init__(self, d_pair: int, n_head: int, d_hidden: int | None = None,
@@ -313,8 +324,10 @@ class TriangleAttention(EngineOp, MasterWeights, nn.Module):
         self.to_query = _linear(d_pair, hidden)
         self.to_key = _linear(d_pair, hidden)
         self.to_value = _linear(d_pair, hidden)
-        self.to_gate = _linear(d_pair, hidden)
-        self.to_out = _linear(hidden, d_pair)
+        self.to_gate = _linear(d_pair, hidden, bias=self.projection_bias)
+        self.to_out = _linear(hidden, d_pair, bias=self.projection_bias)
+        if self.dual_output:
+            self.to_out_t = _linear(hidden, d_pair, bias=self.projection_bias)
         self._init_backend(backend)
 
     def _unsupported_hip(self, x: Tensor, mask: Tensor) -> str | None:
@@ -327,7 +340,7 @@ class TriangleAttention(EngineOp, MasterWeights, nn.Module):
         if (x.shape[-1] != self.d_pair or self.d_hidden % self.n_head
                 or not triangle_attention_supported(self.d_pair, self.n_head, d, self.transposed_bias)):
             return (f"d_pair={x.shape[-1]} heads={self.n_head} hidden={self.d_hidden} (the kernels "
-                    "take 128 with 4 x 32, or pair 64 / 128 / 256 with at most 32 heads of 8 to 32 "
+                    "take 128 with 4 x 32, or pair 64 / 128 / 256 with at most 32 heads of 8 to 64 "
                     "channels, heads x d_head a multiple of 64)")
         if (self.d_pair, self.n_head, d) != (128, 4, 32) and x.shape[0] * x.shape[1] > 65535:
             return f"batch x n = {x.shape[0] * x.shape[1]} exceeds the launch grid"
@@ -349,8 +362,11 @@ class TriangleAttention(EngineOp, MasterWeights, nn.Module):
             to_bias=self.to_bias.weight, to_query=self.to_query.weight,
             to_key=self.to_key.weight, to_value=self.to_value.weight,
             to_gate=self.to_gate.weight, to_out=self.to_out.weight, n_head=self.n_head,
+            gate_bias=self.to_gate.bias, out_bias=self.to_out.bias,
+            to_out_t=self.to_out_t.weight if self.dual_output else None,
+            out_t_bias=self.to_out_t.bias if self.dual_output else None,
             starting=self.starting, transposed_bias=self.transposed_bias,
-            residual=residual, eps=self.ln_pair.eps,
+            untransposed_output=self.untransposed_output, residual=residual, eps=self.ln_pair.eps,
         )
 
 
@@ -364,6 +380,28 @@ class TriangleAttentionOpenFold(TriangleAttention):
     """OpenFold lineage: the ending node's bias comes from the transposed pair."""
 
     transposed_bias = True
+
+
+class TriangleAttentionRF3(TriangleAttentionAF3):
+    """RoseTTAFold3: AF3's form with biases on the gate and output projections
+    (``legacy/attention.py:97-102`` with ``spec.triangle_attention_bias``)."""
+
+    projection_bias = True
+
+
+class TriangleAttentionChai1(TriangleAttentionAF3):
+    """Chai-1's trunk: the ending node's update is added in the attention's own orientation,
+    not turned back (``legacy/attention.py:84-88,160-163``)."""
+
+    untransposed_output = True
+
+
+class TriangleAttentionChai1Confidence(TriangleAttentionAF3):
+    """Chai-1's confidence head: a second output projection ``to_out_t`` of the same gated
+    values, added transposed over the pair axes (``legacy/attention.py:103-106,129-131,152-158``;
+    released ``output_projection_transposed``)."""
+
+    dual_output = True
 
 
 class Transition(EngineOp, MasterWeights, nn.Module):

@@ -123,14 +123,18 @@ _TRIATTN_NAMES = (("to_bias", "pair_bias_projection"), ("to_query", "q_projectio
 
 def triangle_attention_from_released(state: State, *, prefix: str = "") -> dict[str, Tensor]:
     """Released grid self-attention ``act_norm pair_bias_projection q/k/v_projection
-    gating_query output_projection`` (``legacy/attention.py:89-103``) -> engine
-    ``TriangleAttention`` (a rename; gate / output biases carried when present)."""
+    gating_query output_projection [output_projection_transposed]``
+    (``legacy/attention.py:89-106``) -> engine ``TriangleAttention`` (a rename; gate / output
+    biases carried when present, RoseTTAFold3's; Chai-1's confidence head's second output
+    projection becomes ``to_out_t``)."""
     s = _below(state, prefix)
     _require(s, *(f"{key}.weight" for _, key in _TRIATTN_NAMES))
     out: dict[str, Tensor] = {}
     _copy_norm(out, "ln_pair", s, "act_norm")
     for name, key in _TRIATTN_NAMES:
         _copy_linear(out, name, s, key)
+    if "output_projection_transposed.weight" in s:
+        _copy_linear(out, "to_out_t", s, "output_projection_transposed")
     return out
 
 

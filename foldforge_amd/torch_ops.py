@@ -88,9 +88,15 @@ def triangle_attention(m, x: Tensor, mask: Tensor, *, residual: bool = True,
             o[b, r0 : r0 + rows] = att.permute(0, 2, 1, 3).reshape(rows, n, hd)
     empty = ~keep.any(dim=-1)
     o = torch.where(empty[:, None, None, None], torch.zeros_like(o), o)
-    y = _lin(torch.sigmoid(_lin(h, m.to_gate.weight)) * o, m.to_out.weight)
-    if not m.starting:
+    gated = torch.sigmoid(_lin(h, m.to_gate.weight, m.to_gate.bias)) * o
+    y = _lin(gated, m.to_out.weight, m.to_out.bias)
+    if not m.starting and (m.dual_output or not m.untransposed_output):
         y = y.transpose(1, 2)
+    if m.dual_output:
+        other = _lin(gated, m.to_out_t.weight, m.to_out_t.bias)
+        if not m.starting:
+            other = other.transpose(1, 2)
+        y = y + other.transpose(1, 2)
     return (z + y if residual else y).to(dtype)
 
 

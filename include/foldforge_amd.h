@@ -97,11 +97,14 @@ int32_t ffk_swiglu_ffn(const void* x, const float* w_a, const float* w_b, const 
  * the LayerNorm + gated projections prologue and the centre norm + output projection +
  * output gate epilogue. d_pair = d_hidden = 128 runs the fused kernels; other widths (d_pair
  * a multiple of 64 up to 256, d_hidden a multiple of 64 up to 768: the template stack's)
- * run the generic path with a larger workspace.
+ * run the generic path with a larger workspace. length_divided = 1 is RoseTTAFold3's exact
+ * form: the contraction divided by the real length L (positions real in any batch element,
+ * counted on the device from key_mask) before the centre norm.
  * Replaces: engine TriangleMultiplication.forward / `triangle_multiplicative_update`
  * (equations src/foldforge/models/checkpoints/legacy/reference/triangle.py:19-49,
  * engine parameters legacy/released.py:135-173; op name "trimul",
- * src/foldforge/modules/engine/backends.py:36-40).
+ * src/foldforge/modules/engine/backends.py:36-40) and, with length_divided,
+ * TriangleMultiplicationRF3 (legacy/routing.py:33-55).
  */
 size_t ffk_triangle_multiplication_workspace(int64_t batch, int64_t n, int32_t d_pair,
                                              int32_t d_hidden);
@@ -111,29 +114,37 @@ int32_t ffk_triangle_multiplication(
     const float* w_right_gate, const float* ln_out_w, const float* ln_out_b,
     const float* w_out, const float* w_gate, void* out, void* workspace,
     size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_pair, int32_t d_hidden,
-    int32_t outgoing, int32_t residual, float eps, void* stream);
+    int32_t outgoing, int32_t residual, int32_t length_divided, float eps, void* stream);
 
 /*
  * Triangle attention around the starting (starting = 1) or ending (0) node: LayerNorm,
  * pair bias, q/k/v/gate projections, flash attention with key mask, gate, output
  * projection. d_pair = 128 with 4 heads x 32 runs the fused kernels; d_pair 64 / 128 / 256
- * with at most 32 heads of 8 to 32 channels (n_head * d_head a multiple of 64, batch * n at
+ * with at most 32 heads of 8 to 64 channels (n_head * d_head a multiple of 64, batch * n at
  * most 65535) runs the generic path. transposed_bias = 1 takes the ending node's bias from
- * the transposed pair (OpenFold lineage).
- * Replaces: engine TriangleAttention(AF3).forward / `triangle_attention`
- * (src/foldforge/models/checkpoints/legacy/attention.py:108-163,
- * legacy/reference/attention.py:77-100; engine parameters legacy/released.py:176-208;
- * op name "triangle_attention", src/foldforge/modules/engine/backends.py:41-47).
+ * the transposed pair (OpenFold lineage). b_gate [n_head * d_head] and b_out [d_pair] are the
+ * gate / output projection biases (RoseTTAFold3; NULL: none). output_form: 0 the z-frame
+ * update (AF3 and its descendants); 1 the ending node's update left in the attention's
+ * orientation (Chai-1's trunk; the starting node is unchanged); 2 the update plus the
+ * transpose over the pair axes of a second projection w_out_t [d_pair, n_head * d_head]
+ * (+ b_out_t) of the same gated values (Chai-1's confidence head; w_out_t is required by, and
+ * only by, this form). The workspace depends on the form.
+ * Replaces: engine TriangleAttention(AF3 / OpenFold / RF3 / Chai1 / Chai1Confidence).forward
+ * / `triangle_attention` (src/foldforge/models/checkpoints/legacy/attention.py:60-171,
+ * legacy/reference/attention.py:77-100; forms src/foldforge/modules/dense/spec.py:116-125,
+ * 437, 463-478; engine parameters legacy/released.py:176-208; op name "triangle_attention",
+ * src/foldforge/modules/engine/backends.py:41-47).
  */
 size_t ffk_triangle_attention_workspace(int64_t batch, int64_t n, int32_t d_pair,
-                                        int32_t n_head, int32_t d_head);
+                                        int32_t n_head, int32_t d_head, int32_t output_form);
 int32_t ffk_triangle_attention(
     const void* z, const uint8_t* key_mask, const float* ln_pair_w, const float* ln_pair_b,
     const float* w_bias, const float* w_query, const float* w_key, const float* w_value,
-    const float* w_gate, const float* w_out, void* out, void* workspace,
+    const float* w_gate, const float* w_out, const float* b_gate, const float* b_out,
+    const float* w_out_t, const float* b_out_t, void* out, void* workspace,
     size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_pair, int32_t n_head,
-    int32_t d_head, int32_t starting, int32_t transposed_bias, int32_t residual, float eps,
-    void* stream);
+    int32_t d_head, int32_t starting, int32_t transposed_bias, int32_t output_form,
+    int32_t residual, float eps, void* stream);
 
 /*
  * Flash attention core with an additive pair bias, the building block of triangle

@@ -53,11 +53,19 @@ def _softmax_row(logits: list[float]) -> list[float]:
     return [v / s for v in e]
 
 
-def triangle_multiplication(z, mask, p, *, outgoing: bool, eps: float = 1e-5):
-    """``z [B, N, N, c]`` fp64, ``mask [B, N]``; ``p`` numpy fp64 params (engine names)."""
+def triangle_multiplication(z, mask, p, *, outgoing: bool, length_divided: bool = False,
+                            eps: float = 1e-5):
+    """``z [B, N, N, c]`` fp64, ``mask [B, N]``; ``p`` numpy fp64 params (engine names).
+    ``length_divided``: every contraction sum divided by the count of columns j with a real
+    token in some batch element (at least 1)."""
     batch, n, _, c = z.shape
     hid = p["to_left.weight"].shape[0]
     out = np.array(z, dtype=np.float64, copy=True)
+    length = 0
+    for j in range(n):
+        if any(bool(mask[b, j]) for b in range(batch)):
+            length += 1
+    divisor = float(max(length, 1)) if length_divided else 1.0
     for b in range(batch):
         xh = [[layer_norm_vec(z[b, i, j], p["ln_pair.weight"], p["ln_pair.bias"], eps)
                for j in range(n)] for i in range(n)]
@@ -83,7 +91,7 @@ def triangle_multiplication(z, mask, p, *, outgoing: bool, eps: float = 1e-5):
                             acc += a[i][k][h] * bb[j][k][h]
                         else:
                             acc += a[k][i][h] * bb[k][j][h]
-                    pv[h] = acc
+                    pv[h] = acc / divisor
                 y = _matvec(p["to_out.weight"],
                             layer_norm_vec(pv, p["ln_out.weight"], p["ln_out.bias"], eps))
                 g = _matvec(p["to_gate.weight"], xh[i][j])
@@ -93,8 +101,12 @@ def triangle_multiplication(z, mask, p, *, outgoing: bool, eps: float = 1e-5):
 
 
 def triangle_attention(z, mask, p, *, starting: bool, n_head: int,
-                       transposed_bias: bool = False, eps: float = 1e-5):
-    """Row (starting) or column (ending) attention with the shared pair bias, fp64 loops."""
+                       transposed_bias: bool = False, untransposed_output: bool = False,
+                       dual_output: bool = False, eps: float = 1e-5):
+    """Row (starting) or column (ending) attention with the shared pair bias, fp64 loops.
+    Gate / output biases where ``p`` holds them; ``untransposed_output``: the ending node's
+    update lands at (row, query), not (query, row); ``dual_output``: ``to_out_t`` of the same
+    gated values lands at the mirror of the update's position."""
     batch, n, _, c = z.shape
     hd = p["to_query.weight"].shape[0]
     d = hd // n_head
@@ -128,11 +140,19 @@ def triangle_attention(z, mask, p, *, starting: bool, n_head: int,
                     w = _softmax_row(logits)
                     for e in range(d):
                         o[h * d + e] = sum(w[k] * vv[k][h * d + e] for k in range(n)) if any_key else 0.0
-                gated = [_sigmoid(gg[j][f]) * o[f] for f in range(hd)]
+                gb = p.get("to_gate.bias")
+                gated = [_sigmoid(gg[j][f] + (gb[f] if gb is not None else 0.0)) * o[f]
+                         for f in range(hd)]
                 y = _matvec(p["to_out.weight"], gated)
-                zi, zj = (r, j) if starting else (j, r)
+                if p.get("to_out.bias") is not None:
+                    y = [y[ch] + p["to_out.bias"][ch] for ch in range(c)]
+                zi, zj = (r, j) if starting or (untransposed_output and not dual_output) else (j, r)
                 for ch in range(c):
-                    out[b, zi, zj, ch] = z[b, zi, zj, ch] + y[ch]
+                    out[b, zi, zj, ch] += y[ch]
+                if dual_output:
+                    yt = _matvec(p["to_out_t.weight"], gated)
+                    for ch in range(c):
+                        out[b, zj, zi, ch] += yt[ch] + (p["to_out_t.bias"][ch] if p.get("to_out_t.bias") is not None else 0.0)
     return out
 
 

@@ -128,6 +128,7 @@ def triangle_multiplication(
     params: Params,
     *,
     outgoing: bool,
+    length_divided: bool = False,
     eps: float = 1e-5,
     dtype: torch.dtype = torch.float32,
 ) -> Tensor:
@@ -137,6 +138,9 @@ def triangle_multiplication(
     weights, ``M[i, k] = mask_i mask_k``; outgoing ``P[i, j] = sum_k A[i, k] B[j, k]``,
     incoming ``P[i, j] = sum_k A[k, i] B[k, j]``
     (``legacy/reference/triangle.py:39-49``, ``legacy/released.py:143-145``).
+    ``length_divided`` (RoseTTAFold3's exact form): ``P`` divided by the real length ``L``
+    before the centre norm, ``L`` the number of positions real in any batch element, at
+    least 1 (``legacy/routing.py:33-55``, ``legacy/reference/triangle.py:46-48``).
     """
     z = z.detach().to("cpu", dtype)
     x = layer_norm(
@@ -154,6 +158,8 @@ def triangle_multiplication(
     else:
         p = a.transpose(-1, -2) @ b
     p = p.permute(0, 2, 3, 1)
+    if length_divided:
+        p = p / max(1, int(mask.to("cpu").bool().any(dim=0).sum()))
     y = layer_norm(
         p, _p(params, "ln_out.weight", dtype), _p(params, "ln_out.bias", dtype), eps
     )
@@ -183,6 +189,8 @@ def triangle_attention(
     starting: bool,
     n_head: int,
     transposed_bias: bool = False,
+    untransposed_output: bool = False,
+    dual_output: bool = False,
     eps: float = 1e-5,
     dtype: torch.dtype = torch.float32,
     row_chunk: int | None = None,
@@ -193,8 +201,13 @@ def triangle_attention(
     ``x`` (AF3) or its transpose (``transposed_bias``, the ending node of the
     OpenFold lineage); for every row ``r`` of ``x`` (of ``x^T`` when ending):
     ``o[r, j] = softmax_k(q[r, j] . k[r, k] / sqrt(D) + bias[h, j, k]) v[r, k]``;
-    ``out = (sigmoid(x W_g^T) * o) W_out^T``, turned back when ending
-    (``legacy/attention.py:108-163``).
+    ``y = (sigmoid(x W_g^T + b_g) * o) W_out^T + b_out`` (the biases where ``params`` holds
+    them: RoseTTAFold3, ``legacy/attention.py:97-102``), turned back when ending
+    (``legacy/attention.py:108-163``). ``untransposed_output`` (Chai-1's trunk): the ending
+    node's ``y`` is added as it stands, not turned back (``attention.py:84-88,160-163``).
+    ``dual_output`` (Chai-1's confidence head): a second projection ``to_out_t`` of the same
+    gated ``o``, turned back like ``y`` and then transposed over the pair axes, is added too
+    (``attention.py:129-131,152-158``).
     """
     z = z.detach().to("cpu", dtype)
     batch, n = z.shape[0], z.shape[1]
@@ -230,10 +243,19 @@ def triangle_attention(
             if not bool(key_mask[b].any()):
                 o = torch.zeros_like(o)
             out[b, r0 : r0 + rows] = o
-    gate = torch.sigmoid(x @ _p(params, "to_gate.weight", dtype).T)
-    y = (gate * out) @ _p(params, "to_out.weight", dtype).T
-    if not starting:
+    def linear(v: Tensor, name: str) -> Tensor:
+        y = v @ _p(params, f"{name}.weight", dtype).T
+        return y + _p(params, f"{name}.bias", dtype) if f"{name}.bias" in params else y
+
+    gated = torch.sigmoid(linear(x, "to_gate")) * out
+    y = linear(gated, "to_out")
+    if not starting and (dual_output or not untransposed_output):
         y = y.transpose(1, 2)
+    if dual_output:
+        other = linear(gated, "to_out_t")
+        if not starting:
+            other = other.transpose(1, 2)
+        y = y + other.transpose(1, 2)
     return z + y
 
 

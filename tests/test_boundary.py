@@ -26,7 +26,10 @@ from foldforge_amd.modules import (
     Transition,
     TriangleAttention,
     TriangleAttentionAF3,
+    TriangleAttentionChai1,
+    TriangleAttentionChai1Confidence,
     TriangleAttentionOpenFold,
+    TriangleAttentionRF3,
     TriangleMultiplication,
     TriangleMultiplicationRF3,
 )
@@ -241,10 +244,53 @@ def test_factories_precision_and_model_keys():
     assert type(factories.triangle_multiplication(32, outgoing=True, divide_by_length=True)) is TriangleMultiplicationRF3
     assert factories.triangle_multiplication(64, outgoing=False, d_hidden=128).to_left.weight.shape == (128, 64)
     with pytest.raises(ValueError, match="no triangle attention class"):
-        TriangleAttention(32, 4, model="chai1")
+        TriangleAttention(32, 4, model="chai2")
     assert factories.model_keys("alphafold3").triangle == "af3"
     with pytest.raises(ValueError, match="no engine selector keys"):
         factories.model_keys("nope")
+
+
+def test_triangle_attention_classes_follow_the_model_keys():
+    """The reference's class per key (tests/kernels/test_engine_factories.py:75-90) and each
+    lineage's parameters: RF3's projection biases, Chai-1 confidence's to_out_t."""
+    cases = {"af3": TriangleAttentionAF3, "rf3": TriangleAttentionRF3,
+             "chai1": TriangleAttentionChai1, "chai1_confidence": TriangleAttentionChai1Confidence}
+    for key, cls in cases.items():
+        m = factories.triangle_attention(32, 4, starting=key != "rf3", model=key)
+        assert type(m) is cls
+        assert (m.to_gate.bias is not None) == (key == "rf3")
+        assert (m.to_out.bias is not None) == (key == "rf3")
+        assert hasattr(m, "to_out_t") == (key == "chai1_confidence")
+    fast = factories.pairformer_block(d_pair=32, triangle_model="rf3", parallel=True)
+    assert type(fast.tri_atten_starting) is TriangleAttentionRF3
+    assert type(fast.tri_multi_outgoing) is TriangleMultiplication
+    exact = factories.pairformer_block(d_pair=32, triangle_model="rf3", parallel=True,
+                                       divide_by_length=True)
+    assert type(exact.tri_multi_outgoing) is TriangleMultiplicationRF3
+    conf = factories.pairformer_block(d_pair=32, triangle_model="chai1_confidence", d_single=64,
+                                      n_head_single=4, single_gate_bias=1.0, parallel=True)
+    assert type(conf.tri_atten_starting) is TriangleAttentionChai1Confidence
+    assert conf.single_attention.gate_bias == 1.0
+
+
+@pytest.mark.parametrize("key", ["rf3", "chai1", "chai1_confidence"])
+@pytest.mark.parametrize("starting", [True, False])
+def test_triangle_attention_lineage_forms_match_the_oracle(key, starting):
+    """The pytorch backend's RF3 / Chai-1 forms against the fp64 oracle (pinned by loops)."""
+    m = randomise(factories.triangle_attention(16, 2, starting=starting, model=key), seed=3)
+    if key == "rf3":
+        with torch.no_grad():
+            m.to_gate.bias.normal_(0, 0.5)
+            m.to_out.bias.normal_(0, 0.5)
+    g = torch.Generator().manual_seed(4)
+    z = torch.randn(2, 9, 9, 16, generator=g)
+    mask = torch.ones(2, 9, dtype=torch.bool)
+    mask[1, 6:] = False
+    got = m.delta(z, mask)
+    want = ps.triangle_attention(z, mask, m.state_dict(), starting=starting, n_head=2,
+                                 untransposed_output=m.untransposed_output,
+                                 dual_output=m.dual_output, dtype=torch.float64) - z.double()
+    torch.testing.assert_close(got.double(), want, rtol=1e-4, atol=1e-4)
 
 
 def test_master_flag_reaches_every_mixin_below():

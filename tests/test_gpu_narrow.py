@@ -69,6 +69,22 @@ def test_trimul_generic_widths_match_oracle(outgoing, c, h, n, lengths):
     torch.testing.assert_close(full.float(), z.float() + got.float(), atol=3e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_length_divided_trimul_generic_width_matches_oracle(outgoing):
+    """TriangleMultiplicationRF3 at a generic width: the device length (70 of 96) feeds the
+    centre norm of the token-row output GEMM."""
+    n, c, h = 96, 64, 128
+    z, mask = _pair(n, c, [70, 52], seed=31)
+    m = randomise(factories.triangle_multiplication(c, outgoing=outgoing, d_hidden=h,
+                                                    divide_by_length=True), seed=32).cuda()
+    m.set_backend("hip")
+    assert m.unsupported(z.cuda(), mask.cuda()) is None
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
+    want = ps.triangle_multiplication(z, mask, m.state_dict(), outgoing=outgoing, length_divided=True,
+                                      dtype=torch.float64) - z.double()
+    _check(got, want, _pairs(mask), f"trimul RF3 c={c} h={h} outgoing={outgoing}")
+
+
 def test_trimul_generic_width_256_tile_contraction():
     """A padded width of 256: the contraction takes its 256 x 256 tiles."""
     n, c, h = 230, 64, 64
@@ -78,6 +94,44 @@ def test_trimul_generic_width_256_tile_contraction():
     got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
     want = ps.triangle_multiplication(z, mask, m.state_dict(), outgoing=False, dtype=torch.float64) - z.double()
     _check(got, want, _pairs(mask), "trimul c=64 h=64 incoming n=230")
+
+
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("key", ["rf3", "chai1", "chai1_confidence"])
+def test_triattn_lineage_forms_generic_width_match_oracle(starting, key):
+    """The RoseTTAFold3 and Chai-1 forms on the generic path (pair 64, 4 x 16)."""
+    from tests.test_gpu_ops import _lineage_module, _lineage_oracle
+
+    n, c = 75, 64
+    z, mask = _pair(n, c, [75, 52], seed=41)
+    m = _lineage_module(key, c, 4, 16, starting, seed=6)
+    m.set_backend("hip")
+    assert m.unsupported(z.cuda(), mask.cuda()) is None
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
+    where = _pairs(mask)
+    if key.startswith("chai1"):
+        where = where & where.transpose(1, 2)
+    _check(got, _lineage_oracle(m, z, mask), where, f"triattn {key} c={c} starting={starting}")
+
+
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("key,c,heads,d", [("chai1", 256, 4, 64), ("chai1_confidence", 256, 4, 64),
+                                           ("af3", 128, 4, 48)])
+def test_triattn_wide_heads_match_oracle(starting, key, c, heads, d):
+    """Heads wider than 32 channels (two 32-channel output tiles per head): Chai-1's trunk and
+    confidence shapes (pair 256, 4 x 64) and a 48-channel head (a partial second tile)."""
+    from tests.test_gpu_ops import _lineage_module, _lineage_oracle
+
+    n = 44
+    z, mask = _pair(n, c, [44, 30], seed=c + d)
+    m = _lineage_module(key, c, heads, d, starting, seed=7)
+    m.set_backend("hip")
+    assert m.unsupported(z.cuda(), mask.cuda()) is None
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
+    where = _pairs(mask)
+    if key.startswith("chai1"):
+        where = where & where.transpose(1, 2)
+    _check(got, _lineage_oracle(m, z, mask), where, f"triattn {key} {heads}x{d} c={c} starting={starting}")
 
 
 @pytest.mark.parametrize("starting", [True, False])

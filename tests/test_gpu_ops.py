@@ -97,6 +97,59 @@ def test_trimul_matches_oracle(outgoing, n, lengths):
     torch.testing.assert_close(full.float(), (z.float() + got.float()), atol=3e-2, rtol=1e-2)
 
 
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("n,lengths", [(64, None), (100, [77, 61])])
+def test_length_divided_trimul_matches_oracle(outgoing, n, lengths):
+    """RoseTTAFold3's exact triangle multiplication (TriangleMultiplicationRF3) on hip: the real
+    length (77 of 100 in the ragged case: the longest element) is counted on the device."""
+    batch = len(lengths) if lengths else 1
+    z, mask = _pair(n, batch, seed=3 * n, lengths=lengths)
+    m = randomise(factories.triangle_multiplication(128, outgoing=outgoing, divide_by_length=True),
+                  seed=n + 1).cuda()
+    assert m.divide_by_length
+    m.set_backend("hip")
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
+    want = ps.triangle_multiplication(z, mask, m.state_dict(), outgoing=outgoing, length_divided=True,
+                                      dtype=torch.float64) - z.double()
+    _check(got, want, _pairs(mask), f"trimul RF3 outgoing={outgoing} n={n}")
+
+
+def _lineage_oracle(m, z, mask):
+    return ps.triangle_attention(z, mask, m.state_dict(), starting=m.starting, n_head=m.n_head,
+                                 transposed_bias=m.transposed_bias,
+                                 untransposed_output=m.untransposed_output,
+                                 dual_output=m.dual_output, dtype=torch.float64) - z.double()
+
+
+def _lineage_module(key: str, c: int, heads: int, d: int, starting: bool, seed: int):
+    m = randomise(factories.triangle_attention(c, heads, starting=starting, model=key,
+                                               d_hidden=heads * d), seed=seed)
+    if m.projection_bias:
+        g = torch.Generator().manual_seed(seed)
+        with torch.no_grad():
+            m.to_gate.bias.copy_(torch.randn(m.to_gate.bias.shape, generator=g))
+            m.to_out.bias.copy_(0.3 * torch.randn(m.to_out.bias.shape, generator=g))
+    return m.cuda()
+
+
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("key", ["rf3", "chai1", "chai1_confidence"])
+def test_triattn_lineage_forms_match_oracle(starting, key):
+    """RoseTTAFold3's projection biases and Chai-1's untransposed / dual outputs on the fused
+    kernels, ragged batch of 2 (each output out of place and in place)."""
+    n, lengths = 100, [100, 61]
+    z, mask = _pair(n, 2, seed=11 * n, lengths=lengths)
+    m = _lineage_module(key, 128, 4, 32, starting, seed=5)
+    m.set_backend("hip")
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
+    where = _pairs(mask)
+    if key.startswith("chai1"):  # the transposed parts reach every pair with a real mirror
+        where = where & where.transpose(1, 2)
+    _check(got, _lineage_oracle(m, z, mask), where, f"triattn {key} starting={starting}")
+    full = hip_forward(m, z.cuda(), mask.cuda()).cpu()
+    torch.testing.assert_close(full.float(), z.float() + got.float(), atol=3e-2, rtol=1e-2)
+
+
 @pytest.mark.parametrize("starting", [True, False])
 @pytest.mark.parametrize("model", ["af3", "protenix"])
 @pytest.mark.parametrize("n,lengths", [(64, None), (100, [61]), (160, [160, 129])])

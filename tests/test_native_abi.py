@@ -52,11 +52,17 @@ def test_workspace_sizes_follow_the_layouts(lib):
     np_ = 384
     tm = lib.ffk_triangle_multiplication_workspace(b, n, 128, 128)
     weights = up(4 * 128 * 128 * 2) + up(128 * 128 * 2) + up(128 * 128 * 2)
-    assert tm == weights + 3 * up(b * 128 * np_ * np_ * 2) + up(b * np_ * 4) + up(b * 4)
-    ta = lib.ffk_triangle_attention_workspace(b, n, 128, 4, 32)
+    # one float: the centre norm's epsilon of a length-divided call
+    assert tm == up(4) + weights + 3 * up(b * 128 * np_ * np_ * 2) + up(b * np_ * 4) + up(b * 4)
+    ta = lib.ffk_triangle_attention_workspace(b, n, 128, 4, 32, 0)
     weights = up(3 * 128 * 128 * 2) + up(32 * 128 * 2) + 2 * up(128 * 128 * 2)
     qkv = 3 * up(b * 4 * np_ * np_ * 32 * 2)
     assert ta == weights + qkv + up(b * 4 * np_ * np_ * 4) + up(b * n * n * 128 * 2) + up(b * np_ * 4) + up(b * 4)
+    # the untransposed form stages one update; the dual form also packs its second projection
+    update = up(b * n * n * 128 * 2)
+    assert lib.ffk_triangle_attention_workspace(b, n, 128, 4, 32, 1) == ta + update
+    assert lib.ffk_triangle_attention_workspace(b, n, 128, 4, 32, 2) == ta + update + up(128 * 128 * 2)
+    assert lib.ffk_triangle_attention_workspace(b, n, 128, 4, 32, 3) == 0
     assert lib.ffk_transition_workspace(1000, 128, 4) == 3 * up(4 * 128 * 128 * 2)
     assert lib.ffk_transition_workspace(700, 384, 4) == up(700 * 1536 * 4)
     np32 = 320

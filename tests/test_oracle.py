@@ -127,6 +127,47 @@ def test_trimul_matches_brute_force(outgoing):
     np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
 
 
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_length_divided_trimul_matches_brute_force(outgoing):
+    """RoseTTAFold3's exact form: the length is the count of columns real in ANY batch element
+    (here 6 of 7: column 6 is padding in both elements, column 5 only in the second)."""
+    n, c, h = 7, 5, 3
+    p = _rand_params(_tm_shapes(c, h), 13)
+    g = torch.Generator().manual_seed(14)
+    z = torch.randn(2, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(2, n, dtype=torch.bool)
+    mask[0, 5:] = False
+    mask[1, 6] = False
+    got = ps.triangle_multiplication(z, mask, p, outgoing=outgoing, length_divided=True, dtype=F64)
+    want = brute.triangle_multiplication(z.numpy(), mask.numpy(), _np(p), outgoing=outgoing,
+                                         length_divided=True)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+    plain = ps.triangle_multiplication(z, mask, p, outgoing=outgoing, dtype=F64)
+    assert (got - plain).abs().max() > 1e-3  # the division changes the centre norm's eps share
+
+
+def test_length_divided_trimul_is_the_centre_norm_with_eps_times_length_squared():
+    """LN(P / L; eps) = LN(P; eps L^2): the identity the kernels use to keep P undivided."""
+    n, c, h, eps = 6, 4, 3, 1e-2
+    p = _rand_params(_tm_shapes(c, h), 15)
+    g = torch.Generator().manual_seed(16)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(1, n, dtype=torch.bool)
+    mask[0, -1] = False  # L = 5
+    divided = ps.triangle_multiplication(z, mask, p, outgoing=True, length_divided=True, eps=eps,
+                                         dtype=F64)
+    # the same op with the centre norm's eps scaled by L^2 and no division: split the two
+    # norms by running the pair norm at eps and the centre norm at eps * 25 by hand
+    x = ps.layer_norm(z, p["ln_pair.weight"], p["ln_pair.bias"], eps)
+    pm = (mask[:, :, None] & mask[:, None, :]).to(F64)[..., None]
+    a = (x @ p["to_left.weight"].T) * pm * torch.sigmoid(x @ p["to_left_gate.weight"].T)
+    b = (x @ p["to_right.weight"].T) * pm * torch.sigmoid(x @ p["to_right_gate.weight"].T)
+    pr = torch.einsum("bikc,bjkc->bijc", a, b)
+    y = ps.layer_norm(pr, p["ln_out.weight"], p["ln_out.bias"], eps * 25) @ p["to_out.weight"].T
+    want = z + y * torch.sigmoid(x @ p["to_gate.weight"].T)
+    torch.testing.assert_close(divided, want, rtol=1e-12, atol=1e-12)
+
+
 def test_trimul_outgoing_is_incoming_on_the_transpose_with_branches_swapped():
     n, c, h = 7, 6, 4
     p = _rand_params(_tm_shapes(c, h), 21)
@@ -158,6 +199,57 @@ def test_trimul_masked_tokens_contribute_nothing():
 
 
 # ----------------------------------------------------------------------------- triangle attention
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("form", ["rf3", "chai1", "chai1_confidence", "chai1_confidence_biased"])
+def test_triattn_forms_match_brute_force(starting, form):
+    """The RoseTTAFold3 (gate / output biases) and Chai-1 (untransposed ending output; dual
+    output projections) forms against independent loops."""
+    n, c, heads, d = 5, 4, 2, 3
+    shapes = _ta_shapes(c, heads, d)
+    if form in ("rf3", "chai1_confidence_biased"):
+        shapes.update({"to_gate.bias": (heads * d,), "to_out.bias": (c,)})
+    if form.startswith("chai1_confidence"):
+        shapes["to_out_t.weight"] = (c, heads * d)
+        if form.endswith("biased"):
+            shapes["to_out_t.bias"] = (c,)
+    p = _rand_params(shapes, 43)
+    g = torch.Generator().manual_seed(44)
+    z = torch.randn(2, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(2, n, dtype=torch.bool)
+    mask[0, 3:] = False
+    kw = dict(untransposed_output=form == "chai1", dual_output=form.startswith("chai1_confidence"))
+    got = ps.triangle_attention(z, mask, p, starting=starting, n_head=heads, dtype=F64, **kw)
+    want = brute.triangle_attention(z.numpy(), mask.numpy(), _np(p), starting=starting,
+                                    n_head=heads, **kw)
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+
+
+def test_triattn_chai1_forms_reduce_to_the_plain_update():
+    """Closed forms: the untransposed ending update is the plain ending update transposed;
+    the dual output with a zero second projection is the plain update; with the second
+    projection equal to the first it adds the update's own mirror."""
+    n, c, heads, d = 6, 4, 2, 2
+    p = _rand_params(_ta_shapes(c, heads, d), 45)
+    g = torch.Generator().manual_seed(46)
+    z = torch.randn(1, n, n, c, generator=g, dtype=F64)
+    mask = torch.ones(1, n, dtype=torch.bool)
+    mask[0, -2:] = False
+    for starting in (True, False):
+        plain = ps.triangle_attention(z, mask, p, starting=starting, n_head=heads, dtype=F64) - z
+        if not starting:
+            untr = ps.triangle_attention(z, mask, p, starting=False, n_head=heads,
+                                         untransposed_output=True, dtype=F64) - z
+            torch.testing.assert_close(untr, plain.transpose(1, 2), rtol=1e-12, atol=1e-12)
+        q = dict(p, **{"to_out_t.weight": torch.zeros(c, heads * d, dtype=F64)})
+        dual0 = ps.triangle_attention(z, mask, q, starting=starting, n_head=heads,
+                                      dual_output=True, dtype=F64) - z
+        torch.testing.assert_close(dual0, plain, rtol=1e-12, atol=1e-12)
+        q = dict(p, **{"to_out_t.weight": p["to_out.weight"]})
+        dual = ps.triangle_attention(z, mask, q, starting=starting, n_head=heads,
+                                     dual_output=True, dtype=F64) - z
+        torch.testing.assert_close(dual, plain + plain.transpose(1, 2), rtol=1e-12, atol=1e-12)
+
+
 @pytest.mark.parametrize("starting", [True, False])
 @pytest.mark.parametrize("transposed", [False, True])
 def test_triattn_matches_brute_force(starting, transposed):

@@ -91,7 +91,8 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "ffk_attention_pair_bias": (
         c_int32,
-        [c_void_p] * 15
+        [c_void_p] * 13
+        + [c_void_p, c_int32, c_int64, c_int64, c_int64, c_void_p, c_void_p]
         + [c_size_t, c_int64, c_int64, c_int32, c_int32, c_int32, c_float, c_int32, c_float,
            c_float, c_void_p],
     ),

@@ -645,7 +645,7 @@ int32_t ffk_triangle_attention(
     launch_row_gemm(p, kEpiApb, kXLn, st);
     // the pair bias from the un-transposed pair (the OpenFold lineage's ending node: the
     // transposed one); the norm's offset adds one constant per head, which the softmax cancels
-    PairBiasArgs pb;
+    PairBiasArgs pb{};
     pb.z = static_cast<const bf16*>(z);
     pb.mask = key_mask;
     pb.ln_w = ln_pair_w;
@@ -925,10 +925,14 @@ int32_t ffk_attention_pair_bias(
     const void* s, const void* z, const uint8_t* key_mask, const float* ln_single_w,
     const float* ln_single_b, const float* w_query, const float* b_query, const float* w_key,
     const float* w_value, const float* ln_pair_w, const float* w_bias, const float* w_gate,
-    const float* w_out, void* out, void* workspace, size_t workspace_bytes, int64_t batch,
-    int64_t n, int32_t d_single, int32_t d_pair, int32_t n_head, float gate_bias,
-    int32_t residual, float eps_single, float eps_pair, void* stream) {
+    const float* w_out, const void* extra_bias, int32_t extra_bf16, int64_t extra_stride_b,
+    int64_t extra_stride_h, int64_t extra_stride_i, void* out, void* workspace,
+    size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_single, int32_t d_pair,
+    int32_t n_head, float gate_bias, int32_t residual, float eps_single, float eps_pair,
+    void* stream) {
   if (int32_t st = check_device()) return st;
+  if (extra_bias && (extra_stride_b < 0 || extra_stride_h < 0 || extra_stride_i < 0))
+    return fail(FFK_ERR_INVALID, "attention_pair_bias: negative extra_bias stride");
   if (d_pair != 128)
     return fail(FFK_ERR_INVALID, "attention_pair_bias: d_pair=%d (kernels take 128)", d_pair);
   if (n_head <= 0 || n_head > 32 || d_single <= 0 || d_single % 64 != 0 || d_single > kLnGemmMaxK ||
@@ -978,7 +982,7 @@ int32_t ffk_attention_pair_bias(
   p.dh = dh;
   launch_row_gemm(p, kEpiApb, kXLn, st);
 
-  PairBiasArgs pb;
+  PairBiasArgs pb{};
   pb.z = static_cast<const bf16*>(z);
   pb.mask = key_mask;
   pb.ln_w = ln_pair_w;
@@ -991,6 +995,11 @@ int32_t ffk_attention_pair_bias(
   pb.eps = eps_pair;
   pb.c = 128;
   pb.transposed = 0;
+  pb.extra = extra_bias;
+  pb.extra_bf16 = extra_bf16 ? 1 : 0;
+  pb.extra_sb = extra_stride_b;
+  pb.extra_sh = extra_stride_h;
+  pb.extra_si = extra_stride_i;
   launch_apb_pair_bias(pb, st);
 
   ApbAttnArgs at;
@@ -1080,7 +1089,7 @@ int32_t ffk_msa_pair_weighted_averaging(
   p.depth = (int)depth;
   launch_row_gemm(p, kEpiPwa, kXLn, st);
 
-  PairBiasArgs pb;
+  PairBiasArgs pb{};
   pb.z = static_cast<const bf16*>(z);
   pb.mask = key_mask;
   pb.ln_w = ln_pair_w;

@@ -180,6 +180,11 @@ struct PairBiasArgs {
   float eps;
   int c;                 // pair width: 64, 128 or 256
   int transposed;        // 1: the logit of (query i, key j) comes from z[b, j, i]
+  // optional extra logits (natural units) at extra[b sb + h sh + i si + j], fp32 or bf16
+  // (extra_bf16); strides in elements, 0 broadcasts
+  const void* extra;
+  int extra_bf16;
+  int64_t extra_sb, extra_sh, extra_si;
 };
 void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream);
 

@@ -531,11 +531,19 @@ __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
     const int64_t i = bi - b * n;
     const bool valid = key < n && a.mask[b * n + key] != 0;
     float* out = a.bias + (b * a.heads * n + i) * a.np + key;
+    const int64_t xe = b * a.extra_sb + i * a.extra_si + key;  // head 0's extra logit
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int h = acc_row(r, g);
-      if (h < a.heads)
-        out[(int64_t)h * n * a.np] = valid ? rstd * (acc[r] - mean * wsum_s[wave][h]) : kMaskedLogit;
+      if (h < a.heads) {
+        float y = rstd * (acc[r] - mean * wsum_s[wave][h]);
+        if (a.extra && valid) {
+          const int64_t at = xe + h * a.extra_sh;
+          y += kLog2e * (a.extra_bf16 ? (float)static_cast<const bf16*>(a.extra)[at]
+                                      : static_cast<const float*>(a.extra)[at]);
+        }
+        out[(int64_t)h * n * a.np] = valid ? y : kMaskedLogit;
+      }
     }
   };
   while (t < a.tiles) {

@@ -372,13 +372,16 @@ def attention_pair_bias(
     to_out: Tensor,
     n_head: int,
     gate_bias: float = 0.0,
+    extra_bias: Tensor | None = None,
     residual: bool = True,
     eps_single: float = 1e-5,
     eps_pair: float = 1e-5,
     out: Tensor | None = None,
 ) -> Tensor:
     """Single-track attention with pair bias: ``s [B, N, c_s]`` bf16 attends over tokens with
-    the bias ``LN_pair(z) . to_bias`` from ``z [B, N, N, 128]`` bf16, under the key mask."""
+    the bias ``LN_pair(z) . to_bias`` from ``z [B, N, N, 128]`` bf16, under the key mask.
+    ``extra_bias`` (fp32 or bf16, broadcastable to ``[B, H, N, N]``, e.g. an ``[N, N]`` or
+    an expanded view) joins every logit; broadcast axes are passed as zero strides."""
     batch, n = _pair(z, mask)
     _need(_on_device(s) and s.is_contiguous() and s.dtype == torch.bfloat16,
           "s must be a contiguous bf16 device tensor")
@@ -394,13 +397,27 @@ def attention_pair_bias(
             ("ln_pair_weight", ln_pair_weight, (PAIR_WIDTH,)), ("to_bias", to_bias, (n_head, PAIR_WIDTH)),
             ("to_gate", to_gate, (cs, cs)), ("to_out", to_out, (cs, cs)))
     ps = [_param(t, dev, nm, shape) for nm, t, shape in spec]
+    extra, strides, extra_bf16 = None, (0, 0, 0), 0
+    if extra_bias is not None:
+        _need(extra_bias.dtype in (torch.float32, torch.bfloat16),
+              f"extra_bias must be fp32 or bf16 (got {extra_bias.dtype})")
+        _need(extra_bias.device == dev, "extra_bias must be on the device of s")
+        try:
+            extra = extra_bias.expand(batch, n_head, n, n)
+        except RuntimeError:
+            raise ValueError(f"extra_bias {tuple(extra_bias.shape)} does not broadcast to "
+                             f"{(batch, n_head, n, n)}") from None
+        if extra.stride(-1) != 1:
+            extra = extra.contiguous()
+        strides, extra_bf16 = extra.stride()[:3], int(extra.dtype == torch.bfloat16)
     out = _output(out, tuple(s.shape), torch.bfloat16, dev)
     lib = _native.lib()
     ws = _workspace(lib.ffk_attention_pair_bias_workspace(batch, n, cs, PAIR_WIDTH, n_head), dev)
     status = lib.ffk_attention_pair_bias(
-        s.data_ptr(), z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
-        ws.data_ptr(), ws.numel(), batch, n, cs, PAIR_WIDTH, n_head, float(gate_bias),
-        int(residual), float(eps_single), float(eps_pair), _stream(dev),
+        s.data_ptr(), z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), _ptr(extra),
+        extra_bf16, *strides, out.data_ptr(), ws.data_ptr(), ws.numel(), batch, n, cs,
+        PAIR_WIDTH, n_head, float(gate_bias), int(residual), float(eps_single), float(eps_pair),
+        _stream(dev),
     )
     _native.check(status, "attention_pair_bias")
     return out

@@ -483,7 +483,15 @@ class AttentionPairBias(EngineOp, MasterWeights, nn.Module):
             return (f"d_single={self.d_single} heads={self.n_head} (the kernels take a multiple "
                     "of 64 split into at most 32 heads of 8, 16, 24 or 32)")
         if extra_bias is not None:
-            return "an extra attention bias is not in the hip kernels"
+            if extra_bias.dtype not in (torch.float32, torch.bfloat16) or extra_bias.device != s.device:
+                return f"extra bias {extra_bias.dtype} on {extra_bias.device} (the kernels take fp32 / bf16 on the device)"
+            want = (s.shape[0], self.n_head, s.shape[1], s.shape[1])
+            try:
+                fits = torch.broadcast_shapes(tuple(extra_bias.shape), want) == torch.Size(want)
+            except RuntimeError:
+                fits = False
+            if not fits:
+                return f"extra bias {tuple(extra_bias.shape)} does not broadcast to {want}"
         return None
 
     def _forward_pytorch(self, s: Tensor, z: Tensor, mask: Tensor, extra_bias: Tensor | None = None,
@@ -505,8 +513,8 @@ class AttentionPairBias(EngineOp, MasterWeights, nn.Module):
             to_key=self.to_key.weight, to_value=self.to_value.weight,
             ln_pair_weight=self.ln_pair.weight, to_bias=self.to_bias.weight,
             to_gate=self.to_gate.weight, to_out=self.to_out.weight, n_head=self.n_head,
-            gate_bias=self.gate_bias, residual=residual, eps_single=self.ln_single.eps,
-            eps_pair=self.ln_pair.eps,
+            gate_bias=self.gate_bias, extra_bias=extra_bias, residual=residual,
+            eps_single=self.ln_single.eps, eps_pair=self.ln_pair.eps,
         )
 
 

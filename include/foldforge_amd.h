@@ -209,7 +209,11 @@ int32_t ffk_transition_noalloc(const void* x, const float* ln_w, const float* ln
  * with the [batch, n] key mask (masked keys weigh exactly 0; a batch entry without a valid
  * key gets o = 0). s, out [batch, n, d_single] bf16; z [batch, n, n, d_pair] bf16;
  * d_pair = 128; d_single a multiple of 64 split into n_head <= 32 heads of dh = 8, 16, 24
- * or 32 (the trunk: 384 = 16 x 24). `out` may alias `s`.
+ * or 32 (the trunk: 384 = 16 x 24). `out` may alias `s`. extra_bias (NULL: none) adds
+ * extra_bias[b * stride_b + h * stride_h + i * stride_i + j] (fp32, or bf16 with extra_bf16;
+ * strides in elements, 0 broadcasts) to the logit of (head h, query i, key j): the block's
+ * extra_pair_bias (OpenDDE's structural bias, legacy/pairformer.py:216-218; the engine
+ * expands [n, n] over samples and heads, src/foldforge/modules/engine/graph.py:223-225).
  * Replaces: engine AttentionPairBias.forward, op name "single_attention"
  * (src/foldforge/modules/engine/backends.py:50; equations
  * src/foldforge/models/checkpoints/legacy/transformer.py:28-137 as called from
@@ -221,9 +225,11 @@ int32_t ffk_attention_pair_bias(
     const void* s, const void* z, const uint8_t* key_mask, const float* ln_single_w,
     const float* ln_single_b, const float* w_query, const float* b_query, const float* w_key,
     const float* w_value, const float* ln_pair_w, const float* w_bias, const float* w_gate,
-    const float* w_out, void* out, void* workspace, size_t workspace_bytes, int64_t batch,
-    int64_t n, int32_t d_single, int32_t d_pair, int32_t n_head, float gate_bias,
-    int32_t residual, float eps_single, float eps_pair, void* stream);
+    const float* w_out, const void* extra_bias, int32_t extra_bf16, int64_t extra_stride_b,
+    int64_t extra_stride_h, int64_t extra_stride_i, void* out, void* workspace,
+    size_t workspace_bytes, int64_t batch, int64_t n, int32_t d_single, int32_t d_pair,
+    int32_t n_head, float gate_bias, int32_t residual, float eps_single, float eps_pair,
+    void* stream);
 
 /*
  * MSA pair-weighted averaging, residual included:

@@ -172,8 +172,9 @@ def transition(x, p, *, eps: float = 1e-5):
 
 
 def attention_pair_bias(s, z, mask, p, *, n_head: int, gate_bias: float = 0.0,
-                        eps: float = 1e-5):
-    """Single-track attention with the pair bias, fp64 loops."""
+                        extra_bias=None, eps: float = 1e-5):
+    """Single-track attention with the pair bias, fp64 loops; ``extra_bias [B, H, N, N]`` is
+    added to every logit where given."""
     batch, n, cs = s.shape
     d = cs // n_head
     scale = 1.0 / math.sqrt(d)
@@ -196,6 +197,8 @@ def attention_pair_bias(s, z, mask, p, *, n_head: int, gate_bias: float = 0.0,
                 for k in range(n):
                     dot = sum(q[i][h * d + e] * kk[k][h * d + e] for e in range(d))
                     val = dot * scale + zb[i][k][h]
+                    if extra_bias is not None:
+                        val += float(extra_bias[b, h, i, k])
                     logits.append(val if bool(mask[b, k]) else MASK_VALUE)
                 w = _softmax_row(logits)
                 for e in range(d):

@@ -280,13 +280,16 @@ def attention_pair_bias(
     *,
     n_head: int,
     gate_bias: float = 0.0,
+    extra_bias: Tensor | None = None,
     eps: float = 1e-5,
     dtype: torch.dtype = torch.float32,
 ) -> Tensor:
     """Single-track attention with pair bias (``legacy/transformer.py:93-137``).
 
     ``x = LN_single(s)``; ``q = x W_q^T + b_q``, ``k = x W_k^T``, ``v = x W_v^T``;
-    ``bias[h, i, j] = LN_pair(z)[i, j] . W_b[h]`` (norm without offset);
+    ``bias[h, i, j] = LN_pair(z)[i, j] . W_b[h]`` (norm without offset), plus
+    ``extra_bias`` (broadcast to ``[B, H, N, N]``: OpenDDE's structural bias,
+    ``legacy/pairformer.py:216-218``) where given;
     ``s + (sigmoid(x W_g^T + gate_bias) * attn) W_out^T``.
     """
     s = s.detach().to("cpu", dtype)
@@ -305,6 +308,8 @@ def attention_pair_bias(
 
     zn = layer_norm(z, _p(params, "ln_pair.weight", dtype), None, eps)
     bias = torch.einsum("bijc,hc->bhij", zn, _p(params, "to_bias.weight", dtype))
+    if extra_bias is not None:
+        bias = bias + extra_bias.detach().to("cpu", dtype)
     keep = mask.to("cpu", torch.bool)[:, None, None, :]
     o = _masked_softmax_attention(heads(q), heads(k), heads(v), bias, keep, d**-0.5)
     o = o.permute(0, 2, 1, 3).reshape(batch, n, cs)
@@ -424,6 +429,7 @@ def pairformer_block(
     s: Tensor | None = None,
     n_head_single: int = 16,
     single_gate_bias: float = 0.0,
+    extra_pair_bias: Tensor | None = None,
     transposed_bias: bool = False,
     eps: float = 1e-5,
     dtype: torch.dtype = torch.float32,
@@ -438,6 +444,8 @@ def pairformer_block(
     Parallel: every update reads the block's input ``z0`` (``s0``):
     ``z = z0 + (dTM_out + dTM_in + dTA_start + dTA_end) + dTr``, ``s = s0 + dAPB(s0, z0) +
     dTr_s(s0)``. ``params`` holds the block's engine keys (``tri_multi_outgoing.to_left.weight`` ...).
+    ``extra_pair_bias`` (broadcast to ``[B, H, N, N]``) joins the single attention's logits
+    (``legacy/pairformer.py:216-218``).
 
     ``io_dtype`` (e.g. bf16) rounds the residual stream to that dtype after every op, as
     an engine op returns ``x + f(x)`` in its input dtype (``README.md:143-145``; bf16
@@ -462,7 +470,7 @@ def pairformer_block(
             return z_out
         s0 = s.to(dtype)
         ds = attention_pair_bias(s, z, mask, sub_params(params, "single_attention"), n_head=n_head_single,
-                                 gate_bias=single_gate_bias, **kw) - s0
+                                 gate_bias=single_gate_bias, extra_bias=extra_pair_bias, **kw) - s0
         return z_out, io(s0 + ds + (transition(s, sub_params(params, "single_transition"), **kw) - s0))
 
     z = io(triangle_multiplication(
@@ -484,7 +492,7 @@ def pairformer_block(
         return z
     s = io(attention_pair_bias(
         s, z, mask, sub_params(params, "single_attention"), n_head=n_head_single,
-        gate_bias=single_gate_bias, **kw,
+        gate_bias=single_gate_bias, extra_bias=extra_pair_bias, **kw,
     ))
     s = io(transition(s, sub_params(params, "single_transition"), **kw))
     return z, s

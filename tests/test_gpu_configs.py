@@ -226,3 +226,18 @@ def test_run_block_on_hip_matches_the_batched_call_and_the_oracle():
     rs = ps.rel_rms(got_s[None].cpu().double() - sb.double(), os_ - sb.double(), keys.cpu())
     print(f"run_block on hip: pair update rel_rms={rz:.3e} single update rel_rms={rs:.3e}", flush=True)
     assert rz <= 3e-2 and rs <= 3e-2
+    # the block's extra pair bias ([L, L], OpenDDE's structural bias) on hip, against the oracle
+    extra = 1.5 * torch.randn(n, n, generator=g)
+    with torch.no_grad(), adapter.autocast_for(block):
+        before = dispatch.served_count(block, "hip")
+        ez, es = adapter.run_block(block, pair.cuda(), pair_mask.cuda(), single.cuda(), tokens.cuda(),
+                                   extra_pair_bias=extra.cuda())
+        assert dispatch.served_count(block, "hip") > before
+    assert torch.equal(ez, got_z)  # the pair track does not read it
+    _, os2 = ps.pairformer_block(zb, keys.cpu(), {k: v.cpu() for k, v in block.state_dict().items()},
+                                 n_head_pair=4, s=sb, n_head_single=16,
+                                 extra_pair_bias=extra.bfloat16().double(), dtype=torch.float64)
+    rs2 = ps.rel_rms(es[None].cpu().double() - sb.double(), os2 - sb.double(), keys.cpu())
+    print(f"run_block with extra_pair_bias: single update rel_rms={rs2:.3e}", flush=True)
+    assert rs2 <= 3e-2
+    assert ps.rel_rms(os2 - sb.double(), os_ - sb.double(), keys.cpu()) > 0.05

@@ -75,6 +75,29 @@ def test_attention_pair_bias_matches_oracle(cs, heads, n, lengths):
     _check(full, want + s.double(), "attention_pair_bias residual")
 
 
+@pytest.mark.parametrize("form", ["nn_fp32", "bhnn_bf16"])
+def test_attention_pair_bias_extra_bias_matches_oracle(form):
+    """The block's extra pair bias on hip: an fp32 [N, N] map (broadcast by zero strides, as
+    the engine passes it) or a dense bf16 [B, H, N, N]."""
+    n, cs, heads = 100, 384, 16
+    s, z, mask = _inputs(n, cs, [100, 73], seed=31)
+    m = _apb(cs, heads, gate_bias=0.0, seed=32)
+    g = torch.Generator().manual_seed(33)
+    if form == "nn_fp32":
+        extra = 2.0 * torch.randn(n, n, generator=g)
+        dev_extra = extra.cuda().expand(2, heads, n, n)
+    else:
+        extra = (2.0 * torch.randn(2, heads, n, n, generator=g)).bfloat16()
+        dev_extra = extra.cuda()
+    assert m.unsupported(s.cuda(), z.cuda(), mask.cuda(), dev_extra) is None
+    got = hip_delta(m, s.cuda(), z.cuda(), mask.cuda(), dev_extra).cpu()
+    want = ps.attention_pair_bias(s, z, mask, m.state_dict(), n_head=heads,
+                                  extra_bias=extra.double(), dtype=torch.float64) - s.double()
+    _check(got, want, f"attention_pair_bias extra bias {form}")
+    plain = ps.attention_pair_bias(s, z, mask, m.state_dict(), n_head=heads, dtype=torch.float64) - s.double()
+    assert ps.rel_rms(plain, want) > 0.1  # the bias matters at this size
+
+
 def test_attention_pair_bias_masking_is_exact_and_empty_rows_are_zero():
     n, length = 96, 61
     s, z, mask = _inputs(n, 384, [length, 0], seed=11)

@@ -349,6 +349,13 @@ def test_attention_pair_bias_matches_brute_force():
     got = ps.attention_pair_bias(s, z, mask, p, n_head=hs, gate_bias=-1.0, dtype=F64)
     want = brute.attention_pair_bias(s.numpy(), z.numpy(), mask.numpy(), _np(p), n_head=hs, gate_bias=-1.0)
     np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+    # the block's extra pair bias: an [N, N] map broadcast over samples and heads
+    extra = 2.0 * torch.randn(n, n, generator=g, dtype=F64)
+    got = ps.attention_pair_bias(s, z, mask, p, n_head=hs, extra_bias=extra, dtype=F64)
+    want = brute.attention_pair_bias(s.numpy(), z.numpy(), mask.numpy(), _np(p), n_head=hs,
+                                     extra_bias=extra.expand(2, hs, n, n).numpy())
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-11, atol=1e-11)
+    assert (got - ps.attention_pair_bias(s, z, mask, p, n_head=hs, dtype=F64)).abs().max() > 1e-2
 
 
 def _pwa_params(cm: int, c: int, heads: int, d: int, seed: int) -> dict[str, torch.Tensor]:

@@ -324,42 +324,71 @@ __device__ __forceinline__ void wait_vm_lds() {
   asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" ::"n"(N) : "memory");
 }
 
+// Sum of 8 values as a tree (depth 3 rather than a chain of 8 dependent adds).
+__device__ __forceinline__ float sum8(const float (&x)[8]) {
+  return ((x[0] + x[1]) + (x[2] + x[3])) + ((x[4] + x[5]) + (x[6] + x[7]));
+}
+
 // LayerNorm (fp32 statistics and affine) of the rows 0 .. TM - 1 of an off128 tile src into
 // the off128 tile dst (which may be src), NT threads, 16 lanes per row; rows >= valid become
-// zeros.
+// zeros. A thread's rows are all read before any is written (in place, the compiler could not
+// otherwise issue a later row's read ahead of an earlier row's write), and the rows' sums and
+// reductions are independent, so their latencies overlap: this runs between two barriers of
+// every tile of the persistent pair kernels, so its length is on their critical path.
 template <int TM, int NT>
 __device__ __forceinline__ void ln_swz(const bf16* src, bf16* dst, int valid, const float* w,
                                        const float* b, float eps) {
+  constexpr int IT = TM / (NT / 16);
   const int sub = threadIdx.x & 15, pos0 = threadIdx.x >> 4;
-  float wv[8], bv[8];
+  bf16x8 raw[IT];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    wv[e] = w[8 * sub + e];
-    bv[e] = b ? b[8 * sub + e] : 0.f;
+  for (int it = 0; it < IT; ++it)
+    raw[it] = *reinterpret_cast<const bf16x8*>(&src[off128(pos0 + (NT / 16) * it, sub)]);
+  float wv[8], bv[8];
+  {
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(w + 8 * sub);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(w + 8 * sub + 4);
+    f32x4 b0 = {0.f, 0.f, 0.f, 0.f}, b1 = b0;
+    if (b) {
+      b0 = *reinterpret_cast<const f32x4*>(b + 8 * sub);
+      b1 = *reinterpret_cast<const f32x4*>(b + 8 * sub + 4);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      wv[e] = w0[e];
+      wv[e + 4] = w1[e];
+      bv[e] = b0[e];
+      bv[e + 4] = b1[e];
+    }
+  }
+  float x[IT][8], mean[IT], rstd[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[it][e] = (float)raw[it][e];
+    mean[it] = sum8(x[it]);
   }
 #pragma unroll
-  for (int it = 0; it < TM / (NT / 16); ++it) {
+  for (int it = 0; it < IT; ++it) mean[it] = sum16(mean[it]) * (1.f / 128.f);
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    float d2[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[it][e] -= mean[it];
+      d2[e] = x[it][e] * x[it][e];
+    }
+    rstd[it] = sum8(d2);
+  }
+#pragma unroll
+  for (int it = 0; it < IT; ++it) rstd[it] = __builtin_amdgcn_rsqf(sum16(rstd[it]) * (1.f / 128.f) + eps);
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
     const int t = pos0 + (NT / 16) * it;
-    const bf16x8 raw = *reinterpret_cast<const bf16x8*>(&src[off128(t, sub)]);
-    float x[8];
-    float s = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      x[e] = (float)raw[e];
-      s += x[e];
-    }
-    const float mean = sum16(s) * (1.f / 128.f);
-    float q = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      x[e] -= mean;
-      q += x[e] * x[e];
-    }
-    const float rstd = __builtin_amdgcn_rsqf(sum16(q) * (1.f / 128.f) + eps);
     bf16x8 o;
     const bool real = t < valid;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = real ? (bf16)(x[e] * rstd * wv[e] + bv[e]) : (bf16)0.f;
+    for (int e = 0; e < 8; ++e) o[e] = real ? (bf16)(x[it][e] * rstd[it] * wv[e] + bv[e]) : (bf16)0.f;
     *reinterpret_cast<bf16x8*>(&dst[off128(t, sub)]) = o;
   }
 }

@@ -82,7 +82,7 @@ __global__ __launch_bounds__(512, 2) void triattn_project(
   __shared__ __attribute__((aligned(16))) bf16 svt[4][32 * kPT];   // [d][key slot]
   __shared__ __attribute__((aligned(16))) float keep[NB][kPT];     // key mask per position
   __shared__ __attribute__((aligned(16))) bf16 wbl[H * 128];       // the pair-bias rows
-  __shared__ float lnp[2][128];                                    // LayerNorm affine
+  __shared__ __attribute__((aligned(16))) float lnp[2][128];        // LayerNorm affine
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -537,7 +537,7 @@ __global__ __launch_bounds__(512, 2) void triattn_output(
   __shared__ __attribute__((aligned(16))) bf16 zs[NB][kPT * 128];  // raw z, then out (off128)
   __shared__ __attribute__((aligned(16))) bf16 os[NB][kPT * 128];  // o, then gate * o (off128)
   __shared__ __attribute__((aligned(16))) bf16 xh[2][kPT * 128];   // LN(z) (off128)
-  __shared__ float lnp[2][128];
+  __shared__ __attribute__((aligned(16))) float lnp[2][128];
   __shared__ float pbias[2][128];  // gate bias (times -log2 e, as the packed gate), output bias
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;

@@ -41,7 +41,7 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
   __shared__ __attribute__((aligned(16))) bf16 stage[8][32 * kPS];  // [channel][position]
   __shared__ __attribute__((aligned(16))) float msk[NB][8][kPT];    // token mask m[s0 + t], per wave
   __shared__ float mrw[NB][8];                                      // token mask m[r], per wave
-  __shared__ float lnp[2][H];  // LayerNorm affine
+  __shared__ __attribute__((aligned(16))) float lnp[2][H];  // LayerNorm affine
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(512, 2) void trimul_output(
   __shared__ __attribute__((aligned(16))) bf16 xh[kPT * 128];      // LN(z) (off128)
   __shared__ __attribute__((aligned(16))) bf16 y[kPT * 128];       // LN_out(P) (off128)
   __shared__ float red[2][2][8][kPT];  // [tile parity][sum, centred squares][wave][position]
-  __shared__ float lnp[4][H];          // LN_pair and LN_out affine
+  __shared__ __attribute__((aligned(16))) float lnp[4][H];  // LN_pair and LN_out affine
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);

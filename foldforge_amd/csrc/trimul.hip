@@ -449,46 +449,55 @@ __global__ __launch_bounds__(512, 2) void trimul_output(
       dma16_stream(pb, (uint32_t)((lane >> 3) * plane * 2) + 16 * (lane & 7), dp + 1024 * piece);
     }
   };
-  // P statistics of this thread's 16 channels 16 wave .. + 15 at position `lane`
+  // P statistics of this thread's 16 channels 16 wave .. + 15 at position `lane`; every sum is
+  // a tree (these run between the tile's barriers, so their latency is on the tile's path)
+  auto p_load = [&](int buf, float (&v)[16]) {
+    const bf16* col = &ps[buf][(16 * wave) * kPT + lane];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) v[e] = (float)col[e * kPT];
+  };
+  auto sum16v = [](const float (&v)[16]) {
+    float a[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) a[q] = (v[4 * q] + v[4 * q + 1]) + (v[4 * q + 2] + v[4 * q + 3]);
+    return (a[0] + a[1]) + (a[2] + a[3]);
+  };
+  auto red8 = [&](int par, int which) {
+    float a[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) a[q] = red[par][which][q][lane];
+    return ((a[0] + a[1]) + (a[2] + a[3])) + ((a[4] + a[5]) + (a[6] + a[7]));
+  };
   auto p_sum = [&](int buf, int par) {
-    const bf16* col = &ps[buf][(16 * wave) * kPT + lane];
-    float sacc = 0.f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) sacc += (float)col[e * kPT];
-    red[par][0][wave][lane] = sacc;
+    float v[16];
+    p_load(buf, v);
+    red[par][0][wave][lane] = sum16v(v);
   };
-  auto p_mean = [&](int par) {
-    float m = 0.f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) m += red[par][0][q][lane];
-    return m * (1.f / H);
-  };
+  auto p_mean = [&](int par) { return red8(par, 0) * (1.f / H); };
   auto p_centred = [&](int buf, int par) {
-    const bf16* col = &ps[buf][(16 * wave) * kPT + lane];
+    float v[16];
+    p_load(buf, v);
     const float mean = p_mean(par);
-    float ss = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
-      const float d = (float)col[e * kPT] - mean;
-      ss += d * d;
+      v[e] -= mean;
+      v[e] *= v[e];
     }
-    red[par][1][wave][lane] = ss;
+    red[par][1][wave][lane] = sum16v(v);
   };
+  // the centre norm's affine for this thread's 16 channels, read once (the first barrier
+  // publishes lnp)
+  float cn_w[16], cn_b[16];
   auto p_normalise = [&](int buf, int par) {
-    const bf16* col = &ps[buf][(16 * wave) * kPT + lane];
+    float v[16];
+    p_load(buf, v);
     const float mean = p_mean(par);
-    float var = 0.f;
-#pragma unroll
-    for (int q = 0; q < 8; ++q) var += red[par][1][q][lane];
-    const float rstd = __builtin_amdgcn_rsqf(var * (1.f / H) + eps_out);
+    const float rstd = __builtin_amdgcn_rsqf(red8(par, 1) * (1.f / H) + eps_out);
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       bf16x8 o;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int c = 16 * wave + 8 * h + e;
-        o[e] = (bf16)(((float)col[(8 * h + e) * kPT] - mean) * rstd * lnp[2][c] + lnp[3][c]);
-      }
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)((v[8 * h + e] - mean) * rstd * cn_w[8 * h + e] + cn_b[8 * h + e]);
       *reinterpret_cast<bf16x8*>(&y[off128(lane, 2 * wave + h)]) = o;
     }
   };
@@ -508,6 +517,11 @@ __global__ __launch_bounds__(512, 2) void trimul_output(
   dma(blockIdx.x + step, 1);
   wait_vm_lds<4>();  // this wave's transfers of the first tile landed
   __syncthreads();
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    cn_w[e] = lnp[2][16 * wave + e];
+    cn_b[e] = lnp[3][16 * wave + e];
+  }
   {
     int b, i, j0, valid;
     where(blockIdx.x, b, i, j0, valid);

@@ -197,6 +197,10 @@ struct TriattnWs {
   int* kst;
   size_t bytes;
 };
+// Head widths the generic path runs on the flash core (the rest: apb_attention).
+bool triattn_flash_width(int d) { return d == 16 || d == 32; }
+int64_t pad4(int64_t n) { return (n + 3) / 4 * 4; }
+
 TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d, int form) {
   Carver cv{static_cast<char*>(ws)};
   const int64_t np = pad128(n);
@@ -207,11 +211,21 @@ TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d
   if (!triattn_fused(c, heads, d)) {
     const int64_t np32 = pad32(n);
     const size_t tok = (size_t)batch * n * n * hd;
-    w.q = cv.take<bf16>(tok);
-    w.k = cv.take<bf16>(tok);
-    w.gate = cv.take<bf16>(tok);
-    w.vt = cv.take<bf16>((size_t)batch * n * hd * np32);
-    w.bias = cv.take<float>((size_t)batch * heads * n * np32);
+    if (triattn_flash_width(d)) {
+      // the flash core's layouts: rows padded to whole row groups, keys to np32
+      const size_t blk = (size_t)batch * heads * pad4(n) * np32 * d;
+      w.q = cv.take<bf16>(blk);
+      w.k = cv.take<bf16>(blk);
+      w.vt = cv.take<bf16>(blk);
+      w.gate = cv.take<bf16>(tok);
+      w.bias = cv.take<float>((size_t)batch * heads * np32 * np32);
+    } else {
+      w.q = cv.take<bf16>(tok);
+      w.k = cv.take<bf16>(tok);
+      w.gate = cv.take<bf16>(tok);
+      w.vt = cv.take<bf16>((size_t)batch * n * hd * np32);
+      w.bias = cv.take<float>((size_t)batch * heads * n * np32);
+    }
     w.og = cv.take<float>(tok);
     w.bytes = cv.used;
     return w;
@@ -616,7 +630,9 @@ int32_t ffk_triangle_attention(
     if (batch * n > 65535 || batch * n * n * hd / 32 > 0x7fffffffLL * 8)
       return fail(FFK_ERR_INVALID, "triangle_attention: batch * n = %lld exceeds the launch grid", (long long)(batch * n));
     const int64_t np32 = pad32(n);
-    // q, k, v^T, gate of every pair row (the transposed pair for the ending node)
+    const bool flash = triattn_flash_width(d_head);
+    // q, k, v^T, gate of every pair row (the transposed pair for the ending node); for the flash
+    // core on keys padded to np32 (the padding repeats key n - 1, so its k and v are finite)
     RowGemmArgs p{};
     p.ln_x = static_cast<const bf16*>(z);
     p.ln_w = ln_pair_w;
@@ -626,7 +642,7 @@ int32_t ffk_triangle_attention(
     p.w1 = w_key;
     p.w2 = w_value;
     p.w3 = w_gate;
-    p.M = batch * n * n;
+    p.M = flash ? batch * n * np32 : batch * n * n;
     p.K = d_pair;
     p.O = 4 * hd;
     p.q_bias = nullptr;
@@ -641,7 +657,12 @@ int32_t ffk_triangle_attention(
     p.np = (int)np32;
     p.heads = n_head;
     p.dh = d_head;
-    p.tmap = starting ? kMapIdentity : kMapPairT;
+    if (flash) {
+      p.tmap = starting ? kMapPadKeys : kMapPadKeysT;
+      p.flash_rows = (int)pad4(n);
+    } else {
+      p.tmap = starting ? kMapIdentity : kMapPairT;
+    }
     launch_row_gemm(p, kEpiApb, kXLn, st);
     // the pair bias from the un-transposed pair (the OpenFold lineage's ending node: the
     // transposed one); the norm's offset adds one constant per head, which the softmax cancels
@@ -658,22 +679,46 @@ int32_t ffk_triangle_attention(
     pb.eps = eps;
     pb.c = d_pair;
     pb.transposed = !starting && transposed_bias ? 1 : 0;
+    pb.blocked = flash ? 1 : 0;
     launch_apb_pair_bias(pb, st);
-    ApbAttnArgs at;
-    at.q = w.q;
-    at.k = w.k;
-    at.vt = w.vt;
-    at.gate = w.gate;
-    at.bias = w.bias;
-    at.mask = key_mask;
-    at.og = w.og;
-    at.n = (int)n;
-    at.np = (int)np32;
-    at.heads = n_head;
-    at.dh = d_head;
-    at.cs = hd;
-    at.rows_per_bias = (int)n;
-    launch_apb_attention(at, (int)(batch * n), st);
+    if (flash) {
+      // og = gate * o in the attention frame (row r, query j), as apb_attention writes it
+      FlashArgs f{};
+      f.q = w.q;
+      f.k = w.k;
+      f.vt = w.vt;
+      f.bias = w.bias;
+      f.batch = batch;
+      f.rows = pad4(n);
+      f.np = np32;
+      f.rows_valid = n;
+      f.n_valid = n;
+      f.heads = n_head;
+      f.kstages = nullptr;
+      f.dh = d_head;
+      f.gate = w.gate;
+      f.og = w.og;
+      f.o_sb = n * n * hd;
+      f.o_sr = n * hd;
+      f.o_sj = hd;
+      launch_flash(f, st);
+    } else {
+      ApbAttnArgs at;
+      at.q = w.q;
+      at.k = w.k;
+      at.vt = w.vt;
+      at.gate = w.gate;
+      at.bias = w.bias;
+      at.mask = key_mask;
+      at.og = w.og;
+      at.n = (int)n;
+      at.np = (int)np32;
+      at.heads = n_head;
+      at.dh = d_head;
+      at.cs = hd;
+      at.rows_per_bias = (int)n;
+      launch_apb_attention(at, (int)(batch * n), st);
+    }
     // the output projection of the gated values into dst (z frame), with the residual or not
     auto project = [&](const float* wo, const float* bo, bf16* dst, int res) {
       RowGemmArgs o{};
@@ -775,7 +820,7 @@ int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
     return fail(FFK_ERR_INVALID, "flash_attention_bias: q/k/v_t/bias must be 16-byte aligned");
   if (((uintptr_t)o & 7u) != 0 || (o_sb | o_sr | o_sj) % 4 != 0)
     return fail(FFK_ERR_INVALID, "flash_attention_bias: o and its strides must be 8-byte aligned");
-  FlashArgs f;
+  FlashArgs f{};
   f.q = static_cast<const bf16*>(q);
   f.k = static_cast<const bf16*>(k);
   f.vt = static_cast<const bf16*>(v_t);

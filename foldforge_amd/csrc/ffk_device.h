@@ -41,6 +41,19 @@ __device__ __forceinline__ f32x16 zero16() {
 // Row (within a 32x32 MFMA tile) held by accumulator register r of lane group g.
 __device__ __forceinline__ int acc_row(int r, int g) { return 8 * (r >> 2) + 4 * g + (r & 3); }
 
+// Index of pair-bias entry (query, key) in the flash core's blocked layout
+//   [bh][query / 32][key / 32][v][lane][e] (a 32 x 32 tile = 1024 fp32),
+//   lane = 32 g + query % 32, key % 32 = 8 v + 4 g + e:
+// accumulator register 4 v + e of lane `lane` of the S^T tile; a lane's 4 registers of one v
+// are 16 contiguous bytes and consecutive lanes are consecutive, so a DMA'd tile reads back
+// from LDS without bank conflicts.
+__device__ __forceinline__ int64_t bias_index(int64_t bh, int64_t nb, int64_t query, int64_t key) {
+  const int kk = (int)(key & 31);
+  const int v = kk >> 3, g = (kk >> 2) & 1, e = kk & 3;
+  const int lane = 32 * g + (int)(query & 31);
+  return ((((bh * nb + (query >> 5)) * nb + (key >> 5)) * 4 + v) * 64 + lane) * 4 + e;
+}
+
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
 // Stores of intermediates that the next kernel reads once. Bit k of FFK_NT_MASK makes family k

@@ -77,6 +77,13 @@ struct FlashArgs {
   // optional [batch] key-stage counts: the stages past them hold only masked keys (bias
   // -inf), which add exact zeros, and are skipped (NULL: every stage runs)
   const int* kstages;
+  // Head width 16 or 32: q, k [batch heads][rows][np][dh], v^T [batch heads][rows][dh][np]
+  // (keys permuted as the 32-wide layout). With og set, the kernel writes the gated output
+  // og = gate * o (fp32) instead of o, at the same strides (in elements) plus h dh + d, and
+  // reads the gate (bf16) at that offset too.
+  int dh = 32;
+  const bf16* gate = nullptr;
+  float* og = nullptr;
 };
 void launch_flash(const FlashArgs& a, hipStream_t stream);
 
@@ -116,8 +123,10 @@ enum { kActNone = 0, kActSigmoid = 1, kActSilu = 2, kActRelu = 3 };
 // Row maps (RowGemmArgs.tmap): the input row read for logical row m, and the rows the epilogue
 // of kEpiResid writes. kMapPairT: m = (b n + r) n + j reads row (b n + j) n + r (the
 // transposed pair); kMapGridOut / kMapGridIn: m = (b npm + i) npm + k over the padded grid
-// reads pair row (b n + i) n + k / (b n + k) n + i (clamped past n).
-enum { kMapIdentity = 0, kMapPairT = 1, kMapGridOut = 2, kMapGridIn = 3 };
+// reads pair row (b n + i) n + k / (b n + k) n + i (clamped past n); kMapPadKeys /
+// kMapPadKeysT: m = (b n + r) np + j over keys padded to np reads pair row (b n + r) n + j' /
+// (b n + j') n + r with j' = min(j, n - 1).
+enum { kMapIdentity = 0, kMapPairT = 1, kMapGridOut = 2, kMapGridIn = 3, kMapPadKeys = 4, kMapPadKeysT = 5 };
 enum { kXLn = 0, kXF32 = 1 };
 constexpr int kLnGemmMaxK = 768;
 struct RowGemmArgs {
@@ -140,6 +149,11 @@ struct RowGemmArgs {
   const float* gate_b;          // kEpiApb: per-channel gate bias [cs] (NULL: none)
   bf16 *q, *k, *vt, *gate;
   int n, np, heads, dh;
+  // kEpiApb with flash_rows > 0 (logical rows m = (b n + r) np + j, a kMapPadKeys* map): the
+  // flash core's layouts, q, k [batch heads][flash_rows][np][dh] and v^T
+  // [batch heads][flash_rows][dh][np] (keys permuted), written for every j < np; the gate
+  // [batch n n][cs] for j < n
+  int flash_rows;
   // kEpiPwa: w0 = to_value, w1 = to_gate ([hd][K] each, O = 2 hd); tokens m = (b S + s) n + j;
   // v^T [batch][heads][S][dh][np] (bf16, keys contiguous), gate = sigmoid(x W_g^T) [M][hd]
   int depth;
@@ -180,6 +194,9 @@ struct PairBiasArgs {
   float eps;
   int c;                 // pair width: 64, 128 or 256
   int transposed;        // 1: the logit of (query i, key j) comes from z[b, j, i]
+  // 1: bias in the flash core's blocked layout [batch heads][np / 32][np / 32][1024], -inf at
+  // masked keys (rows of queries past n are left unwritten)
+  int blocked;
   // optional extra logits (natural units) at extra[b sb + h sh + i si + j], fp32 or bf16
   // (extra_bf16); strides in elements, 0 broadcasts
   const void* extra;

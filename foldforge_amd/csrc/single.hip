@@ -93,6 +93,13 @@ __device__ inline int64_t mapped_row(const RowGemmArgs& a, int64_t m) {
     const int r = (int)(rem / a.n), j = (int)(rem - (int64_t)r * a.n);
     return (b * a.n + j) * a.n + r;
   }
+  if (a.tmap == kMapPadKeys || a.tmap == kMapPadKeysT) {
+    const int64_t bn = m / a.np;
+    const int j = min((int)(m - bn * a.np), a.n - 1);
+    if (a.tmap == kMapPadKeys) return bn * a.n + j;
+    const int64_t b = bn / a.n;
+    return (b * a.n + j) * a.n + (bn - b * a.n);
+  }
   if (a.tmap == kMapGridOut || a.tmap == kMapGridIn) {
     const int64_t gg = (int64_t)a.npm * a.npm;
     const int64_t b = m / gg, rem = m - b * gg;
@@ -266,7 +273,36 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
 
   const int64_t m = m0 + li;
   if (!active || m >= a.M) return;
-  if (EPI == kEpiApb) {
+  if (EPI == kEpiApb && a.flash_rows > 0) {
+    const int cs = a.O / 4;
+    const int64_t bn = m / a.np;
+    const int j = (int)(m - bn * a.np);
+    const int64_t b = bn / a.n;
+    const int r = (int)(bn - b * a.n);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = cbase + 8 * v + 4 * g;  // 4 channels of one head (dh % 4 == 0)
+      const int hh = c / a.dh, d0 = c - hh * a.dh;
+      const int64_t blk = (b * a.heads + hh) * a.flash_rows + r;  // the (b, h, r) block
+      float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
+      if (seg == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (y[e] + (a.q_bias ? a.q_bias[c + e] : 0.f)) * a.q_scale;
+        store4(a.q + (blk * a.np + j) * a.dh + d0, y[0], y[1], y[2], y[3]);
+      } else if (seg == 1) {
+        store4(a.k + (blk * a.np + j) * a.dh + d0, y[0], y[1], y[2], y[3]);
+      } else if (seg == 2) {
+        const int pos = vkey_pos(j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a.vt[(blk * a.dh + d0 + e) * a.np + pos] = (bf16)y[e];
+      } else if (j < a.n) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = sigmoid_scaled((y[e] + (a.gate_b ? a.gate_b[c + e] : 0.f) + a.gate_bias) * -kLog2e);
+        store4(a.gate + (bn * a.n + j) * cs + c, y[0], y[1], y[2], y[3]);
+      }
+    }
+  } else if (EPI == kEpiApb) {
     const int cs = a.O / 4;
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -531,6 +567,11 @@ __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
     const int64_t i = bi - b * n;
     const bool valid = key < n && a.mask[b * n + key] != 0;
     float* out = a.bias + (b * a.heads * n + i) * a.np + key;
+    // blocked: entry (query i, key) of head h at bias_index(b heads + h, ...), a whole number
+    // of head strides (np^2) apart
+    if (a.blocked) out = a.bias + bias_index(b * a.heads, a.np / 32, i, key);
+    const int64_t hstride = a.blocked ? (int64_t)a.np * a.np : (int64_t)n * a.np;
+    const float masked = a.blocked ? -INFINITY : kMaskedLogit;
     const int64_t xe = b * a.extra_sb + i * a.extra_si + key;  // head 0's extra logit
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
@@ -542,7 +583,7 @@ __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
           y += kLog2e * (a.extra_bf16 ? (float)static_cast<const bf16*>(a.extra)[at]
                                       : static_cast<const float*>(a.extra)[at]);
         }
-        out[(int64_t)h * n * a.np] = valid ? y : kMaskedLogit;
+        out[h * hstride] = valid ? y : masked;
       }
     }
   };

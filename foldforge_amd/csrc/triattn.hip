@@ -48,19 +48,6 @@ constexpr int kFK = 32;     // keys per LDS stage
 constexpr float kSumHigh = 1.2676506002282294e30f;  // 2^100
 constexpr float kSumLow = 7.888609052210118e-31f;    // 2^-100
 
-// Index of bias entry (query, key) in the blocked layout
-//   [bh][query / 32][key / 32][v][lane][e] (a 32 x 32 tile = 1024 fp32),
-//   lane = 32 g + query % 32, key % 32 = 8 v + 4 g + e:
-// accumulator register 4 v + e of lane `lane` of the S^T tile; a lane's 4 registers of one v
-// are 16 contiguous bytes and consecutive lanes are consecutive, so a DMA'd tile reads back
-// from LDS without bank conflicts.
-__device__ __forceinline__ int64_t bias_index(int64_t bh, int64_t nb, int64_t query, int64_t key) {
-  const int kk = (int)(key & 31);
-  const int v = kk >> 3, g = (kk >> 2) & 1, e = kk & 3;
-  const int lane = 32 * g + (int)(query & 31);
-  return ((((bh * nb + (query >> 5)) * nb + (key >> 5)) * 4 + v) * 64 + lane) * 4 + e;
-}
-
 constexpr int kPT = 64;        // positions per projection / output tile
 
 // Persistent, weight-stationary, one barrier per tile. Tiles are (batch, row r of the padded
@@ -268,16 +255,22 @@ __global__ __launch_bounds__(512, 2) void triattn_project(
   wait_vm_lds<0>();  // no LDS write may land after exit
 }
 
+// DQ = head width / 16 (1: 16-wide heads, 2: 32-wide heads).
+template <int DQ>
 struct __attribute__((aligned(16))) FlashLds {
-  bf16 k[2][kFR][kFK * 32];   // [key][d], 16-byte pieces at koff
-  bf16 v[2][kFR][32 * kFK];   // [d][key], 16-byte pieces at voff
-  float bias[kFW][2][1024];   // per wave, two bias tiles (the blocked layout, copied as is)
+  bf16 k[2][kFR][kFK * 16 * DQ];  // [key][d], 16-byte pieces at koff
+  bf16 v[2][kFR][16 * DQ * kFK];  // [d][key], 16-byte pieces at voff
+  float bias[kFW][2][1024];       // per wave, two bias tiles (the blocked layout, copied as is)
 };
 
-// Element offsets of 16-byte piece p of K row `key` (4 pieces: 64 B, four rows fill the 64
-// banks) and of V^T row d (4 pieces of a 32-key stage), XOR-swizzled so that the MFMA operand
-// reads of 16 consecutive rows hit distinct banks.
-__device__ __forceinline__ int koff(int key, int p) { return key * 32 + 8 * (p ^ ((key >> 2) & 3)); }
+// Element offsets of 16-byte piece p of K row `key` (2 DQ pieces: 32 DQ bytes, 8 / DQ rows
+// fill the 64 banks) and of V^T row d (4 pieces of a 32-key stage), XOR-swizzled so that the
+// MFMA operand reads of 16 consecutive rows hit distinct banks.
+template <int DQ>
+__device__ __forceinline__ int koff(int key, int p) {
+  constexpr int sh = DQ == 1 ? 3 : 2;
+  return key * 16 * DQ + 8 * (p ^ ((key >> sh) & (2 * DQ - 1)));
+}
 __device__ __forceinline__ int voff(int d, int p) { return d * kFK + 8 * (p ^ ((d >> 2) & 3)); }
 
 // exp2 of the 32 logits a lane holds for its query, packed into the bf16 P^T operands of
@@ -299,14 +292,15 @@ __device__ __forceinline__ float exp_pack(const f32x16& S, bf16x8& p0, bf16x8& p
   return ts;
 }
 
-// grid (ceil(np / 256) * (np / 4) * batch * heads) workgroups, renumbered per XCD;
-// block 256 = 4 waves x 32 queries, 4 attention rows.
-__global__ __launch_bounds__(256, 2) void flash_attn_bias(
-    const bf16* __restrict__ q, const bf16* __restrict__ k, const bf16* __restrict__ vt,
-    const float* __restrict__ bias, bf16* __restrict__ o, int heads, int64_t rows, int64_t np,
-    int64_t rows_valid, int64_t n_valid, int64_t o_sb, int64_t o_sr, int64_t o_sj,
-    const int* __restrict__ kstages) {
-  __shared__ FlashLds lds;
+// grid (ceil(np / 128) * (rows / 4) * batch * heads) workgroups, renumbered per XCD;
+// block 256 = 4 waves x 32 queries, 4 attention rows. GATED: the output is og = gate * o
+// (fp32), else o (bf16).
+template <int DQ, bool GATED>
+__global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
+  constexpr int D = 16 * DQ;  // head width
+  __shared__ FlashLds<DQ> lds;
+  const int64_t np = a.np, rows = a.rows;
+  const int heads = a.heads;
   const uint32_t nqb = (uint32_t)((np + 32 * kFW - 1) / (32 * kFW));
   const uint32_t nrg = (uint32_t)(rows / kFR);
   const uint32_t total = gridDim.x;
@@ -316,11 +310,12 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
   const int64_t bh = wg / (nqb * nrg);
   const int64_t j0 = (int64_t)qb * 32 * kFW;
   const int64_t r0 = (int64_t)rg * kFR;
-  if (r0 >= rows_valid || j0 >= n_valid) return;  // whole workgroup outside the output
+  if (r0 >= a.rows_valid || j0 >= a.n_valid) return;  // whole workgroup outside the output
   const int64_t bidx = bh / heads;
   const int h = (int)(bh % heads);
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int dl = DQ == 1 ? li & 15 : li;  // V^T row of this lane (16-wide heads: rows repeat)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t jw = j0 + 32 * wave;  // first query of this wave
   const bool active = jw < np;        // the last query block may be partial
@@ -329,32 +324,37 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
   const int64_t nstage = np / kFK;
   // key stages past the batch element's last real key hold bias -inf only: exp2 gives exact
   // zeros there, so leaving them out changes no bit of l or O
-  const int64_t nrun = kstages ? min(nstage, ((int64_t)kstages[bidx] * 32 + kFK - 1) / kFK) : nstage;
+  const int64_t nrun =
+      a.kstages ? min(nstage, ((int64_t)a.kstages[bidx] * 32 + kFK - 1) / kFK) : nstage;
 
-  // Transfers (each one 1 KB LDS DMA per wave): stage s of K / V^T = 16 pieces, 4 per wave
-  // (piece P = 4 wave + u: part P / 8 (K, V^T), row (P / 2) % 4, half P % 2); bias tile
-  // kb of this wave = 4 pieces. Past the last stage / tile a transfer repeats a real one into
-  // a buffer that is no longer read, so every wave always has the same transfers in flight.
-  const bf16* kbase = k + (bh * rows + r0) * np * 32;
-  const bf16* vbase = vt + (bh * rows + r0) * 32 * np;
+  // Transfers (each one 1 KB LDS DMA per wave): stage s of K / V^T = 8 DQ pieces, 2 DQ per
+  // wave (piece P = 2 DQ wave + u: K pieces first, DQ per row, each 32 / DQ keys; then V^T
+  // pieces, DQ per row, each 16 rows d); bias tile kb of this wave = 4 pieces. Past the last
+  // stage / tile a transfer repeats a real one into a buffer that is no longer read, so every
+  // wave always has the same transfers in flight.
+  const bf16* kbase = a.k + (bh * rows + r0) * np * D;
+  const bf16* vbase = a.vt + (bh * rows + r0) * D * np;
   const uint32_t k_lds = lds_addr(&lds.k[0][0][0]), v_lds = lds_addr(&lds.v[0][0][0]);
   auto kv_dma = [&](int64_t s, int buf) {
     const int64_t key0 = (s < nstage ? s : nstage - 1) * kFK;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int P = 4 * wave + u, rr = (P >> 1) & 3, i = P & 1;  // wave-uniform
-      if (P < 8) {
-        const int key = 16 * i + (lane >> 2), p = (lane & 3) ^ ((key >> 2) & 3);
-        dma16(kbase, (uint32_t)((((int64_t)rr * np + key0 + key) * 32 + 8 * p) * 2),
-              k_lds + (uint32_t)(((buf * kFR + rr) * kFK * 32 + 16 * i * 32) * 2));
+    for (int u = 0; u < 2 * DQ; ++u) {
+      const int P = 2 * DQ * wave + u;  // wave-uniform
+      if (P < 4 * DQ) {
+        const int rr = P / DQ, i = P % DQ;
+        const int key = (32 / DQ) * i + lane / (2 * DQ);
+        const int p = (lane % (2 * DQ)) ^ ((key >> (DQ == 1 ? 3 : 2)) & (2 * DQ - 1));
+        dma16(kbase, (uint32_t)((((int64_t)rr * np + key0 + key) * D + 8 * p) * 2),
+              k_lds + (uint32_t)(((buf * kFR + rr) * kFK * D + 512 * i) * 2));
       } else {
+        const int rr = (P - 4 * DQ) / DQ, i = (P - 4 * DQ) % DQ;
         const int d = 16 * i + (lane >> 2), p = (lane & 3) ^ ((d >> 2) & 3);
-        dma16(vbase, (uint32_t)((((int64_t)rr * 32 + d) * np + key0 + 8 * p) * 2),
-              v_lds + (uint32_t)(((buf * kFR + rr) * 32 * kFK + 16 * i * kFK) * 2));
+        dma16(vbase, (uint32_t)((((int64_t)rr * D + d) * np + key0 + 8 * p) * 2),
+              v_lds + (uint32_t)(((buf * kFR + rr) * D * kFK + 16 * i * kFK) * 2));
       }
     }
   };
-  const float* bias_w = bias + (bh * nb + (active ? jw / 32 : 0)) * nb * 1024;
+  const float* bias_w = a.bias + (bh * nb + (active ? jw / 32 : 0)) * nb * 1024;
   const uint32_t b_lds = lds_addr(&lds.bias[wave][0][0]);
   auto bias_dma = [&](int64_t kb) {
     const int64_t kt = kb < nb ? kb : nb - 1;
@@ -366,26 +366,23 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
 
   kv_dma(0, 0);
   bias_dma(0);
-  bf16x8 qa[kFR][2];
+  bf16x8 qa[kFR][DQ];
   float l[kFR];
   f32x16 O[kFR];
   const bf16x8 zero8 = {};
 #pragma unroll
   for (int rr = 0; rr < kFR; ++rr) {
-    if (active) {
-      const bf16* qrow = q + ((bh * rows + r0 + rr) * np + j) * 32;
-      qa[rr][0] = ld8(qrow + 8 * g);
-      qa[rr][1] = ld8(qrow + 16 + 8 * g);
-    } else {
-      qa[rr][0] = zero8;
-      qa[rr][1] = zero8;
-    }
+#pragma unroll
+    for (int f = 0; f < DQ; ++f)
+      qa[rr][f] = active ? ld8(a.q + ((bh * rows + r0 + rr) * np + j) * D + 16 * f + 8 * g) : zero8;
     l[rr] = 0.f;
     O[rr] = zero16();
   }
   // the q loads complete here, not inside the key loop (see settle)
 #pragma unroll
-  for (int rr = 0; rr < kFR; ++rr) asm volatile("" ::"v"(qa[rr][0]), "v"(qa[rr][1]));
+  for (int rr = 0; rr < kFR; ++rr)
+#pragma unroll
+    for (int f = 0; f < DQ; ++f) asm volatile("" ::"v"(qa[rr][f]));
   wait_vm_lds<0>();
   __syncthreads();
 
@@ -433,8 +430,9 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
         for (int u = 0; u < 2; ++u) {
           const int rr = rp + u;
           const bf16* kt = lds.k[sb][rr];
-          S[u] = mfma32(ld8(kt + koff(li, g)), qa[rr][0], bcur);
-          S[u] = mfma32(ld8(kt + koff(li, 2 + g)), qa[rr][1], S[u]);
+          S[u] = mfma32(ld8(kt + koff<DQ>(li, g)), qa[rr][0], bcur);
+#pragma unroll
+          for (int f = 1; f < DQ; ++f) S[u] = mfma32(ld8(kt + koff<DQ>(li, 2 * f + g)), qa[rr][f], S[u]);
         }
         bf16x8 p0[2], p1[2];
         float ts[2];
@@ -445,8 +443,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
           const int rr = rp + u;
           l[rr] += ts[u];
           const bf16* vtile = lds.v[sb][rr];
-          O[rr] = mfma32(ld8(vtile + voff(li, g)), p0[u], O[rr]);
-          O[rr] = mfma32(ld8(vtile + voff(li, 2 + g)), p1[u], O[rr]);
+          O[rr] = mfma32(ld8(vtile + voff(dl, g)), p0[u], O[rr]);
+          O[rr] = mfma32(ld8(vtile + voff(dl, 2 + g)), p1[u], O[rr]);
         }
       }
     }
@@ -463,8 +461,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
   // and the bias tiles straight from global memory (the rare path: rows whose sums left the
   // safe range of the fixed offset).
   auto exact_row = [&](int rr, f32x16& Orow, float& lrow) {
-    const bf16* krow = kbase + (int64_t)rr * np * 32 + li * 32;
-    const bf16* vrow = vbase + (int64_t)rr * 32 * np + (int64_t)li * np;
+    const bf16* krow = kbase + (int64_t)rr * np * D + li * D;
+    const bf16* vrow = vbase + (int64_t)rr * D * np + (int64_t)dl * np;
     auto logits = [&](int64_t kb) {
       f32x16 st;
 #pragma unroll
@@ -473,8 +471,9 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
 #pragma unroll
         for (int e = 0; e < 4; ++e) st[4 * v4 + e] = x[e];
       }
-      st = mfma32(ld8(krow + kb * 32 * 32 + 8 * g), qa[rr][0], st);
-      return mfma32(ld8(krow + kb * 32 * 32 + 16 + 8 * g), qa[rr][1], st);
+#pragma unroll
+      for (int f = 0; f < DQ; ++f) st = mfma32(ld8(krow + kb * 32 * D + 16 * f + 8 * g), qa[rr][f], st);
+      return st;
     };
     float mx = -INFINITY;
     for (int64_t kb = 0; kb < nb; ++kb) {
@@ -499,23 +498,36 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(
     lrow = ls;
   };
 
+  const bool qvalid = j < a.n_valid;
 #pragma unroll
   for (int rr = 0; rr < kFR; ++rr) {
+    const int64_t r = r0 + rr;
+    if (r >= a.rows_valid) continue;  // a padded row: nothing to store
     float lt = pair_sum(l[rr]);
-    if (__builtin_amdgcn_ballot_w64(!(lt < kSumHigh) || !(lt > kSumLow)) != 0) {
+    // padded queries (past n) take no part in the choice
+    if (__builtin_amdgcn_ballot_w64(qvalid && (!(lt < kSumHigh) || !(lt > kSumLow))) != 0) {
       exact_row(rr, O[rr], l[rr]);
       lt = pair_sum(l[rr]);
     }
-    const int64_t r = r0 + rr;
-    if (r >= rows_valid || j >= n_valid) continue;
+    if (!qvalid) continue;
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    bf16* dst = o + bidx * o_sb + r * o_sr + j * o_sj + h * 32;
+    const int64_t off = bidx * a.o_sb + r * a.o_sr + j * a.o_sj + h * D;
 #pragma unroll
     for (int qd = 0; qd < 4; ++qd) {
-      bf16x4 w;
+      const int d0 = 8 * qd + 4 * g;
+      if (d0 >= D) continue;
+      if (GATED) {
+        const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + off + d0);
+        f32x4 y;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) w[t] = (bf16)(O[rr][4 * qd + t] * inv);
-      st8<kNtFlash>(dst + 8 * qd + 4 * g, w);
+        for (int t = 0; t < 4; ++t) y[t] = O[rr][4 * qd + t] * inv * (float)gv[t];
+        *reinterpret_cast<f32x4*>(a.og + off + d0) = y;
+      } else {
+        bf16x4 w;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) w[t] = (bf16)(O[rr][4 * qd + t] * inv);
+        st8<kNtFlash>(a.o + off + d0, w);
+      }
     }
   }
 }
@@ -668,10 +680,19 @@ static int persistent_grid(int ntiles, int per_cu) {
 
 void launch_flash(const FlashArgs& a, hipStream_t stream) {
   const int64_t nqb = (a.np + 32 * kFW - 1) / (32 * kFW);
-  const int64_t blocks = nqb * (a.rows / kFR) * a.batch * a.heads;
-  flash_attn_bias<<<dim3((unsigned)blocks), 64 * kFW, 0, stream>>>(
-      a.q, a.k, a.vt, a.bias, a.o, a.heads, a.rows, a.np, a.rows_valid, a.n_valid, a.o_sb, a.o_sr,
-      a.o_sj, a.kstages);
+  const dim3 grid((unsigned)(nqb * (a.rows / kFR) * a.batch * a.heads));
+  const bool gated = a.og != nullptr;
+  if (a.dh == 16) {
+    if (gated)
+      flash_attn_bias<1, true><<<grid, 64 * kFW, 0, stream>>>(a);
+    else
+      flash_attn_bias<1, false><<<grid, 64 * kFW, 0, stream>>>(a);
+  } else {
+    if (gated)
+      flash_attn_bias<2, true><<<grid, 64 * kFW, 0, stream>>>(a);
+    else
+      flash_attn_bias<2, false><<<grid, 64 * kFW, 0, stream>>>(a);
+  }
 }
 
 void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
@@ -680,7 +701,7 @@ void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
   triattn_project<<<persistent_grid(tiles_p, 1), 512, 0, stream>>>(
       a.z, a.maskf, a.ln_w, a.ln_b, a.wqkv, a.wb, a.q, a.k, a.vt, a.bias, a.batch, a.n, np,
       a.starting, a.transposed_bias, a.eps);
-  FlashArgs f;
+  FlashArgs f{};
   f.q = a.q;
   f.k = a.k;
   f.vt = a.vt;

@@ -15,6 +15,9 @@
 // Logits are carried in log2 units: q is scaled by log2(e) / sqrt(dh) and the pair-bias
 // weights by log2(e), so the softmax uses exp2. Masked keys (and the padding keys past n)
 // get the finite logit kMaskedLogit: their weight is exactly 0 once any valid key is seen.
+#include <algorithm>
+#include <type_traits>
+
 #include "ffk_device.h"
 #include "ffk_kernels.h"
 
@@ -120,23 +123,14 @@ __device__ inline int64_t opm_msa_row(const RowGemmArgs& a, int64_t m) {
   return (b * a.depth + s) * a.n + j;
 }
 
-template <int EPI, int XSRC, int NO>
-__global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
-  constexpr int KS = kGemmWaves / NO;
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  float* red = reinterpret_cast<float*>(smem);  // [NO][KS - 1][64][16]
-  bf16* xs_hi = reinterpret_cast<bf16*>(smem + (kGemmWaves - NO) * 64 * 16 * sizeof(float));
-  const int xstride = a.K + 8;  // [32][K + 8]: rows 16 bytes apart modulo 256, conflict-free
-  bf16* xs_lo = xs_hi + 32 * xstride;
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, g = lane >> 5;
-  const int osub = wave / KS, part = wave % KS;
-  const int ot = blockIdx.y * NO + osub;
-  const bool active = ot * 32 < a.O;
-  const int64_t m0 = (int64_t)blockIdx.x * 32;
-  const int G = a.K / 64;
-
+// The weight row (fp32, K values) multiplied by row li of output tile ot, and the tile's
+// segment and first channel as the epilogue reads them (packed tiles: see kEpiTrimul and
+// kEpiSwiglu below).
+template <int EPI>
+__device__ inline const float* tile_weight_row(const RowGemmArgs& a, int ot, int li, int& seg, int& cbase) {
   const float* wr;
-  int seg = 0, cbase = 0;
+  seg = 0;
+  cbase = 0;
   if (EPI == kEpiApb) {
     const int cs = a.O / 4;
     seg = (ot * 32) / cs;
@@ -162,6 +156,255 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
   } else {
     wr = a.w0 + (int64_t)(ot * 32 + li) * a.K;
   }
+  return wr;
+}
+
+// The per-row value an epilogue reads from memory, once per row rather than per output tile:
+// kEpiTrimul's pair mask factor m_i m_k (symmetric, so the same for the transposed read).
+template <int EPI>
+__device__ __forceinline__ float row_pre(const RowGemmArgs& a, const int64_t m) {
+  if (EPI == kEpiTrimul) {
+    const int64_t gg = (int64_t)a.npm * a.npm;
+    const int64_t b = m / gg, rem = m - b * gg;
+    const int i = (int)(rem / a.npm), k = (int)(rem - (int64_t)i * a.npm);
+    return i < a.n && k < a.n && a.mask[b * a.n + i] && a.mask[b * a.n + k] ? 1.f : 0.f;
+  }
+  return 0.f;
+}
+
+// Epilogue of output tile ot for logical row m (< M): lane half g holds outputs
+// 32 ot + 8 v + 4 g + e in acc[4 v + e]. lb: the per-output biases (q_bias / gate_b of kEpiApb,
+// bias_out of kEpiResid) staged in LDS by output index, or NULL to read them from the arguments.
+// The loads an epilogue needs are all issued before its first store.
+template <int EPI>
+__device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16& acc, const int64_t m, const int ot,
+                                    const int seg, const int cbase, const int g, const float* lb,
+                                    const float pre) {
+  // the bias of output o (global index gi of src when not staged)
+  auto obias = [&](int o, const float* src, int gi) { return lb ? lb[o] : (src ? src[gi] : 0.f); };
+  if (EPI == kEpiApb && a.flash_rows > 0) {
+    const int cs = a.O / 4;
+    const int64_t bn = m / a.np;
+    const int j = (int)(m - bn * a.np);
+    const int64_t b = bn / a.n;
+    const int r = (int)(bn - b * a.n);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = cbase + 8 * v + 4 * g;  // 4 channels of one head (dh % 4 == 0)
+      const int o0 = 32 * ot + 8 * v + 4 * g;
+      const int hh = c / a.dh, d0 = c - hh * a.dh;
+      const int64_t blk = (b * a.heads + hh) * a.flash_rows + r;  // the (b, h, r) block
+      float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
+      if (seg == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = (y[e] + obias(o0 + e, a.q_bias, c + e)) * a.q_scale;
+        store4(a.q + (blk * a.np + j) * a.dh + d0, y[0], y[1], y[2], y[3]);
+      } else if (seg == 1) {
+        store4(a.k + (blk * a.np + j) * a.dh + d0, y[0], y[1], y[2], y[3]);
+      } else if (seg == 2) {
+        const int pos = vkey_pos(j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a.vt[(blk * a.dh + d0 + e) * a.np + pos] = (bf16)y[e];
+      } else if (j < a.n) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          y[e] = sigmoid_scaled((y[e] + obias(o0 + e, a.gate_b, c + e) + a.gate_bias) * -kLog2e);
+        store4(a.gate + (bn * a.n + j) * cs + c, y[0], y[1], y[2], y[3]);
+      }
+    }
+  } else if (EPI == kEpiApb) {
+    const int cs = a.O / 4;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = cbase + 8 * v + 4 * g;
+      const int o0 = 32 * ot + 8 * v + 4 * g;
+      float y0 = acc[4 * v], y1 = acc[4 * v + 1], y2 = acc[4 * v + 2], y3 = acc[4 * v + 3];
+      if (seg == 0) {
+        y0 += obias(o0, a.q_bias, c);
+        y1 += obias(o0 + 1, a.q_bias, c + 1);
+        y2 += obias(o0 + 2, a.q_bias, c + 2);
+        y3 += obias(o0 + 3, a.q_bias, c + 3);
+        y0 *= a.q_scale;
+        y1 *= a.q_scale;
+        y2 *= a.q_scale;
+        y3 *= a.q_scale;
+        store4(a.q + m * cs + c, y0, y1, y2, y3);
+      } else if (seg == 1) {
+        store4(a.k + m * cs + c, y0, y1, y2, y3);
+      } else if (seg == 2) {
+        const int64_t b = m / a.n;
+        const int key = (int)(m - b * a.n);
+        const int pos = vkey_pos(key);
+        const float ys[4] = {y0, y1, y2, y3};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int hh = (c + e) / a.dh, d = (c + e) - hh * a.dh;
+          a.vt[((b * a.heads + hh) * a.dh + d) * a.np + pos] = (bf16)ys[e];
+        }
+      } else {
+        const float nb = -kLog2e;
+        y0 += obias(o0, a.gate_b, c);
+        y1 += obias(o0 + 1, a.gate_b, c + 1);
+        y2 += obias(o0 + 2, a.gate_b, c + 2);
+        y3 += obias(o0 + 3, a.gate_b, c + 3);
+        y0 = sigmoid_scaled((y0 + a.gate_bias) * nb);
+        y1 = sigmoid_scaled((y1 + a.gate_bias) * nb);
+        y2 = sigmoid_scaled((y2 + a.gate_bias) * nb);
+        y3 = sigmoid_scaled((y3 + a.gate_bias) * nb);
+        store4(a.gate + m * cs + c, y0, y1, y2, y3);
+      }
+    }
+  } else if (EPI == kEpiPwa) {
+    const int hd = a.O / 2;
+    const int64_t bs = m / a.n;  // b S + s
+    const int j = (int)(m - bs * a.n);
+    const int64_t b = bs / a.depth, srow = bs - b * a.depth;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = cbase + 8 * v + 4 * g;  // 4 channels of one head (dh % 4 == 0)
+      float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
+      if (seg == 0) {
+        const int hh = c / a.dh, d0 = c - hh * a.dh;
+        bf16* dst = a.vt + (((b * a.heads + hh) * a.depth + srow) * a.dh + d0) * a.np + j;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[(int64_t)e * a.np] = (bf16)y[e];
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = sigmoid_scaled(-kLog2e * y[e]);
+        store4(a.gate + m * hd + c, y[0], y[1], y[2], y[3]);
+      }
+    }
+  } else if (EPI == kEpiOpm) {
+    const int64_t bj = m / a.sp;
+    const int s = (int)(m - bj * a.sp);
+    const int64_t b = bj / a.n;
+    const int j = (int)(bj - b * a.n);
+    const float keep = s < a.depth && a.rows_mask[(b * a.depth + s) * a.n + j] ? 1.f : 0.f;
+    const float* bias = seg == 0 ? a.bias0 : a.bias1;
+    bf16* dst = (seg == 0 ? a.lt : a.rt) + bj * 32 * a.sp + s;
+#pragma unroll
+    for (int v = 0; v < 4; ++v)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = 8 * v + 4 * g + e;
+        dst[(int64_t)c * a.sp] = (bf16)((acc[4 * v + e] + (bias ? bias[c] : 0.f)) * keep);
+      }
+    if (seg == 0 && g == 0) a.mt[bj * a.sp + s] = (bf16)keep;
+  } else if (EPI == kEpiTrimul) {
+    const int hid = a.O / 4;
+    const int64_t gg = (int64_t)a.npm * a.npm;
+    const int64_t b = m / gg, rem = m - b * gg;
+    const float keep = pre;  // the pair mask factor (row_pre)
+    bf16* plane = (seg == 0 ? a.pa : a.pb) + b * hid * gg + rem;
+#pragma unroll
+    for (int v = 0; v < 2; ++v)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int c = cbase + 8 * v + 4 * g + e;
+        const float proj = acc[4 * v + e] * keep;  // masked before the gate, as the reference
+        plane[(int64_t)c * gg] = (bf16)(proj * sigmoid_scaled(-kLog2e * acc[8 + 4 * v + e]));
+      }
+  } else if (EPI == kEpiStore32) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = ot * 32 + 8 * v + 4 * g;
+      f32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = acc[4 * v + e];
+      *reinterpret_cast<f32x4*>(a.h32 + m * a.O + c) = y;
+    }
+  } else if (EPI == kEpiGateResid) {
+    f32x4 yv[4];
+    bf16x4 rv[4];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = ot * 32 + 8 * v + 4 * g;
+      yv[v] = *reinterpret_cast<const f32x4*>(a.y32 + m * a.O + c);
+      if (a.residual) rv[v] = *reinterpret_cast<const bf16x4*>(a.res + m * a.O + c);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = ot * 32 + 8 * v + 4 * g;
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y[e] = yv[v][e] * sigmoid_scaled(-kLog2e * acc[4 * v + e]);
+        if (a.residual) y[e] += (float)rv[v][e];
+      }
+      store4(a.out + m * a.O + c, y[0], y[1], y[2], y[3]);
+    }
+  } else if (EPI == kEpiLinear) {
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = ot * 32 + 8 * v + 4 * g;
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float t = acc[4 * v + e] + (a.bias_out ? a.bias_out[c + e] : 0.f);
+        if (a.act == kActSigmoid)
+          t = sigmoid_scaled(-kLog2e * t);
+        else if (a.act == kActSilu)
+          t = t * sigmoid_scaled(-kLog2e * t);
+        else if (a.act == kActRelu)
+          t = fmaxf(t, 0.f);
+        y[e] = t;
+      }
+      if (a.y_f32) {
+        const f32x4 yv = {y[0], y[1], y[2], y[3]};
+        *reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + m * a.O + c) = yv;
+      } else {
+        store4(static_cast<bf16*>(a.y) + m * a.O + c, y[0], y[1], y[2], y[3]);
+      }
+    }
+  } else if (EPI == kEpiSwiglu) {
+    const int hid = a.O / 2;
+#pragma unroll
+    for (int v = 0; v < 2; ++v) {
+      f32x4 y;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float av = acc[4 * v + e], bv = acc[8 + 4 * v + e];
+        y[e] = av * sigmoid_scaled(-kLog2e * av) * bv;
+      }
+      *reinterpret_cast<f32x4*>(a.h32 + m * hid + ot * 16 + 8 * v + 4 * g) = y;
+    }
+  } else {
+    bf16x4 rv[4];
+    if (a.residual) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) rv[v] = *reinterpret_cast<const bf16x4*>(a.res + m * a.O + ot * 32 + 8 * v + 4 * g);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int c = ot * 32 + 8 * v + 4 * g;
+      float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y[e] += obias(c + e, a.bias_out, c + e);
+        if (a.residual) y[e] += (float)rv[v][e];
+      }
+      store4(a.out + m * a.O + c, y[0], y[1], y[2], y[3]);
+    }
+  }
+}
+
+template <int EPI, int XSRC, int NO>
+__global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
+  constexpr int KS = kGemmWaves / NO;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  float* red = reinterpret_cast<float*>(smem);  // [NO][KS - 1][64][16]
+  bf16* xs_hi = reinterpret_cast<bf16*>(smem + (kGemmWaves - NO) * 64 * 16 * sizeof(float));
+  const int xstride = a.K + 8;  // [32][K + 8]: rows 16 bytes apart modulo 256, conflict-free
+  bf16* xs_lo = xs_hi + 32 * xstride;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, g = lane >> 5;
+  const int osub = wave / KS, part = wave % KS;
+  const int ot = blockIdx.y * NO + osub;
+  const bool active = ot * 32 < a.O;
+  const int64_t m0 = (int64_t)blockIdx.x * 32;
+  const int G = a.K / 64;
+
+  int seg, cbase;
+  const float* wr = tile_weight_row<EPI>(a, ot, li, seg, cbase);
   wr += 32 * g;
   const float* x32 = a.x32 + mapped_row(a, m0 + li) * a.K + 32 * g;
 
@@ -273,207 +516,150 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
 
   const int64_t m = m0 + li;
   if (!active || m >= a.M) return;
-  if (EPI == kEpiApb && a.flash_rows > 0) {
-    const int cs = a.O / 4;
-    const int64_t bn = m / a.np;
-    const int j = (int)(m - bn * a.np);
-    const int64_t b = bn / a.n;
-    const int r = (int)(bn - b * a.n);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = cbase + 8 * v + 4 * g;  // 4 channels of one head (dh % 4 == 0)
-      const int hh = c / a.dh, d0 = c - hh * a.dh;
-      const int64_t blk = (b * a.heads + hh) * a.flash_rows + r;  // the (b, h, r) block
-      float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
-      if (seg == 0) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = (y[e] + (a.q_bias ? a.q_bias[c + e] : 0.f)) * a.q_scale;
-        store4(a.q + (blk * a.np + j) * a.dh + d0, y[0], y[1], y[2], y[3]);
-      } else if (seg == 1) {
-        store4(a.k + (blk * a.np + j) * a.dh + d0, y[0], y[1], y[2], y[3]);
-      } else if (seg == 2) {
-        const int pos = vkey_pos(j);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) a.vt[(blk * a.dh + d0 + e) * a.np + pos] = (bf16)y[e];
-      } else if (j < a.n) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          y[e] = sigmoid_scaled((y[e] + (a.gate_b ? a.gate_b[c + e] : 0.f) + a.gate_bias) * -kLog2e);
-        store4(a.gate + (bn * a.n + j) * cs + c, y[0], y[1], y[2], y[3]);
-      }
+  row_epilogue<EPI>(a, acc, m, ot, seg, cbase, g, nullptr, row_pre<EPI>(a, m));
+}
+
+// ---------------------------------------------------------------------------- streaming row GEMM
+// The products and epilogues of row_gemm for short rows (K = 64 or 128), as a persistent
+// kernel: each workgroup converts the weights to bf16 once (LDS, in output-tile order, rows
+// K + 8 elements apart so that the operand reads of 16 rows hit distinct banks), then every
+// wave walks whole 32-row tiles on its own, with no barrier in the loop. The next tile's input
+// rows are loaded while the current one is normalised, multiplied for all O / 32 output tiles
+// (activations as bf16 hi + lo, as row_gemm) and stored by the epilogue of each output tile.
+// Lane (li, g) holds row li's channels (K / 2) g .. (K / 2) g + K / 2 - 1; MFMA step s takes
+// channels (K / 2) g + 8 s .. + 7 of both operands.
+constexpr int kStreamWaves = 4;
+
+size_t row_stream_lds(int K, int O) {
+  return (size_t)O * (K + 8) * sizeof(bf16) + (size_t)(2 * K + O) * sizeof(float);
+}
+
+template <int EPI, int XSRC, int K>
+__global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
+  constexpr int KS = K / 16;  // MFMA steps
+  constexpr int KH = K / 2;   // channels per lane
+  constexpr int WS = K + 8;   // LDS row stride of the weight image (elements)
+  constexpr int NX = XSRC == kXLn ? KS : 2 * KS;  // 16-byte input pieces per lane
+  using XT = typename std::conditional<XSRC == kXLn, bf16x8, f32x4>::type;
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  bf16* wl = reinterpret_cast<bf16*>(smem);  // [O / 32][32][WS]
+  float* lnp = reinterpret_cast<float*>(smem + (size_t)a.O * WS * sizeof(bf16));  // weight, offset
+  float* lb = lnp + 2 * K;  // per-output biases (row_epilogue)
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, g = lane >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int idx = tid; idx < a.O * (K / 8); idx += 64 * kStreamWaves) {
+    const int row = idx / (K / 8), ch = 8 * (idx % (K / 8));
+    int seg, cbase;
+    const float* wr = tile_weight_row<EPI>(a, row >> 5, row & 31, seg, cbase);
+    *reinterpret_cast<bf16x8*>(wl + row * WS + ch) = cvt8(wr + ch);
+  }
+  for (int o = tid; o < a.O; o += 64 * kStreamWaves) {
+    float v = 0.f;
+    if (EPI == kEpiApb) {
+      const int cs = a.O / 4, seg = o / cs, c = o - seg * cs;
+      if (seg == 0 && a.q_bias) v = a.q_bias[c];
+      if (seg == 3 && a.gate_b) v = a.gate_b[c];
+    } else if (EPI == kEpiResid && a.bias_out) {
+      v = a.bias_out[o];
     }
-  } else if (EPI == kEpiApb) {
-    const int cs = a.O / 4;
+    lb[o] = v;
+  }
+  if (XSRC == kXLn) {
+    const bool plain = a.ln_plain != 0;
+    for (int c = tid; c < K; c += 64 * kStreamWaves) {
+      lnp[c] = a.ln_w && !plain ? a.ln_w[c] : 1.f;
+      lnp[K + c] = a.ln_b && !plain ? a.ln_b[c] : 0.f;
+    }
+  }
+  __syncthreads();
+
+  const int64_t tiles = (a.M + 31) / 32;
+  const int64_t stride = (int64_t)gridDim.x * kStreamWaves;
+  int64_t t = (int64_t)blockIdx.x * kStreamWaves + wave;
+  if (t >= tiles) return;
+  const float eps = XSRC == kXLn && a.eps_dev ? *a.eps_dev : a.eps;
+  const int ntile = a.O / 32;
+
+  // the input rows of a tile (a tile past the end re-reads the last one, so every load stays
+  // inside the input)
+  auto fetch = [&](XT* x, int64_t tile) __attribute__((always_inline)) {
+    const int64_t tt = tile < tiles ? tile : tiles - 1;
+    const int64_t row = mapped_row(a, tt * 32 + li);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = cbase + 8 * v + 4 * g;
-      float y0 = acc[4 * v], y1 = acc[4 * v + 1], y2 = acc[4 * v + 2], y3 = acc[4 * v + 3];
-      if (seg == 0) {
-        if (a.q_bias) {
-          y0 += a.q_bias[c];
-          y1 += a.q_bias[c + 1];
-          y2 += a.q_bias[c + 2];
-          y3 += a.q_bias[c + 3];
+    for (int i = 0; i < NX; ++i) {
+      if (XSRC == kXLn)
+        x[i] = *reinterpret_cast<const XT*>(a.ln_x + row * K + KH * g + 8 * i);
+      else
+        x[i] = *reinterpret_cast<const XT*>(a.x32 + row * K + KH * g + 4 * i);
+    }
+  };
+  auto process = [&](const XT* x, int64_t tile) __attribute__((always_inline)) {
+    bf16x8 xh[KS], xl[KS];
+    if (XSRC == kXLn) {
+      float s1 = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s1 += (float)x[s][e];
+      const bool plain = a.ln_plain != 0;
+      const float mean = plain ? 0.f : pair_sum(s1) * (1.f / K);
+      float s2 = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = (float)x[s][e] - mean;
+          s2 += d * d;
         }
-        y0 *= a.q_scale;
-        y1 *= a.q_scale;
-        y2 *= a.q_scale;
-        y3 *= a.q_scale;
-        store4(a.q + m * cs + c, y0, y1, y2, y3);
-      } else if (seg == 1) {
-        store4(a.k + m * cs + c, y0, y1, y2, y3);
-      } else if (seg == 2) {
-        const int64_t b = m / a.n;
-        const int key = (int)(m - b * a.n);
-        const int pos = vkey_pos(key);
-        const float ys[4] = {y0, y1, y2, y3};
+      const float rstd = plain ? 1.f : __builtin_amdgcn_rsqf(pair_sum(s2) * (1.f / K) + eps);
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        // read per tile: held across the loop, the affine would take K registers
+        int c = KH * g + 8 * s;
+        asm volatile("" : "+v"(c));
+        const f32x4 w0 = *reinterpret_cast<const f32x4*>(lnp + c);
+        const f32x4 w1 = *reinterpret_cast<const f32x4*>(lnp + c + 4);
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(lnp + K + c);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(lnp + K + c + 4);
+        f32x4 y0, y1;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int hh = (c + e) / a.dh, d = (c + e) - hh * a.dh;
-          a.vt[((b * a.heads + hh) * a.dh + d) * a.np + pos] = (bf16)ys[e];
+          y0[e] = ((float)x[s][e] - mean) * rstd * w0[e] + b0[e];
+          y1[e] = ((float)x[s][4 + e] - mean) * rstd * w1[e] + b1[e];
         }
-      } else {
-        const float nb = -kLog2e;
-        if (a.gate_b) {
-          y0 += a.gate_b[c];
-          y1 += a.gate_b[c + 1];
-          y2 += a.gate_b[c + 2];
-          y3 += a.gate_b[c + 3];
-        }
-        y0 = sigmoid_scaled((y0 + a.gate_bias) * nb);
-        y1 = sigmoid_scaled((y1 + a.gate_bias) * nb);
-        y2 = sigmoid_scaled((y2 + a.gate_bias) * nb);
-        y3 = sigmoid_scaled((y3 + a.gate_bias) * nb);
-        store4(a.gate + m * cs + c, y0, y1, y2, y3);
+        split8(y0, y1, xh[s], xl[s]);
       }
+    } else {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) split8(x[2 * s], x[2 * s + 1], xh[s], xl[s]);
     }
-  } else if (EPI == kEpiPwa) {
-    const int hd = a.O / 2;
-    const int64_t bs = m / a.n;  // b S + s
-    const int j = (int)(m - bs * a.n);
-    const int64_t b = bs / a.depth, srow = bs - b * a.depth;
+    const int64_t m = tile * 32 + li;
+    const float pre = m < a.M ? row_pre<EPI>(a, m) : 0.f;
+#pragma unroll 1
+    for (int ot = 0; ot < ntile; ++ot) {
+      const bf16* wt = wl + (ot * 32 + li) * WS + KH * g;
+      f32x16 acc = zero16();
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = cbase + 8 * v + 4 * g;  // 4 channels of one head (dh % 4 == 0)
-      float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
-      if (seg == 0) {
-        const int hh = c / a.dh, d0 = c - hh * a.dh;
-        bf16* dst = a.vt + (((b * a.heads + hh) * a.depth + srow) * a.dh + d0) * a.np + j;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) dst[(int64_t)e * a.np] = (bf16)y[e];
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = sigmoid_scaled(-kLog2e * y[e]);
-        store4(a.gate + m * hd + c, y[0], y[1], y[2], y[3]);
+      for (int s = 0; s < KS; ++s) {
+        const bf16x8 w = *reinterpret_cast<const bf16x8*>(wt + 8 * s);
+        acc = mfma32(w, xl[s], acc);
+        acc = mfma32(w, xh[s], acc);
       }
+      int seg, cbase;
+      (void)tile_weight_row<EPI>(a, ot, li, seg, cbase);
+      if (m < a.M) row_epilogue<EPI>(a, acc, m, ot, seg, cbase, g, lb, pre);
     }
-  } else if (EPI == kEpiOpm) {
-    const int64_t bj = m / a.sp;
-    const int s = (int)(m - bj * a.sp);
-    const int64_t b = bj / a.n;
-    const int j = (int)(bj - b * a.n);
-    const float keep = s < a.depth && a.rows_mask[(b * a.depth + s) * a.n + j] ? 1.f : 0.f;
-    const float* bias = seg == 0 ? a.bias0 : a.bias1;
-    bf16* dst = (seg == 0 ? a.lt : a.rt) + bj * 32 * a.sp + s;
+  };
+
+  XT cur[NX], nxt[NX];
+  fetch(cur, t);
+  while (true) {
+    fetch(nxt, t + stride);
+    process(cur, t);
+    t += stride;
+    if (t >= tiles) break;
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int c = 8 * v + 4 * g + e;
-        dst[(int64_t)c * a.sp] = (bf16)((acc[4 * v + e] + (bias ? bias[c] : 0.f)) * keep);
-      }
-    if (seg == 0 && g == 0) a.mt[bj * a.sp + s] = (bf16)keep;
-  } else if (EPI == kEpiTrimul) {
-    const int hid = a.O / 4;
-    const int64_t gg = (int64_t)a.npm * a.npm;
-    const int64_t b = m / gg, rem = m - b * gg;
-    const int i = (int)(rem / a.npm), k = (int)(rem - (int64_t)i * a.npm);
-    // the pair mask m_i m_k is symmetric: the same for (i, k) and the transposed read (k, i)
-    const float keep = i < a.n && k < a.n && a.mask[b * a.n + i] && a.mask[b * a.n + k] ? 1.f : 0.f;
-    bf16* plane = (seg == 0 ? a.pa : a.pb) + b * hid * gg + rem;
-#pragma unroll
-    for (int v = 0; v < 2; ++v)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int c = cbase + 8 * v + 4 * g + e;
-        const float proj = acc[4 * v + e] * keep;  // masked before the gate, as the reference
-        plane[(int64_t)c * gg] = (bf16)(proj * sigmoid_scaled(-kLog2e * acc[8 + 4 * v + e]));
-      }
-  } else if (EPI == kEpiStore32) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = ot * 32 + 8 * v + 4 * g;
-      f32x4 y;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = acc[4 * v + e];
-      *reinterpret_cast<f32x4*>(a.h32 + m * a.O + c) = y;
-    }
-  } else if (EPI == kEpiGateResid) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = ot * 32 + 8 * v + 4 * g;
-      const f32x4 yv = *reinterpret_cast<const f32x4*>(a.y32 + m * a.O + c);
-      float y[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = yv[e] * sigmoid_scaled(-kLog2e * acc[4 * v + e]);
-      if (a.residual) {
-        const bf16x4 r = *reinterpret_cast<const bf16x4*>(a.res + m * a.O + c);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] += (float)r[e];
-      }
-      store4(a.out + m * a.O + c, y[0], y[1], y[2], y[3]);
-    }
-  } else if (EPI == kEpiLinear) {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = ot * 32 + 8 * v + 4 * g;
-      float y[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        float t = acc[4 * v + e] + (a.bias_out ? a.bias_out[c + e] : 0.f);
-        if (a.act == kActSigmoid)
-          t = sigmoid_scaled(-kLog2e * t);
-        else if (a.act == kActSilu)
-          t = t * sigmoid_scaled(-kLog2e * t);
-        else if (a.act == kActRelu)
-          t = fmaxf(t, 0.f);
-        y[e] = t;
-      }
-      if (a.y_f32) {
-        const f32x4 yv = {y[0], y[1], y[2], y[3]};
-        *reinterpret_cast<f32x4*>(static_cast<float*>(a.y) + m * a.O + c) = yv;
-      } else {
-        store4(static_cast<bf16*>(a.y) + m * a.O + c, y[0], y[1], y[2], y[3]);
-      }
-    }
-  } else if (EPI == kEpiSwiglu) {
-    const int hid = a.O / 2;
-#pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      f32x4 y;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float av = acc[4 * v + e], bv = acc[8 + 4 * v + e];
-        y[e] = av * sigmoid_scaled(-kLog2e * av) * bv;
-      }
-      *reinterpret_cast<f32x4*>(a.h32 + m * hid + ot * 16 + 8 * v + 4 * g) = y;
-    }
-  } else {
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = ot * 32 + 8 * v + 4 * g;
-      float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
-      if (a.bias_out) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] += a.bias_out[c + e];
-      }
-      if (a.residual) {
-        const bf16x4 r = *reinterpret_cast<const bf16x4*>(a.res + m * a.O + c);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] += (float)r[e];
-      }
-      store4(a.out + m * a.O + c, y[0], y[1], y[2], y[3]);
-    }
+    for (int i = 0; i < NX; ++i) cur[i] = nxt[i];
   }
 }
 
@@ -763,7 +949,43 @@ void launch_row_gemm_t(const RowGemmArgs& a, hipStream_t stream) {
 // Tile shapes: the LayerNorm-fed GEMMs give each workgroup several output tiles (the tile is
 // normalised once per workgroup); the fp32-fed ones split k 8 ways when k is long, and give the
 // waves separate output tiles when k has fewer groups than waves.
+template <int EPI, int XSRC, int K>
+void launch_row_stream_t(const RowGemmArgs& a, hipStream_t stream) {
+  const size_t lds = row_stream_lds(K, a.O);
+  auto kernel = row_stream<EPI, XSRC, K>;
+  if (lds > 65536)
+    (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  const int64_t tiles = (a.M + 31) / 32;
+  const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(4, (160 * 1024) / (int64_t)lds));
+  int64_t blocks = std::min<int64_t>((tiles + kStreamWaves - 1) / kStreamWaves, cu_count() * per_cu);
+  kernel<<<dim3((unsigned)std::max<int64_t>(1, blocks)), 64 * kStreamWaves, lds, stream>>>(a);
+}
+
+// The streaming kernel's cases: the pair path's short rows, the weights fitting in LDS.
+template <int EPI, int XSRC>
+bool launch_row_stream(const RowGemmArgs& a, hipStream_t stream) {
+  if (row_stream_lds(a.K, a.O) > 80 * 1024 || a.M < 32 * 256) return false;
+  if (a.K == 64)
+    launch_row_stream_t<EPI, XSRC, 64>(a, stream);
+  else if (a.K == 128)
+    launch_row_stream_t<EPI, XSRC, 128>(a, stream);
+  else
+    return false;
+  return true;
+}
+
 void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream) {
+  // short rows of the pair path: the streaming kernel (false: not a case it takes)
+  if (xsrc == kXLn) {
+    if (epi == kEpiApb && launch_row_stream<kEpiApb, kXLn>(a, stream)) return;
+    if (epi == kEpiTrimul && launch_row_stream<kEpiTrimul, kXLn>(a, stream)) return;
+    if (epi == kEpiStore32 && launch_row_stream<kEpiStore32, kXLn>(a, stream)) return;
+    if (epi == kEpiGateResid && launch_row_stream<kEpiGateResid, kXLn>(a, stream)) return;
+    if (epi == kEpiSwiglu && launch_row_stream<kEpiSwiglu, kXLn>(a, stream)) return;
+  } else if (epi == kEpiResid && launch_row_stream<kEpiResid, kXF32>(a, stream)) {
+    return;
+  }
   if (epi == kEpiApb && xsrc == kXLn)
     launch_row_gemm_t<kEpiApb, kXLn, 4>(a, stream);
   else if (epi == kEpiSwiglu && xsrc == kXLn)

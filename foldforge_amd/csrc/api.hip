@@ -173,7 +173,8 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
     w.B = cv.take<bf16>(plane);
     w.P = cv.take<bf16>(plane);
     w.Pt = cv.take<bf16>((size_t)batch * n * n * h);
-    w.y32 = cv.take<float>((size_t)batch * n * n * c);
+    // the fp32 output projection between the row GEMMs (pair and hidden width 64: one kernel)
+    if (!(c == 64 && h == 64)) w.y32 = cv.take<float>((size_t)batch * n * n * c);
     w.bytes = cv.used;
     return w;
   }
@@ -513,6 +514,24 @@ int32_t ffk_triangle_multiplication(
     launch_row_gemm(p, kEpiTrimul, kXLn, st);
     launch_trimul_contract(w.A, w.B, w.P, batch * d_hidden, (int)np, st);
     launch_planes_to_rows(w.P, w.Pt, (int)batch, d_hidden, (int)n, (int)np, st);
+    if (d_pair == 64 && d_hidden == 64) {
+      TrimulRowsArgs r{};
+      r.p = w.Pt;
+      r.z = static_cast<const bf16*>(z);
+      r.lno_w = ln_out_w;
+      r.lno_b = ln_out_b;
+      r.ln_w = ln_pair_w;
+      r.ln_b = ln_pair_b;
+      r.w_out = w_out;
+      r.w_gate = w_gate;
+      r.eps_out = eps_out;
+      r.out = static_cast<bf16*>(out);
+      r.rows = batch * n * n;
+      r.residual = residual ? 1 : 0;
+      r.eps = eps;
+      launch_trimul_out_rows64(r, st);
+      return check_launch("triangle_multiplication");
+    }
     RowGemmArgs o{};
     o.ln_x = w.Pt;
     o.ln_w = ln_out_w;

@@ -56,6 +56,19 @@ __device__ __forceinline__ int64_t bias_index(int64_t bh, int64_t nb, int64_t qu
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
+// 8 consecutive fp32 values (16-byte aligned) -> one bf16 MFMA operand.
+__device__ __forceinline__ bf16x8 cvt8(const float* p) {
+  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
+  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
+  bf16x8 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    r[e] = (bf16)a[e];
+    r[4 + e] = (bf16)b[e];
+  }
+  return r;
+}
+
 // Stores of intermediates that the next kernel reads once. Bit k of FFK_NT_MASK makes family k
 // use non-temporal (streaming) stores: 1 projections (A, B, q, k, v^T), 2 contraction (P),
 // 4 output kernels (z), 8 flash core (o). Only the output kernels stream by default: streaming

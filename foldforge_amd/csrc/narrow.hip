@@ -2,6 +2,8 @@
 // widths of 64 or 256, triangle-attention heads of 16): the shared pieces below, the rest is
 // the token-row GEMMs of single.hip, the contraction of trimul.hip and the attention of
 // single.hip, composed by api.hip.
+#include <algorithm>
+
 #include "ffk_device.h"
 #include "ffk_kernels.h"
 
@@ -44,6 +46,155 @@ __global__ __launch_bounds__(256) void planes_to_rows(const bf16* __restrict__ p
   }
 }
 
+// Generic-width triangle multiplication output for pair width 64 and hidden width 64:
+//   out = z + (LN_out(p) W_out^T) * sigmoid(LN_pair(z) W_g^T)
+// over the contraction's token rows p [batch n n][64], as one streaming kernel (so the
+// projection never round-trips through memory). Each workgroup converts both weights to bf16
+// once (LDS, rows 72 elements apart); every wave then walks tiles of 32 consecutive tokens on
+// its own, loading the next tile's p and z rows while it works on the current one. Lane
+// (li, g) holds token li's channels 32 g .. 32 g + 31 of p and of z; activations enter both
+// products as bf16 hi + lo. The weight rows are stored permuted (row r = 8 v + 4 g + e of output
+// tile t holds channel 32 g + 16 t + 4 v + e), so a lane's accumulators hold the output
+// channels of its own half-row: the two products meet each other and z in registers, and the
+// lane writes its 32 output channels as four 16-byte pieces.
+constexpr int kTmoWaves = 4;
+constexpr int kTmoWs = 72;  // LDS row stride (elements)
+struct __attribute__((aligned(16))) TmoLds {
+  bf16 wo[64 * kTmoWs];
+  bf16 wg[64 * kTmoWs];
+  float lnow[64], lnob[64], lnw[64], lnb[64];
+};
+
+__device__ __forceinline__ int tmo_perm(int row) {
+  const int t = row >> 5, r = row & 31;
+  return 32 * ((r >> 2) & 1) + 16 * t + 4 * (r >> 3) + (r & 3);
+}
+
+__global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_rows64(TrimulRowsArgs a) {
+  __shared__ TmoLds lds;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int idx = tid; idx < 2 * 64 * 8; idx += 64 * kTmoWaves) {
+    const int which = idx >> 9, row = (idx >> 3) & 63, ch = 8 * (idx & 7);
+    const float* src = (which ? a.w_gate : a.w_out) + tmo_perm(row) * 64 + ch;
+    *reinterpret_cast<bf16x8*>((which ? lds.wg : lds.wo) + row * kTmoWs + ch) = cvt8(src);
+  }
+  if (tid < 64) {
+    lds.lnow[tid] = a.lno_w[tid];
+    lds.lnob[tid] = a.lno_b[tid];
+    lds.lnw[tid] = a.ln_w[tid];
+    lds.lnb[tid] = a.ln_b[tid];
+  }
+  __syncthreads();
+
+  const int64_t tiles = (a.rows + 31) / 32;
+  const int64_t stride = (int64_t)gridDim.x * kTmoWaves;
+  int64_t t = (int64_t)blockIdx.x * kTmoWaves + wave;
+  if (t >= tiles) return;
+  const float eps_out = a.eps_out ? *a.eps_out : a.eps;
+
+  auto fetch = [&](int64_t tile, bf16x8* pr, bf16x8* zr) __attribute__((always_inline)) {
+    const int64_t m = min(min(tile, tiles - 1) * 32 + li, a.rows - 1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) pr[s] = ld8(a.p + m * 64 + 32 * g + 8 * s);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) zr[s] = ld8(a.z + m * 64 + 32 * g + 8 * s);
+  };
+  // LayerNorm of a lane's 32 channels (the row's other 32 in lane li + 32) -> bf16 hi / lo
+  auto norm = [&](const bf16x8* x, const float* w, const float* b, float eps, bf16x8* hi,
+                  bf16x8* lo) __attribute__((always_inline)) {
+    float s1 = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s1 += (float)x[s][e];
+    const float mean = pair_sum(s1) * (1.f / 64);
+    float s2 = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = (float)x[s][e] - mean;
+        s2 += d * d;
+      }
+    const float rstd = __builtin_amdgcn_rsqf(pair_sum(s2) * (1.f / 64) + eps);
+    // the affine is read per tile (held, it would take 64 registers per norm)
+    int cb = 32 * g;
+    asm volatile("" : "+v"(cb));
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(w + cb + 8 * s);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(w + cb + 8 * s + 4);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(b + cb + 8 * s);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(b + cb + 8 * s + 4);
+      f32x4 y0, y1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y0[e] = ((float)x[s][e] - mean) * rstd * w0[e] + b0[e];
+        y1[e] = ((float)x[s][4 + e] - mean) * rstd * w1[e] + b1[e];
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hi[s][e] = (bf16)y0[e];
+        hi[s][4 + e] = (bf16)y1[e];
+        lo[s][e] = (bf16)(y0[e] - (float)hi[s][e]);
+        lo[s][4 + e] = (bf16)(y1[e] - (float)hi[s][4 + e]);
+      }
+    }
+  };
+  auto process = [&](int64_t tile, const bf16x8* pr, const bf16x8* zr) __attribute__((always_inline)) {
+    bf16x8 ph[4], pl[4], zh[4], zl[4];
+    norm(pr, lds.lnow, lds.lnob, eps_out, ph, pl);
+    norm(zr, lds.lnw, lds.lnb, a.eps, zh, zl);
+    const int64_t m = tile * 32 + li;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      const bf16* wor = lds.wo + (32 * t2 + li) * kTmoWs + 32 * g;
+      const bf16* wgr = lds.wg + (32 * t2 + li) * kTmoWs + 32 * g;
+      f32x16 ay = zero16(), ag = zero16();
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 wo8 = ld8(wor + 8 * s), wg8 = ld8(wgr + 8 * s);
+        ay = mfma32(wo8, pl[s], ay);
+        ay = mfma32(wo8, ph[s], ay);
+        ag = mfma32(wg8, zl[s], ag);
+        ag = mfma32(wg8, zh[s], ag);
+      }
+      bf16x8 y[2];
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = 16 * t2 + 4 * v + e;  // channel within the lane's half
+          const float r = a.residual ? (float)zr[c >> 3][c & 7] : 0.f;
+          y[v >> 1][4 * (v & 1) + e] =
+              (bf16)(ay[4 * v + e] * sigmoid_scaled(-kLog2e * ag[4 * v + e]) + r);
+        }
+      if (m < a.rows) {
+        bf16* dst = a.out + m * 64 + 32 * g + 16 * t2;
+        *reinterpret_cast<bf16x8*>(dst) = y[0];
+        *reinterpret_cast<bf16x8*>(dst + 8) = y[1];
+      }
+    }
+  };
+
+  // two register buffers used in turn: the next tile's rows load while the current one is
+  // processed
+  bf16x8 p0[4], z0[4], p1[4], z1[4];
+  fetch(t, p0, z0);
+  while (true) {
+    fetch(t + stride, p1, z1);
+    process(t, p0, z0);
+    t += stride;
+    if (t >= tiles) break;
+    fetch(t + stride, p0, z0);
+    process(t, p1, z1);
+    t += stride;
+    if (t >= tiles) break;
+  }
+}
+
 }  // namespace
 
 // out[b][i][j][:] = (base ? base[b][i][j][:] : 0) + t[b][j][i][:]: one thread per 8 channels
@@ -81,6 +232,12 @@ void launch_planes_to_rows(const bf16* planes, bf16* rows, int batch, int hid, i
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   planes_to_rows<<<dim3((unsigned)((n + kRowTile - 1) / kRowTile), (unsigned)n, (unsigned)batch),
                    256, lds, stream>>>(planes, rows, hid, n, np);
+}
+
+void launch_trimul_out_rows64(const TrimulRowsArgs& a, hipStream_t stream) {
+  const int64_t tiles = (a.rows + 31) / 32;
+  const int64_t blocks = std::min<int64_t>((tiles + kTmoWaves - 1) / kTmoWaves, (int64_t)cu_count() * 6);
+  trimul_out_rows64<<<dim3((unsigned)std::max<int64_t>(1, blocks)), 64 * kTmoWaves, 0, stream>>>(a);
 }
 
 void launch_pair_add_transposed(const bf16* base, const bf16* t, bf16* out, int64_t batch, int n,

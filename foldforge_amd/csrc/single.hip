@@ -34,19 +34,6 @@ __device__ __forceinline__ bf16x8 zero8() {
   return r;
 }
 
-// 8 consecutive fp32 weights -> one bf16 MFMA operand.
-__device__ __forceinline__ bf16x8 cvt8(const float* p) {
-  const f32x4 a = *reinterpret_cast<const f32x4*>(p);
-  const f32x4 b = *reinterpret_cast<const f32x4*>(p + 4);
-  bf16x8 r;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    r[e] = (bf16)a[e];
-    r[4 + e] = (bf16)b[e];
-  }
-  return r;
-}
-
 // Position of key `key` inside the v^T rows: index bits 2 and 3 exchanged, so that the 8
 // consecutive positions a lane loads are the 8 keys its P^T operand holds.
 __device__ __forceinline__ int vkey_pos(int key) {
@@ -651,15 +638,19 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
     }
   };
 
-  XT cur[NX], nxt[NX];
-  fetch(cur, t);
+  // two register buffers used in turn: the next tile's rows load while the current one is
+  // processed
+  XT x0[NX], x1[NX];
+  fetch(x0, t);
   while (true) {
-    fetch(nxt, t + stride);
-    process(cur, t);
+    fetch(x1, t + stride);
+    process(x0, t);
     t += stride;
     if (t >= tiles) break;
-#pragma unroll
-    for (int i = 0; i < NX; ++i) cur[i] = nxt[i];
+    fetch(x0, t + stride);
+    process(x1, t);
+    t += stride;
+    if (t >= tiles) break;
   }
 }
 

@@ -193,7 +193,7 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
 int64_t pad32(int64_t n);
 
 struct TriattnWs {
-  bf16 *wqkv, *wb, *wg, *wo, *wo_t, *q, *k, *vt, *o, *gate, *tbuf;
+  bf16 *wqkv, *wb, *wg, *wo, *wo_t, *q, *k, *vt, *o, *gate, *tbuf, *ogb;
   float *bias, *og, *maskf;
   int* kst;
   size_t bytes;
@@ -220,6 +220,9 @@ TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d
       w.vt = cv.take<bf16>(blk);
       w.gate = cv.take<bf16>(tok);
       w.bias = cv.take<float>((size_t)batch * heads * np32 * np32);
+      w.ogb = cv.take<bf16>(tok);  // the gated output, bf16
+      w.bytes = cv.used;
+      return w;
     } else {
       w.q = cv.take<bf16>(tok);
       w.k = cv.take<bf16>(tok);
@@ -254,7 +257,8 @@ bool transition_fused(int d, int factor) { return d == 128 && factor == 4; }
 
 struct TransitionWs {
   bf16* w;
-  float* h;
+  float* h;   // hidden rows wider than the LayerNorm-fed GEMM's k limit: fp32
+  bf16* hb;   // else bf16 (the squeeze reads them as plain bf16 rows)
   size_t bytes;
 };
 TransitionWs transition_ws(void* ws, int64_t rows, int d, int factor) {
@@ -262,6 +266,8 @@ TransitionWs transition_ws(void* ws, int64_t rows, int d, int factor) {
   TransitionWs w{};
   if (transition_fused(d, factor)) {
     w.w = cv.take<bf16>((size_t)3 * factor * d * d);
+  } else if ((int64_t)factor * d <= kLnGemmMaxK) {
+    w.hb = cv.take<bf16>((size_t)rows * factor * d);
   } else {
     w.h = cv.take<float>((size_t)rows * factor * d);
   }
@@ -365,9 +371,12 @@ int32_t transition_run(const TransitionWs& w, const void* x, const float* ln_w, 
     g.K = d;
     g.O = 2 * factor * d;
     g.h32 = w.h;
+    g.h16 = w.hb;
     launch_row_gemm(g, kEpiSwiglu, kXLn, st);
     RowGemmArgs s{};
     s.x32 = w.h;
+    s.ln_x = w.hb;
+    s.ln_plain = 1;
     s.w0 = wsq;
     s.M = rows;
     s.K = factor * d;
@@ -375,7 +384,7 @@ int32_t transition_run(const TransitionWs& w, const void* x, const float* ln_w, 
     s.res = static_cast<const bf16*>(x);
     s.out = static_cast<bf16*>(out);
     s.residual = residual ? 1 : 0;
-    launch_row_gemm(s, kEpiResid, kXF32, st);
+    launch_row_gemm(s, kEpiResid, w.hb ? kXLn : kXF32, st);
     return check_launch("transition");
   }
   launch_transition_pack(wa, wb, wsq, w.w, st);
@@ -716,7 +725,7 @@ int32_t ffk_triangle_attention(
       f.kstages = nullptr;
       f.dh = d_head;
       f.gate = w.gate;
-      f.og = w.og;
+      f.og = w.ogb;
       f.o_sb = n * n * hd;
       f.o_sr = n * hd;
       f.o_sj = hd;
@@ -742,6 +751,8 @@ int32_t ffk_triangle_attention(
     auto project = [&](const float* wo, const float* bo, bf16* dst, int res) {
       RowGemmArgs o{};
       o.x32 = w.og;
+      o.ln_x = w.ogb;
+      o.ln_plain = 1;
       o.w0 = wo;
       o.bias_out = bo;
       o.M = batch * n * n;
@@ -752,7 +763,7 @@ int32_t ffk_triangle_attention(
       o.res = static_cast<const bf16*>(z);
       o.out = dst;
       o.residual = res;
-      launch_row_gemm(o, kEpiResid, kXF32, st);
+      launch_row_gemm(o, kEpiResid, flash ? kXLn : kXF32, st);
     };
     bf16* dst = static_cast<bf16*>(out);
     if (form == kTriattnUntransposed) {

@@ -79,11 +79,11 @@ struct FlashArgs {
   const int* kstages;
   // Head width 16 or 32: q, k [batch heads][rows][np][dh], v^T [batch heads][rows][dh][np]
   // (keys permuted as the 32-wide layout). With og set, the kernel writes the gated output
-  // og = gate * o (fp32) instead of o, at the same strides (in elements) plus h dh + d, and
+  // og = gate * o (bf16) instead of o, at the same strides (in elements) plus h dh + d, and
   // reads the gate (bf16) at that offset too.
   int dh = 32;
   const bf16* gate = nullptr;
-  float* og = nullptr;
+  bf16* og = nullptr;
 };
 void launch_flash(const FlashArgs& a, hipStream_t stream);
 
@@ -105,7 +105,7 @@ void launch_transition(const TransitionArgs& a, hipStream_t stream);
 // Token-row GEMM out[m][o] = sum_k W[o][k] x[m][k] (single track, single.hip) with one of
 // three epilogues, x either LayerNorm(ln_x) (kXLn, K <= kLnGemmMaxK) or fp32 rows x32 (kXF32).
 // K % 64 == 0, O % 32 == 0; weights are the fp32 parameters. Pairs served: (kEpiApb, kXLn),
-// (kEpiSwiglu, kXLn), (kEpiResid, kXF32), (kEpiPwa, kXLn), (kEpiOpm, kXLn), (kEpiTrimul, kXLn),
+// (kEpiSwiglu, kXLn), (kEpiResid, kXF32), (kEpiResid, kXLn), (kEpiPwa, kXLn), (kEpiOpm, kXLn), (kEpiTrimul, kXLn),
 // (kEpiStore32, kXLn), (kEpiGateResid, kXLn), (kEpiLinear, kXLn).
 enum {
   kEpiApb = 0,
@@ -174,6 +174,7 @@ struct RowGemmArgs {
   int tmap, npm;
   const float* y32;  // kEpiGateResid: [M][O]
   float* h32;  // kEpiSwiglu: [M][hid] = silu(a) * b; kEpiStore32: [M][O] = y
+  bf16* h16;   // kEpiSwiglu: the hidden rows in bf16 instead (h32 unused)
   const bf16* res;  // kEpiResid: out = res + y (residual) or y, y with bias_out when set
   bf16* out;
   int residual;

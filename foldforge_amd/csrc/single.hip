@@ -353,7 +353,10 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
         const float av = acc[4 * v + e], bv = acc[8 + 4 * v + e];
         y[e] = av * sigmoid_scaled(-kLog2e * av) * bv;
       }
-      *reinterpret_cast<f32x4*>(a.h32 + m * hid + ot * 16 + 8 * v + 4 * g) = y;
+      if (a.h16)
+        store4(a.h16 + m * hid + ot * 16 + 8 * v + 4 * g, y[0], y[1], y[2], y[3]);
+      else
+        *reinterpret_cast<f32x4*>(a.h32 + m * hid + ot * 16 + 8 * v + 4 * g) = y;
     }
   } else {
     bf16x4 rv[4];
@@ -956,7 +959,7 @@ void launch_row_stream_t(const RowGemmArgs& a, hipStream_t stream) {
 // The streaming kernel's cases: the pair path's short rows, the weights fitting in LDS.
 template <int EPI, int XSRC>
 bool launch_row_stream(const RowGemmArgs& a, hipStream_t stream) {
-  if (row_stream_lds(a.K, a.O) > 80 * 1024 || a.M < 32 * 256) return false;
+  if (row_stream_lds(a.K, a.O) > 80 * 1024) return false;
   if (a.K == 64)
     launch_row_stream_t<EPI, XSRC, 64>(a, stream);
   else if (a.K == 128)
@@ -974,6 +977,7 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
     if (epi == kEpiStore32 && launch_row_stream<kEpiStore32, kXLn>(a, stream)) return;
     if (epi == kEpiGateResid && launch_row_stream<kEpiGateResid, kXLn>(a, stream)) return;
     if (epi == kEpiSwiglu && launch_row_stream<kEpiSwiglu, kXLn>(a, stream)) return;
+    if (epi == kEpiResid && launch_row_stream<kEpiResid, kXLn>(a, stream)) return;
   } else if (epi == kEpiResid && launch_row_stream<kEpiResid, kXF32>(a, stream)) {
     return;
   }
@@ -993,7 +997,14 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
     else
       launch_row_gemm_t<kEpiResid, kXF32, 8>(a, stream);
   }
-  else if (epi == kEpiPwa && xsrc == kXLn)
+  else if (epi == kEpiResid && xsrc == kXLn) {
+    if (a.O >= 256)
+      launch_row_gemm_t<kEpiResid, kXLn, 8>(a, stream);
+    else if (a.O >= 128)
+      launch_row_gemm_t<kEpiResid, kXLn, 4>(a, stream);
+    else
+      launch_row_gemm_t<kEpiResid, kXLn, 2>(a, stream);
+  } else if (epi == kEpiPwa && xsrc == kXLn)
     launch_row_gemm_t<kEpiPwa, kXLn, 8>(a, stream);
   else if (epi == kEpiOpm && xsrc == kXLn)
     launch_row_gemm_t<kEpiOpm, kXLn, 2>(a, stream);

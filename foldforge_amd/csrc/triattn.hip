@@ -293,8 +293,8 @@ __device__ __forceinline__ float exp_pack(const f32x16& S, bf16x8& p0, bf16x8& p
 }
 
 // grid (ceil(np / 128) * (rows / 4) * batch * heads) workgroups, renumbered per XCD;
-// block 256 = 4 waves x 32 queries, 4 attention rows. GATED: the output is og = gate * o
-// (fp32), else o (bf16).
+// block 256 = 4 waves x 32 queries, 4 attention rows. GATED: the output is og = gate * o,
+// else o (bf16 either way).
 template <int DQ, bool GATED>
 __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
   constexpr int D = 16 * DQ;  // head width
@@ -518,10 +518,10 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
       if (d0 >= D) continue;
       if (GATED) {
         const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + off + d0);
-        f32x4 y;
+        bf16x4 y;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) y[t] = O[rr][4 * qd + t] * inv * (float)gv[t];
-        *reinterpret_cast<f32x4*>(a.og + off + d0) = y;
+        for (int t = 0; t < 4; ++t) y[t] = (bf16)(O[rr][4 * qd + t] * inv * (float)gv[t]);
+        *reinterpret_cast<bf16x4*>(a.og + off + d0) = y;
       } else {
         bf16x4 w;
 #pragma unroll

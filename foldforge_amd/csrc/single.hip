@@ -146,6 +146,29 @@ __device__ inline const float* tile_weight_row(const RowGemmArgs& a, int ot, int
   return wr;
 }
 
+__device__ __forceinline__ int stage_row(int r) { return r ^ ((r >> 2) & 1); }
+
+// A 32-row tile inside one run of an epilogue's row decomposition m = q L + rem (kEpiApb's flash
+// layout: L = np, q = b n + r, rem = the key j; kEpiTrimul: L = npm^2, q = b), computed once per
+// tile from its first row (uniform across the wave) instead of per lane and output tile.
+struct TileRun {
+  int64_t m0, q, rem0, b;
+  int r;
+};
+template <int EPI>
+__device__ __forceinline__ TileRun tile_run(const RowGemmArgs& a, int64_t m0) {
+  TileRun t{};
+  t.m0 = m0;
+  const int64_t len = EPI == kEpiTrimul ? (int64_t)a.npm * a.npm : (int64_t)a.np;
+  t.q = m0 / len;
+  t.rem0 = m0 - t.q * len;
+  if (EPI == kEpiApb) {
+    t.b = t.q / a.n;
+    t.r = (int)(t.q - t.b * a.n);
+  }
+  return t;
+}
+
 // The per-row value an epilogue reads from memory, once per row rather than per output tile:
 // kEpiTrimul's pair mask factor m_i m_k (symmetric, so the same for the transposed read).
 template <int EPI>
@@ -163,18 +186,36 @@ __device__ __forceinline__ float row_pre(const RowGemmArgs& a, const int64_t m) 
 // 32 ot + 8 v + 4 g + e in acc[4 v + e]. lb: the per-output biases (q_bias / gate_b of kEpiApb,
 // bias_out of kEpiResid) staged in LDS by output index, or NULL to read them from the arguments.
 // The loads an epilogue needs are all issued before its first store.
+// stage: a wave-private LDS tile of 32 x 32 bf16 (NULL: none), through which the
+// position-contiguous outputs (kEpiApb's flash-layout v^T, kEpiTrimul's channel planes) are
+// transposed and written as 16-byte pieces of 64-byte runs; tr: the tile's run (tile_run),
+// required with stage, whose 32 rows must then be consecutive positions of one run
+// (np % 32 == 0), so those epilogues take both only from the streaming kernel. rpre: the
+// residual values of kEpiResid, loaded by the caller (NULL: loaded here). Channel row r of the tile sits at LDS row
+// stage_row(r), which puts the rows the two lane halves write at once (r, r + 4) on different
+// banks.
 template <int EPI>
 __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16& acc, const int64_t m, const int ot,
                                     const int seg, const int cbase, const int g, const float* lb,
-                                    const float pre) {
+                                    const float pre, bf16* stage = nullptr,
+                                    const TileRun* tr = nullptr, const bf16x4* rpre = nullptr) {
   // the bias of output o (global index gi of src when not staged)
   auto obias = [&](int o, const float* src, int gi) { return lb ? lb[o] : (src ? src[gi] : 0.f); };
   if (EPI == kEpiApb && a.flash_rows > 0) {
     const int cs = a.O / 4;
-    const int64_t bn = m / a.np;
-    const int j = (int)(m - bn * a.np);
-    const int64_t b = bn / a.n;
-    const int r = (int)(bn - b * a.n);
+    int64_t bn, b;
+    int j, r;
+    if (tr) {
+      bn = tr->q;
+      j = (int)(tr->rem0 + (m - tr->m0));
+      b = tr->b;
+      r = tr->r;
+    } else {
+      bn = m / a.np;
+      j = (int)(m - bn * a.np);
+      b = bn / a.n;
+      r = (int)(bn - b * a.n);
+    }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int c = cbase + 8 * v + 4 * g;  // 4 channels of one head (dh % 4 == 0)
@@ -190,14 +231,37 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
         store4(a.k + (blk * a.np + j) * a.dh + d0, y[0], y[1], y[2], y[3]);
       } else if (seg == 2) {
         const int pos = vkey_pos(j);
+        if (stage) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) a.vt[(blk * a.dh + d0 + e) * a.np + pos] = (bf16)y[e];
+          for (int e = 0; e < 4; ++e) stage[stage_row(8 * v + 4 * g + e) * 32 + (pos & 31)] = (bf16)y[e];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) a.vt[(blk * a.dh + d0 + e) * a.np + pos] = (bf16)y[e];
+        }
       } else if (j < a.n) {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           y[e] = sigmoid_scaled((y[e] + obias(o0 + e, a.gate_b, c + e) + a.gate_bias) * -kLog2e);
         store4(a.gate + (bn * a.n + j) * cs + c, y[0], y[1], y[2], y[3]);
       }
+    }
+    if (seg == 2 && stage) {
+      // the tile's 32 v^T rows (tile-local channel r) of this run of 32 positions: lane L
+      // writes pieces L and L + 64 (row piece / 4, 8 positions each)
+      __builtin_amdgcn_wave_barrier();
+      const int lane = 32 * g + (int)(m - tr->m0);
+      const int jt = (int)tr->rem0;
+      const int64_t bt = tr->b;
+      const int rt = tr->r;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int piece = lane + 64 * u, r = piece >> 2, part = piece & 3;
+        const int c = cbase + r, hh = c / a.dh, d = c - hh * a.dh;
+        const int64_t blk = (bt * a.heads + hh) * a.flash_rows + rt;
+        *reinterpret_cast<bf16x8*>(a.vt + (blk * a.dh + d) * a.np + jt + 8 * part) =
+            *reinterpret_cast<const bf16x8*>(stage + stage_row(r) * 32 + 8 * part);
+      }
+      __builtin_amdgcn_wave_barrier();
     }
   } else if (EPI == kEpiApb) {
     const int cs = a.O / 4;
@@ -280,7 +344,8 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
   } else if (EPI == kEpiTrimul) {
     const int hid = a.O / 4;
     const int64_t gg = (int64_t)a.npm * a.npm;
-    const int64_t b = m / gg, rem = m - b * gg;
+    const int64_t b = tr ? tr->q : m / gg;
+    const int64_t rem = tr ? tr->rem0 + (m - tr->m0) : m - b * gg;
     const float keep = pre;  // the pair mask factor (row_pre)
     bf16* plane = (seg == 0 ? a.pa : a.pb) + b * hid * gg + rem;
 #pragma unroll
@@ -289,8 +354,22 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
       for (int e = 0; e < 4; ++e) {
         const int c = cbase + 8 * v + 4 * g + e;
         const float proj = acc[4 * v + e] * keep;  // masked before the gate, as the reference
-        plane[(int64_t)c * gg] = (bf16)(proj * sigmoid_scaled(-kLog2e * acc[8 + 4 * v + e]));
+        const bf16 y = (bf16)(proj * sigmoid_scaled(-kLog2e * acc[8 + 4 * v + e]));
+        if (stage)
+          stage[stage_row(8 * v + 4 * g + e) * 32 + (int)(m - tr->m0)] = y;
+        else
+          plane[(int64_t)c * gg] = y;
       }
+    if (stage) {
+      // the tile's 16 channel rows of 32 positions: lane L writes piece L (row L / 4)
+      __builtin_amdgcn_wave_barrier();
+      const int lane = 32 * g + (int)(m - tr->m0);
+      const int r = lane >> 2, part = lane & 3;
+      const int64_t bt = tr->q, remt = tr->rem0;
+      *reinterpret_cast<bf16x8*>((seg == 0 ? a.pa : a.pb) + bt * hid * gg + (int64_t)(cbase + r) * gg + remt +
+                                 8 * part) = *reinterpret_cast<const bf16x8*>(stage + stage_row(r) * 32 + 8 * part);
+      __builtin_amdgcn_wave_barrier();
+    }
   } else if (EPI == kEpiStore32) {
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -362,7 +441,8 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
     bf16x4 rv[4];
     if (a.residual) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) rv[v] = *reinterpret_cast<const bf16x4*>(a.res + m * a.O + ot * 32 + 8 * v + 4 * g);
+      for (int v = 0; v < 4; ++v)
+        rv[v] = rpre ? rpre[v] : *reinterpret_cast<const bf16x4*>(a.res + m * a.O + ot * 32 + 8 * v + 4 * g);
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -521,7 +601,8 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
 constexpr int kStreamWaves = 4;
 
 size_t row_stream_lds(int K, int O) {
-  return (size_t)O * (K + 8) * sizeof(bf16) + (size_t)(2 * K + O) * sizeof(float);
+  return (size_t)O * (K + 8) * sizeof(bf16) + (size_t)(2 * K + O) * sizeof(float) +
+         (size_t)kStreamWaves * 32 * 32 * sizeof(bf16);
 }
 
 template <int EPI, int XSRC, int K>
@@ -535,6 +616,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
   bf16* wl = reinterpret_cast<bf16*>(smem);  // [O / 32][32][WS]
   float* lnp = reinterpret_cast<float*>(smem + (size_t)a.O * WS * sizeof(bf16));  // weight, offset
   float* lb = lnp + 2 * K;  // per-output biases (row_epilogue)
+  // this wave's transpose tile (row_epilogue), for the epilogues that write position runs
+  bf16* stage = reinterpret_cast<bf16*>(lb + a.O) + (threadIdx.x >> 6) * 32 * 32;
+  const bool staged = (EPI == kEpiTrimul || (EPI == kEpiApb && a.flash_rows > 0)) && a.M % 32 == 0;
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   for (int idx = tid; idx < a.O * (K / 8); idx += 64 * kStreamWaves) {
@@ -625,8 +709,8 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
     }
     const int64_t m = tile * 32 + li;
     const float pre = m < a.M ? row_pre<EPI>(a, m) : 0.f;
-#pragma unroll 1
-    for (int ot = 0; ot < ntile; ++ot) {
+    const TileRun tr = staged ? tile_run<EPI>(a, tile * 32) : TileRun{};
+    auto out_tile = [&](int ot, const bf16x4* rpre) __attribute__((always_inline)) {
       const bf16* wt = wl + (ot * 32 + li) * WS + KH * g;
       f32x16 acc = zero16();
 #pragma unroll
@@ -637,7 +721,27 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
       }
       int seg, cbase;
       (void)tile_weight_row<EPI>(a, ot, li, seg, cbase);
-      if (m < a.M) row_epilogue<EPI>(a, acc, m, ot, seg, cbase, g, lb, pre);
+      if (m < a.M)
+        row_epilogue<EPI>(a, acc, m, ot, seg, cbase, g, lb, pre, staged ? stage : nullptr,
+                          staged ? &tr : nullptr, rpre);
+    };
+    if (EPI == kEpiResid && a.residual && ntile <= 4) {
+      // the residual of every output tile is loaded before the tile's first store: a wait
+      // for a load issued after stores would wait for those stores too (vmcnt counts both)
+      bf16x4 rv[4][4];
+      const int64_t mm = m < a.M ? m : a.M - 1;
+#pragma unroll
+      for (int ot = 0; ot < 4; ++ot)
+        if (ot < ntile)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            rv[ot][v] = *reinterpret_cast<const bf16x4*>(a.res + mm * a.O + ot * 32 + 8 * v + 4 * g);
+#pragma unroll
+      for (int ot = 0; ot < 4; ++ot)
+        if (ot < ntile) out_tile(ot, rv[ot]);
+    } else {
+#pragma unroll 1
+      for (int ot = 0; ot < ntile; ++ot) out_tile(ot, nullptr);
     }
   };
 

@@ -21,6 +21,9 @@ Reported beside it, in the same JSON line:
   host's cores on the same block and input (1 warm-up, median of 3), with the GPU
   result's rel-RMS against it.
 
+* ``shapes``: the same block at its other widths, N = 384: AF3's template stack (pair 64,
+  4 x 16 heads, hidden 64, transition x 2, 4 templates) and the confidence head (pair 128 +
+  single 384, 5 samples), ms per block on ``hip`` and on the engine ``pytorch`` backend.
 * ``trunk``: the 48-block trunk with its single track (c_s 384, 16 x 24 attention with
   pair bias) at N = 512, all-ones mask, z and s ~N(0,1), 3 passes (144 block evaluations),
   every op on ``hip``: ms per trunk run, ms per block, the single track's share, and the
@@ -77,7 +80,9 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--msa", action="store_true",
                     help="time the MSA-stack ops at L = 256 / 384 tokens, 512 MSA rows")
     ap.add_argument("--shapes", action="store_true",
-                    help="time the template-stack and confidence-head shapes of the block")
+                    help="time only the template-stack and confidence-head shapes of the block")
+    ap.add_argument("--no-shapes", action="store_true",
+                    help="leave the template-stack and confidence-head blocks out of the default line")
     ap.add_argument("--ladder-max", type=int, default=16384)
     return ap.parse_args()
 
@@ -711,6 +716,12 @@ def main() -> int:
             row = trunk_measure(ln_, 1)
             ladder_rows.append({k: row[k] for k in ("n", "ms_per_trunk", "ms_per_block", "trunk_tflops", "finite")})
             print(f"ladder N={ln_}: trunk {row['ms_per_trunk']} ms", file=sys.stderr, flush=True)
+    shapes = None
+    if not args.no_shapes:
+        torch.cuda.empty_cache()
+        shapes = shapes_measure(10)
+        print("shapes: " + "; ".join(f"{r['workload'].split(':')[0]} {r['hip_ms']} ms" for r in shapes["rows"]),
+              file=sys.stderr, flush=True)
     line = {
         "metric": METRIC,
         "value": round(ms_per_step, 4),
@@ -740,6 +751,7 @@ def main() -> int:
         "ops": {"n512_ragged": per_op, "n384": per_op_384},
         "trunk": trunk,
         "ladder": ladder_rows,
+        "shapes": shapes,
     }
     print(json.dumps(line), flush=True)
     return 0

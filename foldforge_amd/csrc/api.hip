@@ -162,6 +162,12 @@ struct TrimulWs {
   int* kst;
   size_t bytes;
 };
+// Pair and hidden width 64 on the generic path: one output kernel reading the contraction's
+// planes (its tile index is a 32-bit int).
+bool trimul_planes64(int64_t batch, int64_t n, int c, int h) {
+  return c == 64 && h == 64 && batch * n * ((n + 31) / 32) < 0x7fffffffLL;
+}
+
 TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
   Carver cv{static_cast<char*>(ws)};
   const int64_t np = pad128(n);
@@ -172,9 +178,12 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
     w.A = cv.take<bf16>(plane);
     w.B = cv.take<bf16>(plane);
     w.P = cv.take<bf16>(plane);
-    w.Pt = cv.take<bf16>((size_t)batch * n * n * h);
-    // the fp32 output projection between the row GEMMs (pair and hidden width 64: one kernel)
-    if (!(c == 64 && h == 64)) w.y32 = cv.take<float>((size_t)batch * n * n * c);
+    // the token rows of P and the fp32 output projection between the row GEMMs (pair and
+    // hidden width 64: one kernel reading the planes)
+    if (!trimul_planes64(batch, n, c, h)) {
+      w.Pt = cv.take<bf16>((size_t)batch * n * n * h);
+      w.y32 = cv.take<float>((size_t)batch * n * n * c);
+    }
     w.bytes = cv.used;
     return w;
   }
@@ -522,10 +531,9 @@ int32_t ffk_triangle_multiplication(
     p.pb = w.B;
     launch_row_gemm(p, kEpiTrimul, kXLn, st);
     launch_trimul_contract(w.A, w.B, w.P, batch * d_hidden, (int)np, st);
-    launch_planes_to_rows(w.P, w.Pt, (int)batch, d_hidden, (int)n, (int)np, st);
-    if (d_pair == 64 && d_hidden == 64) {
-      TrimulRowsArgs r{};
-      r.p = w.Pt;
+    if (trimul_planes64(batch, n, d_pair, d_hidden)) {
+      TrimulPlanesArgs r{};
+      r.planes = w.P;
       r.z = static_cast<const bf16*>(z);
       r.lno_w = ln_out_w;
       r.lno_b = ln_out_b;
@@ -535,12 +543,15 @@ int32_t ffk_triangle_multiplication(
       r.w_gate = w_gate;
       r.eps_out = eps_out;
       r.out = static_cast<bf16*>(out);
-      r.rows = batch * n * n;
+      r.batch = (int)batch;
+      r.n = (int)n;
+      r.np = (int)np;
       r.residual = residual ? 1 : 0;
       r.eps = eps;
-      launch_trimul_out_rows64(r, st);
+      launch_trimul_out_planes64(r, st);
       return check_launch("triangle_multiplication");
     }
+    launch_planes_to_rows(w.P, w.Pt, (int)batch, d_hidden, (int)n, (int)np, st);
     RowGemmArgs o{};
     o.ln_x = w.Pt;
     o.ln_w = ln_out_w;

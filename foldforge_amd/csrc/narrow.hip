@@ -48,12 +48,13 @@ __global__ __launch_bounds__(256) void planes_to_rows(const bf16* __restrict__ p
 
 // Generic-width triangle multiplication output for pair width 64 and hidden width 64:
 //   out = z + (LN_out(p) W_out^T) * sigmoid(LN_pair(z) W_g^T)
-// over the contraction's token rows p [batch n n][64], as one streaming kernel (so the
+// with p read straight from the contraction's channel planes, as one streaming kernel (so the
 // projection never round-trips through memory). Each workgroup converts both weights to bf16
-// once (LDS, rows 72 elements apart); every wave then walks tiles of 32 consecutive tokens on
-// its own, loading the next tile's p and z rows while it works on the current one. Lane
-// (li, g) holds token li's channels 32 g .. 32 g + 31 of p and of z; activations enter both
-// products as bf16 hi + lo. The weight rows are stored permuted (row r = 8 v + 4 g + e of output
+// once (LDS, rows 72 elements apart); every wave then walks tiles of 32 consecutive keys j of
+// one (b, i) on its own, loading the next tile's plane segments (64 channels x 64 contiguous
+// bytes) and z rows while it works on the current one. The plane segments are turned into token
+// rows through a wave-private LDS tile. Lane (li, g) holds token li's channels 32 g .. 32 g + 31
+// of p and of z; activations enter both products as bf16 hi + lo. The weight rows are stored permuted (row r = 8 v + 4 g + e of output
 // tile t holds channel 32 g + 16 t + 4 v + e), so a lane's accumulators hold the output
 // channels of its own half-row: the two products meet each other and z in registers, and the
 // lane writes its 32 output channels as four 16-byte pieces.
@@ -62,6 +63,7 @@ constexpr int kTmoWs = 72;  // LDS row stride (elements)
 struct __attribute__((aligned(16))) TmoLds {
   bf16 wo[64 * kTmoWs];
   bf16 wg[64 * kTmoWs];
+  bf16 rows[kTmoWaves][32 * kTmoWs];  // per wave: the tile's p as 32 token rows
   float lnow[64], lnob[64], lnw[64], lnb[64];
 };
 
@@ -70,7 +72,7 @@ __device__ __forceinline__ int tmo_perm(int row) {
   return 32 * ((r >> 2) & 1) + 16 * t + 4 * (r >> 3) + (r & 3);
 }
 
-__global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_rows64(TrimulRowsArgs a) {
+__global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_planes64(TrimulPlanesArgs a) {
   __shared__ TmoLds lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;
@@ -88,16 +90,29 @@ __global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_rows64(TrimulRowsAr
   }
   __syncthreads();
 
-  const int64_t tiles = (a.rows + 31) / 32;
-  const int64_t stride = (int64_t)gridDim.x * kTmoWaves;
-  int64_t t = (int64_t)blockIdx.x * kTmoWaves + wave;
+  const int n = a.n, njt = (n + 31) / 32;
+  const int tiles = a.batch * n * njt;
+  const int stride = (int)gridDim.x * kTmoWaves;
+  int t = (int)blockIdx.x * kTmoWaves + wave;
   if (t >= tiles) return;
   const float eps_out = a.eps_out ? *a.eps_out : a.eps;
+  const int64_t gg = (int64_t)a.np * a.np;
+  bf16* trow = lds.rows[wave];
 
-  auto fetch = [&](int64_t tile, bf16x8* pr, bf16x8* zr) __attribute__((always_inline)) {
-    const int64_t m = min(min(tile, tiles - 1) * 32 + li, a.rows - 1);
+  // Tile (b, i, jt): keys j = 32 jt + li. pc: this lane's 4 plane pieces (piece q = lane + 64 u:
+  // channel q / 4, keys 8 (q % 4) .. + 7; np % 32 == 0 keeps them inside the plane); zr: z row j
+  // (the last real one past n). A tile past the end re-reads the last tile.
+  auto fetch = [&](int tile, bf16x8* pc, bf16x8* zr) __attribute__((always_inline)) {
+    const int tt = tile < tiles ? tile : tiles - 1;
+    const int bi = tt / njt, jt = tt - bi * njt;
+    const int b = bi / n, i = bi - b * n;
+    const bf16* pl = a.planes + (int64_t)b * 64 * gg + (int64_t)i * a.np + 32 * jt;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) pr[s] = ld8(a.p + m * 64 + 32 * g + 8 * s);
+    for (int u = 0; u < 4; ++u) {
+      const int q = lane + 64 * u;
+      pc[u] = ld8(pl + (int64_t)(q >> 2) * gg + 8 * (q & 3));
+    }
+    const int64_t m = (int64_t)bi * n + min(32 * jt + li, n - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) zr[s] = ld8(a.z + m * 64 + 32 * g + 8 * s);
   };
@@ -143,11 +158,25 @@ __global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_rows64(TrimulRowsAr
       }
     }
   };
-  auto process = [&](int64_t tile, const bf16x8* pr, const bf16x8* zr) __attribute__((always_inline)) {
+  auto process = [&](int tile, const bf16x8* pc, const bf16x8* zr) __attribute__((always_inline)) {
+    // plane pieces -> token rows (LDS operations of a wave complete in order)
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int q = lane + 64 * u, c = q >> 2, k0 = 8 * (q & 3);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) trow[(k0 + e) * kTmoWs + c] = pc[u][e];
+    }
+    __builtin_amdgcn_wave_barrier();
+    bf16x8 pr[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) pr[s] = ld8(trow + li * kTmoWs + 32 * g + 8 * s);
     bf16x8 ph[4], pl[4], zh[4], zl[4];
     norm(pr, lds.lnow, lds.lnob, eps_out, ph, pl);
     norm(zr, lds.lnw, lds.lnb, a.eps, zh, zl);
-    const int64_t m = tile * 32 + li;
+    const int bi = tile / njt, jt = tile - bi * njt;
+    const int j = 32 * jt + li;
+    const int64_t m = (int64_t)bi * n + j;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
       const bf16* wor = lds.wo + (32 * t2 + li) * kTmoWs + 32 * g;
@@ -171,7 +200,7 @@ __global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_rows64(TrimulRowsAr
           y[v >> 1][4 * (v & 1) + e] =
               (bf16)(ay[4 * v + e] * sigmoid_scaled(-kLog2e * ag[4 * v + e]) + r);
         }
-      if (m < a.rows) {
+      if (j < n) {
         bf16* dst = a.out + m * 64 + 32 * g + 16 * t2;
         *reinterpret_cast<bf16x8*>(dst) = y[0];
         *reinterpret_cast<bf16x8*>(dst + 8) = y[1];
@@ -234,10 +263,10 @@ void launch_planes_to_rows(const bf16* planes, bf16* rows, int batch, int hid, i
                    256, lds, stream>>>(planes, rows, hid, n, np);
 }
 
-void launch_trimul_out_rows64(const TrimulRowsArgs& a, hipStream_t stream) {
-  const int64_t tiles = (a.rows + 31) / 32;
+void launch_trimul_out_planes64(const TrimulPlanesArgs& a, hipStream_t stream) {
+  const int64_t tiles = (int64_t)a.batch * a.n * ((a.n + 31) / 32);
   const int64_t blocks = std::min<int64_t>((tiles + kTmoWaves - 1) / kTmoWaves, (int64_t)cu_count() * 6);
-  trimul_out_rows64<<<dim3((unsigned)std::max<int64_t>(1, blocks)), 64 * kTmoWaves, 0, stream>>>(a);
+  trimul_out_planes64<<<dim3((unsigned)std::max<int64_t>(1, blocks)), 64 * kTmoWaves, 0, stream>>>(a);
 }
 
 void launch_pair_add_transposed(const bf16* base, const bf16* t, bf16* out, int64_t batch, int n,

@@ -21,9 +21,10 @@ Reported beside it, in the same JSON line:
   host's cores on the same block and input (1 warm-up, median of 3), with the GPU
   result's rel-RMS against it.
 
-* ``shapes``: the same block at its other widths, N = 384: AF3's template stack (pair 64,
-  4 x 16 heads, hidden 64, transition x 2, 4 templates) and the confidence head (pair 128 +
-  single 384, 5 samples), ms per block on ``hip`` and on the engine ``pytorch`` backend.
+* ``shapes``: the same block at its other widths, N = 384: the template stacks of AF3 (pair 64,
+  4 x 16 heads, hidden 64, transition x 2), Protenix-1 (4 x 32 heads, hidden 128) and Boltz-2
+  (4 x 32 heads, transition x 4), 4 templates each, and the confidence head (pair 128 + single
+  384, 5 samples), ms per block on ``hip`` and on the engine ``pytorch`` backend.
 * ``trunk``: the 48-block trunk with its single track (c_s 384, 16 x 24 attention with
   pair bias) at N = 512, all-ones mask, z and s ~N(0,1), 3 passes (144 block evaluations),
   every op on ``hip``: ms per trunk run, ms per block, the single track's share, and the
@@ -444,9 +445,11 @@ def opm_measure(reps: int = 20) -> dict:
 
 
 def shapes_measure(reps: int = 10) -> dict:
-    """The same block at its other shapes: AF3's template stack (pair 64, triangle attention
-    4 x 16, hidden 64, transition x 2; 4 templates batched) and the confidence head's block
-    (pair 128 with the single track, 5 samples batched), both at N = 384; ms per block on hip
+    """The same block at its other shapes: the template stacks of AF3 (pair 64, triangle
+    attention 4 x 16, hidden 64, transition x 2), Protenix-1 (4 x 32 heads, hidden 128) and
+    Boltz-2 (4 x 32 heads, transition x 4), 4 templates batched (``spec.py`` of the reference:
+    template heads, head width and hidden width per family), and the confidence head's block
+    (pair 128 with the single track, 5 samples batched), all at N = 384; ms per block on hip
     and on the engine pytorch backend (same GPU)."""
     import torch
 
@@ -458,6 +461,11 @@ def shapes_measure(reps: int = 10) -> dict:
     cases = (
         ("template stack block (AF3): pair 64, 4 x 16 heads, hidden 64, transition x2, 4 templates",
          dict(d_pair=64, triangle_model="af3", d_hidden_tri_attention=16, pair_transition_n=2), 4, 64, 0),
+        ("template stack block (Protenix-1): pair 64, 4 x 32 heads, hidden 128, transition x2, 4 templates",
+         dict(d_pair=64, triangle_model="protenix", d_hidden_tri_attention=32, d_hidden_tri_multi=128,
+              pair_transition_n=2), 4, 64, 0),
+        ("template stack block (Boltz-2): pair 64, 4 x 32 heads, hidden 64, transition x4, 4 templates",
+         dict(d_pair=64, triangle_model="boltz2", d_hidden_tri_attention=32, pair_transition_n=4), 4, 64, 0),
         ("confidence head block (AF3): pair 128 + single 384, 5 samples",
          dict(d_pair=128, triangle_model="af3", d_single=384), 5, 128, 384),
     )

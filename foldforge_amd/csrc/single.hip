@@ -593,15 +593,18 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
 // The products and epilogues of row_gemm for short rows (K = 64 or 128), as a persistent
 // kernel: each workgroup converts the weights to bf16 once (LDS, in output-tile order, rows
 // K + 8 elements apart so that the operand reads of 16 rows hit distinct banks), then every
-// wave walks whole 32-row tiles on its own, with no barrier in the loop. The next tile's input
+// wave walks whole 32-row tiles on its own, with no barrier in the loop. With gridDim.y > 1 the
+// output tiles are split into that many equal parts, one per grid row (wide outputs: each
+// workgroup then holds a part of the weights and more workgroups fit on a CU). The next tile's input
 // rows are loaded while the current one is normalised, multiplied for all O / 32 output tiles
 // (activations as bf16 hi + lo, as row_gemm) and stored by the epilogue of each output tile.
 // Lane (li, g) holds row li's channels (K / 2) g .. (K / 2) g + K / 2 - 1; MFMA step s takes
 // channels (K / 2) g + 8 s .. + 7 of both operands.
 constexpr int kStreamWaves = 4;
 
-size_t row_stream_lds(int K, int O) {
-  return (size_t)O * (K + 8) * sizeof(bf16) + (size_t)(2 * K + O) * sizeof(float) +
+// LDS of one workgroup holding the weight rows of Op of the O outputs.
+size_t row_stream_lds(int K, int O, int Op) {
+  return (size_t)Op * (K + 8) * sizeof(bf16) + (size_t)(2 * K + O) * sizeof(float) +
          (size_t)kStreamWaves * 32 * 32 * sizeof(bf16);
 }
 
@@ -613,18 +616,20 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
   constexpr int NX = XSRC == kXLn ? KS : 2 * KS;  // 16-byte input pieces per lane
   using XT = typename std::conditional<XSRC == kXLn, bf16x8, f32x4>::type;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  bf16* wl = reinterpret_cast<bf16*>(smem);  // [O / 32][32][WS]
-  float* lnp = reinterpret_cast<float*>(smem + (size_t)a.O * WS * sizeof(bf16));  // weight, offset
+  const int nt = a.O / 32 / (int)gridDim.y;  // output tiles of this workgroup's part
+  const int ot0 = (int)blockIdx.y * nt;
+  bf16* wl = reinterpret_cast<bf16*>(smem);  // [nt][32][WS]: output tiles ot0 ..
+  float* lnp = reinterpret_cast<float*>(smem + (size_t)nt * 32 * WS * sizeof(bf16));  // weight, offset
   float* lb = lnp + 2 * K;  // per-output biases (row_epilogue)
   // this wave's transpose tile (row_epilogue), for the epilogues that write position runs
   bf16* stage = reinterpret_cast<bf16*>(lb + a.O) + (threadIdx.x >> 6) * 32 * 32;
   const bool staged = (EPI == kEpiTrimul || (EPI == kEpiApb && a.flash_rows > 0)) && a.M % 32 == 0;
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  for (int idx = tid; idx < a.O * (K / 8); idx += 64 * kStreamWaves) {
+  for (int idx = tid; idx < nt * 32 * (K / 8); idx += 64 * kStreamWaves) {
     const int row = idx / (K / 8), ch = 8 * (idx % (K / 8));
     int seg, cbase;
-    const float* wr = tile_weight_row<EPI>(a, row >> 5, row & 31, seg, cbase);
+    const float* wr = tile_weight_row<EPI>(a, ot0 + (row >> 5), row & 31, seg, cbase);
     *reinterpret_cast<bf16x8*>(wl + row * WS + ch) = cvt8(wr + ch);
   }
   for (int o = tid; o < a.O; o += 64 * kStreamWaves) {
@@ -652,7 +657,6 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
   int64_t t = (int64_t)blockIdx.x * kStreamWaves + wave;
   if (t >= tiles) return;
   const float eps = XSRC == kXLn && a.eps_dev ? *a.eps_dev : a.eps;
-  const int ntile = a.O / 32;
 
   // the input rows of a tile (a tile past the end re-reads the last one, so every load stays
   // inside the input)
@@ -711,7 +715,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
     const float pre = m < a.M ? row_pre<EPI>(a, m) : 0.f;
     const TileRun tr = staged ? tile_run<EPI>(a, tile * 32) : TileRun{};
     auto out_tile = [&](int ot, const bf16x4* rpre) __attribute__((always_inline)) {
-      const bf16* wt = wl + (ot * 32 + li) * WS + KH * g;
+      const bf16* wt = wl + ((ot - ot0) * 32 + li) * WS + KH * g;
       f32x16 acc = zero16();
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
@@ -725,23 +729,23 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
         row_epilogue<EPI>(a, acc, m, ot, seg, cbase, g, lb, pre, staged ? stage : nullptr,
                           staged ? &tr : nullptr, rpre);
     };
-    if (EPI == kEpiResid && a.residual && ntile <= 4) {
+    if (EPI == kEpiResid && a.residual && nt <= 4) {
       // the residual of every output tile is loaded before the tile's first store: a wait
       // for a load issued after stores would wait for those stores too (vmcnt counts both)
       bf16x4 rv[4][4];
       const int64_t mm = m < a.M ? m : a.M - 1;
 #pragma unroll
-      for (int ot = 0; ot < 4; ++ot)
-        if (ot < ntile)
+      for (int u = 0; u < 4; ++u)
+        if (u < nt)
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            rv[ot][v] = *reinterpret_cast<const bf16x4*>(a.res + mm * a.O + ot * 32 + 8 * v + 4 * g);
+            rv[u][v] = *reinterpret_cast<const bf16x4*>(a.res + mm * a.O + (ot0 + u) * 32 + 8 * v + 4 * g);
 #pragma unroll
-      for (int ot = 0; ot < 4; ++ot)
-        if (ot < ntile) out_tile(ot, rv[ot]);
+      for (int u = 0; u < 4; ++u)
+        if (u < nt) out_tile(ot0 + u, rv[u]);
     } else {
 #pragma unroll 1
-      for (int ot = 0; ot < ntile; ++ot) out_tile(ot, nullptr);
+      for (int ot = ot0; ot < ot0 + nt; ++ot) out_tile(ot, nullptr);
     }
   };
 
@@ -1047,23 +1051,34 @@ void launch_row_gemm_t(const RowGemmArgs& a, hipStream_t stream) {
 // Tile shapes: the LayerNorm-fed GEMMs give each workgroup several output tiles (the tile is
 // normalised once per workgroup); the fp32-fed ones split k 8 ways when k is long, and give the
 // waves separate output tiles when k has fewer groups than waves.
+// Output parts: halve the weight rows per workgroup until a workgroup's LDS is at most 56 KiB
+// (three workgroups of 4 waves per CU), as long as the parts stay whole tiles.
+int row_stream_parts(int K, int O) {
+  int parts = 1;
+  while (row_stream_lds(K, O, O / parts) > 56 * 1024 && (O / 32) % (2 * parts) == 0) parts *= 2;
+  return parts;
+}
+
 template <int EPI, int XSRC, int K>
 void launch_row_stream_t(const RowGemmArgs& a, hipStream_t stream) {
-  const size_t lds = row_stream_lds(K, a.O);
+  const int parts = row_stream_parts(K, a.O);
+  const size_t lds = row_stream_lds(K, a.O, a.O / parts);
   auto kernel = row_stream<EPI, XSRC, K>;
   if (lds > 65536)
     (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
                               hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   const int64_t tiles = (a.M + 31) / 32;
   const int64_t per_cu = std::max<int64_t>(1, std::min<int64_t>(4, (160 * 1024) / (int64_t)lds));
-  int64_t blocks = std::min<int64_t>((tiles + kStreamWaves - 1) / kStreamWaves, cu_count() * per_cu);
-  kernel<<<dim3((unsigned)std::max<int64_t>(1, blocks)), 64 * kStreamWaves, lds, stream>>>(a);
+  const int64_t blocks = std::min<int64_t>((tiles + kStreamWaves - 1) / kStreamWaves,
+                                           std::max<int64_t>(1, cu_count() * per_cu / parts));
+  kernel<<<dim3((unsigned)std::max<int64_t>(1, blocks), (unsigned)parts), 64 * kStreamWaves, lds, stream>>>(a);
 }
 
-// The streaming kernel's cases: the pair path's short rows, the weights fitting in LDS.
+// The streaming kernel's cases: the pair path's short rows, a part of the weights fitting in LDS.
 template <int EPI, int XSRC>
 bool launch_row_stream(const RowGemmArgs& a, hipStream_t stream) {
-  if (row_stream_lds(a.K, a.O) > 80 * 1024) return false;
+  if (a.K != 64 && a.K != 128) return false;
+  if (row_stream_lds(a.K, a.O, a.O / row_stream_parts(a.K, a.O)) > 80 * 1024) return false;
   if (a.K == 64)
     launch_row_stream_t<EPI, XSRC, 64>(a, stream);
   else if (a.K == 128)

@@ -127,7 +127,8 @@ enum { kActNone = 0, kActSigmoid = 1, kActSilu = 2, kActRelu = 3 };
 // kMapPadKeysT: m = (b n + r) np + j over keys padded to np reads pair row (b n + r) n + j' /
 // (b n + j') n + r with j' = min(j, n - 1).
 enum { kMapIdentity = 0, kMapPairT = 1, kMapGridOut = 2, kMapGridIn = 3, kMapPadKeys = 4, kMapPadKeysT = 5 };
-enum { kXLn = 0, kXF32 = 1 };
+// kXBf16: bf16 rows entered as they are (the streaming kernel's form of kXLn with ln_plain)
+enum { kXLn = 0, kXF32 = 1, kXBf16 = 2 };
 constexpr int kLnGemmMaxK = 768;
 struct RowGemmArgs {
   const bf16* ln_x;             // kXLn: [M][K] rows to normalise with ln_w, ln_b, eps

@@ -613,8 +613,9 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
   constexpr int KS = K / 16;  // MFMA steps
   constexpr int KH = K / 2;   // channels per lane
   constexpr int WS = K + 8;   // LDS row stride of the weight image (elements)
-  constexpr int NX = XSRC == kXLn ? KS : 2 * KS;  // 16-byte input pieces per lane
-  using XT = typename std::conditional<XSRC == kXLn, bf16x8, f32x4>::type;
+  constexpr bool BF = XSRC != kXF32;                // bf16 input rows
+  constexpr int NX = BF ? KS : 2 * KS;              // 16-byte input pieces per lane
+  using XT = typename std::conditional<BF, bf16x8, f32x4>::type;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int nt = a.O / 32 / (int)gridDim.y;  // output tiles of this workgroup's part
   const int ot0 = (int)blockIdx.y * nt;
@@ -665,15 +666,19 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
     const int64_t row = mapped_row(a, tt * 32 + li);
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
-      if (XSRC == kXLn)
+      if (BF)
         x[i] = *reinterpret_cast<const XT*>(a.ln_x + row * K + KH * g + 8 * i);
       else
         x[i] = *reinterpret_cast<const XT*>(a.x32 + row * K + KH * g + 4 * i);
     }
   };
   auto process = [&](const XT* x, int64_t tile) __attribute__((always_inline)) {
-    bf16x8 xh[KS], xl[KS];
-    if (XSRC == kXLn) {
+    // the MFMA operands: hi + lo of the activations (kXBf16: the rows themselves, no lo)
+    bf16x8 xh[KS], xl[XSRC == kXBf16 ? 1 : KS];
+    if (XSRC == kXBf16) {
+#pragma unroll
+      for (int s = 0; s < KS; ++s) xh[s] = x[s];
+    } else if (XSRC == kXLn) {
       float s1 = 0.f;
 #pragma unroll
       for (int s = 0; s < KS; ++s)
@@ -720,7 +725,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const bf16x8 w = *reinterpret_cast<const bf16x8*>(wt + 8 * s);
-        acc = mfma32(w, xl[s], acc);
+        if (XSRC != kXBf16) acc = mfma32(w, xl[s], acc);
         acc = mfma32(w, xh[s], acc);
       }
       int seg, cbase;
@@ -1077,14 +1082,15 @@ void launch_row_stream_t(const RowGemmArgs& a, hipStream_t stream) {
 // The streaming kernel's cases: the pair path's short rows, a part of the weights fitting in LDS.
 template <int EPI, int XSRC>
 bool launch_row_stream(const RowGemmArgs& a, hipStream_t stream) {
-  if (a.K != 64 && a.K != 128) return false;
+  // k 64 or 128; plain bf16 rows (no normalisation, no lo operand) also 256
+  if (a.K != 64 && a.K != 128 && !(XSRC == kXBf16 && a.K == 256)) return false;
   if (row_stream_lds(a.K, a.O, a.O / row_stream_parts(a.K, a.O)) > 80 * 1024) return false;
   if (a.K == 64)
     launch_row_stream_t<EPI, XSRC, 64>(a, stream);
   else if (a.K == 128)
     launch_row_stream_t<EPI, XSRC, 128>(a, stream);
-  else
-    return false;
+  else if constexpr (XSRC == kXBf16)
+    launch_row_stream_t<EPI, XSRC, 256>(a, stream);
   return true;
 }
 
@@ -1096,6 +1102,7 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
     if (epi == kEpiStore32 && launch_row_stream<kEpiStore32, kXLn>(a, stream)) return;
     if (epi == kEpiGateResid && launch_row_stream<kEpiGateResid, kXLn>(a, stream)) return;
     if (epi == kEpiSwiglu && launch_row_stream<kEpiSwiglu, kXLn>(a, stream)) return;
+    if (epi == kEpiResid && a.ln_plain && launch_row_stream<kEpiResid, kXBf16>(a, stream)) return;
     if (epi == kEpiResid && launch_row_stream<kEpiResid, kXLn>(a, stream)) return;
   } else if (epi == kEpiResid && launch_row_stream<kEpiResid, kXF32>(a, stream)) {
     return;

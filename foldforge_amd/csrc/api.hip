@@ -209,6 +209,11 @@ struct TriattnWs {
 };
 // Head widths the generic path runs on the flash core (the rest: apb_attention).
 bool triattn_flash_width(int d) { return d == 16 || d == 32; }
+// Generic widths whose output kernel computes the gate from z (pair 64, gated width 64 or 128):
+// the projection then writes q, k, v only and the flash core the plain attention output.
+bool triattn_gate_out(int c, int heads, int d) {
+  return triattn_flash_width(d) && c == 64 && (heads * d == 64 || heads * d == 128);
+}
 int64_t pad4(int64_t n) { return (n + 3) / 4 * 4; }
 
 TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d, int form) {
@@ -227,9 +232,9 @@ TriattnWs triattn_ws(void* ws, int64_t batch, int64_t n, int c, int heads, int d
       w.q = cv.take<bf16>(blk);
       w.k = cv.take<bf16>(blk);
       w.vt = cv.take<bf16>(blk);
-      w.gate = cv.take<bf16>(tok);
+      if (!triattn_gate_out(c, heads, d)) w.gate = cv.take<bf16>(tok);
       w.bias = cv.take<float>((size_t)batch * heads * np32 * np32);
-      w.ogb = cv.take<bf16>(tok);  // the gated output, bf16
+      w.ogb = cv.take<bf16>(tok);  // the attention output (gated unless the output kernel gates it), bf16
       w.bytes = cv.used;
       return w;
     } else {
@@ -670,6 +675,7 @@ int32_t ffk_triangle_attention(
       return fail(FFK_ERR_INVALID, "triangle_attention: batch * n = %lld exceeds the launch grid", (long long)(batch * n));
     const int64_t np32 = pad32(n);
     const bool flash = triattn_flash_width(d_head);
+    const bool gate_out = triattn_gate_out(d_pair, n_head, d_head);
     // q, k, v^T, gate of every pair row (the transposed pair for the ending node); for the flash
     // core on keys padded to np32 (the padding repeats key n - 1, so its k and v are finite)
     RowGemmArgs p{};
@@ -683,7 +689,8 @@ int32_t ffk_triangle_attention(
     p.w3 = w_gate;
     p.M = flash ? batch * n * np32 : batch * n * n;
     p.K = d_pair;
-    p.O = 4 * hd;
+    p.O = (gate_out ? 3 : 4) * hd;
+    p.apb_no_gate = gate_out ? 1 : 0;
     p.q_bias = nullptr;
     p.q_scale = kLog2e / sqrtf((float)d_head);
     p.gate_bias = 0.f;
@@ -735,8 +742,12 @@ int32_t ffk_triangle_attention(
       f.heads = n_head;
       f.kstages = nullptr;
       f.dh = d_head;
-      f.gate = w.gate;
-      f.og = w.ogb;
+      if (gate_out) {
+        f.o = w.ogb;
+      } else {
+        f.gate = w.gate;
+        f.og = w.ogb;
+      }
       f.o_sb = n * n * hd;
       f.o_sr = n * hd;
       f.o_sj = hd;
@@ -760,6 +771,26 @@ int32_t ffk_triangle_attention(
     }
     // the output projection of the gated values into dst (z frame), with the residual or not
     auto project = [&](const float* wo, const float* bo, bf16* dst, int res) {
+      if (gate_out) {
+        TriattnRowsArgs r{};
+        r.z = static_cast<const bf16*>(z);
+        r.o = w.ogb;
+        r.ln_w = ln_pair_w;
+        r.ln_b = ln_pair_b;
+        r.w_gate = w_gate;
+        r.b_gate = b_gate;
+        r.w_out = wo;
+        r.b_out = bo;
+        r.out = dst;
+        r.batch = (int)batch;
+        r.n = (int)n;
+        r.hd = hd;
+        r.transposed = starting ? 0 : 1;
+        r.residual = res;
+        r.eps = eps;
+        launch_triattn_out_rows(r, st);
+        return;
+      }
       RowGemmArgs o{};
       o.x32 = w.og;
       o.ln_x = w.ogb;

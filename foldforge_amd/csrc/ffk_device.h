@@ -56,6 +56,17 @@ __device__ __forceinline__ int64_t bias_index(int64_t bh, int64_t nb, int64_t qu
 
 __device__ __forceinline__ bf16x8 ld8(const bf16* p) { return *reinterpret_cast<const bf16x8*>(p); }
 
+// 8 fp32 values -> bf16 hi + lo (hi + lo carries the value to about 16 bits of mantissa).
+__device__ __forceinline__ void split8(const f32x4& a, const f32x4& b, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    hi[e] = (bf16)a[e];
+    hi[4 + e] = (bf16)b[e];
+    lo[e] = (bf16)(a[e] - (float)hi[e]);
+    lo[4 + e] = (bf16)(b[e] - (float)hi[4 + e]);
+  }
+}
+
 // 8 consecutive fp32 values (16-byte aligned) -> one bf16 MFMA operand.
 __device__ __forceinline__ bf16x8 cvt8(const float* p) {
   const f32x4 a = *reinterpret_cast<const f32x4*>(p);

@@ -155,6 +155,7 @@ struct RowGemmArgs {
   // [batch heads][flash_rows][dh][np] (keys permuted), written for every j < np; the gate
   // [batch n n][cs] for j < n
   int flash_rows;
+  int apb_no_gate;  // kEpiApb: 1 = q, k, v only (O = 3 cs; the gate is computed downstream)
   // kEpiPwa: w0 = to_value, w1 = to_gate ([hd][K] each, O = 2 hd); tokens m = (b S + s) n + j;
   // v^T [batch][heads][S][dh][np] (bf16, keys contiguous), gate = sigmoid(x W_g^T) [M][hd]
   int depth;
@@ -233,6 +234,22 @@ struct TrimulPlanesArgs {
   float eps;
 };
 void launch_trimul_out_planes64(const TrimulPlanesArgs& a, hipStream_t stream);
+
+// Generic-width triangle attention output at pair width 64, gated width hd 64 or 128:
+// out = (residual ? z : 0) + (sigmoid(LN_pair(z) W_g^T + b_g) * o) W_out^T + b_out.
+struct TriattnRowsArgs {
+  const bf16* z;                  // [batch][n][n][64]
+  const bf16* o;                  // [batch][n][n][hd] attention output in the attention's frame
+  const float *ln_w, *ln_b;       // pair norm affine [64]
+  const float *w_gate, *b_gate;   // [hd][64], [hd] (NULL: none)
+  const float *w_out, *b_out;     // [64][hd], [64] (NULL: none)
+  bf16* out;                      // [batch][n][n][64]; may alias z
+  int batch, n, hd;
+  int transposed;                 // 1: position (b, i, j) takes o row (b, j, i)
+  int residual;
+  float eps;
+};
+void launch_triattn_out_rows(const TriattnRowsArgs& a, hipStream_t stream);
 
 // Channel planes P [batch][hid][np][np] -> token rows Pt [batch][n][n][hid] (bf16).
 void launch_planes_to_rows(const bf16* planes, bf16* rows, int batch, int hid, int n, int np,

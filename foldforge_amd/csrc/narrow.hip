@@ -224,6 +224,184 @@ __global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_planes64(TrimulPlan
   }
 }
 
+// Generic-width triangle attention output for pair width 64 and gated width HD (64 or 128):
+//   out = z + (sigmoid(LN_pair(z) W_g^T + b_g) * o) W_out^T + b_out
+// as one streaming kernel (the gate is computed here from z, which the residual reads anyway,
+// instead of being stored by the projection and read by the attention core). Same scheme as
+// trimul_out_planes64: both weights converted to bf16 once per workgroup; every wave walks
+// tiles of 32 consecutive pair positions m on its own, loading the next tile's z and o rows
+// while it works on the current one; lane (li, g) holds position li's channels
+// 32 g .. 32 g + 31 of z and HD/2 g .. HD/2 g + HD/2 - 1 of o. The gate rows are permuted so
+// that a lane's accumulators hold the gate of its own o channels; the gated values are then the
+// output product's operand as they stand, and the output rows are permuted so that a lane's
+// accumulators hold its own z channels. o is read in the attention's frame: position (b, i, j)
+// of z takes o row (b, j, i) for the ending node (transposed).
+template <int HD>
+struct __attribute__((aligned(16))) TaoLds {
+  bf16 wg[HD * kTmoWs];            // gate rows (permuted), k = 64 pair channels
+  bf16 wo[64 * (HD + 8)];          // output rows (permuted), k = HD gated channels
+  float lnw[64], lnb[64], bg[HD], bo[64];  // bg times -log2(e), as the gate rows
+};
+
+template <int HD>
+__device__ __forceinline__ int tao_perm(int row, int half) {
+  const int t = row >> 5, r = row & 31;
+  return half * ((r >> 2) & 1) + 16 * t + 4 * (r >> 3) + (r & 3);
+}
+
+template <int HD>
+__global__ __launch_bounds__(64 * kTmoWaves) void triattn_out_rows(TriattnRowsArgs a) {
+  constexpr int KO = HD / 16;  // 8-channel pieces of a lane's half o row
+  constexpr int WOS = HD + 8;
+  __shared__ TaoLds<HD> lds;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, g = lane >> 5, li = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  for (int idx = tid; idx < HD * 8; idx += 64 * kTmoWaves) {  // gate: HD rows x 64
+    const int row = idx >> 3, ch = 8 * (idx & 7);
+    const float* src = a.w_gate + tao_perm<HD>(row, HD / 2) * 64 + ch;
+    bf16x8 w;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = (bf16)(-kLog2e * src[e]);
+    *reinterpret_cast<bf16x8*>(lds.wg + row * kTmoWs + ch) = w;
+  }
+  for (int idx = tid; idx < 64 * (HD / 8); idx += 64 * kTmoWaves) {  // output: 64 rows x HD
+    const int row = idx / (HD / 8), ch = 8 * (idx % (HD / 8));
+    *reinterpret_cast<bf16x8*>(lds.wo + row * WOS + ch) = cvt8(a.w_out + tao_perm<HD>(row, 32) * HD + ch);
+  }
+  if (tid < 64) {
+    lds.lnw[tid] = a.ln_w[tid];
+    lds.lnb[tid] = a.ln_b[tid];
+    lds.bo[tid] = a.b_out ? a.b_out[tid] : 0.f;
+  }
+  if (tid < HD) lds.bg[tid] = a.b_gate ? -kLog2e * a.b_gate[tid] : 0.f;
+  __syncthreads();
+
+  const int n = a.n;
+  const int64_t rows = (int64_t)a.batch * n * n;
+  const int64_t tiles = (rows + 31) / 32;
+  const int64_t stride = (int64_t)gridDim.x * kTmoWaves;
+  int64_t t = (int64_t)blockIdx.x * kTmoWaves + wave;
+  if (t >= tiles) return;
+
+  // the z row and the o row of this lane's position (the last one past the end)
+  auto rows_of = [&](int64_t tile, int64_t& mz, int64_t& mo) __attribute__((always_inline)) {
+    mz = min(min(tile, tiles - 1) * 32 + li, rows - 1);
+    mo = mz;
+    if (a.transposed) {
+      const int64_t bi = mz / n;
+      const int j = (int)(mz - bi * n);
+      const int64_t b = bi / n;
+      const int i = (int)(bi - b * n);
+      mo = (b * n + j) * n + i;
+    }
+  };
+  auto fetch = [&](int64_t tile, bf16x8* zr, bf16x8* orr) __attribute__((always_inline)) {
+    int64_t mz, mo;
+    rows_of(tile, mz, mo);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) zr[s] = ld8(a.z + mz * 64 + 32 * g + 8 * s);
+#pragma unroll
+    for (int s = 0; s < KO; ++s) orr[s] = ld8(a.o + mo * HD + (HD / 2) * g + 8 * s);
+  };
+  auto process = [&](int64_t tile, const bf16x8* zr, bf16x8* orr) __attribute__((always_inline)) {
+    // LayerNorm of z (the row's other 32 channels in lane li + 32) -> bf16 hi / lo
+    float s1 = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s1 += (float)zr[s][e];
+    const float mean = pair_sum(s1) * (1.f / 64);
+    float s2 = 0.f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = (float)zr[s][e] - mean;
+        s2 += d * d;
+      }
+    const float rstd = __builtin_amdgcn_rsqf(pair_sum(s2) * (1.f / 64) + a.eps);
+    int cb = 32 * g, hb = (HD / 2) * g;  // read per tile (held, they would take registers)
+    asm volatile("" : "+v"(cb), "+v"(hb));
+    bf16x8 xh[4], xl[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(&lds.lnw[cb + 8 * s]);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(&lds.lnw[cb + 8 * s + 4]);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(&lds.lnb[cb + 8 * s]);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(&lds.lnb[cb + 8 * s + 4]);
+      f32x4 y0, y1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y0[e] = ((float)zr[s][e] - mean) * rstd * w0[e] + b0[e];
+        y1[e] = ((float)zr[s][4 + e] - mean) * rstd * w1[e] + b1[e];
+      }
+      split8(y0, y1, xh[s], xl[s]);
+    }
+    // gate tiles: gated channel HD/2 g + 16 t + 4 v + e in acc[4 v + e], gated in place in orr
+#pragma unroll
+    for (int t4 = 0; t4 < HD / 32; ++t4) {
+      const bf16* wr = lds.wg + (32 * t4 + li) * kTmoWs + 32 * g;
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bf16x8 w8 = ld8(wr + 8 * s);
+        acc = mfma32(w8, xl[s], acc);
+        acc = mfma32(w8, xh[s], acc);
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const f32x4 gb = *reinterpret_cast<const f32x4*>(&lds.bg[hb + 16 * t4 + 4 * v]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = 16 * t4 + 4 * v + e;  // channel within the lane's half
+          orr[c >> 3][c & 7] = (bf16)(sigmoid_scaled(acc[4 * v + e] + gb[e]) * (float)orr[c >> 3][c & 7]);
+        }
+      }
+    }
+    // output tiles: pair channel 32 g + 16 t + 4 v + e, plus the bias and the residual
+    const int64_t m = tile * 32 + li;
+#pragma unroll
+    for (int t2 = 0; t2 < 2; ++t2) {
+      const bf16* wr = lds.wo + (32 * t2 + li) * WOS + (HD / 2) * g;
+      f32x16 acc = zero16();
+#pragma unroll
+      for (int s = 0; s < KO; ++s) acc = mfma32(ld8(wr + 8 * s), orr[s], acc);
+      bf16x8 y[2];
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const f32x4 ob = *reinterpret_cast<const f32x4*>(&lds.bo[cb + 16 * t2 + 4 * v]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = 16 * t2 + 4 * v + e;
+          const float r = a.residual ? (float)zr[c >> 3][c & 7] : 0.f;
+          y[v >> 1][4 * (v & 1) + e] = (bf16)(acc[4 * v + e] + ob[e] + r);
+        }
+      }
+      if (m < rows) {
+        bf16* dst = a.out + m * 64 + 32 * g + 16 * t2;
+        *reinterpret_cast<bf16x8*>(dst) = y[0];
+        *reinterpret_cast<bf16x8*>(dst + 8) = y[1];
+      }
+    }
+  };
+
+  // two register buffers used in turn: the next tile's rows load while the current one is
+  // processed
+  bf16x8 z0[4], o0[KO], z1[4], o1[KO];
+  fetch(t, z0, o0);
+  while (true) {
+    fetch(t + stride, z1, o1);
+    process(t, z0, o0);
+    t += stride;
+    if (t >= tiles) break;
+    fetch(t + stride, z0, o0);
+    process(t, z1, o1);
+    t += stride;
+    if (t >= tiles) break;
+  }
+}
+
 }  // namespace
 
 // out[b][i][j][:] = (base ? base[b][i][j][:] : 0) + t[b][j][i][:]: one thread per 8 channels
@@ -267,6 +445,16 @@ void launch_trimul_out_planes64(const TrimulPlanesArgs& a, hipStream_t stream) {
   const int64_t tiles = (int64_t)a.batch * a.n * ((a.n + 31) / 32);
   const int64_t blocks = std::min<int64_t>((tiles + kTmoWaves - 1) / kTmoWaves, (int64_t)cu_count() * 6);
   trimul_out_planes64<<<dim3((unsigned)std::max<int64_t>(1, blocks)), 64 * kTmoWaves, 0, stream>>>(a);
+}
+
+void launch_triattn_out_rows(const TriattnRowsArgs& a, hipStream_t stream) {
+  const int64_t tiles = ((int64_t)a.batch * a.n * a.n + 31) / 32;
+  const int64_t blocks = std::min<int64_t>((tiles + kTmoWaves - 1) / kTmoWaves, (int64_t)cu_count() * 6);
+  const dim3 grid((unsigned)std::max<int64_t>(1, blocks));
+  if (a.hd == 128)
+    triattn_out_rows<128><<<grid, 64 * kTmoWaves, 0, stream>>>(a);
+  else
+    triattn_out_rows<64><<<grid, 64 * kTmoWaves, 0, stream>>>(a);
 }
 
 void launch_pair_add_transposed(const bf16* base, const bf16* t, bf16* out, int64_t batch, int n,

@@ -55,15 +55,6 @@ __device__ __forceinline__ int vkey_pos(int key) {
 // streamed from x32 [M][K].
 // Epilogue: lane (li, g) holds token m0 + li and outputs o = 32 ot + 8 v + 4 g + e
 // (acc[4 v + e]).
-__device__ __forceinline__ void split8(const f32x4& a, const f32x4& b, bf16x8& hi, bf16x8& lo) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    hi[e] = (bf16)a[e];
-    hi[4 + e] = (bf16)b[e];
-    lo[e] = (bf16)(a[e] - (float)hi[e]);
-    lo[4 + e] = (bf16)(b[e] - (float)hi[4 + e]);
-  }
-}
 
 constexpr int kGemmWaves = 8;
 
@@ -110,6 +101,9 @@ __device__ inline int64_t opm_msa_row(const RowGemmArgs& a, int64_t m) {
   return (b * a.depth + s) * a.n + j;
 }
 
+// kEpiApb's width of one projection (q, k, v and, with apb_no_gate == 0, the gate).
+__device__ __forceinline__ int apb_width(const RowGemmArgs& a) { return a.O / (a.apb_no_gate ? 3 : 4); }
+
 // The weight row (fp32, K values) multiplied by row li of output tile ot, and the tile's
 // segment and first channel as the epilogue reads them (packed tiles: see kEpiTrimul and
 // kEpiSwiglu below).
@@ -119,7 +113,7 @@ __device__ inline const float* tile_weight_row(const RowGemmArgs& a, int ot, int
   seg = 0;
   cbase = 0;
   if (EPI == kEpiApb) {
-    const int cs = a.O / 4;
+    const int cs = apb_width(a);
     seg = (ot * 32) / cs;
     cbase = ot * 32 - seg * cs;
     const float* base = seg == 0 ? a.w0 : seg == 1 ? a.w1 : seg == 2 ? a.w2 : a.w3;
@@ -202,7 +196,7 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
   // the bias of output o (global index gi of src when not staged)
   auto obias = [&](int o, const float* src, int gi) { return lb ? lb[o] : (src ? src[gi] : 0.f); };
   if (EPI == kEpiApb && a.flash_rows > 0) {
-    const int cs = a.O / 4;
+    const int cs = apb_width(a);
     int64_t bn, b;
     int j, r;
     if (tr) {
@@ -264,7 +258,7 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
       __builtin_amdgcn_wave_barrier();
     }
   } else if (EPI == kEpiApb) {
-    const int cs = a.O / 4;
+    const int cs = apb_width(a);
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int c = cbase + 8 * v + 4 * g;
@@ -636,7 +630,7 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
   for (int o = tid; o < a.O; o += 64 * kStreamWaves) {
     float v = 0.f;
     if (EPI == kEpiApb) {
-      const int cs = a.O / 4, seg = o / cs, c = o - seg * cs;
+      const int cs = apb_width(a), seg = o / cs, c = o - seg * cs;
       if (seg == 0 && a.q_bias) v = a.q_bias[c];
       if (seg == 3 && a.gate_b) v = a.gate_b[c];
     } else if (EPI == kEpiResid && a.bias_out) {

@@ -64,14 +64,19 @@ def test_workspace_sizes_follow_the_layouts(lib):
     assert lib.ffk_triangle_attention_workspace(b, n, 128, 4, 32, 2) == ta + update + up(128 * 128 * 2)
     assert lib.ffk_triangle_attention_workspace(b, n, 128, 4, 32, 3) == 0
     # generic widths: 16- and 32-wide heads take the flash core's layouts (rows padded to 4,
-    # keys to 32, blocked bias) and stage the gated output in bf16; others the token layouts
-    # with an fp32 gated output; both stage the gate (bf16)
+    # keys to 32, blocked bias) and stage the attention output in bf16; others the token layouts
+    # with an fp32 gated output; the gate is staged (bf16) except where the output kernel
+    # computes it
     np32, r4 = 320, 300
     tok = b * n * n * 64
-    flash16 = 3 * up(b * 4 * r4 * np32 * 16 * 2) + up(tok * 2) + up(b * 4 * np32 * np32 * 4) + up(tok * 2)
+    # (pair 64 with 64 or 128 gated channels: the output kernel computes the gate, none staged)
+    flash16 = 3 * up(b * 4 * r4 * np32 * 16 * 2) + up(b * 4 * np32 * np32 * 4) + up(tok * 2)
     assert lib.ffk_triangle_attention_workspace(b, n, 64, 4, 16, 0) == flash16
     assert lib.ffk_triangle_attention_workspace(b, n, 64, 2, 32, 0) == (
-        3 * up(b * 2 * r4 * np32 * 32 * 2) + up(tok * 2) + up(b * 2 * np32 * np32 * 4) + up(tok * 2))
+        3 * up(b * 2 * r4 * np32 * 32 * 2) + up(b * 2 * np32 * np32 * 4) + up(tok * 2))
+    tok128 = b * n * n * 128
+    assert lib.ffk_triangle_attention_workspace(b, n, 128, 8, 16, 0) == (
+        3 * up(b * 8 * r4 * np32 * 16 * 2) + up(tok128 * 2) + up(b * 8 * np32 * np32 * 4) + up(tok128 * 2))
     assert lib.ffk_triangle_attention_workspace(b, n, 64, 8, 8, 0) == (
         3 * up(tok * 2) + up(b * n * 64 * np32 * 2) + up(b * 8 * n * np32 * 4) + up(tok * 4))
     assert lib.ffk_transition_workspace(1000, 128, 4) == 3 * up(4 * 128 * 128 * 2)

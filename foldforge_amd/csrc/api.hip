@@ -162,10 +162,10 @@ struct TrimulWs {
   int* kst;
   size_t bytes;
 };
-// Pair and hidden width 64 on the generic path: one output kernel reading the contraction's
-// planes (its tile index is a 32-bit int).
-bool trimul_planes64(int64_t batch, int64_t n, int c, int h) {
-  return c == 64 && h == 64 && batch * n * ((n + 31) / 32) < 0x7fffffffLL;
+// Pair width 64 with hidden 64 or 128 on the generic path: one output kernel reading the
+// contraction's planes (its tile index is a 32-bit int).
+bool trimul_planes(int64_t batch, int64_t n, int c, int h) {
+  return c == 64 && (h == 64 || h == 128) && batch * n * ((n + 31) / 32) < 0x7fffffffLL;
 }
 
 TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
@@ -180,7 +180,7 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
     w.P = cv.take<bf16>(plane);
     // the token rows of P and the fp32 output projection between the row GEMMs (pair and
     // hidden width 64: one kernel reading the planes)
-    if (!trimul_planes64(batch, n, c, h)) {
+    if (!trimul_planes(batch, n, c, h)) {
       w.Pt = cv.take<bf16>((size_t)batch * n * n * h);
       w.y32 = cv.take<float>((size_t)batch * n * n * c);
     }
@@ -536,7 +536,7 @@ int32_t ffk_triangle_multiplication(
     p.pb = w.B;
     launch_row_gemm(p, kEpiTrimul, kXLn, st);
     launch_trimul_contract(w.A, w.B, w.P, batch * d_hidden, (int)np, st);
-    if (trimul_planes64(batch, n, d_pair, d_hidden)) {
+    if (trimul_planes(batch, n, d_pair, d_hidden)) {
       TrimulPlanesArgs r{};
       r.planes = w.P;
       r.z = static_cast<const bf16*>(z);
@@ -551,9 +551,10 @@ int32_t ffk_triangle_multiplication(
       r.batch = (int)batch;
       r.n = (int)n;
       r.np = (int)np;
+      r.hid = d_hidden;
       r.residual = residual ? 1 : 0;
       r.eps = eps;
-      launch_trimul_out_planes64(r, st);
+      launch_trimul_out_planes(r, st);
       return check_launch("triangle_multiplication");
     }
     launch_planes_to_rows(w.P, w.Pt, (int)batch, d_hidden, (int)n, (int)np, st);

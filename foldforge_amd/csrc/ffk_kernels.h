@@ -218,22 +218,22 @@ struct ApbAttnArgs {
 };
 void launch_apb_attention(const ApbAttnArgs& a, int batch, hipStream_t stream);
 
-// Generic-width triangle multiplication output at pair width 64, hidden width 64:
+// Generic-width triangle multiplication output at pair width 64, hidden width 64 or 128:
 // out = (residual ? z : 0) + (LN_out(p) W_out^T) * sigmoid(LN_pair(z) W_g^T), p the contraction's
 // channel planes.
 struct TrimulPlanesArgs {
-  const bf16* planes;             // [batch][64][np][np]
+  const bf16* planes;             // [batch][hid][np][np]
   const bf16* z;                  // [batch][n][n][64]
-  const float *lno_w, *lno_b;     // centre norm affine [64]
+  const float *lno_w, *lno_b;     // centre norm affine [hid]
   const float *ln_w, *ln_b;       // pair norm affine [64]
-  const float *w_out, *w_gate;    // [64][64] fp32 parameters
+  const float *w_out, *w_gate;    // [64][hid], [64][64] fp32 parameters
   const float* eps_out;           // device epsilon of the centre norm (NULL: eps)
   bf16* out;                      // [batch][n][n][64]; may alias z
-  int batch, n, np;               // batch * n * ceil(n / 32) < 2^31
+  int batch, n, np, hid;          // batch * n * ceil(n / 32) < 2^31
   int residual;
   float eps;
 };
-void launch_trimul_out_planes64(const TrimulPlanesArgs& a, hipStream_t stream);
+void launch_trimul_out_planes(const TrimulPlanesArgs& a, hipStream_t stream);
 
 // Generic-width triangle attention output at pair width 64, gated width hd 64 or 128:
 // out = (residual ? z : 0) + (sigmoid(LN_pair(z) W_g^T + b_g) * o) W_out^T + b_out.

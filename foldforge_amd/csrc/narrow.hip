@@ -46,25 +46,28 @@ __global__ __launch_bounds__(256) void planes_to_rows(const bf16* __restrict__ p
   }
 }
 
-// Generic-width triangle multiplication output for pair width 64 and hidden width 64:
+// Generic-width triangle multiplication output for pair width 64 and hidden width H (64 or 128):
 //   out = z + (LN_out(p) W_out^T) * sigmoid(LN_pair(z) W_g^T)
 // with p read straight from the contraction's channel planes, as one streaming kernel (so the
 // projection never round-trips through memory). Each workgroup converts both weights to bf16
-// once (LDS, rows 72 elements apart); every wave then walks tiles of 32 consecutive keys j of
-// one (b, i) on its own, loading the next tile's plane segments (64 channels x 64 contiguous
-// bytes) and z rows while it works on the current one. The plane segments are turned into token
-// rows through a wave-private LDS tile. Lane (li, g) holds token li's channels 32 g .. 32 g + 31
-// of p and of z; activations enter both products as bf16 hi + lo. The weight rows are stored permuted (row r = 8 v + 4 g + e of output
-// tile t holds channel 32 g + 16 t + 4 v + e), so a lane's accumulators hold the output
-// channels of its own half-row: the two products meet each other and z in registers, and the
-// lane writes its 32 output channels as four 16-byte pieces.
+// once (LDS); every wave then walks tiles of 32 consecutive keys j of one (b, i) on its own,
+// loading the next tile's plane segments (H channels x 64 contiguous bytes) and z rows while
+// it works on the current one. The plane segments become 32 token rows in a wave-private LDS
+// tile; the centre norm reads its statistics from there, then normalises one 8-channel piece
+// per k step (hi + lo) into both output tiles, so no token row is held in registers. Lane
+// (li, g) owns token li: channels H/2 g .. of p, 32 g .. 32 g + 31 of z. The weight rows are
+// stored permuted (row r = 8 v + 4 g + e of output tile t holds channel 32 g + 16 t + 4 v + e),
+// so a lane's accumulators hold the output channels of its own z half-row: the two products
+// meet each other and z in registers, and the lane writes its 32 output channels as four
+// 16-byte pieces.
 constexpr int kTmoWaves = 4;
-constexpr int kTmoWs = 72;  // LDS row stride (elements)
+constexpr int kTmoWs = 72;  // LDS row stride of 64-wide rows (elements)
+template <int H>
 struct __attribute__((aligned(16))) TmoLds {
-  bf16 wo[64 * kTmoWs];
-  bf16 wg[64 * kTmoWs];
-  bf16 rows[kTmoWaves][32 * kTmoWs];  // per wave: the tile's p as 32 token rows
-  float lnow[64], lnob[64], lnw[64], lnb[64];
+  bf16 wo[64 * (H + 8)];              // W_out rows (permuted), k = H
+  bf16 wg[64 * kTmoWs];               // W_g rows (permuted), k = 64
+  bf16 rows[kTmoWaves][32 * (H + 8)];  // per wave: the tile's p as 32 token rows
+  float lnow[H], lnob[H], lnw[64], lnb[64];
 };
 
 __device__ __forceinline__ int tmo_perm(int row) {
@@ -72,19 +75,27 @@ __device__ __forceinline__ int tmo_perm(int row) {
   return 32 * ((r >> 2) & 1) + 16 * t + 4 * (r >> 3) + (r & 3);
 }
 
-__global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_planes64(TrimulPlanesArgs a) {
-  __shared__ TmoLds lds;
+template <int H>
+__global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_planes(TrimulPlanesArgs a) {
+  constexpr int HP = H / 16;  // plane pieces per lane, and 8-channel pieces of a half p row
+  constexpr int RS = H + 8;   // LDS row stride of the token rows and the W_out rows
+  __shared__ TmoLds<H> lds;
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  for (int idx = tid; idx < 2 * 64 * 8; idx += 64 * kTmoWaves) {
-    const int which = idx >> 9, row = (idx >> 3) & 63, ch = 8 * (idx & 7);
-    const float* src = (which ? a.w_gate : a.w_out) + tmo_perm(row) * 64 + ch;
-    *reinterpret_cast<bf16x8*>((which ? lds.wg : lds.wo) + row * kTmoWs + ch) = cvt8(src);
+  for (int idx = tid; idx < 64 * (H / 8); idx += 64 * kTmoWaves) {
+    const int row = idx / (H / 8), ch = 8 * (idx % (H / 8));
+    *reinterpret_cast<bf16x8*>(lds.wo + row * RS + ch) = cvt8(a.w_out + tmo_perm(row) * H + ch);
   }
-  if (tid < 64) {
+  for (int idx = tid; idx < 64 * 8; idx += 64 * kTmoWaves) {
+    const int row = idx >> 3, ch = 8 * (idx & 7);
+    *reinterpret_cast<bf16x8*>(lds.wg + row * kTmoWs + ch) = cvt8(a.w_gate + tmo_perm(row) * 64 + ch);
+  }
+  if (tid < H) {
     lds.lnow[tid] = a.lno_w[tid];
     lds.lnob[tid] = a.lno_b[tid];
+  }
+  if (tid < 64) {
     lds.lnw[tid] = a.ln_w[tid];
     lds.lnb[tid] = a.ln_b[tid];
   }
@@ -99,16 +110,16 @@ __global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_planes64(TrimulPlan
   const int64_t gg = (int64_t)a.np * a.np;
   bf16* trow = lds.rows[wave];
 
-  // Tile (b, i, jt): keys j = 32 jt + li. pc: this lane's 4 plane pieces (piece q = lane + 64 u:
+  // Tile (b, i, jt): keys j = 32 jt + li. pc: this lane's plane pieces (piece q = lane + 64 u:
   // channel q / 4, keys 8 (q % 4) .. + 7; np % 32 == 0 keeps them inside the plane); zr: z row j
   // (the last real one past n). A tile past the end re-reads the last tile.
   auto fetch = [&](int tile, bf16x8* pc, bf16x8* zr) __attribute__((always_inline)) {
     const int tt = tile < tiles ? tile : tiles - 1;
     const int bi = tt / njt, jt = tt - bi * njt;
     const int b = bi / n, i = bi - b * n;
-    const bf16* pl = a.planes + (int64_t)b * 64 * gg + (int64_t)i * a.np + 32 * jt;
+    const bf16* pl = a.planes + (int64_t)b * H * gg + (int64_t)i * a.np + 32 * jt;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < HP; ++u) {
       const int q = lane + 64 * u;
       pc[u] = ld8(pl + (int64_t)(q >> 2) * gg + 8 * (q & 3));
     }
@@ -116,80 +127,107 @@ __global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_planes64(TrimulPlan
 #pragma unroll
     for (int s = 0; s < 4; ++s) zr[s] = ld8(a.z + m * 64 + 32 * g + 8 * s);
   };
-  // LayerNorm of a lane's 32 channels (the row's other 32 in lane li + 32) -> bf16 hi / lo
-  auto norm = [&](const bf16x8* x, const float* w, const float* b, float eps, bf16x8* hi,
-                  bf16x8* lo) __attribute__((always_inline)) {
-    float s1 = 0.f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) s1 += (float)x[s][e];
-    const float mean = pair_sum(s1) * (1.f / 64);
-    float s2 = 0.f;
-#pragma unroll
-    for (int s = 0; s < 4; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float d = (float)x[s][e] - mean;
-        s2 += d * d;
-      }
-    const float rstd = __builtin_amdgcn_rsqf(pair_sum(s2) * (1.f / 64) + eps);
-    // the affine is read per tile (held, it would take 64 registers per norm)
-    int cb = 32 * g;
-    asm volatile("" : "+v"(cb));
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const f32x4 w0 = *reinterpret_cast<const f32x4*>(w + cb + 8 * s);
-      const f32x4 w1 = *reinterpret_cast<const f32x4*>(w + cb + 8 * s + 4);
-      const f32x4 b0 = *reinterpret_cast<const f32x4*>(b + cb + 8 * s);
-      const f32x4 b1 = *reinterpret_cast<const f32x4*>(b + cb + 8 * s + 4);
-      f32x4 y0, y1;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        y0[e] = ((float)x[s][e] - mean) * rstd * w0[e] + b0[e];
-        y1[e] = ((float)x[s][4 + e] - mean) * rstd * w1[e] + b1[e];
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        hi[s][e] = (bf16)y0[e];
-        hi[s][4 + e] = (bf16)y1[e];
-        lo[s][e] = (bf16)(y0[e] - (float)hi[s][e]);
-        lo[s][4 + e] = (bf16)(y1[e] - (float)hi[s][4 + e]);
-      }
-    }
-  };
   auto process = [&](int tile, const bf16x8* pc, const bf16x8* zr) __attribute__((always_inline)) {
     // plane pieces -> token rows (LDS operations of a wave complete in order)
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < HP; ++u) {
       const int q = lane + 64 * u, c = q >> 2, k0 = 8 * (q & 3);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) trow[(k0 + e) * kTmoWs + c] = pc[u][e];
+      for (int e = 0; e < 8; ++e) trow[(k0 + e) * RS + c] = pc[u][e];
     }
     __builtin_amdgcn_wave_barrier();
-    bf16x8 pr[4];
+    const bf16* prow = trow + li * RS + (H / 2) * g;
+    // centre-norm statistics of token li (the row's other half in lane li + 32)
+    float s1 = 0.f;
 #pragma unroll
-    for (int s = 0; s < 4; ++s) pr[s] = ld8(trow + li * kTmoWs + 32 * g + 8 * s);
-    bf16x8 ph[4], pl[4], zh[4], zl[4];
-    norm(pr, lds.lnow, lds.lnob, eps_out, ph, pl);
-    norm(zr, lds.lnw, lds.lnb, a.eps, zh, zl);
+    for (int s = 0; s < HP; ++s) {
+      const bf16x8 x = ld8(prow + 8 * s);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s1 += (float)x[e];
+    }
+    const float mean = pair_sum(s1) * (1.f / H);
+    float s2 = 0.f;
+#pragma unroll
+    for (int s = 0; s < HP; ++s) {
+      const bf16x8 x = ld8(prow + 8 * s);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = (float)x[e] - mean;
+        s2 += d * d;
+      }
+    }
+    const float rstd = __builtin_amdgcn_rsqf(pair_sum(s2) * (1.f / H) + eps_out);
+    int hb = (H / 2) * g, cb = 32 * g;  // per-channel constants read per tile
+    asm volatile("" : "+v"(hb), "+v"(cb));
+    f32x16 ay[2] = {zero16(), zero16()}, ag[2] = {zero16(), zero16()};
+    // output projection, one normalised 8-channel piece per k step into both output tiles
+#pragma unroll
+    for (int s = 0; s < HP; ++s) {
+      const bf16x8 x = ld8(prow + 8 * s);
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(&lds.lnow[hb + 8 * s]);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(&lds.lnow[hb + 8 * s + 4]);
+      const f32x4 b0 = *reinterpret_cast<const f32x4*>(&lds.lnob[hb + 8 * s]);
+      const f32x4 b1 = *reinterpret_cast<const f32x4*>(&lds.lnob[hb + 8 * s + 4]);
+      f32x4 y0, y1;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        y0[e] = ((float)x[e] - mean) * rstd * w0[e] + b0[e];
+        y1[e] = ((float)x[4 + e] - mean) * rstd * w1[e] + b1[e];
+      }
+      bf16x8 hi, lo;
+      split8(y0, y1, hi, lo);
+#pragma unroll
+      for (int t2 = 0; t2 < 2; ++t2) {
+        const bf16x8 w8 = ld8(lds.wo + (32 * t2 + li) * RS + (H / 2) * g + 8 * s);
+        ay[t2] = mfma32(w8, lo, ay[t2]);
+        ay[t2] = mfma32(w8, hi, ay[t2]);
+      }
+    }
+    // gate projection of LN_pair(z)
+    {
+      float z1 = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) z1 += (float)zr[s][e];
+      const float zmean = pair_sum(z1) * (1.f / 64);
+      float z2 = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float d = (float)zr[s][e] - zmean;
+          z2 += d * d;
+        }
+      const float zrstd = __builtin_amdgcn_rsqf(pair_sum(z2) * (1.f / 64) + a.eps);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const f32x4 w0 = *reinterpret_cast<const f32x4*>(&lds.lnw[cb + 8 * s]);
+        const f32x4 w1 = *reinterpret_cast<const f32x4*>(&lds.lnw[cb + 8 * s + 4]);
+        const f32x4 b0 = *reinterpret_cast<const f32x4*>(&lds.lnb[cb + 8 * s]);
+        const f32x4 b1 = *reinterpret_cast<const f32x4*>(&lds.lnb[cb + 8 * s + 4]);
+        f32x4 y0, y1;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          y0[e] = ((float)zr[s][e] - zmean) * zrstd * w0[e] + b0[e];
+          y1[e] = ((float)zr[s][4 + e] - zmean) * zrstd * w1[e] + b1[e];
+        }
+        bf16x8 hi, lo;
+        split8(y0, y1, hi, lo);
+#pragma unroll
+        for (int t2 = 0; t2 < 2; ++t2) {
+          const bf16x8 w8 = ld8(lds.wg + (32 * t2 + li) * kTmoWs + 32 * g + 8 * s);
+          ag[t2] = mfma32(w8, lo, ag[t2]);
+          ag[t2] = mfma32(w8, hi, ag[t2]);
+        }
+      }
+    }
     const int bi = tile / njt, jt = tile - bi * njt;
     const int j = 32 * jt + li;
     const int64_t m = (int64_t)bi * n + j;
 #pragma unroll
     for (int t2 = 0; t2 < 2; ++t2) {
-      const bf16* wor = lds.wo + (32 * t2 + li) * kTmoWs + 32 * g;
-      const bf16* wgr = lds.wg + (32 * t2 + li) * kTmoWs + 32 * g;
-      f32x16 ay = zero16(), ag = zero16();
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bf16x8 wo8 = ld8(wor + 8 * s), wg8 = ld8(wgr + 8 * s);
-        ay = mfma32(wo8, pl[s], ay);
-        ay = mfma32(wo8, ph[s], ay);
-        ag = mfma32(wg8, zl[s], ag);
-        ag = mfma32(wg8, zh[s], ag);
-      }
       bf16x8 y[2];
 #pragma unroll
       for (int v = 0; v < 4; ++v)
@@ -198,7 +236,7 @@ __global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_planes64(TrimulPlan
           const int c = 16 * t2 + 4 * v + e;  // channel within the lane's half
           const float r = a.residual ? (float)zr[c >> 3][c & 7] : 0.f;
           y[v >> 1][4 * (v & 1) + e] =
-              (bf16)(ay[4 * v + e] * sigmoid_scaled(-kLog2e * ag[4 * v + e]) + r);
+              (bf16)(ay[t2][4 * v + e] * sigmoid_scaled(-kLog2e * ag[t2][4 * v + e]) + r);
         }
       if (j < n) {
         bf16* dst = a.out + m * 64 + 32 * g + 16 * t2;
@@ -208,9 +246,9 @@ __global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_planes64(TrimulPlan
     }
   };
 
-  // two register buffers used in turn: the next tile's rows load while the current one is
+  // two register buffers used in turn: the next tile's pieces load while the current one is
   // processed
-  bf16x8 p0[4], z0[4], p1[4], z1[4];
+  bf16x8 p0[HP], z0[4], p1[HP], z1[4];
   fetch(t, p0, z0);
   while (true) {
     fetch(t + stride, p1, z1);
@@ -441,10 +479,14 @@ void launch_planes_to_rows(const bf16* planes, bf16* rows, int batch, int hid, i
                    256, lds, stream>>>(planes, rows, hid, n, np);
 }
 
-void launch_trimul_out_planes64(const TrimulPlanesArgs& a, hipStream_t stream) {
+void launch_trimul_out_planes(const TrimulPlanesArgs& a, hipStream_t stream) {
   const int64_t tiles = (int64_t)a.batch * a.n * ((a.n + 31) / 32);
   const int64_t blocks = std::min<int64_t>((tiles + kTmoWaves - 1) / kTmoWaves, (int64_t)cu_count() * 6);
-  trimul_out_planes64<<<dim3((unsigned)std::max<int64_t>(1, blocks)), 64 * kTmoWaves, 0, stream>>>(a);
+  const dim3 grid((unsigned)std::max<int64_t>(1, blocks));
+  if (a.hid == 128)
+    trimul_out_planes<128><<<grid, 64 * kTmoWaves, 0, stream>>>(a);
+  else
+    trimul_out_planes<64><<<grid, 64 * kTmoWaves, 0, stream>>>(a);
 }
 
 void launch_triattn_out_rows(const TriattnRowsArgs& a, hipStream_t stream) {

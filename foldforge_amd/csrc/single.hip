@@ -1050,11 +1050,13 @@ void launch_row_gemm_t(const RowGemmArgs& a, hipStream_t stream) {
 // Tile shapes: the LayerNorm-fed GEMMs give each workgroup several output tiles (the tile is
 // normalised once per workgroup); the fp32-fed ones split k 8 ways when k is long, and give the
 // waves separate output tiles when k has fewer groups than waves.
-// Output parts: halve the weight rows per workgroup until a workgroup's LDS is at most 56 KiB
-// (three workgroups of 4 waves per CU), as long as the parts stay whole tiles.
+// Output parts: halve the weight rows per workgroup until a workgroup's LDS is at most 72 KiB
+// (two workgroups of 4 waves per CU), as long as the parts stay whole tiles. Measured on the
+// template stacks: splitting at 56 KiB instead (three workgroups per CU, the input read twice
+// for 384 outputs) was 2.5% slower per block.
 int row_stream_parts(int K, int O) {
   int parts = 1;
-  while (row_stream_lds(K, O, O / parts) > 56 * 1024 && (O / 32) % (2 * parts) == 0) parts *= 2;
+  while (row_stream_lds(K, O, O / parts) > 72 * 1024 && (O / 32) % (2 * parts) == 0) parts *= 2;
   return parts;
 }
 

@@ -466,6 +466,10 @@ def shapes_measure(reps: int = 10) -> dict:
               pair_transition_n=2), 4, 64, 0),
         ("template stack block (Boltz-2): pair 64, 4 x 32 heads, hidden 64, transition x4, 4 templates",
          dict(d_pair=64, triangle_model="boltz2", d_hidden_tri_attention=32, pair_transition_n=4), 4, 64, 0),
+        ("template stack block (RoseTTAFold3): pair 64, 4 x 64 heads, hidden 64, transition x4, 4 templates",
+         dict(d_pair=64, triangle_model="rf3", d_hidden_tri_attention=64, pair_transition_n=4), 4, 64, 0),
+        ("trunk block (Chai-1): pair 256, 4 x 64 heads, hidden 256, transition x2, batch 1",
+         dict(d_pair=256, triangle_model="chai1", d_hidden_tri_attention=64, pair_transition_n=2), 1, 256, 0),
         ("confidence head block (AF3): pair 128 + single 384, 5 samples",
          dict(d_pair=128, triangle_model="af3", d_single=384), 5, 128, 384),
     )

@@ -208,7 +208,7 @@ struct TriattnWs {
   size_t bytes;
 };
 // Head widths the generic path runs on the flash core (the rest: apb_attention).
-bool triattn_flash_width(int d) { return d == 16 || d == 32; }
+bool triattn_flash_width(int d) { return d == 16 || d == 32 || d == 64; }
 // Generic widths whose output kernel computes the gate from z (pair 64, gated width 64 or 128):
 // the projection then writes q, k, v only and the flash core the plain attention output.
 bool triattn_gate_out(int c, int heads, int d) {

@@ -255,12 +255,17 @@ __global__ __launch_bounds__(512, 2) void triattn_project(
   wait_vm_lds<0>();  // no LDS write may land after exit
 }
 
-// DQ = head width / 16 (1: 16-wide heads, 2: 32-wide heads).
+// DQ = head width / 16 (1: 16-wide heads, 2: 32-wide heads, 4: 64-wide heads). 64-wide heads
+// take 2 attention rows per workgroup (the stage buffers of 4 would halve the occupancy); a stage
+// then carries as many K / V^T pieces and MFMAs as a 32-wide one of 4 rows.
+template <int DQ>
+constexpr int flash_rows() { return DQ == 4 ? 2 : kFR; }
 template <int DQ>
 struct __attribute__((aligned(16))) FlashLds {
-  bf16 k[2][kFR][kFK * 16 * DQ];  // [key][d], 16-byte pieces at koff
-  bf16 v[2][kFR][16 * DQ * kFK];  // [d][key], 16-byte pieces at voff
-  float bias[kFW][2][1024];       // per wave, two bias tiles (the blocked layout, copied as is)
+  static constexpr int FR = flash_rows<DQ>();
+  bf16 k[2][FR][kFK * 16 * DQ];  // [key][d], 16-byte pieces at koff
+  bf16 v[2][FR][16 * DQ * kFK];  // [d][key], 16-byte pieces at voff
+  float bias[kFW][2][1024];      // per wave, two bias tiles (the blocked layout, copied as is)
 };
 
 // Element offsets of 16-byte piece p of K row `key` (2 DQ pieces: 32 DQ bytes, 8 / DQ rows
@@ -268,7 +273,7 @@ struct __attribute__((aligned(16))) FlashLds {
 // MFMA operand reads of 16 consecutive rows hit distinct banks.
 template <int DQ>
 __device__ __forceinline__ int koff(int key, int p) {
-  constexpr int sh = DQ == 1 ? 3 : 2;
+  constexpr int sh = DQ == 1 ? 3 : DQ == 2 ? 2 : 1;
   return key * 16 * DQ + 8 * (p ^ ((key >> sh) & (2 * DQ - 1)));
 }
 __device__ __forceinline__ int voff(int d, int p) { return d * kFK + 8 * (p ^ ((d >> 2) & 3)); }
@@ -292,30 +297,32 @@ __device__ __forceinline__ float exp_pack(const f32x16& S, bf16x8& p0, bf16x8& p
   return ts;
 }
 
-// grid (ceil(np / 128) * (rows / 4) * batch * heads) workgroups, renumbered per XCD;
-// block 256 = 4 waves x 32 queries, 4 attention rows. GATED: the output is og = gate * o,
+// grid (ceil(np / 128) * (rows / FR) * batch * heads) workgroups, renumbered per XCD;
+// block 256 = 4 waves x 32 queries, FR attention rows. GATED: the output is og = gate * o,
 // else o (bf16 either way).
 template <int DQ, bool GATED>
 __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
-  constexpr int D = 16 * DQ;  // head width
+  constexpr int D = 16 * DQ;            // head width
+  constexpr int FR = flash_rows<DQ>();  // attention rows of the workgroup
+  constexpr int DH = DQ == 4 ? 2 : 1;   // 32-row halves of V^T (and of O^T)
   __shared__ FlashLds<DQ> lds;
   const int64_t np = a.np, rows = a.rows;
   const int heads = a.heads;
   const uint32_t nqb = (uint32_t)((np + 32 * kFW - 1) / (32 * kFW));
-  const uint32_t nrg = (uint32_t)(rows / kFR);
+  const uint32_t nrg = (uint32_t)(rows / FR);
   const uint32_t total = gridDim.x;
   const uint32_t wg = xcd_remap(blockIdx.x, total);
   const uint32_t qb = wg % nqb;
   const uint32_t rg = (wg / nqb) % nrg;
   const int64_t bh = wg / (nqb * nrg);
   const int64_t j0 = (int64_t)qb * 32 * kFW;
-  const int64_t r0 = (int64_t)rg * kFR;
+  const int64_t r0 = (int64_t)rg * FR;
   if (r0 >= a.rows_valid || j0 >= a.n_valid) return;  // whole workgroup outside the output
   const int64_t bidx = bh / heads;
   const int h = (int)(bh % heads);
   const int tid = threadIdx.x;
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;
-  const int dl = DQ == 1 ? li & 15 : li;  // V^T row of this lane (16-wide heads: rows repeat)
+  const int dl = DQ == 1 ? li & 15 : li;  // V^T row (of each half) of this lane (16-wide heads: rows repeat)
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t jw = j0 + 32 * wave;  // first query of this wave
   const bool active = jw < np;        // the last query block may be partial
@@ -327,30 +334,31 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
   const int64_t nrun =
       a.kstages ? min(nstage, ((int64_t)a.kstages[bidx] * 32 + kFK - 1) / kFK) : nstage;
 
-  // Transfers (each one 1 KB LDS DMA per wave): stage s of K / V^T = 8 DQ pieces, 2 DQ per
-  // wave (piece P = 2 DQ wave + u: K pieces first, DQ per row, each 32 / DQ keys; then V^T
-  // pieces, DQ per row, each 16 rows d); bias tile kb of this wave = 4 pieces. Past the last
-  // stage / tile a transfer repeats a real one into a buffer that is no longer read, so every
-  // wave always has the same transfers in flight.
+  // Transfers (each one 1 KB LDS DMA per wave): stage s of K / V^T = 2 FR DQ pieces, FR DQ / 2
+  // per wave (piece P = (FR DQ / 2) wave + u: K pieces first, DQ per row, each 32 / DQ keys;
+  // then V^T pieces, DQ per row, each 16 rows d); bias tile kb of this wave = 4 pieces. Past the
+  // last stage / tile a transfer repeats a real one into a buffer that is no longer read, so
+  // every wave always has the same transfers in flight.
   const bf16* kbase = a.k + (bh * rows + r0) * np * D;
   const bf16* vbase = a.vt + (bh * rows + r0) * D * np;
   const uint32_t k_lds = lds_addr(&lds.k[0][0][0]), v_lds = lds_addr(&lds.v[0][0][0]);
   auto kv_dma = [&](int64_t s, int buf) {
     const int64_t key0 = (s < nstage ? s : nstage - 1) * kFK;
+    constexpr int PW = FR * DQ / 2;  // pieces per wave
 #pragma unroll
-    for (int u = 0; u < 2 * DQ; ++u) {
-      const int P = 2 * DQ * wave + u;  // wave-uniform
-      if (P < 4 * DQ) {
+    for (int u = 0; u < PW; ++u) {
+      const int P = PW * wave + u;  // wave-uniform
+      if (P < FR * DQ) {
         const int rr = P / DQ, i = P % DQ;
         const int key = (32 / DQ) * i + lane / (2 * DQ);
-        const int p = (lane % (2 * DQ)) ^ ((key >> (DQ == 1 ? 3 : 2)) & (2 * DQ - 1));
+        const int p = (lane % (2 * DQ)) ^ ((key >> (DQ == 1 ? 3 : DQ == 2 ? 2 : 1)) & (2 * DQ - 1));
         dma16(kbase, (uint32_t)((((int64_t)rr * np + key0 + key) * D + 8 * p) * 2),
-              k_lds + (uint32_t)(((buf * kFR + rr) * kFK * D + 512 * i) * 2));
+              k_lds + (uint32_t)(((buf * FR + rr) * kFK * D + 512 * i) * 2));
       } else {
-        const int rr = (P - 4 * DQ) / DQ, i = (P - 4 * DQ) % DQ;
+        const int rr = (P - FR * DQ) / DQ, i = (P - FR * DQ) % DQ;
         const int d = 16 * i + (lane >> 2), p = (lane & 3) ^ ((d >> 2) & 3);
         dma16(vbase, (uint32_t)((((int64_t)rr * D + d) * np + key0 + 8 * p) * 2),
-              v_lds + (uint32_t)(((buf * kFR + rr) * D * kFK + 16 * i * kFK) * 2));
+              v_lds + (uint32_t)(((buf * FR + rr) * D * kFK + 16 * i * kFK) * 2));
       }
     }
   };
@@ -366,21 +374,22 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
 
   kv_dma(0, 0);
   bias_dma(0);
-  bf16x8 qa[kFR][DQ];
-  float l[kFR];
-  f32x16 O[kFR];
+  bf16x8 qa[FR][DQ];
+  float l[FR];
+  f32x16 O[FR][DH];
   const bf16x8 zero8 = {};
 #pragma unroll
-  for (int rr = 0; rr < kFR; ++rr) {
+  for (int rr = 0; rr < FR; ++rr) {
 #pragma unroll
     for (int f = 0; f < DQ; ++f)
       qa[rr][f] = active ? ld8(a.q + ((bh * rows + r0 + rr) * np + j) * D + 16 * f + 8 * g) : zero8;
     l[rr] = 0.f;
-    O[rr] = zero16();
+#pragma unroll
+    for (int h = 0; h < DH; ++h) O[rr][h] = zero16();
   }
   // the q loads complete here, not inside the key loop (see settle)
 #pragma unroll
-  for (int rr = 0; rr < kFR; ++rr)
+  for (int rr = 0; rr < FR; ++rr)
 #pragma unroll
     for (int f = 0; f < DQ; ++f) asm volatile("" ::"v"(qa[rr][f]));
   wait_vm_lds<0>();
@@ -424,7 +433,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
     if (active) {
       // two rows at a time: S^T = (bias - m) + K Q^T, softmax, O^T += V^T P^T
 #pragma unroll
-      for (int rp = 0; rp < kFR; rp += 2) {
+      for (int rp = 0; rp < FR; rp += 2) {
         f32x16 S[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
@@ -443,8 +452,11 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
           const int rr = rp + u;
           l[rr] += ts[u];
           const bf16* vtile = lds.v[sb][rr];
-          O[rr] = mfma32(ld8(vtile + voff(dl, g)), p0[u], O[rr]);
-          O[rr] = mfma32(ld8(vtile + voff(dl, 2 + g)), p1[u], O[rr]);
+#pragma unroll
+          for (int h = 0; h < DH; ++h) {
+            O[rr][h] = mfma32(ld8(vtile + voff(dl + 32 * h, g)), p0[u], O[rr][h]);
+            O[rr][h] = mfma32(ld8(vtile + voff(dl + 32 * h, 2 + g)), p1[u], O[rr][h]);
+          }
         }
       }
     }
@@ -460,7 +472,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
   // Exact two-pass softmax of one attention row for this wave's 32 queries, reading K, V^T
   // and the bias tiles straight from global memory (the rare path: rows whose sums left the
   // safe range of the fixed offset).
-  auto exact_row = [&](int rr, f32x16& Orow, float& lrow) {
+  auto exact_row = [&](int rr, f32x16 (&Orow)[DH], float& lrow) {
     const bf16* krow = kbase + (int64_t)rr * np * D + li * D;
     const bf16* vrow = vbase + (int64_t)rr * D * np + (int64_t)dl * np;
     auto logits = [&](int64_t kb) {
@@ -483,7 +495,9 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
     }
     mx = pair_max(mx);
     const float off = mx > -INFINITY ? mx : 0.f;
-    f32x16 o = zero16();
+    f32x16 o[DH];
+#pragma unroll
+    for (int h = 0; h < DH; ++h) o[h] = zero16();
     float ls = 0.f;
     for (int64_t kb = 0; kb < nb; ++kb) {
       f32x16 st = logits(kb);
@@ -491,16 +505,20 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
       for (int i = 0; i < 16; ++i) st[i] -= off;
       bf16x8 p0, p1;
       ls += exp_pack(st, p0, p1);
-      o = mfma32(ld8(vrow + kb * 32 + 8 * g), p0, o);
-      o = mfma32(ld8(vrow + kb * 32 + 16 + 8 * g), p1, o);
+#pragma unroll
+      for (int h = 0; h < DH; ++h) {
+        o[h] = mfma32(ld8(vrow + 32 * h * np + kb * 32 + 8 * g), p0, o[h]);
+        o[h] = mfma32(ld8(vrow + 32 * h * np + kb * 32 + 16 + 8 * g), p1, o[h]);
+      }
     }
-    Orow = o;
+#pragma unroll
+    for (int h = 0; h < DH; ++h) Orow[h] = o[h];
     lrow = ls;
   };
 
   const bool qvalid = j < a.n_valid;
 #pragma unroll
-  for (int rr = 0; rr < kFR; ++rr) {
+  for (int rr = 0; rr < FR; ++rr) {
     const int64_t r = r0 + rr;
     if (r >= a.rows_valid) continue;  // a padded row: nothing to store
     float lt = pair_sum(l[rr]);
@@ -513,20 +531,23 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     const int64_t off = bidx * a.o_sb + r * a.o_sr + j * a.o_sj + h * D;
 #pragma unroll
-    for (int qd = 0; qd < 4; ++qd) {
-      const int d0 = 8 * qd + 4 * g;
-      if (d0 >= D) continue;
-      if (GATED) {
-        const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + off + d0);
-        bf16x4 y;
+    for (int h = 0; h < DH; ++h) {
 #pragma unroll
-        for (int t = 0; t < 4; ++t) y[t] = (bf16)(O[rr][4 * qd + t] * inv * (float)gv[t]);
-        *reinterpret_cast<bf16x4*>(a.og + off + d0) = y;
-      } else {
-        bf16x4 w;
+      for (int qd = 0; qd < 4; ++qd) {
+        const int d0 = 32 * h + 8 * qd + 4 * g;
+        if (d0 >= D) continue;
+        if (GATED) {
+          const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + off + d0);
+          bf16x4 y;
 #pragma unroll
-        for (int t = 0; t < 4; ++t) w[t] = (bf16)(O[rr][4 * qd + t] * inv);
-        st8<kNtFlash>(a.o + off + d0, w);
+          for (int t = 0; t < 4; ++t) y[t] = (bf16)(O[rr][h][4 * qd + t] * inv * (float)gv[t]);
+          *reinterpret_cast<bf16x4*>(a.og + off + d0) = y;
+        } else {
+          bf16x4 w;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) w[t] = (bf16)(O[rr][h][4 * qd + t] * inv);
+          st8<kNtFlash>(a.o + off + d0, w);
+        }
       }
     }
   }
@@ -680,9 +701,15 @@ static int persistent_grid(int ntiles, int per_cu) {
 
 void launch_flash(const FlashArgs& a, hipStream_t stream) {
   const int64_t nqb = (a.np + 32 * kFW - 1) / (32 * kFW);
-  const dim3 grid((unsigned)(nqb * (a.rows / kFR) * a.batch * a.heads));
+  const int fr = a.dh == 64 ? flash_rows<4>() : kFR;
+  const dim3 grid((unsigned)(nqb * (a.rows / fr) * a.batch * a.heads));
   const bool gated = a.og != nullptr;
-  if (a.dh == 16) {
+  if (a.dh == 64) {
+    if (gated)
+      flash_attn_bias<4, true><<<grid, 64 * kFW, 0, stream>>>(a);
+    else
+      flash_attn_bias<4, false><<<grid, 64 * kFW, 0, stream>>>(a);
+  } else if (a.dh == 16) {
     if (gated)
       flash_attn_bias<1, true><<<grid, 64 * kFW, 0, stream>>>(a);
     else

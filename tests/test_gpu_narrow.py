@@ -136,7 +136,8 @@ def test_triattn_wide_heads_match_oracle(starting, key, c, heads, d):
 
 @pytest.mark.parametrize("starting", [True, False])
 @pytest.mark.parametrize("model", ["af3", "protenix"])
-@pytest.mark.parametrize("c,heads,d", [(64, 4, 16), (64, 4, 32), (128, 8, 16), (256, 4, 32)])
+@pytest.mark.parametrize("c,heads,d", [(64, 4, 16), (64, 4, 32), (128, 8, 16), (256, 4, 32), (64, 4, 64),
+                                          (128, 1, 64)])
 @pytest.mark.parametrize("n,lengths", [(40, [40]), (75, [75, 52])])
 def test_triattn_generic_widths_match_oracle(starting, model, c, heads, d, n, lengths):
     z, mask = _pair(n, c, lengths, seed=n + c + heads + d)

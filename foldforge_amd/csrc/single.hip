@@ -184,15 +184,17 @@ __device__ __forceinline__ float row_pre(const RowGemmArgs& a, const int64_t m) 
 // position-contiguous outputs (kEpiApb's flash-layout v^T, kEpiTrimul's channel planes) are
 // transposed and written as 16-byte pieces of 64-byte runs; tr: the tile's run (tile_run),
 // required with stage, whose 32 rows must then be consecutive positions of one run
-// (np % 32 == 0), so those epilogues take both only from the streaming kernel. rpre: the
-// residual values of kEpiResid, loaded by the caller (NULL: loaded here). Channel row r of the tile sits at LDS row
+// (np % 32 == 0), so those epilogues take both only from the streaming kernel. ypre: the y32
+// values of kEpiGateResid, loaded by the caller (NULL: loaded here). rpre: the
+// residual values of kEpiResid and kEpiGateResid, loaded by the caller (NULL: loaded here). Channel row r of the tile sits at LDS row
 // stage_row(r), which puts the rows the two lane halves write at once (r, r + 4) on different
 // banks.
 template <int EPI>
 __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16& acc, const int64_t m, const int ot,
                                     const int seg, const int cbase, const int g, const float* lb,
                                     const float pre, bf16* stage = nullptr,
-                                    const TileRun* tr = nullptr, const bf16x4* rpre = nullptr) {
+                                    const TileRun* tr = nullptr, const bf16x4* rpre = nullptr,
+                                    const f32x4* ypre = nullptr) {
   // the bias of output o (global index gi of src when not staged)
   auto obias = [&](int o, const float* src, int gi) { return lb ? lb[o] : (src ? src[gi] : 0.f); };
   if (EPI == kEpiApb && a.flash_rows > 0) {
@@ -379,8 +381,8 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int c = ot * 32 + 8 * v + 4 * g;
-      yv[v] = *reinterpret_cast<const f32x4*>(a.y32 + m * a.O + c);
-      if (a.residual) rv[v] = *reinterpret_cast<const bf16x4*>(a.res + m * a.O + c);
+      yv[v] = ypre ? ypre[v] : *reinterpret_cast<const f32x4*>(a.y32 + m * a.O + c);
+      if (a.residual) rv[v] = rpre ? rpre[v] : *reinterpret_cast<const bf16x4*>(a.res + m * a.O + c);
     }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -584,31 +586,39 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
 }
 
 // ---------------------------------------------------------------------------- streaming row GEMM
-// The products and epilogues of row_gemm for short rows (K = 64 or 128), as a persistent
+// The products and epilogues of row_gemm for rows of K = 64 to 512 channels, as a persistent
 // kernel: each workgroup converts the weights to bf16 once (LDS, in output-tile order, rows
 // K + 8 elements apart so that the operand reads of 16 rows hit distinct banks), then every
 // wave walks whole 32-row tiles on its own, with no barrier in the loop. With gridDim.y > 1 the
 // output tiles are split into that many equal parts, one per grid row (wide outputs: each
 // workgroup then holds a part of the weights and more workgroups fit on a CU). The next tile's input
 // rows are loaded while the current one is normalised, multiplied for all O / 32 output tiles
-// (activations as bf16 hi + lo, as row_gemm) and stored by the epilogue of each output tile.
+// and stored by the epilogue of each output tile. Rows of up to 128 channels enter the MFMAs as
+// bf16 hi + lo (as row_gemm); LayerNorm-fed rows of 256 as the rounded bf16 normalisation (as
+// the reference's bf16 LayerNorm output), and 512-channel (plain bf16) rows are held in one
+// register buffer, loaded after the last product of the previous tile.
 // Lane (li, g) holds row li's channels (K / 2) g .. (K / 2) g + K / 2 - 1; MFMA step s takes
 // channels (K / 2) g + 8 s .. + 7 of both operands.
-constexpr int kStreamWaves = 4;
+// Waves per workgroup: 4, and 8 (two per SIMD, sharing a weight image of up to 154 KiB, one
+// workgroup per CU) for rows of 256 channels or more.
+__host__ __device__ constexpr int stream_waves(int K) { return K >= 256 ? 8 : 4; }
 
 // LDS of one workgroup holding the weight rows of Op of the O outputs.
 size_t row_stream_lds(int K, int O, int Op) {
   return (size_t)Op * (K + 8) * sizeof(bf16) + (size_t)(2 * K + O) * sizeof(float) +
-         (size_t)kStreamWaves * 32 * 32 * sizeof(bf16);
+         (size_t)stream_waves(K) * 32 * 32 * sizeof(bf16);
 }
 
 template <int EPI, int XSRC, int K>
-__global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
+__global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a) {
+  constexpr int kStreamWaves = stream_waves(K);
   constexpr int KS = K / 16;  // MFMA steps
   constexpr int KH = K / 2;   // channels per lane
   constexpr int WS = K + 8;   // LDS row stride of the weight image (elements)
   constexpr bool BF = XSRC != kXF32;                // bf16 input rows
   constexpr int NX = BF ? KS : 2 * KS;              // 16-byte input pieces per lane
+  constexpr bool LO = XSRC != kXBf16 && K <= 128;   // activations as bf16 hi + lo
+  constexpr bool DB = NX <= 16;                     // two input buffers (64 VGPRs each at most)
   using XT = typename std::conditional<BF, bf16x8, f32x4>::type;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int nt = a.O / 32 / (int)gridDim.y;  // output tiles of this workgroup's part
@@ -666,12 +676,11 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
         x[i] = *reinterpret_cast<const XT*>(a.x32 + row * K + KH * g + 4 * i);
     }
   };
-  auto process = [&](const XT* x, int64_t tile) __attribute__((always_inline)) {
-    // the MFMA operands: hi + lo of the activations (kXBf16: the rows themselves, no lo)
-    bf16x8 xh[KS], xl[XSRC == kXBf16 ? 1 : KS];
+  auto process = [&](XT* x, int64_t tile) __attribute__((always_inline)) {
+    // the MFMA operands: hi + lo of the activations (LO), else the rows of x themselves
+    // (kXLn: normalised in place)
+    bf16x8 xh[LO ? KS : 1], xl[LO ? KS : 1];
     if (XSRC == kXBf16) {
-#pragma unroll
-      for (int s = 0; s < KS; ++s) xh[s] = x[s];
     } else if (XSRC == kXLn) {
       float s1 = 0.f;
 #pragma unroll
@@ -680,6 +689,11 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
         for (int e = 0; e < 8; ++e) s1 += (float)x[s][e];
       const bool plain = a.ln_plain != 0;
       const float mean = plain ? 0.f : pair_sum(s1) * (1.f / K);
+      // (K = 256: each pass converts the bf16 rows again; 128 converted values per lane held
+      // from one pass to the next would not fit in registers)
+      if constexpr (!LO)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) asm volatile("" : "+v"(x[s]));
       float s2 = 0.f;
 #pragma unroll
       for (int s = 0; s < KS; ++s)
@@ -689,22 +703,51 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
           s2 += d * d;
         }
       const float rstd = plain ? 1.f : __builtin_amdgcn_rsqf(pair_sum(s2) * (1.f / K) + eps);
+      if constexpr (!LO)
+#pragma unroll
+        for (int s = 0; s < KS; ++s) asm volatile("" : "+v"(x[s]));
+      const float mr = -mean * rstd;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        // read per tile: held across the loop, the affine would take K registers
+        // read per tile: held across the loop, the affine would take K registers (K = 256: the
+        // offset also waits for the previous step's values, so that the scheduler cannot issue
+        // every step's affine reads at once)
         int c = KH * g + 8 * s;
-        asm volatile("" : "+v"(c));
+        if constexpr (!LO) {
+          if (s > 0)
+            asm volatile("" : "+v"(c) : "v"(x[s - 1]));
+          else
+            asm volatile("" : "+v"(c));
+        } else {
+          asm volatile("" : "+v"(c));
+        }
         const f32x4 w0 = *reinterpret_cast<const f32x4*>(lnp + c);
         const f32x4 w1 = *reinterpret_cast<const f32x4*>(lnp + c + 4);
         const f32x4 b0 = *reinterpret_cast<const f32x4*>(lnp + K + c);
         const f32x4 b1 = *reinterpret_cast<const f32x4*>(lnp + K + c + 4);
         f32x4 y0, y1;
+        if constexpr (LO) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          y0[e] = ((float)x[s][e] - mean) * rstd * w0[e] + b0[e];
-          y1[e] = ((float)x[s][4 + e] - mean) * rstd * w1[e] + b1[e];
+          for (int e = 0; e < 4; ++e) {
+            y0[e] = ((float)x[s][e] - mean) * rstd * w0[e] + b0[e];
+            y1[e] = ((float)x[s][4 + e] - mean) * rstd * w1[e] + b1[e];
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            y0[e] = fmaf(fmaf((float)x[s][e], rstd, mr), w0[e], b0[e]);
+            y1[e] = fmaf(fmaf((float)x[s][4 + e], rstd, mr), w1[e], b1[e]);
+          }
         }
-        split8(y0, y1, xh[s], xl[s]);
+        if constexpr (LO) {
+          split8(y0, y1, xh[s], xl[s]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x[s][e] = (bf16)y0[e];
+            x[s][4 + e] = (bf16)y1[e];
+          }
+        }
       }
     } else {
 #pragma unroll
@@ -713,20 +756,24 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
     const int64_t m = tile * 32 + li;
     const float pre = m < a.M ? row_pre<EPI>(a, m) : 0.f;
     const TileRun tr = staged ? tile_run<EPI>(a, tile * 32) : TileRun{};
-    auto out_tile = [&](int ot, const bf16x4* rpre) __attribute__((always_inline)) {
+    auto out_tile = [&](int ot, const bf16x4* rpre, const f32x4* ypre = nullptr) __attribute__((always_inline)) {
       const bf16* wt = wl + ((ot - ot0) * 32 + li) * WS + KH * g;
       f32x16 acc = zero16();
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const bf16x8 w = *reinterpret_cast<const bf16x8*>(wt + 8 * s);
-        if (XSRC != kXBf16) acc = mfma32(w, xl[s], acc);
-        acc = mfma32(w, xh[s], acc);
+        if constexpr (LO) {
+          acc = mfma32(w, xl[s], acc);
+          acc = mfma32(w, xh[s], acc);
+        } else {
+          acc = mfma32(w, x[s], acc);
+        }
       }
       int seg, cbase;
       (void)tile_weight_row<EPI>(a, ot, li, seg, cbase);
       if (m < a.M)
         row_epilogue<EPI>(a, acc, m, ot, seg, cbase, g, lb, pre, staged ? stage : nullptr,
-                          staged ? &tr : nullptr, rpre);
+                          staged ? &tr : nullptr, rpre, ypre);
     };
     if (EPI == kEpiResid && a.residual && nt <= 4) {
       // the residual of every output tile is loaded before the tile's first store: a wait
@@ -742,25 +789,62 @@ __global__ __launch_bounds__(64 * kStreamWaves) void row_stream(RowGemmArgs a) {
 #pragma unroll
       for (int u = 0; u < 4; ++u)
         if (u < nt) out_tile(ot0 + u, rv[u]);
+    } else if (K >= 256 && ((EPI == kEpiResid && a.residual) || EPI == kEpiGateResid)) {
+      // the epilogue operands of each output tile (y32, the residual) are loaded one tile
+      // ahead, before the previous tile's stores, into two register sets used in turn (rows
+      // of 256 channels or more: shorter rows keep the registers for more waves per SIMD)
+      const int64_t mm = m < a.M ? m : a.M - 1;
+      const int last = ot0 + nt - 1;
+      auto epi_load = [&](int ot, bf16x4 (&rv)[4], f32x4 (&yv)[4]) __attribute__((always_inline)) {
+        ot = ot < last ? ot : last;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int64_t at = mm * a.O + ot * 32 + 8 * v + 4 * g;
+          if (EPI == kEpiGateResid) yv[v] = *reinterpret_cast<const f32x4*>(a.y32 + at);
+          if (a.residual) rv[v] = *reinterpret_cast<const bf16x4*>(a.res + at);
+        }
+      };
+      bf16x4 ra[4], rb[4];
+      f32x4 ya[4], yb[4];
+      epi_load(ot0, ra, ya);
+#pragma unroll 1
+      for (int ot = ot0; ot <= last; ot += 2) {
+        epi_load(ot + 1, rb, yb);
+        out_tile(ot, ra, ya);
+        if (ot == last) break;
+        epi_load(ot + 2, ra, ya);
+        out_tile(ot + 1, rb, yb);
+      }
     } else {
 #pragma unroll 1
       for (int ot = ot0; ot < ot0 + nt; ++ot) out_tile(ot, nullptr);
     }
   };
 
-  // two register buffers used in turn: the next tile's rows load while the current one is
-  // processed
-  XT x0[NX], x1[NX];
-  fetch(x0, t);
-  while (true) {
-    fetch(x1, t + stride);
-    process(x0, t);
-    t += stride;
-    if (t >= tiles) break;
-    fetch(x0, t + stride);
-    process(x1, t);
-    t += stride;
-    if (t >= tiles) break;
+  if constexpr (DB) {
+    // two register buffers used in turn: the next tile's rows load while the current one is
+    // processed
+    XT x0[NX], x1[NX];
+    fetch(x0, t);
+    while (true) {
+      fetch(x1, t + stride);
+      process(x0, t);
+      t += stride;
+      if (t >= tiles) break;
+      fetch(x0, t + stride);
+      process(x1, t);
+      t += stride;
+      if (t >= tiles) break;
+    }
+  } else {
+    XT x0[NX];
+    fetch(x0, t);
+    while (true) {
+      process(x0, t);
+      t += stride;
+      if (t >= tiles) break;
+      fetch(x0, t);
+    }
   }
 }
 
@@ -1053,15 +1137,19 @@ void launch_row_gemm_t(const RowGemmArgs& a, hipStream_t stream) {
 // Output parts: halve the weight rows per workgroup until a workgroup's LDS is at most 72 KiB
 // (two workgroups of 4 waves per CU), as long as the parts stay whole tiles. Measured on the
 // template stacks: splitting at 56 KiB instead (three workgroups per CU, the input read twice
-// for 384 outputs) was 2.5% slower per block.
+// for 384 outputs) was 2.5% slower per block. Rows of 256 channels or more: at most 160 KiB
+// (one workgroup of 8 waves per CU), so that each part re-reads and re-normalises the input
+// rows as few times as possible.
+size_t row_stream_lds_cap(int K) { return (K >= 256 ? 160 : 72) * 1024; }
 int row_stream_parts(int K, int O) {
   int parts = 1;
-  while (row_stream_lds(K, O, O / parts) > 72 * 1024 && (O / 32) % (2 * parts) == 0) parts *= 2;
+  while (row_stream_lds(K, O, O / parts) > row_stream_lds_cap(K) && (O / 32) % (2 * parts) == 0) parts *= 2;
   return parts;
 }
 
 template <int EPI, int XSRC, int K>
 void launch_row_stream_t(const RowGemmArgs& a, hipStream_t stream) {
+  constexpr int kStreamWaves = stream_waves(K);
   const int parts = row_stream_parts(K, a.O);
   const size_t lds = row_stream_lds(K, a.O, a.O / parts);
   auto kernel = row_stream<EPI, XSRC, K>;
@@ -1078,15 +1166,21 @@ void launch_row_stream_t(const RowGemmArgs& a, hipStream_t stream) {
 // The streaming kernel's cases: the pair path's short rows, a part of the weights fitting in LDS.
 template <int EPI, int XSRC>
 bool launch_row_stream(const RowGemmArgs& a, hipStream_t stream) {
-  // k 64 or 128; plain bf16 rows (no normalisation, no lo operand) also 256
-  if (a.K != 64 && a.K != 128 && !(XSRC == kXBf16 && a.K == 256)) return false;
-  if (row_stream_lds(a.K, a.O, a.O / row_stream_parts(a.K, a.O)) > 80 * 1024) return false;
-  if (a.K == 64)
+  // k 64 or 128; bf16 rows (normalised or plain) also 256; plain bf16 rows also 512
+  if (a.K != 64 && a.K != 128 && !(XSRC != kXF32 && a.K == 256) && !(XSRC == kXBf16 && a.K == 512))
+    return false;
+  const size_t cap = a.K >= 256 ? 160 * 1024 : 80 * 1024;
+  if (row_stream_lds(a.K, a.O, a.O / row_stream_parts(a.K, a.O)) > cap) return false;
+  if (a.K == 64) {
     launch_row_stream_t<EPI, XSRC, 64>(a, stream);
-  else if (a.K == 128)
+  } else if (a.K == 128) {
     launch_row_stream_t<EPI, XSRC, 128>(a, stream);
-  else if constexpr (XSRC == kXBf16)
-    launch_row_stream_t<EPI, XSRC, 256>(a, stream);
+  } else if constexpr (XSRC != kXF32) {
+    if (a.K == 256)
+      launch_row_stream_t<EPI, XSRC, 256>(a, stream);
+    else if constexpr (XSRC == kXBf16)
+      launch_row_stream_t<EPI, XSRC, 512>(a, stream);
+  }
   return true;
 }
 

@@ -55,7 +55,7 @@ def _check(got, want, where, what):
 
 
 @pytest.mark.parametrize("outgoing", [True, False])
-@pytest.mark.parametrize("c,h", [(64, 64), (64, 128), (128, 64), (256, 128)])
+@pytest.mark.parametrize("c,h", [(64, 64), (64, 128), (128, 64), (256, 128), (256, 256)])
 @pytest.mark.parametrize("n,lengths", [(37, [37]), (96, [70, 96])])
 def test_trimul_generic_widths_match_oracle(outgoing, c, h, n, lengths):
     z, mask = _pair(n, c, lengths, seed=n + c + h)
@@ -184,4 +184,23 @@ def test_template_stack_block_runs_on_the_kernels():
     where = _pairs(mask)
     rr = ps.rel_rms(got - z, want - z.double(), where)
     print(f"template block: update rel_rms={rr:.2e}", flush=True)
+    assert rr <= 3e-2
+
+
+def test_pair_256_block_runs_on_the_kernels():
+    """A block at Chai-1's trunk widths in AF3's op forms: pair 256, triangle multiplication
+    hidden 256, triangle attention 4 x 64, transition x 2 (256-channel LayerNorm-fed row GEMMs,
+    512-channel squeeze), every op on hip."""
+    n, c = 52, 256
+    z, mask = _pair(n, c, [52, 39], seed=12)
+    block = randomise(factories.pairformer_block(d_pair=c, triangle_model="af3", d_hidden_tri_attention=64,
+                                                 pair_transition_n=2), seed=13).cuda()
+    block.set_backend("hip")
+    dispatch.set_refusal(block, "error")
+    with torch.no_grad():
+        got = block(z.cuda(), mask.cuda()).cpu()
+    want = ps.pairformer_block(z, mask, block.state_dict(), n_head_pair=4, dtype=torch.float64)
+    where = _pairs(mask)
+    rr = ps.rel_rms(got - z, want - z.double(), where)
+    print(f"pair-256 block: update rel_rms={rr:.2e}", flush=True)
     assert rr <= 3e-2

@@ -209,10 +209,10 @@ struct TriattnWs {
 };
 // Head widths the generic path runs on the flash core (the rest: apb_attention).
 bool triattn_flash_width(int d) { return d == 16 || d == 32 || d == 64; }
-// Generic widths whose output kernel computes the gate from z (pair 64, gated width 64 or 128):
-// the projection then writes q, k, v only and the flash core the plain attention output.
+// Generic widths whose output kernel computes the gate from z (pair 64, gated width 64, 128 or
+// 256): the projection then writes q, k, v only and the flash core the plain attention output.
 bool triattn_gate_out(int c, int heads, int d) {
-  return triattn_flash_width(d) && c == 64 && (heads * d == 64 || heads * d == 128);
+  return triattn_flash_width(d) && c == 64 && (heads * d == 64 || heads * d == 128 || heads * d == 256);
 }
 int64_t pad4(int64_t n) { return (n + 3) / 4 * 4; }
 

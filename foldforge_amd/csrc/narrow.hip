@@ -262,7 +262,7 @@ __global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_planes(TrimulPlanes
   }
 }
 
-// Generic-width triangle attention output for pair width 64 and gated width HD (64 or 128):
+// Generic-width triangle attention output for pair width 64 and gated width HD (64, 128, 256):
 //   out = z + (sigmoid(LN_pair(z) W_g^T + b_g) * o) W_out^T + b_out
 // as one streaming kernel (the gate is computed here from z, which the residual reads anyway,
 // instead of being stored by the projection and read by the attention core). Same scheme as
@@ -493,7 +493,9 @@ void launch_triattn_out_rows(const TriattnRowsArgs& a, hipStream_t stream) {
   const int64_t tiles = ((int64_t)a.batch * a.n * a.n + 31) / 32;
   const int64_t blocks = std::min<int64_t>((tiles + kTmoWaves - 1) / kTmoWaves, (int64_t)cu_count() * 6);
   const dim3 grid((unsigned)std::max<int64_t>(1, blocks));
-  if (a.hd == 128)
+  if (a.hd == 256)
+    triattn_out_rows<256><<<grid, 64 * kTmoWaves, 0, stream>>>(a);
+  else if (a.hd == 128)
     triattn_out_rows<128><<<grid, 64 * kTmoWaves, 0, stream>>>(a);
   else
     triattn_out_rows<64><<<grid, 64 * kTmoWaves, 0, stream>>>(a);

@@ -98,13 +98,15 @@ def test_trimul_generic_width_256_tile_contraction():
 
 @pytest.mark.parametrize("starting", [True, False])
 @pytest.mark.parametrize("key", ["rf3", "chai1", "chai1_confidence"])
-def test_triattn_lineage_forms_generic_width_match_oracle(starting, key):
-    """The RoseTTAFold3 and Chai-1 forms on the generic path (pair 64, 4 x 16)."""
+@pytest.mark.parametrize("d", [16, 64])
+def test_triattn_lineage_forms_generic_width_match_oracle(starting, key, d):
+    """The RoseTTAFold3 and Chai-1 forms on the generic path (pair 64, 4 x 16 and RoseTTAFold3's
+    template width 4 x 64)."""
     from tests.test_gpu_ops import _lineage_module, _lineage_oracle
 
     n, c = 75, 64
     z, mask = _pair(n, c, [75, 52], seed=41)
-    m = _lineage_module(key, c, 4, 16, starting, seed=6)
+    m = _lineage_module(key, c, 4, d, starting, seed=6)
     m.set_backend("hip")
     assert m.unsupported(z.cuda(), mask.cuda()) is None
     got = hip_delta(m, z.cuda(), mask.cuda()).cpu()

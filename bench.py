@@ -441,6 +441,24 @@ def opm_measure(reps: int = 20) -> dict:
         row["gflop"] = round(gflop, 2)
         row["hip_tflops"] = round(gflop / row["hip_ms"], 1)
         out["rows"].append(row)
+    # Chai-1's grouped form at its trunk width: 8 groups of 8 channels, product norm, c_z 256
+    out["grouped"] = {"workload": "outer product mean (Chai-1), 512 MSA rows, c_m=64, 8 groups of 8, "
+                                  "product norm, c_z=256, 90% of MSA entries real, bf16", "rows": []}
+    gmod = randomise(factories.outer_product_mean(cm, 256, 64, groups=8), seed=1).cuda()
+    for n in (256, 384):
+        g = torch.Generator().manual_seed(n + 1)
+        m = torch.randn(1, depth, n, cm, generator=g).bfloat16().cuda()
+        rows = (torch.rand(1, depth, n, generator=g) < 0.9).cuda()
+        row = {"n": n}
+        with torch.no_grad():
+            for backend in ("hip", "pytorch"):
+                gmod.set_backend(backend)
+                row[f"{backend}_ms"] = round(
+                    event_time_ms(lambda: gmod(m, rows), reps, warm=max(50, reps)), 4)
+        gflop = (2 * depth * n * n * 512 + 2 * n * n * 512 * 256 + 2 * depth * n * cm * 128) / 1e9
+        row["gflop"] = round(gflop, 2)
+        row["hip_tflops"] = round(gflop / row["hip_ms"], 1)
+        out["grouped"]["rows"].append(row)
     return out
 
 

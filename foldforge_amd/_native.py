@@ -85,6 +85,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         + [c_size_t, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_float, c_float,
            c_int32, c_void_p],
     ),
+    "ffk_outer_product_mean_grouped_workspace": (
+        c_size_t,
+        [c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32],
+    ),
+    "ffk_outer_product_mean_grouped": (
+        c_int32,
+        [c_void_p] * 15
+        + [c_size_t, c_int64, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_float, c_float,
+           c_void_p],
+    ),
     "ffk_attention_pair_bias_workspace": (
         c_size_t,
         [c_int64, c_int64, c_int32, c_int32, c_int32],

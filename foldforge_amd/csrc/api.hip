@@ -1255,6 +1255,23 @@ int32_t ffk_msa_pair_weighted_averaging(
   return check_launch("msa_pair_weighted_averaging");
 }
 
+// Chai-1's grouped form: both sides' projections (64 channels each) and the bf16 output weight.
+struct OpmGroupedWs {
+  bf16 *lt, *rt, *mt, *wp;
+  size_t bytes;
+};
+OpmGroupedWs opm_grouped_ws(void* ws, int64_t batch, int64_t depth, int64_t n, int cz) {
+  Carver cv{static_cast<char*>(ws)};
+  const int64_t sp = pad64(depth);
+  OpmGroupedWs w;
+  w.lt = cv.take<bf16>((size_t)batch * n * 64 * sp);
+  w.rt = cv.take<bf16>((size_t)batch * n * 64 * sp);
+  w.mt = cv.take<bf16>((size_t)batch * n * sp);
+  w.wp = cv.take<bf16>((size_t)cz * 512);
+  w.bytes = cv.used;
+  return w;
+}
+
 size_t ffk_outer_product_mean_workspace(int64_t batch, int64_t depth, int64_t n, int32_t d_msa,
                                         int32_t d_hidden, int32_t d_pair) {
   if (batch <= 0 || depth <= 0 || n <= 0 || d_msa <= 0 || d_hidden <= 0 || d_pair <= 0) return 0;
@@ -1337,6 +1354,88 @@ int32_t ffk_outer_product_mean(
   o.normalize_before_proj = normalize_before_proj ? 1 : 0;
   launch_opm_contract(o, st);
   return check_launch("outer_product_mean");
+}
+
+size_t ffk_outer_product_mean_grouped_workspace(int64_t batch, int64_t depth, int64_t n,
+                                                int32_t d_msa, int32_t groups, int32_t d_group,
+                                                int32_t d_pair) {
+  if (batch <= 0 || depth <= 0 || n <= 0 || d_msa <= 0 || groups <= 0 || d_group <= 0 || d_pair <= 0)
+    return 0;
+  return opm_grouped_ws(nullptr, batch, depth, n, d_pair).bytes;
+}
+
+int32_t ffk_outer_product_mean_grouped(
+    const void* m, const uint8_t* rows_mask, const float* ln_w, const float* ln_b,
+    const float* w_left, const float* b_left, const float* w_right, const float* b_right,
+    const float* norm_w, const float* norm_b, const float* w_out, const float* b_out,
+    const void* residual, void* out, void* workspace, size_t workspace_bytes, int64_t batch,
+    int64_t depth, int64_t n, int32_t d_msa, int32_t groups, int32_t d_group, int32_t d_pair,
+    float eps, float norm_eps, void* stream) {
+  if (int32_t st = check_device()) return st;
+  if (groups != 8 || d_group != 8 || (d_pair != 128 && d_pair != 256))
+    return fail(FFK_ERR_INVALID, "outer_product_mean_grouped: %d groups of %d, d_pair=%d (kernels take 8 groups of 8 and d_pair 128 or 256)", groups, d_group, d_pair);
+  if (d_msa <= 0 || d_msa % 64 != 0 || d_msa > kLnGemmMaxK)
+    return fail(FFK_ERR_INVALID, "outer_product_mean_grouped: d_msa=%d (kernels take a multiple of 64 up to %d)", d_msa, kLnGemmMaxK);
+  if (batch <= 0 || depth <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "outer_product_mean_grouped: empty shape");
+  const int64_t sp = pad64(depth);
+  const int64_t tiles = ((n + 3) / 4) * ((n + 7) / 8) * batch;
+  if (batch > 65535 || tiles > 0x7fffffffLL || batch * n * sp / 32 > 0x7fffffffLL || n * n > 0x7fffffffLL)
+    return fail(FFK_ERR_INVALID, "outer_product_mean_grouped: shape exceeds the launch grid");
+  if (!m || !rows_mask || !ln_w || !ln_b || !w_left || !w_right || !norm_w || !norm_b || !w_out ||
+      !b_out || !out)
+    return fail(FFK_ERR_INVALID, "outer_product_mean_grouped: null argument");
+  if (!aligned16(m) || !aligned16(out) || !aligned16(w_left) || !aligned16(w_right) ||
+      !aligned16(b_out) || (residual && !aligned16(residual)))
+    return fail(FFK_ERR_INVALID, "outer_product_mean_grouped: m/out/residual, the projection weights and the output bias must be 16-byte aligned");
+  const OpmGroupedWs need = opm_grouped_ws(nullptr, batch, depth, n, d_pair);
+  if (!workspace || workspace_bytes < need.bytes || !aligned16(workspace))
+    return fail(FFK_ERR_WORKSPACE, "outer_product_mean_grouped: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
+  const OpmGroupedWs w = opm_grouped_ws(workspace, batch, depth, n, d_pair);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+
+  // LayerNorm + both 64-channel projections, masked, MSA rows contiguous (l^T, r^T)
+  RowGemmArgs p{};
+  p.ln_x = static_cast<const bf16*>(m);
+  p.ln_w = ln_w;
+  p.ln_b = ln_b;
+  p.eps = eps;
+  p.w0 = w_left;
+  p.w1 = w_right;
+  p.bias0 = b_left;
+  p.bias1 = b_right;
+  p.M = batch * n * sp;
+  p.K = d_msa;
+  p.O = 128;
+  p.n = (int)n;
+  p.depth = (int)depth;
+  p.sp = (int)sp;
+  p.rows_mask = rows_mask;
+  p.lt = w.lt;
+  p.rt = w.rt;
+  p.mt = w.mt;
+  launch_row_gemm(p, kEpiOpm, kXLn, st);
+
+  PackJob job{};
+  job.seg[0] = {w_out, w.wp, (int64_t)d_pair * 512, 1.f};
+  job.nseg = 1;
+  launch_pack(job, st);
+
+  OpmGroupedArgs o;
+  o.lt = w.lt;
+  o.rt = w.rt;
+  o.wp = w.wp;
+  o.bias = b_out;
+  o.norm_w = norm_w;
+  o.norm_b = norm_b;
+  o.res = static_cast<const bf16*>(residual);
+  o.out = static_cast<bf16*>(out);
+  o.batch = (int)batch;
+  o.n = (int)n;
+  o.sp = (int)sp;
+  o.cz = d_pair;
+  o.norm_eps = norm_eps;
+  launch_opm_contract_grouped(o, st);
+  return check_launch("outer_product_mean_grouped");
 }
 
 }  // extern "C"

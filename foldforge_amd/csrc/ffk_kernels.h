@@ -299,6 +299,17 @@ struct OpmContractArgs {
   int normalize_before_proj;
 };
 void launch_opm_contract(const OpmContractArgs& a, hipStream_t stream);
+// Chai-1's grouped form: 8 groups of 8 channels a side, product norm, no count division.
+struct OpmGroupedArgs {
+  const bf16 *lt, *rt;               // [batch][n][64][sp]
+  const bf16* wp;                    // [c_z][512] bf16 (to_out.weight rounded, same order)
+  const float *bias, *norm_w, *norm_b;  // [c_z], [512], [512]
+  const bf16* res;                   // [batch][n][n][c_z] or NULL
+  bf16* out;                         // [batch][n][n][c_z]
+  int batch, n, sp, cz;              // cz 128 or 256
+  float norm_eps;
+};
+void launch_opm_contract_grouped(const OpmGroupedArgs& a, hipStream_t stream);
 
 struct PackSeg {
   const float* src;  // NULL: write zeros

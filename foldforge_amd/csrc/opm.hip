@@ -207,6 +207,210 @@ __global__ __launch_bounds__(512) void opm_contract(OpmContractArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------- grouped (Chai-1)
+// Chai-1's grouped outer product mean (legacy/primitives.py:122-136, 8 groups of 8 channels a
+// side; src/foldforge/modules/dense/spec.py:687-688): products only within each group, summed
+// over the MSA rows and divided by nothing,
+//   p[i, j, (g, k, l)] = sum_s l[s, i, 8 g + k] r[s, j, 8 g + l]            (512 per pair)
+//   out[i, j] = LN_0.1(p[i, j]) W_out^T + b_out                 (product norm over the 512)
+// grid: ceil(n / 4) * ceil(n / 8) * batch workgroups of 512 threads, one tile of 4 x 8 tokens.
+// Phase 1: wave w takes token i0 + w / 2 against tokens j0 + 4 (w % 2) .. + 3; a pair's groups
+// sit on the diagonal of the two 32 x 32 MFMA tiles of channel block t (channels 32 t ..
+// 32 t + 31 of both sides), where lane (li, g) holds o[c = 32 t + acc_row(r, g)][e = 32 t + li]
+// in acc[r]: its in-group products are r = 4 (li / 8) + q, q = 0..3 (group 4 t + li / 8,
+// k = 4 g + q, l = li % 8). They go to LDS in fp32 in the (g, k, l) order.
+// Phase 2: one wave per pair normalises the 512 products (two passes over 8 per lane), rounds
+// them to bf16 rows; phase 3: the c_z / 32 output tiles (each over 32 pairs, k = 512; at c_z
+// 128 the k range is split over two waves and summed through LDS), bias and residual added.
+constexpr int kOgC = 64;                      // channels per side (8 groups x 8)
+constexpr int kOgTI = 4, kOgTJ = 8;           // tokens per tile side
+constexpr int kOgPairs = kOgTI * kOgTJ;       // 32
+constexpr int kOgN = 512;                     // products per pair
+constexpr int kOgNS = kOgN + 8;               // LDS row stride of a normalised pair (bf16)
+constexpr int kOgXRows = kOgTI * kOgC, kOgYRows = kOgTJ * kOgC;
+constexpr int kOgXPT = kOgXRows * kOpmCPR / 512, kOgYPT = kOgYRows * kOpmCPR / 512;
+constexpr size_t kOgStageBytes = (size_t)2 * (kOgXRows + kOgYRows) * kOpmKS * sizeof(bf16);
+constexpr size_t kOgProdBytes = (size_t)kOgPairs * kOgN * sizeof(float);
+constexpr size_t kOgNormBytes = (size_t)kOgPairs * kOgNS * sizeof(bf16);
+constexpr size_t kOgLds = kOgStageBytes > kOgProdBytes + kOgNormBytes ? kOgStageBytes : kOgProdBytes + kOgNormBytes;
+
+template <int CZ>
+__global__ __launch_bounds__(512) void opm_contract_grouped(OpmGroupedArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  bf16* xs = reinterpret_cast<bf16*>(smem);  // [2][kOgXRows][kOpmKS]
+  bf16* ys = xs + 2 * kOgXRows * kOpmKS;     // [2][kOgYRows][kOpmKS]
+  float* prod = reinterpret_cast<float*>(smem);                     // [32][512], after phase 1
+  bf16* nrm = reinterpret_cast<bf16*>(smem + kOgProdBytes);         // [32][kOgNS]
+  float* red = reinterpret_cast<float*>(smem);                      // phase 3 (c_z 128) partials
+  const int n = a.n, sp = a.sp;
+  const int nti = (n + kOgTI - 1) / kOgTI, ntj = (n + kOgTJ - 1) / kOgTJ;
+  const uint32_t t = xcd_remap(blockIdx.x, gridDim.x);
+  const int64_t b = t / ((uint32_t)nti * ntj);
+  const int ti = (int)((t / ntj) % nti), tj = (int)(t % ntj);
+  const int i0 = ti * kOgTI, j0 = tj * kOgTJ;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, g = lane >> 5;
+
+  // global -> LDS: a stage is the operand rows (token, channel) x kOpmKC MSA rows, 8 bf16 a chunk
+  const bf16* xsrc[kOgXPT];
+  const bf16* ysrc[kOgYPT];
+  int xoff[kOgXPT], yoff[kOgYPT];
+#pragma unroll
+  for (int u = 0; u < kOgXPT; ++u) {
+    const int c = tid + 512 * u, row = c / kOpmCPR, kc = (c % kOpmCPR) * 8;
+    const int tok = min(i0 + row / kOgC, n - 1);
+    xsrc[u] = a.lt + ((b * n + tok) * kOgC + row % kOgC) * sp + kc;
+    xoff[u] = row * kOpmKS + kc;
+  }
+#pragma unroll
+  for (int u = 0; u < kOgYPT; ++u) {
+    const int c = tid + 512 * u, row = c / kOpmCPR, kc = (c % kOpmCPR) * 8;
+    const int tok = min(j0 + row / kOgC, n - 1);
+    ysrc[u] = a.rt + ((b * n + tok) * kOgC + row % kOgC) * sp + kc;
+    yoff[u] = row * kOpmKS + kc;
+  }
+  bf16x8 rx[kOgXPT], ry[kOgYPT];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int u = 0; u < kOgXPT; ++u) rx[u] = ld8(xsrc[u] + k0);
+#pragma unroll
+    for (int u = 0; u < kOgYPT; ++u) ry[u] = ld8(ysrc[u] + k0);
+  };
+  auto sstore = [&](int buf) {
+#pragma unroll
+    for (int u = 0; u < kOgXPT; ++u)
+      *reinterpret_cast<bf16x8*>(xs + buf * kOgXRows * kOpmKS + xoff[u]) = rx[u];
+#pragma unroll
+    for (int u = 0; u < kOgYPT; ++u)
+      *reinterpret_cast<bf16x8*>(ys + buf * kOgYRows * kOpmKS + yoff[u]) = ry[u];
+  };
+
+  const int wi = wave >> 1, wj = 4 * (wave & 1);
+  f32x16 acc[4][2];
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj)
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) acc[nj][tb] = zero16();
+
+  gload(0);
+  sstore(0);
+  __syncthreads();
+  int buf = 0;
+#pragma unroll 1
+  for (int k0 = 0; k0 < sp; k0 += kOpmKC) {
+    const bool more = k0 + kOpmKC < sp;
+    if (more) gload(k0 + kOpmKC);
+    const bf16* xb = xs + buf * kOgXRows * kOpmKS;
+    const bf16* yb = ys + buf * kOgYRows * kOpmKS;
+#pragma unroll
+    for (int kk = 0; kk < kOpmKC; kk += 16) {
+      bf16x8 av[2];
+#pragma unroll
+      for (int tb = 0; tb < 2; ++tb) av[tb] = ld8(xb + (wi * kOgC + 32 * tb + li) * kOpmKS + kk + 8 * g);
+#pragma unroll
+      for (int nj = 0; nj < 4; ++nj)
+#pragma unroll
+        for (int tb = 0; tb < 2; ++tb)
+          acc[nj][tb] = mfma32(av[tb], ld8(yb + ((wj + nj) * kOgC + 32 * tb + li) * kOpmKS + kk + 8 * g),
+                               acc[nj][tb]);
+    }
+    if (more) sstore(buf ^ 1);
+    __syncthreads();  // also ends every read of the stages before the products land
+    buf ^= 1;
+  }
+
+  // the in-group products, fp32, at p (g, k, l) order
+  const int sel = li >> 3;
+#pragma unroll
+  for (int nj = 0; nj < 4; ++nj)
+#pragma unroll
+    for (int tb = 0; tb < 2; ++tb) {
+      const int pair = wi * kOgTJ + wj + nj;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f32x16& A = acc[nj][tb];
+        const float v = sel == 0 ? A[q] : sel == 1 ? A[4 + q] : sel == 2 ? A[8 + q] : A[12 + q];
+        const int idx = (4 * tb + sel) * 64 + (4 * g + q) * 8 + (li & 7);
+        prod[pair * kOgN + idx] = v;
+      }
+    }
+  __syncthreads();
+
+  // product norm: wave w normalises pairs 4 w .. 4 w + 3, lane L the products 8 L .. 8 L + 7
+  {
+    float nw[8], nb[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      nw[e] = a.norm_w[8 * lane + e];
+      nb[e] = a.norm_b[8 * lane + e];
+    }
+#pragma unroll 1
+    for (int u = 0; u < 4; ++u) {
+      const int pair = 4 * wave + u;
+      const f32x4 x0 = *reinterpret_cast<const f32x4*>(prod + pair * kOgN + 8 * lane);
+      const f32x4 x1 = *reinterpret_cast<const f32x4*>(prod + pair * kOgN + 8 * lane + 4);
+      float x[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+      float s1 = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s1 += x[e];
+      const float mean = wave_sum(s1) * (1.f / kOgN);
+      float s2 = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        x[e] -= mean;
+        s2 += x[e] * x[e];
+      }
+      const float rstd = __builtin_amdgcn_rsqf(wave_sum(s2) * (1.f / kOgN) + a.norm_eps);
+      bf16x8 y;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = (bf16)(x[e] * rstd * nw[e] + nb[e]);
+      *reinterpret_cast<bf16x8*>(nrm + pair * kOgNS + 8 * lane) = y;
+    }
+  }
+  __syncthreads();
+
+  // output projection: D[f][pair] = W_out[f] . nrm[pair] (A = bf16 weight rows, B = pair rows)
+  constexpr int NT = CZ / 32;             // output tiles
+  constexpr int KSPLIT = 8 / NT;          // waves per tile (k split)
+  constexpr int KW = kOgN / KSPLIT;       // k per wave
+  const int ft = wave % NT, kpart = wave / NT;
+  const bf16* wrow = a.wp + (int64_t)(32 * ft + li) * kOgN + kpart * KW + 8 * g;
+  const bf16* orow = nrm + li * kOgNS + kpart * KW + 8 * g;
+  f32x16 acc2 = zero16();
+#pragma unroll 4
+  for (int k = 0; k < KW; k += 16) acc2 = mfma32(ld8(wrow + k), ld8(orow + k), acc2);
+  if (KSPLIT > 1) {
+    // (the product rows are no longer read: the partials of waves NT .. 7 go where they were)
+    if (kpart > 0) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) red[((kpart - 1) * NT * 64 + ft * 64 + lane) * 16 + r] = acc2[r];
+    }
+    __syncthreads();
+    if (kpart != 0) return;
+#pragma unroll
+    for (int w = 1; w < KSPLIT; ++w)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc2[r] += red[((w - 1) * NT * 64 + ft * 64 + lane) * 16 + r];
+  }
+  const int pair = li;
+  const int i = i0 + pair / kOgTJ, j = j0 + pair % kOgTJ;
+  if (i >= n || j >= n) return;
+  const int64_t off = ((b * n + i) * n + j) * CZ;
+#pragma unroll
+  for (int v = 0; v < 4; ++v) {
+    const int f = 32 * ft + 8 * v + 4 * g;
+    const f32x4 bias = *reinterpret_cast<const f32x4*>(a.bias + f);
+    float y[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) y[e] = acc2[4 * v + e] + bias[e];
+    if (a.res) {
+      const bf16x4 r = *reinterpret_cast<const bf16x4*>(a.res + off + f);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] += (float)r[e];
+    }
+    store4(a.out + off + f, y[0], y[1], y[2], y[3]);
+  }
+}
 }  // namespace
 
 void launch_opm_count(const OpmCountArgs& a, hipStream_t stream) {
@@ -225,6 +429,14 @@ void launch_opm_contract(const OpmContractArgs& a, hipStream_t stream) {
   (void)hipFuncSetAttribute(reinterpret_cast<const void*>(opm_contract),
                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)kOpmLds);
   opm_contract<<<dim3((unsigned)(nt * nt * a.batch)), 512, kOpmLds, stream>>>(a);
+}
+
+void launch_opm_contract_grouped(const OpmGroupedArgs& a, hipStream_t stream) {
+  const int64_t tiles = (int64_t)((a.n + kOgTI - 1) / kOgTI) * ((a.n + kOgTJ - 1) / kOgTJ) * a.batch;
+  auto kernel = a.cz == 256 ? opm_contract_grouped<256> : opm_contract_grouped<128>;
+  (void)hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)kOgLds);
+  kernel<<<dim3((unsigned)tiles), 512, kOgLds, stream>>>(a);
 }
 
 }  // namespace ffk

@@ -328,15 +328,16 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
     const int j = (int)(bj - b * a.n);
     const float keep = s < a.depth && a.rows_mask[(b * a.depth + s) * a.n + j] ? 1.f : 0.f;
     const float* bias = seg == 0 ? a.bias0 : a.bias1;
-    bf16* dst = (seg == 0 ? a.lt : a.rt) + bj * 32 * a.sp + s;
+    const int hd = a.O / 2;  // channels a side (32; Chai-1's grouped form 64)
+    bf16* dst = (seg == 0 ? a.lt : a.rt) + bj * hd * a.sp + s;
 #pragma unroll
     for (int v = 0; v < 4; ++v)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int c = 8 * v + 4 * g + e;
+        const int c = cbase + 8 * v + 4 * g + e;
         dst[(int64_t)c * a.sp] = (bf16)((acc[4 * v + e] + (bias ? bias[c] : 0.f)) * keep);
       }
-    if (seg == 0 && g == 0) a.mt[bj * a.sp + s] = (bf16)keep;
+    if (seg == 0 && cbase == 0 && g == 0) a.mt[bj * a.sp + s] = (bf16)keep;
   } else if (EPI == kEpiTrimul) {
     const int hid = a.O / 4;
     const int64_t gg = (int64_t)a.npm * a.npm;

@@ -544,6 +544,77 @@ def outer_product_mean(
     return out
 
 
+def outer_product_mean_grouped_supported(d_msa: int, groups: int, d_group: int, d_pair: int) -> bool:
+    """Widths the grouped (Chai-1) outer-product-mean kernels take."""
+    return 0 < d_msa <= 768 and d_msa % 64 == 0 and groups == 8 and d_group == 8 and d_pair in (128, 256)
+
+
+def outer_product_mean_grouped(
+    m: Tensor,
+    rows_mask: Tensor,
+    *,
+    groups: int,
+    ln_weight: Tensor,
+    ln_bias: Tensor,
+    to_left: Tensor,
+    to_right: Tensor,
+    norm_weight: Tensor,
+    norm_bias: Tensor,
+    to_out: Tensor,
+    to_out_bias: Tensor,
+    left_bias: Tensor | None = None,
+    right_bias: Tensor | None = None,
+    residual: Tensor | None = None,
+    eps: float = 1e-5,
+    norm_eps: float = 0.1,
+    out: Tensor | None = None,
+) -> Tensor:
+    """Chai-1's grouped outer product mean of ``m [B, S, N, c_m]`` bf16 under ``rows_mask
+    [B, S, N]`` bool -> ``[B, N, N, c_z]`` bf16: products within each of ``groups`` channel
+    groups, summed over the MSA rows, the product norm (``norm_weight`` / ``norm_bias``, eps
+    ``norm_eps``), then ``to_out`` (plus ``residual`` when given)."""
+    _need(_on_device(m) and m.is_contiguous() and m.dtype == torch.bfloat16,
+          "m must be a contiguous bf16 device tensor")
+    _need(m.dim() == 4, f"m must be [B, S, N, c_m] (got {tuple(m.shape)})")
+    batch, depth, n, cm = m.shape
+    _need(rows_mask.dtype == torch.bool and tuple(rows_mask.shape) == (batch, depth, n)
+          and rows_mask.device == m.device and rows_mask.is_contiguous(),
+          "rows_mask must be a contiguous bool device tensor [B, S, N]")
+    hidden = to_left.shape[0]
+    cz = to_out.shape[0]
+    _need(hidden % groups == 0, f"d_hidden={hidden} is not a multiple of groups={groups}")
+    dg = hidden // groups
+    _need(outer_product_mean_grouped_supported(cm, groups, dg, cz),
+          f"d_msa={cm} {groups} groups of {dg} d_pair={cz} (the kernels take d_msa a multiple of "
+          "64 up to 768, 8 groups of 8, d_pair 128 or 256)")
+    _need(depth > 0 and n > 0 and batch > 0, "empty MSA")
+    dev = m.device
+    k2 = groups * dg * dg
+    spec = (("ln_weight", ln_weight, (cm,)), ("ln_bias", ln_bias, (cm,)),
+            ("to_left", to_left, (hidden, cm)), ("to_right", to_right, (hidden, cm)),
+            ("norm_weight", norm_weight, (k2,)), ("norm_bias", norm_bias, (k2,)),
+            ("to_out", to_out, (cz, k2)), ("to_out_bias", to_out_bias, (cz,)))
+    ln_w, ln_b, wl, wr, nw, nb, wo, bo = (_param(t, dev, nm, shape) for nm, t, shape in spec)
+    bl = None if left_bias is None else _param(left_bias, dev, "left_bias", (hidden,))
+    br = None if right_bias is None else _param(right_bias, dev, "right_bias", (hidden,))
+    if residual is not None:
+        _need(residual.dtype == torch.bfloat16 and residual.is_contiguous()
+              and tuple(residual.shape) == (batch, n, n, cz) and residual.device == dev,
+              f"residual must be a contiguous bf16 [B, N, N, {cz}] device tensor")
+    out = _output(out, (batch, n, n, cz), torch.bfloat16, dev)
+    lib = _native.lib()
+    ws = _workspace(lib.ffk_outer_product_mean_grouped_workspace(batch, depth, n, cm, groups, dg, cz), dev)
+    status = lib.ffk_outer_product_mean_grouped(
+        m.data_ptr(), rows_mask.data_ptr(), ln_w.data_ptr(), ln_b.data_ptr(), wl.data_ptr(),
+        None if bl is None else bl.data_ptr(), wr.data_ptr(), None if br is None else br.data_ptr(),
+        nw.data_ptr(), nb.data_ptr(), wo.data_ptr(), bo.data_ptr(),
+        None if residual is None else residual.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
+        batch, depth, n, cm, groups, dg, cz, float(eps), float(norm_eps), _stream(dev),
+    )
+    _native.check(status, "outer_product_mean_grouped")
+    return out
+
+
 def blocked_bias(bias: Tensor) -> Tensor:
     """``bias [B, H, Np, Np]`` (query, key; log2 units) -> the flash kernel's blocked fp32 layout
     ``[B * H, Np/32, Np/32, 4, 64, 4]``: entry ``[.., qb, kb, v, lane, e]`` with

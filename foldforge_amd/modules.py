@@ -616,8 +616,6 @@ class OuterProductMean(EngineOp, MasterWeights, nn.Module):
         reason = hip_reason(m, mask)
         if reason is not None:
             return reason
-        if self.groups != 1:
-            return f"groups={self.groups} (the kernels take one group)"
         if m.dtype != torch.bfloat16:
             return f"{m.dtype} MSA activations (the kernels take bf16)"
         if m.dim() != 4 or m.shape[3] != self.d_msa:
@@ -629,8 +627,15 @@ class OuterProductMean(EngineOp, MasterWeights, nn.Module):
         if residual is not None and (residual.dtype != torch.bfloat16
                                      or tuple(residual.shape) != (m.shape[0], m.shape[2], m.shape[2], self.d_pair)):
             return f"residual {tuple(residual.shape)} {residual.dtype}"
-        from foldforge_amd.kernels import outer_product_mean_supported
+        from foldforge_amd.kernels import outer_product_mean_grouped_supported, outer_product_mean_supported
 
+        if self.groups != 1:
+            dg = self.d_hidden // self.groups
+            if not outer_product_mean_grouped_supported(self.d_msa, self.groups, dg, self.d_pair):
+                return (f"d_msa={self.d_msa} {self.groups} groups of {dg} d_pair={self.d_pair} (the "
+                        "grouped kernels take d_msa a multiple of 64 up to 768, 8 groups of 8, "
+                        "d_pair 128 or 256)")
+            return None
         if not outer_product_mean_supported(self.d_msa, self.d_hidden, self.d_pair):
             return (f"d_msa={self.d_msa} d_hidden={self.d_hidden} d_pair={self.d_pair} (the kernels "
                     "take d_msa a multiple of 64 up to 768, d_hidden 32, d_pair 128)")
@@ -647,6 +652,16 @@ class OuterProductMean(EngineOp, MasterWeights, nn.Module):
             return self._forward_pytorch(m, mask, residual)
         from foldforge_amd import kernels
 
+        if self.groups != 1:
+            return kernels.outer_product_mean_grouped(
+                m.contiguous(), mask.contiguous(), groups=self.groups, ln_weight=self.ln_msa.weight,
+                ln_bias=self.ln_msa.bias, to_left=self.to_left.weight, to_right=self.to_right.weight,
+                norm_weight=self.product_norm.weight, norm_bias=self.product_norm.bias,
+                to_out=self.to_out.weight, to_out_bias=self.to_out.bias, left_bias=self.to_left.bias,
+                right_bias=self.to_right.bias,
+                residual=None if residual is None else residual.contiguous(),
+                eps=self.ln_msa.eps, norm_eps=self.product_norm.eps,
+            )
         return kernels.outer_product_mean(
             m.contiguous(), mask.contiguous(), ln_weight=self.ln_msa.weight,
             ln_bias=self.ln_msa.bias, to_left=self.to_left.weight, to_right=self.to_right.weight,

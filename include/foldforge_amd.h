@@ -286,6 +286,31 @@ int32_t ffk_outer_product_mean(
     int32_t d_hidden, int32_t d_pair, float eps, float count_offset,
     int32_t normalize_before_proj, void* stream);
 
+/* Chai-1's grouped outer product mean: d_hidden = groups * d_group channels a side, products
+ * only within each group and summed over the MSA rows (no count division),
+ *   p[b, i, j, (g, k, l)] = sum_s l[b, s, i, g d_group + k] r[b, s, j, g d_group + l],
+ *   out = LN_{norm_eps}(p) W_out^T + b_out (+ residual),
+ * with l, r as in ffk_outer_product_mean. Weights fp32: w_left / w_right [d_hidden][d_msa],
+ * b_left / b_right [d_hidden] or NULL, norm_w / norm_b [groups d_group^2] (the product norm),
+ * w_out [d_pair][groups d_group^2] in the (g, k, l) order, b_out [d_pair]. Served: 8 groups of
+ * 8, d_pair 128 or 256, d_msa a multiple of 64 up to 768; anything else returns
+ * FFK_ERR_INVALID. out may not alias m; residual may be out.
+ * Replaces: engine OuterProductMean.forward with groups > 1, op name "opm"
+ * (src/foldforge/modules/engine/backends.py:48; factory modules.py:184-210 with graph.py:252-264;
+ * equations src/foldforge/models/checkpoints/legacy/primitives.py:62-79,122-136; Chai-1's
+ * widths src/foldforge/modules/dense/spec.py:687-688).
+ */
+size_t ffk_outer_product_mean_grouped_workspace(int64_t batch, int64_t depth, int64_t n,
+                                                int32_t d_msa, int32_t groups, int32_t d_group,
+                                                int32_t d_pair);
+int32_t ffk_outer_product_mean_grouped(
+    const void* m, const uint8_t* rows_mask, const float* ln_w, const float* ln_b,
+    const float* w_left, const float* b_left, const float* w_right, const float* b_right,
+    const float* norm_w, const float* norm_b, const float* w_out, const float* b_out,
+    const void* residual, void* out, void* workspace, size_t workspace_bytes, int64_t batch,
+    int64_t depth, int64_t n, int32_t d_msa, int32_t groups, int32_t d_group, int32_t d_pair,
+    float eps, float norm_eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -112,3 +112,25 @@ def test_outer_product_mean_full_size_matches_the_pytorch_backend():
     assert torch.isfinite(a.float()).all()
     assert torch.equal(a, b)
     _check(a.cpu(), ref.cpu(), "opm full size vs pytorch backend")
+
+
+@pytest.mark.parametrize("batch,depth,n,cm,cz", [(1, 5, 16, 64, 256), (1, 33, 50, 64, 256), (2, 40, 23, 128, 128),
+                                                 (1, 100, 130, 64, 256)])
+def test_grouped_outer_product_mean_matches_oracle(batch, depth, n, cm, cz):
+    """Chai-1's grouped form (8 groups of 8 channels, products within each group summed over the
+    MSA rows, the product norm at eps 0.1, no count division; ``legacy/primitives.py:122-136``)."""
+    m, rows = _inputs(batch, depth, n, cm, seed=depth + n + cz)
+    mod = randomise(factories.outer_product_mean(cm, cz, 64, groups=8), seed=n + 1).cuda()
+    mod.set_backend("hip")
+    assert mod.unsupported(m.cuda(), rows.cuda()) is None
+    mc, rc = m.cuda(), rows.cuda()
+    got = hip_forward(mod, mc, rc).cpu()
+    want = ps.outer_product_mean(m, rows, mod.state_dict(), groups=8, dtype=torch.float64)
+    _check(got, want, f"opm grouped B={batch} S={depth} n={n} c_m={cm} c_z={cz}")
+    pair = torch.randn(batch, n, n, cz, generator=torch.Generator().manual_seed(4)).bfloat16()
+    full = hip_forward(mod, mc, rc, residual=pair.cuda()).cpu()
+    _check(full, want + pair.double(), "opm grouped residual")
+    # masked MSA entries take no part, bit for bit
+    m2 = m.clone()
+    m2[~rows] = -9.0
+    assert torch.equal(hip_forward(mod, m2.cuda(), rc).cpu(), got)

@@ -92,6 +92,10 @@ def test_workspace_sizes_follow_the_layouts(lib):
     opm = lib.ffk_outer_product_mean_workspace(b, depth, n, 64, 32, 128)
     assert opm == 2 * up(b * n * 32 * sp * 2) + up(b * n * sp * 2) + up(b * n * n * 4) + up(128 * 1024 * 2)
     assert lib.ffk_outer_product_mean_workspace(b, 0, n, 64, 32, 128) == 0
+    # the grouped (Chai-1) form: 64 channels a side, no count, the 512-wide output weight
+    og = lib.ffk_outer_product_mean_grouped_workspace(b, depth, n, 64, 8, 8, 256)
+    assert og == 2 * up(b * n * 64 * sp * 2) + up(b * n * sp * 2) + up(256 * 512 * 2)
+    assert lib.ffk_outer_product_mean_grouped_workspace(b, depth, 0, 64, 8, 8, 256) == 0
     assert lib.ffk_triangle_multiplication_workspace(0, n, 128, 128) == 0
 
 

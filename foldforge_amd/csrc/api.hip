@@ -158,7 +158,8 @@ bool triattn_fused(int c, int heads, int d) { return c == 128 && heads == 4 && d
 
 struct TrimulWs {
   bf16 *wp, *wg, *wo, *A, *B, *P, *Pt;
-  float *maskf, *y32, *eps_out;
+  bf16* y;  // the update before the gate (generic path, bf16)
+  float *maskf, *eps_out;
   int* kst;
   size_t bytes;
 };
@@ -178,11 +179,11 @@ TrimulWs trimul_ws(void* ws, int64_t batch, int64_t n, int c, int h) {
     w.A = cv.take<bf16>(plane);
     w.B = cv.take<bf16>(plane);
     w.P = cv.take<bf16>(plane);
-    // the token rows of P and the fp32 output projection between the row GEMMs (pair and
+    // the token rows of P and the bf16 output projection between the row GEMMs (pair and
     // hidden width 64: one kernel reading the planes)
     if (!trimul_planes(batch, n, c, h)) {
       w.Pt = cv.take<bf16>((size_t)batch * n * n * h);
-      w.y32 = cv.take<float>((size_t)batch * n * n * c);
+      w.y = cv.take<bf16>((size_t)batch * n * n * c);
     }
     w.bytes = cv.used;
     return w;
@@ -568,8 +569,8 @@ int32_t ffk_triangle_multiplication(
     o.M = batch * n * n;
     o.K = d_hidden;
     o.O = d_pair;
-    o.h32 = w.y32;
-    launch_row_gemm(o, kEpiStore32, kXLn, st);
+    o.hy = w.y;
+    launch_row_gemm(o, kEpiStoreY, kXLn, st);
     RowGemmArgs f{};
     f.ln_x = static_cast<const bf16*>(z);
     f.ln_w = ln_pair_w;
@@ -579,7 +580,7 @@ int32_t ffk_triangle_multiplication(
     f.M = batch * n * n;
     f.K = d_pair;
     f.O = d_pair;
-    f.y32 = w.y32;
+    f.yin = w.y;
     f.res = static_cast<const bf16*>(z);
     f.out = static_cast<bf16*>(out);
     f.residual = residual ? 1 : 0;

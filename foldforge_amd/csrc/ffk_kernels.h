@@ -106,7 +106,7 @@ void launch_transition(const TransitionArgs& a, hipStream_t stream);
 // three epilogues, x either LayerNorm(ln_x) (kXLn, K <= kLnGemmMaxK) or fp32 rows x32 (kXF32).
 // K % 64 == 0, O % 32 == 0; weights are the fp32 parameters. Pairs served: (kEpiApb, kXLn),
 // (kEpiSwiglu, kXLn), (kEpiResid, kXF32), (kEpiResid, kXLn), (kEpiPwa, kXLn), (kEpiOpm, kXLn), (kEpiTrimul, kXLn),
-// (kEpiStore32, kXLn), (kEpiGateResid, kXLn), (kEpiLinear, kXLn).
+// (kEpiStoreY, kXLn), (kEpiGateResid, kXLn), (kEpiLinear, kXLn).
 enum {
   kEpiApb = 0,
   kEpiSwiglu = 1,
@@ -114,8 +114,8 @@ enum {
   kEpiPwa = 3,
   kEpiOpm = 4,
   kEpiTrimul = 5,     // gated, masked left / right projections into channel planes
-  kEpiStore32 = 6,    // h32 = y (fp32)
-  kEpiGateResid = 7,  // out = res + y32 * sigmoid(y) (or y32 * sigmoid(y))
+  kEpiStoreY = 6,     // hy = y (bf16)
+  kEpiGateResid = 7,  // out = res + yin * sigmoid(y) (or yin * sigmoid(y))
   kEpiLinear = 8,     // y = act(W x + bias_out), bf16 or fp32 rows [M][O]
 };
 // kEpiLinear activations (the C-ABI's FFK_ACT_* values)
@@ -174,8 +174,9 @@ struct RowGemmArgs {
   const uint8_t* mask;
   bf16 *pa, *pb;
   int tmap, npm;
-  const float* y32;  // kEpiGateResid: [M][O]
-  float* h32;  // kEpiSwiglu: [M][hid] = silu(a) * b; kEpiStore32: [M][O] = y
+  const bf16* yin;   // kEpiGateResid: [M][O]
+  float* h32;  // kEpiSwiglu: [M][hid] = silu(a) * b
+  bf16* hy;    // kEpiStoreY: [M][O] = y
   bf16* h16;   // kEpiSwiglu: the hidden rows in bf16 instead (h32 unused)
   const bf16* res;  // kEpiResid: out = res + y (residual) or y, y with bias_out when set
   bf16* out;

@@ -176,6 +176,24 @@ __device__ __forceinline__ float row_pre(const RowGemmArgs& a, const int64_t m) 
   return 0.f;
 }
 
+// The 32 outputs of a tile in 16-byte pieces: lanes l and l ^ 32 (halves g of one row) hold
+// outputs 8 v + 4 g + 0..3 of piece v in acc[4 v ..]; one exchange of 8 values leaves half g with
+// the whole pieces g and 2 + g: y[k][0..7] = outputs 8 (2 k + g) + 0..7. Both lanes of a row run
+// it together (an epilogue's row bound is the same for both halves).
+__device__ __forceinline__ void acc_pieces(const f32x16& acc, int g, float (&y)[2][8]) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = acc[8 * k + e], hi = acc[8 * k + 4 + e];
+      const uint32_t send = __float_as_uint(g ? lo : hi);
+      const auto sw = __builtin_amdgcn_permlane32_swap(send, send, false, false);
+      const float recv = __uint_as_float(g ? sw[0] : sw[1]);
+      y[k][e] = g ? recv : lo;
+      y[k][4 + e] = g ? hi : recv;
+    }
+}
+
 // Epilogue of output tile ot for logical row m (< M): lane half g holds outputs
 // 32 ot + 8 v + 4 g + e in acc[4 v + e]. lb: the per-output biases (q_bias / gate_b of kEpiApb,
 // bias_out of kEpiResid) staged in LDS by output index, or NULL to read them from the arguments.
@@ -184,17 +202,18 @@ __device__ __forceinline__ float row_pre(const RowGemmArgs& a, const int64_t m) 
 // position-contiguous outputs (kEpiApb's flash-layout v^T, kEpiTrimul's channel planes) are
 // transposed and written as 16-byte pieces of 64-byte runs; tr: the tile's run (tile_run),
 // required with stage, whose 32 rows must then be consecutive positions of one run
-// (np % 32 == 0), so those epilogues take both only from the streaming kernel. ypre: the y32
+// (np % 32 == 0), so those epilogues take both only from the streaming kernel. ypre: the yin
 // values of kEpiGateResid, loaded by the caller (NULL: loaded here). rpre: the
-// residual values of kEpiResid and kEpiGateResid, loaded by the caller (NULL: loaded here). Channel row r of the tile sits at LDS row
+// residual values of kEpiResid and kEpiGateResid, loaded by the caller (NULL: loaded here); both
+// as the two 16-byte pieces (acc_pieces) of the lane. Channel row r of the tile sits at LDS row
 // stage_row(r), which puts the rows the two lane halves write at once (r, r + 4) on different
 // banks.
 template <int EPI>
 __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16& acc, const int64_t m, const int ot,
                                     const int seg, const int cbase, const int g, const float* lb,
                                     const float pre, bf16* stage = nullptr,
-                                    const TileRun* tr = nullptr, const bf16x4* rpre = nullptr,
-                                    const f32x4* ypre = nullptr) {
+                                    const TileRun* tr = nullptr, const bf16x8* rpre = nullptr,
+                                    const bf16x8* ypre = nullptr) {
   // the bias of output o (global index gi of src when not staged)
   auto obias = [&](int o, const float* src, int gi) { return lb ? lb[o] : (src ? src[gi] : 0.f); };
   if (EPI == kEpiApb && a.flash_rows > 0) {
@@ -212,20 +231,41 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
       b = bn / a.n;
       r = (int)(bn - b * a.n);
     }
+    if (seg != 2) {
+      // q, k (the flash layouts) and the gate (token rows) as 16-byte pieces of 8 channels of
+      // one head (dh % 8 == 0)
+      float y[2][8];
+      acc_pieces(acc, g, y);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int c = cbase + 8 * (2 * k + g);
+        const int o0 = 32 * ot + 8 * (2 * k + g);
+        const int hh = c / a.dh, d0 = c - hh * a.dh;
+        const int64_t blk = (b * a.heads + hh) * a.flash_rows + r;  // the (b, h, r) block
+        bf16x8 o;
+        if (seg == 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = (bf16)((y[k][e] + obias(o0 + e, a.q_bias, c + e)) * a.q_scale);
+          *reinterpret_cast<bf16x8*>(a.q + (blk * a.np + j) * a.dh + d0) = o;
+        } else if (seg == 1) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[e] = (bf16)y[k][e];
+          *reinterpret_cast<bf16x8*>(a.k + (blk * a.np + j) * a.dh + d0) = o;
+        } else if (j < a.n) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            o[e] = (bf16)sigmoid_scaled((y[k][e] + obias(o0 + e, a.gate_b, c + e) + a.gate_bias) * -kLog2e);
+          *reinterpret_cast<bf16x8*>(a.gate + (bn * a.n + j) * cs + c) = o;
+        }
+      }
+    }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int c = cbase + 8 * v + 4 * g;  // 4 channels of one head (dh % 4 == 0)
-      const int o0 = 32 * ot + 8 * v + 4 * g;
       const int hh = c / a.dh, d0 = c - hh * a.dh;
       const int64_t blk = (b * a.heads + hh) * a.flash_rows + r;  // the (b, h, r) block
       float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
-      if (seg == 0) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = (y[e] + obias(o0 + e, a.q_bias, c + e)) * a.q_scale;
-        store4(a.q + (blk * a.np + j) * a.dh + d0, y[0], y[1], y[2], y[3]);
-      } else if (seg == 1) {
-        store4(a.k + (blk * a.np + j) * a.dh + d0, y[0], y[1], y[2], y[3]);
-      } else if (seg == 2) {
+      if (seg == 2) {
         const int pos = vkey_pos(j);
         if (stage) {
 #pragma unroll
@@ -234,11 +274,6 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
 #pragma unroll
           for (int e = 0; e < 4; ++e) a.vt[(blk * a.dh + d0 + e) * a.np + pos] = (bf16)y[e];
         }
-      } else if (j < a.n) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          y[e] = sigmoid_scaled((y[e] + obias(o0 + e, a.gate_b, c + e) + a.gate_bias) * -kLog2e);
-        store4(a.gate + (bn * a.n + j) * cs + c, y[0], y[1], y[2], y[3]);
       }
     }
     if (seg == 2 && stage) {
@@ -367,34 +402,36 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
                                  8 * part) = *reinterpret_cast<const bf16x8*>(stage + stage_row(r) * 32 + 8 * part);
       __builtin_amdgcn_wave_barrier();
     }
-  } else if (EPI == kEpiStore32) {
+  } else if (EPI == kEpiStoreY) {
+    float y[2][8];
+    acc_pieces(acc, g, y);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = ot * 32 + 8 * v + 4 * g;
-      f32x4 y;
+    for (int k = 0; k < 2; ++k) {
+      bf16x8 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = acc[4 * v + e];
-      *reinterpret_cast<f32x4*>(a.h32 + m * a.O + c) = y;
+      for (int e = 0; e < 8; ++e) o[e] = (bf16)y[k][e];
+      *reinterpret_cast<bf16x8*>(a.hy + m * a.O + ot * 32 + 8 * (2 * k + g)) = o;
     }
   } else if (EPI == kEpiGateResid) {
-    f32x4 yv[4];
-    bf16x4 rv[4];
+    bf16x8 yv[2], rv[2];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = ot * 32 + 8 * v + 4 * g;
-      yv[v] = ypre ? ypre[v] : *reinterpret_cast<const f32x4*>(a.y32 + m * a.O + c);
-      if (a.residual) rv[v] = rpre ? rpre[v] : *reinterpret_cast<const bf16x4*>(a.res + m * a.O + c);
+    for (int k = 0; k < 2; ++k) {
+      const int c = ot * 32 + 8 * (2 * k + g);
+      yv[k] = ypre ? ypre[k] : *reinterpret_cast<const bf16x8*>(a.yin + m * a.O + c);
+      if (a.residual) rv[k] = rpre ? rpre[k] : *reinterpret_cast<const bf16x8*>(a.res + m * a.O + c);
     }
+    float y[2][8];
+    acc_pieces(acc, g, y);
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = ot * 32 + 8 * v + 4 * g;
-      float y[4];
+    for (int k = 0; k < 2; ++k) {
+      bf16x8 o;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        y[e] = yv[v][e] * sigmoid_scaled(-kLog2e * acc[4 * v + e]);
-        if (a.residual) y[e] += (float)rv[v][e];
+      for (int e = 0; e < 8; ++e) {
+        float t = (float)yv[k][e] * sigmoid_scaled(-kLog2e * y[k][e]);
+        if (a.residual) t += (float)rv[k][e];
+        o[e] = (bf16)t;
       }
-      store4(a.out + m * a.O + c, y[0], y[1], y[2], y[3]);
+      *reinterpret_cast<bf16x8*>(a.out + m * a.O + ot * 32 + 8 * (2 * k + g)) = o;
     }
   } else if (EPI == kEpiLinear) {
 #pragma unroll
@@ -421,36 +458,51 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
     }
   } else if (EPI == kEpiSwiglu) {
     const int hid = a.O / 2;
+    f32x4 y[2];
 #pragma unroll
-    for (int v = 0; v < 2; ++v) {
-      f32x4 y;
+    for (int v = 0; v < 2; ++v)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float av = acc[4 * v + e], bv = acc[8 + 4 * v + e];
-        y[e] = av * sigmoid_scaled(-kLog2e * av) * bv;
+        y[v][e] = av * sigmoid_scaled(-kLog2e * av) * bv;
       }
-      if (a.h16)
-        store4(a.h16 + m * hid + ot * 16 + 8 * v + 4 * g, y[0], y[1], y[2], y[3]);
-      else
-        *reinterpret_cast<f32x4*>(a.h32 + m * hid + ot * 16 + 8 * v + 4 * g) = y;
-    }
-  } else {
-    bf16x4 rv[4];
-    if (a.residual) {
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        rv[v] = rpre ? rpre[v] : *reinterpret_cast<const bf16x4*>(a.res + m * a.O + ot * 32 + 8 * v + 4 * g);
-    }
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      const int c = ot * 32 + 8 * v + 4 * g;
-      float y[4] = {acc[4 * v], acc[4 * v + 1], acc[4 * v + 2], acc[4 * v + 3]};
+    if (a.h16) {
+      // hidden 8 v + 4 g + 0..3 in y[v]: one exchange gives half g the 8 channels 8 g .. 8 g + 7
+      bf16x8 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        y[e] += obias(c + e, a.bias_out, c + e);
-        if (a.residual) y[e] += (float)rv[v][e];
+        const uint32_t send = __float_as_uint(g ? y[0][e] : y[1][e]);
+        const auto sw = __builtin_amdgcn_permlane32_swap(send, send, false, false);
+        const float recv = __uint_as_float(g ? sw[0] : sw[1]);
+        o[e] = (bf16)(g ? recv : y[0][e]);
+        o[4 + e] = (bf16)(g ? y[1][e] : recv);
       }
-      store4(a.out + m * a.O + c, y[0], y[1], y[2], y[3]);
+      *reinterpret_cast<bf16x8*>(a.h16 + m * hid + ot * 16 + 8 * g) = o;
+    } else {
+#pragma unroll
+      for (int v = 0; v < 2; ++v)
+        *reinterpret_cast<f32x4*>(a.h32 + m * hid + ot * 16 + 8 * v + 4 * g) = y[v];
+    }
+  } else {
+    bf16x8 rv[2];
+    if (a.residual) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        rv[k] = rpre ? rpre[k] : *reinterpret_cast<const bf16x8*>(a.res + m * a.O + ot * 32 + 8 * (2 * k + g));
+    }
+    float y[2][8];
+    acc_pieces(acc, g, y);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int c = ot * 32 + 8 * (2 * k + g);
+      bf16x8 o;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float t = y[k][e] + obias(c + e, a.bias_out, c + e);
+        if (a.residual) t += (float)rv[k][e];
+        o[e] = (bf16)t;
+      }
+      *reinterpret_cast<bf16x8*>(a.out + m * a.O + c) = o;
     }
   }
 }
@@ -619,7 +671,10 @@ __global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a
   constexpr bool BF = XSRC != kXF32;                // bf16 input rows
   constexpr int NX = BF ? KS : 2 * KS;              // 16-byte input pieces per lane
   constexpr bool LO = XSRC != kXBf16 && K <= 128;   // activations as bf16 hi + lo
-  constexpr bool DB = NX <= 16;                     // two input buffers (64 VGPRs each at most)
+  // the gate / residual epilogue of wide rows loads every output tile's operands (up to 128
+  // VGPRs) at the start of a row tile instead of a second input buffer
+  constexpr bool GR = EPI == kEpiGateResid && K >= 256;
+  constexpr bool DB = NX <= 16 && !GR;              // two input buffers (64 VGPRs each at most)
   using XT = typename std::conditional<BF, bf16x8, f32x4>::type;
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int nt = a.O / 32 / (int)gridDim.y;  // output tiles of this workgroup's part
@@ -678,6 +733,23 @@ __global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a
     }
   };
   auto process = [&](XT* x, int64_t tile) __attribute__((always_inline)) {
+    // GR: every output tile's epilogue operands, loaded first: their wait then comes after the
+    // normalisation and the first products, not right behind the previous tile's stores
+    // (vmcnt counts stores too)
+    bf16x8 gy[GR ? 8 : 1][2], gr[GR ? 8 : 1][2];
+    if constexpr (GR) {
+      const int64_t m0 = tile * 32 + li;
+      const int64_t mm = m0 < a.M ? m0 : a.M - 1;
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u < nt)
+#pragma unroll
+          for (int k = 0; k < 2; ++k) {
+            const int64_t at = mm * a.O + (ot0 + u) * 32 + 8 * (2 * k + g);
+            gy[u][k] = *reinterpret_cast<const bf16x8*>(a.yin + at);
+            if (a.residual) gr[u][k] = *reinterpret_cast<const bf16x8*>(a.res + at);
+          }
+    }
     // the MFMA operands: hi + lo of the activations (LO), else the rows of x themselves
     // (kXLn: normalised in place)
     bf16x8 xh[LO ? KS : 1], xl[LO ? KS : 1];
@@ -757,7 +829,7 @@ __global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a
     const int64_t m = tile * 32 + li;
     const float pre = m < a.M ? row_pre<EPI>(a, m) : 0.f;
     const TileRun tr = staged ? tile_run<EPI>(a, tile * 32) : TileRun{};
-    auto out_tile = [&](int ot, const bf16x4* rpre, const f32x4* ypre = nullptr) __attribute__((always_inline)) {
+    auto out_tile = [&](int ot, const bf16x8* rpre, const bf16x8* ypre = nullptr) __attribute__((always_inline)) {
       const bf16* wt = wl + ((ot - ot0) * 32 + li) * WS + KH * g;
       f32x16 acc = zero16();
 #pragma unroll
@@ -779,34 +851,37 @@ __global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a
     if (EPI == kEpiResid && a.residual && nt <= 4) {
       // the residual of every output tile is loaded before the tile's first store: a wait
       // for a load issued after stores would wait for those stores too (vmcnt counts both)
-      bf16x4 rv[4][4];
+      bf16x8 rv[4][2];
       const int64_t mm = m < a.M ? m : a.M - 1;
 #pragma unroll
       for (int u = 0; u < 4; ++u)
         if (u < nt)
 #pragma unroll
-          for (int v = 0; v < 4; ++v)
-            rv[u][v] = *reinterpret_cast<const bf16x4*>(a.res + mm * a.O + (ot0 + u) * 32 + 8 * v + 4 * g);
+          for (int k = 0; k < 2; ++k)
+            rv[u][k] = *reinterpret_cast<const bf16x8*>(a.res + mm * a.O + (ot0 + u) * 32 + 8 * (2 * k + g));
 #pragma unroll
       for (int u = 0; u < 4; ++u)
         if (u < nt) out_tile(ot0 + u, rv[u]);
+    } else if constexpr (GR) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (u < nt) out_tile(ot0 + u, gr[u], gy[u]);
     } else if (K >= 256 && ((EPI == kEpiResid && a.residual) || EPI == kEpiGateResid)) {
-      // the epilogue operands of each output tile (y32, the residual) are loaded one tile
+      // the epilogue operands of each output tile (yin, the residual) are loaded one tile
       // ahead, before the previous tile's stores, into two register sets used in turn (rows
       // of 256 channels or more: shorter rows keep the registers for more waves per SIMD)
       const int64_t mm = m < a.M ? m : a.M - 1;
       const int last = ot0 + nt - 1;
-      auto epi_load = [&](int ot, bf16x4 (&rv)[4], f32x4 (&yv)[4]) __attribute__((always_inline)) {
+      auto epi_load = [&](int ot, bf16x8 (&rv)[2], bf16x8 (&yv)[2]) __attribute__((always_inline)) {
         ot = ot < last ? ot : last;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int64_t at = mm * a.O + ot * 32 + 8 * v + 4 * g;
-          if (EPI == kEpiGateResid) yv[v] = *reinterpret_cast<const f32x4*>(a.y32 + at);
-          if (a.residual) rv[v] = *reinterpret_cast<const bf16x4*>(a.res + at);
+        for (int k = 0; k < 2; ++k) {
+          const int64_t at = mm * a.O + ot * 32 + 8 * (2 * k + g);
+          if (EPI == kEpiGateResid) yv[k] = *reinterpret_cast<const bf16x8*>(a.yin + at);
+          if (a.residual) rv[k] = *reinterpret_cast<const bf16x8*>(a.res + at);
         }
       };
-      bf16x4 ra[4], rb[4];
-      f32x4 ya[4], yb[4];
+      bf16x8 ra[2], rb[2], ya[2], yb[2];
       epi_load(ot0, ra, ya);
 #pragma unroll 1
       for (int ot = ot0; ot <= last; ot += 2) {
@@ -1190,7 +1265,7 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
   if (xsrc == kXLn) {
     if (epi == kEpiApb && launch_row_stream<kEpiApb, kXLn>(a, stream)) return;
     if (epi == kEpiTrimul && launch_row_stream<kEpiTrimul, kXLn>(a, stream)) return;
-    if (epi == kEpiStore32 && launch_row_stream<kEpiStore32, kXLn>(a, stream)) return;
+    if (epi == kEpiStoreY && launch_row_stream<kEpiStoreY, kXLn>(a, stream)) return;
     if (epi == kEpiGateResid && launch_row_stream<kEpiGateResid, kXLn>(a, stream)) return;
     if (epi == kEpiSwiglu && launch_row_stream<kEpiSwiglu, kXLn>(a, stream)) return;
     if (epi == kEpiResid && a.ln_plain && launch_row_stream<kEpiResid, kXBf16>(a, stream)) return;
@@ -1227,13 +1302,13 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
     launch_row_gemm_t<kEpiOpm, kXLn, 2>(a, stream);
   else if (epi == kEpiTrimul && xsrc == kXLn)
     launch_row_gemm_t<kEpiTrimul, kXLn, 8>(a, stream);
-  else if (epi == kEpiStore32 && xsrc == kXLn) {
+  else if (epi == kEpiStoreY && xsrc == kXLn) {
     if (a.O >= 256)
-      launch_row_gemm_t<kEpiStore32, kXLn, 8>(a, stream);
+      launch_row_gemm_t<kEpiStoreY, kXLn, 8>(a, stream);
     else if (a.O >= 128)
-      launch_row_gemm_t<kEpiStore32, kXLn, 4>(a, stream);
+      launch_row_gemm_t<kEpiStoreY, kXLn, 4>(a, stream);
     else
-      launch_row_gemm_t<kEpiStore32, kXLn, 2>(a, stream);
+      launch_row_gemm_t<kEpiStoreY, kXLn, 2>(a, stream);
   } else if (epi == kEpiLinear && xsrc == kXLn) {
     if (a.O >= 256)
       launch_row_gemm_t<kEpiLinear, kXLn, 8>(a, stream);

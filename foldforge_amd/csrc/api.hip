@@ -892,8 +892,8 @@ int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,
     return fail(FFK_ERR_INVALID, "flash_attention_bias: grid too large");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v_t) || !aligned16(bias))
     return fail(FFK_ERR_INVALID, "flash_attention_bias: q/k/v_t/bias must be 16-byte aligned");
-  if (((uintptr_t)o & 7u) != 0 || (o_sb | o_sr | o_sj) % 4 != 0)
-    return fail(FFK_ERR_INVALID, "flash_attention_bias: o and its strides must be 8-byte aligned");
+  if (((uintptr_t)o & 15u) != 0 || (o_sb | o_sr | o_sj) % 8 != 0)
+    return fail(FFK_ERR_INVALID, "flash_attention_bias: o and its strides must be 16-byte aligned");
   FlashArgs f{};
   f.q = static_cast<const bf16*>(q);
   f.k = static_cast<const bf16*>(k);

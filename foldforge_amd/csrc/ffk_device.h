@@ -445,4 +445,22 @@ __device__ __forceinline__ void ln_tile_128(const bf16* __restrict__ base, int64
   ln_finish(tile, valid, w, b, eps, xh, raw);
 }
 
+// The 32 rows of a 32 x 32 accumulator tile in 16-byte pieces: lanes l and l ^ 32 hold rows
+// 8 v + 4 g + 0..3 of piece v in acc[4 v ..]; one exchange of 8 values leaves half g with the
+// whole pieces g and 2 + g (y[k][0..7] = rows 8 (2 k + g) + 0..7). Both lanes of a pair must run
+// it together.
+__device__ __forceinline__ void acc_pieces(const f32x16& acc, int g, float (&y)[2][8]) {
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float lo = acc[8 * k + e], hi = acc[8 * k + 4 + e];
+      const uint32_t send = __float_as_uint(g ? lo : hi);
+      const auto sw = __builtin_amdgcn_permlane32_swap(send, send, false, false);
+      const float recv = __uint_as_float(g ? sw[0] : sw[1]);
+      y[k][e] = g ? recv : lo;
+      y[k][4 + e] = g ? hi : recv;
+    }
+}
+
 }  // namespace ffk

@@ -176,24 +176,6 @@ __device__ __forceinline__ float row_pre(const RowGemmArgs& a, const int64_t m) 
   return 0.f;
 }
 
-// The 32 outputs of a tile in 16-byte pieces: lanes l and l ^ 32 (halves g of one row) hold
-// outputs 8 v + 4 g + 0..3 of piece v in acc[4 v ..]; one exchange of 8 values leaves half g with
-// the whole pieces g and 2 + g: y[k][0..7] = outputs 8 (2 k + g) + 0..7. Both lanes of a row run
-// it together (an epilogue's row bound is the same for both halves).
-__device__ __forceinline__ void acc_pieces(const f32x16& acc, int g, float (&y)[2][8]) {
-#pragma unroll
-  for (int k = 0; k < 2; ++k)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const float lo = acc[8 * k + e], hi = acc[8 * k + 4 + e];
-      const uint32_t send = __float_as_uint(g ? lo : hi);
-      const auto sw = __builtin_amdgcn_permlane32_swap(send, send, false, false);
-      const float recv = __uint_as_float(g ? sw[0] : sw[1]);
-      y[k][e] = g ? recv : lo;
-      y[k][4 + e] = g ? hi : recv;
-    }
-}
-
 // Epilogue of output tile ot for logical row m (< M): lane half g holds outputs
 // 32 ot + 8 v + 4 g + e in acc[4 v + e]. lb: the per-output biases (q_bias / gate_b of kEpiApb,
 // bias_out of kEpiResid) staged in LDS by output index, or NULL to read them from the arguments.

@@ -531,22 +531,25 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
     const int64_t off = bidx * a.o_sb + r * a.o_sr + j * a.o_sj + h * D;
 #pragma unroll
-    for (int h = 0; h < DH; ++h) {
+    for (int hh = 0; hh < DH; ++hh) {
+      // 16-byte pieces of 8 head channels (half the store instructions of 8-byte ones): half g
+      // ends with pieces g and 2 + g of the tile's 32 rows
+      float y[2][8];
+      acc_pieces(O[rr][hh], g, y);
 #pragma unroll
-      for (int qd = 0; qd < 4; ++qd) {
-        const int d0 = 32 * h + 8 * qd + 4 * g;
-        if (d0 >= D) continue;
+      for (int k = 0; k < 2; ++k) {
+        const int d0 = 32 * hh + 8 * (2 * k + g);
+        if (d0 >= D) continue;  // 16-wide heads: rows 16-31 repeat rows 0-15
+        bf16x8 w;
         if (GATED) {
-          const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + off + d0);
-          bf16x4 y;
+          const bf16x8 gv = *reinterpret_cast<const bf16x8*>(a.gate + off + d0);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) y[t] = (bf16)(O[rr][h][4 * qd + t] * inv * (float)gv[t]);
-          *reinterpret_cast<bf16x4*>(a.og + off + d0) = y;
+          for (int t = 0; t < 8; ++t) w[t] = (bf16)(y[k][t] * inv * (float)gv[t]);
+          *reinterpret_cast<bf16x8*>(a.og + off + d0) = w;
         } else {
-          bf16x4 w;
 #pragma unroll
-          for (int t = 0; t < 4; ++t) w[t] = (bf16)(O[rr][h][4 * qd + t] * inv);
-          st8<kNtFlash>(a.o + off + d0, w);
+          for (int t = 0; t < 8; ++t) w[t] = (bf16)(y[k][t] * inv);
+          st16<kNtFlash>(a.o + off + d0, w);
         }
       }
     }
@@ -559,8 +562,9 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
 // + 31 of positions 32 (w >> 2) .. + 31, for the gate and for the output projection. z and o
 // tiles arrive by LDS DMA two tiles ahead (three-slot rings); LN(z) of the next tile is
 // computed during the current one. A step: the gate times o, in place in the o slot; LN of
-// the next tile; a barrier; the output projection plus the residual, in place in the z slot,
-// and the stores (16 bytes per lane, 64-byte runs per position).
+// the next tile; a barrier; the output projection plus the residual, in place in the z slot.
+// After the next step's first barrier, the finished rows leave as whole 256-byte rows (16
+// bytes per lane), before that slot is refilled.
 __global__ __launch_bounds__(512, 2) void triattn_output(
     const bf16* __restrict__ z, const bf16* __restrict__ o, const float* __restrict__ ln_w,
     const float* __restrict__ ln_b, const bf16* __restrict__ wg, const bf16* __restrict__ wo,
@@ -624,20 +628,31 @@ __global__ __launch_bounds__(512, 2) void triattn_output(
     ln_swz<kPT, 512>(zs[0], xh[0], valid, lnp[0], lnp[1], eps);
   }
   const int p0 = 32 * pt + li;  // this lane's position in both products
-  int buf = 0, k = 0, prev_valid = kPT;
+  int buf = 0, k = 0, prev_valid = kPT, last_buf = 0;
+  int64_t prev_off = 0;
+  // the output rows of a finished tile (all 128 channels, in place in its z slot) as whole
+  // 256-byte rows: wave w stores positions 8 w .. 8 w + 7, 16 lanes a position
+  auto store_rows = [&](const bf16* zrow, int64_t o_off, int o_valid) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int p = 8 * wave + 4 * u + (lane >> 4), c = lane & 15;
+      if (p < o_valid) st16<kNtOutput>(out + o_off + (int64_t)p * 128 + 8 * c, ld8(&zrow[off128(p, c)]));
+    }
+  };
 #pragma unroll 1
   for (int tile = blockIdx.x; tile < ntiles; tile += step, ++k, buf = buf == NB - 1 ? 0 : buf + 1) {
     int valid;
     const int64_t off = where(tile, valid);
     const int nbuf = buf == NB - 1 ? 0 : buf + 1, fbuf = nbuf == NB - 1 ? 0 : nbuf + 1;
-    // this wave's transfers of tile + step have landed (issued after them: the previous
-    // tile's 2 stores, fewer for a partial tile); the barrier publishes everyone's pieces and
-    // LN(z), and retires the previous tile's accesses to ring slot fbuf
-    if (k == 0 || prev_valid < kPT)
-      wait_vm_lds<0>();
-    else
-      wait_vm_lds<2>();
+    // this wave's transfers of tile + step have landed (nothing was issued after them); the
+    // barrier publishes everyone's pieces, LN(z) and the previous tile's output rows, and
+    // retires the previous tile's other accesses to ring slot fbuf
+    wait_vm_lds<0>();
     __syncthreads();
+    if (k > 0) {
+      store_rows(zs[fbuf], prev_off, prev_valid);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the rows are read before the slot is refilled
+    }
     dma(tile + 2 * step, fbuf);
     // gate: D[channel][position], lane position p0, registers channels 32 cb + 8 j + 4 g + e
     {
@@ -680,18 +695,13 @@ __global__ __launch_bounds__(512, 2) void triattn_output(
           v[e] = (bf16)(ao[4 * j + e] + pbias[1][32 * cb + 8 * j + 4 * g + e] + (residual ? (float)zv[e] : 0.f));
         *pz = v;
       }
-      // the block is this wave's own: LDS operations of a wave complete in order
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int chunk = lane + 64 * u;
-        const int p = 32 * pt + (chunk >> 2), c = 4 * cb + (chunk & 3);
-        if (p < valid)
-          st16<kNtOutput>(out + off + (int64_t)p * 128 + 8 * c, ld8(&zrow[off128(p, c)]));
-      }
     }
     prev_valid = valid;
+    prev_off = off;
+    last_buf = buf;
   }
+  __syncthreads();  // every wave's part of the last tile's output rows
+  store_rows(zs[last_buf], prev_off, prev_valid);
   wait_vm_lds<0>();  // no LDS write may land after exit
 }
 

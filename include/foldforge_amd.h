@@ -157,7 +157,8 @@ int32_t ffk_triangle_attention(
  * Shapes: q, k [batch * heads, rows, n_pad, 32] bf16; v_t [batch * heads, rows, 32, n_pad]
  * bf16 (v transposed, the keys of every group of 16 stored in the order 0-3, 8-11, 4-7,
  * 12-15); output bf16 written at o + b*o_sb + r*o_sr + j*o_sj + h*32 + d for
- * r < rows_valid, j < n_valid. n_pad must be a multiple of 128 and rows of 4. A query
+ * r < rows_valid, j < n_valid (o and its strides 16-byte aligned). n_pad must be a multiple
+ * of 128 and rows of 4. A query
  * whose keys are all masked gets a zero output. Replaces the engine's triangle-attention
  * kernel (docs/engine-kernel-gaps.md:10-23 names its sm90 source); no reference C signature.
  */

@@ -124,7 +124,7 @@ def flash_roofline(n: int, length: int, reps: int) -> dict:
     g = torch.Generator(device="cuda").manual_seed(1)
     q = (torch.randn(1, heads, n, np_, d, device="cuda", generator=g) * 0.25).bfloat16()
     k = torch.randn(1, heads, n, np_, d, device="cuda", generator=g).bfloat16()
-    vt = torch.randn(1, heads, n, d, np_, device="cuda", generator=g).bfloat16()
+    vt = torch.randn(1, heads, n, np_ // 32, d, 32, device="cuda", generator=g).bfloat16()  # key-blocked v^T
     bias = torch.randn(1, heads, np_, np_, device="cuda", generator=g)
     keep = torch.arange(np_, device="cuda") < length
     bias = torch.where(keep[None, None, None, :], bias, torch.tensor(float("-inf"), device="cuda"))

@@ -45,7 +45,7 @@ struct TriattnArgs {
   const bf16* wb;    // [32][128], rows < heads carry log2(e) * to_bias, others zero
   const bf16* wg;    // [128][128] to_gate
   const bf16* wo;    // [128][128] to_out
-  bf16 *q, *k, *vt;  // [batch * heads][np][np][32], vt: [batch * heads][np][32][np]
+  bf16 *q, *k, *vt;  // [batch * heads][np][np][32], vt: [batch * heads][np][np / 32][32][32]
   float* bias;       // [batch * heads][np / 32][np / 32][2][32][16] blocked, see triattn.hip
   const int* kstages;  // [batch] key stages holding a real key (written by the weight packing)
   bf16* o;           // [batch][n][n][128] z-frame attention output

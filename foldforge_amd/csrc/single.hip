@@ -254,7 +254,8 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
           for (int e = 0; e < 4; ++e) stage[stage_row(8 * v + 4 * g + e) * 32 + (pos & 31)] = (bf16)y[e];
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) a.vt[(blk * a.dh + d0 + e) * a.np + pos] = (bf16)y[e];
+          for (int e = 0; e < 4; ++e)
+            a.vt[blk * a.dh * a.np + (pos >> 5) * 32 * a.dh + (d0 + e) * 32 + (pos & 31)] = (bf16)y[e];
         }
       }
     }
@@ -271,7 +272,8 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
         const int piece = lane + 64 * u, r = piece >> 2, part = piece & 3;
         const int c = cbase + r, hh = c / a.dh, d = c - hh * a.dh;
         const int64_t blk = (bt * a.heads + hh) * a.flash_rows + rt;
-        *reinterpret_cast<bf16x8*>(a.vt + (blk * a.dh + d) * a.np + jt + 8 * part) =
+        // (v^T blocked by 32 keys; jt is a multiple of 32)
+        *reinterpret_cast<bf16x8*>(a.vt + blk * a.dh * a.np + jt * a.dh + d * 32 + 8 * part) =
             *reinterpret_cast<const bf16x8*>(stage + stage_row(r) * 32 + 8 * part);
       }
       __builtin_amdgcn_wave_barrier();

@@ -237,13 +237,15 @@ __global__ __launch_bounds__(512, 2) void triattn_project(
         }
       }
       __builtin_amdgcn_wave_barrier();
-      // 32 rows of d x 64 key slots: 128 contiguous bytes per row
-      bf16* vd = vto + ((bh * np + r) * 32) * np + s0;
+      // 32 rows of d x 64 key slots = two key blocks of [32 d][32 keys] (v^T blocked by 32 keys:
+      // each block 2 contiguous KB)
+      bf16* vd = vto + ((bh * np + r) * 32) * np + s0 * 32;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int chunk = lane + 64 * u;
         const int d = chunk >> 3, c = chunk & 7;
-        st16<kNtProject>(vd + (int64_t)d * np + 8 * c, ld8(&st[d * kPT + 8 * (c ^ ((d >> 1) & 7))]));
+        st16<kNtProject>(vd + (c >> 2) * 1024 + d * 32 + 8 * (c & 3),
+                         ld8(&st[d * kPT + 8 * (c ^ ((d >> 1) & 7))]));
       }
     }
     if (tile + step < ntiles) {
@@ -356,8 +358,9 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
               k_lds + (uint32_t)(((buf * FR + rr) * kFK * D + 512 * i) * 2));
       } else {
         const int rr = (P - FR * DQ) / DQ, i = (P - FR * DQ) % DQ;
+        // (v^T blocked by 32 keys: the stage's 16 rows d are one contiguous KB)
         const int d = 16 * i + (lane >> 2), p = (lane & 3) ^ ((d >> 2) & 3);
-        dma16(vbase, (uint32_t)((((int64_t)rr * D + d) * np + key0 + 8 * p) * 2),
+        dma16(vbase, (uint32_t)(((int64_t)rr * D * np + key0 * D + d * 32 + 8 * p) * 2),
               v_lds + (uint32_t)(((buf * FR + rr) * D * kFK + 16 * i * kFK) * 2));
       }
     }
@@ -474,7 +477,7 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
   // safe range of the fixed offset).
   auto exact_row = [&](int rr, f32x16 (&Orow)[DH], float& lrow) {
     const bf16* krow = kbase + (int64_t)rr * np * D + li * D;
-    const bf16* vrow = vbase + (int64_t)rr * D * np + (int64_t)dl * np;
+    const bf16* vrow = vbase + (int64_t)rr * D * np + dl * 32;  // key block kb at kb * 32 D
     auto logits = [&](int64_t kb) {
       f32x16 st;
 #pragma unroll
@@ -507,8 +510,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
       ls += exp_pack(st, p0, p1);
 #pragma unroll
       for (int h = 0; h < DH; ++h) {
-        o[h] = mfma32(ld8(vrow + 32 * h * np + kb * 32 + 8 * g), p0, o[h]);
-        o[h] = mfma32(ld8(vrow + 32 * h * np + kb * 32 + 16 + 8 * g), p1, o[h]);
+        o[h] = mfma32(ld8(vrow + kb * 32 * D + 32 * h * 32 + 8 * g), p0, o[h]);
+        o[h] = mfma32(ld8(vrow + kb * 32 * D + 32 * h * 32 + 16 + 8 * g), p1, o[h]);
       }
     }
 #pragma unroll

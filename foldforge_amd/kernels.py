@@ -627,13 +627,17 @@ def blocked_bias(bias: Tensor) -> Tensor:
 
 
 def flash_v_layout(v_t: Tensor) -> Tensor:
-    """``v_t [..., 32, Np]`` -> the flash kernel's v^T layout: inside every group of 16 keys the
-    keys are stored in the order 0-3, 8-11, 4-7, 12-15 (index bits 2 and 3 exchanged)."""
+    """``v_t [..., 32, Np]`` -> the flash kernel's v^T layout ``[..., Np / 32, 32, 32]``: blocked
+    by 32 keys (block ``kb`` holds ``[d][keys 32 kb ..]``), and inside every group of 16 keys
+    the keys stored in the order 0-3, 8-11, 4-7, 12-15 (index bits 2 and 3 exchanged)."""
     n = v_t.shape[-1]
-    _need(n % 16 == 0, "the key count must be a multiple of 16")
+    _need(n % 32 == 0, "the key count must be a multiple of 32")
     idx = torch.arange(n, device=v_t.device)
     perm = (idx & ~12) | ((idx & 4) << 1) | ((idx & 8) >> 1)
-    return v_t[..., perm].contiguous()
+    d = v_t.shape[-2]
+    blocked = v_t[..., perm].unflatten(-1, (n // 32, 32)).transpose(-3, -2)  # [..., Np/32, d, 32]
+    _need(blocked.shape[-2] == d, "v_t must be [..., d, Np]")
+    return blocked.contiguous()
 
 
 def flash_attention_bias(
@@ -649,13 +653,13 @@ def flash_attention_bias(
     """The flash core on prepared operands (see ``ffk_flash_attention_bias``).
 
     ``q, k [B, H, R, Np, 32]`` bf16 (q pre-scaled by ``d^-1/2 log2 e``),
-    ``v_t [B, H, R, 32, Np]`` bf16 from :func:`flash_v_layout`, ``bias_blk`` from
+    ``v_t [B, H, R, Np / 32, 32, 32]`` bf16 from :func:`flash_v_layout`, ``bias_blk`` from
     :func:`blocked_bias`;
     ``out [B, R, n_valid, H * 32]`` bf16 receives ``o`` for rows < rows_valid.
     """
     batch, heads, rows, n_pad, d = q.shape
     _need(d == TRI_HEAD_DIM, f"head dim {d} (the kernel takes {TRI_HEAD_DIM})")
-    _need(k.shape == q.shape and v_t.shape == (batch, heads, rows, d, n_pad), "q/k/v_t shapes")
+    _need(k.shape == q.shape and v_t.shape == (batch, heads, rows, n_pad // 32, d, 32), "q/k/v_t shapes")
     _need(bias_blk.dtype == torch.float32 and bias_blk.numel() == batch * heads * n_pad * n_pad,
           "bias_blk must be the blocked fp32 layout of [B, H, Np, Np]")
     _need(all(t.is_contiguous() for t in (q, k, v_t, bias_blk)), "operands must be contiguous")

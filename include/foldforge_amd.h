@@ -154,9 +154,10 @@ int32_t ffk_triangle_attention(
  * fp32 in log2 units with -inf at masked keys, in the blocked layout
  *   bias_blk[b*heads + h][j / 32][k / 32][v][32 g + j % 32][e],  k % 32 = 8 v + 4 g + e
  * (v in 0..3, g in 0..1, e in 0..3): the register order of the kernel's 32 x 32 logit tiles.
- * Shapes: q, k [batch * heads, rows, n_pad, 32] bf16; v_t [batch * heads, rows, 32, n_pad]
- * bf16 (v transposed, the keys of every group of 16 stored in the order 0-3, 8-11, 4-7,
- * 12-15); output bf16 written at o + b*o_sb + r*o_sr + j*o_sj + h*32 + d for
+ * Shapes: q, k [batch * heads, rows, n_pad, 32] bf16; v_t [batch * heads, rows, n_pad / 32,
+ * 32, 32] bf16 (v transposed and blocked by 32 keys: block kb holds [d][32 keys], the keys of
+ * every group of 16 stored in the order 0-3, 8-11, 4-7, 12-15); output bf16 written at
+ * o + b*o_sb + r*o_sr + j*o_sj + h*32 + d for
  * r < rows_valid, j < n_valid (o and its strides 16-byte aligned). n_pad must be a multiple
  * of 128 and rows of 4. A query
  * whose keys are all masked gets a zero output. Replaces the engine's triangle-attention

@@ -131,7 +131,7 @@ def test_single_and_msa_ops_reject_bad_parameters():
 
 def test_flash_core_rejects_an_output_too_small():
     q = torch.zeros(1, 4, 4, 128, 32, dtype=torch.bfloat16)
-    vt = torch.zeros(1, 4, 4, 32, 128, dtype=torch.bfloat16)
+    vt = torch.zeros(1, 4, 4, 128 // 32, 32, 32, dtype=torch.bfloat16)  # the key-blocked v^T layout
     blk = torch.zeros(1 * 4 * 128 * 128)
     with pytest.raises(ValueError, match="cover"):
         kernels.flash_attention_bias(q, q, vt, blk, torch.zeros(1, 4, 100, 128, dtype=torch.bfloat16),

@@ -24,13 +24,17 @@ def test_blocked_bias_follows_the_register_order():
         assert flat[index] == bias.reshape(B * H, n, n)[bh, j, k]
 
 
-def test_flash_v_layout_swaps_key_bits_2_and_3():
-    vt = torch.arange(2 * 32 * 48, dtype=torch.float32).reshape(2, 32, 48)
+def test_flash_v_layout_blocks_keys_and_swaps_key_bits_2_and_3():
+    vt = torch.arange(2 * 32 * 64, dtype=torch.float32).reshape(2, 32, 64)
     out = kernels.flash_v_layout(vt)
-    for s in range(48):
+    assert out.shape == (2, 2, 32, 32)
+    flat = out.reshape(2, -1)
+    for s in range(64):
         key = (s & ~12) | ((s & 4) << 1) | ((s & 8) >> 1)
-        assert torch.equal(out[..., s], vt[..., key])
-    # the permutation is its own inverse
-    assert torch.equal(kernels.flash_v_layout(out), vt)
-    # within each 16-group: stored positions 0-3, 4-7, 8-11, 12-15 hold keys 0-3, 8-11, 4-7, 12-15
-    assert out[0, 0, :16].tolist() == [float(x) for x in [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]]
+        for d in (0, 7, 31):
+            # the documented index: block s / 32, row d, slot s % 32
+            assert flat[1, (s // 32) * 32 * 32 + d * 32 + s % 32] == vt[1, d, key]
+    # within each 16-group: stored slots 0-3, 4-7, 8-11, 12-15 hold keys 0-3, 8-11, 4-7, 12-15
+    assert out[0, 0, 0, :16].tolist() == [float(x) for x in [0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15]]
+    # the second block holds keys 32 .. 63 of the same rows
+    assert out[0, 1, 0, :4].tolist() == [32.0, 33.0, 34.0, 35.0]

@@ -280,15 +280,16 @@ __global__ __launch_bounds__(256) void trimul_contract(const bf16* __restrict__ 
 }
 
 // The same product with 256 x 256 output tiles for np % 256 == 0: 8 waves of 128 x 64, the
-// operand tiles (256 rows x 32 k of X and of Y, 32 KB a stage) arrive by LDS DMA in a
-// four-stage ring, three stages ahead, so a plane's operands are read twice rather than
-// four times and the loads of three k steps are in flight behind the MFMAs. Operand rows
-// are 64 bytes with their 16-byte pieces XOR-swizzled by (row / 4) % 4, so the sixteen rows
-// of an MFMA fragment fetch hit distinct banks. The ring then holds the output tile for the
-// stores (rows of 512 bytes, pieces swizzled by row % 16).
+// operand tiles (256 rows x 64 k of X and of Y, 64 KB a stage) arrive by LDS DMA in two stage
+// buffers, one stage ahead, so a plane's operands are read twice rather than four times.
+// Operand rows are 128 bytes (whole cache lines per DMA piece: with 32-k stages of 64-byte
+// rows the trimul op took 3.5% longer) with their 16-byte pieces XOR-swizzled by (row / 2) % 8,
+// so the sixteen rows of an MFMA fragment fetch hit distinct banks. The two buffers then hold
+// the output tile for the stores (rows of 512 bytes, pieces swizzled by row % 16).
 constexpr int kBT = 256;                    // output tile
-constexpr int kBStages = 4;
-constexpr int kBStage = 2 * kBT * kCK;      // bf16 per stage (X then Y)
+constexpr int kBK = 64;                     // k per stage (128-byte operand rows)
+constexpr int kBStages = 2;
+constexpr int kBStage = 2 * kBT * kBK;      // bf16 per stage (X then Y)
 __global__ __launch_bounds__(512, 2) void trimul_contract256(const bf16* __restrict__ X,
                                                              const bf16* __restrict__ Y,
                                                              bf16* __restrict__ P, int np,
@@ -307,15 +308,17 @@ __global__ __launch_bounds__(512, 2) void trimul_contract256(const bf16* __restr
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63, g = lane >> 5, li = lane & 31;
   const int wm = wave >> 2, wn = wave & 3;  // rows 128 wm .., columns 64 wn ..
-  // this wave's 4 one-KB pieces of stage s (pieces 0-15 of X, 16-31 of Y, 16 rows each)
+  // this wave's 8 one-KB pieces of stage s (pieces 0-31 of X, 32-63 of Y, 8 rows of 128 bytes
+  // each: whole cache lines); the 16-byte slot c of row r sits at slot c ^ ((r >> 1) & 7), so
+  // the 16 rows of an MFMA fragment read hit distinct banks
   auto stage_dma = [&](int s) {
     const uint32_t base = lds_addr(&smem[(s % kBStages) * kBStage]);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int piece = 4 * wave + u, half = piece >> 4;
-      const int row = 16 * (piece & 15) + (lane >> 2);
-      const int c = (lane & 3) ^ ((row >> 2) & 3);
-      const bf16* src = (half ? Yb : Xb) + s * kCK;
+    for (int u = 0; u < 8; ++u) {
+      const int piece = 8 * wave + u, half = piece >> 5;
+      const int row = 8 * (piece & 31) + (lane >> 3);
+      const int c = (lane & 7) ^ ((row >> 1) & 7);
+      const bf16* src = (half ? Yb : Xb) + s * kBK;
       dma16(src, (uint32_t)(row * np * 2 + 16 * c), base + 1024 * piece);
     }
   };
@@ -324,36 +327,30 @@ __global__ __launch_bounds__(512, 2) void trimul_contract256(const bf16* __restr
   for (int a = 0; a < 4; ++a)
 #pragma unroll
     for (int c = 0; c < 2; ++c) acc[a][c] = zero16();
-  // k stages past the batch element's last real key: zero operands, left out
-  const int nk = kstages ? min(np / kCK, kstages[bh / planes_per_batch]) : np / kCK;
+  // 32-key stages past the batch element's last real key: zero operands, left out (a 64-wide
+  // stage may end with one of them)
+  const int nk32 = kstages ? min(np / kCK, kstages[bh / planes_per_batch]) : np / kCK;
+  const int nk = (nk32 + 1) / 2;
   if (nk > 0) stage_dma(0);
-  if (nk > 1) stage_dma(1);
-  if (nk > 2) stage_dma(2);
 #pragma unroll 1
   for (int s = 0; s < nk; ++s) {
-    // this wave's pieces of stage s landed (the later stages' transfers may be in flight)
-    if (s + 2 < nk)
-      wait_vm_lds<8>();
-    else if (s + 1 < nk)
-      wait_vm_lds<4>();
-    else
-      wait_vm_lds<0>();
-    __syncthreads();  // everyone's pieces of stage s; stage s - 1's slot is free
-    if (s + 3 < nk) stage_dma(s + 3);
+    wait_vm_lds<0>();  // this wave's pieces of stage s landed (nothing later is in flight)
+    __syncthreads();   // everyone's pieces of stage s; stage s - 1's slot is free
+    if (s + 1 < nk) stage_dma(s + 1);
     const bf16* xs = &smem[(s % kBStages) * kBStage];
-    const bf16* ys = xs + kBT * kCK;
+    const bf16* ys = xs + kBT * kBK;
 #pragma unroll
-    for (int kk = 0; kk < kCK / 16; ++kk) {
+    for (int kk = 0; kk < kBK / 16; ++kk) {
       bf16x8 av[4], bv[2];
 #pragma unroll
       for (int mi = 0; mi < 4; ++mi) {
         const int r = 128 * wm + 32 * mi + li;
-        av[mi] = ld8(&xs[r * kCK + 8 * ((2 * kk + g) ^ ((r >> 2) & 3))]);
+        av[mi] = ld8(&xs[r * kBK + 8 * ((2 * kk + g) ^ ((r >> 1) & 7))]);
       }
 #pragma unroll
       for (int ni = 0; ni < 2; ++ni) {
         const int r = 64 * wn + 32 * ni + li;
-        bv[ni] = ld8(&ys[r * kCK + 8 * ((2 * kk + g) ^ ((r >> 2) & 3))]);
+        bv[ni] = ld8(&ys[r * kBK + 8 * ((2 * kk + g) ^ ((r >> 1) & 7))]);
       }
       // D[j][i]: lane li is row i, its registers 4 t .. 4 t + 3 columns 8 t + 4 g + 0 .. 3
 #pragma unroll

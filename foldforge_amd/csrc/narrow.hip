@@ -246,19 +246,33 @@ __global__ __launch_bounds__(64 * kTmoWaves) void trimul_out_planes(TrimulPlanes
     }
   };
 
-  // two register buffers used in turn: the next tile's pieces load while the current one is
-  // processed
-  bf16x8 p0[HP], z0[4], p1[HP], z1[4];
-  fetch(t, p0, z0);
-  while (true) {
-    fetch(t + stride, p1, z1);
-    process(t, p0, z0);
-    t += stride;
-    if (t >= tiles) break;
-    fetch(t + stride, p0, z0);
-    process(t, p1, z1);
-    t += stride;
-    if (t >= tiles) break;
+  if constexpr (H >= 128) {
+    // one register buffer (with two, 194 VGPRs left one wave per SIMD and the kernel took 132
+    // instead of 98 µs on the Protenix-1 template shape): the next tile's pieces load after the
+    // current one, other waves cover the wait
+    bf16x8 p0[HP], z0[4];
+    fetch(t, p0, z0);
+    while (true) {
+      process(t, p0, z0);
+      t += stride;
+      if (t >= tiles) break;
+      fetch(t, p0, z0);
+    }
+  } else {
+    // two register buffers used in turn: the next tile's pieces load while the current one is
+    // processed
+    bf16x8 p0[HP], z0[4], p1[HP], z1[4];
+    fetch(t, p0, z0);
+    while (true) {
+      fetch(t + stride, p1, z1);
+      process(t, p0, z0);
+      t += stride;
+      if (t >= tiles) break;
+      fetch(t + stride, p0, z0);
+      process(t, p1, z1);
+      t += stride;
+      if (t >= tiles) break;
+    }
   }
 }
 
@@ -424,10 +438,10 @@ __global__ __launch_bounds__(64 * kTmoWaves) void triattn_out_rows(TriattnRowsAr
     }
   };
 
-  if constexpr (HD >= 256) {
-    // one register buffer (the o rows of 256 gated channels take 64 VGPRs a buffer; with two,
-    // one wave per SIMD fitted and the kernel took 189 instead of 135 µs on RoseTTAFold3's
-    // template shape): the next tile's rows load after the current one, other waves cover the wait
+  if constexpr (HD >= 128) {
+    // one register buffer (the o rows of 128 / 256 gated channels take 32 / 64 VGPRs a buffer;
+    // with two, the kernel took 124 / 189 instead of 85 / 135 µs on the Protenix-1 / RoseTTAFold3
+    // template shapes): the next tile's rows load after the current one, other waves cover the wait
     bf16x8 z0[4], o0[KO];
     fetch(t, z0, o0);
     while (true) {

@@ -153,7 +153,7 @@ template <int EPI>
 __device__ __forceinline__ TileRun tile_run(const RowGemmArgs& a, int64_t m0) {
   TileRun t{};
   t.m0 = m0;
-  const int64_t len = EPI == kEpiTrimul ? (int64_t)a.npm * a.npm : (int64_t)a.np;
+  const int64_t len = EPI == kEpiTrimul ? (int64_t)a.npm * a.npm : EPI == kEpiOpm ? (int64_t)a.sp : (int64_t)a.np;
   t.q = m0 / len;
   t.rem0 = m0 - t.q * len;
   if (EPI == kEpiApb) {
@@ -349,13 +349,36 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
     const float* bias = seg == 0 ? a.bias0 : a.bias1;
     const int hd = a.O / 2;  // channels a side (32; Chai-1's grouped form 64)
     bf16* dst = (seg == 0 ? a.lt : a.rt) + bj * hd * a.sp + s;
+    if (stage) {
+      // the tile's 32 channel rows of this run of 32 MSA rows, transposed through the wave's
+      // LDS tile and written as 16-byte pieces of 64-byte runs (lane L: pieces L and L + 64)
 #pragma unroll
-    for (int v = 0; v < 4; ++v)
+      for (int v = 0; v < 4; ++v)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int c = cbase + 8 * v + 4 * g + e;
-        dst[(int64_t)c * a.sp] = (bf16)((acc[4 * v + e] + (bias ? bias[c] : 0.f)) * keep);
+        for (int e = 0; e < 4; ++e) {
+          const int c = cbase + 8 * v + 4 * g + e;
+          stage[stage_row(8 * v + 4 * g + e) * 32 + (s & 31)] =
+              (bf16)((acc[4 * v + e] + (bias ? bias[c] : 0.f)) * keep);
+        }
+      __builtin_amdgcn_wave_barrier();
+      const int lane = 32 * g + (int)(m - tr->m0);
+      bf16* run = (seg == 0 ? a.lt : a.rt) + tr->q * hd * a.sp + tr->rem0;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int piece = lane + 64 * u, r = piece >> 2, part = piece & 3;
+        *reinterpret_cast<bf16x8*>(run + (int64_t)(cbase + r) * a.sp + 8 * part) =
+            *reinterpret_cast<const bf16x8*>(stage + stage_row(r) * 32 + 8 * part);
       }
+      __builtin_amdgcn_wave_barrier();
+    } else {
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int c = cbase + 8 * v + 4 * g + e;
+          dst[(int64_t)c * a.sp] = (bf16)((acc[4 * v + e] + (bias ? bias[c] : 0.f)) * keep);
+        }
+    }
     if (seg == 0 && cbase == 0 && g == 0) a.mt[bj * a.sp + s] = (bf16)keep;
   } else if (EPI == kEpiTrimul) {
     const int hid = a.O / 4;
@@ -668,7 +691,7 @@ __global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a
   float* lb = lnp + 2 * K;  // per-output biases (row_epilogue)
   // this wave's transpose tile (row_epilogue), for the epilogues that write position runs
   bf16* stage = reinterpret_cast<bf16*>(lb + a.O) + (threadIdx.x >> 6) * 32 * 32;
-  const bool staged = (EPI == kEpiTrimul || (EPI == kEpiApb && a.flash_rows > 0)) && a.M % 32 == 0;
+  const bool staged = (EPI == kEpiTrimul || EPI == kEpiOpm || (EPI == kEpiApb && a.flash_rows > 0)) && a.M % 32 == 0;
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   for (int idx = tid; idx < nt * 32 * (K / 8); idx += 64 * kStreamWaves) {
@@ -707,7 +730,7 @@ __global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a
   // inside the input)
   auto fetch = [&](XT* x, int64_t tile) __attribute__((always_inline)) {
     const int64_t tt = tile < tiles ? tile : tiles - 1;
-    const int64_t row = mapped_row(a, tt * 32 + li);
+    const int64_t row = EPI == kEpiOpm ? opm_msa_row(a, tt * 32 + li) : mapped_row(a, tt * 32 + li);
 #pragma unroll
     for (int i = 0; i < NX; ++i) {
       if (BF)
@@ -1254,6 +1277,7 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
     if (epi == kEpiSwiglu && launch_row_stream<kEpiSwiglu, kXLn>(a, stream)) return;
     if (epi == kEpiResid && a.ln_plain && launch_row_stream<kEpiResid, kXBf16>(a, stream)) return;
     if (epi == kEpiResid && launch_row_stream<kEpiResid, kXLn>(a, stream)) return;
+    if (epi == kEpiOpm && launch_row_stream<kEpiOpm, kXLn>(a, stream)) return;
   } else if (epi == kEpiResid && launch_row_stream<kEpiResid, kXF32>(a, stream)) {
     return;
   }

@@ -153,7 +153,10 @@ template <int EPI>
 __device__ __forceinline__ TileRun tile_run(const RowGemmArgs& a, int64_t m0) {
   TileRun t{};
   t.m0 = m0;
-  const int64_t len = EPI == kEpiTrimul ? (int64_t)a.npm * a.npm : EPI == kEpiOpm ? (int64_t)a.sp : (int64_t)a.np;
+  const int64_t len = EPI == kEpiTrimul ? (int64_t)a.npm * a.npm
+                      : EPI == kEpiOpm   ? (int64_t)a.sp
+                      : EPI == kEpiPwa   ? (int64_t)a.n
+                                         : (int64_t)a.np;
   t.q = m0 / len;
   t.rem0 = m0 - t.q * len;
   if (EPI == kEpiApb) {
@@ -325,6 +328,27 @@ __device__ __forceinline__ void row_epilogue(const RowGemmArgs& a, const f32x16&
     const int64_t bs = m / a.n;  // b S + s
     const int j = (int)(m - bs * a.n);
     const int64_t b = bs / a.depth, srow = bs - b * a.depth;
+    if (seg == 0 && stage) {
+      // v^T: the tile's 32 channel rows of this run of 32 tokens (n % 32 == 0), transposed
+      // through the wave's LDS tile and written as 16-byte pieces of 64-byte runs
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) stage[stage_row(8 * v + 4 * g + e) * 32 + (j & 31)] = (bf16)acc[4 * v + e];
+      __builtin_amdgcn_wave_barrier();
+      const int lane = 32 * g + (int)(m - tr->m0);
+      const int64_t bt = tr->q / a.depth, st = tr->q - bt * a.depth;
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int piece = lane + 64 * u, r = piece >> 2, part = piece & 3;
+        const int c = cbase + r, hh = c / a.dh, d = c - hh * a.dh;
+        *reinterpret_cast<bf16x8*>(a.vt + (((bt * a.heads + hh) * a.depth + st) * a.dh + d) * a.np +
+                                   tr->rem0 + 8 * part) =
+            *reinterpret_cast<const bf16x8*>(stage + stage_row(r) * 32 + 8 * part);
+      }
+      __builtin_amdgcn_wave_barrier();
+      return;
+    }
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
       const int c = cbase + 8 * v + 4 * g;  // 4 channels of one head (dh % 4 == 0)
@@ -691,7 +715,9 @@ __global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a
   float* lb = lnp + 2 * K;  // per-output biases (row_epilogue)
   // this wave's transpose tile (row_epilogue), for the epilogues that write position runs
   bf16* stage = reinterpret_cast<bf16*>(lb + a.O) + (threadIdx.x >> 6) * 32 * 32;
-  const bool staged = (EPI == kEpiTrimul || EPI == kEpiOpm || (EPI == kEpiApb && a.flash_rows > 0)) && a.M % 32 == 0;
+  const bool staged = (EPI == kEpiTrimul || EPI == kEpiOpm || (EPI == kEpiApb && a.flash_rows > 0) ||
+                       (EPI == kEpiPwa && a.n % 32 == 0)) &&
+                      a.M % 32 == 0;
   const int tid = threadIdx.x, lane = tid & 63, li = lane & 31, g = lane >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   for (int idx = tid; idx < nt * 32 * (K / 8); idx += 64 * kStreamWaves) {
@@ -1278,6 +1304,7 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
     if (epi == kEpiResid && a.ln_plain && launch_row_stream<kEpiResid, kXBf16>(a, stream)) return;
     if (epi == kEpiResid && launch_row_stream<kEpiResid, kXLn>(a, stream)) return;
     if (epi == kEpiOpm && launch_row_stream<kEpiOpm, kXLn>(a, stream)) return;
+    if (epi == kEpiPwa && launch_row_stream<kEpiPwa, kXLn>(a, stream)) return;
   } else if (epi == kEpiResid && launch_row_stream<kEpiResid, kXF32>(a, stream)) {
     return;
   }

@@ -295,8 +295,8 @@ int64_t pad32(int64_t n) { return (n + 31) / 32 * 32; }
 int64_t pad64(int64_t n) { return (n + 63) / 64 * 64; }
 
 struct PwaWs {
-  bf16 *vt, *gate, *w;
-  float *logits, *og;
+  bf16 *vt, *gate, *w, *og;
+  float* logits;
   size_t bytes;
 };
 PwaWs pwa_ws(void* ws, int64_t batch, int64_t depth, int64_t n, int heads, int dh) {
@@ -308,7 +308,7 @@ PwaWs pwa_ws(void* ws, int64_t batch, int64_t depth, int64_t n, int heads, int d
   w.gate = cv.take<bf16>(tok);
   w.logits = cv.take<float>((size_t)batch * heads * n * np);
   w.w = cv.take<bf16>((size_t)batch * heads * n * np);
-  w.og = cv.take<float>(tok);
+  w.og = cv.take<bf16>(tok);
   w.bytes = cv.used;
   return w;
 }
@@ -1169,8 +1169,8 @@ int32_t ffk_msa_pair_weighted_averaging(
   if (d_pair != 128)
     return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: d_pair=%d (kernels take 128)", d_pair);
   if (d_msa <= 0 || d_msa % 64 != 0 || d_msa > kLnGemmMaxK || n_head <= 0 || n_head > 32 ||
-      d_head <= 0 || d_head % 4 != 0 || hd % 64 != 0)
-    return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: d_msa=%d heads=%d x %d (kernels take d_msa a multiple of 64 up to %d, at most 32 heads, d_head a multiple of 4, heads * d_head a multiple of 64)", d_msa, n_head, d_head, kLnGemmMaxK);
+      d_head <= 0 || d_head % 4 != 0 || hd % 64 != 0 || hd > kLnGemmMaxK)
+    return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: d_msa=%d heads=%d x %d (kernels take d_msa a multiple of 64 up to %d, at most 32 heads, d_head a multiple of 4, heads * d_head a multiple of 64 up to %d)", d_msa, n_head, d_head, kLnGemmMaxK, kLnGemmMaxK);
   if (batch <= 0 || depth <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "msa_pair_weighted_averaging: empty shape");
   if ((depth * d_head + 127) / 128 * ((n + 127) / 128) * batch * n_head > 0x7fffffffLL ||
       batch * n_head * n > 0x7fffffffLL * 4)
@@ -1244,7 +1244,8 @@ int32_t ffk_msa_pair_weighted_averaging(
   launch_pwa_average(av, st);
 
   RowGemmArgs o{};
-  o.x32 = w.og;
+  o.ln_x = w.og;
+  o.ln_plain = 1;
   o.w0 = w_out;
   o.M = rows;
   o.K = (int)hd;
@@ -1252,7 +1253,7 @@ int32_t ffk_msa_pair_weighted_averaging(
   o.res = static_cast<const bf16*>(m);
   o.out = static_cast<bf16*>(out);
   o.residual = residual ? 1 : 0;
-  launch_row_gemm(o, kEpiResid, kXF32, st);
+  launch_row_gemm(o, kEpiResid, kXLn, st);
   return check_launch("msa_pair_weighted_averaging");
 }
 

@@ -270,7 +270,7 @@ struct PwaAverageArgs {
   const bf16* vt;    // [batch][heads][S][dh][np]
   const bf16* w;     // [batch][heads][n][np]
   const bf16* gate;  // [batch][S][n][heads dh]
-  float* og;         // [batch][S][n][heads dh] = gate * sum_j w[h][i][j] v[s][j][h]
+  bf16* og;          // [batch][S][n][heads dh] = gate * sum_j w[h][i][j] v[s][j][h], bf16
   int batch, heads, depth, n, np, dh;
 };
 void launch_pwa_average(const PwaAverageArgs& a, hipStream_t stream);

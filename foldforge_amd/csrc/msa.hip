@@ -158,10 +158,8 @@ __global__ __launch_bounds__(256) void pwa_average(PwaAverageArgs a) {
         const int s = r / a.dh, c = r - s * a.dh;
         const int64_t off = ((b * a.depth + s) * n + q) * hd + h * a.dh + c;
         const bf16x4 gv = *reinterpret_cast<const bf16x4*>(a.gate + off);
-        f32x4 y;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = acc[mi][ni][4 * v + e] * (float)gv[e];
-        *reinterpret_cast<f32x4*>(a.og + off) = y;
+        store4(a.og + off, acc[mi][ni][4 * v] * (float)gv[0], acc[mi][ni][4 * v + 1] * (float)gv[1],
+               acc[mi][ni][4 * v + 2] * (float)gv[2], acc[mi][ni][4 * v + 3] * (float)gv[3]);
       }
   }
 }

@@ -426,7 +426,7 @@ def attention_pair_bias(
 def msa_pair_weighted_averaging_supported(d_msa: int, n_head: int, d_head: int) -> bool:
     """MSA widths and head splits the pair-weighted averaging kernels take."""
     return (0 < d_msa <= 768 and d_msa % 64 == 0 and 0 < n_head <= 32 and d_head > 0
-            and d_head % 4 == 0 and (n_head * d_head) % 64 == 0)
+            and d_head % 4 == 0 and (n_head * d_head) % 64 == 0 and n_head * d_head <= 768)
 
 
 def msa_pair_weighted_averaging(

@@ -554,7 +554,7 @@ class MSAPairWeightedAveraging(EngineOp, MasterWeights, nn.Module):
         if not msa_pair_weighted_averaging_supported(self.d_msa, self.n_head, self.d_hidden):
             return (f"d_msa={self.d_msa} heads={self.n_head} x {self.d_hidden} (the kernels take "
                     "d_msa a multiple of 64 up to 768, at most 32 heads of a multiple of 4, "
-                    "heads x d_head a multiple of 64)")
+                    "heads x d_head a multiple of 64 up to 768)")
         return None
 
     def _forward_pytorch(self, m: Tensor, z: Tensor, mask: Tensor, *, residual: bool = True) -> Tensor:

@@ -242,8 +242,8 @@ int32_t ffk_attention_pair_bias(
  * m, out [batch, depth, n, d_msa] bf16 (depth = MSA rows); z [batch, n, n, d_pair] bf16;
  * key_mask [batch, n] (a column is a key when any MSA row has it); a batch element without a
  * valid key gets a zero update. d_pair = 128; d_msa a multiple of 64 up to 768; at most 32
- * heads of d_head (a multiple of 4), n_head * d_head a multiple of 64 (AF3: 8 x 8). `out`
- * may alias `m`.
+ * heads of d_head (a multiple of 4), n_head * d_head a multiple of 64 up to 768 (AF3: 8 x 8).
+ * `out` may alias `m`.
  * Replaces: engine MSAPairWeightedAveraging.forward, op name "msa_pwa"
  * (src/foldforge/modules/engine/backends.py:49; equations
  * src/foldforge/models/checkpoints/legacy/attention.py:174-229; engine parameters

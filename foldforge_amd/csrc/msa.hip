@@ -55,6 +55,8 @@ __global__ __launch_bounds__(256) void pwa_softmax(PwaSoftmaxArgs a) {
 constexpr int kPT = 128;         // output tile: 128 (s, c) rows x 128 queries
 constexpr int kPK = 32;          // keys per LDS stage
 constexpr int kPKP = kPK + 8;    // LDS row stride (80 B: conflict-free 16-byte reads)
+constexpr int kPOS = kPT + 4;    // epilogue fp32 row stride: 64 x kPOS floats fit in the operand stages
+static_assert(64 * kPOS * 4 <= 4 * kPT * kPKP * 2, "epilogue staging exceeds the operand LDS");
 
 // Per (batch, head): O[(s, c)][i] = sum_j v^T[(s, c)][j] w[i][j], an NT GEMM with both operands
 // key-contiguous. grid: ceil(S dh / 128) * ceil(n / 128) * batch * heads workgroups (renumbered
@@ -64,8 +66,10 @@ constexpr int kPKP = kPK + 8;    // LDS row stride (80 B: conflict-free 16-byte 
 // Epilogue: lane (li, g) holds query q0' + li and rows r = r0' + 8 v + 4 g + e, i.e.
 // (s, c) = (r / dh, r % dh): four consecutive channels of one MSA row (dh % 4 == 0).
 __global__ __launch_bounds__(256) void pwa_average(PwaAverageArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16 xs[2][kPT * kPKP];
-  __shared__ __attribute__((aligned(16))) bf16 ys[2][kPT * kPKP];
+  // operand stages xs[2] then ys[2]; after the key loop the epilogue reuses it as fp32 [64][kPOS]
+  __shared__ __attribute__((aligned(16))) bf16 lds[4 * kPT * kPKP];
+  bf16 (*xs)[kPT * kPKP] = reinterpret_cast<bf16 (*)[kPT * kPKP]>(lds);
+  bf16 (*ys)[kPT * kPKP] = reinterpret_cast<bf16 (*)[kPT * kPKP]>(lds + 2 * kPT * kPKP);
   const int rows = a.depth * a.dh, n = a.n, np = a.np;
   const int rt = (rows + kPT - 1) / kPT, qt = (n + kPT - 1) / kPT;
   const uint32_t wg = xcd_remap(blockIdx.x, gridDim.x);
@@ -145,6 +149,45 @@ __global__ __launch_bounds__(256) void pwa_average(PwaAverageArgs a) {
   }
 
   const int hd = a.heads * a.dh;
+  if (a.dh % 8 == 0) {
+    // Staged: one half of the queries (ni) at a time goes through LDS as fp32 [query][row]; each
+    // lane then gates and stores 8 consecutive rows of one query, i.e. 16 bytes of one MSA
+    // row's head channels (dh % 8 == 0 keeps such a piece inside one MSA row).
+    float* T = reinterpret_cast<float*>(lds);
+#pragma unroll
+    for (int ni = 0; ni < 2; ++ni) {
+      if (ni) __syncthreads();
+#pragma unroll
+      for (int mi = 0; mi < 2; ++mi)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          f32x4 y;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = acc[mi][ni][4 * v + e];
+          *reinterpret_cast<f32x4*>(&T[(wn * 32 + li) * kPOS + wm * 64 + mi * 32 + 8 * v + 4 * g]) = y;
+        }
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int id = tid + 256 * u, ql = id >> 4, rl = (id & 15) * 8;
+        const int q = q0 + (ql >> 5) * 64 + ni * 32 + (ql & 31), r = r0 + rl;
+        if (q >= n || r >= rows) continue;
+        const int s = r / a.dh, c = r - s * a.dh;
+        const int64_t off = ((b * a.depth + s) * n + q) * hd + h * a.dh + c;
+        const bf16x8 gv = ld8(a.gate + off);
+        const f32x4 y0 = *reinterpret_cast<const f32x4*>(&T[ql * kPOS + rl]);
+        const f32x4 y1 = *reinterpret_cast<const f32x4*>(&T[ql * kPOS + rl + 4]);
+        bf16x8 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] = (bf16)(y0[e] * (float)gv[e]);
+          o[4 + e] = (bf16)(y1[e] * (float)gv[4 + e]);
+        }
+        *reinterpret_cast<bf16x8*>(a.og + off) = o;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int ni = 0; ni < 2; ++ni) {
     const int q = q0 + wn * 64 + ni * 32 + li;

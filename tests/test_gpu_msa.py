@@ -57,7 +57,10 @@ def _pwa(cm: int, heads: int, dh: int | None, seed: int):
     return m
 
 
-@pytest.mark.parametrize("cm,heads,dh", [(64, 8, None), (64, 4, 16), (128, 8, 8)])
+# d_head 32 is the released models' width; 24 ends MSA rows inside a 128-row output tile; 12 (not a
+# multiple of 8) takes the unstaged 8-byte epilogue
+@pytest.mark.parametrize("cm,heads,dh", [(64, 8, None), (64, 4, 16), (128, 8, 8), (64, 8, 32), (64, 8, 24),
+                                        (64, 16, 12)])
 @pytest.mark.parametrize("depth,n,lengths", [(5, 64, [64]), (7, 100, [77]), (3, 130, [130, 41])])
 def test_msa_pair_weighted_averaging_matches_oracle(cm, heads, dh, depth, n, lengths):
     msa, z, mask = _inputs(depth, n, cm, lengths, seed=n + cm + heads)

@@ -964,9 +964,10 @@ __global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a
 // hi + lo (two MFMA passes), so the bias keeps fp32 accuracy: its error does not grow with
 // the logit size (large pair logits would otherwise shift the softmax weights).
 // One wave handles a tile of 32 consecutive keys j of one (b, i): lane (li, g) loads its
-// row's channels 64 g .. 64 g + 63 (128 contiguous bytes), the statistics come from those
+// row's channels 16 t + 8 g .. 16 t + 8 g + 7 for t < C / 16, so each load instruction reads
+// 32 contiguous bytes per row (lanes l and l ^ 32 together), the statistics come from those
 // registers (two passes, halves joined across lane l ^ 32), and the heads x keys block is
-// one 32 x 32 MFMA tile (A = W' rows, B = the z rows; channel 64 g + 8 t + e feeds step t).
+// one 32 x 32 MFMA tile (A = W' rows, B = the z rows; channels 16 t .. 16 t + 15 feed step t).
 template <int C>
 __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
   constexpr int kU = C / 16;  // 8-channel chunks per lane (each lane half holds C / 2)
@@ -988,9 +989,9 @@ __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
       const int64_t b = bi / n;
       row = (b * n + key) * n + (bi - b * n);
     }
-    const bf16* zr = a.z + row * C + (C / 2) * g;
+    const bf16* zr = a.z + row * C + 8 * g;
 #pragma unroll
-    for (int u = 0; u < kU; ++u) zf[u] = ld8(zr + 8 * u);
+    for (int u = 0; u < kU; ++u) zf[u] = ld8(zr + 16 * u);
   };
   int64_t t = (int64_t)blockIdx.x * 4 + wave;
   bf16x8 z0[kU], z1[kU];
@@ -998,15 +999,15 @@ __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
 
   bf16x8 wf[kU], wl[kU];
   float rs = 0.f;
-  const float* wrow = a.w_bias + min(li, a.heads - 1) * C + (C / 2) * g;
-  const float* lrow = a.ln_w + (C / 2) * g;
+  const float* wrow = a.w_bias + min(li, a.heads - 1) * C + 8 * g;
+  const float* lrow = a.ln_w + 8 * g;
   const float keep = li < a.heads ? kLog2e : 0.f;
 #pragma unroll
   for (int u = 0; u < kU; ++u) {
-    const f32x4 w0 = *reinterpret_cast<const f32x4*>(wrow + 8 * u);
-    const f32x4 w1 = *reinterpret_cast<const f32x4*>(wrow + 8 * u + 4);
-    const f32x4 l0 = *reinterpret_cast<const f32x4*>(lrow + 8 * u);
-    const f32x4 l1 = *reinterpret_cast<const f32x4*>(lrow + 8 * u + 4);
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(wrow + 16 * u);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(wrow + 16 * u + 4);
+    const f32x4 l0 = *reinterpret_cast<const f32x4*>(lrow + 16 * u);
+    const f32x4 l1 = *reinterpret_cast<const f32x4*>(lrow + 16 * u + 4);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const float v = keep * (e < 4 ? l0[e] * w0[e] : l1[e - 4] * w1[e - 4]);
@@ -1363,7 +1364,7 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
 }
 
 void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream) {
-  int64_t blocks = (a.tiles + 15) / 16;  // about four tiles per wave
+  int64_t blocks = (a.tiles + 7) / 8;  // about two tiles per wave
   const int64_t cap = (int64_t)cu_count() * 8;
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;

@@ -215,11 +215,13 @@ __global__ __launch_bounds__(512) void opm_contract(OpmContractArgs a) {
 //   p[i, j, (g, k, l)] = sum_s l[s, i, 8 g + k] r[s, j, 8 g + l]            (512 per pair)
 //   out[i, j] = LN_0.1(p[i, j]) W_out^T + b_out                 (product norm over the 512)
 // grid: ceil(n / 4) * ceil(n / 8) * batch workgroups of 512 threads, one tile of 4 x 8 tokens.
-// Phase 1: wave w takes token i0 + w / 2 against tokens j0 + 4 (w % 2) .. + 3; a pair's groups
-// sit on the diagonal of the two 32 x 32 MFMA tiles of channel block t (channels 32 t ..
-// 32 t + 31 of both sides), where lane (li, g) holds o[c = 32 t + acc_row(r, g)][e = 32 t + li]
-// in acc[r]: its in-group products are r = 4 (li / 8) + q, q = 0..3 (group 4 t + li / 8,
-// k = 4 g + q, l = li % 8). They go to LDS in fp32 in the (g, k, l) order.
+// Phase 1: per group the products are one dense product, rows (token i, k) x columns (token j,
+// l) over the MSA rows, so wave w takes group w: two 32 x 32 MFMA tiles, rows (i = row / 8,
+// k = row % 8) for the tile's 4 tokens i, columns (j = 4 h + li / 8, l = li % 8) for h = 0, 1.
+// Lane (li, g) holds row acc_row(r, g) of column li in acc[h][r]; the products go to LDS in
+// fp32 in the (g, k, l) order. In the operand stages token t's 64 rows (8 groups x 8) start
+// 128 t bytes later than unpadded, so the 16 lanes of a read (two neighbouring tokens' 8 rows of
+// one group, 80-byte rows) cover all 64 banks.
 // Phase 2: one wave per pair normalises the 512 products (two passes over 8 per lane), rounds
 // them to bf16 rows; phase 3: the c_z / 32 output tiles (each over 32 pairs, k = 512; at c_z
 // 128 the k range is split over two waves and summed through LDS), bias and residual added.
@@ -230,7 +232,10 @@ constexpr int kOgN = 512;                     // products per pair
 constexpr int kOgNS = kOgN + 8;               // LDS row stride of a normalised pair (bf16)
 constexpr int kOgXRows = kOgTI * kOgC, kOgYRows = kOgTJ * kOgC;
 constexpr int kOgXPT = kOgXRows * kOpmCPR / 512, kOgYPT = kOgYRows * kOpmCPR / 512;
-constexpr size_t kOgStageBytes = (size_t)2 * (kOgXRows + kOgYRows) * kOpmKS * sizeof(bf16);
+constexpr int kOgTokPad = 64;                 // stage rows of token t shifted by t x 128 bytes (bf16 units)
+constexpr int kOgXB = kOgXRows * kOpmKS + kOgTI * kOgTokPad;  // one stage of each operand
+constexpr int kOgYB = kOgYRows * kOpmKS + kOgTJ * kOgTokPad;
+constexpr size_t kOgStageBytes = (size_t)2 * (kOgXB + kOgYB) * sizeof(bf16);
 constexpr size_t kOgProdBytes = (size_t)kOgPairs * kOgN * sizeof(float);
 constexpr size_t kOgNormBytes = (size_t)kOgPairs * kOgNS * sizeof(bf16);
 constexpr size_t kOgLds = kOgStageBytes > kOgProdBytes + kOgNormBytes ? kOgStageBytes : kOgProdBytes + kOgNormBytes;
@@ -238,8 +243,8 @@ constexpr size_t kOgLds = kOgStageBytes > kOgProdBytes + kOgNormBytes ? kOgStage
 template <int CZ>
 __global__ __launch_bounds__(512) void opm_contract_grouped(OpmGroupedArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  bf16* xs = reinterpret_cast<bf16*>(smem);  // [2][kOgXRows][kOpmKS]
-  bf16* ys = xs + 2 * kOgXRows * kOpmKS;     // [2][kOgYRows][kOpmKS]
+  bf16* xs = reinterpret_cast<bf16*>(smem);  // [2][kOgXB]: rows (token, channel) x kOpmKS
+  bf16* ys = xs + 2 * kOgXB;                 // [2][kOgYB]
   float* prod = reinterpret_cast<float*>(smem);                     // [32][512], after phase 1
   bf16* nrm = reinterpret_cast<bf16*>(smem + kOgProdBytes);         // [32][kOgNS]
   float* red = reinterpret_cast<float*>(smem);                      // phase 3 (c_z 128) partials
@@ -260,14 +265,14 @@ __global__ __launch_bounds__(512) void opm_contract_grouped(OpmGroupedArgs a) {
     const int c = tid + 512 * u, row = c / kOpmCPR, kc = (c % kOpmCPR) * 8;
     const int tok = min(i0 + row / kOgC, n - 1);
     xsrc[u] = a.lt + ((b * n + tok) * kOgC + row % kOgC) * sp + kc;
-    xoff[u] = row * kOpmKS + kc;
+    xoff[u] = row * kOpmKS + kc + (row / kOgC) * kOgTokPad;
   }
 #pragma unroll
   for (int u = 0; u < kOgYPT; ++u) {
     const int c = tid + 512 * u, row = c / kOpmCPR, kc = (c % kOpmCPR) * 8;
     const int tok = min(j0 + row / kOgC, n - 1);
     ysrc[u] = a.rt + ((b * n + tok) * kOgC + row % kOgC) * sp + kc;
-    yoff[u] = row * kOpmKS + kc;
+    yoff[u] = row * kOpmKS + kc + (row / kOgC) * kOgTokPad;
   }
   bf16x8 rx[kOgXPT], ry[kOgYPT];
   auto gload = [&](int k0) {
@@ -279,18 +284,21 @@ __global__ __launch_bounds__(512) void opm_contract_grouped(OpmGroupedArgs a) {
   auto sstore = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < kOgXPT; ++u)
-      *reinterpret_cast<bf16x8*>(xs + buf * kOgXRows * kOpmKS + xoff[u]) = rx[u];
+      *reinterpret_cast<bf16x8*>(xs + buf * kOgXB + xoff[u]) = rx[u];
 #pragma unroll
     for (int u = 0; u < kOgYPT; ++u)
-      *reinterpret_cast<bf16x8*>(ys + buf * kOgYRows * kOpmKS + yoff[u]) = ry[u];
+      *reinterpret_cast<bf16x8*>(ys + buf * kOgYB + yoff[u]) = ry[u];
   };
 
-  const int wi = wave >> 1, wj = 4 * (wave & 1);
-  f32x16 acc[4][2];
+  // this lane's operand rows: token li / 8 (i; j within each half), channel 8 w + li % 8
+  const int ti8 = li >> 3, ch = 8 * wave + (li & 7);
+  const int arow = (ti8 * kOgC + ch) * kOpmKS + ti8 * kOgTokPad + 8 * g;
+  int brow[2];
 #pragma unroll
-  for (int nj = 0; nj < 4; ++nj)
+  for (int h = 0; h < 2; ++h) brow[h] = ((4 * h + ti8) * kOgC + ch) * kOpmKS + (4 * h + ti8) * kOgTokPad + 8 * g;
+  f32x16 acc[2];
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) acc[nj][tb] = zero16();
+  for (int h = 0; h < 2; ++h) acc[h] = zero16();
 
   gload(0);
   sstore(0);
@@ -300,39 +308,27 @@ __global__ __launch_bounds__(512) void opm_contract_grouped(OpmGroupedArgs a) {
   for (int k0 = 0; k0 < sp; k0 += kOpmKC) {
     const bool more = k0 + kOpmKC < sp;
     if (more) gload(k0 + kOpmKC);
-    const bf16* xb = xs + buf * kOgXRows * kOpmKS;
-    const bf16* yb = ys + buf * kOgYRows * kOpmKS;
+    const bf16* xb = xs + buf * kOgXB;
+    const bf16* yb = ys + buf * kOgYB;
 #pragma unroll
     for (int kk = 0; kk < kOpmKC; kk += 16) {
-      bf16x8 av[2];
+      const bf16x8 av = ld8(xb + arow + kk);
 #pragma unroll
-      for (int tb = 0; tb < 2; ++tb) av[tb] = ld8(xb + (wi * kOgC + 32 * tb + li) * kOpmKS + kk + 8 * g);
-#pragma unroll
-      for (int nj = 0; nj < 4; ++nj)
-#pragma unroll
-        for (int tb = 0; tb < 2; ++tb)
-          acc[nj][tb] = mfma32(av[tb], ld8(yb + ((wj + nj) * kOgC + 32 * tb + li) * kOpmKS + kk + 8 * g),
-                               acc[nj][tb]);
+      for (int h = 0; h < 2; ++h) acc[h] = mfma32(av, ld8(yb + brow[h] + kk), acc[h]);
     }
     if (more) sstore(buf ^ 1);
     __syncthreads();  // also ends every read of the stages before the products land
     buf ^= 1;
   }
 
-  // the in-group products, fp32, at p (g, k, l) order
-  const int sel = li >> 3;
+  // the in-group products, fp32, at p (g, k, l) order: acc[h][r] is row acc_row(r, g) =
+  // (i = r / 4, k = 4 g + r % 4) of column li = (j = 4 h + li / 8, l = li % 8), group w
 #pragma unroll
-  for (int nj = 0; nj < 4; ++nj)
+  for (int h = 0; h < 2; ++h)
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-      const int pair = wi * kOgTJ + wj + nj;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const f32x16& A = acc[nj][tb];
-        const float v = sel == 0 ? A[q] : sel == 1 ? A[4 + q] : sel == 2 ? A[8 + q] : A[12 + q];
-        const int idx = (4 * tb + sel) * 64 + (4 * g + q) * 8 + (li & 7);
-        prod[pair * kOgN + idx] = v;
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int pair = (r >> 2) * kOgTJ + 4 * h + ti8;
+      prod[pair * kOgN + wave * 64 + (4 * g + (r & 3)) * 8 + (li & 7)] = acc[h][r];
     }
   __syncthreads();
 

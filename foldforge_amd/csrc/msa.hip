@@ -61,7 +61,7 @@ static_assert(64 * kPOS * 4 <= 4 * kPT * kPKP * 2, "epilogue staging exceeds the
 // Per (batch, head): O[(s, c)][i] = sum_j v^T[(s, c)][j] w[i][j], an NT GEMM with both operands
 // key-contiguous. grid: ceil(S dh / 128) * ceil(n / 128) * batch * heads workgroups (renumbered
 // so that neighbours share an XCD's L2), block 256 = 2 x 2 waves of 64 x 64; operands staged
-// through LDS 32 keys at a time (register prefetch, double buffer, one barrier per stage).
+// through LDS 32 keys at a time (register prefetch two stages ahead, double buffer, one barrier per stage).
 // v^T is not written at keys >= n: those operand entries are zeroed as they are staged.
 // Epilogue: lane (li, g) holds query q0' + li and rows r = r0' + 8 v + 4 g + e, i.e.
 // (s, c) = (r / dh, r % dh): four consecutive channels of one MSA row (dh % 4 == 0).
@@ -94,13 +94,17 @@ __global__ __launch_bounds__(256) void pwa_average(PwaAverageArgs a) {
     soff[u] = row * kPKP + kc;
     kcol[u] = kc;
   }
-  bf16x8 rx[2], ry[2];
-  auto gload = [&](int k0) {
+  // Two register sets carry the next two stages (stage s + 1 lands in LDS while stage s + 3 is
+  // fetched), so a stage's global loads have two stages of MFMAs to land behind.
+  bf16x8 rx0[2], ry0[2], rx1[2], ry1[2];
+  auto gload = [&](bf16x8 (&rx)[2], bf16x8 (&ry)[2], int k0) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       rx[u] = ld8(xsrc[u] + k0);
       ry[u] = ld8(ysrc[u] + k0);
     }
+  };
+  auto sstore = [&](bf16x8 (&rx)[2], const bf16x8 (&ry)[2], int k0, int buf) {
     if (k0 + kPK > n) {
 #pragma unroll
       for (int u = 0; u < 2; ++u)
@@ -108,8 +112,6 @@ __global__ __launch_bounds__(256) void pwa_average(PwaAverageArgs a) {
         for (int e = 0; e < 8; ++e)
           if (k0 + kcol[u] + e >= n) rx[u][e] = (bf16)0.f;
     }
-  };
-  auto sstore = [&](int buf) {
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       *reinterpret_cast<bf16x8*>(&xs[buf][soff[u]]) = rx[u];
@@ -122,15 +124,7 @@ __global__ __launch_bounds__(256) void pwa_average(PwaAverageArgs a) {
   for (int mi = 0; mi < 2; ++mi)
 #pragma unroll
     for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = zero16();
-
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  int buf = 0;
-#pragma unroll 1
-  for (int k0 = 0; k0 < np; k0 += kPK) {
-    const bool more = k0 + kPK < np;
-    if (more) gload(k0 + kPK);
+  auto compute = [&](int buf) {
 #pragma unroll
     for (int kk = 0; kk < kPK; kk += 16) {
       bf16x8 av[2], bv[2];
@@ -143,9 +137,27 @@ __global__ __launch_bounds__(256) void pwa_average(PwaAverageArgs a) {
 #pragma unroll
         for (int ni = 0; ni < 2; ++ni) acc[mi][ni] = mfma32(av[mi], bv[ni], acc[mi][ni]);
     }
-    if (more) sstore(buf ^ 1);
+  };
+
+  // np is a multiple of 64: an even number (>= 2) of stages, taken two per iteration (buffers 0, 1)
+  const int ns = np / kPK;
+  gload(rx0, ry0, 0);
+  sstore(rx0, ry0, 0, 0);
+  gload(rx1, ry1, kPK);
+  if (ns > 2) gload(rx0, ry0, 2 * kPK);
+  __syncthreads();
+#pragma unroll 1
+  for (int st = 0; st < ns; st += 2) {
+    compute(0);                   // stage st; rx1 holds stage st + 1, rx0 stage st + 2 (if any)
+    sstore(rx1, ry1, (st + 1) * kPK, 1);
+    if (st + 3 < ns) gload(rx1, ry1, (st + 3) * kPK);
     __syncthreads();
-    buf ^= 1;
+    compute(1);                   // stage st + 1
+    if (st + 2 < ns) {
+      sstore(rx0, ry0, (st + 2) * kPK, 0);
+      if (st + 4 < ns) gload(rx0, ry0, (st + 4) * kPK);
+    }
+    __syncthreads();
   }
 
   const int hd = a.heads * a.dh;

@@ -139,3 +139,11 @@ def test_flash_core_rejects_an_output_too_small():
     with pytest.raises(ValueError, match="valid extents"):
         kernels.flash_attention_bias(q, q, vt, blk, torch.zeros(1, 4, 128, 128, dtype=torch.bfloat16),
                                      rows_valid=5, n_valid=128)
+
+
+def test_pair_weighted_averaging_head_split_bounds():
+    # the gated average feeds the output projection as bf16 rows of heads x d_head <= 768 channels
+    assert kernels.msa_pair_weighted_averaging_supported(64, 8, 32)
+    assert kernels.msa_pair_weighted_averaging_supported(64, 24, 32)
+    assert not kernels.msa_pair_weighted_averaging_supported(64, 32, 32)
+    assert not kernels.msa_pair_weighted_averaging_supported(64, 8, 6)

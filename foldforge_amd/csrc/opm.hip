@@ -33,6 +33,18 @@ constexpr int kOpmPT = kOpmRows * kOpmCPR / 512;  // chunks per thread and opera
 constexpr int kOpmPairs = kOpmT * kOpmT;    // pairs per tile
 constexpr int kOpmK2 = kOpmC * kOpmC;       // 1024: the projection's k
 constexpr int kOpmOS = kOpmK2 + 8;          // LDS row stride of a pair's outer product
+
+// Tile order within a batch element: runs of 8 tile rows, walked column by column, so the 32
+// neighbouring workgroups an XCD holds at once (consecutive ids after xcd_remap) cover 8 tile
+// rows x 4 tile columns and share each operand block through that XCD's L2 (a row-major order
+// gives them one tile row and 32 distinct column operands). A bijection of [0, nti * ntj).
+__device__ __forceinline__ void grouped_tile(int t, int nti, int ntj, int& ti, int& tj) {
+  constexpr int kRows = 8;
+  const int per = kRows * ntj, first = (t / per) * kRows;
+  const int rows = min(nti - first, kRows), u = t - (t / per) * per;
+  ti = first + u % rows;
+  tj = u / rows;
+}
 constexpr size_t kOpmStageBytes = (size_t)2 * 2 * kOpmRows * kOpmKS * sizeof(bf16);
 constexpr size_t kOpmOBytes = (size_t)kOpmPairs * kOpmOS * sizeof(bf16);
 constexpr size_t kOpmLds = kOpmStageBytes > kOpmOBytes ? kOpmStageBytes : kOpmOBytes;
@@ -84,7 +96,8 @@ __global__ __launch_bounds__(512) void opm_contract(OpmContractArgs a) {
   const int nt = (n + kOpmT - 1) / kOpmT;
   const uint32_t t = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t b = t / ((uint32_t)nt * nt);
-  const int ti = (int)((t / nt) % nt), tj = (int)(t % nt);
+  int ti, tj;
+  grouped_tile((int)(t - b * nt * nt), nt, nt, ti, tj);
   const int i0 = ti * kOpmT, j0 = tj * kOpmT;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, g = lane >> 5;
 
@@ -252,7 +265,8 @@ __global__ __launch_bounds__(512) void opm_contract_grouped(OpmGroupedArgs a) {
   const int nti = (n + kOgTI - 1) / kOgTI, ntj = (n + kOgTJ - 1) / kOgTJ;
   const uint32_t t = xcd_remap(blockIdx.x, gridDim.x);
   const int64_t b = t / ((uint32_t)nti * ntj);
-  const int ti = (int)((t / ntj) % nti), tj = (int)(t % ntj);
+  int ti, tj;
+  grouped_tile((int)(t - b * nti * ntj), nti, ntj, ti, tj);
   const int i0 = ti * kOgTI, j0 = tj * kOgTJ;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, li = lane & 31, g = lane >> 5;
 

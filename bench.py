@@ -28,7 +28,10 @@ Reported beside it, in the same JSON line:
 * ``trunk``: the 48-block trunk with its single track (c_s 384, 16 x 24 attention with
   pair bias) at N = 512, all-ones mask, z and s ~N(0,1), 3 passes (144 block evaluations),
   every op on ``hip``: ms per trunk run, ms per block, the single track's share, and the
-  residual-stream RMS after the last block.
+  residual-stream RMS after the last block. ``trunk.parity`` (with the CPU baseline): block
+  evaluations 1, 72 and 144 of the hip trunk re-run on the fp32 CPU oracle from the same
+  input (update rel-RMS), and the final state against the fp32 reference trunk.
+* ``ladder``: the same trunk at N = 768, 1024, 1536 and 2048 (ms per trunk run).
 
 ``python bench.py [--steps K] [--warmup W] [--n 512] [--no-cpu-baseline] [--no-trunk]``;
 one GPU only. ``--ladder`` instead prints one JSON line per length of the trunk's length
@@ -357,6 +360,74 @@ def trunk_measure(n: int, runs: int, *, pytorch_too: bool = False, cpu_too: bool
     return out
 
 
+def cpu_baseline_trunk_parity(n: int, evals=(0, 71, 143)) -> dict:
+    """The trunk's parity check beside its timing (the fp32 oracle as the checker only).
+
+    The hip trunk of ``trunk_measure`` is run once more, untimed, recording the input and
+    output of block evaluations ``evals`` (0-based); the fp32 CPU oracle is run from each
+    recorded input and the update's rel-RMS (pair over valid pairs, single over valid tokens)
+    is reported. The final state is compared with the fp32 reference trunk (the engine
+    ``pytorch`` backend with an fp32 residual stream, same GPU), beside the ``pytorch``
+    backend's own bf16 trunk: the rounding floor of a bf16 stream."""
+    import torch
+
+    import foldforge_amd
+    from oracle import pairstack as ps
+
+    z_cpu, s_cpu, mask_cpu = trunk_inputs(n)
+    model = foldforge_amd.load(backend="miniworld", device="cuda", blocks=TRUNK_BLOCKS, seed=0,
+                               d_single=D_SINGLE, unsupported="error")
+    prev, taken = [z_cpu.cuda(), s_cpu.cuda()], {}
+
+    def observe(p, i, pair, single):
+        e = TRUNK_BLOCKS * p + i
+        if e in evals:
+            taken[e] = (prev[0].cpu(), prev[1].cpu(), pair.cpu(), single.cpu())
+        prev[0], prev[1] = pair, single
+
+    with torch.no_grad():
+        hz, hs = model(z_cpu.cuda(), mask_cpu.cuda(), s_cpu.cuda(), passes=TRUNK_PASSES, on_block=observe)
+    hz, hs = hz.cpu().double(), hs.cpu().double()
+    state = model.state_dict()
+    del model
+    prev.clear()
+    torch.set_num_threads(min(16, os.cpu_count() or 1))
+    where = mask_cpu[:, :, None] & mask_cpu[:, None, :]
+    rows = []
+    for e in evals:
+        zi, si, zo, so = taken[e]
+        i = e % TRUNK_BLOCKS
+        sub = {k[len(f"blocks.{i}."):]: v.cpu() for k, v in state.items() if k.startswith(f"blocks.{i}.")}
+        wz, ws = ps.pairformer_block(zi, mask_cpu, sub, n_head_pair=4, s=si, n_head_single=16)
+        rows.append({"evaluation": e + 1,
+                     "pair_update_rel_rms": round(ps.rel_rms(zo.double() - zi.double(), wz.double() - zi.double(),
+                                                             where), 5),
+                     "single_update_rel_rms": round(ps.rel_rms(so.double() - si.double(),
+                                                               ws.double() - si.double(), mask_cpu), 5)})
+    with torch.no_grad():
+        ref = foldforge_amd.load(backend="pytorch", device="cuda", blocks=TRUNK_BLOCKS, seed=0,
+                                 d_single=D_SINGLE, dtype=torch.float32)
+        fz, fs = ref(z_cpu.float().cuda(), mask_cpu.cuda(), s_cpu.float().cuda(), passes=TRUNK_PASSES)
+        fz, fs = fz.cpu().double(), fs.cpu().double()
+        del ref
+        bref = foldforge_amd.load(backend="pytorch", device="cuda", blocks=TRUNK_BLOCKS, seed=0,
+                                  d_single=D_SINGLE)
+        bz, bs = bref(z_cpu.cuda(), mask_cpu.cuda(), s_cpu.cuda(), passes=TRUNK_PASSES)
+        bz, bs = bz.cpu().double(), bs.cpu().double()
+        del bref
+    torch.cuda.empty_cache()
+    return {
+        "sampled_block_updates_vs_fp32_oracle": rows,
+        "final_state_vs_fp32_reference_trunk": {
+            "hip": {"pair": round(ps.rel_rms(hz, fz, where), 5), "single": round(ps.rel_rms(hs, fs), 5)},
+            "pytorch_backend_bf16": {"pair": round(ps.rel_rms(bz, fz, where), 5),
+                                     "single": round(ps.rel_rms(bs, fs), 5)},
+        },
+        "note": "per-block bar 3e-2 on the update; the fp32 reference trunk is the engine pytorch backend "
+                "with an fp32 residual stream on the same GPU",
+    }
+
+
 def graph_measure(n: int, runs: int = 3) -> dict:
     """The 48 x 3 trunk run eagerly and as one captured graph (foldforge_amd.execution)."""
     import torch
@@ -613,6 +684,8 @@ def cpu_baseline(z, mask, state, gpu_out, runs: int, small: dict | None = None) 
     rr = ps.rel_rms(gpu_out.double() - z.double(), out.double() - z.double(), where)
     result = {"value": round(block_ms, 1), "unit": "ms per block",
               "cores": threads, "kind": "port",
+              "cores_note": f"capped at 16 threads: the host's CPU share for one GPU (os.cpu_count() = "
+                            f"{os.cpu_count()} counts the whole host, shared with the other GPUs' jobs)",
               "sample": f"the full timed workload: one block at N={z.shape[1]}, fp32, oracle/pairstack.py, "
                         f"op by op, median of {runs} after 1 warm-up; {threads} threads of {cpu_model()}",
               "ops_ms": ops, "gpu_vs_cpu_update_rel_rms": round(rr, 5)}
@@ -740,8 +813,11 @@ def main() -> int:
         trunk = trunk_measure(512, 2)
         print(f"trunk {trunk['ms_per_trunk']} ms ({trunk['ms_per_block']} ms/block)", file=sys.stderr,
               flush=True)
+        if not args.no_cpu_baseline:
+            trunk["parity"] = cpu_baseline_trunk_parity(512)
+            print(f"trunk parity {json.dumps(trunk['parity'])}", file=sys.stderr, flush=True)
         ladder_rows = []
-        for ln_ in (768, 1024):
+        for ln_ in (768, 1024, 1536, 2048):
             torch.cuda.empty_cache()
             row = trunk_measure(ln_, 1)
             ladder_rows.append({k: row[k] for k in ("n", "ms_per_trunk", "ms_per_block", "trunk_tflops", "finite")})

@@ -508,14 +508,15 @@ int32_t ffk_triangle_multiplication(
     return fail(FFK_ERR_WORKSPACE, "triangle_multiplication: workspace %zu bytes < %zu", workspace_bytes, need.bytes);
   const TrimulWs w = trimul_ws(workspace, batch, n, d_pair, d_hidden);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (length_divided) launch_length_eps(key_mask, (int)batch, (int)n, eps, w.eps_out, st);
-  const float* eps_out = length_divided ? w.eps_out : nullptr;
   // the output kernel addresses 8 channel planes from one base with 32-bit byte offsets
   if (fused && 7 * 2 * pad128(n) * pad128(n) > 0xffffffffLL)
     return fail(FFK_ERR_INVALID, "triangle_multiplication: n=%lld exceeds the fused kernels' plane offsets", (long long)n);
+  if (!fused && batch * d_hidden * (pad128(n) / 128) * (pad128(n) / 128) > 0x7fffffffLL)
+    return fail(FFK_ERR_INVALID, "triangle_multiplication: shape exceeds the launch grid");
+  // every argument check is behind us: nothing is queued or written before a refusal
+  if (length_divided) launch_length_eps(key_mask, (int)batch, (int)n, eps, w.eps_out, st);
+  const float* eps_out = length_divided ? w.eps_out : nullptr;
   if (!fused) {
-    if (batch * d_hidden * (pad128(n) / 128) * (pad128(n) / 128) > 0x7fffffffLL)
-      return fail(FFK_ERR_INVALID, "triangle_multiplication: shape exceeds the launch grid");
     const int64_t np = pad128(n);
     RowGemmArgs p{};
     p.ln_x = static_cast<const bf16*>(z);

@@ -279,7 +279,9 @@ def triangle_attention(
     extra = (("gate_bias", gate_bias, (hd,)), ("out_bias", out_bias, (c,)),
              ("to_out_t", to_out_t, (c, hd)), ("out_t_bias", out_t_bias, (c,)))
     opt = [None if t is None else _param(t, dev, nm, shape) for nm, t, shape in extra]
-    form = 2 if to_out_t is not None else 1 if untransposed_output else 0
+    # the starting node's untransposed update is the standard one: asking for form 0 spares the
+    # workspace the staging buffer of form 1
+    form = 2 if to_out_t is not None else 1 if untransposed_output and not starting else 0
     d = hd // n_head
     _need(triangle_attention_supported(c, n_head, d, transposed_bias),
           f"d_pair={c} heads={n_head} x {d} (the kernels take 128 with 4 x 32, or pair 64 / 128 / "

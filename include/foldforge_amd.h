@@ -128,7 +128,10 @@ int32_t ffk_triangle_multiplication(
  * orientation (Chai-1's trunk; the starting node is unchanged); 2 the update plus the
  * transpose over the pair axes of a second projection w_out_t [d_pair, n_head * d_head]
  * (+ b_out_t) of the same gated values (Chai-1's confidence head; w_out_t is required by, and
- * only by, this form). The workspace depends on the form.
+ * only by, this form). The workspace depends on the form: forms 1 and 2 add a staging buffer
+ * of batch * n * n * d_pair bf16; a starting-node call of form 1 is the standard form and
+ * never touches that buffer, so a caller may pass output_form 0 for it (and size the
+ * workspace for form 0).
  * Replaces: engine TriangleAttention(AF3 / OpenFold / RF3 / Chai1 / Chai1Confidence).forward
  * / `triangle_attention` (src/foldforge/models/checkpoints/legacy/attention.py:60-171,
  * legacy/reference/attention.py:77-100; forms src/foldforge/modules/dense/spec.py:116-125,

@@ -148,3 +148,84 @@ def test_trunk_48_blocks_3_passes_tracks_the_oracle():
                   f"stream rms pair {fz[where].pow(2).mean().sqrt():.3f}", flush=True)
     assert drift[0] <= 1.25 * ref_drift[0] + 1e-2, (drift, ref_drift)
     assert drift[1] <= 1.25 * ref_drift[1] + 1e-2, (drift, ref_drift)
+
+
+def test_trunk_n512_against_fp32_reference():
+    """The headline trunk: 48 blocks x 3 passes with the single track (c_s 384, 16 heads) at
+    N = 512, all-ones mask, the benchmark's model (seed 0, ``to_out`` / ``squeeze`` x 0.25)
+    and inputs, every op on ``hip``.
+    * Block evaluations 1, 72 and 144, each re-run from the hip trunk's own input to it: on
+      the fp32 CPU oracle with the residual stream rounded to bf16 after every op (the engine
+      contract: an op returns ``x + f(x)`` in its input dtype), and on the engine ``pytorch``
+      backend (same GPU, fp32 arithmetic inside every op). The hip update within rel-RMS
+      3e-2 of the oracle's (the per-block bar), pair and single. The same comparison against
+      the oracle with an fp32 stream throughout is printed beside it: at this depth the
+      stream's own bf16 rounding dominates that difference, for either backend.
+    * The final state against the fp32 reference trunk (the ``pytorch`` backend with an fp32
+      residual stream; its equations are pinned to the oracle by the CPU tests). The
+      ``pytorch`` backend's bf16 trunk against the same fp32 trunk is the floor a bf16
+      stream reaches: the hip trunk within 1.25 x that floor + 1e-2, pair and single alike."""
+    n, evals = 512, (0, 71, 143)
+    g = torch.Generator().manual_seed(7)
+    z = torch.randn(1, n, n, 128, generator=g).bfloat16()
+    s = torch.randn(1, n, 384, generator=g).bfloat16()
+    mask = torch.ones(1, n, dtype=torch.bool)
+    model = foldforge_amd.load(backend="miniworld", device="cuda", blocks=48, seed=0, d_single=384,
+                               unsupported="error")
+    prev, taken = [z.cuda(), s.cuda()], {}
+
+    def observe(p, i, pair, single):
+        e = 48 * p + i
+        if e in evals:
+            taken[e] = (prev[0].cpu(), prev[1].cpu(), pair.cpu(), single.cpu())
+        prev[0], prev[1] = pair, single
+
+    print("trunk N=512: hip", flush=True)
+    with torch.no_grad():
+        hz, hs = model(z.cuda(), mask.cuda(), s.cuda(), passes=3, on_block=observe)
+    assert dispatch.served_count(model, "hip") == 144 * 7
+    hz, hs = hz.cpu(), hs.cpu()
+    assert torch.isfinite(hz.float()).all() and torch.isfinite(hs.float()).all()
+    where = _valid_pairs(mask)
+
+    def upd(out, inp):
+        return out.double() - inp.double()
+
+    for e in evals:
+        zi, si, zo, so = taken[e]
+        blk = model.blocks[e % 48]
+        sub = {k: v.cpu() for k, v in blk.state_dict().items()}
+        with torch.no_grad():
+            blk.set_backend("pytorch")
+            pz, pss = blk(zi.cuda(), mask.cuda(), si.cuda())
+            blk.set_backend("hip")
+        pz, pss = pz.cpu(), pss.cpu()
+        oz, os_ = ps.pairformer_block(zi, mask, sub, n_head_pair=4, s=si, n_head_single=16,
+                                      io_dtype=torch.bfloat16)
+        fz, fs = ps.pairformer_block(zi, mask, sub, n_head_pair=4, s=si, n_head_single=16)
+        rows = {}
+        for name, (az, as_) in (("hip", (zo, so)), ("pytorch backend", (pz, pss))):
+            rows[name] = (ps.rel_rms(upd(az, zi), upd(oz, zi), where), ps.rel_rms(upd(as_, si), upd(os_, si), mask),
+                          ps.rel_rms(upd(az, zi), upd(fz, zi), where), ps.rel_rms(upd(as_, si), upd(fs, si), mask))
+        for name, r in rows.items():
+            print(f"trunk N=512 evaluation {e + 1} {name}: update vs fp32 oracle (bf16 stream) pair {r[0]:.3e} "
+                  f"single {r[1]:.3e}; vs fp32 stream pair {r[2]:.3e} single {r[3]:.3e}", flush=True)
+        assert rows["hip"][0] <= 3e-2 and rows["hip"][1] <= 3e-2, (e, rows)
+    del model, taken, prev
+    print("trunk N=512: fp32 reference and bf16 pytorch backend", flush=True)
+    with torch.no_grad():
+        ref = foldforge_amd.load(backend="pytorch", device="cuda", blocks=48, seed=0, d_single=384,
+                                 dtype=torch.float32)
+        fz, fs = ref(z.float().cuda(), mask.cuda(), s.float().cuda(), passes=3)
+        fz, fs = fz.cpu().double(), fs.cpu().double()
+        del ref
+        bref = foldforge_amd.load(backend="pytorch", device="cuda", blocks=48, seed=0, d_single=384)
+        bz, bs = bref(z.cuda(), mask.cuda(), s.cuda(), passes=3)
+        bz, bs = bz.cpu().double(), bs.cpu().double()
+    drift = (ps.rel_rms(hz.double(), fz, where), ps.rel_rms(hs.double(), fs, mask))
+    floor = (ps.rel_rms(bz, fz, where), ps.rel_rms(bs, fs, mask))
+    print(f"trunk N=512 final state vs fp32 trunk: hip pair {drift[0]:.3e} single {drift[1]:.3e}; "
+          f"pytorch backend bf16 pair {floor[0]:.3e} single {floor[1]:.3e}; stream rms pair "
+          f"{fz.pow(2).mean().sqrt():.3f} single {fs.pow(2).mean().sqrt():.3f}", flush=True)
+    assert drift[0] <= 1.25 * floor[0] + 1e-2, (drift, floor)
+    assert drift[1] <= 1.25 * floor[1] + 1e-2, (drift, floor)

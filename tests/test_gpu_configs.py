@@ -4,10 +4,10 @@
   the 128-tile contraction with three tiles per side. Against the fp64 oracle on valid pairs,
   the block update within rel-RMS 3e-2, one all-real and one ragged batch element.
 * Triangle multiplication at N = 320 (padded 384) in both directions, per-op bar.
-* The length ladder, one block with the single track at N = 768 and 1024: finite, bitwise
-  run-to-run, valid region bitwise invariant to padded content, and the update within 3e-2 of
-  the engine ``pytorch`` backend (fp32 arithmetic inside every op; it is pinned to the oracle
-  by the CPU tests) on the same GPU.
+* The length ladder, one block with the single track at N = 768, 1024, 1536 and 2048: finite,
+  bitwise run-to-run, valid region bitwise invariant to padded content, and the update within
+  3e-2 of the engine ``pytorch`` backend (fp32 arithmetic inside every op; it is pinned to the
+  oracle by the CPU tests) on the same GPU.
 * Every entry point whose C-ABI lets ``out`` alias its input, called in place: bitwise the
   out-of-place result.
 * ``run_block`` (FoldForge's unbatched layout, fp32 activations under autocast) on ``hip``.
@@ -86,7 +86,7 @@ def test_trimul_n320_three_tiles_per_side(outgoing):
     assert rr <= 1e-2 and ma <= 4e-2 * ref
 
 
-@pytest.mark.parametrize("n,length", [(768, 701), (1024, 977)])
+@pytest.mark.parametrize("n,length", [(768, 701), (1024, 977), (1536, 1489), (2048, 1999)])
 def test_ladder_block_with_single_track(n, length):
     g = torch.Generator(device="cuda").manual_seed(n)
     z = torch.randn(1, n, n, 128, device="cuda", generator=g).bfloat16()
@@ -129,12 +129,19 @@ def _module_args(m):
     return dict(ln_pair_weight=m.ln_pair.weight, ln_pair_bias=m.ln_pair.bias, to_bias=m.to_bias.weight,
                 to_query=m.to_query.weight, to_key=m.to_key.weight, to_value=m.to_value.weight,
                 to_gate=m.to_gate.weight, to_out=m.to_out.weight, n_head=m.n_head, starting=m.starting,
-                transposed_bias=m.transposed_bias)
+                transposed_bias=m.transposed_bias, gate_bias=m.to_gate.bias, out_bias=m.to_out.bias,
+                to_out_t=m.to_out_t.weight if m.dual_output else None,
+                out_t_bias=m.to_out_t.bias if m.dual_output else None,
+                untransposed_output=m.untransposed_output)
 
 
 @pytest.mark.parametrize("c,generic", [(128, False), (64, True)])
 def test_pair_ops_in_place(c, generic):
-    """``out`` aliasing ``z`` (the header's promise) gives the out-of-place result bitwise."""
+    """``out`` aliasing ``z`` (the header's promise) gives the out-of-place result bitwise: both
+    triangle multiplications, triangle attention in every lineage's output form (AF3's
+    transposed-back ending node, RoseTTAFold3's projection biases, Chai-1's untransposed and
+    dual outputs, which stage the ending node's update before adding it to ``out``), the
+    transition."""
     n = 100
     g = torch.Generator().manual_seed(46)
     z = torch.randn(2, n, n, c, generator=g).bfloat16().cuda()
@@ -145,15 +152,15 @@ def test_pair_ops_in_place(c, generic):
     heads, dh = (4, 16) if generic else (4, 32)
     mods = [randomise(factories.triangle_multiplication(c, outgoing=o, d_hidden=hidden), seed=47).cuda()
             for o in (True, False)]
-    mods += [randomise(factories.triangle_attention(c, heads, starting=st, model="af3", d_hidden=heads * dh),
-                       seed=48).cuda() for st in (True, False)]
+    mods += [randomise(factories.triangle_attention(c, heads, starting=st, model=key, d_hidden=heads * dh),
+                       seed=48).cuda() for st in (True, False) for key in ("af3", "rf3", "chai1", "chai1_confidence")]
     for m in mods:
         call = kernels.triangle_multiplicative_update if "Multiplication" in type(m).__name__ else kernels.triangle_attention
         want = call(z, mask, **_module_args(m))
         buf = z.clone()
         got = call(buf, mask, **_module_args(m), out=buf)
         assert got.data_ptr() == buf.data_ptr()
-        assert torch.equal(got, want), type(m).__name__
+        assert torch.equal(got, want), (type(m).__name__, m.starting)
     tr = randomise(factories.transition(c, 4 if not generic else 2), seed=49).cuda()
     targs = dict(ln_weight=tr.ln_in.weight, ln_bias=tr.ln_in.bias, expand_a=tr.expand_a.weight,
                  expand_b=tr.expand_b.weight, squeeze=tr.squeeze.weight)

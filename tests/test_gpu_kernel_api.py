@@ -60,7 +60,8 @@ def test_layer_norm_linear_without_affine_or_bias():
     _check(got, want, "layer_norm_linear, no affine, no bias")
 
 
-@pytest.mark.parametrize("rows,d,hidden", [(2 * 96 * 96, 128, 512), (513, 384, 1536), (77, 64, 128)])
+@pytest.mark.parametrize("rows,d,hidden", [(2 * 96 * 96, 128, 512), (513, 384, 1536), (77, 64, 128),
+                                           (300, 768, 1536)])
 def test_swiglu_ffn_matches_oracle(rows, d, hidden):
     g = torch.Generator().manual_seed(rows + d)
     x = torch.randn(rows, d, generator=g).bfloat16()

@@ -164,6 +164,17 @@ def test_triattn_matches_oracle(starting, model, n, lengths):
     _check(got, want, _pairs(mask), f"triattn starting={starting} {model} n={n}")
 
 
+def test_triattn_single_op_workload_shape():
+    """The single-op workload the CPU baseline times: starting node on z [1, 128, 128, 128]
+    ~N(0, 1) (seed 0), 4 heads x 32, all-ones mask, random init from seed 0."""
+    z, mask = _pair(128, 1, seed=0)
+    m = randomise(factories.triangle_attention(128, 4, starting=True, model="af3"), seed=0).cuda()
+    m.set_backend("hip")
+    got = hip_delta(m, z.cuda(), mask.cuda()).cpu()
+    want = ps.triangle_attention(z, mask, m.state_dict(), starting=True, n_head=4, dtype=torch.float64) - z.double()
+    _check(got, want, None, "triattn starting af3 n=128 (single-op workload)")
+
+
 def test_transition_matches_oracle():
     z, _ = _pair(72, 2, seed=3)
     m = randomise(factories.transition(128, 4), seed=5).cuda()

@@ -35,6 +35,8 @@
 //    B-operand order of the P V product.
 #include <math.h>
 
+#include <type_traits>
+
 #include "ffk_device.h"
 #include "ffk_kernels.h"
 
@@ -47,6 +49,7 @@ constexpr int kFW = 4;      // waves per flash workgroup, 32 queries each (two w
 constexpr int kFK = 32;     // keys per LDS stage
 constexpr float kSumHigh = 1.2676506002282294e30f;  // 2^100
 constexpr float kSumLow = 7.888609052210118e-31f;    // 2^-100
+constexpr float kSumRescale = 1.8446744073709552e19f; // 2^64: a tile's partial sum that raises m
 
 constexpr int kPT = 64;        // positions per projection / output tile
 
@@ -398,9 +401,17 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
   wait_vm_lds<0>();
   __syncthreads();
 
-  // one offset per query, shared by the wave's rows: the largest bias of the first key tile
-  // (0 when that tile is fully masked). It depends on the bias row alone, so no row of the
-  // workgroup (a padded one included) can change another row's rounding.
+  // Offsets. Each query starts from one offset shared by the wave's rows: the largest bias of
+  // its first key tile (0 when that tile is fully masked), subtracted from the bias tile once
+  // per stage, so the key loop needs no subtraction of its own. A tile whose partial sum
+  // reaches 2^64 (logits more than 64 log2 units above the offset, e.g. large q.k) gives that
+  // row an extra offset of its own: the tile's maximum rounded up to bf16, while the row's
+  // l and O so far are scaled down by the increase and the tile is recomputed (a uniform
+  // branch the common case never takes). From then on the extra offset enters the row's S
+  // accumulation through one more MFMA with constant operands (A: 1 at k = 0 of every key
+  // row; B: minus the offset at k = 0 of the lane's query). Every offset depends on the row's
+  // and query's own logits, so no row of the workgroup (a padded one included) changes another
+  // row's rounding.
   float msh = 0.f;
   if (active) {
     const float* bt = &lds.bias[wave][0][4 * lane];
@@ -414,9 +425,21 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
     tm = pair_max(tm);
     msh = tm > -INFINITY ? tm : 0.f;
   }
+  const bf16x8 ones8 = g == 0 ? bf16x8{(bf16)1.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f, (bf16)0.f} : zero8;
+  bf16x8 moff[FR];  // minus the row's extra offset at k = 0 of this lane's query (half 1: zeros)
+  float xoff[FR];   // the extra offset (a bf16 value), the same in both lanes of a query
+#pragma unroll
+  for (int rr = 0; rr < FR; ++rr) {
+    moff[rr] = zero8;
+    xoff[rr] = 0.f;
+  }
 
-#pragma unroll 1
-  for (int64_t st = 0; st < nrun; ++st) {
+  // One stage; XOFF: with the rows' extra offsets. The key loop runs without them until some
+  // row of the wave needs one (never, for moderate logits), then with them to the end: two
+  // straight loops rather than a test per row and tile.
+  bool xrows = false;  // some row of the wave has an extra offset (wave-uniform)
+  auto stage = [&](int64_t st, auto xo) {
+    constexpr bool XOFF = decltype(xo)::value;
     const int sb = (int)(st & 1);
     // this wave's bias tile st and everyone's K / V^T stage st have landed (waited for and
     // published at the end of the last stage)
@@ -434,7 +457,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
     kv_dma(st + 1, sb ^ 1);  // the other stage buffer, read last stage
     bias_dma(st + 1);        // the other tile buffer, read last stage (issued last: see below)
     if (active) {
-      // two rows at a time: S^T = (bias - m) + K Q^T, softmax, O^T += V^T P^T
+      // two rows at a time: S^T = (bias - m) + K Q^T and the exponentials, one check of the
+      // partial sums, then O^T += V^T P^T
 #pragma unroll
       for (int rp = 0; rp < FR; rp += 2) {
         f32x16 S[2];
@@ -442,14 +466,42 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
         for (int u = 0; u < 2; ++u) {
           const int rr = rp + u;
           const bf16* kt = lds.k[sb][rr];
-          S[u] = mfma32(ld8(kt + koff<DQ>(li, g)), qa[rr][0], bcur);
+          S[u] = XOFF ? mfma32(ones8, moff[rr], bcur) : bcur;
 #pragma unroll
-          for (int f = 1; f < DQ; ++f) S[u] = mfma32(ld8(kt + koff<DQ>(li, 2 * f + g)), qa[rr][f], S[u]);
+          for (int f = 0; f < DQ; ++f) S[u] = mfma32(ld8(kt + koff<DQ>(li, 2 * f + g)), qa[rr][f], S[u]);
         }
         bf16x8 p0[2], p1[2];
         float ts[2];
 #pragma unroll
         for (int u = 0; u < 2; ++u) ts[u] = exp_pack(S[u], p0[u], p1[u]);
+        if (__builtin_amdgcn_ballot_w64(!(ts[0] < kSumRescale) || !(ts[1] < kSumRescale)) != 0) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int rr = rp + u;
+            if (__builtin_amdgcn_ballot_w64(!(ts[u] < kSumRescale)) == 0) continue;
+            // logits far above the offset: the row's extra offset rises to the tile's maximum
+            // (rounded up to bf16), its sum and output so far are scaled by 2^-(increase), and
+            // the tile is recomputed
+            float tm = -INFINITY;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) tm = fmaxf(tm, S[u][e]);
+            tm = pair_max(tm);
+            const float xn = tm > 0.f ? bf16_ceil(xoff[rr] + tm) : xoff[rr];
+            const float dm = xn - xoff[rr];
+            const float f = fast_exp2(-dm);
+#pragma unroll
+            for (int e = 0; e < 16; ++e) S[u][e] -= dm;
+            l[rr] *= f;
+#pragma unroll
+            for (int h = 0; h < DH; ++h)
+#pragma unroll
+              for (int e = 0; e < 16; ++e) O[rr][h][e] *= f;
+            xoff[rr] = xn;
+            if (g == 0) moff[rr][0] = (bf16)(-xn);
+            xrows = true;
+            ts[u] = exp_pack(S[u], p0[u], p1[u]);
+          }
+        }
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int rr = rp + u;
@@ -468,7 +520,12 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
     // stage's reads of the buffer the next transfers overwrite
     wait_vm_lds<4>();
     __syncthreads();
-  }
+    };
+  int64_t st = 0;
+#pragma unroll 1
+  for (; st < nrun && !xrows; ++st) stage(st, std::false_type{});
+#pragma unroll 1
+  for (; st < nrun; ++st) stage(st, std::true_type{});
   wait_vm_lds<0>();  // no LDS write may land after exit
   if (!active) return;
 

@@ -229,6 +229,29 @@ def test_flash_core_large_logits_and_exact_masking():
     assert torch.equal(out.cpu(), out2.cpu())
 
 
+@pytest.mark.parametrize("q_scale", [4.0, 25.0])
+def test_flash_core_large_qk_logits(q_scale):
+    """Logits dominated by q . k (std 4 x 5.7 and 25 x 5.7 log2 units: about 16 and 100 nats,
+    the trained-weight regime), unit-scale bias, a masked key block: the rows' offsets rise
+    during the key loop (rescale of l and O), and the result still matches an fp32 softmax."""
+    B, H, R, n = 1, 4, 8, 256
+    g = torch.Generator().manual_seed(23)
+    q = (q_scale * torch.randn(B, H, R, n, 32, generator=g)).bfloat16()
+    k = torch.randn(B, H, R, n, 32, generator=g).bfloat16()
+    v = torch.randn(B, H, R, n, 32, generator=g).bfloat16()
+    bias = torch.randn(B, H, n, n, generator=g)
+    bias[..., 96:128] = float("-inf")
+    out = torch.zeros(B, R, n, H * 32, dtype=torch.bfloat16, device="cuda")
+    kernels.flash_attention_bias(q.cuda(), k.cuda(), kernels.flash_v_layout(v.transpose(-1, -2)).cuda(),
+                                 kernels.blocked_bias(bias).cuda(), out, rows_valid=R, n_valid=n)
+    logits = q.double() @ k.double().transpose(-1, -2) + bias.double()[:, :, None]
+    w = torch.softmax(logits * 0.6931471805599453, dim=-1)
+    want = (w @ v.double()).permute(0, 2, 3, 1, 4).reshape(B, R, n, H * 32)
+    got = out.cpu().float()
+    assert torch.isfinite(got).all()
+    _check(got, want, None, f"flash core, q.k logits x{q_scale}")
+
+
 def test_flash_core_moderate_logits_and_partial_query_block():
     """Unit-scale logits (the lazy offset never moves after the first tile), n = 384 so the
     last 256-query block is half outside, and only some rows / queries are stored."""

@@ -193,16 +193,36 @@ def copy_reference(mib: int, reps: int = 3) -> dict:
             "gbs": round(2.0 * (mib << 20) / (ms * 1e-3) / 1e9, 1)}
 
 
+FLASH_SOURCES = ("foldforge_amd/csrc/triattn.hip", "foldforge_amd/csrc/ffk_device.h",
+                 "foldforge_amd/csrc/ffk_kernels.h")
+
+
+def source_digest(paths=FLASH_SOURCES) -> str:
+    """sha256 over the named source files (in order): the code a counter summary was taken on."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for p in paths:
+        h.update((ROOT / p).read_bytes())
+    return h.hexdigest()
+
+
 def recorded_traffic(kernel: str) -> float | None:
     """HBM bytes per launch of ``kernel`` from the committed rocprofv3 counter summary
-    (``profiles/<kernel>_traffic.md``, line ``traffic_bytes_per_launch: <n>``), else None."""
+    (``profiles/<kernel>_traffic.md``, line ``traffic_bytes_per_launch: <n>``). The summary
+    names the digest of the flash-core sources it was measured on (``source_sha256: <hex>``);
+    a summary of other sources is stale and gives None, as does a missing one."""
     path = ROOT / "profiles" / f"{kernel}_traffic.md"
     if not path.exists():
         return None
+    fields = {}
     for line in path.read_text().splitlines():
-        if line.strip().startswith("traffic_bytes_per_launch:"):
-            return float(line.split(":", 1)[1])
-    return None
+        key, sep, val = line.strip().partition(":")
+        if sep and key in ("traffic_bytes_per_launch", "source_sha256"):
+            fields[key] = val.strip()
+    if fields.get("source_sha256") != source_digest() or "traffic_bytes_per_launch" not in fields:
+        return None
+    return float(fields["traffic_bytes_per_launch"])
 
 
 TRUNK_BLOCKS, TRUNK_PASSES, D_SINGLE = 48, 3, 384

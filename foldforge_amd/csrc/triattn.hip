@@ -16,16 +16,18 @@
 //  * S^T (32 keys x 32 queries) is one MFMA accumulator. Its initial value is the pair-bias
 //    tile (fp32, stored by kernel 1 in the accumulator's register order), shared by the 4
 //    attention rows of the workgroup (the bias does not depend on the row).
-//  * Fixed-offset softmax: one offset m per query, shared by the wave's 4 rows, is the
-//    largest bias of the first key tile (computed before the loop from the bias alone, so
-//    padded rows cannot change a valid row's rounding) and never moves. It is subtracted
-//    from the bias tile once per key block (the accumulator's initial value), so the key
-//    loop has no branch and no extra work per row: two MFMAs, exp2, bf16 packing and a
-//    v_dot2 row sum, about one VALU op plus one exp per logit, and the compiler can
-//    interleave the rows' matrix and vector work freely. A row whose final sum leaves
-//    [2^-100, 2^100] (logits more than ~100 log2 units above m, or all of them that far
-//    below) is recomputed exactly at the end with a two-pass softmax (true maximum first);
-//    the sum bound keeps every intermediate finite, so the check after the loop suffices.
+//  * Offsets without a running maximum: one offset m per query, shared by the wave's 4 rows,
+//    is the largest bias of the first key tile (computed before the loop from the bias alone,
+//    so padded rows cannot change a valid row's rounding). It is subtracted from the bias
+//    tile once per key block (the accumulator's initial value), so the common key loop has
+//    no per-logit work beyond two MFMAs, exp2, bf16 packing and a v_dot2 row sum, and one
+//    test of the partial sums per pair of rows. A tile whose partial sum reaches 2^64 gives
+//    its row an extra offset (the tile maximum, rounded up to bf16) and rescales the row's
+//    l and O: the lazy form of a running maximum, paid only where logits outgrow the offset
+//    (large q . k), and the extra offset then enters the row's S accumulation through one
+//    more MFMA with constant operands. A row whose final sum still leaves [2^-100, 2^100]
+//    (every logit far below the offset) is recomputed exactly at the end with a two-pass
+//    softmax (true maximum first).
 //  * Every operand tile reaches LDS by LDS DMA (no registers, no VALU): K and V^T of the 4
 //    rows in stages of 64 keys (double-buffered, shared by the 8 waves) and each wave's bias
 //    tiles (double-buffered), all one step ahead, with explicit waits on the wave's own

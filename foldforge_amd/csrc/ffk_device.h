@@ -341,18 +341,27 @@ __device__ __forceinline__ int off128(int r, int k8) { return r * 128 + 8 * (k8 
 // wait insertion does not treat every later LDS read as dependent on it: each use is paired
 // with an explicit s_waitcnt vmcnt (vector-memory operations of a wave complete in order)
 // before the data is read, and a kernel waits for its last transfers before it exits.
+// The compiler does not look inside inline assembly for hazards, so the transfer is preceded
+// by the wait states the ISA requires of its operands: 5 after a VALU instruction writes an
+// SGPR that a VMEM instruction reads (the compiler materialises sbase with v_readlane or
+// v_readfirstlane when scalar registers run short), which also covers the 1 after an SALU
+// write of M0 before a global load with LDS = 1.
+#define FFK_DMA_HAZARD "s_nop 4\n"
 __device__ __forceinline__ void dma16(const void* sbase, uint32_t voff, uint32_t m0) {
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+  asm volatile(FFK_DMA_HAZARD "global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0)
+               : "memory");
 }
 // Same for data read once (the pair tensor): non-temporal, so the stream does not evict
 // reused data (weights) from L2.
 __device__ __forceinline__ void dma16_stream(const void* sbase, uint32_t voff, uint32_t m0) {
-  asm volatile("global_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase), "{m0}"(m0)
+  asm volatile(FFK_DMA_HAZARD "global_load_lds_dwordx4 %0, %1 nt" ::"v"(voff), "s"(sbase),
+               "{m0}"(m0)
                : "memory");
 }
 // Same for 4 bytes per lane: lane L copies sbase + voff to LDS byte address m0 + 4 L.
 __device__ __forceinline__ void dma4(const void* sbase, uint32_t voff, uint32_t m0) {
-  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0) : "memory");
+  asm volatile(FFK_DMA_HAZARD "global_load_lds_dword %0, %1" ::"v"(voff), "s"(sbase), "{m0}"(m0)
+               : "memory");
 }
 // Wait until at most N vector-memory operations of this wave are in flight and its LDS
 // operations are done.

@@ -175,13 +175,16 @@ def test_triattn_single_op_workload_shape():
     _check(got, want, None, "triattn starting af3 n=128 (single-op workload)")
 
 
-def test_transition_matches_oracle():
-    z, _ = _pair(72, 2, seed=3)
+@pytest.mark.parametrize("n,batch", [(72, 2), (300, 1)])
+def test_transition_matches_oracle(n, batch):
+    """(300, 1): 90000 positions = 703 full tiles of 128 and a ragged one, more tiles than the
+    persistent grid holds, so workgroups carry the weight stream from one tile into the next."""
+    z, _ = _pair(n, batch, seed=3)
     m = randomise(factories.transition(128, 4), seed=5).cuda()
     m.set_backend("hip")
     got = hip_delta(m, z.cuda()).cpu()
     want = ps.transition(z, m.state_dict(), dtype=torch.float64) - z.double()
-    _check(got, want, None, "transition")
+    _check(got, want, None, f"transition n={n} batch={batch}")
 
 
 def test_padding_is_bitwise_invisible_to_the_valid_region():

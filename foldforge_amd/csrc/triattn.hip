@@ -304,6 +304,19 @@ __device__ __forceinline__ float exp_pack(const f32x16& S, bf16x8& p0, bf16x8& p
   return ts;
 }
 
+// Scheduling of one pipelined region of the flash stage: its NR operand reads from LDS first,
+// then NM times one MFMA followed by NV VALU instructions (the exponentials, packing and sums
+// of the other row pair).
+template <int NR, int NM, int NV>
+__device__ __forceinline__ void flash_interleave() {
+  __builtin_amdgcn_sched_group_barrier(0x100, NR, 0);
+#pragma unroll
+  for (int i = 0; i < NM; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);
+  }
+}
+
 // grid (ceil(np / 128) * (rows / FR) * batch * heads) workgroups, renumbered per XCD;
 // block 256 = 4 waves x 32 queries, FR attention rows. GATED: the output is og = gate * o,
 // else o (bf16 either way).
@@ -459,11 +472,13 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
     kv_dma(st + 1, sb ^ 1);  // the other stage buffer, read last stage
     bias_dma(st + 1);        // the other tile buffer, read last stage (issued last: see below)
     if (active) {
-      // two rows at a time: S^T = (bias - m) + K Q^T and the exponentials, one check of the
-      // partial sums, then O^T += V^T P^T
-#pragma unroll
-      for (int rp = 0; rp < FR; rp += 2) {
-        f32x16 S[2];
+      // Rows in pairs: S^T = (bias - m) + K Q^T, the exponentials, one check of the partial
+      // sums, then O^T += V^T P^T. With two pairs the stage is software-pipelined inside the
+      // wave: the exponentials of one pair are issued between the MFMAs of the other (the
+      // logits of pair 2 under the exponentials of pair 0, then the P V products of pair 0
+      // under those of pair 2), since a SIMD overlaps a wave's VALU work with that wave's own
+      // MFMAs but not with another wave's.
+      auto qk_pair = [&](int rp, f32x16 (&S)[2]) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int rr = rp + u;
@@ -472,10 +487,12 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
 #pragma unroll
           for (int f = 0; f < DQ; ++f) S[u] = mfma32(ld8(kt + koff<DQ>(li, 2 * f + g)), qa[rr][f], S[u]);
         }
-        bf16x8 p0[2], p1[2];
-        float ts[2];
+      };
+      auto exp_pair = [&](const f32x16 (&S)[2], bf16x8 (&p0)[2], bf16x8 (&p1)[2], float (&ts)[2]) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) ts[u] = exp_pack(S[u], p0[u], p1[u]);
+      };
+      auto check_pair = [&](int rp, f32x16 (&S)[2], bf16x8 (&p0)[2], bf16x8 (&p1)[2], float (&ts)[2]) {
         if (__builtin_amdgcn_ballot_w64(!(ts[0] < kSumRescale) || !(ts[1] < kSumRescale)) != 0) {
 #pragma unroll
           for (int u = 0; u < 2; ++u) {
@@ -504,6 +521,8 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
             ts[u] = exp_pack(S[u], p0[u], p1[u]);
           }
         }
+      };
+      auto pv_pair = [&](int rp, const bf16x8 (&p0)[2], const bf16x8 (&p1)[2], const float (&ts)[2]) {
 #pragma unroll
         for (int u = 0; u < 2; ++u) {
           const int rr = rp + u;
@@ -515,6 +534,33 @@ __global__ __launch_bounds__(256, 2) void flash_attn_bias(FlashArgs a) {
             O[rr][h] = mfma32(ld8(vtile + voff(dl + 32 * h, 2 + g)), p1[u], O[rr][h]);
           }
         }
+      };
+      f32x16 SA[2], SB[2];
+      bf16x8 pA0[2], pA1[2], pB0[2], pB1[2];
+      float tsA[2], tsB[2];
+      if constexpr (FR == 2) {
+        qk_pair(0, SA);
+        exp_pair(SA, pA0, pA1, tsA);
+        check_pair(0, SA, pA0, pA1, tsA);
+        pv_pair(0, pA0, pA1, tsA);
+      } else {
+        static_assert(FR == 4, "flash rows per workgroup");
+        constexpr int NQK = 2 * (DQ + (XOFF ? 1 : 0));  // MFMAs of one pair's logits
+        qk_pair(0, SA);
+        __builtin_amdgcn_sched_barrier(0);  // (each pipelined region is scheduled on its own)
+        // the logits of rows 2, 3 under the exponentials of rows 0, 1
+        qk_pair(2, SB);
+        exp_pair(SA, pA0, pA1, tsA);
+        flash_interleave<2 * DQ, NQK, 64 / NQK>();
+        __builtin_amdgcn_sched_barrier(0);
+        check_pair(0, SA, pA0, pA1, tsA);
+        // the P V products of rows 0, 1 under the exponentials of rows 2, 3
+        pv_pair(0, pA0, pA1, tsA);
+        exp_pair(SB, pB0, pB1, tsB);
+        flash_interleave<4 * DH, 4 * DH, 64 / (4 * DH)>();
+        __builtin_amdgcn_sched_barrier(0);
+        check_pair(2, SB, pB0, pB1, tsB);
+        pv_pair(2, pB0, pB1, tsB);
       }
     }
     // this wave's pieces of the next K / V^T stage have landed (only its 4 bias pieces, issued

@@ -1079,6 +1079,131 @@ __global__ __launch_bounds__(256) void apb_pair_bias(PairBiasArgs a) {
   }
 }
 
+// The same bias at pair width 128 with the z rows staged through LDS: each wave owns two 8 KB
+// tile buffers that its own LDS DMA fills (each transfer is 4 whole rows, 1 KB contiguous for
+// the un-transposed orientation, swizzled by off128), one tile ahead of the one it processes, so
+// the rows arrive as full lines instead of 32-byte pieces of 32 rows per load; a wave's buffers
+// are its own, so the loop has no barrier. Persistent: every wave walks tiles t0, t0 + stride, ...
+// (stride = 4 gridDim.x). The waits count this wave's vector-memory operations, which on gfx950
+// include its stores: waiting for tile k's rows also waits for the stores of tile k - 1, issued
+// one tile earlier.
+__global__ __launch_bounds__(256, 2) void apb_pair_bias_lds(PairBiasArgs a) {
+  constexpr int C = 128, kU = C / 16;
+  __shared__ float wsum_s[4][32];
+  __shared__ __attribute__((aligned(16))) bf16 zt[4][2][32 * C];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63, li = lane & 31, g = lane >> 5;
+  const int n = a.n;
+  const int njt = a.np / 32;
+  const int64_t stride = (int64_t)gridDim.x * 4;
+  const uint32_t zt_lds = lds_addr(&zt[wave][0][0]);
+
+  // Rows j0 .. j0 + 31 of tile `tile` (keys past n repeat key n - 1: finite, masked) into
+  // buffer buf; a tile index past the end re-reads the last tile. Piece p = rows 4 p .. 4 p + 3:
+  // lane L fills slot L & 15 of row 4 p + L / 16 with the row's chunk (L & 15) ^ (row & 15).
+  auto tile_dma = [&](int64_t tile, int buf) {
+    const int64_t tt = tile < a.tiles ? tile : a.tiles - 1;
+    const int64_t bi = tt / njt;
+    const int j0 = (int)(tt - bi * njt) * 32;
+    const int64_t b = bi / n, i = bi - b * n;
+    const bf16* base = a.transposed ? a.z + (b * n * n + i) * C : a.z + bi * n * C;
+    const uint32_t rstride = a.transposed ? (uint32_t)n * C * 2 : (uint32_t)C * 2;
+#pragma unroll
+    for (int p = 0; p < 8; ++p) {
+      const int r = 4 * p + (lane >> 4);
+      const int key = min(j0 + r, n - 1);
+      dma16_stream(base, (uint32_t)key * rstride + 16 * ((lane & 15) ^ (r & 15)),
+                   zt_lds + (uint32_t)(buf * 32 * C * 2 + 1024 * p));
+    }
+  };
+  int64_t t = (int64_t)blockIdx.x * 4 + wave;
+  if (t < a.tiles) tile_dma(t, 0);
+
+  bf16x8 wf[kU], wl[kU];
+  float rs = 0.f;
+  const float* wrow = a.w_bias + min(li, a.heads - 1) * C + 8 * g;
+  const float* lrow = a.ln_w + 8 * g;
+  const float keep = li < a.heads ? kLog2e : 0.f;
+#pragma unroll
+  for (int u = 0; u < kU; ++u) {
+    const f32x4 w0 = *reinterpret_cast<const f32x4*>(wrow + 16 * u);
+    const f32x4 w1 = *reinterpret_cast<const f32x4*>(wrow + 16 * u + 4);
+    const f32x4 l0 = *reinterpret_cast<const f32x4*>(lrow + 16 * u);
+    const f32x4 l1 = *reinterpret_cast<const f32x4*>(lrow + 16 * u + 4);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float v = keep * (e < 4 ? l0[e] * w0[e] : l1[e - 4] * w1[e - 4]);
+      wf[u][e] = (bf16)v;
+      wl[u][e] = (bf16)(v - (float)wf[u][e]);
+      rs += v;
+    }
+  }
+  rs = pair_sum(rs);
+  if (g == 0) wsum_s[wave][li] = rs;
+  __syncthreads();
+  if (t >= a.tiles) return;  // no transfer of this wave is in flight
+
+  for (int k = 0;; ++k) {
+    const bool more = t + stride < a.tiles;
+    if (more) {
+      tile_dma(t + stride, (k + 1) & 1);
+      wait_vm_lds<8>();  // tile k's rows (and everything before them) landed
+    } else {
+      wait_vm_lds<0>();
+    }
+    bf16x8 zf[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) zf[u] = ld8(&zt[wave][k & 1][off128(li, 2 * u + g)]);
+
+    float s1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s1 += (float)zf[u][e];
+    const float mean = pair_sum(s1) * (1.f / C);
+    float s2 = 0.f;
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float d = (float)zf[u][e] - mean;
+        s2 += d * d;
+      }
+    const float rstd = __builtin_amdgcn_rsqf(pair_sum(s2) * (1.f / C) + a.eps);
+    f32x16 acc = zero16();
+#pragma unroll
+    for (int u = 0; u < kU; ++u) acc = mfma32(wl[u], zf[u], acc);
+#pragma unroll
+    for (int u = 0; u < kU; ++u) acc = mfma32(wf[u], zf[u], acc);
+
+    const int64_t bi = t / njt;
+    const int key = (int)(t - bi * njt) * 32 + li;
+    const int64_t b = bi / n;
+    const int64_t i = bi - b * n;
+    const bool valid = key < n && a.mask[b * n + key] != 0;
+    float* out = a.bias + (b * a.heads * n + i) * a.np + key;
+    if (a.blocked) out = a.bias + bias_index(b * a.heads, a.np / 32, i, key);
+    const int64_t hstride = a.blocked ? (int64_t)a.np * a.np : (int64_t)n * a.np;
+    const float masked = a.blocked ? -INFINITY : kMaskedLogit;
+    const int64_t xe = b * a.extra_sb + i * a.extra_si + key;  // head 0's extra logit
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int h = acc_row(r, g);
+      if (h < a.heads) {
+        float y = rstd * (acc[r] - mean * wsum_s[wave][h]);
+        if (a.extra && valid) {
+          const int64_t at = xe + h * a.extra_sh;
+          y += kLog2e * (a.extra_bf16 ? (float)static_cast<const bf16*>(a.extra)[at]
+                                      : static_cast<const float*>(a.extra)[at]);
+        }
+        out[h * hstride] = valid ? y : masked;
+      }
+    }
+    t += stride;
+    if (t >= a.tiles) break;
+  }
+}
+
 // ---------------------------------------------------------------------------- attention
 // One workgroup per (32 queries, head, batch); its four waves split the key blocks
 // (wave w takes blocks w, w + 4, ...), run an online softmax each and are merged through LDS.
@@ -1364,6 +1489,16 @@ void launch_row_gemm(const RowGemmArgs& a, int epi, int xsrc, hipStream_t stream
 }
 
 void launch_apb_pair_bias(const PairBiasArgs& a, hipStream_t stream) {
+  // pair width 128: the LDS-staged persistent kernel (two workgroups per CU), unless a
+  // transposed key offset would not fit its 32-bit DMA offset
+  if (a.c == 128 && (!a.transposed || (int64_t)a.n * a.n * 256 <= 0xffffffffLL)) {
+    int64_t blocks = (a.tiles + 3) / 4;
+    const int64_t cap = (int64_t)cu_count() * 2;
+    if (blocks > cap) blocks = cap;
+    if (blocks < 1) blocks = 1;
+    apb_pair_bias_lds<<<dim3((unsigned)blocks), 256, 0, stream>>>(a);
+    return;
+  }
   int64_t blocks = (a.tiles + 7) / 8;  // about two tiles per wave
   const int64_t cap = (int64_t)cu_count() * 8;
   if (blocks > cap) blocks = cap;

@@ -376,6 +376,7 @@ int32_t transition_run(const TransitionWs& w, const void* x, const float* ln_w, 
                        int d, int factor, int residual, float eps, hipStream_t st) {
   if (!transition_fused(d, factor)) {
     RowGemmArgs g{};
+    g.w_split = 1;  // fp32-accurate weights (see row_gemm)
     g.ln_x = static_cast<const bf16*>(x);
     g.ln_w = ln_w;
     g.ln_b = ln_b;
@@ -389,6 +390,7 @@ int32_t transition_run(const TransitionWs& w, const void* x, const float* ln_w, 
     g.h16 = w.hb;
     launch_row_gemm(g, kEpiSwiglu, kXLn, st);
     RowGemmArgs s{};
+    s.w_split = 1;  // fp32-accurate weights (see row_gemm)
     s.x32 = w.h;
     s.ln_x = w.hb;
     s.ln_plain = 1;
@@ -1013,6 +1015,7 @@ int32_t ffk_swiglu_ffn(const void* x, const float* w_a, const float* w_b, const 
   if (rows == 0) return ok();
   hipStream_t st = static_cast<hipStream_t>(stream);
   RowGemmArgs g{};
+  g.w_split = 1;  // fp32-accurate weights (see row_gemm)
   g.ln_x = static_cast<const bf16*>(x);
   g.ln_plain = 1;
   g.w0 = w_a;
@@ -1023,6 +1026,7 @@ int32_t ffk_swiglu_ffn(const void* x, const float* w_a, const float* w_b, const 
   g.h32 = static_cast<float*>(workspace);
   launch_row_gemm(g, kEpiSwiglu, kXLn, st);
   RowGemmArgs s{};
+  s.w_split = 1;  // fp32-accurate weights (see row_gemm)
   s.x32 = static_cast<const float*>(workspace);
   s.w0 = w_out;
   s.M = rows;
@@ -1078,6 +1082,7 @@ int32_t ffk_attention_pair_bias(
   const int64_t np = pad32(n);
   const int dh = d_single / n_head;
   RowGemmArgs p{};
+  p.w_split = 1;  // fp32-accurate weights (see row_gemm)
   p.ln_x = static_cast<const bf16*>(s);
   p.ln_w = ln_single_w;
   p.ln_b = ln_single_b;
@@ -1139,6 +1144,7 @@ int32_t ffk_attention_pair_bias(
   launch_apb_attention(at, (int)batch, st);
 
   RowGemmArgs o{};
+  o.w_split = 1;  // fp32-accurate weights (see row_gemm)
   o.x32 = w.og;
   o.w0 = w_out;
   o.M = rows;

@@ -141,6 +141,10 @@ struct RowGemmArgs {
   // kEpiSwiglu: w0 = expand_a, w1 = expand_b ([hid][K] each, O = 2 hid);
   // kEpiResid: w0 = [O][K]
   const float *w0, *w1, *w2, *w3;
+  // token-row GEMM (row_gemm): 1 = the weights enter as bf16 hi + lo as well, three MFMAs per
+  // k step (W x to about fp32 accuracy, as fp32 parameters multiply in the reference); 0 = the
+  // weights are rounded to bf16. The streaming GEMM (row_stream) always holds bf16 weights.
+  int w_split;
   int64_t M;
   int K, O;
   // kEpiApb: q = (x W_q^T + q_bias) * q_scale, k, v^T [batch][heads][dh][np] (keys permuted

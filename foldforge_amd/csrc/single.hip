@@ -48,8 +48,12 @@ __device__ __forceinline__ int vkey_pos(int key) {
 // multiplying the current one, and add their partial tiles through LDS; part 0 runs the
 // epilogue. For MFMA step t of a group, lane half g supplies k = 64 kg + 32 g + 8 t + (0..7)
 // of both operands.
-// Precision: activations enter as fp32 and are split into bf16 hi + lo (two MFMAs), so only
-// the weights are rounded to bf16.
+// Precision: activations enter as fp32 and are split into bf16 hi + lo (two MFMAs); the weights
+// are rounded to bf16, or with w_split also split into hi + lo (a third MFMA, lo x hi: the
+// products then carry about fp32 accuracy, the lo x lo term below it dropped). The single-track
+// ops set w_split: their GEMMs are small and latency-bound, and a bf16 rounding of a weight is
+// the same perturbation at every application of the block, so it moves the trunk's trajectory
+// rather than averaging out.
 // X sources: kXLn = LayerNorm of bf16 rows (ln_x [M][K], statistics and affine in fp32, the
 // normalised tile staged in LDS once per workgroup as hi / lo rows); kXF32 = fp32 rows
 // streamed from x32 [M][K].
@@ -641,6 +645,7 @@ __global__ __launch_bounds__(512) void row_gemm(RowGemmArgs a) {
         }
         acc = mfma32(whi, xlo, acc);
         acc = mfma32(whi, xhi, acc);
+        if (a.w_split) acc = mfma32(wlo, xhi, acc);
       }
       if (more) {
 #pragma unroll

@@ -109,7 +109,11 @@ def test_trunk_48_blocks_3_passes_tracks_the_oracle():
       rounding, amplified by the blocks (about 7e-2 at this init, where the stream's RMS grows
       from 1 to 5). The engine ``pytorch`` backend's bf16 trunk (fp32 arithmetic inside every
       op, bf16 between ops), run on the same model and inputs, measures that floor: the hip
-      trunk must stay within 1.25 x its drift + 1e-2, pair and single alike."""
+      trunk must stay within 1.08 x its drift, pair and single alike (measured 1.03 x for
+      both; 1-ulp perturbations of the inputs move either trunk's drift by up to 2-4%). The
+      single track's token-row GEMMs carry their fp32 weights as bf16 hi + lo: with the weights
+      rounded to bf16 (the same perturbation at every application of a block) the single drift
+      was 1.16 x the floor."""
     n, length = 64, 57
     model = foldforge_amd.load(backend="miniworld", device="cuda", blocks=48, seed=3, d_single=384,
                                unsupported="error")
@@ -146,8 +150,8 @@ def test_trunk_48_blocks_3_passes_tracks_the_oracle():
             print(f"block evaluation {step + 1}: hip pair {drift[0]:.3e} single {drift[1]:.3e}; "
                   f"pytorch backend pair {ref_drift[0]:.3e} single {ref_drift[1]:.3e}; "
                   f"stream rms pair {fz[where].pow(2).mean().sqrt():.3f}", flush=True)
-    assert drift[0] <= 1.25 * ref_drift[0] + 1e-2, (drift, ref_drift)
-    assert drift[1] <= 1.25 * ref_drift[1] + 1e-2, (drift, ref_drift)
+    assert drift[0] <= 1.08 * ref_drift[0], (drift, ref_drift)
+    assert drift[1] <= 1.08 * ref_drift[1], (drift, ref_drift)
 
 
 def test_trunk_n512_against_fp32_reference():

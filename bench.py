@@ -150,6 +150,53 @@ def flash_roofline(n: int, length: int, reps: int) -> dict:
             "flop_per_launch": flops}
 
 
+def flash_logit_regimes(n: int, reps: int, q_scales=(0.25, 2.0, 8.5)) -> list[dict]:
+    """The flash core at the workload's full-size shape with q scaled so that the q . k logits
+    grow from the bench's small ones to the trained-weight regime (a row's largest logit about
+    100 nats, 144 log2 units, above the offset taken from its first bias tile). For each scale:
+    the time per launch, and the share of (head, row, query) softmax rows whose largest logit
+    exceeds that offset by more than 64 log2 units (each takes the lazy rescale at least once)
+    or falls more than 100 below it (the exact two-pass path), counted on the same operands."""
+    import torch
+
+    from foldforge_amd import kernels
+
+    heads, d = 4, 32
+    np_ = (n + 127) // 128 * 128
+    rows = []
+    for qs in q_scales:
+        g = torch.Generator(device="cuda").manual_seed(1)
+        q = (torch.randn(1, heads, n, np_, d, device="cuda", generator=g) * qs).bfloat16()
+        k = torch.randn(1, heads, n, np_, d, device="cuda", generator=g).bfloat16()
+        vt = torch.randn(1, heads, n, np_ // 32, d, 32, device="cuda", generator=g).bfloat16()
+        bias = torch.randn(1, heads, np_, np_, device="cuda", generator=g)
+        offset = bias[0, :, :, :32].amax(dim=-1)  # [heads, query]: the first key tile's maximum
+        over = under = 0
+        top = torch.empty(0)
+        for h in range(heads):
+            for r0 in range(0, n, 64):
+                logits = torch.matmul(q[0, h, r0:r0 + 64].float(), k[0, h, r0:r0 + 64].float().transpose(1, 2))
+                top = (logits + bias[0, h][None]).amax(dim=-1) - offset[h][None]  # [rows, query]
+                over += int((top > 64).sum())
+                under += int((top < -100).sum())
+        total = heads * n * np_
+        blocked = kernels.blocked_bias(bias)
+        out = torch.empty(1, n, n, heads * d, device="cuda", dtype=torch.bfloat16)
+
+        def launch():
+            kernels.flash_attention_bias(q, k, vt, blocked, out, rows_valid=n, n_valid=n)
+
+        one = event_time_ms(launch, 1)
+        ms = event_time_ms(launch, reps, warm=max(50, int(300.0 / max(one, 1e-3))))
+        rows.append({"q_scale": qs, "logit_std_log2": round(qs * d ** 0.5, 2),
+                     "us_per_launch": round(ms * 1e3, 2),
+                     "rows_rescaled_frac": round(over / total, 5), "rows_exact_frac": round(under / total, 5),
+                     "finite": bool(torch.isfinite(out.float()).all())})
+        del q, k, vt, bias, blocked, out, top
+        torch.cuda.empty_cache()
+    return rows
+
+
 def layernorm_roofline(n: int, reps: int) -> dict:
     import torch
 
@@ -811,6 +858,10 @@ def main() -> int:
           ", ".join(f"{k} {v['ms']}" for k, v in per_op_384["ops"].items()), file=sys.stderr, flush=True)
 
     roof = flash_roofline(n, length, args.kernel_reps)
+    roof["logit_regimes"] = flash_logit_regimes(n, args.kernel_reps)
+    print("flash logit regimes: " + "; ".join(
+        f"q x{r['q_scale']} {r['us_per_launch']} us (rescaled {r['rows_rescaled_frac']})" for r in roof["logit_regimes"]),
+        file=sys.stderr, flush=True)
     ln = layernorm_roofline(n, args.kernel_reps)
     print(f"flash core {roof['us_per_launch']} us {roof['achieved']} TFLOP/s; "
           f"layernorm {ln['us_per_launch']} us {ln['achieved']} GB/s", file=sys.stderr, flush=True)

@@ -771,22 +771,25 @@ __global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a
     }
   };
   auto process = [&](XT* x, int64_t tile) __attribute__((always_inline)) {
-    // GR: every output tile's epilogue operands, loaded first: their wait then comes after the
-    // normalisation and the first products, not right behind the previous tile's stores
-    // (vmcnt counts stores too)
-    bf16x8 gy[GR ? 8 : 1][2], gr[GR ? 8 : 1][2];
+    // GR: the epilogue operands of the first GRS output tiles, loaded first: their wait then
+    // comes after the normalisation and the first products, not right behind the previous
+    // tile's stores (vmcnt counts stores too). Tiles GRS .. 7 reuse the slots of tiles 0, 1,
+    // loaded once those are consumed (all 8 at once would exceed the register file).
+    constexpr int GRS = 6;
+    bf16x8 gy[GR ? GRS : 1][2], gr[GR ? GRS : 1][2];
+    const int64_t mg = tile * 32 + li < a.M ? tile * 32 + li : a.M - 1;
+    auto gr_load = [&](int u, bf16x8 (&yv)[2], bf16x8 (&rv)[2]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int64_t at = mg * a.O + (ot0 + u) * 32 + 8 * (2 * k + g);
+        yv[k] = *reinterpret_cast<const bf16x8*>(a.yin + at);
+        if (a.residual) rv[k] = *reinterpret_cast<const bf16x8*>(a.res + at);
+      }
+    };
     if constexpr (GR) {
-      const int64_t m0 = tile * 32 + li;
-      const int64_t mm = m0 < a.M ? m0 : a.M - 1;
 #pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (u < nt)
-#pragma unroll
-          for (int k = 0; k < 2; ++k) {
-            const int64_t at = mm * a.O + (ot0 + u) * 32 + 8 * (2 * k + g);
-            gy[u][k] = *reinterpret_cast<const bf16x8*>(a.yin + at);
-            if (a.residual) gr[u][k] = *reinterpret_cast<const bf16x8*>(a.res + at);
-          }
+      for (int u = 0; u < GRS; ++u)
+        if (u < nt) gr_load(u, gy[u], gr[u]);
     }
     // the MFMA operands: hi + lo of the activations (LO), else the rows of x themselves
     // (kXLn: normalised in place)
@@ -903,7 +906,10 @@ __global__ __launch_bounds__(64 * stream_waves(K)) void row_stream(RowGemmArgs a
     } else if constexpr (GR) {
 #pragma unroll
       for (int u = 0; u < 8; ++u)
-        if (u < nt) out_tile(ot0 + u, gr[u], gy[u]);
+        if (u < nt) {
+          out_tile(ot0 + u, gr[u % GRS], gy[u % GRS]);
+          if (u + GRS < 8 && u + GRS < nt) gr_load(u + GRS, gy[u % GRS], gr[u % GRS]);
+        }
     } else if (K >= 256 && ((EPI == kEpiResid && a.residual) || EPI == kEpiGateResid)) {
       // the epilogue operands of each output tile (yin, the residual) are loaded one tile
       // ahead, before the previous tile's stores, into two register sets used in turn (rows

@@ -136,7 +136,8 @@ def _lineage_module(key: str, c: int, heads: int, d: int, starting: bool, seed: 
 @pytest.mark.parametrize("key", ["rf3", "chai1", "chai1_confidence"])
 def test_triattn_lineage_forms_match_oracle(starting, key):
     """RoseTTAFold3's projection biases and Chai-1's untransposed / dual outputs on the fused
-    kernels, ragged batch of 2 (each output out of place and in place)."""
+    kernels, ragged batch of 2, out of place (the same forms in place, bitwise against out of
+    place: ``test_gpu_configs.py::test_pair_ops_in_place``)."""
     n, lengths = 100, [100, 61]
     z, mask = _pair(n, 2, seed=11 * n, lengths=lengths)
     m = _lineage_module(key, 128, 4, 32, starting, seed=5)

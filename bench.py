@@ -17,6 +17,9 @@ Reported beside it, in the same JSON line:
   launched on operands of the workload's exact shape between HIP events on the stream it
   runs on; achieved = 4 N^3 H D FLOP per launch / average launch time, against the
   2.5 PFLOP/s dense bf16 peak. ``kernels`` adds the LayerNorm's HBM rate the same way.
+  ``roofline.logit_regimes``: the same launch with q scaled x0.25 / x2 / x8.5 (x8.5: logits up
+  to about 100 nats above the offset, the trained-weight scale), time per launch and the share
+  of softmax rows that take the lazy rescale or the exact path.
 * ``cpu_baseline``: the fp32 CPU oracle (``oracle/pairstack.py``, kind "port") timed on the
   host's cores on the same block and input (1 warm-up, median of 3), with the GPU
   result's rel-RMS against it.
@@ -75,6 +78,8 @@ def parse() -> argparse.Namespace:
     ap.add_argument("--copy-reference-mb", type=int, default=0,
                     help="also run a plain device copy of this many MiB (the HBM-counter calibration)")
     ap.add_argument("--no-trunk", action="store_true", help="skip the 48-block trunk measurement")
+    ap.add_argument("--no-logit-regimes", action="store_true",
+                    help="skip the flash core's large-logit timings (counter passes take the bench shape only)")
     ap.add_argument("--trunk-only", action="store_true")
     ap.add_argument("--no-reference-backend", action="store_true",
                     help="with --trunk-only: skip the engine pytorch backend's trunk run")
@@ -858,10 +863,11 @@ def main() -> int:
           ", ".join(f"{k} {v['ms']}" for k, v in per_op_384["ops"].items()), file=sys.stderr, flush=True)
 
     roof = flash_roofline(n, length, args.kernel_reps)
-    roof["logit_regimes"] = flash_logit_regimes(n, args.kernel_reps)
-    print("flash logit regimes: " + "; ".join(
-        f"q x{r['q_scale']} {r['us_per_launch']} us (rescaled {r['rows_rescaled_frac']})" for r in roof["logit_regimes"]),
-        file=sys.stderr, flush=True)
+    if not args.no_logit_regimes:
+        roof["logit_regimes"] = flash_logit_regimes(n, args.kernel_reps)
+        print("flash logit regimes: " + "; ".join(
+            f"q x{r['q_scale']} {r['us_per_launch']} us (rescaled {r['rows_rescaled_frac']})"
+            for r in roof["logit_regimes"]), file=sys.stderr, flush=True)
     ln = layernorm_roofline(n, args.kernel_reps)
     print(f"flash core {roof['us_per_launch']} us {roof['achieved']} TFLOP/s; "
           f"layernorm {ln['us_per_launch']} us {ln['achieved']} GB/s", file=sys.stderr, flush=True)

@@ -12,7 +12,8 @@
 // The gate is recomputed from z in kernel 3 rather than stored (z is read there for the
 // residual anyway).
 //
-// Flash core (one wave = 32 queries of up to 4 attention rows; 8 waves per workgroup):
+// Flash core (one wave = 32 queries of up to 4 attention rows; 4 waves per workgroup, two
+// workgroups per CU):
 //  * S^T (32 keys x 32 queries) is one MFMA accumulator. Its initial value is the pair-bias
 //    tile (fp32, stored by kernel 1 in the accumulator's register order), shared by the 4
 //    attention rows of the workgroup (the bias does not depend on the row).
@@ -29,10 +30,11 @@
 //    (every logit far below the offset) is recomputed exactly at the end with a two-pass
 //    softmax (true maximum first).
 //  * Every operand tile reaches LDS by LDS DMA (no registers, no VALU): K and V^T of the 4
-//    rows in stages of 64 keys (double-buffered, shared by the 8 waves) and each wave's bias
+//    rows in stages of 32 keys (double-buffered, shared by the 4 waves) and each wave's bias
 //    tiles (double-buffered), all one step ahead, with explicit waits on the wave's own
-//    transfers. V^T is stored by kernel 1 with the keys of each 16-key group permuted
-//    (0-3, 8-11, 4-7, 12-15), so that a lane's 8 keys of the P V product are one 16-byte read.
+//    transfers. V^T is stored by kernel 1 blocked by 32 keys, with the keys of each 16-key
+//    group permuted (0-3, 8-11, 4-7, 12-15), so that a lane's 8 keys of the P V product are
+//    one 16-byte read.
 //  * Each lane owns one query; P^T comes out of the S^T accumulator already in the
 //    B-operand order of the P V product.
 #include <math.h>

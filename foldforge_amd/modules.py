@@ -743,6 +743,13 @@ class PairformerBlock(MasterWeights, nn.Module):
 
     def forward(self, pair: Tensor, key_mask: Tensor, single: Tensor | None = None,
                 bias: Tensor | None = None):
+        pair_out = self.pair_track(pair, key_mask)
+        if single is None or self.config.d_single == 0:
+            return pair_out
+        return pair_out, self.single_track(single, pair, pair_out, key_mask, bias)
+
+    def pair_track(self, pair: Tensor, key_mask: Tensor) -> Tensor:
+        """The block's pair updates (``forward`` without the single track)."""
         c = self.config
         if c.parallel:
             # every pair update reads the block's input (legacy/pairformer.py:176-190)
@@ -750,24 +757,25 @@ class PairformerBlock(MasterWeights, nn.Module):
             upd = self.tri_multi_outgoing.delta(z0, key_mask) + self.tri_multi_incoming.delta(z0, key_mask)
             if c.use_triangle_attention:
                 upd = upd + self.tri_atten_starting.delta(z0, key_mask) + self.tri_atten_ending.delta(z0, key_mask)
-            pair_out = z0 + upd + self.transition_pair.delta(z0)
-        else:
-            z = self.tri_multi_outgoing(pair, key_mask)
-            z = self.tri_multi_incoming(z, key_mask)
-            if c.use_triangle_attention:
-                z = self.tri_atten_starting(z, key_mask)
-                z = self.tri_atten_ending(z, key_mask)
-            pair_out = self.transition_pair(z)
-        if single is None or c.d_single == 0:
-            return pair_out
-        source = pair if c.parallel else pair_out
+            return z0 + upd + self.transition_pair.delta(z0)
+        z = self.tri_multi_outgoing(pair, key_mask)
+        z = self.tri_multi_incoming(z, key_mask)
+        if c.use_triangle_attention:
+            z = self.tri_atten_starting(z, key_mask)
+            z = self.tri_atten_ending(z, key_mask)
+        return self.transition_pair(z)
+
+    def single_track(self, single: Tensor, pair: Tensor, pair_out: Tensor, key_mask: Tensor,
+                     bias: Tensor | None = None) -> Tensor:
+        """The block's single updates from its pair input (parallel schedule) or output
+        (sequential schedule): they read no other state, so they may run beside the next
+        block's pair track."""
+        c = self.config
         if c.parallel:
-            s = single + self.single_attention.delta(single, source, key_mask, bias) \
+            return single + self.single_attention.delta(single, pair, key_mask, bias) \
                 + self.single_transition.delta(single)
-        else:
-            s = self.single_attention(single, source, key_mask, bias)
-            s = self.single_transition(s)
-        return pair_out, s
+        s = self.single_attention(single, pair_out, key_mask, bias)
+        return self.single_transition(s)
 
 
 class MSABlock(MasterWeights, nn.Module):

@@ -38,8 +38,21 @@ def randomise(model: nn.Module, seed: int, *, out_scale: float | None = None) ->
     return model
 
 
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """The second stream of a device's trunks (one per device and process, default priority)."""
+    key = torch.cuda._utils._get_device_index(device)
+    if key not in _SIDE_STREAMS:
+        _SIDE_STREAMS[key] = torch.cuda.Stream(device)
+    return _SIDE_STREAMS[key]
+
+
 class PairformerTrunk(nn.Module):
     """``n_blocks`` Pairformer blocks with a single track (AF3 trunk widths by default)."""
+
+    overlap_single: bool = True  # run each block's single track beside the next block's pair track
 
     def __init__(self, n_blocks: int = 48, *, d_pair: int = 128, d_single: int = 384,
                  n_head_single: int = 16, triangle_model: str = "af3",
@@ -53,7 +66,17 @@ class PairformerTrunk(nn.Module):
 
     def forward(self, pair: Tensor, key_mask: Tensor, single: Tensor | None = None,
                 passes: int = 1, on_block=None):
-        """``passes`` times over the blocks; ``on_block(pass, index, pair, single)`` observes each output."""
+        """``passes`` times over the blocks; ``on_block(pass, index, pair, single)`` observes each output.
+
+        With a single track on the GPU, block b's single updates (which read only the single
+        state and the pair around block b) run on a second stream beside block b + 1's pair
+        updates (``overlap_single``, on by default; off while a graph is being captured and
+        while ``on_block`` observes the blocks). Every op runs as in the sequential order on the
+        same inputs, so the results are the same bit for bit."""
+        overlap = (single is not None and self.overlap_single and on_block is None and pair.is_cuda
+                   and not torch.cuda.is_current_stream_capturing())
+        if overlap:
+            return self._forward_overlapped(pair, key_mask, single, passes)
         for p in range(passes):
             for i, block in enumerate(self.blocks):
                 if single is None:
@@ -63,3 +86,26 @@ class PairformerTrunk(nn.Module):
                 if on_block is not None:
                     on_block(p, i, pair, single)
         return pair if single is None else (pair, single)
+
+    def _forward_overlapped(self, pair: Tensor, key_mask: Tensor, single: Tensor, passes: int):
+        main = torch.cuda.current_stream(pair.device)
+        side = _side_stream(pair.device)
+        # the single track starts from state the main stream produced
+        side.wait_stream(main)
+        for _ in range(passes):
+            for block in self.blocks:
+                pair_in = pair
+                pair = block.pair_track(pair_in, key_mask)
+                ready = torch.cuda.Event()
+                ready.record(main)
+                with torch.cuda.stream(side):
+                    side.wait_event(ready)
+                    single = block.single_track(single, pair_in, pair, key_mask)
+                # the side stream reads these after the main stream has moved on: their memory
+                # must not be handed to a later main-stream allocation before it is done
+                pair_in.record_stream(side)
+                pair.record_stream(side)
+        key_mask.record_stream(side)
+        main.wait_stream(side)
+        single.record_stream(main)
+        return pair, single

@@ -10,6 +10,8 @@ and bitwise invariance of the valid region to padded content.
 
 from __future__ import annotations
 
+import dataclasses
+
 import pytest
 import torch
 
@@ -98,6 +100,35 @@ def test_full_size_block_properties():
     z2[0, :, length:] = -3.0
     c = block(z2, mask)
     assert torch.equal(a[0, :length, :length], c[0, :length, :length])
+
+
+@pytest.mark.parametrize("n,length,parallel", [(128, 101, False), (96, 96, True)])
+def test_trunk_overlapped_single_track_is_bitwise_sequential(n, length, parallel):
+    """The trunk runs each block's single track on a second stream beside the next block's pair
+    track: its pair and single results equal the strictly sequential order bit for bit (the
+    sequential and the parallel schedule, a ragged mask, two passes), and every op is still
+    served by ``hip``."""
+    g = torch.Generator().manual_seed(21)
+    z = torch.randn(1, n, n, 128, generator=g).bfloat16().cuda()
+    s = torch.randn(1, n, 384, generator=g).bfloat16().cuda()
+    mask = torch.zeros(1, n, dtype=torch.bool)
+    mask[0, :length] = True
+    mask = mask.cuda()
+    model = foldforge_amd.load(backend="miniworld", device="cuda", blocks=4, seed=2, d_single=384,
+                               unsupported="error")
+    if parallel:
+        for blk in model.blocks:
+            blk.config = dataclasses.replace(blk.config, parallel=True)
+    with torch.no_grad():
+        model.overlap_single = False
+        want = model(z, mask, s, passes=2)
+        model.overlap_single = True
+        got = model(z, mask, s, passes=2)
+        again = model(z, mask, s, passes=2)
+    torch.cuda.synchronize()
+    assert dispatch.served_count(model, "hip") == 3 * 4 * 2 * 7
+    for a, b, c in zip(got, want, again):
+        assert torch.equal(a, b) and torch.equal(c, b)
 
 
 def test_trunk_48_blocks_3_passes_tracks_the_oracle():

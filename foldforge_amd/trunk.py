@@ -70,11 +70,11 @@ class PairformerTrunk(nn.Module):
 
         With a single track on the GPU, block b's single updates (which read only the single
         state and the pair around block b) run on a second stream beside block b + 1's pair
-        updates (``overlap_single``, on by default; off while a graph is being captured and
-        while ``on_block`` observes the blocks). Every op runs as in the sequential order on the
-        same inputs, so the results are the same bit for bit."""
-        overlap = (single is not None and self.overlap_single and on_block is None and pair.is_cuda
-                   and not torch.cuda.is_current_stream_capturing())
+        updates (``overlap_single``, on by default; off while ``on_block`` observes the blocks).
+        Every op runs as in the sequential order on the same inputs, so the results are the same
+        bit for bit. Under graph capture the second stream joins the capture through the
+        per-block events (a fork and a join per block in the graph)."""
+        overlap = single is not None and self.overlap_single and on_block is None and pair.is_cuda
         if overlap:
             return self._forward_overlapped(pair, key_mask, single, passes)
         for p in range(passes):

@@ -577,6 +577,40 @@ def msa_measure(reps: int = 20) -> dict:
     return out
 
 
+def msa_block_measure(reps: int = 10) -> dict:
+    """One AF3 MSA-stack block (outer product mean, MSA pair-weighted averaging 8 x 8, MSA
+    transition, the pair track with triangle attention) at L = 256 / 384 tokens, 512 MSA rows,
+    every op on hip: ms per block with the MSA track on a second stream beside the pair track
+    (the default) and strictly sequential, and the engine pytorch backend on the same GPU."""
+    import torch
+
+    from foldforge_amd import dispatch, factories
+    from foldforge_amd.trunk import randomise
+
+    out = {"workload": "AF3 MSA-stack block, 512 MSA rows, c_m=64, c_z=128, all-ones masks, bf16, "
+                       "seeded random init", "rows": []}
+    depth, cm = 512, 64
+    block = randomise(factories.msa_block(cm, 128, 4), seed=0).cuda()
+    for n in (256, 384):
+        g = torch.Generator().manual_seed(n)
+        msa = torch.randn(depth, n, cm, generator=g).bfloat16().cuda()
+        z = torch.randn(n, n, 128, generator=g).bfloat16().cuda()
+        msa_mask = torch.ones(depth, n, device="cuda")
+        pair_mask = torch.ones(n, n, device="cuda")
+        row = {"n": n}
+        with torch.no_grad():
+            block.set_backend("hip")
+            dispatch.set_refusal(block, "error")
+            for overlap, key in ((True, "hip_ms"), (False, "hip_sequential_ms")):
+                block.overlap_tracks = overlap
+                row[key] = round(event_time_ms(lambda: block(msa, z, msa_mask, pair_mask), reps, warm=reps), 4)
+            block.overlap_tracks = True
+            block.set_backend("pytorch")
+            row["pytorch_ms"] = round(event_time_ms(lambda: block(msa, z, msa_mask, pair_mask), max(2, reps // 5)), 4)
+        out["rows"].append(row)
+    return out
+
+
 def opm_measure(reps: int = 20) -> dict:
     """Outer product mean at the reference's op-table shapes: L = 256 / 384 tokens, 512 MSA
     rows, c_m 64, 32 x 32 outer products, c_z 128, AF3 form (n + 1e-3 divisor, bias before
@@ -825,7 +859,8 @@ def main() -> int:
         print(json.dumps({"shapes": shapes_measure(args.steps)}), flush=True)
         return 0
     if args.msa:
-        print(json.dumps({"msa": msa_measure(args.steps), "opm": opm_measure(args.steps)}), flush=True)
+        print(json.dumps({"msa": msa_measure(args.steps), "opm": opm_measure(args.steps),
+                          "msa_block": msa_block_measure(max(5, args.steps // 2))}), flush=True)
         return 0
     if args.trunk_only:
         trunk = trunk_measure(512, max(1, args.steps // 10), pytorch_too=not args.no_reference_backend,

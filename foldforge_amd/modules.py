@@ -827,29 +827,57 @@ class MSABlock(MasterWeights, nn.Module):
         for m in self.children_ops():
             m.set_backend(name if name in m.backends else "pytorch")
 
+    # after the outer product mean the MSA track and the pair track read only the stage's MSA
+    # and pair: on the GPU the MSA track runs on a second stream beside the pair track (the
+    # same ops on the same inputs, so the same results bit for bit)
+    overlap_tracks: bool = True
+
     def forward(self, msa: Tensor, pair: Tensor, msa_mask: Tensor, pair_mask: Tensor):
         m, z = msa[None], pair[None]
         rows = (msa_mask > 0)[None].contiguous()
         columns = (msa_mask.max(dim=0).values > 0)[None].contiguous()
         tokens = (pair_mask.diagonal(dim1=-2, dim2=-1) > 0)[None].contiguous()
+        if self.msa_first:
+            m = self.msa_transition(self.msa_attention1(m, z, columns))
+        z = self.outer_product_mean(m, rows, residual=z)
+
+        def msa_track() -> Tensor:
+            if self.parallel:
+                return m + self.msa_attention1.delta(m, z, columns) + self.msa_transition.delta(m)
+            if self.msa_first:
+                return m
+            return self.msa_transition(self.msa_attention1(m, z, columns))
+
+        side = None
+        if self.overlap_tracks and z.is_cuda and not self.msa_first:
+            from foldforge_amd.trunk import _side_stream
+
+            main, side = torch.cuda.current_stream(z.device), _side_stream(z.device)
+            side.wait_stream(main)
+            with torch.cuda.stream(side):
+                m_out = msa_track()
+            for t in (m, z, columns):  # read on the side stream after the main one moves on
+                t.record_stream(side)
+        else:
+            m_out = msa_track()
+        z = self.pair_track(z, tokens)
+        if side is not None:
+            main.wait_stream(side)
+            m_out.record_stream(main)
+        return m_out[0], z[0]
+
+    def pair_track(self, z: Tensor, tokens: Tensor) -> Tensor:
+        """The block's pair updates after the outer product mean."""
         if self.parallel:
-            z = self.outer_product_mean(m, rows, residual=z)
-            m = m + self.msa_attention1.delta(m, z, columns) + self.msa_transition.delta(m)
             z = z + (self.triangle_multiplication_outgoing.delta(z, tokens)
                      + self.triangle_multiplication_incoming.delta(z, tokens)
                      + self.pair_transition.delta(z))
             if self.with_pair_attention:
                 z = z + self.pair_attention1.delta(z, tokens) + self.pair_attention2.delta(z, tokens)
-            return m[0], z[0]
-        if self.msa_first:
-            m = self.msa_transition(self.msa_attention1(m, z, columns))
-        z = self.outer_product_mean(m, rows, residual=z)
-        if not self.msa_first:
-            m = self.msa_transition(self.msa_attention1(m, z, columns))
+            return z
         z = self.triangle_multiplication_outgoing(z, tokens)
         z = self.triangle_multiplication_incoming(z, tokens)
         if self.with_pair_attention:
             z = self.pair_attention1(z, tokens)
             z = self.pair_attention2(z, tokens)
-        z = self.pair_transition(z)
-        return m[0], z[0]
+        return self.pair_transition(z)

@@ -97,3 +97,35 @@ def test_msa_pair_weighted_averaging_full_size_is_finite_and_deterministic():
     b = mod(mc, zc, kc)
     assert torch.isfinite(a.float()).all()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("options", [{}, {"parallel": True, "opm_groups": 8, "opm_channel": 8}])
+def test_msa_block_overlapped_tracks_are_bitwise_sequential(options):
+    """After the outer product mean the MSA block runs its MSA track on a second stream beside
+    the pair track: the results equal the sequential order bit for bit (the AF3 order and
+    Chai-1's parallel stages with the grouped outer product mean), with every op on ``hip``."""
+    from foldforge_amd import dispatch
+
+    n, length, depth, cm, c = 96, 83, 41, 64, 128
+    block = randomise(factories.msa_block(cm, c, 4, **options), seed=12).cuda()
+    block.set_backend("hip")
+    dispatch.set_refusal(block, "error")
+    g = torch.Generator().manual_seed(13)
+    msa = torch.randn(depth, n, cm, generator=g).bfloat16().cuda()
+    z = torch.randn(n, n, c, generator=g).bfloat16().cuda()
+    tokens = torch.zeros(n, dtype=torch.bool)
+    tokens[:length] = True
+    msa_mask = ((torch.rand(depth, n, generator=g) > 0.2) & tokens[None]).float()
+    msa_mask[0] = tokens.float()
+    pair_mask = (tokens[:, None] & tokens[None, :]).float()
+    msa_mask, pair_mask = msa_mask.cuda(), pair_mask.cuda()
+    with torch.no_grad():
+        block.overlap_tracks = False
+        want = block(msa, z, msa_mask, pair_mask)
+        block.overlap_tracks = True
+        got = block(msa, z, msa_mask, pair_mask)
+        again = block(msa, z, msa_mask, pair_mask)
+    torch.cuda.synchronize()
+    assert dispatch.served_count(block, "hip") == 3 * 8
+    for a, b, r in zip(got, want, again):
+        assert torch.equal(a, b) and torch.equal(r, b)

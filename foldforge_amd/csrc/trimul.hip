@@ -117,13 +117,23 @@ __global__ __launch_bounds__(512, 2) void trimul_project(
     z_dma(far, fbuf);
     const bf16* xh = zt[buf];
     // pair mask m[r] m[s]: lane t holds m[s0 + t]; a tile whose 64 pairs are all real takes
-    // the unmasked epilogue
+    // the unmasked epilogue, a tile whose pairs are all masked (a padded row, or every
+    // position past the real length) is zero without any product
     const float mr = mrw[buf][wave];
     const float ms = msk[buf][wave][lane];
     const bool full = mr == 1.f && __builtin_amdgcn_ballot_w64(ms != 1.f) == 0;
+    const bool none = mr == 0.f || __builtin_amdgcn_ballot_w64(ms != 0.f) == 0;
     bf16* st = stage[wave];
+    if (none) {
+      const bf16x4 zero4 = {};
 #pragma unroll
-    for (int pt = 0; pt < kPT / 32; ++pt) {
+      for (int pt = 0; pt < kPT / 32; ++pt)
+#pragma unroll
+        for (int m4 = 0; m4 < 4; ++m4)
+          *reinterpret_cast<bf16x4*>(&st[li * kPS + pt * 32 + 8 * m4 + 4 * g]) = zero4;
+    }
+#pragma unroll
+    for (int pt = 0; pt < kPT / 32 && !none; ++pt) {
       f32x16 av = zero16(), ag = zero16();
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) {

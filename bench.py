@@ -341,6 +341,32 @@ def op_times(block, z, mask, length: int, reps: int) -> dict:
     return {"ops": ops, "ms_per_block": round(block_ms, 4), "sum_of_ops_ms": round(sum(o["ms"] for o in ops.values()), 4)}
 
 
+def single_op_n128(reps: int) -> dict:
+    """The reference's CPU-runnable case on the GPU: the triangle-attention op (starting node) on
+    z [1, 128, 128, 128] ~N(0, 1) (seed 0), 4 heads x 32, all-ones mask, random init from seed 0;
+    the hip op on the bf16 rounding of z, and the engine pytorch backend on the same GPU in fp32
+    (the case's own precision)."""
+    import torch
+
+    from foldforge_amd import factories
+    from foldforge_amd.trunk import randomise
+
+    z = torch.randn(1, 128, 128, 128, generator=torch.Generator().manual_seed(0)).cuda()
+    mask = torch.ones(1, 128, dtype=torch.bool, device="cuda")
+    ta = randomise(factories.triangle_attention(128, 4, starting=True, model="af3"), seed=0).cuda()
+    out = {"workload": "triangle attention, starting node, z [1, 128, 128, 128], 4 x 32 heads, all-ones mask, "
+                       "seed 0"}
+    with torch.no_grad():
+        ta.set_backend("hip")
+        zb = z.bfloat16()
+        out["hip_ms_bf16"] = round(event_time_ms(lambda: ta(zb, mask), reps, warm=max(20, reps)), 4)
+        ref = randomise(factories.triangle_attention(128, 4, starting=True, model="af3", precision="fp32"),
+                        seed=0).cuda()
+        ref.set_backend("pytorch")
+        out["pytorch_gpu_ms_fp32"] = round(event_time_ms(lambda: ref(z, mask), reps, warm=5), 4)
+    return out
+
+
 def trunk_inputs(n: int, seed: int = 0):
     import torch
 
@@ -915,6 +941,7 @@ def main() -> int:
     dispatch.set_refusal(block384, "error")
     per_op_384 = op_times(block384, z384_cpu.to(dev), mask384_cpu.to(dev), 384, args.kernel_reps)
     per_op_384["reference_h100_engine_cuda_ms"] = REFERENCE_H100_MS_384
+    per_op_128 = single_op_n128(args.kernel_reps)
     print(f"N=384 block {per_op_384['ms_per_block']} ms; ops " +
           ", ".join(f"{k} {v['ms']}" for k, v in per_op_384["ops"].items()), file=sys.stderr, flush=True)
 
@@ -987,7 +1014,7 @@ def main() -> int:
         "roofline": roof,
         "kernels": {"layer_norm": ln, **({"copy_reference": copy} if copy else {})},
         "cpu_baseline": base,
-        "ops": {"n512_ragged": per_op, "n384": per_op_384},
+        "ops": {"n512_ragged": per_op, "n384": per_op_384, "n128_single_triattn_op": per_op_128},
         "trunk": trunk,
         "ladder": ladder_rows,
         "shapes": shapes,

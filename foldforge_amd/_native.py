@@ -40,6 +40,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         + [c_void_p, c_size_t, c_int64, c_int64, c_int32, c_int32, c_int32, c_int32, c_int32,
            c_int32, c_int32, c_float, c_void_p],
     ),
+    "ffk_triangle_attention_transition_workspace": (c_size_t, [c_int64, c_int64]),
+    "ffk_triangle_attention_transition": (
+        c_int32,
+        [c_void_p] * 16 + [c_void_p, c_size_t, c_int64, c_int64, c_int32, c_int32, c_float,
+                           c_float, c_void_p],
+    ),
     "ffk_flash_attention_bias": (
         c_int32,
         [c_void_p] * 5

@@ -634,6 +634,74 @@ int32_t ffk_triangle_multiplication(
   return check_launch("triangle_multiplication");
 }
 
+// The pack and the launches of the fused-width triangle attention (d_pair 128, 4 x 32) on a
+// carved workspace; project_only: the projection and the flash core only (w.o holds the
+// attention output in z frame, nothing is written to out).
+static void triattn_fused_launch(const TriattnWs& w, const void* z, const uint8_t* key_mask,
+                          const float* ln_pair_w, const float* ln_pair_b, const float* w_bias,
+                          const float* w_query, const float* w_key, const float* w_value,
+                          const float* w_gate, const float* w_out, const float* b_gate,
+                          const float* b_out, const float* w_out_t, const float* b_out_t,
+                          void* out, int64_t batch, int64_t n, int n_head, int d_head,
+                          int starting, int transposed_bias, int form, int residual, float eps,
+                          bool project_only, hipStream_t st) {
+  const int d_pair = 128;
+  const int hd = n_head * d_head;
+  const int64_t m = (int64_t)hd * d_pair;
+  const float qscale = kLog2e / sqrtf((float)d_head);
+  PackJob job{};
+  job.seg[0] = {w_query, w.wqkv, m, qscale};
+  job.seg[1] = {w_key, w.wqkv + m, m, 1.f};
+  job.seg[2] = {w_value, w.wqkv + 2 * m, m, 1.f};
+  job.seg[3] = {w_bias, w.wb, (int64_t)n_head * d_pair, kLog2e};
+  job.seg[4] = {nullptr, w.wb + (int64_t)n_head * d_pair, (int64_t)(32 - n_head) * d_pair, 0.f};
+  // (the fused output-transition kernel packs the gate and output weights itself)
+  job.seg[5] = {w_gate, w.wg, project_only ? 0 : m, -kLog2e};  // sigmoid(x) = 1 / (1 + 2^(-log2(e) x))
+  job.seg[6] = {w_out, w.wo, project_only ? 0 : m, 1.f};
+  job.seg[7] = {w_out_t, w.wo_t, form == kTriattnDual ? m : 0, 1.f};
+  job.nseg = 8;
+  job.mask = key_mask;
+  job.maskf = w.maskf;
+  job.kstages = w.kst;
+  job.batch = (int)batch;
+  job.n = (int)n;
+  job.np = (int)pad128(n);
+  launch_pack(job, st);
+  TriattnArgs a{};
+  a.z = static_cast<const bf16*>(z);
+  a.mask = key_mask;
+  a.maskf = w.maskf;
+  a.kstages = w.kst;
+  a.ln_w = ln_pair_w;
+  a.ln_b = ln_pair_b;
+  a.wqkv = w.wqkv;
+  a.wb = w.wb;
+  a.wg = w.wg;
+  a.wo = w.wo;
+  a.q = w.q;
+  a.k = w.k;
+  a.vt = w.vt;
+  a.bias = w.bias;
+  a.o = w.o;
+  a.bg = b_gate;
+  a.bo = b_out;
+  a.form = form;
+  a.wo_t = w.wo_t;
+  a.bo_t = b_out_t;
+  a.tbuf = w.tbuf;
+  a.out = static_cast<bf16*>(out);
+  a.batch = (int)batch;
+  a.n = (int)n;
+  a.np = (int)pad128(n);
+  a.heads = n_head;
+  a.starting = starting ? 1 : 0;
+  a.transposed_bias = transposed_bias ? 1 : 0;
+  a.residual = residual ? 1 : 0;
+  a.eps = eps;
+  a.project_only = project_only ? 1 : 0;
+  launch_triattn(a, st);
+}
+
 size_t ffk_triangle_attention_workspace(int64_t batch, int64_t n, int32_t d_pair,
                                         int32_t n_head, int32_t d_head, int32_t output_form) {
   if (batch <= 0 || n <= 0 || d_pair <= 0 || n_head <= 0 || d_head <= 0) return 0;
@@ -826,58 +894,69 @@ int32_t ffk_triangle_attention(
     }
     return check_launch("triangle_attention");
   }
-  const int64_t m = (int64_t)hd * d_pair;
-  const float qscale = kLog2e / sqrtf((float)d_head);
-  PackJob job{};
-  job.seg[0] = {w_query, w.wqkv, m, qscale};
-  job.seg[1] = {w_key, w.wqkv + m, m, 1.f};
-  job.seg[2] = {w_value, w.wqkv + 2 * m, m, 1.f};
-  job.seg[3] = {w_bias, w.wb, (int64_t)n_head * d_pair, kLog2e};
-  job.seg[4] = {nullptr, w.wb + (int64_t)n_head * d_pair, (int64_t)(32 - n_head) * d_pair, 0.f};
-  job.seg[5] = {w_gate, w.wg, m, -kLog2e};  // sigmoid(x) = 1 / (1 + 2^(-log2(e) x))
-  job.seg[6] = {w_out, w.wo, m, 1.f};
-  job.seg[7] = {w_out_t, w.wo_t, form == kTriattnDual ? m : 0, 1.f};
-  job.nseg = 8;
-  job.mask = key_mask;
-  job.maskf = w.maskf;
-  job.kstages = w.kst;
-  job.batch = (int)batch;
-  job.n = (int)n;
-  job.np = (int)pad128(n);
-  launch_pack(job, st);
-  TriattnArgs a;
-  a.z = static_cast<const bf16*>(z);
-  a.mask = key_mask;
-  a.maskf = w.maskf;
-  a.kstages = w.kst;
-  a.ln_w = ln_pair_w;
-  a.ln_b = ln_pair_b;
-  a.wqkv = w.wqkv;
-  a.wb = w.wb;
-  a.wg = w.wg;
-  a.wo = w.wo;
-  a.q = w.q;
-  a.k = w.k;
-  a.vt = w.vt;
-  a.bias = w.bias;
-  a.o = w.o;
-  a.bg = b_gate;
-  a.bo = b_out;
-  a.form = form;
-  a.wo_t = w.wo_t;
-  a.bo_t = b_out_t;
-  a.tbuf = w.tbuf;
-  a.out = static_cast<bf16*>(out);
-  a.batch = (int)batch;
-  a.n = (int)n;
-  a.np = (int)pad128(n);
-  a.heads = n_head;
-  a.starting = starting ? 1 : 0;
-  a.transposed_bias = transposed_bias ? 1 : 0;
-  a.residual = residual ? 1 : 0;
-  a.eps = eps;
-  launch_triattn(a, st);
+  triattn_fused_launch(w, z, key_mask, ln_pair_w, ln_pair_b, w_bias, w_query, w_key, w_value,
+                       w_gate, w_out, b_gate, b_out, w_out_t, b_out_t, out, batch, n, n_head,
+                       d_head, starting, transposed_bias, form, residual, eps, false, st);
   return check_launch("triangle_attention");
+}
+
+// The ending node's triangle attention and the pair transition behind it, with the
+// attention's gate / output projection fused into the transition kernel.
+static TriattnWs attn_transition_ws(void* ws, int64_t batch, int64_t n, bf16** wt) {
+  TriattnWs w = triattn_ws(ws, batch, n, 128, 4, 32, kTriattnStandard);
+  Carver cv{static_cast<char*>(ws), w.bytes};  // after the attention's pieces
+  *wt = cv.take<bf16>((size_t)(16 + 3) * 3 * 32 * 128);
+  w.bytes = cv.used;
+  return w;
+}
+
+size_t ffk_triangle_attention_transition_workspace(int64_t batch, int64_t n) {
+  if (batch <= 0 || n <= 0) return 0;
+  bf16* wt;
+  return attn_transition_ws(nullptr, batch, n, &wt).bytes;
+}
+
+int32_t ffk_triangle_attention_transition(
+    const void* z, const uint8_t* key_mask, const float* ln_pair_w, const float* ln_pair_b,
+    const float* w_bias, const float* w_query, const float* w_key, const float* w_value,
+    const float* w_gate, const float* w_out, const float* ln_in_w, const float* ln_in_b,
+    const float* w_expand_a, const float* w_expand_b, const float* w_squeeze, void* out,
+    void* workspace, size_t workspace_bytes, int64_t batch, int64_t n, int32_t starting,
+    int32_t transposed_bias, float eps_pair, float eps_in, void* stream) {
+  if (int32_t s = check_device()) return s;
+  if (batch <= 0 || n <= 0) return fail(FFK_ERR_INVALID, "triangle_attention_transition: empty shape");
+  if (batch * 4 > 65535 || pad128(n) > 65535)
+    return fail(FFK_ERR_INVALID, "triangle_attention_transition: batch=%lld n=%lld exceed the launch grid", (long long)batch, (long long)n);
+  if (!z || !key_mask || !ln_pair_w || !ln_pair_b || !w_bias || !w_query || !w_key || !w_value ||
+      !w_gate || !w_out || !ln_in_w || !ln_in_b || !w_expand_a || !w_expand_b || !w_squeeze || !out)
+    return fail(FFK_ERR_INVALID, "triangle_attention_transition: null argument");
+  if (!aligned16(z) || !aligned16(out))
+    return fail(FFK_ERR_INVALID, "triangle_attention_transition: z/out must be 16-byte aligned");
+  bf16* wt = nullptr;
+  const size_t need = attn_transition_ws(nullptr, batch, n, &wt).bytes;
+  if (!workspace || workspace_bytes < need || !aligned16(workspace))
+    return fail(FFK_ERR_WORKSPACE, "triangle_attention_transition: workspace %zu bytes < %zu", workspace_bytes, need);
+  const TriattnWs w = attn_transition_ws(workspace, batch, n, &wt);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  launch_attention_transition_pack(w_gate, w_out, w_expand_a, w_expand_b, w_squeeze, wt, st);
+  triattn_fused_launch(w, z, key_mask, ln_pair_w, ln_pair_b, w_bias, w_query, w_key, w_value,
+                       w_gate, w_out, nullptr, nullptr, nullptr, nullptr, out, batch, n, 4, 32,
+                       starting ? 1 : 0, transposed_bias ? 1 : 0, kTriattnStandard, 1, eps_pair,
+                       true, st);
+  AttnTransitionArgs a{};
+  a.z = static_cast<const bf16*>(z);
+  a.o = w.o;
+  a.lnp_w = ln_pair_w;
+  a.lnp_b = ln_pair_b;
+  a.ln_w = ln_in_w;
+  a.ln_b = ln_in_b;
+  a.w = wt;
+  a.out = static_cast<bf16*>(out);
+  a.rows = batch * n * n;
+  a.eps_pair = eps_pair;
+  a.eps = eps_in;
+  launch_attention_output_transition(a, st);
+  return check_launch("triangle_attention_transition");
 }
 
 int32_t ffk_flash_attention_bias(const void* q, const void* k, const void* v_t,

@@ -57,6 +57,7 @@ struct TriattnArgs {
   bf16* out;
   int batch, n, np, heads, starting, transposed_bias, residual;
   float eps;
+  int project_only;  // 1: the projection and the flash core only (o in z frame, no output)
 };
 // Output forms: the z-frame update (AF3 and its descendants); the update transposed (Chai-1's
 // trunk, ending node); the update plus the transpose of a second projection's (Chai-1's
@@ -101,6 +102,24 @@ struct TransitionArgs {
 void launch_transition_pack(const float* wa, const float* wb, const float* ws, bf16* dst,
                             hipStream_t stream);
 void launch_transition(const TransitionArgs& a, hipStream_t stream);
+// Triangle attention's gate / output projection (no biases) fused in front of the pair
+// transition: out = y + transition(y), y = z + (sigmoid(LN_pair(z) w_gate^T) * o) w_out^T with
+// y rounded to bf16 (the two ops' result). z, o, out [rows][128] bf16 (out may alias z); w as
+// written by launch_attention_transition_pack (gate [128][128], out [128][128] and the
+// transition's weights: (16 + 3) * 12288 elements).
+struct AttnTransitionArgs {
+  const bf16 *z, *o;
+  const float *lnp_w, *lnp_b;  // the attention's pair LayerNorm
+  const float *ln_w, *ln_b;    // the transition's LayerNorm
+  const bf16* w;
+  bf16* out;
+  int64_t rows;
+  float eps_pair, eps;
+};
+void launch_attention_transition_pack(const float* wg, const float* wo, const float* wa,
+                                      const float* wb, const float* ws, bf16* dst,
+                                      hipStream_t stream);
+void launch_attention_output_transition(const AttnTransitionArgs& a, hipStream_t stream);
 
 // Token-row GEMM out[m][o] = sum_k W[o][k] x[m][k] (single track, single.hip) with one of
 // three epilogues, x either LayerNorm(ln_x) (kXLn, K <= kLnGemmMaxK) or fp32 rows x32 (kXF32).

@@ -873,6 +873,7 @@ void launch_triattn(const TriattnArgs& a, hipStream_t stream) {
     f.o_sj = (int64_t)a.n * c;
   }
   launch_flash(f, stream);
+  if (a.project_only) return;
   const int tiles_o = a.batch * a.n * ((a.n + kPT - 1) / kPT);
   auto output = [&](const bf16* wo, const float* bo, bf16* dst, int residual) {
     triattn_output<<<persistent_grid(tiles_o, 1), 512, 0, stream>>>(

@@ -343,6 +343,57 @@ def transition(
 transition_layer = transition
 
 
+def triangle_attention_transition(
+    z: Tensor,
+    mask: Tensor,
+    *,
+    ln_pair_weight: Tensor,
+    ln_pair_bias: Tensor,
+    to_bias: Tensor,
+    to_query: Tensor,
+    to_key: Tensor,
+    to_value: Tensor,
+    to_gate: Tensor,
+    to_out: Tensor,
+    ln_weight: Tensor,
+    ln_bias: Tensor,
+    expand_a: Tensor,
+    expand_b: Tensor,
+    squeeze: Tensor,
+    starting: bool = False,
+    transposed_bias: bool = False,
+    eps_pair: float = 1e-5,
+    eps: float = 1e-5,
+    out: Tensor | None = None,
+) -> Tensor:
+    """``transition(triangle_attention(z))`` with both residuals, the attention's gate and
+    output projection computed inside the transition kernel (the attention's output never
+    reaches HBM): the last two pair updates of a sequential Pairformer block
+    (``legacy/pairformer.py:200-202``). AF3 trunk widths only (pair 128, 4 heads x 32,
+    transition 128 x 4), no gate / output projection biases."""
+    batch, n = _pair(z, mask)
+    dev = z.device
+    c, hd = PAIR_WIDTH, TRI_HEADS * TRI_HEAD_DIM
+    spec = (("ln_pair_weight", ln_pair_weight, (c,)), ("ln_pair_bias", ln_pair_bias, (c,)),
+            ("to_bias", to_bias, (TRI_HEADS, c)), ("to_query", to_query, (hd, c)),
+            ("to_key", to_key, (hd, c)), ("to_value", to_value, (hd, c)),
+            ("to_gate", to_gate, (hd, c)), ("to_out", to_out, (c, hd)),
+            ("ln_weight", ln_weight, (c,)), ("ln_bias", ln_bias, (c,)),
+            ("expand_a", expand_a, (4 * c, c)), ("expand_b", expand_b, (4 * c, c)),
+            ("squeeze", squeeze, (c, 4 * c)))
+    ps = [_param(t, dev, nm, shape) for nm, t, shape in spec]
+    out = _output(out, tuple(z.shape), torch.bfloat16, dev)
+    lib = _native.lib()
+    ws = _workspace(lib.ffk_triangle_attention_transition_workspace(batch, n), dev)
+    status = lib.ffk_triangle_attention_transition(
+        z.data_ptr(), mask.data_ptr(), *(p.data_ptr() for p in ps), out.data_ptr(),
+        ws.data_ptr(), ws.numel(), batch, n, int(starting), int(transposed_bias),
+        float(eps_pair), float(eps), _stream(dev),
+    )
+    _native.check(status, "triangle_attention_transition")
+    return out
+
+
 def transition_supported(d: int, factor: int) -> bool:
     """Widths the transition kernels take."""
     return (d == PAIR_WIDTH and factor == 4) or (d > 0 and factor > 0 and d % 64 == 0

@@ -678,6 +678,45 @@ class OuterProductMean(EngineOp, MasterWeights, nn.Module):
 
 
 # ------------------------------------------------------------------------------------ block
+
+def _fused_attention_transition(att: "TriangleAttention", tr: "Transition") -> bool:
+    """Whether ``att`` then ``tr`` fit the fused kernel (AF3 trunk widths, the z-frame update,
+    no projection biases, neither op dead)."""
+    return (not att.dead and not tr.dead and not att.untransposed_output and not att.dual_output
+            and att.to_gate.bias is None and att.to_out.bias is None
+            and (att.d_pair, att.n_head, att.d_hidden) == (128, 4, 128) and (tr.d, tr.n) == (128, 4))
+
+
+def attention_then_transition(att: "TriangleAttention", tr: "Transition", z: Tensor, mask: Tensor,
+                              fuse: bool = True) -> Tensor:
+    """``tr(att(z, mask))``: a sequential block's last two pair updates
+    (``legacy/pairformer.py:200-202``). Where both ops route to ``hip`` and their widths fit,
+    one call runs them with the attention's output projection inside the transition kernel
+    (``kernels.triangle_attention_transition``: the same results, the attention output never
+    written). Each op is routed (refusal policy, ledger) exactly as its own call would be."""
+    b_att = att._route((z, mask), {})
+    if b_att == "hip" and fuse and _fused_attention_transition(att, tr):
+        # the transition's refusal reasons (device, dtype, width) read the same on z as on the
+        # attention's output, which has z's shape, dtype and device
+        b_tr = tr._route((z,), {})
+        if b_tr == "hip":
+            from foldforge_amd import kernels
+
+            return kernels.triangle_attention_transition(
+                z.contiguous(), mask.contiguous(),
+                ln_pair_weight=att.ln_pair.weight, ln_pair_bias=att.ln_pair.bias,
+                to_bias=att.to_bias.weight, to_query=att.to_query.weight,
+                to_key=att.to_key.weight, to_value=att.to_value.weight,
+                to_gate=att.to_gate.weight, to_out=att.to_out.weight,
+                ln_weight=tr.ln_in.weight, ln_bias=tr.ln_in.bias, expand_a=tr.expand_a.weight,
+                expand_b=tr.expand_b.weight, squeeze=tr.squeeze.weight, starting=att.starting,
+                transposed_bias=att.transposed_bias, eps_pair=att.ln_pair.eps, eps=tr.ln_in.eps,
+            )
+        return getattr(tr, f"_forward_{b_tr}")(att._forward_hip(z, mask))
+    z = getattr(att, f"_forward_{b_att}")(z, mask)
+    return tr(z)
+
+
 @dataclass(frozen=True)
 class PairformerConfig:
     """The engine's block configuration (``src/foldforge/modules/engine/pairformer.py:38-52``).
@@ -712,6 +751,9 @@ class PairformerBlock(MasterWeights, nn.Module):
     """
 
     backends = ("pytorch",)
+    #: the ending node's attention and the pair transition as one fused call where both run
+    #: on ``hip`` (``attention_then_transition``; False: two calls, the same results)
+    fuse_attention_transition: bool = True
 
     def __init__(self, config: PairformerConfig) -> None:
         super().__init__()
@@ -762,7 +804,8 @@ class PairformerBlock(MasterWeights, nn.Module):
         z = self.tri_multi_incoming(z, key_mask)
         if c.use_triangle_attention:
             z = self.tri_atten_starting(z, key_mask)
-            z = self.tri_atten_ending(z, key_mask)
+            return attention_then_transition(self.tri_atten_ending, self.transition_pair, z,
+                                             key_mask, self.fuse_attention_transition)
         return self.transition_pair(z)
 
     def single_track(self, single: Tensor, pair: Tensor, pair_out: Tensor, key_mask: Tensor,
@@ -831,6 +874,9 @@ class MSABlock(MasterWeights, nn.Module):
     # and pair: on the GPU the MSA track runs on a second stream beside the pair track (the
     # same ops on the same inputs, so the same results bit for bit)
     overlap_tracks: bool = True
+    #: the ending node's attention and the pair transition as one fused call where both run
+    #: on ``hip`` (``attention_then_transition``; False: two calls, the same results)
+    fuse_attention_transition: bool = True
 
     def forward(self, msa: Tensor, pair: Tensor, msa_mask: Tensor, pair_mask: Tensor):
         m, z = msa[None], pair[None]
@@ -879,5 +925,6 @@ class MSABlock(MasterWeights, nn.Module):
         z = self.triangle_multiplication_incoming(z, tokens)
         if self.with_pair_attention:
             z = self.pair_attention1(z, tokens)
-            z = self.pair_attention2(z, tokens)
+            return attention_then_transition(self.pair_attention2, self.pair_transition, z, tokens,
+                                             self.fuse_attention_transition)
         return self.pair_transition(z)

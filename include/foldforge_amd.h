@@ -150,6 +150,32 @@ int32_t ffk_triangle_attention(
     int32_t residual, float eps, void* stream);
 
 /*
+ * The ending (or starting) node's triangle attention followed by the pair transition, the
+ * two last pair updates of a Pairformer block in the sequential order:
+ *   y   = z + (sigmoid(LN_pair(z) w_gate^T) * attention(z)) w_out^T     (y rounded to bf16)
+ *   out = y + w_squeeze (silu(w_expand_a LN_in(y)) * w_expand_b LN_in(y))
+ * with the attention's output projection computed inside the transition kernel, so y never
+ * reaches HBM; the result equals ffk_triangle_attention (output_form 0, residual 1) followed
+ * by ffk_transition (residual 1). Widths fixed at the AF3 trunk's: d_pair 128, 4 heads x 32,
+ * transition 128 x 4; no gate / output biases (the RoseTTAFold3 lineage runs the two entry
+ * points). out may alias z. Arguments as the two entry points'; eps_pair / eps_in are the
+ * two LayerNorms' epsilons.
+ * Replaces: the block's last two pair updates, the ending node's attention residual then the
+ * transition residual (src/foldforge/models/checkpoints/legacy/pairformer.py:200-202; the
+ * engine block, src/foldforge/modules/engine/graph.py:191-235, runs them as the ops
+ * tri_atten_ending and transition_pair), each op as ffk_triangle_attention and ffk_transition
+ * replace it.
+ */
+size_t ffk_triangle_attention_transition_workspace(int64_t batch, int64_t n);
+int32_t ffk_triangle_attention_transition(
+    const void* z, const uint8_t* key_mask, const float* ln_pair_w, const float* ln_pair_b,
+    const float* w_bias, const float* w_query, const float* w_key, const float* w_value,
+    const float* w_gate, const float* w_out, const float* ln_in_w, const float* ln_in_b,
+    const float* w_expand_a, const float* w_expand_b, const float* w_squeeze, void* out,
+    void* workspace, size_t workspace_bytes, int64_t batch, int64_t n, int32_t starting,
+    int32_t transposed_bias, float eps_pair, float eps_in, void* stream);
+
+/*
  * Flash attention core with an additive pair bias, the building block of triangle
  * attention:
  *   o[b, r, j, h*32 + :] = sum_k softmax_k(q[b,h,r,j,:] . k[b,h,r,k,:] + bias[b,h,j,k]) v[b,h,r,k,:]

@@ -1,0 +1,141 @@
+"""GPU: the ending node's triangle attention and the pair transition as one fused call.
+
+``kernels.triangle_attention_transition`` computes the attention's gate and output projection
+inside the transition kernel (``attention_output_transition``), so the attention's output is
+never written. It must give the two ops' result: bit for bit against ``triangle_attention``
+followed by ``transition`` on the same inputs (the intermediate is rounded to bf16 where the
+separate kernels store it, and both paths run the same per-position arithmetic), and within
+the op tolerance of the fp64 oracle. The blocks that use it (``PairformerBlock``, ``MSABlock``)
+must return the same tensors with the fusion on and off, every op still served by ``hip``.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+from foldforge_amd import dispatch, factories, kernels
+from foldforge_amd.trunk import randomise
+from oracle import pairstack as ps
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU in this environment")
+    from foldforge_amd import _native
+
+    _native.lib()
+
+
+def _pair(n: int, batch: int, seed: int, lengths=None):
+    g = torch.Generator().manual_seed(seed)
+    z = torch.randn(batch, n, n, 128, generator=g).bfloat16()
+    mask = torch.ones(batch, n, dtype=torch.bool)
+    for b, length in enumerate(lengths or []):
+        mask[b, length:] = False
+    return z, mask
+
+
+def _modules(model: str, starting: bool, seed: int):
+    att = randomise(factories.triangle_attention(128, 4, starting=starting, model=model), seed=seed).cuda()
+    tr = randomise(factories.transition(128, 4), seed=seed + 1).cuda()
+    att.set_backend("hip")
+    tr.set_backend("hip")
+    return att, tr
+
+
+def _fused(att, tr, z, mask, out=None):
+    return kernels.triangle_attention_transition(
+        z, mask, ln_pair_weight=att.ln_pair.weight, ln_pair_bias=att.ln_pair.bias,
+        to_bias=att.to_bias.weight, to_query=att.to_query.weight, to_key=att.to_key.weight,
+        to_value=att.to_value.weight, to_gate=att.to_gate.weight, to_out=att.to_out.weight,
+        ln_weight=tr.ln_in.weight, ln_bias=tr.ln_in.bias, expand_a=tr.expand_a.weight,
+        expand_b=tr.expand_b.weight, squeeze=tr.squeeze.weight, starting=att.starting,
+        transposed_bias=att.transposed_bias, eps_pair=att.ln_pair.eps, eps=tr.ln_in.eps, out=out)
+
+
+@pytest.mark.parametrize("starting", [False, True])
+@pytest.mark.parametrize("model", ["af3", "protenix"])
+@pytest.mark.parametrize("n,lengths", [(64, None), (100, [100, 61]), (130, [117]), (300, [300])])
+def test_attention_transition_is_the_two_ops_bitwise(starting, model, n, lengths):
+    """(130, [117]): 16900 positions, the last 128-position tile ragged; (300, [300]): 704 tiles,
+    more than the persistent grid holds, so the lead chunks wrap from one tile into the next."""
+    batch = len(lengths) if lengths else 1
+    z, mask = _pair(n, batch, seed=3 * n + batch, lengths=lengths)
+    z, mask = z.cuda(), mask.cuda()
+    att, tr = _modules(model, starting, seed=n)
+    with torch.no_grad():
+        want = tr(att(z, mask))
+        got = _fused(att, tr, z, mask)
+        inplace = z.clone()
+        _fused(att, tr, inplace, mask, out=inplace)
+    torch.cuda.synchronize()
+    diff = (got.float() - want.float()).abs().max().item()
+    print(f"fused attention+transition {model} starting={starting} n={n}: max |fused - two ops| = {diff:.3e}",
+          flush=True)
+    assert torch.equal(got, want)
+    assert torch.equal(inplace, want)
+
+
+@pytest.mark.parametrize("model", ["af3", "protenix"])
+def test_attention_transition_matches_oracle(model):
+    n, lengths = 100, [100, 61]
+    z, mask = _pair(n, 2, seed=17, lengths=lengths)
+    att, tr = _modules(model, starting=False, seed=9)
+    with torch.no_grad():
+        got = _fused(att, tr, z.cuda(), mask.cuda()).cpu()
+    y = ps.triangle_attention(z, mask, att.state_dict(), starting=False, n_head=4,
+                              transposed_bias=att.transposed_bias, dtype=torch.float64)
+    want = ps.transition(y, tr.state_dict(), dtype=torch.float64)
+    where = mask[:, :, None] & mask[:, None, :]
+    rr = ps.rel_rms(got.double() - z.double(), want - z.double(), where)
+    ma = ps.max_abs(got.double() - z.double(), want - z.double(), where)
+    ref = (want - z.double())[where].abs().max().item()
+    print(f"fused attention+transition {model} vs oracle: rel_rms={rr:.2e} max_abs={ma:.2e} max_ref={ref:.2e}",
+          flush=True)
+    assert rr <= 1e-2 and ma <= 4e-2 * ref
+
+
+def test_pairformer_block_fusion_is_bitwise_and_served_by_hip():
+    n, length = 128, 101
+    z, mask = _pair(n, 1, seed=23, lengths=[length])
+    z, mask = z.cuda(), mask.cuda()
+    block = randomise(factories.pairformer_block(d_pair=128, triangle_model="af3"), seed=24).cuda()
+    block.set_backend("hip")
+    dispatch.set_refusal(block, "error")
+    with torch.no_grad():
+        block.fuse_attention_transition = False
+        want = block(z, mask)
+        block.fuse_attention_transition = True
+        got = block(z, mask)
+    torch.cuda.synchronize()
+    assert dispatch.served_count(block, "hip") == 2 * 5
+    assert torch.equal(got, want)
+
+
+def test_msa_block_fusion_is_bitwise_and_served_by_hip():
+    n, length, depth, cm, c = 96, 83, 41, 64, 128
+    block = randomise(factories.msa_block(cm, c, 4), seed=31).cuda()
+    block.set_backend("hip")
+    dispatch.set_refusal(block, "error")
+    g = torch.Generator().manual_seed(32)
+    msa = torch.randn(depth, n, cm, generator=g).bfloat16().cuda()
+    z = torch.randn(n, n, c, generator=g).bfloat16().cuda()
+    tokens = torch.zeros(n, dtype=torch.bool)
+    tokens[:length] = True
+    msa_mask = ((torch.rand(depth, n, generator=g) > 0.2) & tokens[None]).float()
+    msa_mask[0] = tokens.float()
+    pair_mask = (tokens[:, None] & tokens[None, :]).float()
+    msa_mask, pair_mask = msa_mask.cuda(), pair_mask.cuda()
+    with torch.no_grad():
+        block.fuse_attention_transition = False
+        want = block(msa, z, msa_mask, pair_mask)
+        block.fuse_attention_transition = True
+        got = block(msa, z, msa_mask, pair_mask)
+    torch.cuda.synchronize()
+    assert dispatch.served_count(block, "hip") == 2 * 8
+    for a, b in zip(got, want):
+        assert torch.equal(a, b)

@@ -147,3 +147,36 @@ def test_pair_weighted_averaging_head_split_bounds():
     assert kernels.msa_pair_weighted_averaging_supported(64, 24, 32)
     assert not kernels.msa_pair_weighted_averaging_supported(64, 32, 32)
     assert not kernels.msa_pair_weighted_averaging_supported(64, 8, 6)
+
+
+def _attn_transition_args(t, tr):
+    return dict(ln_pair_weight=t.ln_pair.weight, ln_pair_bias=t.ln_pair.bias, to_bias=t.to_bias.weight,
+                to_query=t.to_query.weight, to_key=t.to_key.weight, to_value=t.to_value.weight,
+                to_gate=t.to_gate.weight, to_out=t.to_out.weight, ln_weight=tr.ln_in.weight,
+                ln_bias=tr.ln_in.bias, expand_a=tr.expand_a.weight, expand_b=tr.expand_b.weight,
+                squeeze=tr.squeeze.weight)
+
+
+@pytest.mark.parametrize("name,shape", [
+    ("to_bias", (8, 128)), ("to_gate", (128, 64)), ("to_out", (64, 128)), ("ln_weight", (64,)),
+    ("expand_b", (256, 128)), ("squeeze", (128, 256)),
+])
+def test_attention_transition_rejects_a_parameter_of_the_wrong_shape(name, shape):
+    t = randomise(factories.triangle_attention(128, 4, starting=False, model="af3"), 1)
+    tr = randomise(factories.transition(128, 4), 1)
+    args = _attn_transition_args(t, tr)
+    args[name] = torch.zeros(shape)
+    z, mask = _pair()
+    with pytest.raises(ValueError, match=name):
+        kernels.triangle_attention_transition(z, mask, **args)
+
+
+def test_attention_transition_checks_out_and_width():
+    t = randomise(factories.triangle_attention(128, 4, starting=False, model="af3"), 1)
+    tr = randomise(factories.transition(128, 4), 1)
+    z, mask = _pair()
+    with pytest.raises(ValueError, match="out"):
+        kernels.triangle_attention_transition(z, mask, **_attn_transition_args(t, tr),
+                                              out=torch.zeros(1, 8, 8, 64, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="pair width"):
+        kernels.triangle_attention_transition(*_pair(c=64), **_attn_transition_args(t, tr))

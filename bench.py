@@ -328,6 +328,8 @@ def op_times(block, z, mask, length: int, reps: int) -> dict:
     residual) between HIP events, with its executed TFLOP/s, and the block's own ms."""
     import torch
 
+    from foldforge_amd.modules import attention_then_transition
+
     n = z.shape[1]
     gf = op_gflop(n, key_extent(n, length))
     ops = {}
@@ -337,8 +339,17 @@ def op_times(block, z, mask, length: int, reps: int) -> dict:
             call = (lambda: op(z)) if name == "transition" else (lambda: op(z, mask))
             ms = event_time_ms(call, reps, warm=max(20, reps))
             ops[name] = {"ms": round(ms, 4), "tflops_executed": round(gf[name] / ms, 1)}
+        # the block runs its last two ops as one call (the attention's output projection inside
+        # the transition kernel)
+        fused_ms = event_time_ms(lambda: attention_then_transition(
+            block.tri_atten_ending, block.transition_pair, z, mask), reps, warm=max(20, reps))
         block_ms = event_time_ms(lambda: block(z, mask), reps, warm=max(10, reps))
-    return {"ops": ops, "ms_per_block": round(block_ms, 4), "sum_of_ops_ms": round(sum(o["ms"] for o in ops.values()), 4)}
+    fused = {"ms": round(fused_ms, 4),
+             "tflops_executed": round((gf["triattn_ending"] + gf["transition"]) / fused_ms, 1)}
+    calls = sum(ops[k]["ms"] for k in ("trimul_outgoing", "trimul_incoming", "triattn_starting")) + fused_ms
+    return {"ops": ops, "triattn_ending_transition_fused": fused, "ms_per_block": round(block_ms, 4),
+            "sum_of_ops_ms": round(sum(o["ms"] for o in ops.values()), 4),
+            "sum_of_block_calls_ms": round(calls, 4)}
 
 
 def single_op_n128(reps: int) -> dict:

@@ -141,6 +141,22 @@ __device__ __forceinline__ void transition_chunk(const TransitionChunk* cur, uin
   }
 }
 
+// Two workgroups share each SIMD of a CU. At equal priority the older wave wins every issue
+// conflict, so the workgroup dispatched first runs ahead and the other finishes its last tiles
+// alone, one wave per SIMD. A workgroup's waves therefore drop one priority level per quarter
+// of its tiles done (done of total): the workgroup ahead yields to its partner.
+__device__ __forceinline__ void progress_priority(int64_t done, int64_t total) {
+  const int64_t q = 4 * done / total;
+  if (q == 0)
+    __builtin_amdgcn_s_setprio(3);
+  else if (q == 1)
+    __builtin_amdgcn_s_setprio(2);
+  else if (q == 2)
+    __builtin_amdgcn_s_setprio(1);
+  else
+    __builtin_amdgcn_s_setprio(0);
+}
+
 // The rows of one wave: this wave's 32 rows of the tile at row0 of src straight into its rows
 // of the LDS tile (xr_lds: the wave's first row): piece j = rows 4 j .. 4 j + 3, lane L fills
 // bytes 16 L of it. Rows past the end re-read the last row (finite values, never stored:
@@ -311,6 +327,7 @@ __global__ __launch_bounds__(64 * NW, WG_PER_CU) void transition_swiglu(
 #pragma unroll 1
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int64_t row0 = tile * XT;
+    progress_priority((tile - blockIdx.x) / gridDim.x, (ntiles - 1 - blockIdx.x) / gridDim.x + 1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // own x rows and chunk-0 pieces landed
     __syncthreads();                                   // everyone's chunk-0 pieces landed
     // the last tile re-reads its own rows instead of a next tile's
@@ -392,6 +409,7 @@ __global__ __launch_bounds__(64 * NW, WG_PER_CU) void attention_output_transitio
 #pragma unroll 1
   for (int64_t tile = blockIdx.x; tile < ntiles; tile += gridDim.x) {
     const int64_t row0 = tile * XT;
+    progress_priority((tile - blockIdx.x) / gridDim.x, (ntiles - 1 - blockIdx.x) / gridDim.x + 1);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // own z rows and chunk-0 pieces landed
     __syncthreads();                                   // everyone's chunk-0 pieces landed
     // z in the accumulator layout (the residual of y)

@@ -59,9 +59,11 @@ def _fused(att, tr, z, mask, out=None):
 
 @pytest.mark.parametrize("starting", [False, True])
 @pytest.mark.parametrize("model", ["af3", "protenix"])
-@pytest.mark.parametrize("n,lengths", [(64, None), (100, [100, 61]), (130, [117]), (300, [300]), (512, [386])])
+@pytest.mark.parametrize("n,lengths", [(1, None), (33, [20]), (64, None), (96, [40, 0]), (100, [100, 61]),
+                                       (130, [117]), (300, [300]), (512, [386])])
 def test_attention_transition_is_the_two_ops_bitwise(starting, model, n, lengths):
-    """(130, [117]): 16900 positions, the last 128-position tile ragged; (300, [300]): 704 tiles,
+    """(1, None) and (33, [20]): a single partial tile; (96, [40, 0]): a batch element with no
+    real token; (130, [117]): 16900 positions, the last 128-position tile ragged; (300, [300]): 704 tiles,
     more than the persistent grid holds, so the lead chunks wrap from one tile into the next;
     (512, [386]): the benchmark block's shape and padding."""
     batch = len(lengths) if lengths else 1

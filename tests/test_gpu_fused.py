@@ -102,26 +102,37 @@ def test_attention_transition_matches_oracle(model):
     assert rr <= 1e-2 and ma <= 4e-2 * ref
 
 
-def test_pairformer_block_fusion_is_bitwise_and_served_by_hip():
+@pytest.mark.parametrize("model,d_single", [("af3", 0), ("protenix", 0), ("af3", 384)])
+def test_pairformer_block_fusion_is_bitwise_and_served_by_hip(model, d_single):
+    """With and without the single track (its attention reads the block's pair output)."""
     n, length = 128, 101
     z, mask = _pair(n, 1, seed=23, lengths=[length])
     z, mask = z.cuda(), mask.cuda()
-    block = randomise(factories.pairformer_block(d_pair=128, triangle_model="af3"), seed=24).cuda()
+    block = randomise(factories.pairformer_block(d_pair=128, triangle_model=model, d_single=d_single),
+                      seed=24).cuda()
     block.set_backend("hip")
     dispatch.set_refusal(block, "error")
+    args = (z, mask)
+    if d_single:
+        g = torch.Generator().manual_seed(25)
+        args = (z, mask, torch.randn(1, n, d_single, generator=g).bfloat16().cuda())
     with torch.no_grad():
         block.fuse_attention_transition = False
-        want = block(z, mask)
+        want = block(*args)
         block.fuse_attention_transition = True
-        got = block(z, mask)
+        got = block(*args)
     torch.cuda.synchronize()
-    assert dispatch.served_count(block, "hip") == 2 * 5
-    assert torch.equal(got, want)
+    ops = 7 if d_single else 5
+    assert dispatch.served_count(block, "hip") == 2 * ops
+    for a, b in zip(got if d_single else (got,), want if d_single else (want,)):
+        assert torch.equal(a, b)
 
 
-def test_msa_block_fusion_is_bitwise_and_served_by_hip():
+@pytest.mark.parametrize("options", [{}, {"msa_first": True}])
+def test_msa_block_fusion_is_bitwise_and_served_by_hip(options):
+    """The AF3 order and the Boltz order (MSA track first)."""
     n, length, depth, cm, c = 96, 83, 41, 64, 128
-    block = randomise(factories.msa_block(cm, c, 4), seed=31).cuda()
+    block = randomise(factories.msa_block(cm, c, 4, **options), seed=31).cuda()
     block.set_backend("hip")
     dispatch.set_refusal(block, "error")
     g = torch.Generator().manual_seed(32)

@@ -4,9 +4,11 @@
 // src/foldforge/modules/dense/diffusion_transformer.py:36-44 (SwiGLU). The 4c-wide hidden
 // layer never leaves registers: x is read once and the output written once.
 //
-// Persistent over tiles of 256 positions; 8 waves per workgroup (two per SIMD, so one wave's
-// silu VALU work overlaps the other's MFMAs). Wave w owns positions 32 w .. 32 w + 31 of the
-// tile for the whole tile:
+// Persistent over tiles of 128 positions; 4 waves per workgroup and two workgroups per CU (two
+// waves per SIMD from different workgroups, so one wave's silu VALU work fills the other's MFMA
+// gaps without a shared barrier; each tile start lowers the waves' priority with the
+// workgroup's progress so that neither workgroup finishes far ahead of its partner). Wave w
+// owns positions 32 w .. 32 w + 31 of the tile for the whole tile:
 //   * its LN'd operand x^ (32 positions x 128 channels) sits in registers as the B operand;
 //   * the expand GEMMs are computed transposed, D = W_a,b (hidden x k) * x^ (k x positions),
 //     so a lane holds one position and 16 hidden channels of a 32-hidden block;
@@ -24,6 +26,8 @@
 // columns), each already in the byte order the kernel wants in LDS, so streaming a chunk is a
 // plain linear copy; chunks are double-buffered, one barrier per chunk, and the next tile's
 // raw x arrives behind the first chunk's compute. LDS tiles are unpadded and XOR-swizzled.
+// attention_output_transition runs the triangle attention's gate / output projection in front
+// of the same tile (three lead chunks of weights ahead of the 16), see there.
 #include "ffk_device.h"
 #include "ffk_kernels.h"
 

@@ -5,11 +5,15 @@
 //                      written channel-major [B][h][np][np] so that the contraction is a
 //                      K-contiguous batched GEMM in both directions (incoming tiles walk
 //                      columns of z, which stores A^T).
-//   2. trimul_contract P[bh] = X[bh] Y[bh]^T on MFMA, 128x128 tiles, LDS double buffer.
+//   2. trimul_contract P[bh] = X[bh] Y[bh]^T on MFMA: 256 x 256 tiles (trimul_contract256,
+//                      64-k stages by LDS DMA, two 64 KB buffers) when the padded width is a
+//                      multiple of 256, else 128 x 128 tiles; both stop at the last 32-key
+//                      stage holding a real key (the operands are zero past it).
 //   3. trimul_output   LN_out(P) W_out^T * sigmoid(LN_pair(z) W_g^T) + z, channel-last.
 // Kernels 1 and 3 are persistent and weight-stationary: each wave keeps its 32-channel
 // slice of every projection in registers (one load per workgroup), loops over 64-position
-// tiles, and stages its results through LDS so that every global store is 16 bytes.
+// tiles, and stages its results through LDS so that every global store is 16 bytes. A
+// projection tile whose pairs are all masked stores zeros without its products.
 // The output gate is recomputed from z in kernel 3 (z is read there for the residual
 // anyway) instead of being stored: 128 channels of gate would cost 2 x 67 MB of HBM
 // traffic at N = 512 against 8.6 GFLOP of MFMA work.

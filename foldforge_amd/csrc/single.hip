@@ -8,9 +8,11 @@
 //   bias[h, i, j] = LN_pair(z[i, j]) . W_b[h]   (the pair norm has no offset)
 //   o = softmax_j(q_i . k_j / sqrt(dh) + bias[h, i, j]) over valid keys j, 0 for an empty row
 //   out = s + (g * o) W_out^T
-// is run as: LayerNorm (layernorm.hip) -> row_gemm<kEpiApb> (q, k, v^T, gate) ->
-// apb_pair_bias -> apb_attention (gate applied) -> row_gemm<kEpiResid>.
-// The wide transition is LayerNorm -> row_gemm<kEpiSwiglu> -> row_gemm<kEpiResid>.
+// is run as: row_gemm<kEpiApb, kXLn> (LayerNorm prologue; q, k, v^T, gate) -> apb_pair_bias
+// -> apb_attention (gate applied) -> row_gemm<kEpiResid>.
+// The wide transition is row_gemm<kEpiSwiglu, kXLn> -> row_gemm<kEpiResid>.
+// The same file holds row_stream, the streaming LayerNorm-fed token-row GEMM that the
+// generic pair widths (template stacks, Chai-1's pair 256) run their projections on.
 //
 // Logits are carried in log2 units: q is scaled by log2(e) / sqrt(dh) and the pair-bias
 // weights by log2(e), so the softmax uses exp2. Masked keys (and the padding keys past n)

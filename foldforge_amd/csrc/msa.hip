@@ -5,7 +5,8 @@
 //   o[s, i, h] = sum_j w[h, i, j] v[s, j, h], v = x W_v^T; out = m + (sigmoid(x W_g^T) o) W_out^T.
 // The weights do not depend on the MSA row s, so per head the average is one GEMM
 //   O_h[(s, c)][i] = sum_j v^T_h[(s, c)][j] w_h[i][j]
-// with all S MSA rows stacked along M. The C-ABI (api.hip) runs:
+// with all S MSA rows stacked along M. The C-ABI (api.hip) runs (the token-row GEMMs through
+// launch_row_gemm, which takes the streaming row_stream where the width allows):
 //   row_gemm<kEpiPwa, kXLn> (single.hip): LN_msa + value / gate projections -> v^T, gate
 //   apb_pair_bias (single.hip): pair logits in log2 units, masked keys very negative
 //   pwa_softmax: the softmax of every (batch, head, query) row -> bf16 weights

@@ -462,7 +462,8 @@ __global__ __launch_bounds__(64 * NW, WG_PER_CU) void attention_output_transitio
     // lead chunk 0: gate rows 0-95
     {
       const TransitionChunk* cur = &W[k % NB];
-      weight_dma<NW>(wpack, 1, w_lds + ((k + NB - 1) % NB) * sizeof(TransitionChunk), wave, lane);
+      weight_dma<NW>(wpack, (0 + NB - 1) % NCH, w_lds + ((k + NB - 1) % NB) * sizeof(TransitionChunk), wave,
+                     lane);
       f32x16 ag[3];
 #pragma unroll
       for (int cb = 0; cb < 3; ++cb) ag[cb] = project(lead_slab(cur, cb), xb);
@@ -476,7 +477,8 @@ __global__ __launch_bounds__(64 * NW, WG_PER_CU) void attention_output_transitio
     f32x16 ao[4];
     {
       const TransitionChunk* cur = &W[k % NB];
-      weight_dma<NW>(wpack, 2, w_lds + ((k + NB - 1) % NB) * sizeof(TransitionChunk), wave, lane);
+      weight_dma<NW>(wpack, (1 + NB - 1) % NCH, w_lds + ((k + NB - 1) % NB) * sizeof(TransitionChunk), wave,
+                     lane);
       gate_rows(project(lead_slab(cur, 0), xb), 3);
 #pragma unroll
       for (int kk = 0; kk < 8; ++kk) gb[kk] = ld8(&XR[off128(rw + li, 2 * kk + g)]);
@@ -487,7 +489,8 @@ __global__ __launch_bounds__(64 * NW, WG_PER_CU) void attention_output_transitio
     // lead chunk 2: output rows 64-127, then y = z + projection into the rows
     {
       const TransitionChunk* cur = &W[k % NB];
-      weight_dma<NW>(wpack, 3, w_lds + ((k + NB - 1) % NB) * sizeof(TransitionChunk), wave, lane);
+      weight_dma<NW>(wpack, (2 + NB - 1) % NCH, w_lds + ((k + NB - 1) % NB) * sizeof(TransitionChunk), wave,
+                     lane);
       ao[2] = project(lead_slab(cur, 0), gb);
       ao[3] = project(lead_slab(cur, 1), gb);
 #pragma unroll

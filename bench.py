@@ -491,12 +491,15 @@ def cpu_baseline_trunk_parity(n: int, evals=(0, 71, 143)) -> dict:
     z_cpu, s_cpu, mask_cpu = trunk_inputs(n)
     model = foldforge_amd.load(backend="miniworld", device="cuda", blocks=TRUNK_BLOCKS, seed=0,
                                d_single=D_SINGLE, unsupported="error")
-    prev, taken = [z_cpu.cuda(), s_cpu.cuda()], {}
+    prev, taken, stream = [z_cpu.cuda(), s_cpu.cuda()], {}, []
+    rms = lambda t: round(float(t.float().pow(2).mean().sqrt()), 3)  # noqa: E731
 
     def observe(p, i, pair, single):
         e = TRUNK_BLOCKS * p + i
         if e in evals:
             taken[e] = (prev[0].cpu(), prev[1].cpu(), pair.cpu(), single.cpu())
+        if (e + 1) % 16 == 0:
+            stream.append([e + 1, rms(pair), rms(single)])
         prev[0], prev[1] = pair, single
 
     with torch.no_grad():
@@ -547,6 +550,8 @@ def cpu_baseline_trunk_parity(n: int, evals=(0, 71, 143)) -> dict:
     torch.cuda.empty_cache()
     return {
         "sampled_block_updates_vs_fp32_oracle": rows,
+        "stream_rms": {"every_16_evaluations": stream, "columns": ["evaluation", "pair", "single"],
+                       "input": [rms(z_cpu), rms(s_cpu)]},
         "final_state_vs_fp32_reference_trunk": {
             "hip": {"pair": round(ps.rel_rms(hz, fz, where), 5), "single": round(ps.rel_rms(hs, fs), 5)},
             "pytorch_backend_bf16": {"pair": round(ps.rel_rms(bz, fz, where), 5),
